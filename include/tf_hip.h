@@ -1,0 +1,229 @@
+/*
+ * tf_hip.h — C ABI of the MI355X (gfx950) backend for tensorforge's training
+ * hot path: the reverse-mode backward pass, its gradient kernels and the
+ * fused SGD-momentum update.
+ *
+ * Every entry point is extern "C", takes plain pointers and sizes, returns a
+ * tf_status (0 = TF_OK) and records a human-readable message retrievable with
+ * tf_last_error() (thread-local) on failure.  Kernels are asynchronous on the
+ * context's current stream; nothing synchronises implicitly except the calls
+ * documented as synchronous (tf_hip_sync, tf_hip_memcpy with D2H/H2H,
+ * tf_hip_event_elapsed).
+ *
+ * All matrices are row-major.  Dtype codes match tensorforge's
+ * `enum class Dtype : uint8_t` (reference tensor/Dtype.hpp:9-16).
+ *
+ * The reference interfaces each group replaces are cited beside it
+ * (paths relative to the reference repository root).
+ */
+#ifndef TF_HIP_H
+#define TF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct tf_ctx tf_ctx;
+typedef int tf_status;
+
+enum {
+    TF_OK = 0,
+    TF_ERR_INVALID = 1,     /* bad argument (shape, dtype, null pointer) */
+    TF_ERR_HIP = 2,         /* a HIP runtime call failed */
+    TF_ERR_UNSUPPORTED = 3, /* dtype/layout combination not implemented */
+    TF_ERR_OOM = 4          /* device allocation failed */
+};
+
+/* == tensorforge Dtype (tensor/Dtype.hpp:9-16) */
+enum {
+    TF_F32 = 0,
+    TF_F16 = 1,
+    TF_BF16 = 2,
+    TF_I32 = 3,
+    TF_I64 = 4,
+    TF_BOOL = 5
+};
+
+/* == allocator_dispatch::CudaCopyKind (tensor/CPUStorageAllocator.hpp:69-74) */
+enum {
+    TF_COPY_H2H = 0,
+    TF_COPY_H2D = 1,
+    TF_COPY_D2H = 2,
+    TF_COPY_D2D = 3
+};
+
+/* GEMM epilogues applied after alpha*acc + beta*C. */
+enum {
+    TF_EPI_NONE = 0,
+    TF_EPI_BIAS = 1,      /* + bias[n] */
+    TF_EPI_BIAS_RELU = 2, /* max(. + bias[n], 0) */
+    TF_EPI_RELU = 3       /* max(., 0) */
+};
+
+/* ---------------------------------------------------------------------------
+ * Errors and version
+ * ------------------------------------------------------------------------- */
+const char* tf_last_error(void);
+const char* tf_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Runtime: context, stream, allocator, copies, events.
+ * Replaces DeviceContext / CudaStream / CudaEvent (cuda/CudaContext.hpp:23-140,
+ * cuda/CudaContext.cpp:18-60) and CudaStorageAllocator
+ * (cuda/memory/CudaStorageAllocator.cpp:34-143).
+ * ------------------------------------------------------------------------- */
+
+/* Number of visible GPUs (0 when none). Never fails on a GPU-less host. */
+tf_status tf_hip_device_count(int* count);
+
+/* Create a context on `device`: one non-blocking stream at default priority
+ * and a hipMemPool_t with a raised release threshold (the reference pool keeps
+ * 64 MiB, cuda/memory/CudaStorageAllocator.cpp:48-50; this one keeps all freed
+ * memory cached until tf_hip_trim). */
+tf_status tf_hip_init(int device, tf_ctx** out);
+tf_status tf_hip_shutdown(tf_ctx* ctx);
+
+/* The stream kernels are launched on (hipStream_t as void*). */
+tf_status tf_hip_stream(tf_ctx* ctx, void** stream);
+/* Launch on a caller-owned stream from now on; NULL restores the context's. */
+tf_status tf_hip_set_stream(tf_ctx* ctx, void* stream);
+/* Block until all work on the current stream has finished. */
+tf_status tf_hip_sync(tf_ctx* ctx);
+
+/* Stream-ordered pool allocation (hipMallocAsync on the context's pool).
+ * bytes == 0 allocates 1 byte, as the reference does
+ * (cuda/memory/storage_allocator_test.cpp:42-48). */
+tf_status tf_hip_alloc(tf_ctx* ctx, size_t bytes, void** out);
+/* Stream-ordered free back into the pool. NULL is a no-op. */
+tf_status tf_hip_free(tf_ctx* ctx, void* ptr);
+/* Return cached pool memory above `keep_bytes` to the device. */
+tf_status tf_hip_trim(tf_ctx* ctx, size_t keep_bytes);
+/* Bytes currently reserved by the pool and in use by live allocations. */
+tf_status tf_hip_pool_stats(tf_ctx* ctx, uint64_t* reserved, uint64_t* used);
+
+/* Copy `bytes` (kind = TF_COPY_*). H2D and D2D are stream-ordered; D2H and
+ * H2H return after the data has landed.  Replaces cuda_copy_dispatch
+ * (cuda/memory/CudaStorageAllocator.cpp:67-87). */
+tf_status tf_hip_memcpy(tf_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
+
+/* p[i] = value for i < n (float32) — a kernel, safe under graph capture. */
+tf_status tf_hip_fill_f32(tf_ctx* ctx, float* p, float value, int64_t n);
+/* Byte fill through a kernel (no hipMemsetAsync). */
+tf_status tf_hip_zero(tf_ctx* ctx, void* p, size_t bytes);
+
+/* Events on the current stream, for timing. */
+tf_status tf_hip_event_create(tf_ctx* ctx, void** event);
+tf_status tf_hip_event_record(tf_ctx* ctx, void* event);
+/* Waits for `end`, then returns the elapsed milliseconds start -> end. */
+tf_status tf_hip_event_elapsed(void* start, void* end, float* ms);
+tf_status tf_hip_event_destroy(void* event);
+
+/* ---------------------------------------------------------------------------
+ * GEMM on MFMA.  C[m,n] = epi(alpha * sum_k op(A)[m,k] * op(B)[k,n] + beta*C[m,n])
+ *   op(A) is M x K: trans_a == 0 -> A[m*lda + k], trans_a == 1 -> A[k*lda + m]
+ *   op(B) is K x N: trans_b == 0 -> B[k*ldb + n], trans_b == 1 -> B[n*ldb + k]
+ * in_dtype: TF_F32 (v_mfma_f32_32x32x2_f32) or TF_BF16 (bf16 MFMA, fp32
+ * accumulate).  out_dtype: TF_F32 or TF_BF16.  bias: float32[N] or NULL.
+ * beta != 0 requires out_dtype == TF_F32.
+ * Replaces launch_gemm_{naive,tiled_16x16,optimized} (cuda/kernels/gemm.cuh:33-53)
+ * and the CPU loops of Tensor::matmul (tensor/Tensor.cpp:334-368) plus the
+ * transpose copies of MatmulBackward (autograd/ops/MatmulBackward.hpp:29-32),
+ * which become layout flags.
+ * ------------------------------------------------------------------------- */
+tf_status tf_gemm(tf_ctx* ctx, int trans_a, int trans_b,
+                  int64_t M, int64_t N, int64_t K, float alpha,
+                  const void* A, int64_t lda, const void* B, int64_t ldb,
+                  float beta, void* C, int64_t ldc,
+                  int in_dtype, int out_dtype, int epilogue, const float* bias);
+
+/* Strided-batched GEMM: for b < batch, the same op on A + b*stride_a,
+ * B + b*stride_b, C + b*stride_c (strides in elements).  Used by Conv2d
+ * forward/backward in place of the reference's per-sample launches
+ * (nn/Conv2d.cpp:124-127, 186-198, 213-243). */
+tf_status tf_gemm_strided_batched(tf_ctx* ctx, int trans_a, int trans_b,
+                                  int64_t M, int64_t N, int64_t K, float alpha,
+                                  const void* A, int64_t lda, int64_t stride_a,
+                                  const void* B, int64_t ldb, int64_t stride_b,
+                                  float beta, void* C, int64_t ldc, int64_t stride_c,
+                                  int64_t batch, int in_dtype, int out_dtype);
+
+/* ---------------------------------------------------------------------------
+ * Elementwise forward + backward (bandwidth kernels, float32 unless noted).
+ * Forward ops replace the registered elementwise launchers
+ * (cuda/CudaKernelRegistry.hpp:15-26, cuda/kernels/elementwise.cu:80-173).
+ * ------------------------------------------------------------------------- */
+tf_status tf_add(tf_ctx* ctx, const void* a, const void* b, void* out, int64_t n, int dtype);
+tf_status tf_mul(tf_ctx* ctx, const void* a, const void* b, void* out, int64_t n, int dtype);
+/* out = a * s[0] where s is a device scalar. */
+tf_status tf_scale_by(tf_ctx* ctx, const void* a, const float* s, void* out, int64_t n, int dtype);
+tf_status tf_relu_fwd(tf_ctx* ctx, const void* x, void* y, int64_t n, int dtype);
+tf_status tf_sigmoid_fwd(tf_ctx* ctx, const void* x, void* y, int64_t n, int dtype);
+tf_status tf_tanh_fwd(tf_ctx* ctx, const void* x, void* y, int64_t n, int dtype);
+
+/* dx = dy * (x > 0 ? 1 : 0)   (autograd/ops/ReluBackward.hpp:22-32) */
+tf_status tf_relu_bwd(tf_ctx* ctx, const void* dy, const void* x, void* dx, int64_t n, int dtype);
+/* dx = dy * y * (1 - y), y = sigmoid output (autograd/TensorAutograd.cpp:152-156) */
+tf_status tf_sigmoid_bwd(tf_ctx* ctx, const void* dy, const void* y, void* dx, int64_t n, int dtype);
+/* dx = dy * (1 - y*y), y = tanh output (autograd/TensorAutograd.cpp:158-164) */
+tf_status tf_tanh_bwd(tf_ctx* ctx, const void* dy, const void* y, void* dx, int64_t n, int dtype);
+
+/* ---------------------------------------------------------------------------
+ * Row kernels (one wave64 per row).
+ * ------------------------------------------------------------------------- */
+/* Cross-entropy forward: lse[r] = logsumexp(logits[r,:]) (may be NULL) and
+ * loss[0] = mean_r (lse[r] - logits[r, t_r]).  targets are int64 in [0, cols).
+ * Equals the loss of the train_mlp chain (examples/train_mlp.cpp:54-76). */
+tf_status tf_ce_fwd(tf_ctx* ctx, const float* logits, const int64_t* targets,
+                    float* loss, float* lse, int64_t rows, int64_t cols);
+/* Fused LogSoftmax+NLL backward: dlogits = g * (softmax(logits) - onehot) / rows
+ * where g = grad_loss[0] (NULL means 1).  With lse from tf_ce_fwd the kernel
+ * is a single streaming pass; with lse == NULL it recomputes row statistics.
+ * Replaces LogSoftmaxBackward + MulBackward + 2x SumBackward + 2x scalar
+ * MulBackward of the chain (autograd/ops/LogSoftmaxBackward.hpp:26-58). */
+tf_status tf_ce_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets,
+                    const float* lse, const float* grad_loss, float* dlogits,
+                    int64_t rows, int64_t cols);
+/* Forward and backward in one pass over logits (upstream gradient 1). */
+tf_status tf_ce_fwd_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets,
+                        float* loss, float* dlogits, int64_t rows, int64_t cols);
+/* Row log_softmax / softmax forward (tensor/Tensor.cpp:370-447). */
+tf_status tf_log_softmax_fwd(tf_ctx* ctx, const float* x, float* y, int64_t rows, int64_t cols);
+tf_status tf_softmax_fwd(tf_ctx* ctx, const float* x, float* y, int64_t rows, int64_t cols);
+/* dx = dy - exp(y) * sum_j dy  (autograd/ops/LogSoftmaxBackward.hpp:26-58) */
+tf_status tf_log_softmax_bwd(tf_ctx* ctx, const float* y, const float* dy, float* dx,
+                             int64_t rows, int64_t cols);
+/* dx = y * (dy - sum_j dy*y)  (autograd/ops/SoftmaxBackward.hpp:27-55) */
+tf_status tf_softmax_bwd(tf_ctx* ctx, const float* y, const float* dy, float* dx,
+                         int64_t rows, int64_t cols);
+
+/* ---------------------------------------------------------------------------
+ * Reductions (deterministic two-stage, no atomics).
+ * ------------------------------------------------------------------------- */
+/* db[c] = sum_r dy[r, c]  (Linear bias grad; no reference counterpart, the
+ * reference Linear drops its bias, nn/Linear.cpp:60-63) */
+tf_status tf_colsum(tf_ctx* ctx, const float* dy, float* db, int64_t rows, int64_t cols);
+/* db[c] = sum_{n,hw} dy[n, c, hw]  (replaces launch_reduce_sum_axis_nchw,
+ * cuda/kernels/reduce_sum_axis.cu:53-120, which is wrong for H*W > 256) */
+tf_status tf_chansum_nchw(tf_ctx* ctx, const float* dy, float* db,
+                          int64_t N, int64_t C, int64_t HW);
+
+/* ---------------------------------------------------------------------------
+ * Optimiser: fused SGD with momentum (nn/optim/SGD.hpp:3-6):
+ *   v <- mu * v + g ;  p <- p - lr * v        (mu == 0: p <- p - lr * g, v untouched)
+ * p, g, v float32[n]; p_bf16 (optional, may be NULL) receives bf16(p).
+ * ------------------------------------------------------------------------- */
+tf_status tf_sgd_momentum(tf_ctx* ctx, float* p, const float* g, float* v,
+                          void* p_bf16, int64_t n, float lr, float mu);
+
+/* float32 <-> bf16 conversion (round to nearest even). */
+tf_status tf_cast_f32_bf16(tf_ctx* ctx, const float* x, void* y, int64_t n);
+tf_status tf_cast_bf16_f32(tf_ctx* ctx, const void* x, float* y, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TF_HIP_H */

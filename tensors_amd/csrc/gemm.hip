@@ -1,0 +1,534 @@
+// MFMA GEMMs for Matmul forward and backward on gfx950.
+//
+//   C = epi(alpha * op(A) op(B) + beta * C)      row-major, see tf_hip.h
+//
+// One kernel template covers NN, NT, TN and TT: the transpose flags pick how
+// each operand tile is staged in LDS rather than materialising a transposed
+// copy as the reference does (autograd/ops/MatmulBackward.hpp:29-32,
+// nn/Linear.cpp:62).  An operand whose reduction index k is contiguous in
+// memory ("K-major": A with trans_a == 0, B with trans_b == 1) is staged as
+// [rows][k]; one whose row index is contiguous ("MN-major") as [k][rows].
+// Global->LDS copies are then straight 16-byte vector copies in both cases,
+// and the MFMA fragment reads differ:
+//   K-major : each lane reads 16 consecutive k of its row  -> 4 x ds_read_b128
+//   MN-major: each lane reads its row at 16 different k    -> 16 x ds_read_b32
+// The reduction order inside a 32-deep k block is permuted (lanes 0-31 feed
+// k = s, lanes 32-63 feed k = 16 + s to the s-th MFMA) so that the K-major
+// reads are contiguous; the sum is the same, the rounding order differs from
+// the reference's sequential loop (tensor/Tensor.cpp:356-360) within fp32
+// tolerance.
+//
+// fp32 tile: 128 x 128 x 32 per 256-thread workgroup (4 waves in 2 x 2, each
+// wave 64 x 64 = 2 x 2 tiles of v_mfma_f32_32x32x2_f32), LDS double buffered
+// with one barrier per k block, global loads for block k+1 issued before the
+// MFMAs of block k.  bf16: same structure with v_mfma_f32_32x32x16_bf16 and a
+// 64-deep k block.
+//
+// Work distribution: the tile index is remapped so that each of the 8 XCDs
+// (which receive workgroups round-robin) owns a contiguous, row-grouped block
+// of output tiles, keeping its A and B panels in its own L2.  When there are
+// too few tiles to fill the GPU and K is long, K is split across
+// workgroups; partial tiles go to a workspace and a second kernel reduces
+// them in a fixed order (deterministic, no atomics) and applies the epilogue.
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+constexpr int BM = 128;
+constexpr int BN = 128;
+constexpr int kThreads = 256;
+
+struct GemmParams {
+    const void* A;
+    const void* B;
+    void* C;
+    const float* bias;
+    float* partial;        // split-K workspace [splits][M][N] (nullptr: write C)
+    int64_t lda, ldb, ldc;
+    int64_t stride_a, stride_b, stride_c;  // batch strides (elements)
+    int M, N, K;
+    int tiles_m, tiles_n;
+    int k_per_split;       // multiple of the k block
+    float alpha, beta;
+    int epi;
+    int out_bf16;
+    int vec_a, vec_b;      // 16-byte vector loads legal for A / B
+};
+
+// Remap a linear workgroup id so that the ids one XCD receives (id % 8 == x)
+// cover a contiguous range of tiles, then order tiles in groups of GROUP_M
+// tile-rows so concurrently running workgroups share A and B panels.
+__device__ __forceinline__ void tile_coords(int wg, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int total = tiles_m * tiles_n;
+    int id = wg;
+    if ((total & 7) == 0) id = (wg & 7) * (total >> 3) + (wg >> 3);
+    constexpr int GROUP_M = 4;
+    const int group_size = GROUP_M * tiles_n;
+    const int g = id / group_size;
+    const int first_m = g * GROUP_M;
+    const int gm = min(tiles_m - first_m, GROUP_M);
+    const int in_g = id - g * group_size;
+    tm = first_m + in_g % gm;
+    tn = in_g / gm;
+}
+
+// ---------------------------------------------------------------------------
+// Operand staging.  ELEM = float (fp32 path) or uint16_t (bf16 bits).
+// A "tile" is 128 rows x BK k.  K-major LDS layout: [128][BK + PADK];
+// MN-major: [BK][128 + PADM].
+// ---------------------------------------------------------------------------
+template <typename ELEM, int BK, bool KMAJ>
+struct Stage {
+    static constexpr int VEC = 16 / sizeof(ELEM);            // elements per 16 B
+    static constexpr int PADK = (sizeof(ELEM) == 4) ? 4 : 8;  // keeps b128 reads conflict-free
+    static constexpr int PADM = (sizeof(ELEM) == 4) ? 2 : 4;  // halves 16 rows apart land in other banks
+    static constexpr int LD = KMAJ ? (BK + PADK) : (128 + PADM);
+    static constexpr int LDS_ELEMS = KMAJ ? 128 * LD : BK * LD;
+    static constexpr int ELEMS_PER_THREAD = 128 * BK / kThreads;
+    static constexpr int LOADS = ELEMS_PER_THREAD / VEC;      // 16-byte loads per thread
+
+    uint4 reg[LOADS];
+
+    // Global -> registers for the tile whose first row is row0 and first k is k0.
+    // rows: valid row count of the operand; kend: end of this split's k range.
+    __device__ __forceinline__ void load(const ELEM* __restrict__ p, int64_t ld, int row0, int rows,
+                                         int k0, int kend, bool vec_ok) {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            int r, k;
+            if (KMAJ) {
+                constexpr int TPR = BK / VEC;          // threads per row
+                r = row0 + t / TPR + (kThreads / TPR) * i;
+                k = k0 + (t % TPR) * VEC;
+            } else {
+                constexpr int TPR = 128 / VEC;         // threads per k-row
+                k = k0 + t / TPR + (kThreads / TPR) * i;
+                r = row0 + (t % TPR) * VEC;
+            }
+            const bool full = KMAJ ? (r < rows && k + VEC <= kend) : (k < kend && r + VEC <= rows);
+            if (vec_ok && full) {
+                const ELEM* src = KMAJ ? p + (int64_t)r * ld + k : p + (int64_t)k * ld + r;
+                reg[i] = *reinterpret_cast<const uint4*>(src);
+            } else {
+                ELEM tmp[VEC];
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) {
+                    int rr = KMAJ ? r : r + v;
+                    int kk = KMAJ ? k + v : k;
+                    bool ok = rr < rows && kk < kend;
+                    tmp[v] = ok ? (KMAJ ? p[(int64_t)rr * ld + kk] : p[(int64_t)kk * ld + rr]) : ELEM(0);
+                }
+                reg[i] = *reinterpret_cast<uint4*>(tmp);
+            }
+        }
+    }
+
+    // Registers -> LDS (same thread mapping as load()).
+    __device__ __forceinline__ void store(ELEM* __restrict__ lds) const {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            if (KMAJ) {
+                constexpr int TPR = BK / VEC;
+                int r = t / TPR + (kThreads / TPR) * i;
+                int k = (t % TPR) * VEC;
+                *reinterpret_cast<uint4*>(lds + r * LD + k) = reg[i];
+            } else {
+                constexpr int TPR = 128 / VEC;
+                int k = t / TPR + (kThreads / TPR) * i;
+                int r = (t % TPR) * VEC;
+                // Rows are 8-byte aligned only (padding), so store as 2 x 8 B.
+                uint2* dst = reinterpret_cast<uint2*>(lds + k * LD + r);
+                dst[0] = make_uint2(reg[i].x, reg[i].y);
+                dst[1] = make_uint2(reg[i].z, reg[i].w);
+            }
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Epilogue for one 32 x 32 accumulator tile held in the v_mfma 32x32 layout:
+// lane l, register r  ->  row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void store_tile(const GemmParams& p, const v16f& acc, int row0, int col0,
+                                           int64_t batch_off_c, int split) {
+    const int lane = threadIdx.x & 63;
+    const int col = col0 + (lane & 31);
+    if (col >= p.N) return;
+    const int rbase = row0 + 4 * (lane >> 5);
+    if (p.partial) {
+        float* dst = p.partial + (int64_t)split * p.M * p.N;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            int row = rbase + 8 * (r >> 2) + (r & 3);
+            if (row < p.M) dst[(int64_t)row * p.N + col] = acc[r];
+        }
+        return;
+    }
+    const float b = (p.epi == TF_EPI_BIAS || p.epi == TF_EPI_BIAS_RELU) ? p.bias[col] : 0.0f;
+    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        int row = rbase + 8 * (r >> 2) + (r & 3);
+        if (row >= p.M) continue;
+        int64_t off = batch_off_c + (int64_t)row * p.ldc + col;
+        float v = p.alpha * acc[r];
+        if (p.beta != 0.0f) v += p.beta * reinterpret_cast<const float*>(p.C)[off];
+        v += b;
+        if (relu) v = fmaxf(v, 0.0f);
+        if (p.out_bf16) reinterpret_cast<uint16_t*>(p.C)[off] = tfd::f32_to_bf16(v);
+        else reinterpret_cast<float*>(p.C)[off] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 kernel: BK = 32, v_mfma_f32_32x32x2_f32.
+// ---------------------------------------------------------------------------
+template <bool A_KMAJ, bool B_KMAJ>
+__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
+    constexpr int BK = 32;
+    using SA = Stage<float, BK, A_KMAJ>;
+    using SB = Stage<float, BK, B_KMAJ>;
+    __shared__ __attribute__((aligned(16))) float lds_a[2][SA::LDS_ELEMS];
+    __shared__ __attribute__((aligned(16))) float lds_b[2][SB::LDS_ELEMS];
+
+    int tm, tn;
+    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int split = blockIdx.y;
+    const int batch = blockIdx.z;
+    const float* A = reinterpret_cast<const float*>(p.A) + (int64_t)batch * p.stride_a;
+    const float* B = reinterpret_cast<const float*>(p.B) + (int64_t)batch * p.stride_b;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int kbeg = split * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
+    const int nk = (kend - kbeg + BK - 1) / BK;
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int half = lane >> 5, l32 = lane & 31;
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+
+    SA sa;
+    SB sb;
+    if (nk > 0) {
+        sa.load(A, p.lda, m0, p.M, kbeg, kend, p.vec_a);
+        sb.load(B, p.ldb, n0, p.N, kbeg, kend, p.vec_b);
+        sa.store(lds_a[0]);
+        sb.store(lds_b[0]);
+    }
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            const int k0 = kbeg + (kt + 1) * BK;
+            sa.load(A, p.lda, m0, p.M, k0, kend, p.vec_a);
+            sb.load(B, p.ldb, n0, p.N, k0, kend, p.vec_b);
+        }
+        // Fragments: lane supplies k = 16*half + s to the s-th MFMA.
+        float fa[2][16], fb[2][16];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row = wm * 64 + i * 32 + l32;
+            if (A_KMAJ) {
+                const float* src = &lds_a[cur][row * SA::LD + 16 * half];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
+                    fa[i][4 * q + 0] = v.x; fa[i][4 * q + 1] = v.y;
+                    fa[i][4 * q + 2] = v.z; fa[i][4 * q + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < 16; ++s) fa[i][s] = lds_a[cur][(16 * half + s) * SA::LD + row];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = wn * 64 + j * 32 + l32;
+            if (B_KMAJ) {
+                const float* src = &lds_b[cur][col * SB::LD + 16 * half];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
+                    fb[j][4 * q + 0] = v.x; fb[j][4 * q + 1] = v.y;
+                    fb[j][4 * q + 2] = v.z; fb[j][4 * q + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < 16; ++s) fb[j][s] = lds_b[cur][(16 * half + s) * SB::LD + col];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+        if (more) {
+            sa.store(lds_a[cur ^ 1]);
+            sb.store(lds_b[cur ^ 1]);
+        }
+        __syncthreads();
+    }
+
+    const int64_t boff = (int64_t)batch * p.stride_c;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            store_tile(p, acc[i][j], m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, boff, split);
+}
+
+// ---------------------------------------------------------------------------
+// bf16 kernel: BK = 64, v_mfma_f32_32x32x16_bf16 (lane supplies 8 consecutive
+// k: lanes 0-31 k = 0..7, lanes 32-63 k = 8..15 of each 16-deep step).
+// ---------------------------------------------------------------------------
+template <bool A_KMAJ, bool B_KMAJ>
+__global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(GemmParams p) {
+    constexpr int BK = 64;
+    using SA = Stage<uint16_t, BK, A_KMAJ>;
+    using SB = Stage<uint16_t, BK, B_KMAJ>;
+    __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][SA::LDS_ELEMS];
+    __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][SB::LDS_ELEMS];
+
+    int tm, tn;
+    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int split = blockIdx.y;
+    const int batch = blockIdx.z;
+    const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A) + (int64_t)batch * p.stride_a;
+    const uint16_t* B = reinterpret_cast<const uint16_t*>(p.B) + (int64_t)batch * p.stride_b;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int kbeg = split * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
+    const int nk = (kend - kbeg + BK - 1) / BK;
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int half = lane >> 5, l32 = lane & 31;
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+
+    SA sa;
+    SB sb;
+    if (nk > 0) {
+        sa.load(A, p.lda, m0, p.M, kbeg, kend, p.vec_a);
+        sb.load(B, p.ldb, n0, p.N, kbeg, kend, p.vec_b);
+        sa.store(lds_a[0]);
+        sb.store(lds_b[0]);
+    }
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            const int k0 = kbeg + (kt + 1) * BK;
+            sa.load(A, p.lda, m0, p.M, k0, kend, p.vec_a);
+            sb.load(B, p.ldb, n0, p.N, k0, kend, p.vec_b);
+        }
+#pragma unroll
+        for (int s = 0; s < BK / 16; ++s) {
+            v8bf fa[2], fb[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int row = wm * 64 + i * 32 + l32;
+                const int kk = 16 * s + 8 * half;
+                if (A_KMAJ) {
+                    fa[i] = *reinterpret_cast<const v8bf*>(&lds_a[cur][row * SA::LD + kk]);
+                } else {
+                    uint16_t t[8];
+#pragma unroll
+                    for (int v = 0; v < 8; ++v) t[v] = lds_a[cur][(kk + v) * SA::LD + row];
+                    fa[i] = *reinterpret_cast<v8bf*>(t);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int col = wn * 64 + j * 32 + l32;
+                const int kk = 16 * s + 8 * half;
+                if (B_KMAJ) {
+                    fb[j] = *reinterpret_cast<const v8bf*>(&lds_b[cur][col * SB::LD + kk]);
+                } else {
+                    uint16_t t[8];
+#pragma unroll
+                    for (int v = 0; v < 8; ++v) t[v] = lds_b[cur][(kk + v) * SB::LD + col];
+                    fb[j] = *reinterpret_cast<v8bf*>(t);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            sa.store(lds_a[cur ^ 1]);
+            sb.store(lds_b[cur ^ 1]);
+        }
+        __syncthreads();
+    }
+
+    const int64_t boff = (int64_t)batch * p.stride_c;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            store_tile(p, acc[i][j], m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, boff, split);
+}
+
+// Split-K reduction: C = epi(alpha * sum_s partial[s] + beta * C), summing the
+// splits in ascending order (deterministic).
+__global__ void splitk_reduce_kernel(GemmParams p, int splits) {
+    const int64_t total = (int64_t)p.M * p.N;
+    const int64_t plane = total;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU;
+    const bool has_bias = p.epi == TF_EPI_BIAS || p.epi == TF_EPI_BIAS_RELU;
+    for (; i < total; i += stride) {
+        float s = 0.0f;
+        for (int k = 0; k < splits; ++k) s += p.partial[k * plane + i];
+        const int row = (int)(i / p.N), col = (int)(i - (int64_t)row * p.N);
+        const int64_t off = (int64_t)row * p.ldc + col;
+        float v = p.alpha * s;
+        if (p.beta != 0.0f) v += p.beta * reinterpret_cast<const float*>(p.C)[off];
+        if (has_bias) v += p.bias[col];
+        if (relu) v = fmaxf(v, 0.0f);
+        if (p.out_bf16) reinterpret_cast<uint16_t*>(p.C)[off] = tfd::f32_to_bf16(v);
+        else reinterpret_cast<float*>(p.C)[off] = v;
+    }
+}
+
+using KernelFn = void (*)(GemmParams);
+
+KernelFn pick_f32(bool a_kmaj, bool b_kmaj) {
+    if (a_kmaj && b_kmaj) return gemm_f32_kernel<true, true>;
+    if (a_kmaj && !b_kmaj) return gemm_f32_kernel<true, false>;
+    if (!a_kmaj && b_kmaj) return gemm_f32_kernel<false, true>;
+    return gemm_f32_kernel<false, false>;
+}
+
+KernelFn pick_bf16(bool a_kmaj, bool b_kmaj) {
+    if (a_kmaj && b_kmaj) return gemm_bf16_kernel<true, true>;
+    if (a_kmaj && !b_kmaj) return gemm_bf16_kernel<true, false>;
+    if (!a_kmaj && b_kmaj) return gemm_bf16_kernel<false, true>;
+    return gemm_bf16_kernel<false, false>;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                    const void* A, int64_t lda, int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b,
+                    float beta, void* C, int64_t ldc, int64_t stride_c, int64_t batch, int in_dtype,
+                    int out_dtype, int epi, const float* bias) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "tf_gemm: negative extent");
+    TF_REQUIRE(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31), "tf_gemm: extent exceeds 2^31");
+    if (M == 0 || N == 0 || batch == 0) return TF_OK;
+    TF_REQUIRE(A && B && C, "tf_gemm: null matrix pointer");
+    TF_REQUIRE(in_dtype == TF_F32 || in_dtype == TF_BF16, "tf_gemm: in_dtype must be Float32 or BFloat16");
+    TF_REQUIRE(out_dtype == TF_F32 || out_dtype == TF_BF16, "tf_gemm: out_dtype must be Float32 or BFloat16");
+    TF_REQUIRE(beta == 0.0f || out_dtype == TF_F32, "tf_gemm: beta != 0 needs a Float32 output");
+    TF_REQUIRE(epi >= TF_EPI_NONE && epi <= TF_EPI_RELU, "tf_gemm: bad epilogue");
+    TF_REQUIRE(!(epi == TF_EPI_BIAS || epi == TF_EPI_BIAS_RELU) || bias != nullptr, "tf_gemm: epilogue needs bias");
+    // Leading dimensions must cover the stored row length.
+    TF_REQUIRE(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N) && ldc >= N, "tf_gemm: leading dimension too small");
+
+    const bool a_kmaj = trans_a == 0;  // A[m*lda + k]
+    const bool b_kmaj = trans_b != 0;  // B[n*ldb + k]
+    const int esz = in_dtype == TF_F32 ? 4 : 2;
+    const int vec_elems = 16 / esz;
+    const int BK = in_dtype == TF_F32 ? 32 : 64;
+
+    GemmParams p{};
+    p.A = A; p.B = B; p.C = C; p.bias = bias; p.partial = nullptr;
+    p.lda = lda; p.ldb = ldb; p.ldc = ldc;
+    p.stride_a = stride_a; p.stride_b = stride_b; p.stride_c = stride_c;
+    p.M = (int)M; p.N = (int)N; p.K = (int)K;
+    p.tiles_m = (int)((M + BM - 1) / BM);
+    p.tiles_n = (int)((N + BN - 1) / BN);
+    p.alpha = alpha; p.beta = beta; p.epi = epi;
+    p.out_bf16 = out_dtype == TF_BF16;
+    p.vec_a = aligned16(A) && (lda % vec_elems == 0) && (stride_a % vec_elems == 0);
+    p.vec_b = aligned16(B) && (ldb % vec_elems == 0) && (stride_b % vec_elems == 0);
+
+    const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+    TF_REQUIRE(tiles < (1LL << 31), "tf_gemm: too many tiles");
+
+    // Split K when one batch of tiles leaves most CUs idle and K is long.
+    int splits = 1;
+    const int64_t kblocks = (K + BK - 1) / BK;
+    if (batch == 1 && tiles * 2 <= ctx->num_cus && kblocks >= 8) {
+        int64_t want = (ctx->num_cus + tiles - 1) / tiles;     // fill the CUs once
+        int64_t max_by_k = kblocks / 4;                         // keep >= 4 k blocks per split
+        splits = (int)std::max<int64_t>(1, std::min<int64_t>({want, max_by_k, 64}));
+    }
+    if (kblocks == 0) {
+        splits = 1;
+        p.k_per_split = 0;
+    } else {
+        int64_t kblk_per_split = (kblocks + splits - 1) / splits;
+        splits = (int)((kblocks + kblk_per_split - 1) / kblk_per_split);
+        p.k_per_split = (int)(kblk_per_split * BK);
+    }
+
+    if (splits > 1) {
+        size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(float);
+        tf_status st = tfh::ensure_workspace(ctx, need);
+        if (st != TF_OK) return st;
+        p.partial = reinterpret_cast<float*>(ctx->ws);
+    }
+
+    KernelFn fn = in_dtype == TF_F32 ? pick_f32(a_kmaj, b_kmaj) : pick_bf16(a_kmaj, b_kmaj);
+    TF_REQUIRE(batch < 65536 && splits < 65536, "tf_gemm: grid too large");
+    dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)batch);
+    fn<<<grid, kThreads, 0, ctx->stream>>>(p);
+    tf_status st = tfh::check_launch("gemm kernel");
+    if (st != TF_OK) return st;
+    if (splits > 1) {
+        splitk_reduce_kernel<<<tfd::grid_for(M * N, 4), 256, 0, ctx->stream>>>(p, splits);
+        st = tfh::check_launch("splitk_reduce_kernel");
+    }
+    return st;
+}
+
+}  // namespace
+
+extern "C" {
+
+tf_status tf_gemm(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                  const void* A, int64_t lda, const void* B, int64_t ldb, float beta, void* C, int64_t ldc,
+                  int in_dtype, int out_dtype, int epilogue, const float* bias) {
+    return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1,
+                     in_dtype, out_dtype, epilogue, bias);
+}
+
+tf_status tf_gemm_strided_batched(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                                  float alpha, const void* A, int64_t lda, int64_t stride_a, const void* B,
+                                  int64_t ldb, int64_t stride_b, float beta, void* C, int64_t ldc,
+                                  int64_t stride_c, int64_t batch, int in_dtype, int out_dtype) {
+    return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
+                     stride_c, batch, in_dtype, out_dtype, TF_EPI_NONE, nullptr);
+}
+
+}  // extern "C"

@@ -1,0 +1,419 @@
+// Row kernels: cross-entropy forward/backward (fused LogSoftmax+NLL),
+// log_softmax / softmax forward and backward.  One wave64 per row, 4 rows per
+// 256-thread block.  Rows of up to kMaxCached * 256 columns stay in registers
+// (one HBM read per pass); wider rows are streamed twice.
+//
+// Element mapping inside a row: chunk c covers columns [256c, 256c + 256).
+// With 16-byte aligned rows lane l owns columns 256c + 4l .. 4l+3 (one
+// float4); otherwise lane l owns 256c + l + 64q, q = 0..3.  Both cover every
+// column exactly once, so the same code handles ragged widths.
+#include "common.hpp"
+
+#include <cmath>
+
+namespace {
+
+constexpr int kRowsPerBlock = 4;
+constexpr int kMaxCached = 8;  // 2048 columns cached in registers
+
+__device__ __forceinline__ int col_of(int c, int lane, int q, bool vec) {
+    return vec ? 256 * c + 4 * lane + q : 256 * c + lane + 64 * q;
+}
+
+template <int NC>
+__device__ __forceinline__ void load_row(const float* __restrict__ row, int cols, int lane, bool vec,
+                                         float (&v)[NC][4], float fill) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        int base = 256 * c + 4 * lane;
+        if (vec && base + 4 <= cols) {
+            float4 t = *reinterpret_cast<const float4*>(row + base);
+            v[c][0] = t.x; v[c][1] = t.y; v[c][2] = t.z; v[c][3] = t.w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                int j = col_of(c, lane, q, vec);
+                v[c][q] = j < cols ? row[j] : fill;
+            }
+        }
+    }
+}
+
+template <int NC>
+__device__ __forceinline__ void store_row(float* __restrict__ row, int cols, int lane, bool vec,
+                                          const float (&v)[NC][4]) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        int base = 256 * c + 4 * lane;
+        if (vec && base + 4 <= cols) {
+            *reinterpret_cast<float4*>(row + base) = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                int j = col_of(c, lane, q, vec);
+                if (j < cols) row[j] = v[c][q];
+            }
+        }
+    }
+}
+
+// Row statistics of a streamed (uncached) row: max and sum exp(x - max),
+// online over 256-column chunks.
+__device__ __forceinline__ void stream_stats(const float* __restrict__ row, int cols, int lane, bool vec,
+                                             float& mx, float& sum) {
+    float m = -INFINITY, s = 0.0f;
+    for (int c = 0; 256 * c < cols; ++c) {
+        float v[1][4];
+        // load one chunk at offset 256c
+        const float* base = row + 256 * c;
+        load_row<1>(base, cols - 256 * c, lane, vec, v, -INFINITY);
+        float cm = fmaxf(fmaxf(v[0][0], v[0][1]), fmaxf(v[0][2], v[0][3]));
+        float nm = fmaxf(m, cm);
+        if (nm != -INFINITY) {
+            s = s * __expf(m - nm);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s += __expf(v[0][q] - nm);
+        }
+        m = nm;
+    }
+    // combine lanes: each lane has (m, s); rescale to the wave max.
+    float gm = tfd::wave_max(m);
+    s = (m == -INFINITY) ? 0.0f : s * __expf(m - gm);
+    sum = tfd::wave_sum(s);
+    mx = gm;
+}
+
+// ---------------------------------------------------------------------------
+// Cross entropy.  MODE 0: forward only (lse, per-row nll).  MODE 1: backward
+// only (dlogits).  MODE 2: fused forward + backward.
+// nll[r] = lse_r - x[r, t_r] (0 for a target outside [0, cols), whose row
+// also receives a zero gradient: the train_mlp chain's one-hot mask skips
+// such labels, examples/train_mlp.cpp:60-66).
+// dlogits = scale * (exp(x - lse) - onehot), scale = g / rows.
+// ---------------------------------------------------------------------------
+template <int NC, int MODE>
+__global__ __launch_bounds__(256) void ce_kernel(const float* __restrict__ logits, const int64_t* __restrict__ targets,
+                                                 const float* __restrict__ lse_in, const float* __restrict__ grad_loss,
+                                                 float* __restrict__ lse_out, float* __restrict__ nll,
+                                                 float* __restrict__ dlogits, int rows, int cols, float inv_rows,
+                                                 int vec) {
+    constexpr int NCC = NC > 0 ? NC : 1;
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float* x = logits + (int64_t)r * cols;
+    const int64_t t = targets[r];
+    const bool t_ok = t >= 0 && t < cols;
+
+    float lse;
+    float v[NCC][4];
+    if constexpr (NC > 0) {
+        load_row<NCC>(x, cols, lane, vec, v, -INFINITY);
+    }
+    if (MODE == 1 && lse_in != nullptr) {
+        lse = lse_in[r];
+    } else if constexpr (NC > 0) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) m = fmaxf(m, v[c][q]);
+        m = tfd::wave_max(m);
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s += __expf(v[c][q] - m);
+        s = tfd::wave_sum(s);
+        lse = m + __logf(s);
+    } else {
+        float m, s;
+        stream_stats(x, cols, lane, vec, m, s);
+        lse = m + __logf(s);
+    }
+
+    if (MODE != 1) {
+        if (lane == 0) {
+            if (lse_out) lse_out[r] = lse;
+            nll[r] = t_ok ? lse - x[t] : 0.0f;
+        }
+    }
+    if (MODE != 0) {
+        const float g = grad_loss ? grad_loss[0] : 1.0f;
+        const float scale = t_ok ? g * inv_rows : 0.0f;
+        float* dx = dlogits + (int64_t)r * cols;
+        if constexpr (NC > 0) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    int j = col_of(c, lane, q, vec);
+                    float pj = __expf(v[c][q] - lse);
+                    v[c][q] = pj * scale - (j == t ? scale : 0.0f);
+                }
+            store_row<NCC>(dx, cols, lane, vec, v);
+        } else {
+            for (int c = 0; 256 * c < cols; ++c) {
+                float w[1][4];
+                load_row<1>(x + 256 * c, cols - 256 * c, lane, vec, w, -INFINITY);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    int j = 256 * c + col_of(0, lane, q, vec);
+                    float pj = __expf(w[0][q] - lse);
+                    w[0][q] = pj * scale - (j == t ? scale : 0.0f);
+                }
+                store_row<1>(dx + 256 * c, cols - 256 * c, lane, vec, w);
+            }
+        }
+    }
+}
+
+// loss[0] = (sum_r nll[r]) * inv_rows, one block, fixed reduction order.
+__global__ __launch_bounds__(256) void mean_kernel(const float* __restrict__ nll, int rows, float inv_rows,
+                                                   float* __restrict__ loss) {
+    __shared__ float part[4];
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < rows; i += 256) s += nll[i];
+    s = tfd::wave_sum(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) loss[0] = ((part[0] + part[1]) + (part[2] + part[3])) * inv_rows;
+}
+
+// ---------------------------------------------------------------------------
+// log_softmax / softmax forward (tensor/Tensor.cpp:370-447) and backward
+// (autograd/ops/LogSoftmaxBackward.hpp:26-58, SoftmaxBackward.hpp:27-55).
+// KIND 0: y = x - lse.   KIND 1: y = exp(x - max) / sum.
+// ---------------------------------------------------------------------------
+template <int NC, int KIND>
+__global__ __launch_bounds__(256) void softmax_fwd_kernel(const float* __restrict__ xs, float* __restrict__ ys,
+                                                          int rows, int cols, int vec) {
+    constexpr int NCC = NC > 0 ? NC : 1;
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float* x = xs + (int64_t)r * cols;
+    float* y = ys + (int64_t)r * cols;
+    if constexpr (NC > 0) {
+        float v[NCC][4];
+        load_row<NCC>(x, cols, lane, vec, v, -INFINITY);
+        float m = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) m = fmaxf(m, v[c][q]);
+        m = tfd::wave_max(m);
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s += __expf(v[c][q] - m);
+        s = tfd::wave_sum(s);
+        const float lz = m + __logf(s), inv = 1.0f / s;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[c][q] = KIND == 0 ? v[c][q] - lz : __expf(v[c][q] - m) * inv;
+        store_row<NCC>(y, cols, lane, vec, v);
+    } else {
+        float m, s;
+        stream_stats(x, cols, lane, vec, m, s);
+        const float lz = m + __logf(s), inv = 1.0f / s;
+        for (int c = 0; 256 * c < cols; ++c) {
+            float w[1][4];
+            load_row<1>(x + 256 * c, cols - 256 * c, lane, vec, w, -INFINITY);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) w[0][q] = KIND == 0 ? w[0][q] - lz : __expf(w[0][q] - m) * inv;
+            store_row<1>(y + 256 * c, cols - 256 * c, lane, vec, w);
+        }
+    }
+}
+
+// KIND 0 (log_softmax): dx = dy - exp(y) * sum(dy).
+// KIND 1 (softmax):     dx = y * (dy - sum(dy * y)).
+template <int NC, int KIND>
+__global__ __launch_bounds__(256) void softmax_bwd_kernel(const float* __restrict__ ys, const float* __restrict__ dys,
+                                                          float* __restrict__ dxs, int rows, int cols, int vec) {
+    constexpr int NCC = NC > 0 ? NC : 1;
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float* y = ys + (int64_t)r * cols;
+    const float* dy = dys + (int64_t)r * cols;
+    float* dx = dxs + (int64_t)r * cols;
+    if constexpr (NC > 0) {
+        float yv[NCC][4], gv[NCC][4];
+        load_row<NCC>(y, cols, lane, vec, yv, 0.0f);
+        load_row<NCC>(dy, cols, lane, vec, gv, 0.0f);
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s += KIND == 0 ? gv[c][q] : gv[c][q] * yv[c][q];
+        s = tfd::wave_sum(s);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                gv[c][q] = KIND == 0 ? gv[c][q] - expf(yv[c][q]) * s : yv[c][q] * (gv[c][q] - s);
+        store_row<NCC>(dx, cols, lane, vec, gv);
+    } else {
+        float s = 0.0f;
+        for (int c = 0; 256 * c < cols; ++c) {
+            float a[1][4], b[1][4];
+            load_row<1>(y + 256 * c, cols - 256 * c, lane, vec, a, 0.0f);
+            load_row<1>(dy + 256 * c, cols - 256 * c, lane, vec, b, 0.0f);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s += KIND == 0 ? b[0][q] : b[0][q] * a[0][q];
+        }
+        s = tfd::wave_sum(s);
+        for (int c = 0; 256 * c < cols; ++c) {
+            float a[1][4], b[1][4];
+            load_row<1>(y + 256 * c, cols - 256 * c, lane, vec, a, 0.0f);
+            load_row<1>(dy + 256 * c, cols - 256 * c, lane, vec, b, 0.0f);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) b[0][q] = KIND == 0 ? b[0][q] - expf(a[0][q]) * s : a[0][q] * (b[0][q] - s);
+            store_row<1>(dx + 256 * c, cols - 256 * c, lane, vec, b);
+        }
+    }
+}
+
+bool row_vec_ok(const void* p, int64_t cols) {
+    return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && (cols % 4) == 0;
+}
+
+// Number of register-cached 256-column chunks for a row width (0 = stream).
+int chunks_for(int64_t cols) {
+    int64_t c = (cols + 255) / 256;
+    if (c <= 1) return 1;
+    if (c <= 2) return 2;
+    if (c <= 4) return 4;
+    if (c <= kMaxCached) return kMaxCached;
+    return 0;
+}
+
+template <int MODE>
+tf_status launch_ce(tf_ctx* ctx, const float* logits, const int64_t* targets, const float* lse_in,
+                    const float* grad_loss, float* lse_out, float* nll, float* dlogits, int64_t rows, int64_t cols) {
+    const int vec = row_vec_ok(logits, cols) && (dlogits == nullptr || row_vec_ok(dlogits, cols));
+    const float inv_rows = (float)(1.0 / (double)rows);
+    dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+#define TF_CE_LAUNCH(NC)                                                                              \
+    ce_kernel<NC, MODE><<<grid, 256, 0, ctx->stream>>>(logits, targets, lse_in, grad_loss, lse_out, nll, \
+                                                         dlogits, (int)rows, (int)cols, inv_rows, vec)
+    switch (chunks_for(cols)) {
+    case 1: TF_CE_LAUNCH(1); break;
+    case 2: TF_CE_LAUNCH(2); break;
+    case 4: TF_CE_LAUNCH(4); break;
+    case kMaxCached: TF_CE_LAUNCH(kMaxCached); break;
+    default: TF_CE_LAUNCH(0); break;
+    }
+#undef TF_CE_LAUNCH
+    return tfh::check_launch("ce_kernel");
+}
+
+tf_status check_rows(tf_ctx* ctx, int64_t rows, int64_t cols) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(rows >= 0 && cols >= 0, "row kernel: negative extent");
+    TF_REQUIRE(rows < (1LL << 31) && cols < (1LL << 31), "row kernel: extent exceeds 2^31");
+    return TF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+tf_status tf_ce_fwd(tf_ctx* ctx, const float* logits, const int64_t* targets, float* loss, float* lse,
+                    int64_t rows, int64_t cols) {
+    tf_status st = check_rows(ctx, rows, cols);
+    if (st != TF_OK) return st;
+    TF_REQUIRE(rows > 0 && cols > 0, "tf_ce_fwd: empty logits");
+    TF_REQUIRE(logits && targets && loss, "tf_ce_fwd: null pointer");
+    st = tfh::ensure_workspace(ctx, (size_t)rows * sizeof(float));
+    if (st != TF_OK) return st;
+    float* nll = reinterpret_cast<float*>(ctx->ws);
+    st = launch_ce<0>(ctx, logits, targets, nullptr, nullptr, lse, nll, nullptr, rows, cols);
+    if (st != TF_OK) return st;
+    mean_kernel<<<1, 256, 0, ctx->stream>>>(nll, (int)rows, (float)(1.0 / (double)rows), loss);
+    return tfh::check_launch("mean_kernel");
+}
+
+tf_status tf_ce_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets, const float* lse,
+                    const float* grad_loss, float* dlogits, int64_t rows, int64_t cols) {
+    tf_status st = check_rows(ctx, rows, cols);
+    if (st != TF_OK) return st;
+    if (rows == 0 || cols == 0) return TF_OK;
+    TF_REQUIRE(logits && targets && dlogits, "tf_ce_bwd: null pointer");
+    return launch_ce<1>(ctx, logits, targets, lse, grad_loss, nullptr, nullptr, dlogits, rows, cols);
+}
+
+tf_status tf_ce_fwd_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets, float* loss, float* dlogits,
+                        int64_t rows, int64_t cols) {
+    tf_status st = check_rows(ctx, rows, cols);
+    if (st != TF_OK) return st;
+    TF_REQUIRE(rows > 0 && cols > 0, "tf_ce_fwd_bwd: empty logits");
+    TF_REQUIRE(logits && targets && loss && dlogits, "tf_ce_fwd_bwd: null pointer");
+    st = tfh::ensure_workspace(ctx, (size_t)rows * sizeof(float));
+    if (st != TF_OK) return st;
+    float* nll = reinterpret_cast<float*>(ctx->ws);
+    st = launch_ce<2>(ctx, logits, targets, nullptr, nullptr, nullptr, nll, dlogits, rows, cols);
+    if (st != TF_OK) return st;
+    mean_kernel<<<1, 256, 0, ctx->stream>>>(nll, (int)rows, (float)(1.0 / (double)rows), loss);
+    return tfh::check_launch("mean_kernel");
+}
+
+#define TF_ROW_LAUNCH(KERNEL, KIND, ...)                                          \
+    do {                                                                          \
+        dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));        \
+        switch (chunks_for(cols)) {                                               \
+        case 1: KERNEL<1, KIND><<<grid, 256, 0, ctx->stream>>>(__VA_ARGS__); break; \
+        case 2: KERNEL<2, KIND><<<grid, 256, 0, ctx->stream>>>(__VA_ARGS__); break; \
+        case 4: KERNEL<4, KIND><<<grid, 256, 0, ctx->stream>>>(__VA_ARGS__); break; \
+        case kMaxCached: KERNEL<kMaxCached, KIND><<<grid, 256, 0, ctx->stream>>>(__VA_ARGS__); break; \
+        default: KERNEL<0, KIND><<<grid, 256, 0, ctx->stream>>>(__VA_ARGS__); break; \
+        }                                                                         \
+    } while (0)
+
+tf_status tf_log_softmax_fwd(tf_ctx* ctx, const float* x, float* y, int64_t rows, int64_t cols) {
+    tf_status st = check_rows(ctx, rows, cols);
+    if (st != TF_OK) return st;
+    if (rows == 0 || cols == 0) return TF_OK;
+    TF_REQUIRE(x && y, "tf_log_softmax_fwd: null pointer");
+    int vec = row_vec_ok(x, cols) && row_vec_ok(y, cols);
+    TF_ROW_LAUNCH(softmax_fwd_kernel, 0, x, y, (int)rows, (int)cols, vec);
+    return tfh::check_launch("softmax_fwd_kernel");
+}
+
+tf_status tf_softmax_fwd(tf_ctx* ctx, const float* x, float* y, int64_t rows, int64_t cols) {
+    tf_status st = check_rows(ctx, rows, cols);
+    if (st != TF_OK) return st;
+    if (rows == 0 || cols == 0) return TF_OK;
+    TF_REQUIRE(x && y, "tf_softmax_fwd: null pointer");
+    int vec = row_vec_ok(x, cols) && row_vec_ok(y, cols);
+    TF_ROW_LAUNCH(softmax_fwd_kernel, 1, x, y, (int)rows, (int)cols, vec);
+    return tfh::check_launch("softmax_fwd_kernel");
+}
+
+tf_status tf_log_softmax_bwd(tf_ctx* ctx, const float* y, const float* dy, float* dx, int64_t rows, int64_t cols) {
+    tf_status st = check_rows(ctx, rows, cols);
+    if (st != TF_OK) return st;
+    if (rows == 0 || cols == 0) return TF_OK;
+    TF_REQUIRE(y && dy && dx, "tf_log_softmax_bwd: null pointer");
+    int vec = row_vec_ok(y, cols) && row_vec_ok(dy, cols) && row_vec_ok(dx, cols);
+    TF_ROW_LAUNCH(softmax_bwd_kernel, 0, y, dy, dx, (int)rows, (int)cols, vec);
+    return tfh::check_launch("softmax_bwd_kernel");
+}
+
+tf_status tf_softmax_bwd(tf_ctx* ctx, const float* y, const float* dy, float* dx, int64_t rows, int64_t cols) {
+    tf_status st = check_rows(ctx, rows, cols);
+    if (st != TF_OK) return st;
+    if (rows == 0 || cols == 0) return TF_OK;
+    TF_REQUIRE(y && dy && dx, "tf_softmax_bwd: null pointer");
+    int vec = row_vec_ok(y, cols) && row_vec_ok(dy, cols) && row_vec_ok(dx, cols);
+    TF_ROW_LAUNCH(softmax_bwd_kernel, 1, y, dy, dx, (int)rows, (int)cols, vec);
+    return tfh::check_launch("softmax_bwd_kernel");
+}
+
+#undef TF_ROW_LAUNCH
+
+}  // extern "C"

@@ -1,0 +1,245 @@
+// Runtime half of the C ABI: context + stream, pool allocator, copies,
+// fills and events.  Replaces the reference's DeviceContext/CudaStream/
+// CudaEvent (cuda/CudaContext.{hpp,cpp}) and CudaStorageAllocator
+// (cuda/memory/CudaStorageAllocator.cpp:34-143).
+//
+// Design: one context per (caller, device).  Each context owns a
+// non-blocking stream at default priority and the device's memory pool with
+// an unlimited release threshold, so steady-state training steps never call
+// into the driver for memory: every tensor allocation is a hipMallocAsync
+// served from cached pool blocks, every free a hipFreeAsync.
+#include "common.hpp"
+
+#include <mutex>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+__global__ void fill_f32_kernel(float* __restrict__ p, float v, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    // float4 body over the 16-byte aligned prefix, scalar tail.
+    int64_t n4 = ((reinterpret_cast<uintptr_t>(p) & 15) == 0) ? n / 4 : 0;
+    float4* p4 = reinterpret_cast<float4*>(p);
+    for (int64_t j = i; j < n4; j += stride) p4[j] = make_float4(v, v, v, v);
+    for (int64_t j = n4 * 4 + i; j < n; j += stride) p[j] = v;
+}
+
+__global__ void zero_bytes_kernel(uint8_t* __restrict__ p, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t n16 = ((reinterpret_cast<uintptr_t>(p) & 15) == 0) ? n / 16 : 0;
+    uint4* p16 = reinterpret_cast<uint4*>(p);
+    for (size_t j = i; j < n16; j += stride) p16[j] = make_uint4(0, 0, 0, 0);
+    for (size_t j = n16 * 16 + i; j < n; j += stride) p[j] = 0;
+}
+
+}  // namespace
+
+namespace tfh {
+
+tf_status set_error(tf_status code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+tf_status hip_error(hipError_t e, const char* what) {
+    g_last_error = std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
+    return e == hipErrorOutOfMemory ? TF_ERR_OOM : TF_ERR_HIP;
+}
+
+tf_status ensure_workspace(tf_ctx* ctx, size_t bytes) {
+    if (ctx->ws_bytes >= bytes) return TF_OK;
+    if (ctx->ws) {
+        TF_HIP_CHECK(hipFreeAsync(ctx->ws, ctx->stream));
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+    }
+    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+    TF_HIP_CHECK(hipMallocFromPoolAsync(&ctx->ws, want, ctx->pool, ctx->stream));
+    ctx->ws_bytes = want;
+    return TF_OK;
+}
+
+}  // namespace tfh
+
+extern "C" {
+
+const char* tf_last_error(void) { return g_last_error.c_str(); }
+
+const char* tf_version(void) { return "tensors_amd 0.1 (gfx950)"; }
+
+tf_status tf_hip_device_count(int* count) {
+    TF_REQUIRE(count != nullptr, "tf_hip_device_count: null count");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    *count = (e == hipSuccess) ? n : 0;
+    if (e != hipSuccess) (void)hipGetLastError();
+    return TF_OK;
+}
+
+tf_status tf_hip_init(int device, tf_ctx** out) {
+    TF_REQUIRE(out != nullptr, "tf_hip_init: null out");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) {
+        (void)hipGetLastError();
+        return tfh::set_error(TF_ERR_HIP, "tf_hip_init: no HIP device visible");
+    }
+    TF_REQUIRE(device >= 0 && device < n, "tf_hip_init: device index out of range");
+    TF_HIP_CHECK(hipSetDevice(device));
+
+    tf_ctx* ctx = new tf_ctx();
+    ctx->device = device;
+    hipDeviceProp_t prop;
+    TF_HIP_CHECK(hipGetDeviceProperties(&prop, device));
+    ctx->num_cus = prop.multiProcessorCount;
+    // Default priority only: streams of mixed priority have hung these boxes.
+    TF_HIP_CHECK(hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking));
+    ctx->stream = ctx->own_stream;
+    TF_HIP_CHECK(hipDeviceGetDefaultMemPool(&ctx->pool, device));
+    uint64_t threshold = UINT64_MAX;  // keep freed blocks cached
+    TF_HIP_CHECK(hipMemPoolSetAttribute(ctx->pool, hipMemPoolAttrReleaseThreshold, &threshold));
+    *out = ctx;
+    return TF_OK;
+}
+
+tf_status tf_hip_shutdown(tf_ctx* ctx) {
+    if (ctx == nullptr) return TF_OK;
+    if (ctx->own_stream) {
+        if (ctx->ws) (void)hipFreeAsync(ctx->ws, ctx->own_stream);
+        (void)hipStreamSynchronize(ctx->own_stream);
+        (void)hipStreamDestroy(ctx->own_stream);
+    }
+    delete ctx;
+    return TF_OK;
+}
+
+tf_status tf_hip_stream(tf_ctx* ctx, void** stream) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(stream != nullptr, "tf_hip_stream: null out");
+    *stream = (void*)ctx->stream;
+    return TF_OK;
+}
+
+tf_status tf_hip_set_stream(tf_ctx* ctx, void* stream) {
+    TF_CTX_CHECK(ctx);
+    // Workspace frees are stream-ordered on the stream that last used them:
+    // order the switch so the workspace is never used on two streams at once.
+    hipStream_t next = stream ? (hipStream_t)stream : ctx->own_stream;
+    if (next != ctx->stream) TF_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    ctx->stream = next;
+    return TF_OK;
+}
+
+tf_status tf_hip_sync(tf_ctx* ctx) {
+    TF_CTX_CHECK(ctx);
+    TF_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    return TF_OK;
+}
+
+tf_status tf_hip_alloc(tf_ctx* ctx, size_t bytes, void** out) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(out != nullptr, "tf_hip_alloc: null out");
+    if (bytes == 0) bytes = 1;
+    hipError_t e = hipMallocFromPoolAsync(out, bytes, ctx->pool, ctx->stream);
+    if (e != hipSuccess) {
+        *out = nullptr;
+        return tfh::hip_error(e, "tf_hip_alloc: hipMallocFromPoolAsync");
+    }
+    return TF_OK;
+}
+
+tf_status tf_hip_free(tf_ctx* ctx, void* ptr) {
+    TF_CTX_CHECK(ctx);
+    if (ptr == nullptr) return TF_OK;
+    TF_HIP_CHECK(hipFreeAsync(ptr, ctx->stream));
+    return TF_OK;
+}
+
+tf_status tf_hip_trim(tf_ctx* ctx, size_t keep_bytes) {
+    TF_CTX_CHECK(ctx);
+    TF_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    TF_HIP_CHECK(hipMemPoolTrimTo(ctx->pool, keep_bytes));
+    return TF_OK;
+}
+
+tf_status tf_hip_pool_stats(tf_ctx* ctx, uint64_t* reserved, uint64_t* used) {
+    TF_CTX_CHECK(ctx);
+    uint64_t r = 0, u = 0;
+    TF_HIP_CHECK(hipMemPoolGetAttribute(ctx->pool, hipMemPoolAttrReservedMemCurrent, &r));
+    TF_HIP_CHECK(hipMemPoolGetAttribute(ctx->pool, hipMemPoolAttrUsedMemCurrent, &u));
+    if (reserved) *reserved = r;
+    if (used) *used = u;
+    return TF_OK;
+}
+
+tf_status tf_hip_memcpy(tf_ctx* ctx, void* dst, const void* src, size_t bytes, int kind) {
+    TF_CTX_CHECK(ctx);
+    if (bytes == 0) return TF_OK;
+    TF_REQUIRE(dst != nullptr && src != nullptr, "tf_hip_memcpy: null pointer");
+    hipMemcpyKind k;
+    switch (kind) {
+    case TF_COPY_H2H: k = hipMemcpyHostToHost; break;
+    case TF_COPY_H2D: k = hipMemcpyHostToDevice; break;
+    case TF_COPY_D2H: k = hipMemcpyDeviceToHost; break;
+    case TF_COPY_D2D: k = hipMemcpyDeviceToDevice; break;
+    default: return tfh::set_error(TF_ERR_INVALID, "tf_hip_memcpy: bad copy kind");
+    }
+    TF_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, k, ctx->stream));
+    if (kind == TF_COPY_D2H || kind == TF_COPY_H2H || kind == TF_COPY_H2D) {
+        // Host buffers are pageable and caller-owned: finish before returning.
+        TF_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    }
+    return TF_OK;
+}
+
+tf_status tf_hip_fill_f32(tf_ctx* ctx, float* p, float value, int64_t n) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(n >= 0, "tf_hip_fill_f32: negative n");
+    if (n == 0) return TF_OK;
+    TF_REQUIRE(p != nullptr, "tf_hip_fill_f32: null pointer");
+    fill_f32_kernel<<<tfd::grid_for(n, 4), 256, 0, ctx->stream>>>(p, value, n);
+    return tfh::check_launch("fill_f32_kernel");
+}
+
+tf_status tf_hip_zero(tf_ctx* ctx, void* p, size_t bytes) {
+    TF_CTX_CHECK(ctx);
+    if (bytes == 0) return TF_OK;
+    TF_REQUIRE(p != nullptr, "tf_hip_zero: null pointer");
+    zero_bytes_kernel<<<tfd::grid_for((int64_t)bytes, 16), 256, 0, ctx->stream>>>((uint8_t*)p, bytes);
+    return tfh::check_launch("zero_bytes_kernel");
+}
+
+tf_status tf_hip_event_create(tf_ctx* ctx, void** event) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(event != nullptr, "tf_hip_event_create: null out");
+    hipEvent_t e;
+    TF_HIP_CHECK(hipEventCreate(&e));
+    *event = (void*)e;
+    return TF_OK;
+}
+
+tf_status tf_hip_event_record(tf_ctx* ctx, void* event) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(event != nullptr, "tf_hip_event_record: null event");
+    TF_HIP_CHECK(hipEventRecord((hipEvent_t)event, ctx->stream));
+    return TF_OK;
+}
+
+tf_status tf_hip_event_elapsed(void* start, void* end, float* ms) {
+    TF_REQUIRE(start && end && ms, "tf_hip_event_elapsed: null argument");
+    TF_HIP_CHECK(hipEventSynchronize((hipEvent_t)end));
+    TF_HIP_CHECK(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end));
+    return TF_OK;
+}
+
+tf_status tf_hip_event_destroy(void* event) {
+    if (event == nullptr) return TF_OK;
+    TF_HIP_CHECK(hipEventDestroy((hipEvent_t)event));
+    return TF_OK;
+}
+
+}  // extern "C"

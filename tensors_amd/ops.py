@@ -1,0 +1,174 @@
+"""Python-level calls of the hot-path kernels on DeviceArrays.
+
+Each function checks shapes on the host (so a kernel is never launched on a
+shape it does not assume), then calls the C ABI.  Names follow the reference
+operations they implement; the reference file each one mirrors is cited in
+``include/tf_hip.h``.
+"""
+from __future__ import annotations
+
+from . import _lib
+from ._lib import call
+from .device import DeviceArray
+
+
+def _ctx(*arrays: DeviceArray):
+    return arrays[0].ctx.handle
+
+
+def _same(*arrays: DeviceArray) -> int:
+    n = arrays[0].size
+    for a in arrays[1:]:
+        if a.size != n:
+            raise ValueError(f"size mismatch: {[x.shape for x in arrays]}")
+    return n
+
+
+def gemm(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, trans_a=False, trans_b=False, alpha=1.0,
+         beta=0.0, bias: DeviceArray | None = None, relu=False) -> DeviceArray:
+    """c = epi(alpha * op(a) @ op(b) + beta * c) for 2-D row-major arrays."""
+    if len(a.shape) != 2 or len(b.shape) != 2 or len(c.shape) != 2:
+        raise ValueError("gemm expects 2-D arrays")
+    M, K = (a.shape[1], a.shape[0]) if trans_a else a.shape
+    Kb, N = (b.shape[1], b.shape[0]) if trans_b else b.shape
+    if K != Kb or c.shape != (M, N):
+        raise ValueError(f"gemm shape mismatch: op(a) {M}x{K}, op(b) {Kb}x{N}, c {c.shape}")
+    if bias is not None and bias.size != N:
+        raise ValueError("gemm: bias must have N elements")
+    epi = (_lib.TF_EPI_BIAS_RELU if relu else _lib.TF_EPI_BIAS) if bias is not None else \
+        (_lib.TF_EPI_RELU if relu else _lib.TF_EPI_NONE)
+    call("tf_gemm", _ctx(a), int(trans_a), int(trans_b), M, N, K, alpha, a.ptr, a.shape[1], b.ptr, b.shape[1],
+         beta, c.ptr, c.shape[1], a.tf_dtype, c.tf_dtype, epi, bias.ptr if bias is not None else None)
+    return c
+
+
+def relu_bwd(dy, x, dx):
+    call("tf_relu_bwd", _ctx(dy), dy.ptr, x.ptr, dx.ptr, _same(dy, x, dx), dy.tf_dtype)
+    return dx
+
+
+def sigmoid_bwd(dy, y, dx):
+    call("tf_sigmoid_bwd", _ctx(dy), dy.ptr, y.ptr, dx.ptr, _same(dy, y, dx), dy.tf_dtype)
+    return dx
+
+
+def tanh_bwd(dy, y, dx):
+    call("tf_tanh_bwd", _ctx(dy), dy.ptr, y.ptr, dx.ptr, _same(dy, y, dx), dy.tf_dtype)
+    return dx
+
+
+def relu(x, y):
+    call("tf_relu_fwd", _ctx(x), x.ptr, y.ptr, _same(x, y), x.tf_dtype)
+    return y
+
+
+def sigmoid(x, y):
+    call("tf_sigmoid_fwd", _ctx(x), x.ptr, y.ptr, _same(x, y), x.tf_dtype)
+    return y
+
+
+def tanh(x, y):
+    call("tf_tanh_fwd", _ctx(x), x.ptr, y.ptr, _same(x, y), x.tf_dtype)
+    return y
+
+
+def add(a, b, out):
+    call("tf_add", _ctx(a), a.ptr, b.ptr, out.ptr, _same(a, b, out), a.tf_dtype)
+    return out
+
+
+def mul(a, b, out):
+    call("tf_mul", _ctx(a), a.ptr, b.ptr, out.ptr, _same(a, b, out), a.tf_dtype)
+    return out
+
+
+def _rows_cols(x: DeviceArray):
+    if len(x.shape) != 2:
+        raise ValueError("row kernels expect 2-D arrays")
+    return x.shape
+
+
+def _check_targets(logits, targets):
+    rows, _ = _rows_cols(logits)
+    if targets.size != rows or targets.tf_dtype != _lib.TF_I64:
+        raise ValueError("targets must be int64 with one entry per row")
+
+
+def ce_fwd(logits, targets, loss, lse=None):
+    rows, cols = _rows_cols(logits)
+    _check_targets(logits, targets)
+    if lse is not None and lse.size != rows:
+        raise ValueError("lse must have one entry per row")
+    call("tf_ce_fwd", _ctx(logits), logits.ptr, targets.ptr, loss.ptr, lse.ptr if lse is not None else None,
+         rows, cols)
+    return loss
+
+
+def ce_bwd(logits, targets, dlogits, lse=None, grad_loss=None):
+    rows, cols = _rows_cols(logits)
+    _check_targets(logits, targets)
+    _same(logits, dlogits)
+    call("tf_ce_bwd", _ctx(logits), logits.ptr, targets.ptr, lse.ptr if lse is not None else None,
+         grad_loss.ptr if grad_loss is not None else None, dlogits.ptr, rows, cols)
+    return dlogits
+
+
+def ce_fwd_bwd(logits, targets, loss, dlogits):
+    rows, cols = _rows_cols(logits)
+    _check_targets(logits, targets)
+    _same(logits, dlogits)
+    call("tf_ce_fwd_bwd", _ctx(logits), logits.ptr, targets.ptr, loss.ptr, dlogits.ptr, rows, cols)
+    return loss, dlogits
+
+
+def log_softmax(x, y):
+    rows, cols = _rows_cols(x)
+    _same(x, y)
+    call("tf_log_softmax_fwd", _ctx(x), x.ptr, y.ptr, rows, cols)
+    return y
+
+
+def softmax(x, y):
+    rows, cols = _rows_cols(x)
+    _same(x, y)
+    call("tf_softmax_fwd", _ctx(x), x.ptr, y.ptr, rows, cols)
+    return y
+
+
+def log_softmax_bwd(y, dy, dx):
+    rows, cols = _rows_cols(y)
+    _same(y, dy, dx)
+    call("tf_log_softmax_bwd", _ctx(y), y.ptr, dy.ptr, dx.ptr, rows, cols)
+    return dx
+
+
+def softmax_bwd(y, dy, dx):
+    rows, cols = _rows_cols(y)
+    _same(y, dy, dx)
+    call("tf_softmax_bwd", _ctx(y), y.ptr, dy.ptr, dx.ptr, rows, cols)
+    return dx
+
+
+def colsum(dy, db):
+    rows, cols = _rows_cols(dy)
+    if db.size != cols:
+        raise ValueError("colsum: db must have one entry per column")
+    call("tf_colsum", _ctx(dy), dy.ptr, db.ptr, rows, cols)
+    return db
+
+
+def chansum_nchw(dy, db):
+    if len(dy.shape) != 4:
+        raise ValueError("chansum expects NCHW")
+    N, Cc, H, W = dy.shape
+    if db.size != Cc:
+        raise ValueError("chansum: db must have C entries")
+    call("tf_chansum_nchw", _ctx(dy), dy.ptr, db.ptr, N, Cc, H * W)
+    return db
+
+
+def sgd_momentum(p, g, v, lr, mu, p_bf16=None):
+    n = _same(p, g) if v is None else _same(p, g, v)
+    call("tf_sgd_momentum", _ctx(p), p.ptr, g.ptr, v.ptr if v is not None else None,
+         p_bf16.ptr if p_bf16 is not None else None, n, lr, mu)
+    return p

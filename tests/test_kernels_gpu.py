@@ -1,0 +1,390 @@
+"""Parity of every hot-path kernel against the CPU oracle, through the C ABI.
+
+Bars: integer/index work and kernels whose arithmetic order equals the
+reference's (ReLU backward, add/mul, SGD) are bit-exact; floating-point
+reductions are within rtol 1e-4 (fp32) / 2e-2 (bf16) of float64 truth with
+atol = rtol * rms(truth).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from tensors_amd import synth
+from tests.conftest import assert_bitexact, assert_close
+
+pytestmark = pytest.mark.gpu
+
+RTOL32 = 1e-4
+RTOL16 = 2e-2
+
+
+def _ops():
+    from tensors_amd import ops
+    return ops
+
+
+# ---------------------------------------------------------------------------
+# runtime
+# ---------------------------------------------------------------------------
+def test_memcpy_roundtrip_and_fill(ctx):
+    x = synth.normal(1, (1000, 3))
+    d = ctx.array(x)
+    assert_bitexact(d.numpy(), x, "H2D/D2H round trip")
+    from tensors_amd._lib import call
+    call("tf_hip_fill_f32", ctx.handle, d.ptr, 2.5, 2999)
+    got = d.numpy().reshape(-1)
+    assert np.all(got[:2999] == 2.5) and got[2999] == x.reshape(-1)[2999]
+    z = ctx.zeros((37,), np.float32)
+    assert np.all(z.numpy() == 0)
+    r, u = ctx.pool_stats()
+    assert r >= u > 0
+
+
+def test_zero_size_alloc_and_event_timing(ctx):
+    e = ctx.empty((0,), np.float32)
+    assert e.ptr is not None            # zero bytes allocates 1 byte
+    a, b = ctx.event(), ctx.event()
+    a.record()
+    b.record()
+    assert b is not None and a.elapsed_ms(b) >= 0.0
+
+
+# ---------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------
+def _gemm_truth(a, b, ta, tb, alpha=1.0, beta=0.0, c0=None, bias=None, relu=False):
+    A = a.astype(np.float64).T if ta else a.astype(np.float64)
+    B = b.astype(np.float64).T if tb else b.astype(np.float64)
+    out = alpha * (A @ B)
+    if beta != 0.0:
+        out += beta * c0.astype(np.float64)
+    if bias is not None:
+        out += bias.astype(np.float64)[None, :]
+    if relu:
+        out = np.maximum(out, 0.0)
+    return out
+
+
+def _run_gemm(ctx, a, b, ta, tb, M, N, **kw):
+    ops = _ops()
+    da, db = ctx.array(a), ctx.array(b)
+    c0 = kw.pop("c0", None)
+    dc = ctx.array(c0) if c0 is not None else ctx.zeros((M, N), np.float32)
+    bias = kw.pop("bias", None)
+    dbias = ctx.array(bias) if bias is not None else None
+    ops.gemm(da, db, dc, trans_a=ta, trans_b=tb, bias=dbias, **kw)
+    return dc.numpy()
+
+
+def test_gemm_known_answers(ctx):
+    # autograd/ops/autograd_all_ops_test.cpp:281-328: arange A[2x3] @ B[3x2]
+    a = np.arange(6, dtype=np.float32).reshape(2, 3)
+    b = np.arange(6, dtype=np.float32).reshape(3, 2)
+    got = _run_gemm(ctx, a, b, False, False, 2, 2)
+    assert np.array_equal(got, np.array([[10, 13], [28, 40]], np.float32))
+    # cuda/kernels/gemm_optimized_test.cpp:109-125: [[1,2],[3,4]] @ [[5,6],[7,8]]
+    a = np.array([[1, 2], [3, 4]], np.float32)
+    b = np.array([[5, 6], [7, 8]], np.float32)
+    assert np.array_equal(_run_gemm(ctx, a, b, False, False, 2, 2), np.array([[19, 22], [43, 50]], np.float32))
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(64, 256, 784), (17, 19, 23), (128, 128, 128), (300, 200, 100),
+                                   (1, 1, 1), (129, 257, 65), (64, 10, 128), (256, 784, 64)])
+def test_gemm_layouts_vs_truth(ctx, ta, tb, M, N, K):
+    rng_seed = synth.seed(2, 7) + M * 131 + N * 17 + K
+    a = synth.normal(rng_seed, (K, M) if ta else (M, K))
+    b = synth.normal(rng_seed + 1, (N, K) if tb else (K, N))
+    got = _run_gemm(ctx, a, b, ta, tb, M, N)
+    assert_close(got, _gemm_truth(a, b, ta, tb), RTOL32, f"gemm ta={ta} tb={tb} {M}x{N}x{K}")
+
+
+def test_gemm_matches_reference_order_oracle(ctx):
+    # The oracle reproduces Tensor::matmul's sequential loop; the MFMA kernel
+    # sums in another order, so the bar is the fp32 tolerance, not bits.
+    a = synth.normal(11, (64, 784))
+    b = synth.normal(12, (784, 256))
+    got = _run_gemm(ctx, a, b, False, False, 64, 256)
+    assert_close(got, oracle.matmul(a, b), RTOL32, "gemm vs ref-order oracle")
+
+
+def test_gemm_splitk_long_k(ctx):
+    # C4's classifier: [128 x 16384] @ [16384 x 10] -> one tile, split over K.
+    a = synth.normal(21, (128, 16384))
+    w = synth.normal(22, (10, 16384))
+    got = _run_gemm(ctx, a, w, False, True, 128, 10)
+    assert_close(got, _gemm_truth(a, w, False, True), RTOL32, "split-K gemm")
+
+
+def test_gemm_epilogues(ctx):
+    M, N, K = 96, 200, 150
+    a = synth.normal(31, (M, K))
+    b = synth.normal(32, (K, N))
+    c0 = synth.normal(33, (M, N))
+    bias = synth.normal(34, (N,))
+    got = _run_gemm(ctx, a, b, False, False, M, N, alpha=0.5, beta=0.25, c0=c0)
+    assert_close(got, _gemm_truth(a, b, False, False, 0.5, 0.25, c0), RTOL32, "alpha/beta")
+    got = _run_gemm(ctx, a, b, False, False, M, N, bias=bias, relu=True)
+    assert_close(got, _gemm_truth(a, b, False, False, bias=bias, relu=True), RTOL32, "bias+relu")
+    # K == 0: C = beta*C + bias
+    z = np.zeros((M, 0), np.float32)
+    got = _run_gemm(ctx, z, np.zeros((0, N), np.float32), False, False, M, N, bias=bias)
+    assert_close(got, np.broadcast_to(bias, (M, N)), RTOL32, "K=0")
+
+
+def test_gemm_splitk_with_epilogue(ctx):
+    a = synth.normal(41, (64, 8192))
+    b = synth.normal(42, (8192, 64))
+    bias = synth.normal(43, (64,))
+    got = _run_gemm(ctx, a, b, False, False, 64, 64, bias=bias, relu=True)
+    assert_close(got, _gemm_truth(a, b, False, False, bias=bias, relu=True), RTOL32, "split-K + bias/relu")
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False)])
+def test_gemm_bf16_fp32_accumulate(ctx, ta, tb):
+    import tensors_amd as ta_mod
+    from tensors_amd import ops
+    M, N, K = 192, 160, 320
+    a32 = synth.normal(51, (K, M) if ta else (M, K))
+    b32 = synth.normal(52, (N, K) if tb else (K, N))
+    a16, b16 = ta_mod.f32_to_bf16_bits(a32), ta_mod.f32_to_bf16_bits(b32)
+    truth = _gemm_truth(ta_mod.bf16_bits_to_f32(a16), ta_mod.bf16_bits_to_f32(b16), ta, tb)
+    da, db = ctx.array(a16, ta_mod.BF16), ctx.array(b16, ta_mod.BF16)
+    dc = ctx.zeros((M, N), np.float32)
+    ops.gemm(da, db, dc, trans_a=ta, trans_b=tb)
+    assert_close(dc.numpy(), truth, RTOL32, "bf16 in / fp32 out")   # exact products, fp32 sums
+    dc16 = ctx.zeros((M, N), ta_mod.BF16)
+    ops.gemm(da, db, dc16, trans_a=ta, trans_b=tb)
+    assert_close(ta_mod.bf16_bits_to_f32(dc16.numpy()), truth, RTOL16, "bf16 in / bf16 out")
+
+
+def test_gemm_strided_batched(ctx):
+    from tensors_amd._lib import TF_F32, call
+    B, M, N, K = 5, 33, 47, 29
+    a = synth.normal(61, (B, M, K))
+    b = synth.normal(62, (B, K, N))
+    da, db = ctx.array(a), ctx.array(b)
+    dc = ctx.zeros((B, M, N))
+    call("tf_gemm_strided_batched", ctx.handle, 0, 0, M, N, K, 1.0, da.ptr, K, M * K, db.ptr, N, K * N,
+         0.0, dc.ptr, N, M * N, B, TF_F32, TF_F32)
+    truth = np.einsum("bmk,bkn->bmn", a.astype(np.float64), b.astype(np.float64))
+    assert_close(dc.numpy(), truth, RTOL32, "strided batched")
+
+
+def test_gemm_rejects_bad_shapes(ctx):
+    from tensors_amd._lib import TF_F32, TFError, call
+    d = ctx.zeros((4, 4))
+    with pytest.raises(TFError):
+        call("tf_gemm", ctx.handle, 0, 0, 4, 4, 4, 1.0, d.ptr, 2, d.ptr, 4, 0.0, d.ptr, 4, TF_F32, TF_F32, 0, None)
+    with pytest.raises(TFError):
+        call("tf_gemm", ctx.handle, 0, 0, 4, 4, 4, 1.0, d.ptr, 4, d.ptr, 4, 0.0, d.ptr, 4, TF_F32, TF_F32, 1, None)
+
+
+def test_c2_linear_full_size(ctx):
+    """Config 2 at full size: Y = X W^T + b, dX = dY W, dW = dY^T X, db = colsum(dY)."""
+    ops = _ops()
+    n = 2048
+    X = synth.normal(synth.seed(2, 0), (n, n))
+    W = synth.normal(synth.seed(2, 1), (n, n))
+    dY = synth.normal(synth.seed(2, 2), (n, n))
+    b = synth.normal(synth.seed(2, 3), (n,))
+    dX_, dW_, dY_, dB_ = ctx.array(X), ctx.array(W), ctx.array(dY), ctx.array(b)
+    Y, dXo, dWo, db = ctx.empty((n, n)), ctx.empty((n, n)), ctx.empty((n, n)), ctx.empty((n,))
+    ops.gemm(dX_, dW_, Y, trans_b=True, bias=dB_)
+    ops.gemm(dY_, dW_, dXo)
+    ops.gemm(dY_, dX_, dWo, trans_a=True)
+    ops.colsum(dY_, db)
+    X64, W64, dY64 = X.astype(np.float64), W.astype(np.float64), dY.astype(np.float64)
+    assert_close(Y.numpy(), X64 @ W64.T + b, RTOL32, "C2 Y")
+    assert_close(dXo.numpy(), dY64 @ W64, RTOL32, "C2 dX")
+    assert_close(dWo.numpy(), dY64.T @ X64, RTOL32, "C2 dW")
+    assert_close(db.numpy(), dY64.sum(0), RTOL32, "C2 db")
+
+
+# ---------------------------------------------------------------------------
+# elementwise backward
+# ---------------------------------------------------------------------------
+SIZES = [0, 1, 17, 1000, 4096 * 1024 + 3]
+
+
+@pytest.mark.parametrize("n", SIZES)
+def test_relu_bwd_bitexact(ctx, n):
+    ops = _ops()
+    x = synth.normal(71, (n,))
+    dy = synth.normal(72, (n,))
+    if n >= 4:
+        x[:4] = [0.0, -0.0, 1e-38, -1e-38]     # x == 0 masks to 0 (strict >)
+    d = ctx.empty((n,))
+    ops.relu_bwd(ctx.array(dy), ctx.array(x), d)
+    assert_bitexact(d.numpy(), oracle.relu_bwd(dy, x), f"relu_bwd n={n}")
+
+
+@pytest.mark.parametrize("n", [1, 1000, 1 << 20])
+def test_sigmoid_tanh_bwd(ctx, n):
+    ops = _ops()
+    x = synth.normal(81, (n,))
+    dy = synth.normal(82, (n,))
+    ys, yt = oracle.sigmoid(x), oracle.tanh(x)
+    d = ctx.empty((n,))
+    ops.sigmoid_bwd(ctx.array(dy), ctx.array(ys), d)
+    assert_close(d.numpy(), oracle.sigmoid_bwd(dy, ys), 1e-6, "sigmoid_bwd", atol=1e-7)
+    ops.tanh_bwd(ctx.array(dy), ctx.array(yt), d)
+    assert_close(d.numpy(), oracle.tanh_bwd(dy, yt), 1e-6, "tanh_bwd", atol=1e-7)
+
+
+def test_forward_activations(ctx):
+    ops = _ops()
+    x = synth.normal(91, (5000,), std=3.0)
+    d = ctx.empty((5000,))
+    ops.relu(ctx.array(x), d)
+    assert_bitexact(d.numpy(), oracle.relu(x), "relu fwd")
+    ops.sigmoid(ctx.array(x), d)
+    assert_close(d.numpy(), oracle.sigmoid(x), 1e-6, "sigmoid fwd", atol=1e-7)
+    ops.tanh(ctx.array(x), d)
+    assert_close(d.numpy(), oracle.tanh(x), 1e-6, "tanh fwd", atol=1e-7)
+
+
+@pytest.mark.parametrize("n", [3, 4096, 1 << 20])
+def test_add_mul_bitexact(ctx, n):
+    ops = _ops()
+    a, b = synth.normal(101, (n,)), synth.normal(102, (n,))
+    d = ctx.empty((n,))
+    ops.add(ctx.array(a), ctx.array(b), d)
+    assert_bitexact(d.numpy(), oracle.add(a, b), "add")
+    ops.mul(ctx.array(a), ctx.array(b), d)
+    assert_bitexact(d.numpy(), a * b, "mul")
+
+
+def test_relu_bwd_bf16(ctx):
+    import tensors_amd as ta_mod
+    ops = _ops()
+    n = 4099
+    x16 = ta_mod.f32_to_bf16_bits(synth.normal(111, (n,)))
+    dy16 = ta_mod.f32_to_bf16_bits(synth.normal(112, (n,)))
+    d = ctx.empty((n,), ta_mod.BF16)
+    ops.relu_bwd(ctx.array(dy16, ta_mod.BF16), ctx.array(x16, ta_mod.BF16), d)
+    want = ta_mod.f32_to_bf16_bits(oracle.relu_bwd(ta_mod.bf16_bits_to_f32(dy16), ta_mod.bf16_bits_to_f32(x16)))
+    assert_bitexact(d.numpy(), want, "relu_bwd bf16")
+
+
+# ---------------------------------------------------------------------------
+# cross entropy / softmax rows
+# ---------------------------------------------------------------------------
+CE_SHAPES = [(64, 10), (128, 10), (4096, 1024), (4096, 1000), (33, 1023), (7, 3000), (5, 9000), (1, 1)]
+
+
+@pytest.mark.parametrize("R,Cc", CE_SHAPES)
+def test_ce_fwd_bwd_vs_chain(ctx, R, Cc):
+    ops = _ops()
+    logits = synth.normal(121 + R, (R, Cc), std=3.0)
+    labels = synth.uniform_int(122 + Cc, (R,), Cc)
+    loss_ref, d_ref = oracle.ce_chain(logits, labels)
+    dl, dt = ctx.array(logits), ctx.array(labels)
+    loss, lse, d = ctx.empty((1,)), ctx.empty((R,)), ctx.empty((R, Cc))
+    ops.ce_fwd(dl, dt, loss, lse)
+    assert_close(loss.numpy(), [loss_ref], RTOL32, "ce loss")
+    ops.ce_bwd(dl, dt, d, lse=lse)
+    assert_close(d.numpy(), d_ref, RTOL32, "ce bwd (saved lse)")
+    ops.ce_bwd(dl, dt, d)
+    assert_close(d.numpy(), d_ref, RTOL32, "ce bwd (recomputed lse)")
+    loss2 = ctx.empty((1,))
+    ops.ce_fwd_bwd(dl, dt, loss2, d)
+    assert_close(loss2.numpy(), [loss_ref], RTOL32, "fused loss")
+    assert_close(d.numpy(), d_ref, RTOL32, "fused dlogits")
+
+
+def test_ce_upstream_scale_and_bad_labels(ctx):
+    ops = _ops()
+    R, Cc = 16, 10
+    logits = synth.normal(131, (R, Cc))
+    labels = synth.uniform_int(132, (R,), Cc)
+    labels[3], labels[7] = -1, Cc          # skipped by the chain's one-hot mask
+    loss_ref, d_ref = oracle.ce_chain(logits, labels)
+    g = ctx.array(np.array([0.75], np.float32))
+    d = ctx.empty((R, Cc))
+    ops.ce_bwd(ctx.array(logits), ctx.array(labels), d, grad_loss=g)
+    assert_close(d.numpy(), 0.75 * d_ref, RTOL32, "ce bwd * upstream")
+    assert np.all(d.numpy()[[3, 7]] == 0.0)
+    loss = ctx.empty((1,))
+    ops.ce_fwd(ctx.array(logits), ctx.array(labels), loss)
+    assert_close(loss.numpy(), [loss_ref], RTOL32, "loss with skipped labels")
+
+
+@pytest.mark.parametrize("R,Cc", [(64, 10), (256, 1024), (3, 777), (2, 5000)])
+def test_softmax_family(ctx, R, Cc):
+    ops = _ops()
+    x = synth.normal(141 + Cc, (R, Cc), std=2.0)
+    dy = synth.normal(142 + Cc, (R, Cc))
+    dx, dy_d, y = ctx.array(x), ctx.array(dy), ctx.empty((R, Cc))
+    ops.log_softmax(dx, y)
+    ly = oracle.log_softmax(x)
+    assert_close(y.numpy(), ly, RTOL32, "log_softmax fwd")
+    ops.softmax(dx, y)
+    sy = oracle.softmax(x)
+    assert_close(y.numpy(), sy, RTOL32, "softmax fwd")
+    g = ctx.empty((R, Cc))
+    ops.log_softmax_bwd(ctx.array(ly), dy_d, g)
+    assert_close(g.numpy(), oracle.log_softmax_bwd(ly, dy), RTOL32, "log_softmax bwd")
+    ops.softmax_bwd(ctx.array(sy), dy_d, g)
+    assert_close(g.numpy(), oracle.softmax_bwd(sy, dy), RTOL32, "softmax bwd")
+
+
+def test_softmax_bwd_uniform_is_zero(ctx):
+    # autograd/ops/autograd_all_ops_test.cpp:108-121: uniform input, grad 0.
+    ops = _ops()
+    R, Cc = 4, 8
+    y = np.full((R, Cc), 1.0 / Cc, np.float32)
+    g = ctx.empty((R, Cc))
+    ops.softmax_bwd(ctx.array(y), ctx.array(np.ones((R, Cc), np.float32)), g)
+    assert np.max(np.abs(g.numpy())) < 1e-7
+
+
+# ---------------------------------------------------------------------------
+# reductions
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("R,Cc", [(2048, 2048), (64, 256), (17, 19), (1, 5), (4096, 10), (3, 1001)])
+def test_colsum(ctx, R, Cc):
+    ops = _ops()
+    dy = synth.normal(151 + R, (R, Cc))
+    db = ctx.empty((Cc,))
+    ops.colsum(ctx.array(dy), db)
+    assert_close(db.numpy(), dy.astype(np.float64).sum(0), RTOL32, f"colsum {R}x{Cc}")
+    assert_close(db.numpy(), oracle.colsum(dy), RTOL32, "colsum vs oracle")
+
+
+def test_colsum_zero_rows(ctx):
+    ops = _ops()
+    db = ctx.array(np.full(7, 3.0, np.float32))
+    ops.colsum(ctx.empty((0, 7)), db)
+    assert np.all(db.numpy() == 0.0)
+
+
+@pytest.mark.parametrize("shape", [(128, 32, 32, 32), (128, 64, 16, 16), (2, 3, 5, 7), (1, 1, 1, 1)])
+def test_chansum_nchw(ctx, shape):
+    ops = _ops()
+    dy = synth.normal(161 + shape[1], shape)
+    db = ctx.empty((shape[1],))
+    ops.chansum_nchw(ctx.array(dy), db)
+    assert_close(db.numpy(), dy.astype(np.float64).sum((0, 2, 3)), RTOL32, f"chansum {shape}")
+    assert_close(db.numpy(), oracle.chansum_nchw(dy), RTOL32, "chansum vs oracle")
+
+
+# ---------------------------------------------------------------------------
+# SGD
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("n", [1, 7, 235146, 1 << 20])
+@pytest.mark.parametrize("mu", [0.9, 0.0])
+def test_sgd_momentum_bitexact(ctx, n, mu):
+    import tensors_amd as ta_mod
+    ops = _ops()
+    p, g, v = synth.normal(171, (n,)), synth.normal(172, (n,)), synth.normal(173, (n,))
+    dp, dg, dv = ctx.array(p), ctx.array(g), ctx.array(v)
+    sh = ctx.empty((n,), ta_mod.BF16)
+    for _ in range(3):
+        ops.sgd_momentum(dp, dg, dv, 0.1, mu, p_bf16=sh)
+        p, v = oracle.sgd_momentum(p, g, v, 0.1, mu)
+    assert_bitexact(dp.numpy(), p, "sgd p")
+    assert_bitexact(dv.numpy(), v, "sgd v")
+    assert_bitexact(sh.numpy(), ta_mod.f32_to_bf16_bits(p), "bf16 shadow")
