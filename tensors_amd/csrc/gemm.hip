@@ -11,18 +11,22 @@
 // Global->LDS copies are then straight 16-byte vector copies in both cases,
 // and the MFMA fragment reads differ:
 //   K-major : each lane reads 16 consecutive k of its row  -> 4 x ds_read_b128
-//   MN-major: each lane reads its row at 16 different k    -> 16 x ds_read_b32
+//   MN-major: each lane reads its row at 16 different k; the wave's two
+//             accumulators along that dimension take interleaved rows so one
+//             ds_read_b64 serves both                      -> 16 x ds_read_b64
 // The reduction order inside a 32-deep k block is permuted (lanes 0-31 feed
 // k = s, lanes 32-63 feed k = 16 + s to the s-th MFMA) so that the K-major
 // reads are contiguous; the sum is the same, the rounding order differs from
 // the reference's sequential loop (tensor/Tensor.cpp:356-360) within fp32
 // tolerance.
 //
-// fp32 tile: 128 x 128 x 32 per 256-thread workgroup (4 waves in 2 x 2, each
-// wave 64 x 64 = 2 x 2 tiles of v_mfma_f32_32x32x2_f32), LDS double buffered
-// with one barrier per k block, global loads for block k+1 issued before the
-// MFMAs of block k.  bf16: same structure with v_mfma_f32_32x32x16_bf16 and a
-// 64-deep k block.
+// fp32 tile: 128 x BN x 32 per 256-thread workgroup, BN = 128 or 64 (4 waves
+// in 2 x 2, each wave 64 x BN/2 = 2 x BN/64 tiles of v_mfma_f32_32x32x2_f32),
+// LDS double buffered with one barrier per k block, global loads for block
+// k+1 issued before the MFMAs of block k; interior tiles take an unguarded
+// 16-byte load path.  bf16: same structure with v_mfma_f32_32x32x16_bf16 and
+// a 64-deep k block.  At most ~74 KB of LDS per workgroup, so two workgroups
+// share a CU and fill each other's stalls.
 //
 // Work distribution: the tile index is remapped so that each of the 8 XCDs
 // (which receive workgroups round-robin) owns a contiguous, row-grouped block
@@ -40,7 +44,6 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 constexpr int BM = 128;
-constexpr int BN = 128;
 constexpr int kThreads = 256;
 
 struct GemmParams {
@@ -58,6 +61,7 @@ struct GemmParams {
     int epi;
     int out_bf16;
     int vec_a, vec_b;      // 16-byte vector loads legal for A / B
+    int pair_c;            // 8-byte paired stores legal for C
 };
 
 // Remap a linear workgroup id so that the ids one XCD receives (id % 8 == x)
@@ -78,39 +82,48 @@ __device__ __forceinline__ void tile_coords(int wg, int tiles_m, int tiles_n, in
 }
 
 // ---------------------------------------------------------------------------
-// Operand staging.  ELEM = float (fp32 path) or uint16_t (bf16 bits).
-// A "tile" is 128 rows x BK k.  K-major LDS layout: [128][BK + PADK];
-// MN-major: [BK][128 + PADM].
+// Operand staging.  ELEM = float (fp32 path) or uint16_t (bf16 bits).  A
+// tile is ROWS rows x BK k.  K-major LDS layout: [ROWS][BK + PADK];
+// MN-major: [BK][ROWS + PADM].  The paddings keep the fragment reads free of
+// bank conflicts (b128 row reads for K-major; for MN-major the two lane
+// halves read k-rows 16 apart, which the padding moves to the other banks).
 // ---------------------------------------------------------------------------
-template <typename ELEM, int BK, bool KMAJ>
+template <typename ELEM, int ROWS, int BK, bool KMAJ>
 struct Stage {
     static constexpr int VEC = 16 / sizeof(ELEM);            // elements per 16 B
-    static constexpr int PADK = (sizeof(ELEM) == 4) ? 4 : 8;  // keeps b128 reads conflict-free
-    static constexpr int PADM = (sizeof(ELEM) == 4) ? 2 : 4;  // halves 16 rows apart land in other banks
-    static constexpr int LD = KMAJ ? (BK + PADK) : (128 + PADM);
-    static constexpr int LDS_ELEMS = KMAJ ? 128 * LD : BK * LD;
-    static constexpr int ELEMS_PER_THREAD = 128 * BK / kThreads;
-    static constexpr int LOADS = ELEMS_PER_THREAD / VEC;      // 16-byte loads per thread
+    static constexpr int PADK = (sizeof(ELEM) == 4) ? 4 : 8;
+    static constexpr int PADM = (sizeof(ELEM) == 4) ? 2 : 4;
+    static constexpr int LD = KMAJ ? (BK + PADK) : (ROWS + PADM);
+    static constexpr int LDS_ELEMS = KMAJ ? ROWS * LD : BK * LD;
+    static constexpr int LOADS = ROWS * BK / kThreads / VEC;  // 16-byte loads per thread
+    static constexpr int TPR = KMAJ ? BK / VEC : ROWS / VEC;  // threads per stored row
+    static constexpr int RPP = kThreads / TPR;                // stored rows per pass
+    static_assert(LOADS * kThreads * VEC == ROWS * BK, "tile does not divide among threads");
 
     uint4 reg[LOADS];
 
-    // Global -> registers for the tile whose first row is row0 and first k is k0.
-    // rows: valid row count of the operand; kend: end of this split's k range.
+    // Global -> registers for the tile whose first row is row0 and first k is
+    // k0.  rows: valid row count of the operand; kend: end of this split's k
+    // range.  `fast`: the whole tile is in range and 16-byte loads are legal.
     __device__ __forceinline__ void load(const ELEM* __restrict__ p, int64_t ld, int row0, int rows,
                                          int k0, int kend, bool vec_ok) {
         const int t = threadIdx.x;
+        const bool fast = vec_ok && row0 + ROWS <= rows && k0 + BK <= kend;
+        if (fast) {
+#pragma unroll
+            for (int i = 0; i < LOADS; ++i) {
+                const int a = t / TPR + RPP * i, b = (t % TPR) * VEC;
+                const ELEM* src = KMAJ ? p + (int64_t)(row0 + a) * ld + (k0 + b)
+                                       : p + (int64_t)(k0 + a) * ld + (row0 + b);
+                reg[i] = *reinterpret_cast<const uint4*>(src);
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
-            int r, k;
-            if (KMAJ) {
-                constexpr int TPR = BK / VEC;          // threads per row
-                r = row0 + t / TPR + (kThreads / TPR) * i;
-                k = k0 + (t % TPR) * VEC;
-            } else {
-                constexpr int TPR = 128 / VEC;         // threads per k-row
-                k = k0 + t / TPR + (kThreads / TPR) * i;
-                r = row0 + (t % TPR) * VEC;
-            }
+            const int a = t / TPR + RPP * i, b = (t % TPR) * VEC;
+            const int r = KMAJ ? row0 + a : row0 + b;
+            const int k = KMAJ ? k0 + b : k0 + a;
             const bool full = KMAJ ? (r < rows && k + VEC <= kend) : (k < kend && r + VEC <= rows);
             if (vec_ok && full) {
                 const ELEM* src = KMAJ ? p + (int64_t)r * ld + k : p + (int64_t)k * ld + r;
@@ -119,9 +132,9 @@ struct Stage {
                 ELEM tmp[VEC];
 #pragma unroll
                 for (int v = 0; v < VEC; ++v) {
-                    int rr = KMAJ ? r : r + v;
-                    int kk = KMAJ ? k + v : k;
-                    bool ok = rr < rows && kk < kend;
+                    const int rr = KMAJ ? r : r + v;
+                    const int kk = KMAJ ? k + v : k;
+                    const bool ok = rr < rows && kk < kend;
                     tmp[v] = ok ? (KMAJ ? p[(int64_t)rr * ld + kk] : p[(int64_t)kk * ld + rr]) : ELEM(0);
                 }
                 reg[i] = *reinterpret_cast<uint4*>(tmp);
@@ -134,17 +147,12 @@ struct Stage {
         const int t = threadIdx.x;
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
+            const int a = t / TPR + RPP * i, b = (t % TPR) * VEC;
             if (KMAJ) {
-                constexpr int TPR = BK / VEC;
-                int r = t / TPR + (kThreads / TPR) * i;
-                int k = (t % TPR) * VEC;
-                *reinterpret_cast<uint4*>(lds + r * LD + k) = reg[i];
+                *reinterpret_cast<uint4*>(lds + a * LD + b) = reg[i];
             } else {
-                constexpr int TPR = 128 / VEC;
-                int k = t / TPR + (kThreads / TPR) * i;
-                int r = (t % TPR) * VEC;
-                // Rows are 8-byte aligned only (padding), so store as 2 x 8 B.
-                uint2* dst = reinterpret_cast<uint2*>(lds + k * LD + r);
+                // MN-major rows are 8-byte aligned only (padding): 2 x 8 B.
+                uint2* dst = reinterpret_cast<uint2*>(lds + a * LD + b);
                 dst[0] = make_uint2(reg[i].x, reg[i].y);
                 dst[1] = make_uint2(reg[i].z, reg[i].w);
             }
@@ -153,48 +161,82 @@ struct Stage {
 };
 
 // ---------------------------------------------------------------------------
-// Epilogue for one 32 x 32 accumulator tile held in the v_mfma 32x32 layout:
-// lane l, register r  ->  row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+// Fragment-to-tile mapping.  A wave owns a 64 x WN block of the tile made of
+// 2 x NSUB accumulators of 32 x 32 (v_mfma 32x32 layout: lane l, register r
+// hold row 8*(r/4) + 4*(l/32) + r%4, column l%32 of the accumulator).  For a
+// K-major operand accumulator i covers rows 32i .. 32i+31 of the wave block;
+// for an MN-major operand with two accumulators the rows are interleaved
+// (accumulator i takes rows 2l + i), so one 8-byte LDS read feeds both.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void store_tile(const GemmParams& p, const v16f& acc, int row0, int col0,
+template <bool PAIR>
+__device__ __forceinline__ int sub_row(int i, int l) { return PAIR ? 2 * l + i : 32 * i + l; }
+
+__device__ __forceinline__ void emit(const GemmParams& p, int64_t off, float acc, float bias_v, bool relu) {
+    float v = p.alpha * acc;
+    if (p.beta != 0.0f) v += p.beta * reinterpret_cast<const float*>(p.C)[off];
+    v += bias_v;
+    if (relu) v = fmaxf(v, 0.0f);
+    if (p.out_bf16) reinterpret_cast<uint16_t*>(p.C)[off] = tfd::f32_to_bf16(v);
+    else reinterpret_cast<float*>(p.C)[off] = v;
+}
+
+// Write the wave's accumulators.  m_base/n_base: first row/column of the
+// wave block in C.
+template <int NSUB, bool A_PAIR, bool B_PAIR>
+__device__ __forceinline__ void store_wave(const GemmParams& p, const v16f (&acc)[2][NSUB], int m_base, int n_base,
                                            int64_t batch_off_c, int split) {
     const int lane = threadIdx.x & 63;
-    const int col = col0 + (lane & 31);
-    if (col >= p.N) return;
-    const int rbase = row0 + 4 * (lane >> 5);
-    if (p.partial) {
-        float* dst = p.partial + (int64_t)split * p.M * p.N;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            int row = rbase + 8 * (r >> 2) + (r & 3);
-            if (row < p.M) dst[(int64_t)row * p.N + col] = acc[r];
-        }
-        return;
-    }
-    const float b = (p.epi == TF_EPI_BIAS || p.epi == TF_EPI_BIAS_RELU) ? p.bias[col] : 0.0f;
+    const int l32 = lane & 31, half = lane >> 5;
+    const bool has_bias = p.epi == TF_EPI_BIAS || p.epi == TF_EPI_BIAS_RELU;
     const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU;
+    float* part = p.partial ? p.partial + (int64_t)split * p.M * p.N : nullptr;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        int row = rbase + 8 * (r >> 2) + (r & 3);
-        if (row >= p.M) continue;
-        int64_t off = batch_off_c + (int64_t)row * p.ldc + col;
-        float v = p.alpha * acc[r];
-        if (p.beta != 0.0f) v += p.beta * reinterpret_cast<const float*>(p.C)[off];
-        v += b;
-        if (relu) v = fmaxf(v, 0.0f);
-        if (p.out_bf16) reinterpret_cast<uint16_t*>(p.C)[off] = tfd::f32_to_bf16(v);
-        else reinterpret_cast<float*>(p.C)[off] = v;
+    for (int j = 0; j < NSUB; ++j) {
+        if (B_PAIR && j == 1) break;  // paired columns are written together with j == 0
+        const int col = n_base + sub_row<B_PAIR>(j, l32);
+        const bool c0 = col < p.N, c1 = B_PAIR && col + 1 < p.N;
+        if (!c0) continue;
+        const float b0 = has_bias ? p.bias[col] : 0.0f;
+        const float b1 = (has_bias && c1) ? p.bias[col + 1] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m_base + sub_row<A_PAIR>(i, 8 * (r >> 2) + 4 * half + (r & 3));
+                if (row >= p.M) continue;
+                if (part) {
+                    float* dst = part + (int64_t)row * p.N + col;
+                    dst[0] = acc[i][j][r];
+                    if (B_PAIR && c1) dst[1] = acc[i][1][r];
+                    continue;
+                }
+                const int64_t off = batch_off_c + (int64_t)row * p.ldc + col;
+                if (B_PAIR && c1 && p.pair_c && p.beta == 0.0f && !p.out_bf16) {
+                    float v0 = p.alpha * acc[i][0][r] + b0, v1 = p.alpha * acc[i][1][r] + b1;
+                    if (relu) { v0 = fmaxf(v0, 0.0f); v1 = fmaxf(v1, 0.0f); }
+                    *reinterpret_cast<float2*>(reinterpret_cast<float*>(p.C) + off) = make_float2(v0, v1);
+                } else {
+                    emit(p, off, acc[i][j][r], b0, relu);
+                    if (B_PAIR && c1) emit(p, off + 1, acc[i][1][r], b1, relu);
+                }
+            }
+        }
     }
 }
 
 // ---------------------------------------------------------------------------
-// fp32 kernel: BK = 32, v_mfma_f32_32x32x2_f32.
+// fp32 kernel: BK = 32, v_mfma_f32_32x32x2_f32.  Lane half h feeds k = 16h + s
+// to the s-th MFMA of a k block.
 // ---------------------------------------------------------------------------
-template <bool A_KMAJ, bool B_KMAJ>
+template <int BN, bool A_KMAJ, bool B_KMAJ>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
     constexpr int BK = 32;
-    using SA = Stage<float, BK, A_KMAJ>;
-    using SB = Stage<float, BK, B_KMAJ>;
+    constexpr int WN = BN / 2;
+    constexpr int NSUB = WN / 32;
+    constexpr bool A_PAIR = !A_KMAJ;
+    constexpr bool B_PAIR = !B_KMAJ && NSUB == 2;
+    using SA = Stage<float, BM, BK, A_KMAJ>;
+    using SB = Stage<float, BN, BK, B_KMAJ>;
     __shared__ __attribute__((aligned(16))) float lds_a[2][SA::LDS_ELEMS];
     __shared__ __attribute__((aligned(16))) float lds_b[2][SB::LDS_ELEMS];
 
@@ -214,11 +256,11 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
     const int wm = wave >> 1, wn = wave & 1;
     const int half = lane >> 5, l32 = lane & 31;
 
-    v16f acc[2][2];
+    v16f acc[2][NSUB];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+        for (int j = 0; j < NSUB; ++j) acc[i][j] = v16f{};
 
     SA sa;
     SB sb;
@@ -238,46 +280,56 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
             sa.load(A, p.lda, m0, p.M, k0, kend, p.vec_a);
             sb.load(B, p.ldb, n0, p.N, k0, kend, p.vec_b);
         }
-        // Fragments: lane supplies k = 16*half + s to the s-th MFMA.
-        float fa[2][16], fb[2][16];
+        float fa[2][16], fb[NSUB][16];
+        const float* la = lds_a[cur];
+        const float* lb = lds_b[cur];
+        if (A_KMAJ) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int row = wm * 64 + i * 32 + l32;
-            if (A_KMAJ) {
-                const float* src = &lds_a[cur][row * SA::LD + 16 * half];
+            for (int i = 0; i < 2; ++i) {
+                const float* src = la + (wm * 64 + sub_row<false>(i, l32)) * SA::LD + 16 * half;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
                     fa[i][4 * q + 0] = v.x; fa[i][4 * q + 1] = v.y;
                     fa[i][4 * q + 2] = v.z; fa[i][4 * q + 3] = v.w;
                 }
-            } else {
+            }
+        } else {
 #pragma unroll
-                for (int s = 0; s < 16; ++s) fa[i][s] = lds_a[cur][(16 * half + s) * SA::LD + row];
+            for (int s = 0; s < 16; ++s) {
+                float2 v = *reinterpret_cast<const float2*>(la + (16 * half + s) * SA::LD + wm * 64 + 2 * l32);
+                fa[0][s] = v.x;
+                fa[1][s] = v.y;
             }
         }
+        if (B_KMAJ) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int col = wn * 64 + j * 32 + l32;
-            if (B_KMAJ) {
-                const float* src = &lds_b[cur][col * SB::LD + 16 * half];
+            for (int j = 0; j < NSUB; ++j) {
+                const float* src = lb + (wn * WN + sub_row<false>(j, l32)) * SB::LD + 16 * half;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
                     fb[j][4 * q + 0] = v.x; fb[j][4 * q + 1] = v.y;
                     fb[j][4 * q + 2] = v.z; fb[j][4 * q + 3] = v.w;
                 }
-            } else {
-#pragma unroll
-                for (int s = 0; s < 16; ++s) fb[j][s] = lds_b[cur][(16 * half + s) * SB::LD + col];
             }
+        } else if (B_PAIR) {
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                float2 v = *reinterpret_cast<const float2*>(lb + (16 * half + s) * SB::LD + wn * WN + 2 * l32);
+                fb[0][s] = v.x;
+                fb[NSUB - 1][s] = v.y;
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 16; ++s) fb[0][s] = lb[(16 * half + s) * SB::LD + wn * WN + l32];
         }
 #pragma unroll
         for (int s = 0; s < 16; ++s)
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < NSUB; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
         if (more) {
             sa.store(lds_a[cur ^ 1]);
@@ -286,23 +338,22 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
         __syncthreads();
     }
 
-    const int64_t boff = (int64_t)batch * p.stride_c;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            store_tile(p, acc[i][j], m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, boff, split);
+    store_wave<NSUB, A_PAIR, B_PAIR>(p, acc, m0 + wm * 64, n0 + wn * WN, (int64_t)batch * p.stride_c, split);
 }
 
 // ---------------------------------------------------------------------------
-// bf16 kernel: BK = 64, v_mfma_f32_32x32x16_bf16 (lane supplies 8 consecutive
-// k: lanes 0-31 k = 0..7, lanes 32-63 k = 8..15 of each 16-deep step).
+// bf16 kernel: BK = 64, v_mfma_f32_32x32x16_bf16 (lane half h supplies the 8
+// consecutive k 16s + 8h .. 16s + 8h + 7 to the s-th MFMA of a k block).
 // ---------------------------------------------------------------------------
-template <bool A_KMAJ, bool B_KMAJ>
+template <int BN, bool A_KMAJ, bool B_KMAJ>
 __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(GemmParams p) {
     constexpr int BK = 64;
-    using SA = Stage<uint16_t, BK, A_KMAJ>;
-    using SB = Stage<uint16_t, BK, B_KMAJ>;
+    constexpr int WN = BN / 2;
+    constexpr int NSUB = WN / 32;
+    constexpr bool A_PAIR = !A_KMAJ;
+    constexpr bool B_PAIR = !B_KMAJ && NSUB == 2;
+    using SA = Stage<uint16_t, BM, BK, A_KMAJ>;
+    using SB = Stage<uint16_t, BN, BK, B_KMAJ>;
     __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][SA::LDS_ELEMS];
     __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][SB::LDS_ELEMS];
 
@@ -322,11 +373,11 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(GemmParams p) {
     const int wm = wave >> 1, wn = wave & 1;
     const int half = lane >> 5, l32 = lane & 31;
 
-    v16f acc[2][2];
+    v16f acc[2][NSUB];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+        for (int j = 0; j < NSUB; ++j) acc[i][j] = v16f{};
 
     SA sa;
     SB sb;
@@ -346,39 +397,51 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(GemmParams p) {
             sa.load(A, p.lda, m0, p.M, k0, kend, p.vec_a);
             sb.load(B, p.ldb, n0, p.N, k0, kend, p.vec_b);
         }
+        const uint16_t* la = lds_a[cur];
+        const uint16_t* lb = lds_b[cur];
 #pragma unroll
         for (int s = 0; s < BK / 16; ++s) {
-            v8bf fa[2], fb[2];
+            const int kk = 16 * s + 8 * half;
+            v8bf fa[2], fb[NSUB];
+            if (A_KMAJ) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int row = wm * 64 + i * 32 + l32;
-                const int kk = 16 * s + 8 * half;
-                if (A_KMAJ) {
-                    fa[i] = *reinterpret_cast<const v8bf*>(&lds_a[cur][row * SA::LD + kk]);
-                } else {
-                    uint16_t t[8];
+                for (int i = 0; i < 2; ++i)
+                    fa[i] = *reinterpret_cast<const v8bf*>(la + (wm * 64 + sub_row<false>(i, l32)) * SA::LD + kk);
+            } else {
+                uint16_t t0[8], t1[8];
 #pragma unroll
-                    for (int v = 0; v < 8; ++v) t[v] = lds_a[cur][(kk + v) * SA::LD + row];
-                    fa[i] = *reinterpret_cast<v8bf*>(t);
+                for (int v = 0; v < 8; ++v) {
+                    uint32_t w = *reinterpret_cast<const uint32_t*>(la + (kk + v) * SA::LD + wm * 64 + 2 * l32);
+                    t0[v] = (uint16_t)(w & 0xffffu);
+                    t1[v] = (uint16_t)(w >> 16);
                 }
+                fa[0] = *reinterpret_cast<v8bf*>(t0);
+                fa[1] = *reinterpret_cast<v8bf*>(t1);
             }
+            if (B_KMAJ) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int col = wn * 64 + j * 32 + l32;
-                const int kk = 16 * s + 8 * half;
-                if (B_KMAJ) {
-                    fb[j] = *reinterpret_cast<const v8bf*>(&lds_b[cur][col * SB::LD + kk]);
-                } else {
-                    uint16_t t[8];
+                for (int j = 0; j < NSUB; ++j)
+                    fb[j] = *reinterpret_cast<const v8bf*>(lb + (wn * WN + sub_row<false>(j, l32)) * SB::LD + kk);
+            } else if (B_PAIR) {
+                uint16_t t0[8], t1[8];
 #pragma unroll
-                    for (int v = 0; v < 8; ++v) t[v] = lds_b[cur][(kk + v) * SB::LD + col];
-                    fb[j] = *reinterpret_cast<v8bf*>(t);
+                for (int v = 0; v < 8; ++v) {
+                    uint32_t w = *reinterpret_cast<const uint32_t*>(lb + (kk + v) * SB::LD + wn * WN + 2 * l32);
+                    t0[v] = (uint16_t)(w & 0xffffu);
+                    t1[v] = (uint16_t)(w >> 16);
                 }
+                fb[0] = *reinterpret_cast<v8bf*>(t0);
+                fb[NSUB - 1] = *reinterpret_cast<v8bf*>(t1);
+            } else {
+                uint16_t t0[8];
+#pragma unroll
+                for (int v = 0; v < 8; ++v) t0[v] = lb[(kk + v) * SB::LD + wn * WN + l32];
+                fb[0] = *reinterpret_cast<v8bf*>(t0);
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < NSUB; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
         }
         if (more) {
@@ -388,12 +451,7 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(GemmParams p) {
         __syncthreads();
     }
 
-    const int64_t boff = (int64_t)batch * p.stride_c;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            store_tile(p, acc[i][j], m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32, boff, split);
+    store_wave<NSUB, A_PAIR, B_PAIR>(p, acc, m0 + wm * 64, n0 + wn * WN, (int64_t)batch * p.stride_c, split);
 }
 
 // Split-K reduction: C = epi(alpha * sum_s partial[s] + beta * C), summing the
@@ -421,18 +479,20 @@ __global__ void splitk_reduce_kernel(GemmParams p, int splits) {
 
 using KernelFn = void (*)(GemmParams);
 
+template <int BN>
 KernelFn pick_f32(bool a_kmaj, bool b_kmaj) {
-    if (a_kmaj && b_kmaj) return gemm_f32_kernel<true, true>;
-    if (a_kmaj && !b_kmaj) return gemm_f32_kernel<true, false>;
-    if (!a_kmaj && b_kmaj) return gemm_f32_kernel<false, true>;
-    return gemm_f32_kernel<false, false>;
+    if (a_kmaj && b_kmaj) return gemm_f32_kernel<BN, true, true>;
+    if (a_kmaj && !b_kmaj) return gemm_f32_kernel<BN, true, false>;
+    if (!a_kmaj && b_kmaj) return gemm_f32_kernel<BN, false, true>;
+    return gemm_f32_kernel<BN, false, false>;
 }
 
+template <int BN>
 KernelFn pick_bf16(bool a_kmaj, bool b_kmaj) {
-    if (a_kmaj && b_kmaj) return gemm_bf16_kernel<true, true>;
-    if (a_kmaj && !b_kmaj) return gemm_bf16_kernel<true, false>;
-    if (!a_kmaj && b_kmaj) return gemm_bf16_kernel<false, true>;
-    return gemm_bf16_kernel<false, false>;
+    if (a_kmaj && b_kmaj) return gemm_bf16_kernel<BN, true, true>;
+    if (a_kmaj && !b_kmaj) return gemm_bf16_kernel<BN, true, false>;
+    if (!a_kmaj && b_kmaj) return gemm_bf16_kernel<BN, false, true>;
+    return gemm_bf16_kernel<BN, false, false>;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -465,12 +525,19 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
     p.stride_a = stride_a; p.stride_b = stride_b; p.stride_c = stride_c;
     p.M = (int)M; p.N = (int)N; p.K = (int)K;
-    p.tiles_m = (int)((M + BM - 1) / BM);
+    // Tile width: 128 x 128 when that gives every CU at least two workgroups
+    // (two resident workgroups per CU hide each other's barrier and LDS
+    // latency), 128 x 64 otherwise and for narrow outputs.
+    const int64_t tiles_m = (M + BM - 1) / BM;
+    const int64_t t128 = tiles_m * ((N + 127) / 128) * batch;
+    const int BN = (N <= 64 || t128 < 2 * (int64_t)ctx->num_cus) ? 64 : 128;
+    p.tiles_m = (int)tiles_m;
     p.tiles_n = (int)((N + BN - 1) / BN);
     p.alpha = alpha; p.beta = beta; p.epi = epi;
     p.out_bf16 = out_dtype == TF_BF16;
     p.vec_a = aligned16(A) && (lda % vec_elems == 0) && (stride_a % vec_elems == 0);
     p.vec_b = aligned16(B) && (ldb % vec_elems == 0) && (stride_b % vec_elems == 0);
+    p.pair_c = (reinterpret_cast<uintptr_t>(C) & 7) == 0 && (ldc % 2 == 0) && (stride_c % 2 == 0);
 
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     TF_REQUIRE(tiles < (1LL << 31), "tf_gemm: too many tiles");
@@ -499,7 +566,8 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
         p.partial = reinterpret_cast<float*>(ctx->ws);
     }
 
-    KernelFn fn = in_dtype == TF_F32 ? pick_f32(a_kmaj, b_kmaj) : pick_bf16(a_kmaj, b_kmaj);
+    KernelFn fn = in_dtype == TF_F32 ? (BN == 128 ? pick_f32<128>(a_kmaj, b_kmaj) : pick_f32<64>(a_kmaj, b_kmaj))
+                                     : (BN == 128 ? pick_bf16<128>(a_kmaj, b_kmaj) : pick_bf16<64>(a_kmaj, b_kmaj));
     TF_REQUIRE(batch < 65536 && splits < 65536, "tf_gemm: grid too large");
     dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)batch);
     fn<<<grid, kThreads, 0, ctx->stream>>>(p);

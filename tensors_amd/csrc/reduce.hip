@@ -51,13 +51,20 @@ __global__ __launch_bounds__(256) void colsum_stage1(const float* __restrict__ d
     }
 }
 
-// Stage 2 (shared by colsum and chansum): out[c] = sum_k part[k, c].
-__global__ void partial_sum_stage2(const float* __restrict__ part, float* __restrict__ out, int chunks, int cols) {
-    int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= cols) return;
+// Stage 2 (shared by colsum and chansum): out[c] = sum_k part[k, c].  A block
+// owns 64 columns; its 4 waves take chunks k = w, w + 4, ... and LDS adds the
+// four wave sums in a fixed order.
+__global__ __launch_bounds__(256) void partial_sum_stage2(const float* __restrict__ part, float* __restrict__ out,
+                                                          int chunks, int cols) {
+    __shared__ float red[4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + lane;
     float s = 0.0f;
-    for (int k = 0; k < chunks; ++k) s += part[(int64_t)k * cols + c];
-    out[c] = s;
+    if (c < cols)
+        for (int k = wave; k < chunks; k += 4) s += part[(int64_t)k * cols + c];
+    red[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && c < cols) out[c] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
 }
 
 // Stage 1 of chansum: block (c, chunk) sums samples [chunk*npc, ...) of
@@ -97,8 +104,8 @@ tf_status tf_colsum(tf_ctx* ctx, const float* dy, float* db, int64_t rows, int64
     TF_REQUIRE(db != nullptr && (rows == 0 || dy != nullptr), "tf_colsum: null pointer");
     if (rows == 0) return tf_hip_fill_f32(ctx, db, 0.0f, cols);
     const int strips = (int)((cols + kColsPerBlock - 1) / kColsPerBlock);
-    // Aim for ~2048 blocks with at least 16 rows per chunk.
-    int64_t chunks = (2048 + strips - 1) / strips;
+    // Aim for ~512 stage-1 blocks (two per CU) with at least 16 rows each.
+    int64_t chunks = (512 + strips - 1) / strips;
     chunks = std::min<int64_t>(chunks, (rows + 15) / 16);
     if (chunks < 1) chunks = 1;
     int rpc = (int)((rows + chunks - 1) / chunks);
@@ -110,7 +117,7 @@ tf_status tf_colsum(tf_ctx* ctx, const float* dy, float* db, int64_t rows, int64
     colsum_stage1<<<dim3(strips, (unsigned)chunks), 256, 0, ctx->stream>>>(dy, part, (int)rows, (int)cols, rpc, vec);
     st = tfh::check_launch("colsum_stage1");
     if (st != TF_OK) return st;
-    partial_sum_stage2<<<(unsigned)((cols + 255) / 256), 256, 0, ctx->stream>>>(part, db, (int)chunks, (int)cols);
+    partial_sum_stage2<<<(unsigned)((cols + 63) / 64), 256, 0, ctx->stream>>>(part, db, (int)chunks, (int)cols);
     return tfh::check_launch("partial_sum_stage2");
 }
 
@@ -132,7 +139,7 @@ tf_status tf_chansum_nchw(tf_ctx* ctx, const float* dy, float* db, int64_t N, in
                                                                                    (int)n_per_chunk, vec);
     st = tfh::check_launch("chansum_stage1");
     if (st != TF_OK) return st;
-    partial_sum_stage2<<<(unsigned)((C + 255) / 256), 256, 0, ctx->stream>>>(part, db, (int)chunks, (int)C);
+    partial_sum_stage2<<<(unsigned)((C + 63) / 64), 256, 0, ctx->stream>>>(part, db, (int)chunks, (int)C);
     return tfh::check_launch("partial_sum_stage2");
 }
 
