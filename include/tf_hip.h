@@ -60,7 +60,9 @@ enum {
     TF_EPI_NONE = 0,
     TF_EPI_BIAS = 1,      /* + bias[n] */
     TF_EPI_BIAS_RELU = 2, /* max(. + bias[n], 0) */
-    TF_EPI_RELU = 3       /* max(., 0) */
+    TF_EPI_RELU = 3,      /* max(., 0) */
+    TF_EPI_ROW_BIAS = 4,  /* + bias[m]          (conv forward: one bias per output channel) */
+    TF_EPI_ROW_BIAS_RELU = 5
 };
 
 /* ---------------------------------------------------------------------------
@@ -150,6 +152,20 @@ tf_status tf_gemm_strided_batched(tf_ctx* ctx, int trans_a, int trans_b,
                                   float beta, void* C, int64_t ldc, int64_t stride_c,
                                   int64_t batch, int in_dtype, int out_dtype);
 
+/* General form.  batch > 1 with reduce_batch == 0: independent products as
+ * tf_gemm_strided_batched.  reduce_batch != 0: one output,
+ *   C = epi(alpha * sum_b op(A + b*stride_a) op(B + b*stride_b) + beta*C),
+ * i.e. a GEMM whose reduction runs over (b, k) — Conv2d's weight gradient
+ * dW = sum_n dY[n] col[n]^T without the reference's per-sample host
+ * accumulation (nn/Conv2d.cpp:213-243).  stride_c is ignored then. */
+tf_status tf_gemm_ex(tf_ctx* ctx, int trans_a, int trans_b,
+                     int64_t M, int64_t N, int64_t K, float alpha,
+                     const void* A, int64_t lda, int64_t stride_a,
+                     const void* B, int64_t ldb, int64_t stride_b,
+                     float beta, void* C, int64_t ldc, int64_t stride_c,
+                     int64_t batch, int reduce_batch,
+                     int in_dtype, int out_dtype, int epilogue, const float* bias);
+
 /* ---------------------------------------------------------------------------
  * Elementwise forward + backward (bandwidth kernels, float32 unless noted).
  * Forward ops replace the registered elementwise launchers
@@ -209,6 +225,32 @@ tf_status tf_colsum(tf_ctx* ctx, const float* dy, float* db, int64_t rows, int64
  * cuda/kernels/reduce_sum_axis.cu:53-120, which is wrong for H*W > 256) */
 tf_status tf_chansum_nchw(tf_ctx* ctx, const float* dy, float* db,
                           int64_t N, int64_t C, int64_t HW);
+
+/* ---------------------------------------------------------------------------
+ * LayerNorm over the last dimension (tensor/Tensor.cpp:449-494).
+ * ------------------------------------------------------------------------- */
+/* y = (x - mean) * rstd * gamma + beta; saves mean[rows], rstd[rows]. */
+tf_status tf_layernorm_fwd(tf_ctx* ctx, const float* x, const float* gamma, const float* beta,
+                           float* y, float* mean, float* rstd, int64_t rows, int64_t cols, float eps);
+/* True gradient: dx = rstd * (g - mean(g) - xhat * mean(g * xhat)), g = dy*gamma,
+ * dgamma = sum_rows dy*xhat, dbeta = sum_rows dy.  reference_compat != 0
+ * reproduces the reference's stub (autograd/ops/LayerNormBackward.hpp:39-59):
+ * dx = dy * gamma, dgamma = dbeta = 0 (x, mean, rstd may then be NULL). */
+tf_status tf_layernorm_bwd(tf_ctx* ctx, const float* dy, const float* x, const float* gamma,
+                           const float* mean, const float* rstd, float* dx, float* dgamma,
+                           float* dbeta, int64_t rows, int64_t cols, int reference_compat);
+
+/* ---------------------------------------------------------------------------
+ * Conv2d index maps, NCHW (same parameter list as launch_im2col /
+ * launch_col2im, cuda/kernels/im2col.cuh:37-43, cuda/kernels/col2im.cuh:22-29).
+ * col is [N][C*kH*kW][outH*outW].  col2im gathers (deterministic).
+ * ------------------------------------------------------------------------- */
+tf_status tf_im2col(tf_ctx* ctx, const void* x, void* col, int64_t N, int64_t C, int64_t H, int64_t W,
+                    int64_t kH, int64_t kW, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                    int64_t pad_w, int64_t dilation_h, int64_t dilation_w, int dtype);
+tf_status tf_col2im(tf_ctx* ctx, const void* col, void* dx, int64_t N, int64_t C, int64_t H, int64_t W,
+                    int64_t kH, int64_t kW, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                    int64_t pad_w, int64_t dilation_h, int64_t dilation_w, int dtype);
 
 /* ---------------------------------------------------------------------------
  * Optimiser: fused SGD with momentum (nn/optim/SGD.hpp:3-6):

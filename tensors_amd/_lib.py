@@ -15,7 +15,7 @@ HIP_LIB_PATH = LIB_DIR / "libtf_hip.so"
 TF_OK, TF_ERR_INVALID, TF_ERR_HIP, TF_ERR_UNSUPPORTED, TF_ERR_OOM = range(5)
 TF_F32, TF_F16, TF_BF16, TF_I32, TF_I64, TF_BOOL = range(6)
 TF_COPY_H2H, TF_COPY_H2D, TF_COPY_D2H, TF_COPY_D2D = range(4)
-TF_EPI_NONE, TF_EPI_BIAS, TF_EPI_BIAS_RELU, TF_EPI_RELU = range(4)
+TF_EPI_NONE, TF_EPI_BIAS, TF_EPI_BIAS_RELU, TF_EPI_RELU, TF_EPI_ROW_BIAS, TF_EPI_ROW_BIAS_RELU = range(6)
 
 
 class TFError(RuntimeError):
@@ -54,6 +54,12 @@ SIGNATURES: dict[str, list] = {
     "tf_gemm": [_p, _i, _i, _i64, _i64, _i64, _f, _p, _i64, _p, _i64, _f, _p, _i64, _i, _i, _i, _p],
     "tf_gemm_strided_batched": [_p, _i, _i, _i64, _i64, _i64, _f, _p, _i64, _i64, _p, _i64, _i64,
                                 _f, _p, _i64, _i64, _i64, _i, _i],
+    "tf_gemm_ex": [_p, _i, _i, _i64, _i64, _i64, _f, _p, _i64, _i64, _p, _i64, _i64, _f, _p, _i64, _i64,
+                   _i64, _i, _i, _i, _i, _p],
+    "tf_layernorm_fwd": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _f],
+    "tf_layernorm_bwd": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i],
+    "tf_im2col": [_p, _p, _p] + [_i64] * 12 + [_i],
+    "tf_col2im": [_p, _p, _p] + [_i64] * 12 + [_i],
     "tf_add": [_p, _p, _p, _p, _i64, _i],
     "tf_mul": [_p, _p, _p, _p, _i64, _i],
     "tf_scale_by": [_p, _p, _p, _p, _i64, _i],

@@ -56,9 +56,11 @@ struct GemmParams {
     int64_t stride_a, stride_b, stride_c;  // batch strides (elements)
     int M, N, K;
     int tiles_m, tiles_n;
-    int k_per_split;       // multiple of the k block
+    int kb_per_split;      // k blocks per split-K slice
+    int reduce_batch;      // >1: C = sum over that many (A_b, B_b) pairs
     float alpha, beta;
     int epi;
+    int row_bias;          // bias indexed by row (m) instead of column (n)
     int out_bf16;
     int vec_a, vec_b;      // 16-byte vector loads legal for A / B
     int pair_c;            // 8-byte paired stores legal for C
@@ -187,8 +189,8 @@ __device__ __forceinline__ void store_wave(const GemmParams& p, const v16f (&acc
                                            int64_t batch_off_c, int split) {
     const int lane = threadIdx.x & 63;
     const int l32 = lane & 31, half = lane >> 5;
-    const bool has_bias = p.epi == TF_EPI_BIAS || p.epi == TF_EPI_BIAS_RELU;
-    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU;
+    const bool has_bias = p.epi != TF_EPI_NONE && p.epi != TF_EPI_RELU;
+    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU || p.epi == TF_EPI_ROW_BIAS_RELU;
     float* part = p.partial ? p.partial + (int64_t)split * p.M * p.N : nullptr;
 #pragma unroll
     for (int j = 0; j < NSUB; ++j) {
@@ -196,14 +198,17 @@ __device__ __forceinline__ void store_wave(const GemmParams& p, const v16f (&acc
         const int col = n_base + sub_row<B_PAIR>(j, l32);
         const bool c0 = col < p.N, c1 = B_PAIR && col + 1 < p.N;
         if (!c0) continue;
-        const float b0 = has_bias ? p.bias[col] : 0.0f;
-        const float b1 = (has_bias && c1) ? p.bias[col + 1] : 0.0f;
+        const bool col_bias = has_bias && !p.row_bias;
+        const float cb0 = col_bias ? p.bias[col] : 0.0f;
+        const float cb1 = (col_bias && c1) ? p.bias[col + 1] : 0.0f;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m_base + sub_row<A_PAIR>(i, 8 * (r >> 2) + 4 * half + (r & 3));
                 if (row >= p.M) continue;
+                const float rb = (has_bias && p.row_bias) ? p.bias[row] : 0.0f;
+                const float b0 = cb0 + rb, b1 = cb1 + rb;
                 if (part) {
                     float* dst = part + (int64_t)row * p.N + col;
                     dst[0] = acc[i][j][r];
@@ -247,9 +252,12 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
     const float* A = reinterpret_cast<const float*>(p.A) + (int64_t)batch * p.stride_a;
     const float* B = reinterpret_cast<const float*>(p.B) + (int64_t)batch * p.stride_b;
     const int m0 = tm * BM, n0 = tn * BN;
-    const int kbeg = split * p.k_per_split;
-    const int kend = min(p.K, kbeg + p.k_per_split);
-    const int nk = (kend - kbeg + BK - 1) / BK;
+    // k blocks of this split: block kb covers batch element kb / kb_per_b
+    // (only when reducing over the batch) and k range [(kb % kb_per_b) * BK, ...).
+    const int kb_per_b = (p.K + BK - 1) / BK;
+    const int kb_total = kb_per_b * p.reduce_batch;
+    const int kb_beg = split * p.kb_per_split;
+    const int nk = max(0, min(kb_total, kb_beg + p.kb_per_split) - kb_beg);
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -264,9 +272,13 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
 
     SA sa;
     SB sb;
+    auto load_block = [&](int kb) {
+        const int b = kb / kb_per_b, k0 = (kb - b * kb_per_b) * BK;
+        sa.load(A + (int64_t)b * p.stride_a, p.lda, m0, p.M, k0, p.K, p.vec_a);
+        sb.load(B + (int64_t)b * p.stride_b, p.ldb, n0, p.N, k0, p.K, p.vec_b);
+    };
     if (nk > 0) {
-        sa.load(A, p.lda, m0, p.M, kbeg, kend, p.vec_a);
-        sb.load(B, p.ldb, n0, p.N, kbeg, kend, p.vec_b);
+        load_block(kb_beg);
         sa.store(lds_a[0]);
         sb.store(lds_b[0]);
     }
@@ -275,11 +287,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
         const bool more = kt + 1 < nk;
-        if (more) {
-            const int k0 = kbeg + (kt + 1) * BK;
-            sa.load(A, p.lda, m0, p.M, k0, kend, p.vec_a);
-            sb.load(B, p.ldb, n0, p.N, k0, kend, p.vec_b);
-        }
+        if (more) load_block(kb_beg + kt + 1);
         float fa[2][16], fb[NSUB][16];
         const float* la = lds_a[cur];
         const float* lb = lds_b[cur];
@@ -364,9 +372,12 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(GemmParams p) {
     const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A) + (int64_t)batch * p.stride_a;
     const uint16_t* B = reinterpret_cast<const uint16_t*>(p.B) + (int64_t)batch * p.stride_b;
     const int m0 = tm * BM, n0 = tn * BN;
-    const int kbeg = split * p.k_per_split;
-    const int kend = min(p.K, kbeg + p.k_per_split);
-    const int nk = (kend - kbeg + BK - 1) / BK;
+    // k blocks of this split: block kb covers batch element kb / kb_per_b
+    // (only when reducing over the batch) and k range [(kb % kb_per_b) * BK, ...).
+    const int kb_per_b = (p.K + BK - 1) / BK;
+    const int kb_total = kb_per_b * p.reduce_batch;
+    const int kb_beg = split * p.kb_per_split;
+    const int nk = max(0, min(kb_total, kb_beg + p.kb_per_split) - kb_beg);
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -381,9 +392,13 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(GemmParams p) {
 
     SA sa;
     SB sb;
+    auto load_block = [&](int kb) {
+        const int b = kb / kb_per_b, k0 = (kb - b * kb_per_b) * BK;
+        sa.load(A + (int64_t)b * p.stride_a, p.lda, m0, p.M, k0, p.K, p.vec_a);
+        sb.load(B + (int64_t)b * p.stride_b, p.ldb, n0, p.N, k0, p.K, p.vec_b);
+    };
     if (nk > 0) {
-        sa.load(A, p.lda, m0, p.M, kbeg, kend, p.vec_a);
-        sb.load(B, p.ldb, n0, p.N, kbeg, kend, p.vec_b);
+        load_block(kb_beg);
         sa.store(lds_a[0]);
         sb.store(lds_b[0]);
     }
@@ -392,11 +407,7 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(GemmParams p) {
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
         const bool more = kt + 1 < nk;
-        if (more) {
-            const int k0 = kbeg + (kt + 1) * BK;
-            sa.load(A, p.lda, m0, p.M, k0, kend, p.vec_a);
-            sb.load(B, p.ldb, n0, p.N, k0, kend, p.vec_b);
-        }
+        if (more) load_block(kb_beg + kt + 1);
         const uint16_t* la = lds_a[cur];
         const uint16_t* lb = lds_b[cur];
 #pragma unroll
@@ -461,8 +472,8 @@ __global__ void splitk_reduce_kernel(GemmParams p, int splits) {
     const int64_t plane = total;
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU;
-    const bool has_bias = p.epi == TF_EPI_BIAS || p.epi == TF_EPI_BIAS_RELU;
+    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU || p.epi == TF_EPI_ROW_BIAS_RELU;
+    const bool has_bias = p.epi != TF_EPI_NONE && p.epi != TF_EPI_RELU;
     for (; i < total; i += stride) {
         float s = 0.0f;
         for (int k = 0; k < splits; ++k) s += p.partial[k * plane + i];
@@ -470,7 +481,7 @@ __global__ void splitk_reduce_kernel(GemmParams p, int splits) {
         const int64_t off = (int64_t)row * p.ldc + col;
         float v = p.alpha * s;
         if (p.beta != 0.0f) v += p.beta * reinterpret_cast<const float*>(p.C)[off];
-        if (has_bias) v += p.bias[col];
+        if (has_bias) v += p.row_bias ? p.bias[row] : p.bias[col];
         if (relu) v = fmaxf(v, 0.0f);
         if (p.out_bf16) reinterpret_cast<uint16_t*>(p.C)[off] = tfd::f32_to_bf16(v);
         else reinterpret_cast<float*>(p.C)[off] = v;
@@ -499,64 +510,71 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                     const void* A, int64_t lda, int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b,
-                    float beta, void* C, int64_t ldc, int64_t stride_c, int64_t batch, int in_dtype,
-                    int out_dtype, int epi, const float* bias) {
+                    float beta, void* C, int64_t ldc, int64_t stride_c, int64_t batch, int reduce_batch,
+                    int in_dtype, int out_dtype, int epi, const float* bias) {
     TF_CTX_CHECK(ctx);
     TF_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "tf_gemm: negative extent");
     TF_REQUIRE(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31), "tf_gemm: extent exceeds 2^31");
+    TF_REQUIRE(stride_a >= 0 && stride_b >= 0 && stride_c >= 0, "tf_gemm: negative batch stride");
     if (M == 0 || N == 0 || batch == 0) return TF_OK;
     TF_REQUIRE(A && B && C, "tf_gemm: null matrix pointer");
     TF_REQUIRE(in_dtype == TF_F32 || in_dtype == TF_BF16, "tf_gemm: in_dtype must be Float32 or BFloat16");
     TF_REQUIRE(out_dtype == TF_F32 || out_dtype == TF_BF16, "tf_gemm: out_dtype must be Float32 or BFloat16");
     TF_REQUIRE(beta == 0.0f || out_dtype == TF_F32, "tf_gemm: beta != 0 needs a Float32 output");
-    TF_REQUIRE(epi >= TF_EPI_NONE && epi <= TF_EPI_RELU, "tf_gemm: bad epilogue");
-    TF_REQUIRE(!(epi == TF_EPI_BIAS || epi == TF_EPI_BIAS_RELU) || bias != nullptr, "tf_gemm: epilogue needs bias");
+    TF_REQUIRE(epi >= TF_EPI_NONE && epi <= TF_EPI_ROW_BIAS_RELU, "tf_gemm: bad epilogue");
+    const bool row_bias = epi == TF_EPI_ROW_BIAS || epi == TF_EPI_ROW_BIAS_RELU;
+    TF_REQUIRE(!(epi == TF_EPI_BIAS || epi == TF_EPI_BIAS_RELU || row_bias) || bias != nullptr,
+               "tf_gemm: epilogue needs bias");
     // Leading dimensions must cover the stored row length.
     TF_REQUIRE(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N) && ldc >= N, "tf_gemm: leading dimension too small");
+    TF_REQUIRE(batch < 65536, "tf_gemm: batch exceeds 65535");
+    TF_REQUIRE(!reduce_batch || batch * ((K + 31) / 32) < (1LL << 31), "tf_gemm: reduced K too long");
 
     const bool a_kmaj = trans_a == 0;  // A[m*lda + k]
     const bool b_kmaj = trans_b != 0;  // B[n*ldb + k]
     const int esz = in_dtype == TF_F32 ? 4 : 2;
     const int vec_elems = 16 / esz;
     const int BK = in_dtype == TF_F32 ? 32 : 64;
+    const int64_t grid_batch = reduce_batch ? 1 : batch;
 
     GemmParams p{};
     p.A = A; p.B = B; p.C = C; p.bias = bias; p.partial = nullptr;
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
-    p.stride_a = stride_a; p.stride_b = stride_b; p.stride_c = stride_c;
+    p.stride_a = stride_a; p.stride_b = stride_b; p.stride_c = reduce_batch ? 0 : stride_c;
     p.M = (int)M; p.N = (int)N; p.K = (int)K;
     // Tile width: 128 x 128 when that gives every CU at least two workgroups
     // (two resident workgroups per CU hide each other's barrier and LDS
     // latency), 128 x 64 otherwise and for narrow outputs.
     const int64_t tiles_m = (M + BM - 1) / BM;
-    const int64_t t128 = tiles_m * ((N + 127) / 128) * batch;
+    const int64_t t128 = tiles_m * ((N + 127) / 128) * grid_batch;
     const int BN = (N <= 64 || t128 < 2 * (int64_t)ctx->num_cus) ? 64 : 128;
     p.tiles_m = (int)tiles_m;
     p.tiles_n = (int)((N + BN - 1) / BN);
-    p.alpha = alpha; p.beta = beta; p.epi = epi;
+    p.alpha = alpha; p.beta = beta; p.epi = epi; p.row_bias = row_bias;
     p.out_bf16 = out_dtype == TF_BF16;
+    p.reduce_batch = reduce_batch ? (int)batch : 1;
     p.vec_a = aligned16(A) && (lda % vec_elems == 0) && (stride_a % vec_elems == 0);
     p.vec_b = aligned16(B) && (ldb % vec_elems == 0) && (stride_b % vec_elems == 0);
-    p.pair_c = (reinterpret_cast<uintptr_t>(C) & 7) == 0 && (ldc % 2 == 0) && (stride_c % 2 == 0);
+    p.pair_c = (reinterpret_cast<uintptr_t>(C) & 7) == 0 && (ldc % 2 == 0) && (p.stride_c % 2 == 0);
 
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     TF_REQUIRE(tiles < (1LL << 31), "tf_gemm: too many tiles");
 
-    // Split K when one batch of tiles leaves most CUs idle and K is long.
+    // Split the k blocks when the tiles leave most CUs idle and K is long.
+    const int64_t kblocks = ((K + BK - 1) / BK) * p.reduce_batch;
     int splits = 1;
-    const int64_t kblocks = (K + BK - 1) / BK;
-    if (batch == 1 && tiles * 2 <= ctx->num_cus && kblocks >= 8) {
-        int64_t want = (ctx->num_cus + tiles - 1) / tiles;     // fill the CUs once
-        int64_t max_by_k = kblocks / 4;                         // keep >= 4 k blocks per split
-        splits = (int)std::max<int64_t>(1, std::min<int64_t>({want, max_by_k, 64}));
+    if (grid_batch == 1 && tiles * 2 <= ctx->num_cus && kblocks >= 8) {
+        int64_t want = (2 * (int64_t)ctx->num_cus + tiles - 1) / tiles;  // two workgroups per CU
+        int64_t max_by_k = kblocks / 4;                                  // >= 4 k blocks per split
+        splits = (int)std::max<int64_t>(1, std::min<int64_t>({want, max_by_k, 256}));
     }
     if (kblocks == 0) {
         splits = 1;
-        p.k_per_split = 0;
+        p.kb_per_split = 0;
     } else {
-        int64_t kblk_per_split = (kblocks + splits - 1) / splits;
-        splits = (int)((kblocks + kblk_per_split - 1) / kblk_per_split);
-        p.k_per_split = (int)(kblk_per_split * BK);
+        int64_t per = (kblocks + splits - 1) / splits;
+        splits = (int)((kblocks + per - 1) / per);
+        p.kb_per_split = (int)per;
     }
 
     if (splits > 1) {
@@ -568,8 +586,7 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
 
     KernelFn fn = in_dtype == TF_F32 ? (BN == 128 ? pick_f32<128>(a_kmaj, b_kmaj) : pick_f32<64>(a_kmaj, b_kmaj))
                                      : (BN == 128 ? pick_bf16<128>(a_kmaj, b_kmaj) : pick_bf16<64>(a_kmaj, b_kmaj));
-    TF_REQUIRE(batch < 65536 && splits < 65536, "tf_gemm: grid too large");
-    dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)batch);
+    dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)grid_batch);
     fn<<<grid, kThreads, 0, ctx->stream>>>(p);
     tf_status st = tfh::check_launch("gemm kernel");
     if (st != TF_OK) return st;
@@ -587,7 +604,7 @@ extern "C" {
 tf_status tf_gemm(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                   const void* A, int64_t lda, const void* B, int64_t ldb, float beta, void* C, int64_t ldc,
                   int in_dtype, int out_dtype, int epilogue, const float* bias) {
-    return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1,
+    return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1, 0,
                      in_dtype, out_dtype, epilogue, bias);
 }
 
@@ -596,7 +613,15 @@ tf_status tf_gemm_strided_batched(tf_ctx* ctx, int trans_a, int trans_b, int64_t
                                   int64_t ldb, int64_t stride_b, float beta, void* C, int64_t ldc,
                                   int64_t stride_c, int64_t batch, int in_dtype, int out_dtype) {
     return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
-                     stride_c, batch, in_dtype, out_dtype, TF_EPI_NONE, nullptr);
+                     stride_c, batch, 0, in_dtype, out_dtype, TF_EPI_NONE, nullptr);
+}
+
+tf_status tf_gemm_ex(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                     const void* A, int64_t lda, int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b,
+                     float beta, void* C, int64_t ldc, int64_t stride_c, int64_t batch, int reduce_batch,
+                     int in_dtype, int out_dtype, int epilogue, const float* bias) {
+    return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
+                     stride_c, batch, reduce_batch, in_dtype, out_dtype, epilogue, bias);
 }
 
 }  // extern "C"

@@ -1,0 +1,411 @@
+// LayerNorm forward and backward over the last dimension.
+//
+// Forward (tensor/Tensor.cpp:449-494): two-pass mean / variance per row,
+// y = (x - mean) * rstd * gamma + beta, saving mean and rstd.
+//
+// Backward, true gradient (the reference ships only a stub,
+// autograd/ops/LayerNormBackward.hpp:39-59):
+//   xhat = (x - mean) * rstd,  g = dy * gamma
+//   dx   = rstd * (g - mean_j(g) - xhat * mean_j(g * xhat))
+//   dgamma[j] = sum_r dy * xhat,  dbeta[j] = sum_r dy
+// Reference-compatible mode reproduces the stub exactly: dx = dy * gamma,
+// dgamma = dbeta = 0.
+//
+// Rows of up to 2048 columns: one fused pass (one wave per row, the row held
+// in registers; each wave also accumulates its rows' dgamma/dbeta column
+// partials, combined per block in LDS and then across blocks by a second,
+// fixed-order kernel).  Wider rows: a streaming row kernel for dx and a
+// column kernel for dgamma/dbeta.
+#include "common.hpp"
+
+#include <algorithm>
+#include <cmath>
+
+namespace {
+
+constexpr int kMaxCached = 8;  // 8 x 256 columns
+
+__device__ __forceinline__ int col_of(int c, int lane, int q, bool vec) {
+    return vec ? 256 * c + 4 * lane + q : 256 * c + lane + 64 * q;
+}
+
+template <int NC>
+__device__ __forceinline__ void load_row(const float* __restrict__ row, int cols, int lane, bool vec,
+                                         float (&v)[NC][4]) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        int base = 256 * c + 4 * lane;
+        if (vec && base + 4 <= cols) {
+            float4 t = *reinterpret_cast<const float4*>(row + base);
+            v[c][0] = t.x; v[c][1] = t.y; v[c][2] = t.z; v[c][3] = t.w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                int j = col_of(c, lane, q, vec);
+                v[c][q] = j < cols ? row[j] : 0.0f;
+            }
+        }
+    }
+}
+
+template <int NC>
+__device__ __forceinline__ void store_row(float* __restrict__ row, int cols, int lane, bool vec,
+                                          const float (&v)[NC][4]) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        int base = 256 * c + 4 * lane;
+        if (vec && base + 4 <= cols) {
+            *reinterpret_cast<float4*>(row + base) = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                int j = col_of(c, lane, q, vec);
+                if (j < cols) row[j] = v[c][q];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Forward.  Grid-stride over rows, one wave per row.
+// ---------------------------------------------------------------------------
+template <int NC>
+__global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                     const float* __restrict__ beta, float* __restrict__ y,
+                                                     float* __restrict__ mean, float* __restrict__ rstd, int rows,
+                                                     int cols, float eps, int vec) {
+    const int lane = threadIdx.x & 63;
+    const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int n_waves = gridDim.x * 4;
+    const float inv_c = 1.0f / (float)cols;
+    for (int r = wave_id; r < rows; r += n_waves) {
+        const float* xr = x + (int64_t)r * cols;
+        float v[NC][4];
+        load_row<NC>(xr, cols, lane, vec, v);
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s += v[c][q];
+        const float m = tfd::wave_sum(s) * inv_c;
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int j = col_of(c, lane, q, vec);
+                const float d = j < cols ? v[c][q] - m : 0.0f;
+                ss += d * d;
+            }
+        const float var = tfd::wave_sum(ss) * inv_c;
+        const float rs = 1.0f / sqrtf(var + eps);
+        if (lane == 0) {
+            mean[r] = m;
+            rstd[r] = rs;
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int j = col_of(c, lane, q, vec);
+                v[c][q] = j < cols ? (v[c][q] - m) * rs * gamma[j] + beta[j] : 0.0f;
+            }
+        store_row<NC>(y + (int64_t)r * cols, cols, lane, vec, v);
+    }
+}
+
+// Streaming forward for rows wider than the register cache.
+__global__ __launch_bounds__(256) void ln_fwd_stream_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                            const float* __restrict__ beta, float* __restrict__ y,
+                                                            float* __restrict__ mean, float* __restrict__ rstd,
+                                                            int rows, int cols, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int n_waves = gridDim.x * 4;
+    const float inv_c = 1.0f / (float)cols;
+    for (int r = wave_id; r < rows; r += n_waves) {
+        const float* xr = x + (int64_t)r * cols;
+        float s = 0.0f;
+        for (int j = lane; j < cols; j += 64) s += xr[j];
+        const float m = tfd::wave_sum(s) * inv_c;
+        float ss = 0.0f;
+        for (int j = lane; j < cols; j += 64) {
+            float d = xr[j] - m;
+            ss += d * d;
+        }
+        const float rs = 1.0f / sqrtf(tfd::wave_sum(ss) * inv_c + eps);
+        if (lane == 0) {
+            mean[r] = m;
+            rstd[r] = rs;
+        }
+        float* yr = y + (int64_t)r * cols;
+        for (int j = lane; j < cols; j += 64) yr[j] = (xr[j] - m) * rs * gamma[j] + beta[j];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fused backward for cols <= 256 * NC.  Block b handles rows
+// [b * rpb, (b+1) * rpb); each wave takes every 4th of them.  Column partial
+// sums of dy * xhat and dy go to part[b][0][:] and part[b][1][:].
+// ---------------------------------------------------------------------------
+template <int NC>
+__global__ __launch_bounds__(256) void ln_bwd_fused_kernel(const float* __restrict__ dy, const float* __restrict__ x,
+                                                           const float* __restrict__ gamma,
+                                                           const float* __restrict__ mean,
+                                                           const float* __restrict__ rstd, float* __restrict__ dx,
+                                                           float* __restrict__ part, int rows, int cols,
+                                                           int rows_per_block, int vec) {
+    __shared__ float red[4][2][NC * 256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * rows_per_block;
+    const int r1 = min(rows, r0 + rows_per_block);
+    const float inv_c = 1.0f / (float)cols;
+    float gacc[NC][4], bacc[NC][4];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) gacc[c][q] = bacc[c][q] = 0.0f;
+    float gm[NC][4];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int j = col_of(c, lane, q, vec);
+            gm[c][q] = j < cols ? gamma[j] : 0.0f;
+        }
+    for (int r = r0 + wave; r < r1; r += 4) {
+        float xv[NC][4], gv[NC][4];
+        load_row<NC>(x + (int64_t)r * cols, cols, lane, vec, xv);
+        load_row<NC>(dy + (int64_t)r * cols, cols, lane, vec, gv);
+        const float m = mean[r], rs = rstd[r];
+        float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float xh = (xv[c][q] - m) * rs;
+                const float g = gv[c][q] * gm[c][q];
+                s1 += g;
+                s2 += g * xh;
+                gacc[c][q] += gv[c][q] * xh;
+                bacc[c][q] += gv[c][q];
+                xv[c][q] = xh;
+            }
+        s1 = tfd::wave_sum(s1) * inv_c;
+        s2 = tfd::wave_sum(s2) * inv_c;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float g = gv[c][q] * gm[c][q];
+                xv[c][q] = rs * (g - s1 - xv[c][q] * s2);
+            }
+        store_row<NC>(dx + (int64_t)r * cols, cols, lane, vec, xv);
+    }
+    // Block combine of the four waves' column partials (fixed order).
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int slot = 256 * c + 4 * lane + q;   // storage slot, not column
+            red[wave][0][slot] = gacc[c][q];
+            red[wave][1][slot] = bacc[c][q];
+        }
+    __syncthreads();
+    for (int slot = threadIdx.x; slot < NC * 256; slot += 256) {
+        const int c = slot / 256, rem = slot % 256, l = rem / 4, q = rem % 4;
+        const int j = col_of(c, l, q, vec);
+        if (j >= cols) continue;
+        float* pg = part + (int64_t)blockIdx.x * 2 * cols;
+        pg[j] = (red[0][0][slot] + red[1][0][slot]) + (red[2][0][slot] + red[3][0][slot]);
+        pg[cols + j] = (red[0][1][slot] + red[1][1][slot]) + (red[2][1][slot] + red[3][1][slot]);
+    }
+}
+
+// Streaming dx for wide rows (three passes over the row).
+__global__ __launch_bounds__(256) void ln_bwd_dx_stream_kernel(const float* __restrict__ dy, const float* __restrict__ x,
+                                                               const float* __restrict__ gamma,
+                                                               const float* __restrict__ mean,
+                                                               const float* __restrict__ rstd, float* __restrict__ dx,
+                                                               int rows, int cols) {
+    const int lane = threadIdx.x & 63;
+    const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int n_waves = gridDim.x * 4;
+    const float inv_c = 1.0f / (float)cols;
+    for (int r = wave_id; r < rows; r += n_waves) {
+        const float* xr = x + (int64_t)r * cols;
+        const float* gr = dy + (int64_t)r * cols;
+        const float m = mean[r], rs = rstd[r];
+        float s1 = 0.0f, s2 = 0.0f;
+        for (int j = lane; j < cols; j += 64) {
+            const float g = gr[j] * gamma[j];
+            s1 += g;
+            s2 += g * (xr[j] - m) * rs;
+        }
+        s1 = tfd::wave_sum(s1) * inv_c;
+        s2 = tfd::wave_sum(s2) * inv_c;
+        float* dr = dx + (int64_t)r * cols;
+        for (int j = lane; j < cols; j += 64) {
+            const float g = gr[j] * gamma[j];
+            dr[j] = rs * (g - s1 - (xr[j] - m) * rs * s2);
+        }
+    }
+}
+
+// Column partials of dy * xhat and dy for wide rows: block (strip, chunk).
+__global__ __launch_bounds__(256) void ln_bwd_cols_kernel(const float* __restrict__ dy, const float* __restrict__ x,
+                                                          const float* __restrict__ mean,
+                                                          const float* __restrict__ rstd, float* __restrict__ part,
+                                                          int rows, int cols, int rows_per_chunk) {
+    __shared__ float red[4][2][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = blockIdx.x * 64 + lane;
+    const int r0 = blockIdx.y * rows_per_chunk;
+    const int r1 = min(rows, r0 + rows_per_chunk);
+    float ga = 0.0f, ba = 0.0f;
+    if (j < cols)
+        for (int r = r0 + wave; r < r1; r += 4) {
+            const float g = dy[(int64_t)r * cols + j];
+            ga += g * ((x[(int64_t)r * cols + j] - mean[r]) * rstd[r]);
+            ba += g;
+        }
+    red[wave][0][lane] = ga;
+    red[wave][1][lane] = ba;
+    __syncthreads();
+    if (wave == 0 && j < cols) {
+        float* pg = part + (int64_t)blockIdx.y * 2 * cols;
+        pg[j] = (red[0][0][lane] + red[1][0][lane]) + (red[2][0][lane] + red[3][0][lane]);
+        pg[cols + j] = (red[0][1][lane] + red[1][1][lane]) + (red[2][1][lane] + red[3][1][lane]);
+    }
+}
+
+// out_g[j] = sum_b part[b][0][j], out_b[j] = sum_b part[b][1][j] (fixed order).
+__global__ __launch_bounds__(256) void ln_partials_kernel(const float* __restrict__ part, float* __restrict__ dgamma,
+                                                          float* __restrict__ dbeta, int nparts, int cols) {
+    __shared__ float red[4][2][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = blockIdx.x * 64 + lane;
+    float g = 0.0f, b = 0.0f;
+    if (j < cols)
+        for (int k = wave; k < nparts; k += 4) {
+            g += part[(int64_t)k * 2 * cols + j];
+            b += part[(int64_t)k * 2 * cols + cols + j];
+        }
+    red[wave][0][lane] = g;
+    red[wave][1][lane] = b;
+    __syncthreads();
+    if (wave == 0 && j < cols) {
+        dgamma[j] = (red[0][0][lane] + red[1][0][lane]) + (red[2][0][lane] + red[3][0][lane]);
+        dbeta[j] = (red[0][1][lane] + red[1][1][lane]) + (red[2][1][lane] + red[3][1][lane]);
+    }
+}
+
+// Reference-compatible stub: dx = dy * gamma[col].
+__global__ void ln_bwd_stub_kernel(const float* __restrict__ dy, const float* __restrict__ gamma,
+                                   float* __restrict__ dx, int64_t n, int cols) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) dx[i] = dy[i] * gamma[i % cols];
+}
+
+int chunks_for(int64_t cols) {
+    int64_t c = (cols + 255) / 256;
+    if (c <= 1) return 1;
+    if (c <= 2) return 2;
+    if (c <= 4) return 4;
+    if (c <= kMaxCached) return kMaxCached;
+    return 0;
+}
+
+bool row_vec(const void* p, int64_t cols) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && cols % 4 == 0; }
+
+int row_grid(int64_t rows) { return (int)std::min<int64_t>((rows + 3) / 4, 2048); }
+
+}  // namespace
+
+extern "C" {
+
+tf_status tf_layernorm_fwd(tf_ctx* ctx, const float* x, const float* gamma, const float* beta, float* y,
+                           float* mean, float* rstd, int64_t rows, int64_t cols, float eps) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(rows >= 0 && cols >= 0 && rows < (1LL << 31) && cols < (1LL << 31), "tf_layernorm_fwd: bad extent");
+    if (rows == 0 || cols == 0) return TF_OK;
+    TF_REQUIRE(x && gamma && beta && y && mean && rstd, "tf_layernorm_fwd: null pointer");
+    const int vec = row_vec(x, cols) && row_vec(y, cols);
+    const dim3 grid(row_grid(rows));
+    switch (chunks_for(cols)) {
+    case 1: ln_fwd_kernel<1><<<grid, 256, 0, ctx->stream>>>(x, gamma, beta, y, mean, rstd, (int)rows, (int)cols, eps, vec); break;
+    case 2: ln_fwd_kernel<2><<<grid, 256, 0, ctx->stream>>>(x, gamma, beta, y, mean, rstd, (int)rows, (int)cols, eps, vec); break;
+    case 4: ln_fwd_kernel<4><<<grid, 256, 0, ctx->stream>>>(x, gamma, beta, y, mean, rstd, (int)rows, (int)cols, eps, vec); break;
+    case kMaxCached: ln_fwd_kernel<kMaxCached><<<grid, 256, 0, ctx->stream>>>(x, gamma, beta, y, mean, rstd, (int)rows, (int)cols, eps, vec); break;
+    default: ln_fwd_stream_kernel<<<grid, 256, 0, ctx->stream>>>(x, gamma, beta, y, mean, rstd, (int)rows, (int)cols, eps); break;
+    }
+    return tfh::check_launch("ln_fwd_kernel");
+}
+
+tf_status tf_layernorm_bwd(tf_ctx* ctx, const float* dy, const float* x, const float* gamma, const float* mean,
+                           const float* rstd, float* dx, float* dgamma, float* dbeta, int64_t rows, int64_t cols,
+                           int reference_compat) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(rows >= 0 && cols >= 0 && rows < (1LL << 31) && cols < (1LL << 31), "tf_layernorm_bwd: bad extent");
+    if (cols == 0) return TF_OK;
+    TF_REQUIRE(gamma && (rows == 0 || (dy && dx)), "tf_layernorm_bwd: null pointer");
+    if (reference_compat) {
+        if (rows > 0) {
+            ln_bwd_stub_kernel<<<tfd::grid_for(rows * cols, 4), 256, 0, ctx->stream>>>(dy, gamma, dx, rows * cols, (int)cols);
+            tf_status st = tfh::check_launch("ln_bwd_stub_kernel");
+            if (st != TF_OK) return st;
+        }
+        if (dgamma) { tf_status st = tf_hip_fill_f32(ctx, dgamma, 0.0f, cols); if (st != TF_OK) return st; }
+        if (dbeta) { tf_status st = tf_hip_fill_f32(ctx, dbeta, 0.0f, cols); if (st != TF_OK) return st; }
+        return TF_OK;
+    }
+    TF_REQUIRE(x && mean && rstd && dgamma && dbeta, "tf_layernorm_bwd: null pointer");
+    if (rows == 0) {
+        tf_status st = tf_hip_fill_f32(ctx, dgamma, 0.0f, cols);
+        if (st != TF_OK) return st;
+        return tf_hip_fill_f32(ctx, dbeta, 0.0f, cols);
+    }
+    const int nc = chunks_for(cols);
+    if (nc > 0) {
+        // ~256 blocks of >= 4 rows each.
+        int64_t rpb = std::max<int64_t>(4, (rows + 255) / 256);
+        int64_t nblocks = (rows + rpb - 1) / rpb;
+        tf_status st = tfh::ensure_workspace(ctx, (size_t)nblocks * 2 * cols * sizeof(float));
+        if (st != TF_OK) return st;
+        float* part = reinterpret_cast<float*>(ctx->ws);
+        const int vec = row_vec(x, cols) && row_vec(dy, cols) && row_vec(dx, cols);
+        const dim3 grid((unsigned)nblocks);
+#define TF_LN_BWD(NC) ln_bwd_fused_kernel<NC><<<grid, 256, 0, ctx->stream>>>(dy, x, gamma, mean, rstd, dx, part, \
+                                                     (int)rows, (int)cols, (int)rpb, vec)
+        switch (nc) {
+        case 1: TF_LN_BWD(1); break;
+        case 2: TF_LN_BWD(2); break;
+        case 4: TF_LN_BWD(4); break;
+        default: TF_LN_BWD(kMaxCached); break;
+        }
+#undef TF_LN_BWD
+        st = tfh::check_launch("ln_bwd_fused_kernel");
+        if (st != TF_OK) return st;
+        ln_partials_kernel<<<(unsigned)((cols + 63) / 64), 256, 0, ctx->stream>>>(part, dgamma, dbeta, (int)nblocks, (int)cols);
+        return tfh::check_launch("ln_partials_kernel");
+    }
+    ln_bwd_dx_stream_kernel<<<row_grid(rows), 256, 0, ctx->stream>>>(dy, x, gamma, mean, rstd, dx, (int)rows, (int)cols);
+    tf_status st = tfh::check_launch("ln_bwd_dx_stream_kernel");
+    if (st != TF_OK) return st;
+    const int strips = (int)((cols + 63) / 64);
+    int64_t chunks = std::max<int64_t>(1, std::min<int64_t>((512 + strips - 1) / strips, (rows + 15) / 16));
+    int rpc = (int)((rows + chunks - 1) / chunks);
+    chunks = (rows + rpc - 1) / rpc;
+    st = tfh::ensure_workspace(ctx, (size_t)chunks * 2 * cols * sizeof(float));
+    if (st != TF_OK) return st;
+    float* part = reinterpret_cast<float*>(ctx->ws);
+    ln_bwd_cols_kernel<<<dim3(strips, (unsigned)chunks), 256, 0, ctx->stream>>>(dy, x, mean, rstd, part, (int)rows,
+                                                                               (int)cols, rpc);
+    st = tfh::check_launch("ln_bwd_cols_kernel");
+    if (st != TF_OK) return st;
+    ln_partials_kernel<<<(unsigned)strips, 256, 0, ctx->stream>>>(part, dgamma, dbeta, (int)chunks, (int)cols);
+    return tfh::check_launch("ln_partials_kernel");
+}
+
+}  // extern "C"

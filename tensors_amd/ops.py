@@ -172,3 +172,72 @@ def sgd_momentum(p, g, v, lr, mu, p_bf16=None):
     call("tf_sgd_momentum", _ctx(p), p.ptr, g.ptr, v.ptr if v is not None else None,
          p_bf16.ptr if p_bf16 is not None else None, n, lr, mu)
     return p
+
+
+def gemm_ex(a, b, c, M, N, K, *, lda, ldb, ldc, trans_a=False, trans_b=False, stride_a=0, stride_b=0, stride_c=0,
+            batch=1, reduce_batch=False, alpha=1.0, beta=0.0, epilogue=_lib.TF_EPI_NONE, bias=None):
+    """Raw tf_gemm_ex on DeviceArrays (extents and strides in elements; the
+    caller is responsible for them fitting the arrays — checked here)."""
+    def need(rows, ld, stride, nb):
+        return (nb - 1) * stride + (rows - 1) * ld if rows > 0 else 0
+    a_rows, a_w = (K, M) if trans_a else (M, K)
+    b_rows, b_w = (N, K) if trans_b else (K, N)
+    nb = batch
+    if K > 0 and need(a_rows, lda, stride_a, nb) + a_w > a.size:
+        raise ValueError("gemm_ex: A extents exceed the array")
+    if K > 0 and need(b_rows, ldb, stride_b, nb) + b_w > b.size:
+        raise ValueError("gemm_ex: B extents exceed the array")
+    if need(M, ldc, 0 if reduce_batch else stride_c, 1 if reduce_batch else nb) + N > c.size:
+        raise ValueError("gemm_ex: C extents exceed the array")
+    call("tf_gemm_ex", _ctx(a), int(trans_a), int(trans_b), M, N, K, alpha, a.ptr, lda, stride_a, b.ptr, ldb,
+         stride_b, beta, c.ptr, ldc, stride_c, batch, int(reduce_batch), a.tf_dtype, c.tf_dtype, epilogue,
+         bias.ptr if bias is not None else None)
+    return c
+
+
+def layernorm_fwd(x, gamma, beta, y, mean, rstd, eps=1e-5):
+    rows, cols = _rows_cols(x)
+    if gamma.size != cols or beta.size != cols or mean.size != rows or rstd.size != rows:
+        raise ValueError("layernorm_fwd: parameter sizes")
+    _same(x, y)
+    call("tf_layernorm_fwd", _ctx(x), x.ptr, gamma.ptr, beta.ptr, y.ptr, mean.ptr, rstd.ptr, rows, cols, eps)
+    return y
+
+
+def layernorm_bwd(dy, x, gamma, mean, rstd, dx, dgamma, dbeta, reference_compat=False):
+    rows, cols = _rows_cols(dy)
+    _same(dy, dx)
+    if gamma.size != cols or dgamma.size != cols or dbeta.size != cols:
+        raise ValueError("layernorm_bwd: parameter sizes")
+    if not reference_compat:
+        _same(dy, x)
+        if mean.size != rows or rstd.size != rows:
+            raise ValueError("layernorm_bwd: mean/rstd sizes")
+    call("tf_layernorm_bwd", _ctx(dy), dy.ptr, x.ptr if x is not None else None, gamma.ptr,
+         mean.ptr if mean is not None else None, rstd.ptr if rstd is not None else None, dx.ptr, dgamma.ptr,
+         dbeta.ptr, rows, cols, int(reference_compat))
+    return dx
+
+
+def conv_out(H, k, s, p, d):
+    return (H + 2 * p - d * (k - 1) - 1) // s + 1
+
+
+def im2col(x, col, kH, kW, stride=(1, 1), pad=(0, 0), dil=(1, 1)):
+    N, Cc, H, W = x.shape
+    oh, ow = conv_out(H, kH, stride[0], pad[0], dil[0]), conv_out(W, kW, stride[1], pad[1], dil[1])
+    if col.size != N * Cc * kH * kW * oh * ow:
+        raise ValueError("im2col: col has the wrong size")
+    call("tf_im2col", _ctx(x), x.ptr, col.ptr, N, Cc, H, W, kH, kW, stride[0], stride[1], pad[0], pad[1],
+         dil[0], dil[1], x.tf_dtype)
+    return col
+
+
+def col2im(col, dx, kH, kW, stride=(1, 1), pad=(0, 0), dil=(1, 1)):
+    N, Cc, H, W = dx.shape
+    oh, ow = conv_out(H, kH, stride[0], pad[0], dil[0]), conv_out(W, kW, stride[1], pad[1], dil[1])
+    if col.size != N * Cc * kH * kW * oh * ow:
+        raise ValueError("col2im: col has the wrong size")
+    call("tf_col2im", _ctx(col), col.ptr, dx.ptr, N, Cc, H, W, kH, kW, stride[0], stride[1], pad[0], pad[1],
+         dil[0], dil[1], col.tf_dtype)
+    return dx

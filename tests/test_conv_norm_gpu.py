@@ -1,0 +1,173 @@
+"""LayerNorm forward/backward, im2col/col2im and the Conv2d backward built from
+them (batched / batch-reduced MFMA GEMMs), against the CPU oracle."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from tensors_amd import synth
+from tests.conftest import assert_bitexact, assert_close
+
+pytestmark = pytest.mark.gpu
+RTOL32 = 1e-4
+
+
+def _ops():
+    from tensors_amd import ops
+    return ops
+
+
+@pytest.mark.parametrize("R,Cc", [(1024, 1024), (64, 128), (7, 3000), (33, 1001), (1, 1), (300, 2048)])
+def test_layernorm_fwd_bwd(ctx, R, Cc):
+    ops = _ops()
+    x = synth.normal(201 + Cc, (R, Cc))
+    dy = synth.normal(202 + Cc, (R, Cc))
+    gamma = synth.normal(203, (Cc,), mean=1.0, std=0.1)
+    beta = synth.normal(204, (Cc,))
+    y_ref, m_ref, r_ref = oracle.layernorm_fwd(x, gamma, beta)
+    dx_, dg_, db_ = ctx.array(x), ctx.array(gamma), ctx.array(beta)
+    y, mean, rstd = ctx.empty((R, Cc)), ctx.empty((R,)), ctx.empty((R,))
+    ops.layernorm_fwd(dx_, dg_, db_, y, mean, rstd)
+    assert_close(y.numpy(), y_ref, RTOL32, "ln fwd")
+    assert_close(mean.numpy(), m_ref, RTOL32, "ln mean", atol=1e-6)
+    assert_close(rstd.numpy(), r_ref, RTOL32, "ln rstd")
+    dx, dgam, dbet = ctx.empty((R, Cc)), ctx.empty((Cc,)), ctx.empty((Cc,))
+    ops.layernorm_bwd(ctx.array(dy), dx_, dg_, mean, rstd, dx, dgam, dbet)
+    want_dx, want_dg, want_db = oracle.layernorm_bwd(x, dy, gamma, m_ref, r_ref)
+    assert_close(dx.numpy(), want_dx, RTOL32, "ln dx")
+    assert_close(dgam.numpy(), want_dg, RTOL32, "ln dgamma")
+    assert_close(dbet.numpy(), want_db, RTOL32, "ln dbeta")
+
+
+def test_layernorm_bwd_reference_stub_bitexact(ctx):
+    ops = _ops()
+    R, Cc = 1024, 1024
+    dy = synth.normal(211, (R, Cc))
+    gamma = synth.normal(212, (Cc,), mean=1.0, std=0.1)
+    dx, dgam, dbet = ctx.empty((R, Cc)), ctx.array(np.ones(Cc, np.float32)), ctx.array(np.ones(Cc, np.float32))
+    ops.layernorm_bwd(ctx.array(dy), None, ctx.array(gamma), None, None, dx, dgam, dbet, reference_compat=True)
+    want_dx, want_dg, want_db = oracle.layernorm_bwd_stub(dy, gamma)
+    assert_bitexact(dx.numpy(), want_dx, "stub dx")
+    assert_bitexact(dgam.numpy(), want_dg, "stub dgamma")
+    assert_bitexact(dbet.numpy(), want_db, "stub dbeta")
+
+
+IM2COL_CASES = [
+    # N, C, H, W, k, stride, pad, dil
+    (2, 3, 8, 8, 3, 1, 1, 1),
+    (2, 4, 9, 7, 3, 2, 1, 1),
+    (1, 2, 10, 10, 3, 1, 2, 2),
+    (3, 1, 5, 6, 1, 1, 0, 1),
+    (128, 3, 32, 32, 3, 1, 1, 1),       # C4 conv1
+    (16, 32, 32, 32, 3, 2, 1, 1),       # C4 conv2 geometry (reduced batch)
+]
+
+
+@pytest.mark.parametrize("case", IM2COL_CASES)
+def test_im2col_bitexact_and_col2im_adjoint(ctx, case):
+    ops = _ops()
+    N, Cc, H, W, k, s, p, d = case
+    x = synth.normal(221 + N * Cc, (N, Cc, H, W))
+    col_ref = oracle.im2col(x, k, k, s, s, p, p, d, d)
+    col = ctx.empty(col_ref.shape)
+    ops.im2col(ctx.array(x), col, k, k, (s, s), (p, p), (d, d))
+    assert_bitexact(col.numpy(), col_ref, f"im2col {case}")
+    c = synth.normal(222 + N, col_ref.shape)
+    dx = ctx.empty(x.shape)
+    ops.col2im(ctx.array(c), dx, k, k, (s, s), (p, p), (d, d))
+    assert_close(dx.numpy(), oracle.col2im(c, x.shape, k, k, s, s, p, p, d, d), 1e-5, "col2im vs scatter")
+    # adjoint: <im2col x, c> == <x, col2im c>
+    lhs = float(np.dot(col_ref.astype(np.float64).ravel(), c.astype(np.float64).ravel()))
+    rhs = float(np.dot(x.astype(np.float64).ravel(), dx.numpy().astype(np.float64).ravel()))
+    assert abs(lhs - rhs) <= 1e-4 * (abs(lhs) + 1.0)
+
+
+def _conv_bwd_gpu(ctx, x, w, gout, stride, pad, need_dx=True):
+    """Conv2d backward from the C-ABI pieces, as the Conv2dModule backward node runs it."""
+    from tensors_amd._lib import TF_EPI_NONE
+    ops = _ops()
+    N, Cin, H, W = x.shape
+    Cout, _, kH, kW = w.shape
+    oh, ow = ops.conv_out(H, kH, stride, pad, 1), ops.conv_out(W, kW, stride, pad, 1)
+    P, KK = oh * ow, Cin * kH * kW
+    dx_, dw_, dg_ = ctx.array(x), ctx.array(w), ctx.array(gout)
+    col = ctx.empty((N, KK, P))
+    ops.im2col(dx_, col, kH, kW, (stride, stride), (pad, pad))
+    gw = ctx.empty((Cout, KK))
+    # dW = sum_n dY[n] (Cout x P) @ col[n]^T (P x KK)
+    ops.gemm_ex(dg_, col, gw, Cout, KK, P, lda=P, ldb=P, ldc=KK, trans_b=True, stride_a=Cout * P,
+                stride_b=KK * P, batch=N, reduce_batch=True, epilogue=TF_EPI_NONE)
+    gb = ctx.empty((Cout,))
+    ops.chansum_nchw(dg_, gb)
+    gin = None
+    if need_dx:
+        dcol = ctx.empty((N, KK, P))
+        # dcol[n] = W^T (KK x Cout) @ dY[n] (Cout x P)
+        ops.gemm_ex(dw_, dg_, dcol, KK, P, Cout, lda=KK, ldb=P, ldc=P, trans_a=True, stride_a=0,
+                    stride_b=Cout * P, stride_c=KK * P, batch=N)
+        gin = ctx.empty(x.shape)
+        ops.col2im(dcol, gin, kH, kW, (stride, stride), (pad, pad))
+    return gin, gw, gb
+
+
+CONV_CASES = [(2, 3, 8, 8, 4, 3, 1, 1), (4, 5, 9, 9, 6, 3, 2, 1), (2, 2, 6, 6, 3, 1, 1, 0),
+              (8, 3, 32, 32, 32, 3, 1, 1), (4, 32, 32, 32, 64, 3, 2, 1)]
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_conv2d_backward_vs_reference_loop(ctx, case):
+    N, Cin, H, W, Cout, k, s, p = case
+    x = synth.normal(231 + N, (N, Cin, H, W))
+    w = synth.normal(232 + Cout, (Cout, Cin, k, k), std=0.2)
+    oh = (H + 2 * p - k) // s + 1
+    gout = synth.normal(233, (N, Cout, oh, oh))
+    gin, gw, gb = _conv_bwd_gpu(ctx, x, w, gout, s, p)
+    rin, rw, rb = oracle.conv2d_bwd(x, w, gout, (s, s), (p, p), (1, 1))
+    assert_close(gin.numpy(), rin, RTOL32, f"conv dX {case}")
+    assert_close(gw.numpy().reshape(rw.shape), rw, RTOL32, f"conv dW {case}")
+    assert_close(gb.numpy(), rb, RTOL32, f"conv db {case}")
+
+
+def test_conv2d_backward_golden_1x1(ctx):
+    # nn/conv2d_backward_test.cpp:110-160: 1x1 kernel golden values.
+    x = np.array([1, 2, 3, 4], np.float32).reshape(1, 1, 2, 2)
+    w = np.array([0.5], np.float32).reshape(1, 1, 1, 1)
+    gout = np.array([0.4, 0.8, 1.2, 1.6], np.float32).reshape(1, 1, 2, 2)
+    gin, gw, gb = _conv_bwd_gpu(ctx, x, w, gout, 1, 0)
+    rin, rw, rb = oracle.conv2d_bwd(x, w, gout, (1, 1), (0, 0), (1, 1))
+    assert_close(gin.numpy(), rin, 1e-6, "1x1 dX", atol=1e-7)
+    assert_close(gw.numpy().reshape(rw.shape), rw, 1e-6, "1x1 dW", atol=1e-7)
+    assert_close(gb.numpy(), rb, 1e-6, "1x1 db", atol=1e-7)
+
+
+@pytest.mark.parametrize("relu", [False, True])
+def test_conv2d_forward_row_bias(ctx, relu):
+    from tensors_amd._lib import TF_EPI_ROW_BIAS, TF_EPI_ROW_BIAS_RELU
+    ops = _ops()
+    N, Cin, H, W, Cout, k, s, p = 4, 3, 16, 16, 8, 3, 1, 1
+    x = synth.normal(241, (N, Cin, H, W))
+    w = synth.normal(242, (Cout, Cin, k, k), std=0.2)
+    b = synth.normal(243, (Cout,))
+    P, KK = H * W, Cin * k * k
+    col = ctx.empty((N, KK, P))
+    ops.im2col(ctx.array(x), col, k, k, (s, s), (p, p))
+    y = ctx.empty((N, Cout, H, W))
+    ops.gemm_ex(ctx.array(w), col, y, Cout, P, KK, lda=KK, ldb=P, ldc=P, stride_b=KK * P, stride_c=Cout * P,
+                batch=N, epilogue=TF_EPI_ROW_BIAS_RELU if relu else TF_EPI_ROW_BIAS, bias=ctx.array(b))
+    want = oracle.conv2d_fwd(x, w, b, s, p)
+    assert_close(y.numpy(), np.maximum(want, 0) if relu else want, RTOL32, "conv fwd")
+
+
+def test_gemm_row_bias_relu_splitk(ctx):
+    from tensors_amd._lib import TF_EPI_ROW_BIAS_RELU
+    ops = _ops()
+    M, N, K = 40, 24, 9000
+    a = synth.normal(251, (M, K))
+    b = synth.normal(252, (K, N))
+    bias = synth.normal(253, (M,))
+    c = ctx.empty((M, N))
+    ops.gemm_ex(ctx.array(a), ctx.array(b), c, M, N, K, lda=K, ldb=N, ldc=N, epilogue=TF_EPI_ROW_BIAS_RELU,
+                bias=ctx.array(bias))
+    want = np.maximum(a.astype(np.float64) @ b.astype(np.float64) + bias[:, None], 0)
+    assert_close(c.numpy(), want, RTOL32, "row bias relu split-K")
