@@ -172,6 +172,7 @@ tf_status tf_gemm_ex(tf_ctx* ctx, int trans_a, int trans_b,
  * (cuda/CudaKernelRegistry.hpp:15-26, cuda/kernels/elementwise.cu:80-173).
  * ------------------------------------------------------------------------- */
 tf_status tf_add(tf_ctx* ctx, const void* a, const void* b, void* out, int64_t n, int dtype);
+tf_status tf_sub(tf_ctx* ctx, const void* a, const void* b, void* out, int64_t n, int dtype);
 tf_status tf_mul(tf_ctx* ctx, const void* a, const void* b, void* out, int64_t n, int dtype);
 /* out = a * s[0] where s is a device scalar. */
 tf_status tf_scale_by(tf_ctx* ctx, const void* a, const float* s, void* out, int64_t n, int dtype);
@@ -251,6 +252,20 @@ tf_status tf_im2col(tf_ctx* ctx, const void* x, void* col, int64_t N, int64_t C,
 tf_status tf_col2im(tf_ctx* ctx, const void* col, void* dx, int64_t N, int64_t C, int64_t H, int64_t W,
                     int64_t kH, int64_t kW, int64_t stride_h, int64_t stride_w, int64_t pad_h,
                     int64_t pad_w, int64_t dilation_h, int64_t dilation_w, int dtype);
+
+/* ---------------------------------------------------------------------------
+ * Layout kernels over contiguous data viewed as [outer][reduce][inner].
+ * ------------------------------------------------------------------------- */
+/* out[o][i] = sum_r x[o][r][i]  (Tensor::sum along one dim, tensor/Tensor.cpp:513-561) */
+tf_status tf_sum_dim(tf_ctx* ctx, const float* x, float* out, int64_t outer, int64_t reduce, int64_t inner);
+/* out[o][r][i] = up[o][i]  (SumBackward's broadcast along the reduced dim;
+ * equals the reference's autograd/ops/SumBackward.hpp:35-37 wherever that
+ * one is correct, i.e. for uniform upstream gradients) */
+tf_status tf_expand_dim(tf_ctx* ctx, const float* up, float* out, int64_t outer, int64_t reduce, int64_t inner);
+/* out[b][j][i] = x[b][i][j] for b < batch  (Tensor::transpose of the last two
+ * dims, tensor/Tensor.cpp:579-619, which copies) */
+tf_status tf_transpose2d(tf_ctx* ctx, const void* x, void* out, int64_t batch, int64_t rows, int64_t cols,
+                         int dtype);
 
 /* ---------------------------------------------------------------------------
  * Optimiser: fused SGD with momentum (nn/optim/SGD.hpp:3-6):

@@ -1,0 +1,60 @@
+/*
+ * tfa_harness.h — C entry points of libtensorforge.so that drive the C++20
+ * tensorforge API (Tensor / Engine / nn / optim) end to end.  They are the
+ * test and benchmark harness of this backend (the reference's equivalents
+ * are its example programs, examples/train_mlp.cpp and
+ * examples/train_cnn.cpp, and its doctest suites); they are not part of the
+ * drop-in kernel boundary, which is include/tf_hip.h.
+ *
+ * Every function returns 0 on success and non-zero on failure, with a
+ * message from tfa_last_error().
+ */
+#ifndef TFA_HARNESS_H
+#define TFA_HARNESS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+const char* tfa_last_error(void);
+
+/* MLP training through nn::Linear, nn::ReLU, nn::CrossEntropyLoss,
+ * Tensor::backward and optim::SGD.
+ *   dims[ndims]        layer widths, e.g. {784, 256, 128, 10}
+ *   xs                 [n_batches][batch][dims[0]] float32, ys [n_batches][batch] int64;
+ *                      step s uses batch s % n_batches
+ *   on_gpu             0: CPU tensors, 1: GPU 0
+ *   reference_compat   1: Linear drops its bias (as the reference does)
+ *   bf16               1: Linear layers compute in bf16 with fp32 master weights (GPU only)
+ *   init_weights       NULL (module init) or the concatenated weights [dims[l+1] x dims[l]]
+ *   losses[steps]      out: loss of every step (read back after the loop)
+ *   final_weights      NULL or out: concatenated weights after the last step
+ *   ms_per_step        NULL or out: wall time per timed step (steps after `warmup`),
+ *                      host launch work included, device drained at both ends. */
+int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t steps, int64_t warmup,
+                  int64_t n_batches, const float* xs, const int64_t* ys, float lr, float mu, int32_t on_gpu,
+                  int32_t reference_compat, int32_t bf16, const float* init_weights, float* losses,
+                  float* final_weights, double* ms_per_step);
+
+/* CNN training (the config-4 network): Conv2dModule(3,32,3,1,1) - ReLU -
+ * Conv2dModule(32,64,3,2,1) - ReLU - flatten - Linear(64*(H/2)*(W/2), 10) -
+ * CrossEntropyLoss, optim::SGD.  xs [n_batches][batch][3][H][W]; init_params
+ * NULL or {conv1.w, conv1.b, conv2.w, conv2.b, fc.w, fc.b} concatenated. */
+int tfa_cnn_train(int64_t batch, int64_t H, int64_t W, int64_t steps, int64_t warmup, int64_t n_batches,
+                  const float* xs, const int64_t* ys, float lr, float mu, int32_t on_gpu, const float* init_params,
+                  float* losses, double* ms_per_step);
+
+/* Runs one of the C++ self-tests (`name`, see tfa_selftest_names) on the CPU
+ * (on_gpu = 0) or on GPU 0 (on_gpu = 1). */
+int tfa_selftest(const char* name, int32_t on_gpu);
+/* Space-separated list of self-test names. */
+const char* tfa_selftest_names(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TFA_HARNESS_H */

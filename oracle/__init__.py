@@ -15,6 +15,7 @@ Pinning of each function is listed in ``oracle/README.md``.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
@@ -333,6 +334,35 @@ def mlp_step(weights, vels, x, labels, lr, mu):
     return loss
 
 
+def cnn_step(params, vels, x, labels, lr, mu):
+    """One config-4 training step in reference order: Conv(3->32, s1 p1) +
+    ReLU, Conv(32->64, s2 p1) + ReLU, flatten, Linear(+bias), CE chain;
+    backward through the reference's conv loop (nn/conv2d_backward_test.cpp:
+    50-106), Linear backward and ReluBackward; momentum SGD on all six
+    parameters (updated in place).  params = [w1, b1, w2, b2, wf, bf]."""
+    w1, b1, w2, b2, wf, bfc = params
+    x = _f32(x)
+    B = x.shape[0]
+    z1 = conv2d_fwd(x, w1, b1, 1, 1)
+    h1 = relu(z1)
+    z2 = conv2d_fwd(h1, w2, b2, 2, 1)
+    h2 = relu(z2)
+    f = h2.reshape(B, -1)
+    logits = add(linear_fwd(f, wf), np.broadcast_to(bfc, (B, bfc.size)))
+    loss, g = ce_chain(logits, labels)
+    df, dwf = linear_bwd(f, wf, g)
+    dbf = colsum(g)
+    dz2 = relu_bwd(df.reshape(h2.shape), z2)
+    dh1, dw2, db2 = conv2d_bwd(h1, w2, dz2, (2, 2), (1, 1), (1, 1))
+    dz1 = relu_bwd(dh1, z1)
+    _, dw1, db1 = conv2d_bwd(x, w1, dz1, (1, 1), (1, 1), (1, 1))
+    for i, gr in enumerate((dw1, db1, dw2, db2, dwf, dbf)):
+        p, v = sgd_momentum(params[i], gr, vels[i], lr, mu)
+        params[i][...] = p
+        vels[i][...] = v
+    return loss
+
+
 # --------------------------------------------------------------------------
 # The compiled reference (optional)
 # --------------------------------------------------------------------------
@@ -349,7 +379,7 @@ def ref():
     if _ref is None:
         if not REF_SO.exists():
             raise FileNotFoundError(f"{REF_SO} not built (needs the reference tree)")
-        r = C.CDLL(str(REF_SO))
+        r = C.CDLL(str(REF_SO), mode=os.RTLD_NOW | os.RTLD_LOCAL)
         r.ref_last_error.restype = C.c_char_p
         for name in ("ref_matmul", "ref_transpose2d", "ref_matmul_backward", "ref_linear", "ref_linear_init",
                      "ref_conv2d_init", "ref_relu_fwd", "ref_sigmoid_fwd", "ref_tanh_fwd", "ref_relu_bwd",

@@ -260,7 +260,7 @@ int ref_conv2d_fwd(const float* x, const float* w, const float* b, float* y, int
 // nn/optim/SGD.cpp:50-54) since SGD::step throws for mu > 0.  Weights start
 // from the reference init.  xs: [steps][B][784], ys: [steps][B].
 int ref_mlp_train(const float* xs, const int64_t* ys, int64_t steps, int64_t B, float lr, float mu, float* losses,
-                  const int32_t* dims, int64_t ndims) {
+                  const int32_t* dims, int64_t ndims, float* final_weights) {
     return guarded([&] {
         std::vector<std::shared_ptr<nn::Linear>> layers;
         for (int64_t l = 0; l + 1 < ndims; ++l)
@@ -296,6 +296,13 @@ int ref_mlp_train(const float* xs, const int64_t* ys, int64_t steps, int64_t B, 
                     float step = vp[k] * lr;
                     pp[k] = pp[k] - step;
                 }
+            }
+        }
+        if (final_weights) {
+            size_t off = 0;
+            for (Tensor* p : params) {
+                copy_out(*p, final_weights + off);
+                off += static_cast<size_t>(p->numel());
             }
         }
     });

@@ -61,6 +61,10 @@ SIGNATURES: dict[str, list] = {
     "tf_im2col": [_p, _p, _p] + [_i64] * 12 + [_i],
     "tf_col2im": [_p, _p, _p] + [_i64] * 12 + [_i],
     "tf_add": [_p, _p, _p, _p, _i64, _i],
+    "tf_sub": [_p, _p, _p, _p, _i64, _i],
+    "tf_sum_dim": [_p, _p, _p, _i64, _i64, _i64],
+    "tf_expand_dim": [_p, _p, _p, _i64, _i64, _i64],
+    "tf_transpose2d": [_p, _p, _p, _i64, _i64, _i64, _i],
     "tf_mul": [_p, _p, _p, _p, _i64, _i],
     "tf_scale_by": [_p, _p, _p, _p, _i64, _i],
     "tf_relu_fwd": [_p, _p, _p, _i64, _i],

@@ -1,0 +1,89 @@
+"""ctypes binding of ``lib/libtensorforge.so``'s harness entry points
+(``include/tfa_harness.h``), which drive the C++20 tensorforge API —
+nn::Linear / Conv2dModule / CrossEntropyLoss, Tensor::backward through the
+Engine, optim::SGD — on CPU tensors or on GPU 0.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from ._lib import LIB_DIR, lib as _hip_lib  # noqa: F401  (libtf_hip must load first)
+
+TF_LIB_PATH = LIB_DIR / "libtensorforge.so"
+
+
+class HarnessError(RuntimeError):
+    pass
+
+
+def _load() -> C.CDLL:
+    if not TF_LIB_PATH.exists():
+        raise ImportError(f"{TF_LIB_PATH} is missing: run __graft_entry__.build()")
+    lib = C.CDLL(str(TF_LIB_PATH), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+    lib.tfa_last_error.restype = C.c_char_p
+    lib.tfa_selftest_names.restype = C.c_char_p
+    lib.tfa_selftest.argtypes = [C.c_char_p, C.c_int32]
+    lib.tfa_selftest.restype = C.c_int
+    p, i64, i32, f = C.c_void_p, C.c_int64, C.c_int32, C.c_float
+    lib.tfa_mlp_train.argtypes = [p, i32, i64, i64, i64, i64, p, p, f, f, i32, i32, i32, p, p, p, p]
+    lib.tfa_mlp_train.restype = C.c_int
+    lib.tfa_cnn_train.argtypes = [i64, i64, i64, i64, i64, i64, p, p, f, f, i32, p, p, p]
+    lib.tfa_cnn_train.restype = C.c_int
+    return lib
+
+
+lib = _load()
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise HarnessError(lib.tfa_last_error().decode(errors="replace"))
+
+
+def _ptr(a):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+def selftest_names() -> list[str]:
+    return lib.tfa_selftest_names().decode().split()
+
+
+def selftest(name: str, on_gpu: bool) -> None:
+    _check(lib.tfa_selftest(name.encode(), int(on_gpu)))
+
+
+def mlp_train(dims, xs, ys, *, steps, lr, mu, on_gpu, reference_compat=False, bf16=False, init_weights=None,
+              warmup=0, want_weights=False):
+    """Returns (losses[steps], final_weights or None, ms_per_step)."""
+    dims_a = np.ascontiguousarray(dims, dtype=np.int32)
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    ys = np.ascontiguousarray(ys, dtype=np.int64)
+    n_batches, batch = ys.shape
+    assert xs.shape == (n_batches, batch, dims_a[0])
+    losses = np.zeros(steps, np.float32)
+    nw = int(sum(int(dims_a[i]) * int(dims_a[i + 1]) for i in range(len(dims_a) - 1)))
+    fw = np.zeros(nw, np.float32) if want_weights else None
+    iw = None if init_weights is None else np.ascontiguousarray(init_weights, dtype=np.float32)
+    if iw is not None:
+        assert iw.size == nw
+    ms = C.c_double(0.0)
+    _check(lib.tfa_mlp_train(_ptr(dims_a), len(dims_a), batch, steps, warmup, n_batches, _ptr(xs), _ptr(ys), lr, mu,
+                             int(on_gpu), int(reference_compat), int(bf16), _ptr(iw), _ptr(losses), _ptr(fw),
+                             C.byref(ms)))
+    return losses, fw, ms.value
+
+
+def cnn_train(xs, ys, *, steps, lr, mu, on_gpu, init_params=None, warmup=0):
+    """xs [n_batches, B, 3, H, W]; returns (losses, ms_per_step)."""
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    ys = np.ascontiguousarray(ys, dtype=np.int64)
+    n_batches, batch, _, H, W = xs.shape
+    losses = np.zeros(steps, np.float32)
+    ip = None if init_params is None else np.ascontiguousarray(init_params, dtype=np.float32)
+    ms = C.c_double(0.0)
+    _check(lib.tfa_cnn_train(batch, H, W, steps, warmup, n_batches, _ptr(xs), _ptr(ys), lr, mu, int(on_gpu), _ptr(ip),
+                             _ptr(losses), C.byref(ms)))
+    return losses, ms.value

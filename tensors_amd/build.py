@@ -78,7 +78,8 @@ def build_cpp(jobs: int = 8) -> Path | None:
             f.result()
     out = LIB / "libtensorforge.so"
     tmp = LIB / "libtensorforge.so.tmp"
-    _run([CXX, "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
+    # -Bsymbolic: internal calls bind to this library's own definitions.
+    _run([CXX, "-shared", "-fPIC", "-Wl,-Bsymbolic", "-o", str(tmp), *map(str, objs),
           f"-L{LIB}", "-ltf_hip", "-Wl,-rpath,$ORIGIN"])
     os.replace(tmp, out)
     return out

@@ -1,0 +1,38 @@
+// Conv2d backward (reference nn/Conv2d.cpp:140-260, without its per-sample
+// launches and host accumulation):
+//   dW = sum_n dY[n] col[n]^T     one batch-reduced MFMA GEMM
+//   dcol[n] = W^T dY[n]           one batched GEMM, then dX = col2im(dcol)
+//   db = sum_{n,h,w} dY           deterministic channel reduction
+// col = im2col(x) is saved from the forward.  Outputs follow
+// next_edges_ = {x, W, b}; an empty edge skips that gradient (e.g. dX of the
+// network input).
+#pragma once
+
+#include "autograd/Node.hpp"
+#include "autograd/SavedTensor.hpp"
+#include "tensor/Tensor.hpp"
+
+#include <cstdint>
+
+namespace tensorforge {
+
+struct ConvGeometry {
+    int64_t N, Cin, H, W, Cout, kH, kW, sh, sw, ph, pw, dh, dw, outH, outW;
+};
+
+class Conv2dBackward : public Node {
+public:
+    // GPU: `x_or_col` is the im2col matrix [N, Cin*kH*kW, outH*outW];
+    // CPU: the input itself.
+    Conv2dBackward(const Tensor& x_or_col, const Tensor& weight, bool has_bias, ConvGeometry g)
+        : saved_(x_or_col), w_(weight), has_bias_(has_bias), g_(g) {}
+    std::vector<Tensor> apply(std::vector<Tensor>&& grads) override;
+    void release_saved() override { saved_.reset(); w_.reset(); }
+
+private:
+    SavedTensor saved_, w_;
+    bool has_bias_;
+    ConvGeometry g_;
+};
+
+}  // namespace tensorforge

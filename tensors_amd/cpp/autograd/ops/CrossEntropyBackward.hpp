@@ -1,0 +1,26 @@
+// loss = mean_r (logsumexp(logits_r) - logits_r[t_r]):
+//   dlogits = g * (softmax(logits) - onehot(t)) / N
+// One node in place of the train_mlp chain's LogSoftmax + Mul + 2 x Sum +
+// 2 x scalar Mul backward nodes (examples/train_mlp.cpp:54-76); on the GPU a
+// single streaming kernel using the saved row log-sum-exp.
+#pragma once
+
+#include "autograd/Node.hpp"
+#include "autograd/SavedTensor.hpp"
+#include "tensor/Tensor.hpp"
+
+namespace tensorforge {
+
+class CrossEntropyBackward : public Node {
+public:
+    // lse: saved row log-sum-exp (GPU) or softmax probabilities (CPU).
+    CrossEntropyBackward(const Tensor& logits, const Tensor& targets, const Tensor& row_stats)
+        : logits_(logits), targets_(targets), stats_(row_stats) {}
+    std::vector<Tensor> apply(std::vector<Tensor>&& grads) override;
+    void release_saved() override { logits_.reset(); targets_.reset(); stats_.reset(); }
+
+private:
+    SavedTensor logits_, targets_, stats_;
+};
+
+}  // namespace tensorforge

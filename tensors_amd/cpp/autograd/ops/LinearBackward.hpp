@@ -1,0 +1,30 @@
+// y = x W^T (+ b), one node for nn::Linear: dX = dY W, dW = dY^T X,
+// db = sum_rows dY.  The reference reaches the same dW through
+// MatmulBackward + TransposeBackward with two transpose copies
+// (nn/Linear.cpp:61-63, autograd/ops/TransposeBackward.hpp:26-28); here
+// each gradient is one GEMM written directly in W's layout.  Outputs follow
+// next_edges_ = {x, W, b}; an empty edge skips that gradient.
+#pragma once
+
+#include "autograd/Node.hpp"
+#include "autograd/SavedTensor.hpp"
+#include "tensor/Tensor.hpp"
+
+namespace tensorforge {
+
+class LinearBackward : public Node {
+public:
+    // `weight` is the tensor the forward multiplied with (the bf16 shadow in
+    // mixed precision); dW is produced in `grad_dtype` on its device.
+    LinearBackward(const Tensor& x, const Tensor& weight, bool has_bias, Dtype grad_dtype)
+        : x_(x), w_(weight), has_bias_(has_bias), grad_dtype_(grad_dtype) {}
+    std::vector<Tensor> apply(std::vector<Tensor>&& grads) override;
+    void release_saved() override { x_.reset(); w_.reset(); }
+
+private:
+    SavedTensor x_, w_;
+    bool has_bias_;
+    Dtype grad_dtype_;
+};
+
+}  // namespace tensorforge

@@ -1,0 +1,633 @@
+// C entry points that drive the C++ API end to end (include/tfa_harness.h):
+// training loops shaped like the reference's examples and self-tests that
+// restate the reference's own unit tests (each cites the test it restates).
+// Every self-test runs on CPU tensors or on GPU 0.
+#include "tfa_harness.h"
+
+#include "autograd/AccumulateGrad.hpp"
+#include "autograd/AutogradMeta.hpp"
+#include "autograd/Engine.hpp"
+#include "autograd/ops/AddBackward.hpp"
+#include "hip/HipBackend.hpp"
+#include "nn/Activations.hpp"
+#include "nn/Conv2d.hpp"
+#include "nn/Conv2dModule.hpp"
+#include "nn/CrossEntropyLoss.hpp"
+#include "nn/Linear.hpp"
+#include "nn/optim/SGD.hpp"
+#include "tensor/AutogradWirer.hpp"
+#include "tensor/Compat.hpp"
+#include "tensor/factory.hpp"
+#include "tensor/shape_ops.hpp"
+
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+using namespace tensorforge;
+
+namespace {
+
+thread_local std::string g_err;
+
+template <typename F>
+int guarded(F&& f) {
+    try {
+        init_tensor_autograd();
+        f();
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 1;
+    } catch (...) {
+        g_err = "unknown exception";
+        return 1;
+    }
+}
+
+// Restores the reference-compat switches when a harness call returns.
+struct CompatScope {
+    bool bias, ln;
+    explicit CompatScope(bool on) : bias(compat::linear_drops_bias()), ln(compat::layernorm_stub_backward()) {
+        compat::set_reference_compat(on);
+    }
+    ~CompatScope() {
+        compat::set_linear_drops_bias(bias);
+        compat::set_layernorm_stub_backward(ln);
+    }
+};
+
+Device dev_of(int on_gpu) { return on_gpu ? Device::cuda(0) : Device::cpu(); }
+
+Tensor host_f32(const float* src, Shape s) {
+    Tensor t = Tensor::empty(std::move(s), Dtype::Float32, Device::cpu());
+    if (src) std::memcpy(t.data(), src, sizeof(float) * static_cast<size_t>(t.numel()));
+    return t;
+}
+
+Tensor host_i64(const int64_t* src, Shape s) {
+    Tensor t = Tensor::empty(std::move(s), Dtype::Int64, Device::cpu());
+    std::memcpy(t.data(), src, sizeof(int64_t) * static_cast<size_t>(t.numel()));
+    return t;
+}
+
+std::vector<float> to_host(const Tensor& t) {
+    Tensor h = t.device().type == DeviceType::CPU ? t : t.to(Device::cpu());
+    if (h.dtype() != Dtype::Float32) h = h.to(Dtype::Float32);
+    const float* p = static_cast<const float*>(h.data());
+    return std::vector<float>(p, p + h.numel());
+}
+
+void sync_if_gpu(int on_gpu) {
+    if (on_gpu) hip::synchronize(0);
+}
+
+// ---------------------------------------------------------------------------
+// self-tests
+// ---------------------------------------------------------------------------
+#define TFA_CHECK(cond)                                                                          \
+    do {                                                                                         \
+        if (!(cond)) throw std::runtime_error(std::string("check failed: ") + #cond);            \
+    } while (0)
+
+void check_near(float got, float want, float tol, const std::string& what) {
+    if (!(std::fabs(got - want) <= tol * std::max(1.0f, std::fabs(want)))) {
+        std::ostringstream os;
+        os << what << ": got " << got << " want " << want;
+        throw std::runtime_error(os.str());
+    }
+}
+
+void check_all(const Tensor& t, float want, const std::string& what, float tol = 1e-6f) {
+    auto v = to_host(t);
+    TFA_CHECK(!v.empty());
+    for (size_t i = 0; i < v.size(); ++i) check_near(v[i], want, tol, what + "[" + std::to_string(i) + "]");
+}
+
+void check_vec(const Tensor& t, const std::vector<float>& want, const std::string& what, float tol = 1e-5f) {
+    auto v = to_host(t);
+    if (v.size() != want.size()) throw std::runtime_error(what + ": size mismatch");
+    for (size_t i = 0; i < v.size(); ++i) check_near(v[i], want[i], tol, what + "[" + std::to_string(i) + "]");
+}
+
+Tensor filled(Shape s, float v, Device d) { return full(std::move(s), v, Dtype::Float32, d); }
+
+Tensor from_vals(const std::vector<float>& v, Shape s, Device d) { return host_f32(v.data(), std::move(s)).to(d); }
+
+// autograd/engine_test.cpp:65-100 — a.grad == 2 through fan-in of a hand-built graph.
+void t_engine_fan_in(Device d) {
+    Tensor a = filled({2, 3}, 1.0f, d), b = filled({2, 3}, 1.0f, d), c = filled({2, 3}, 1.0f, d);
+    a.requires_grad(true);
+    b.requires_grad(true);
+    c.requires_grad(true);
+    auto e = std::make_shared<AddBackward>();
+    e->next_edges_ = {Edge(a.autograd_meta()->grad_accumulator_, 0), Edge(b.autograd_meta()->grad_accumulator_, 0)};
+    auto f = std::make_shared<AddBackward>();
+    f->next_edges_ = {Edge(a.autograd_meta()->grad_accumulator_, 0), Edge(c.autograd_meta()->grad_accumulator_, 0)};
+    auto loss = std::make_shared<AddBackward>();
+    loss->next_edges_ = {Edge(e, 0), Edge(f, 0)};
+    Engine().execute(loss, filled({2, 3}, 1.0f, d), false);
+    check_all(a.grad(), 2.0f, "a.grad");
+    check_all(b.grad(), 1.0f, "b.grad");
+    check_all(c.grad(), 1.0f, "c.grad");
+}
+
+// autograd/engine_test.cpp:126-152 — a deep chain of adds reaches the leaf.
+void t_engine_deep_chain(Device d) {
+    Tensor a = filled({4}, 1.0f, d);
+    a.requires_grad(true);
+    Tensor z = filled({4}, 0.0f, d);
+    Tensor h = a;
+    for (int i = 0; i < 64; ++i) h = h + z;
+    h.backward();
+    check_all(a.grad(), 1.0f, "a.grad");
+}
+
+// tests/autograd/chain_autograd_test.cpp:25-54 — d = (a+b)*a, e = d.sum(0).
+void t_chain_add_mul_sum(Device d) {
+    Tensor a = filled({2, 3}, 2.0f, d), b = filled({2, 3}, 3.0f, d);
+    a.requires_grad(true);
+    b.requires_grad(true);
+    Tensor c = a + b;
+    Tensor dd = c * a;
+    Tensor e = dd.sum(0);
+    TFA_CHECK(e.requires_grad() && e.autograd_meta()->grad_fn_ != nullptr);
+    e.backward();
+    check_all(a.grad(), 7.0f, "a.grad");
+    check_all(b.grad(), 2.0f, "b.grad");
+}
+
+// tests/autograd/chain_autograd_test.cpp:56-68 — transpose reaches the leaf.
+void t_transpose_grad(Device d) {
+    Tensor W = filled({3, 4}, 0.5f, d);
+    W.requires_grad(true);
+    Tensor Wt = W.transpose(0, 1);
+    TFA_CHECK(Wt.shape() == (Shape{4, 3}));
+    Tensor s = Wt.sum(0).sum(0);
+    s.backward();
+    check_all(W.grad(), 1.0f, "W.grad");
+    TFA_CHECK(W.grad().shape() == (Shape{3, 4}));
+}
+
+// autograd/ops/autograd_all_ops_test.cpp:281-328 — matmul arange known answers.
+void t_matmul_known_answer(Device d) {
+    Tensor a = from_vals({0, 1, 2, 3, 4, 5}, {2, 3}, d);
+    Tensor b = from_vals({0, 1, 2, 3, 4, 5}, {3, 2}, d);
+    a.requires_grad(true);
+    b.requires_grad(true);
+    Tensor c = a.matmul(b);
+    check_vec(c, {10, 13, 28, 40}, "C");
+    c.backward();
+    check_vec(a.grad(), {1, 5, 9, 1, 5, 9}, "dA");
+    check_vec(b.grad(), {3, 3, 5, 5, 7, 7}, "dB");
+}
+
+// autograd/ops/autograd_all_ops_test.cpp:253-268 — ones @ ones, grads 2.
+void t_matmul_ones(Device d) {
+    Tensor a = filled({2, 2}, 1.0f, d), b = filled({2, 2}, 1.0f, d);
+    a.requires_grad(true);
+    b.requires_grad(true);
+    a.matmul(b).backward();
+    check_all(a.grad(), 2.0f, "dA");
+    check_all(b.grad(), 2.0f, "dB");
+}
+
+// autograd/ops/autograd_all_ops_test.cpp:73-94 — relu mask, x == 0 -> 0.
+void t_relu_mask(Device d) {
+    Tensor x = from_vals({-2, -0.5f, 0, 0.5f, 2, 3}, {6}, d);
+    x.requires_grad(true);
+    Tensor y = x.relu();
+    check_vec(y, {0, 0, 0, 0.5f, 2, 3}, "relu");
+    y.backward();
+    check_vec(x.grad(), {0, 0, 0, 1, 1, 1}, "relu grad");
+}
+
+// autograd/ops/autograd_all_ops_test.cpp:108-121 — uniform softmax, grad 0.
+void t_softmax_uniform(Device d) {
+    Tensor x = filled({2, 4}, 0.3f, d);
+    x.requires_grad(true);
+    Tensor y = x.softmax(-1);
+    check_all(y, 0.25f, "softmax");
+    y.backward();
+    check_all(x.grad(), 0.0f, "softmax grad", 1e-6f);
+}
+
+// autograd/ops/autograd_all_ops_test.cpp:164-177 — log_softmax closed form.
+void t_log_softmax_closed_form(Device d) {
+    Tensor x = from_vals({1, 2, 3}, {1, 3}, d);
+    Tensor y = x.log_softmax(-1);
+    const double lz = std::log(std::exp(1.0) + std::exp(2.0) + std::exp(3.0));
+    check_vec(y, {float(1 - lz), float(2 - lz), float(3 - lz)}, "log_softmax");
+}
+
+// autograd/ops/autograd_add_mul_test.cpp:122-143 — c = a * b arange grads.
+void t_mul_arange(Device d) {
+    Tensor a = from_vals({0, 1, 2, 3}, {4}, d), b = from_vals({4, 5, 6, 7}, {4}, d);
+    a.requires_grad(true);
+    b.requires_grad(true);
+    (a * b).backward();
+    check_vec(a.grad(), {4, 5, 6, 7}, "da");
+    check_vec(b.grad(), {0, 1, 2, 3}, "db");
+}
+
+// autograd/ops/autograd_add_mul_test.cpp:145-162 — mutating a saved input throws.
+void t_saved_tensor_version(Device d) {
+    Tensor a = filled({3}, 2.0f, d), b = filled({3}, 3.0f, d);
+    a.requires_grad(true);
+    b.requires_grad(true);
+    Tensor c = a * b;
+    (void)b.bump_version();
+    bool threw = false;
+    try {
+        c.backward();
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    TFA_CHECK(threw);
+}
+
+// nn/cross_entropy_test.cpp:10-49 — CE known answers 0.4076 and 1.0986.
+void t_cross_entropy_known(Device d) {
+    nn::CrossEntropyLoss ce;
+    Tensor logits = from_vals({1, 2, 3}, {1, 3}, d);
+    int64_t t2 = 2;
+    Tensor tg = host_i64(&t2, {1}).to(d);
+    check_near(to_host(ce.forward(logits, tg))[0], 0.4076f, 1e-3f, "single");
+    Tensor l2 = filled({2, 3}, 1.0f, d);
+    int64_t tt[2] = {0, 2};
+    check_near(to_host(ce.forward(l2, host_i64(tt, {2}).to(d)))[0], 1.0986f, 1e-3f, "batch");
+}
+
+// CE gradient = (softmax - onehot) / N (no reference test covers it).
+void t_cross_entropy_grad(Device d) {
+    nn::CrossEntropyLoss ce;
+    Tensor logits = from_vals({1, 2, 3, 0, 0, 0}, {2, 3}, d);
+    logits.requires_grad(true);
+    int64_t tt[2] = {2, 0};
+    ce.forward(logits, host_i64(tt, {2}).to(d)).backward();
+    const double z = std::exp(1.0) + std::exp(2.0) + std::exp(3.0);
+    std::vector<float> want = {float(std::exp(1.0) / z / 2), float(std::exp(2.0) / z / 2),
+                               float((std::exp(3.0) / z - 1) / 2), float((1.0 / 3 - 1) / 2), float(1.0 / 6),
+                               float(1.0 / 6)};
+    check_vec(logits.grad(), want, "dlogits", 1e-5f);
+}
+
+// Sigmoid / tanh backward (wired here; the reference leaves them unwired).
+void t_sigmoid_tanh_grad(Device d) {
+    Tensor x = from_vals({-1.5f, 0.0f, 0.7f}, {3}, d);
+    x.requires_grad(true);
+    x.sigmoid().backward();
+    std::vector<float> ws, wt;
+    for (float v : {-1.5f, 0.0f, 0.7f}) {
+        double s = 1.0 / (1.0 + std::exp(-double(v)));
+        ws.push_back(float(s * (1 - s)));
+        double t = std::tanh(double(v));
+        wt.push_back(float(1 - t * t));
+    }
+    check_vec(x.grad(), ws, "sigmoid'");
+    Tensor x2 = from_vals({-1.5f, 0.0f, 0.7f}, {3}, d);
+    x2.requires_grad(true);
+    x2.tanh().backward();
+    check_vec(x2.grad(), wt, "tanh'");
+}
+
+// LayerNorm: true gradient of sum(y * w) vs double-precision finite differences;
+// stub mode reproduces dx = dy * gamma.
+void t_layernorm_grad(Device d) {
+    const int R = 3, C = 5;
+    std::vector<float> xv = {0.3f, -1.2f, 0.8f, 2.0f, -0.4f, 1.1f, 0.0f, -0.7f, 0.5f, 0.9f,
+                             -2.0f, 0.25f, 1.5f, -0.1f, 0.6f};
+    std::vector<float> gv = {1.0f, 0.5f, 2.0f, -1.0f, 1.5f};
+    std::vector<float> bv = {0.1f, 0.0f, -0.2f, 0.3f, 0.0f};
+    auto loss_at = [&](const std::vector<float>& xs) {
+        double tot = 0.0;
+        for (int r = 0; r < R; ++r) {
+            double m = 0, v = 0;
+            for (int j = 0; j < C; ++j) m += xs[r * C + j];
+            m /= C;
+            for (int j = 0; j < C; ++j) v += (xs[r * C + j] - m) * (xs[r * C + j] - m);
+            v /= C;
+            const double rs = 1.0 / std::sqrt(v + 1e-5);
+            for (int j = 0; j < C; ++j) tot += ((xs[r * C + j] - m) * rs * gv[j] + bv[j]) * (j + 1);
+        }
+        return tot;
+    };
+    Tensor x = from_vals(xv, {R, C}, d), g = from_vals(gv, {C}, d), b = from_vals(bv, {C}, d);
+    x.requires_grad(true);
+    g.requires_grad(true);
+    b.requires_grad(true);
+    Tensor y = x.layer_norm(g, b, 1e-5f);
+    std::vector<float> wv;
+    for (int r = 0; r < R; ++r)
+        for (int j = 0; j < C; ++j) wv.push_back(float(j + 1));
+    Tensor w = from_vals(wv, {R, C}, d);
+    Engine().execute(y.autograd_meta()->grad_fn_, w, false);
+    std::vector<float> want;
+    for (int i = 0; i < R * C; ++i) {
+        auto xp = xv, xm = xv;
+        const double h = 1e-3;
+        xp[i] += float(h);
+        xm[i] -= float(h);
+        want.push_back(float((loss_at(xp) - loss_at(xm)) / (2 * h)));
+    }
+    check_vec(x.grad(), want, "ln dx", 5e-3f);
+    std::vector<float> wb(C, 0.0f);
+    for (int j = 0; j < C; ++j) wb[j] = float(R * (j + 1));
+    check_vec(b.grad(), wb, "ln dbeta", 1e-5f);
+
+    compat::set_layernorm_stub_backward(true);
+    Tensor x2 = from_vals(xv, {R, C}, d);
+    x2.requires_grad(true);
+    Tensor y2 = x2.layer_norm(g, b, 1e-5f);
+    Engine().execute(y2.autograd_meta()->grad_fn_, w, false);
+    compat::set_layernorm_stub_backward(false);
+    std::vector<float> stub;
+    for (int r = 0; r < R; ++r)
+        for (int j = 0; j < C; ++j) stub.push_back(float(j + 1) * gv[j]);
+    check_vec(x2.grad(), stub, "stub dx", 0.0f);
+}
+
+// nn/conv2d_backward_test.cpp:110-160 — 1x1 kernel golden gradients
+// (weight 2, grad_out 0.1..0.4: dX = 0.2..0.8, dW = 3.0), through
+// Conv2dModule's autograd node on either device.
+void t_conv_1x1_golden(Device d) {
+    Tensor x = from_vals({1, 2, 3, 4}, {1, 1, 2, 2}, d);
+    x.requires_grad(true);
+    nn::Conv2dModule conv(1, 1, 1);
+    conv.to(d);
+    for (auto& np : conv.named_parameters()) {
+        if (np.first == "weight") np.second->data_ = from_vals({2.0f}, {1, 1, 1, 1}, d);
+        np.second->data_.requires_grad(true);
+    }
+    Tensor y = conv.forward(x);
+    check_vec(y, {2, 4, 6, 8}, "y");
+    Tensor up = from_vals({0.1f, 0.2f, 0.3f, 0.4f}, {1, 1, 2, 2}, d);
+    Engine().execute(y.autograd_meta()->grad_fn_, up, false);
+    check_vec(x.grad(), {0.2f, 0.4f, 0.6f, 0.8f}, "dX");
+    for (auto& np : conv.named_parameters()) {
+        if (np.first == "weight") check_vec(np.second->data_.grad(), {3.0f}, "dW");
+        if (np.first == "bias") check_vec(np.second->data_.grad(), {1.0f}, "db");
+    }
+}
+
+// The same golden case through nn::Conv2d's explicit backward (GPU module,
+// bias disabled -> zero bias gradient).
+void t_conv2d_module_explicit_backward(Device d) {
+    if (d.type != DeviceType::CUDA) return;  // nn::Conv2d lives on the GPU, as in the reference
+    nn::Conv2d conv(1, 1, 1, 1, 1, 1, 0, 0, 1, 1, false);
+    conv.weight().data_ = from_vals({2.0f}, {1, 1, 1, 1}, d);
+    Tensor x = from_vals({1, 2, 3, 4}, {1, 1, 2, 2}, d);
+    Tensor go = from_vals({0.1f, 0.2f, 0.3f, 0.4f}, {1, 1, 2, 2}, d);
+    nn::Conv2dGrad g = conv.backward(go, x);
+    check_vec(g.grad_input, {0.2f, 0.4f, 0.6f, 0.8f}, "dX");
+    check_vec(g.grad_weight, {3.0f}, "dW");
+    check_vec(g.grad_bias, {0.0f}, "db");
+}
+
+// Linear: y = x W^T + b, dX = dY W, dW = dY^T X, db = colsum dY.
+void t_linear_grads(Device d) {
+    nn::Linear fc(3, 2);
+    fc.to(d);
+    Tensor W = from_vals({1, 2, 3, 4, 5, 6}, {2, 3}, d);
+    Tensor b = from_vals({0.5f, -1.0f}, {2}, d);
+    for (auto& np : fc.named_parameters()) {
+        np.second->data_ = np.first == "weight" ? W : b;
+        np.second->data_.requires_grad(true);
+    }
+    Tensor x = from_vals({1, 0, -1, 2, 1, 0}, {2, 3}, d);
+    x.requires_grad(true);
+    Tensor y = fc.forward(x);
+    check_vec(y, {-1.5f, -3.0f, 4.5f, 12.0f}, "y");
+    Tensor up = from_vals({1, 2, 3, 4}, {2, 2}, d);
+    Engine().execute(y.autograd_meta()->grad_fn_, up, false);
+    check_vec(x.grad(), {9, 12, 15, 19, 26, 33}, "dX");
+    for (auto& np : fc.named_parameters()) {
+        if (np.first == "weight") check_vec(np.second->data_.grad(), {7, 3, -1, 10, 4, -2}, "dW");
+        if (np.first == "bias") check_vec(np.second->data_.grad(), {4, 6}, "db");
+    }
+}
+
+// optim::SGD momentum rule v = mu v + g; p = p - lr v (nn/optim/SGD.hpp:3-6).
+void t_sgd_momentum_rule(Device d) {
+    Tensor p = from_vals({1.0f, -2.0f}, {2}, d);
+    p.requires_grad(true);
+    nn::optim::SGD opt({&p}, 0.5f, 0.9f);
+    for (int s = 0; s < 2; ++s) {
+        Tensor g = from_vals({0.2f, 0.4f}, {2}, d);
+        p.autograd_meta()->grad_ = g;
+        opt.step();
+    }
+    // v1 = g, p1 = p0 - 0.5 g; v2 = 0.9 g + g = 1.9 g; p2 = p1 - 0.95 g.
+    check_vec(p, {1.0f - 0.5f * 0.2f - 0.95f * 0.2f, -2.0f - 0.5f * 0.4f - 0.95f * 0.4f}, "p", 1e-6f);
+}
+
+// Reshape is wired: a flatten feeding a Linear reaches the conv output.
+void t_reshape_grad(Device d) {
+    Tensor x = filled({2, 3, 2}, 1.0f, d);
+    x.requires_grad(true);
+    Tensor f = reshape(x, Shape{2, 6});
+    f.sum(1).sum(0).backward();
+    check_all(x.grad(), 1.0f, "dx");
+    TFA_CHECK(x.grad().shape() == (Shape{2, 3, 2}));
+}
+
+// Sum over a non-final dim with a non-uniform upstream: true broadcast.
+void t_sum_broadcast(Device d) {
+    Tensor x = filled({2, 3}, 1.0f, d);
+    x.requires_grad(true);
+    Tensor s = x.sum(1);  // [2]
+    Engine().execute(s.autograd_meta()->grad_fn_, from_vals({1.0f, 5.0f}, {2}, d), false);
+    check_vec(x.grad(), {1, 1, 1, 5, 5, 5}, "dx");
+}
+
+const std::map<std::string, std::function<void(Device)>>& registry() {
+    static const std::map<std::string, std::function<void(Device)>> r = {
+        {"engine_fan_in", t_engine_fan_in},
+        {"engine_deep_chain", t_engine_deep_chain},
+        {"chain_add_mul_sum", t_chain_add_mul_sum},
+        {"transpose_grad", t_transpose_grad},
+        {"matmul_known_answer", t_matmul_known_answer},
+        {"matmul_ones", t_matmul_ones},
+        {"relu_mask", t_relu_mask},
+        {"softmax_uniform", t_softmax_uniform},
+        {"log_softmax_closed_form", t_log_softmax_closed_form},
+        {"mul_arange", t_mul_arange},
+        {"saved_tensor_version", t_saved_tensor_version},
+        {"cross_entropy_known", t_cross_entropy_known},
+        {"cross_entropy_grad", t_cross_entropy_grad},
+        {"sigmoid_tanh_grad", t_sigmoid_tanh_grad},
+        {"layernorm_grad", t_layernorm_grad},
+        {"conv_1x1_golden", t_conv_1x1_golden},
+        {"conv2d_explicit_backward", t_conv2d_module_explicit_backward},
+        {"linear_grads", t_linear_grads},
+        {"sgd_momentum_rule", t_sgd_momentum_rule},
+        {"reshape_grad", t_reshape_grad},
+        {"sum_broadcast", t_sum_broadcast},
+    };
+    return r;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* tfa_last_error(void) { return g_err.c_str(); }
+
+const char* tfa_selftest_names(void) {
+    static std::string names;
+    if (names.empty())
+        for (const auto& kv : registry()) names += (names.empty() ? "" : " ") + kv.first;
+    return names.c_str();
+}
+
+int tfa_selftest(const char* name, int32_t on_gpu) {
+    return guarded([&] {
+        auto it = registry().find(name ? name : "");
+        if (it == registry().end()) throw std::invalid_argument(std::string("unknown self-test ") + (name ? name : ""));
+        CompatScope scope(false);
+        it->second(dev_of(on_gpu));
+        sync_if_gpu(on_gpu);
+    });
+}
+
+int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t steps, int64_t warmup, int64_t n_batches,
+                  const float* xs, const int64_t* ys, float lr, float mu, int32_t on_gpu, int32_t reference_compat,
+                  int32_t bf16, const float* init_weights, float* losses, float* final_weights, double* ms_per_step) {
+    return guarded([&] {
+        if (ndims < 2 || batch <= 0 || steps < 0 || n_batches <= 0 || warmup < 0 || warmup > steps)
+            throw std::invalid_argument("tfa_mlp_train: bad sizes");
+        if (bf16 && !on_gpu) throw std::invalid_argument("tfa_mlp_train: bf16 needs the GPU");
+        CompatScope scope(reference_compat != 0);
+        const Device d = dev_of(on_gpu);
+        std::vector<std::shared_ptr<nn::Linear>> layers;
+        size_t off = 0;
+        for (int32_t l = 0; l + 1 < ndims; ++l) {
+            auto fc = std::make_shared<nn::Linear>(dims[l], dims[l + 1]);
+            if (init_weights) {
+                for (auto& np : fc->named_parameters())
+                    if (np.first == "weight")
+                        std::memcpy(np.second->data_.data(), init_weights + off, sizeof(float) * np.second->data_.numel());
+            }
+            off += static_cast<size_t>(dims[l]) * dims[l + 1];
+            fc->to(d);
+            if (bf16) fc->set_compute_dtype(Dtype::BFloat16);
+            layers.push_back(fc);
+        }
+        std::vector<Tensor*> params;
+        for (auto& fc : layers)
+            for (auto* p : fc->parameters()) params.push_back(&p->data_);
+        nn::optim::SGD opt(params, lr, mu);
+        nn::ReLU relu;
+        nn::CrossEntropyLoss ce;
+
+        std::vector<Tensor> xb, yb;
+        for (int64_t i = 0; i < n_batches; ++i) {
+            xb.push_back(host_f32(xs + i * batch * dims[0], Shape{batch, dims[0]}).to(d));
+            yb.push_back(host_i64(ys + i * batch, Shape{batch}).to(d));
+        }
+        std::vector<Tensor> loss_t;
+        loss_t.reserve(static_cast<size_t>(steps));
+        auto run_step = [&](int64_t s) {
+            Tensor h = xb[s % n_batches];
+            for (size_t l = 0; l < layers.size(); ++l) {
+                h = layers[l]->forward(h);
+                if (l + 1 < layers.size()) h = relu.forward(h);
+            }
+            Tensor loss = ce.forward(h, yb[s % n_batches]);
+            loss.backward();
+            opt.step();
+            loss_t.push_back(loss);
+        };
+        for (int64_t s = 0; s < warmup; ++s) run_step(s);
+        sync_if_gpu(on_gpu);
+        auto t0 = std::chrono::steady_clock::now();
+        for (int64_t s = warmup; s < steps; ++s) run_step(s);
+        sync_if_gpu(on_gpu);
+        auto t1 = std::chrono::steady_clock::now();
+        if (ms_per_step)
+            *ms_per_step = steps > warmup ? std::chrono::duration<double, std::milli>(t1 - t0).count() / double(steps - warmup) : 0.0;
+        if (losses)
+            for (int64_t s = 0; s < steps; ++s) losses[s] = to_host(loss_t[static_cast<size_t>(s)])[0];
+        if (final_weights) {
+            size_t o = 0;
+            for (auto& fc : layers)
+                for (auto& np : fc->named_parameters())
+                    if (np.first == "weight") {
+                        auto v = to_host(np.second->data_);
+                        std::memcpy(final_weights + o, v.data(), sizeof(float) * v.size());
+                        o += v.size();
+                    }
+        }
+    });
+}
+
+int tfa_cnn_train(int64_t batch, int64_t H, int64_t W, int64_t steps, int64_t warmup, int64_t n_batches, const float* xs,
+                  const int64_t* ys, float lr, float mu, int32_t on_gpu, const float* init_params, float* losses,
+                  double* ms_per_step) {
+    return guarded([&] {
+        if (batch <= 0 || steps < 0 || n_batches <= 0 || warmup < 0 || warmup > steps || H % 2 || W % 2)
+            throw std::invalid_argument("tfa_cnn_train: bad sizes");
+        CompatScope scope(false);
+        const Device d = dev_of(on_gpu);
+        nn::Conv2dModule conv1(3, 32, 3, 1, 1), conv2(32, 64, 3, 2, 1);
+        const int64_t flat = 64 * (H / 2) * (W / 2);
+        nn::Linear fc(static_cast<int>(flat), 10);
+        if (init_params) {
+            size_t off = 0;
+            auto load = [&](nn::Module& m, const char* name, int64_t n) {
+                for (auto& np : m.named_parameters())
+                    if (np.first == name) std::memcpy(np.second->data_.data(), init_params + off, sizeof(float) * n);
+                off += static_cast<size_t>(n);
+            };
+            load(conv1, "weight", 32 * 3 * 9);
+            load(conv1, "bias", 32);
+            load(conv2, "weight", 64 * 32 * 9);
+            load(conv2, "bias", 64);
+            load(fc, "weight", 10 * flat);
+            load(fc, "bias", 10);
+        }
+        conv1.to(d);
+        conv2.to(d);
+        fc.to(d);
+        std::vector<Tensor*> params;
+        for (nn::Module* m : std::initializer_list<nn::Module*>{&conv1, &conv2, &fc})
+            for (auto* p : m->parameters()) params.push_back(&p->data_);
+        nn::optim::SGD opt(params, lr, mu);
+        nn::ReLU relu;
+        nn::CrossEntropyLoss ce;
+        std::vector<Tensor> xb, yb;
+        for (int64_t i = 0; i < n_batches; ++i) {
+            xb.push_back(host_f32(xs + i * batch * 3 * H * W, Shape{batch, 3, H, W}).to(d));
+            yb.push_back(host_i64(ys + i * batch, Shape{batch}).to(d));
+        }
+        std::vector<Tensor> loss_t;
+        auto run_step = [&](int64_t s) {
+            Tensor h = relu.forward(conv1.forward(xb[s % n_batches]));
+            h = relu.forward(conv2.forward(h));
+            h = reshape(h, Shape{batch, flat});
+            Tensor loss = ce.forward(fc.forward(h), yb[s % n_batches]);
+            loss.backward();
+            opt.step();
+            loss_t.push_back(loss);
+        };
+        for (int64_t s = 0; s < warmup; ++s) run_step(s);
+        sync_if_gpu(on_gpu);
+        auto t0 = std::chrono::steady_clock::now();
+        for (int64_t s = warmup; s < steps; ++s) run_step(s);
+        sync_if_gpu(on_gpu);
+        auto t1 = std::chrono::steady_clock::now();
+        if (ms_per_step)
+            *ms_per_step = steps > warmup ? std::chrono::duration<double, std::milli>(t1 - t0).count() / double(steps - warmup) : 0.0;
+        if (losses)
+            for (int64_t s = 0; s < steps; ++s) losses[s] = to_host(loss_t[static_cast<size_t>(s)])[0];
+    });
+}
+
+}  // extern "C"

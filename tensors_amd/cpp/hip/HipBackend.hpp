@@ -1,0 +1,96 @@
+// HIP backend of the C++ API: replaces the reference's DeviceContext
+// (cuda/CudaContext.{hpp,cpp}), CudaStorageAllocator
+// (cuda/memory/CudaStorageAllocator.cpp) and the kernel registrations
+// (cuda/kernels/elementwise.cu:318-336).  Everything goes through the C ABI
+// of libtf_hip (include/tf_hip.h); a failing call throws std::runtime_error
+// carrying tf_last_error().
+//
+// The device-op wrappers below take Tensors, check shapes / dtypes / devices
+// on the host and launch on the device's stream.  Operands must be
+// contiguous; outputs are caller-allocated.
+#pragma once
+
+#include "tensor/CPUStorageAllocator.hpp"
+#include "tensor/Tensor.hpp"
+
+#include <cstddef>
+#include <cstdint>
+
+struct tf_ctx;
+
+namespace tensorforge::hip {
+
+// The context of GPU `device` (created on first use; one stream and the
+// device's memory pool).  Throws when no GPU is visible.
+tf_ctx* context(int device = 0);
+// Throws std::runtime_error("<what>: <tf_last_error()>") when status != 0.
+void check(int status, const char* what);
+// Registers the GPU allocator, copy callback and elementwise slots (idempotent;
+// also runs when libtensorforge is loaded).
+void register_backend();
+// Blocks until the device's stream has drained.
+void synchronize(int device = 0);
+// Launch on a caller-owned hipStream_t from now on (nullptr: the context's own).
+void set_stream(void* stream, int device = 0);
+
+// ---- memory --------------------------------------------------------------
+Storage allocate(size_t size_bytes, Device device, Dtype dtype);
+void copy_bytes(void* dst, const void* src, size_t bytes, allocator_dispatch::CudaCopyKind kind, int device = 0);
+void fill(Tensor& t, float value);
+void zero(Tensor& t);
+
+// ---- elementwise ---------------------------------------------------------
+void add(const Tensor& a, const Tensor& b, Tensor& out);
+void sub(const Tensor& a, const Tensor& b, Tensor& out);
+void mul(const Tensor& a, const Tensor& b, Tensor& out);
+void relu(const Tensor& x, Tensor& y);
+void sigmoid(const Tensor& x, Tensor& y);
+void tanh(const Tensor& x, Tensor& y);
+void relu_backward(const Tensor& dy, const Tensor& x, Tensor& dx);
+void sigmoid_backward(const Tensor& dy, const Tensor& y, Tensor& dx);
+void tanh_backward(const Tensor& dy, const Tensor& y, Tensor& dx);
+void cast(const Tensor& x, Tensor& y);  // Float32 <-> BFloat16
+
+// ---- GEMM ----------------------------------------------------------------
+// C (M x N) = epi(alpha * op(A) op(B) + beta * C) on 2-D row-major tensors;
+// op(X) = X^T when the flag is set.  bias: Float32 [N] or nullptr.
+void gemm(const Tensor& A, bool trans_a, const Tensor& B, bool trans_b, Tensor& C, float alpha = 1.0f,
+          float beta = 0.0f, const Tensor* bias = nullptr, bool relu = false);
+// Raw tf_gemm_ex on device pointers (conv layers).
+void gemm_ex(int device, bool trans_a, bool trans_b, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+             int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b, void* C, int64_t ldc, int64_t stride_c,
+             int64_t batch, bool reduce_batch, Dtype in_dtype, Dtype out_dtype, int epilogue, const float* bias,
+             float beta = 0.0f);
+
+// ---- rows ----------------------------------------------------------------
+void softmax(const Tensor& x, Tensor& y);
+void log_softmax(const Tensor& x, Tensor& y);
+void softmax_backward(const Tensor& y, const Tensor& dy, Tensor& dx);
+void log_softmax_backward(const Tensor& y, const Tensor& dy, Tensor& dx);
+void cross_entropy_forward(const Tensor& logits, const Tensor& targets, Tensor& loss, Tensor* lse);
+void cross_entropy_backward(const Tensor& logits, const Tensor& targets, const Tensor* lse, const Tensor* grad_loss,
+                            Tensor& dlogits);
+void layernorm_forward(const Tensor& x, const Tensor& gamma, const Tensor& beta, Tensor& y, Tensor& mean,
+                       Tensor& rstd, float eps);
+void layernorm_backward(const Tensor& dy, const Tensor& x, const Tensor& gamma, const Tensor& mean, const Tensor& rstd,
+                        Tensor& dx, Tensor& dgamma, Tensor& dbeta, bool reference_compat);
+
+// ---- reductions / layout ---------------------------------------------------
+void sum_dim(const Tensor& x, Tensor& out, int64_t outer, int64_t reduce, int64_t inner);
+void expand_dim(const Tensor& up, Tensor& out, int64_t outer, int64_t reduce, int64_t inner);
+void transpose2d(const Tensor& x, Tensor& out, int64_t batch, int64_t rows, int64_t cols);
+void colsum(const Tensor& dy, Tensor& db);
+void chansum_nchw(const Tensor& dy, Tensor& db);
+
+// ---- conv index maps -----------------------------------------------------
+void im2col(const Tensor& x, Tensor& col, int64_t kH, int64_t kW, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+            int64_t dh, int64_t dw);
+void col2im(const Tensor& col, Tensor& dx, int64_t kH, int64_t kW, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+            int64_t dh, int64_t dw);
+
+// ---- optimiser -----------------------------------------------------------
+// Fused v = mu*v + g; p -= lr*v (mu == 0: p -= lr*g); shadow (BFloat16, may
+// be nullptr) receives bf16(p).
+void sgd_momentum(Tensor& p, const Tensor& g, Tensor* v, Tensor* shadow, float lr, float mu);
+
+}  // namespace tensorforge::hip

@@ -1,0 +1,68 @@
+#include "nn/CrossEntropyLoss.hpp"
+
+#include "autograd/Wiring.hpp"
+#include "autograd/ops/CrossEntropyBackward.hpp"
+#include "hip/HipBackend.hpp"
+
+#include <cmath>
+#include <stdexcept>
+
+namespace tensorforge::nn {
+
+Tensor CrossEntropyLoss::forward(Tensor logits, Tensor targets) {
+    const bool on_gpu = logits.device().type == DeviceType::CUDA;
+    if (logits.dtype() != Dtype::Float32 && !(on_gpu && logits.dtype() == Dtype::BFloat16))
+        throw std::invalid_argument("CrossEntropyLoss: logits must be Float32 (or BFloat16 on the GPU)");
+    if (logits.shape().ndim() != 2) throw std::invalid_argument("CrossEntropyLoss: logits must be 2D (N, C)");
+    if (targets.dtype() != Dtype::Int64) throw std::invalid_argument("CrossEntropyLoss: targets must be Int64");
+    const int64_t N = logits.shape()[0], C = logits.shape()[1];
+    if (targets.numel() != N) throw std::invalid_argument("CrossEntropyLoss: targets.numel() must equal logits.shape()[0]");
+    if (targets.device() != logits.device()) targets = targets.to(logits.device());
+
+    Tensor loss = Tensor::empty(Shape{1}, Dtype::Float32, logits.device());
+    NodePtr<CrossEntropyBackward> node;
+    if (on_gpu) {
+        // Target indices outside [0, C) contribute neither loss nor gradient
+        // (the train_mlp chain's one-hot mask skips them); they are not
+        // checked on the host, which would need a device->host copy per step.
+        Tensor lf = logits.dtype() == Dtype::Float32 ? logits : logits.to(Dtype::Float32);
+        Tensor lse = Tensor::empty(Shape{N}, Dtype::Float32, logits.device());
+        hip::cross_entropy_forward(lf, targets, loss, &lse);
+        if (logits.requires_grad()) node = std::make_shared<CrossEntropyBackward>(lf, targets, lse);
+    } else {
+        // softmax -> gather -> clamp(1e-9) -> -log -> mean, as
+        // reference nn/CrossEntropyLoss.cpp:36-62.
+        Tensor probs = Tensor::empty(logits.shape(), Dtype::Float32, Device::cpu());
+        const float* x = static_cast<const float*>(logits.data());
+        float* p = static_cast<float*>(probs.data());
+        for (int64_t r = 0; r < N; ++r) {
+            float mx = x[r * C];
+            for (int64_t j = 1; j < C; ++j) mx = x[r * C + j] > mx ? x[r * C + j] : mx;
+            float s = 0.0f;
+            for (int64_t j = 0; j < C; ++j) {
+                p[r * C + j] = std::exp(x[r * C + j] - mx);
+                s += p[r * C + j];
+            }
+            const float inv = 1.0f / s;
+            for (int64_t j = 0; j < C; ++j) p[r * C + j] *= inv;
+        }
+        const int64_t* t = static_cast<const int64_t*>(targets.data());
+        float total = 0.0f;
+        for (int64_t r = 0; r < N; ++r) {
+            if (t[r] < 0 || t[r] >= C) throw std::out_of_range("CrossEntropyLoss: target index out of range");
+            const float pt = p[r * C + t[r]];
+            total += -std::log(pt < 1e-9f ? 1e-9f : pt);
+        }
+        static_cast<float*>(loss.data())[0] = total / static_cast<float>(N);
+        if (logits.requires_grad()) node = std::make_shared<CrossEntropyBackward>(logits, targets, probs);
+    }
+    if (node) wiring::attach(loss, node, {wiring::accumulator_edge(logits)});
+    return loss;
+}
+
+Tensor CrossEntropyLoss::forward(Tensor) {
+    throw std::logic_error(
+        "CrossEntropyLoss::forward(logits) requires targets; call forward(logits, targets) instead.");
+}
+
+}  // namespace tensorforge::nn

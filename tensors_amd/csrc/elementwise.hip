@@ -74,6 +74,7 @@ __global__ void unary_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t
 // (autograd/ops/ReluBackward.hpp:25-31), so negative dy over a masked
 // element yields -0.0 exactly as on the CPU.
 struct AddOp { __device__ float operator()(float a, float b) const { return a + b; } };
+struct SubOp { __device__ float operator()(float a, float b) const { return a - b; } };
 struct MulOp { __device__ float operator()(float a, float b) const { return a * b; } };
 struct ReluBwdOp {
     __device__ float operator()(float dy, float x) const { return dy * (x > 0.0f ? 1.0f : 0.0f); }
@@ -219,6 +220,9 @@ extern "C" {
 
 tf_status tf_add(tf_ctx* ctx, const void* a, const void* b, void* out, int64_t n, int dtype) {
     return launch_binary(ctx, a, b, out, n, dtype, AddOp{}, "tf_add");
+}
+tf_status tf_sub(tf_ctx* ctx, const void* a, const void* b, void* out, int64_t n, int dtype) {
+    return launch_binary(ctx, a, b, out, n, dtype, SubOp{}, "tf_sub");
 }
 tf_status tf_mul(tf_ctx* ctx, const void* a, const void* b, void* out, int64_t n, int dtype) {
     return launch_binary(ctx, a, b, out, n, dtype, MulOp{}, "tf_mul");

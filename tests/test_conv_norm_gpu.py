@@ -132,9 +132,11 @@ def test_conv2d_backward_vs_reference_loop(ctx, case):
 def test_conv2d_backward_golden_1x1(ctx):
     # nn/conv2d_backward_test.cpp:110-160: 1x1 kernel golden values.
     x = np.array([1, 2, 3, 4], np.float32).reshape(1, 1, 2, 2)
-    w = np.array([0.5], np.float32).reshape(1, 1, 1, 1)
-    gout = np.array([0.4, 0.8, 1.2, 1.6], np.float32).reshape(1, 1, 2, 2)
+    w = np.array([2.0], np.float32).reshape(1, 1, 1, 1)
+    gout = np.array([0.1, 0.2, 0.3, 0.4], np.float32).reshape(1, 1, 2, 2)
     gin, gw, gb = _conv_bwd_gpu(ctx, x, w, gout, 1, 0)
+    assert_close(gin.numpy().ravel(), [0.2, 0.4, 0.6, 0.8], 1e-6, "golden dX", atol=1e-7)
+    assert_close(gw.numpy().ravel(), [3.0], 1e-6, "golden dW", atol=1e-7)
     rin, rw, rb = oracle.conv2d_bwd(x, w, gout, (1, 1), (0, 0), (1, 1))
     assert_close(gin.numpy(), rin, 1e-6, "1x1 dX", atol=1e-7)
     assert_close(gw.numpy().reshape(rw.shape), rw, 1e-6, "1x1 dW", atol=1e-7)
