@@ -96,6 +96,98 @@ def bench_c2(steps: int, warmup: int):
     return wall_ms / steps, mean, per
 
 
+def _rotating_bench(ctx, n_sets, launch, reps=60):
+    """Average device time of `launch(i)` cycling over n_sets buffer sets (the
+    sets together exceed the 256 MB Infinity Cache, so every launch streams
+    from HBM).  Event pair around `reps` back-to-back launches."""
+    for i in range(n_sets):
+        launch(i)
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record()
+    for r in range(reps):
+        launch(r % n_sets)
+    e1.record()
+    return e0.elapsed_ms(e1) / reps
+
+
+def bench_c3():
+    """Config 3 bandwidth kernels: fused LogSoftmax+NLL backward [4096 x 1024],
+    ReLU backward [4096 x 1024], LayerNorm backward [1024 x 1024]."""
+    import tensors_amd as ta
+    from tensors_amd import ops, synth
+
+    ctx = ta.Context(0)
+    out = {}
+    R, Cc = 4096, 1024
+    sets = 10
+    logits = [ctx.array(synth.normal(synth.seed(3, 0) + i, (R, Cc), std=3.0)) for i in range(sets)]
+    tg = ctx.array(synth.uniform_int(synth.seed(3, 1), (R,), Cc))
+    lse = [ctx.empty((R,)) for _ in range(sets)]
+    loss = ctx.empty((1,))
+    for i in range(sets):
+        ops.ce_fwd(logits[i], tg, loss, lse[i])
+    dl = [ctx.empty((R, Cc)) for _ in range(sets)]
+    ms = _rotating_bench(ctx, sets, lambda i: ops.ce_bwd(logits[i], tg, dl[i], lse=lse[i]))
+    algo = R * Cc * 4 * 2 + R * 8
+    out["c3a_logsoftmax_nll_bwd"] = {"us": round(ms * 1e3, 2), "bytes": algo, "gbps": round(algo / ms / 1e6, 1),
+                                     "frac_hbm": round(algo / ms / 1e6 / PEAK_HBM_GBPS, 3)}
+    ms = _rotating_bench(ctx, sets, lambda i: ops.ce_fwd_bwd(logits[i], tg, loss, dl[i]))
+    out["c3a_ce_fused_fwd_bwd"] = {"us": round(ms * 1e3, 2), "bytes": algo, "gbps": round(algo / ms / 1e6, 1)}
+    del logits, dl, lse
+    sets = 6
+    xs = [ctx.array(synth.normal(synth.seed(3, 2) + i, (R, Cc))) for i in range(sets)]
+    dys = [ctx.array(synth.normal(synth.seed(3, 3) + i, (R, Cc))) for i in range(sets)]
+    dxs = [ctx.empty((R, Cc)) for _ in range(sets)]
+    ms = _rotating_bench(ctx, sets, lambda i: ops.relu_bwd(dys[i], xs[i], dxs[i]))
+    algo = R * Cc * 4 * 3
+    out["c3b_relu_bwd"] = {"us": round(ms * 1e3, 2), "bytes": algo, "gbps": round(algo / ms / 1e6, 1),
+                           "frac_hbm": round(algo / ms / 1e6 / PEAK_HBM_GBPS, 3)}
+    del xs, dys, dxs
+    R = Cc = 1024
+    sets = 24
+    g = ctx.array(np.ones(Cc, np.float32))
+    xs = [ctx.array(synth.normal(synth.seed(3, 4) + i, (R, Cc))) for i in range(sets)]
+    dys = [ctx.array(synth.normal(synth.seed(3, 5) + i, (R, Cc))) for i in range(sets)]
+    means = [ctx.empty((R,)) for _ in range(sets)]
+    rstds = [ctx.empty((R,)) for _ in range(sets)]
+    ys = ctx.empty((R, Cc))
+    beta = ctx.zeros((Cc,))
+    for i in range(sets):
+        ops.layernorm_fwd(xs[i], g, beta, ys, means[i], rstds[i])
+    dxs = [ctx.empty((R, Cc)) for _ in range(sets)]
+    dg, db = ctx.empty((Cc,)), ctx.empty((Cc,))
+    ms = _rotating_bench(ctx, sets, lambda i: ops.layernorm_bwd(dys[i], xs[i], g, means[i], rstds[i], dxs[i], dg, db))
+    algo = R * Cc * 4 * 3 + Cc * 4 * 3 + R * 8
+    out["c3c_layernorm_bwd"] = {"us": round(ms * 1e3, 2), "bytes": algo, "gbps": round(algo / ms / 1e6, 1),
+                                "frac_hbm": round(algo / ms / 1e6 / PEAK_HBM_GBPS, 3)}
+    ctx.close()
+    return out
+
+
+def bench_api_steps():
+    """Whole training steps through the C++ API (host launch work included)."""
+    from tensors_amd import api, synth
+    out = {}
+    xs = synth.mnist_like(synth.seed(1, 0), (100, 64, 784))
+    ys = synth.uniform_int(synth.seed(1, 1), (100, 64), 10)
+    _, _, ms = api.mlp_train([784, 256, 128, 10], xs, ys, steps=100, warmup=10, lr=0.1, mu=0.9, on_gpu=True,
+                             reference_compat=True)
+    out["c1_mlp_step_ms"] = round(ms, 4)
+    xs = synth.normal(synth.seed(4, 0), (1, 128, 3, 32, 32))
+    ys = synth.uniform_int(synth.seed(4, 1), (1, 128), 10)
+    _, ms = api.cnn_train(xs, ys, steps=23, warmup=3, lr=0.01, mu=0.9, on_gpu=True)
+    out["c4_cnn_step_ms"] = round(ms, 4)
+    dims = [4096, 8192, 8192, 4096, 1000]
+    xs = synth.normal(synth.seed(5, 0), (1, 4096, 4096))
+    ys = synth.uniform_int(synth.seed(5, 1), (1, 4096), 1000)
+    _, _, ms = api.mlp_train(dims, xs, ys, steps=13, warmup=3, lr=0.01, mu=0.9, on_gpu=True, bf16=True)
+    flop = 2 * 4096 * sum(dims[i] * dims[i + 1] for i in range(4)) * 3 - 2 * 4096 * dims[0] * dims[1]
+    out["c5_bf16_mlp_step_ms"] = round(ms, 4)
+    out["c5_bf16_step_tflops"] = round(flop / (ms * 1e-3) / 1e12, 1)
+    return out
+
+
 def cpu_baseline_c2():
     """Reference CPU path on a bounded sample of config 2.
 
@@ -154,6 +246,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only-c2", action="store_true", help="skip the other configurations' measurements")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -202,6 +295,8 @@ def main(argv=None):
         "sgd_gbps": round(sgd_gbps, 1),
         "step_ms_device_median": round(_median(per["step_dev"]), 4),
     }
+    if not args.only_c2:
+        line["other_configs"] = {"c3": bench_c3(), **bench_api_steps()}
     if rank == 0 and not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_c2()
     if rank == 0:

@@ -38,6 +38,9 @@ void require_contig(const Tensor& t, const char* what) {
 
 tf_ctx* ctx_of(const Tensor& t) { return context(t.device().index); }
 
+// Elements a tensor's storage holds: a 0-d tensor holds one value.
+int64_t slots(const Tensor& t) { return t.shape().ndim() == 0 ? 1 : t.numel(); }
+
 void release_gpu(void* data, Device device) {
     if (g_exiting.load()) return;
     tf_ctx* c = nullptr;
@@ -313,7 +316,7 @@ void layernorm_backward(const Tensor& dy, const Tensor& x, const Tensor& gamma, 
 
 void sum_dim(const Tensor& x, Tensor& out, int64_t outer, int64_t reduce, int64_t inner) {
     require_gpu(x, "hip::sum"); require_gpu(out, "hip::sum");
-    require(x.numel() == outer * reduce * inner && out.numel() == outer * inner, "hip::sum: extents");
+    require(slots(x) == outer * reduce * inner && slots(out) == outer * inner, "hip::sum: extents");
     require(x.dtype() == Dtype::Float32, "hip::sum: Float32 only");
     check(tf_sum_dim(ctx_of(x), static_cast<const float*>(x.data()), static_cast<float*>(out.data()), outer, reduce, inner),
           "hip::sum");
@@ -321,7 +324,7 @@ void sum_dim(const Tensor& x, Tensor& out, int64_t outer, int64_t reduce, int64_
 
 void expand_dim(const Tensor& up, Tensor& out, int64_t outer, int64_t reduce, int64_t inner) {
     require_gpu(up, "hip::expand"); require_gpu(out, "hip::expand");
-    require(up.numel() == outer * inner && out.numel() == outer * reduce * inner, "hip::expand: extents");
+    require(slots(up) == outer * inner && slots(out) == outer * reduce * inner, "hip::expand: extents");
     check(tf_expand_dim(ctx_of(up), static_cast<const float*>(up.data()), static_cast<float*>(out.data()), outer,
                         reduce, inner),
           "hip::expand");

@@ -116,7 +116,10 @@ float host_bf16_to_f32(uint16_t h) {
 }  // namespace
 
 Tensor Tensor::empty(Shape shape, Dtype dtype, Device device) {
-    const size_t bytes = static_cast<size_t>(shape.numel()) * dtype_size(dtype);
+    // A 0-d shape has numel() == 0 (reference convention) yet holds one value
+    // (e.g. a full reduction): give it room for one element.
+    const int64_t slots = shape.ndim() == 0 ? 1 : shape.numel();
+    const size_t bytes = static_cast<size_t>(slots) * dtype_size(dtype);
     Storage storage = allocator_dispatch::allocate(bytes, device, dtype);
     Stride stride = Stride::compute_row_major(shape);
     return Tensor(std::move(storage), 0, std::move(shape), std::move(stride));
