@@ -10,7 +10,8 @@ baseline); the product path never does.
   compiled from its sources by ``oracle/Makefile`` with ``ref_shim.cpp``; only
   present where the reference tree was available at build time.
 
-Pinning of each function is listed in ``oracle/README.md``.
+How each function is pinned is described in oracle/README.md and tested in
+tests/test_oracle.py.
 """
 from __future__ import annotations
 
