@@ -34,6 +34,9 @@ ARCH = "gfx950"
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Private arrays stay in registers or scratch; never silently in LDS (the
+    # GEMM kernels size their LDS to one workgroup per CU).
+    "-mllvm", "-disable-promote-alloca-to-lds",
     "-Wno-unused-command-line-argument",
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]

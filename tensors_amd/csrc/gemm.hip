@@ -37,11 +37,16 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <type_traits>
+#include <utility>
 
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+// Native 16-byte vector (HIP's uint4 is a struct whose copies lower to
+// memcpy, which keeps staging arrays out of registers).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128;
 constexpr int kThreads = 256;
@@ -64,6 +69,8 @@ struct GemmParams {
     int out_bf16;
     int vec_a, vec_b;      // 16-byte vector loads legal for A / B
     int pair_c;            // 8-byte paired stores legal for C
+    uint32_t a_bytes, b_bytes;  // byte extent of one batch element of A / B (buffer loads)
+    int int_m, int_n;           // large-tile path: tile rows / columns covered by the interior kernel
 };
 
 // Remap a linear workgroup id so that the ids one XCD receives (id % 8 == x)
@@ -465,6 +472,658 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(GemmParams p) {
     store_wave<NSUB, A_PAIR, B_PAIR>(p, acc, m0 + wm * 64, n0 + wn * WN, (int64_t)batch * p.stride_c, split);
 }
 
+// ---------------------------------------------------------------------------
+// Large-tile bf16 kernel: 256 x 256 x 64 per 256-thread workgroup, each wave
+// a 128 x 128 block (4 x 4 accumulators of 32 x 32, 256 accumulator
+// registers).  Per 16-deep k step a wave reads 8 KB of fragments for 16
+// MFMAs, half the LDS traffic per flop of a 64 x 64 wave block.
+//
+// Both operands are kept K-major in LDS ([256 rows][64 k], 128 B per row) so
+// every fragment is one ds_read_b128.  The 16-byte chunk c of row r sits at
+// chunk position c ^ swz(r); with swz(r) = (r ^ r >> 3) & 7 the 16 lanes of
+// a b128 access (16 consecutive rows, one chunk) hit 64 distinct banks.
+// MN-major operands are transposed on the way in: each thread loads an
+// 8 (k) x 8 (rows) block with eight 16-byte loads and rebuilds eight
+// k-contiguous rows in registers (byte permutes).  Threads with mb & 8 write
+// their rows in pairwise-swapped order so every 16-lane store group covers
+// both row parities, which keeps those stores conflict-free too.
+//
+// 2 x 32 KB x 2 (double buffer) = 128 KB of LDS: one workgroup per CU.
+// ---------------------------------------------------------------------------
+constexpr int kBigTile = 256;
+constexpr int kBigK = 64;
+
+// Lambdas in the large-tile kernel must inline: an out-of-line lambda takes
+// its captures (accumulators, staging registers) through memory.
+#define TF_LAMBDA_INLINE __attribute__((always_inline))
+
+__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
+
+// Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 (compile-time unroll).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// One 16-byte chunk of bf16 values at p[0 .. 7] with elements i >= n read as
+// zero (n <= 0: all zero).
+__device__ __forceinline__ u32x4 load_bf16x8_guarded(const uint16_t* __restrict__ p, int n, bool vec_ok) {
+    if (vec_ok && n >= 8) return *reinterpret_cast<const u32x4*>(p);
+    uint32_t d[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t lo = 2 * w < n ? p[2 * w] : 0u;
+        const uint32_t hi = 2 * w + 1 < n ? p[2 * w + 1] : 0u;
+        d[w] = lo | (hi << 16);
+    }
+    return u32x4{d[0], d[1], d[2], d[3]};
+}
+
+// Global -> registers -> LDS staging of one 256 x 64 operand tile.  GUARD:
+// clip rows to `rows` and k to `kend` (zero fill); without it the caller
+// guarantees the whole tile is in range and 16-byte loads are legal.
+template <bool KMAJ, bool GUARD>
+struct BigStage {
+    u32x4 reg[8];  // indexed only through static_for: must stay in registers
+
+    __device__ __forceinline__ void load(const uint16_t* __restrict__ p, int64_t ld, int row0, int rows, int k0,
+                                         int kend, bool vec_ok) {
+        const int t = threadIdx.x;
+        if (KMAJ) {
+            // reg[i]: row t/8 + 32i of the tile, k chunk t%8 (8 values).
+            const int c = t & 7, r = t >> 3;
+            const uint16_t* src = p + (int64_t)(row0 + r) * ld + k0 + 8 * c;
+            static_for<8>([&](auto I) TF_LAMBDA_INLINE {
+                constexpr int i = decltype(I)::value;
+                if (!GUARD) {
+                    reg[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)32 * i * ld);
+                } else {
+                    const bool in = row0 + r + 32 * i < rows;
+                    reg[i] = in ? load_bf16x8_guarded(src + (int64_t)32 * i * ld, kend - (k0 + 8 * c), vec_ok)
+                                : u32x4{0u, 0u, 0u, 0u};
+                }
+            });
+        } else {
+            // Block (kb, mb) = (t/32, t%32): reg[kk] = rows 8mb .. 8mb+7 at k = 8kb + kk.
+            const int mb = t & 31, kb = t >> 5;
+            const uint16_t* src = p + (int64_t)(k0 + 8 * kb) * ld + row0 + 8 * mb;
+            static_for<8>([&](auto KK) TF_LAMBDA_INLINE {
+                constexpr int kk = decltype(KK)::value;
+                if (!GUARD) {
+                    reg[kk] = *reinterpret_cast<const u32x4*>(src + (int64_t)kk * ld);
+                } else {
+                    const bool in = k0 + 8 * kb + kk < kend;
+                    reg[kk] = in ? load_bf16x8_guarded(src + (int64_t)kk * ld, rows - (row0 + 8 * mb), vec_ok)
+                                 : u32x4{0u, 0u, 0u, 0u};
+                }
+            });
+        }
+    }
+
+    __device__ __forceinline__ void store(u32x4* __restrict__ lds) const {
+        const int t = threadIdx.x;
+        if (KMAJ) {
+            const int c = t & 7, r = t >> 3;
+            static_for<8>([&](auto I) TF_LAMBDA_INLINE {
+                constexpr int i = decltype(I)::value;
+                const int row = r + 32 * i;
+                lds[row * 8 + (c ^ swz(row))] = reg[i];
+            });
+        } else {
+            const int mb = t & 31, kb = t >> 5;
+            const int flip = (mb >> 3) & 1;
+            const uint32_t keep = flip ? 0u : ~0u;  // bit blend, not a runtime index
+            // Row 8mb + m as 4 bf16 pairs: pair j = (k 2j, k 2j+1) = element m of reg[2j], reg[2j+1].
+            auto row_words = [&](auto M) TF_LAMBDA_INLINE {
+                constexpr int m = decltype(M)::value;
+                uint32_t d[4];
+                static_for<4>([&](auto J) TF_LAMBDA_INLINE {
+                    constexpr int j = decltype(J)::value;
+                    const uint32_t lo = reg[2 * j][m >> 1];
+                    const uint32_t hi = reg[2 * j + 1][m >> 1];
+                    d[j] = (m & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+                });
+                return u32x4{d[0], d[1], d[2], d[3]};
+            };
+            static_for<8>([&](auto J) TF_LAMBDA_INLINE {
+                constexpr int j = decltype(J)::value;
+                const u32x4 x = row_words(std::integral_constant<int, j>{});
+                const u32x4 y = row_words(std::integral_constant<int, j ^ 1>{});
+                const u32x4 v = (x & keep) | (y & ~keep);
+                const int row = 8 * mb + (j ^ flip);
+                lds[row * 8 + (kb ^ swz(row))] = v;
+            });
+        }
+    }
+};
+
+// Fragments of k step s (0..3) of an LDS block: lane half h feeds
+// k = 16s + 8h .. +7, i.e. chunk 2s + h of its row.  a_row/b_row: u32x4
+// offsets of the lane's four A and B rows; a_sw/b_sw: their swizzles.
+struct BigFrags {
+    v8bf a[4], b[4];
+};
+
+__device__ __forceinline__ void big_read(const u32x4* __restrict__ la, const u32x4* __restrict__ lb, int s,
+                                         const int (&a_row)[4], const int (&a_sw)[4], const int (&b_row)[4],
+                                         const int (&b_sw)[4], int half, BigFrags& f) {
+    const int c = 2 * s + half;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f.a[i] = __builtin_bit_cast(v8bf, la[a_row[i] + (c ^ a_sw[i])]);
+        f.b[i] = __builtin_bit_cast(v8bf, lb[b_row[i] + (c ^ b_sw[i])]);
+    }
+}
+
+__device__ __forceinline__ void big_mfma(const BigFrags& f, v16f (&acc)[4][4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+}
+
+// MFMAs BEGIN .. END-1 of the 16 of one k step (index 4i + j).
+template <int BEGIN, int END>
+__device__ __forceinline__ void big_mfma_part(const BigFrags& f, v16f (&acc)[4][4]) {
+#pragma unroll
+    for (int x = BEGIN; x < END; ++x)
+        acc[x >> 2][x & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[x >> 2], f.b[x & 3], acc[x >> 2][x & 3], 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Interior tiles (gemm_bf16_dl_kernel): operands go global -> LDS directly
+// with buffer_load_dwordx4 ... lds (no registers, no LDS write
+// instructions), 32-deep k blocks in 5 LDS buffers of 2 x 16 KB, so four
+// blocks (128 KB) are in flight while one is computed.  Loads are issued
+// about seven 16-deep k steps ahead of use, which covers the L2/HBM round
+// trip at full MFMA rate.
+//
+// A wave's load instruction fills 1 KB of LDS, lane l bytes 16l .. 16l+15,
+// so the swizzle is applied to the global addresses:
+//   K-major operand, LDS [256 rows][32 k] (64 B rows, 4 chunks): 1 KB = 16
+//     rows; lane l loads row l/4, logical chunk (l%4) ^ swz32(row) with
+//     swz32(row) = (row >> 2) & 3, which spreads the 16 rows of one b128
+//     fragment read over all 64 banks.  Fragments: ds_read_b128.
+//   MN-major operand, LDS [32 k][256 rows] (512 B per k row): 1 KB = 2 k
+//     rows; lane l loads k row l/32, logical chunk (l%32) ^ 4(k%4).
+//     Fragments: ds_read_b64_tr_b16, which hands lane i (of each 16-lane
+//     group) element i%4 of the 8-byte rows addressed by lanes i/4 + 4j,
+//     j = 0..3: with lane a addressing [k = kb + a/4][m = mb + 4(a%4)], lane
+//     i receives A[mb + i][kb + j], the MFMA operand layout.  The chunk
+//     rotation by 4(k%4) spreads the four k rows of one read over all banks.
+// ---------------------------------------------------------------------------
+constexpr int kDlK = 32;                                  // k per LDS block
+constexpr int kDlBufs = 5;                                // LDS blocks
+constexpr int kDlVec = kBigTile * kDlK * 2 / 16;          // u32x4 per operand block (16 KB)
+constexpr int kDlLoads = kBigTile * kDlK * 2 / 1024 / 4;  // 1 KB loads per wave per operand block
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+__device__ __forceinline__ int swz32(int row) { return (row >> 2) & 3; }
+
+// s_waitcnt immediate (gfx9 encoding) waiting for at most n outstanding
+// vector memory operations, leaving the other counters unconstrained.
+constexpr int waitcnt_vm(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
+// ... and for all outstanding LDS operations.
+constexpr int waitcnt_vm_lds(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0070; }
+
+// Workgroup barrier for the direct-to-LDS pipeline: waits for this wave's
+// loads except the newest `outstanding` and for all of its LDS reads, then
+// s_barrier.  __syncthreads() would add a release fence, which must wait for
+// every in-flight LDS load (vmcnt(0)) and so would drain the pipeline.  The
+// "memory" clobber keeps the compiler from moving memory accesses across.
+template <int OUTSTANDING>
+__device__ __forceinline__ void dl_barrier() {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lds(OUTSTANDING));
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// Byte offsets (from the operand's base) of this lane's kDlLoads direct
+// loads of a tile at row0 = k0 = 0; the tile position is added as a uniform
+// offset.  Wave w fills 1 KB blocks kDlLoads*w .. of the LDS block.
+template <bool KMAJ>
+__device__ __forceinline__ void dl_offsets(int64_t ld, uint32_t (&voff)[kDlLoads]) {
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < kDlLoads; ++i) {
+        const int blk = w * kDlLoads + i;
+        if (KMAJ) {
+            const int row = blk * 16 + (l >> 2);
+            voff[i] = 2u * ((uint32_t)row * (uint32_t)ld + 8u * (uint32_t)((l & 3) ^ swz32(row)));
+        } else {
+            const int k = blk * 2 + (l >> 5);
+            voff[i] = 2u * ((uint32_t)k * (uint32_t)ld + 8u * (uint32_t)((l & 31) ^ (4 * (k & 3))));
+        }
+    }
+}
+
+// Buffer resource descriptor for raw 16-byte loads from `base` (gfx9-family
+// word 3: raw dword access; reads beyond `bytes` return zero).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 dl_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return i32x4{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), (int)bytes, 0x00020000};
+}
+
+// Issue this wave's direct loads of one operand block:
+// buffer_load_dwordx4 ... lds, M0 = the 1 KB LDS destination.  Written as
+// inline assembly on purpose: the compiler's wait-count tracking of LDS
+// loads loses track of which buffer each one writes (at the loop header) and
+// then makes fragment reads wait for every load in flight, draining the
+// pipeline.  The kernel waits for these loads itself (dl_barrier, and a
+// final vmcnt(0)), and nothing else in it uses M0.
+__device__ __forceinline__ void dl_issue(i32x4 rsrc, uint32_t tile_off, const uint32_t (&voff)[kDlLoads],
+                                         u32x4* lds_block) {
+    const int w = threadIdx.x >> 6;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_ptr)(lds_block + w * kDlLoads * 64);
+    static_for<kDlLoads>([&](auto I) TF_LAMBDA_INLINE {
+        constexpr int i = decltype(I)::value;
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(lds0 + i * 1024u);
+        const uint32_t v = voff[i], so = tile_off;  // asm operands must be locals of the lambda
+        const i32x4 r = rsrc;
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                     :
+                     : "s"(dst), "v"(v), "s"(r), "s"(so)
+                     : "memory", "m0");
+    });
+}
+
+// Per-lane fragment offsets of one operand (4 sub-tiles of 32 rows from
+// row wbase).  K-major: u32x4 index of the row and its swizzle.  MN-major:
+// bf16 element offset of the lane's first transposed read.
+template <bool KMAJ>
+struct DlOperand {
+    int off[4], sw[4];
+    __device__ __forceinline__ void init(int wbase) {
+        const int l = threadIdx.x & 63;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (KMAJ) {
+                const int r = wbase + 32 * i + (l & 31);
+                off[i] = r * (kDlK / 8);
+                sw[i] = swz32(r);
+            } else {
+                const int g = l >> 4, a = l & 15, q = a & 3, j = a >> 2;
+                const int m = wbase + 32 * i + 16 * (g & 1) + 4 * q;
+                off[i] = (8 * (g >> 1) + j) * kBigTile + (((m >> 3) ^ (4 * j)) * 8) + (m & 7);
+                sw[i] = 0;
+            }
+        }
+    }
+    // Fragment of sub-tile i at k step s (lane half h: k = 16s + 8h .. +7).
+    __device__ __forceinline__ v8bf frag(const u32x4* __restrict__ lds, int i, int s, int half) const {
+        if (KMAJ) return __builtin_bit_cast(v8bf, lds[off[i] + ((2 * s + half) ^ sw[i])]);
+        const short* base = reinterpret_cast<const short*>(lds) + off[i] + 16 * s * kBigTile;
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)base);
+        const v4s hi =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(base + 4 * kBigTile));
+        return __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+};
+
+// Writes a 256 x 256 accumulator tile (bounds-checked when GUARD).
+template <bool GUARD>
+__device__ __forceinline__ void big_epilogue(const GemmParams& p, v16f (&acc)[4][4], int m0, int n0, int split,
+                                             int batch) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int half = lane >> 5, l32 = lane & 31;
+    // Epilogue: lane l, register r of acc[i][j] is row 32i + 8(r/4) + 4(l/32)
+    // + r%4, column 32j + l%32 of the wave block.  static_for keeps every
+    // accumulator index a compile-time constant (a runtime index would move
+    // the accumulators to scratch memory); the output variant is chosen once
+    // outside the unrolled loops.
+    const int m_base = m0 + wm * 128 + 4 * half, n_base = n0 + wn * 128 + l32;
+    auto for_each = [&](auto&& st) TF_LAMBDA_INLINE {
+        static_for<4>([&](auto J) TF_LAMBDA_INLINE {
+            constexpr int j = decltype(J)::value;
+            const int col = n_base + 32 * j;
+            if (GUARD && col >= p.N) return;
+            static_for<4>([&](auto I) TF_LAMBDA_INLINE {
+                constexpr int i = decltype(I)::value;
+                static_for<16>([&](auto R) TF_LAMBDA_INLINE {
+                    constexpr int r = decltype(R)::value;
+                    const int row = m_base + 32 * i + 8 * (r >> 2) + (r & 3);
+                    if (GUARD && row >= p.M) return;
+                    st(row, col, acc[i][j][r]);
+                });
+            });
+        });
+    };
+    if (p.partial) {
+        float* part = p.partial + (int64_t)split * p.M * p.N;
+        for_each([&](int row, int col, float v) TF_LAMBDA_INLINE { part[(int64_t)row * p.N + col] = v; });
+        return;
+    }
+    const bool has_bias = p.epi != TF_EPI_NONE && p.epi != TF_EPI_RELU;
+    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU || p.epi == TF_EPI_ROW_BIAS_RELU;
+    const float* col_bias = has_bias && !p.row_bias ? p.bias : nullptr;
+    const float* row_bias = has_bias && p.row_bias ? p.bias : nullptr;
+    const float alpha = p.alpha;
+    const int64_t ldc = p.ldc;
+    if (p.beta == 0.0f && !p.out_bf16 && !has_bias && !relu) {
+        float* C = reinterpret_cast<float*>(p.C) + (int64_t)batch * p.stride_c;
+        for_each([&](int row, int col, float v) TF_LAMBDA_INLINE { C[(int64_t)row * ldc + col] = alpha * v; });
+    } else if (p.beta == 0.0f && p.out_bf16) {
+        uint16_t* C = reinterpret_cast<uint16_t*>(p.C) + (int64_t)batch * p.stride_c;
+        for_each([&](int row, int col, float v) TF_LAMBDA_INLINE {
+            v = alpha * v + (col_bias ? col_bias[col] : 0.0f) + (row_bias ? row_bias[row] : 0.0f);
+            if (relu) v = fmaxf(v, 0.0f);
+            C[(int64_t)row * ldc + col] = tfd::f32_to_bf16(v);
+        });
+    } else {
+        const int64_t batch_off_c = (int64_t)batch * p.stride_c;
+        for_each([&](int row, int col, float v) TF_LAMBDA_INLINE {
+            const float b = (col_bias ? col_bias[col] : 0.0f) + (row_bias ? row_bias[row] : 0.0f);
+            emit(p, batch_off_c + (int64_t)row * ldc + col, v, b, relu);
+        });
+    }
+}
+
+// One 256 x 256 tile with register-staged, bounds-checked 64-deep blocks.
+template <bool A_KMAJ, bool B_KMAJ>
+__device__ __forceinline__ void big_tile_guarded(const GemmParams& p, int m0, int n0, int split, int batch,
+                                                 int kb_beg, int nk, u32x4* a0, u32x4* a1, u32x4* b0, u32x4* b1) {
+    const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A) + (int64_t)batch * p.stride_a;
+    const uint16_t* B = reinterpret_cast<const uint16_t*>(p.B) + (int64_t)batch * p.stride_b;
+    const int kb_per_b = (p.K + kBigK - 1) / kBigK;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int half = lane >> 5, l32 = lane & 31;
+
+    v16f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = v16f{};
+
+    int a_row[4], a_sw[4], b_row[4], b_sw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int ra = wm * 128 + 32 * i + l32, rb = wn * 128 + 32 * i + l32;
+        a_row[i] = ra * 8; a_sw[i] = swz(ra);
+        b_row[i] = rb * 8; b_sw[i] = swz(rb);
+    }
+
+    // Software pipeline over k blocks (LDS buffer kt & 1 holds block kt):
+    //   step 0: MFMAs of k step 0 | fragment reads for step 1
+    //   step 1: MFMAs of step 1   | reads for step 2
+    //   step 2: MFMAs of step 2   | reads for step 3; LDS writes of block
+    //                               kt+1 (staged in registers) to the other buffer
+    //   barrier                   (block kt+1 complete; block kt-1 no longer read)
+    //   step 3: MFMAs of step 3   | global loads of block kt+2 into the staging
+    //                               registers; reads of block kt+1's step 0
+    // Global loads get three k steps to land; the MFMA pipe is fed across the
+    // barrier.  sched_group_barrier pins the interleaving (the default
+    // scheduler clusters the memory operations and exposes their latency).
+    if (nk > 0) {
+        u32x4* lds_a[2] = {a0, a1};
+        u32x4* lds_b[2] = {b0, b1};
+        BigStage<A_KMAJ, true> sa;
+        BigStage<B_KMAJ, true> sb;
+        BigFrags f[2];
+        auto load_block = [&](int kb) TF_LAMBDA_INLINE {
+            const int b = kb / kb_per_b, k0 = (kb - b * kb_per_b) * kBigK;
+            sa.load(A + (int64_t)b * p.stride_a, p.lda, m0, p.M, k0, p.K, p.vec_a);
+            sb.load(B + (int64_t)b * p.stride_b, p.ldb, n0, p.N, k0, p.K, p.vec_b);
+        };
+        auto read = [&](int buf, int s, BigFrags& dst) TF_LAMBDA_INLINE {
+            big_read(lds_a[buf], lds_b[buf], s, a_row, a_sw, b_row, b_sw, half, dst);
+        };
+        // One k block.  STORE: block kt+1 is staged and goes to LDS in step 2.
+        // LOAD: block kt+2 exists and is loaded in step 3.
+        auto block = [&](int kt, auto STORE, auto LOAD) TF_LAMBDA_INLINE {
+            constexpr bool store = decltype(STORE)::value, load = decltype(LOAD)::value;
+            const int cur = kt & 1;
+            static_for<3>([&](auto S) TF_LAMBDA_INLINE {
+                constexpr int s = decltype(S)::value;
+                read(cur, s + 1, f[(s + 1) & 1]);
+                big_mfma(f[s & 1], acc);
+                if constexpr (s == 2 && store) {
+                    sa.store(lds_a[cur ^ 1]);
+                    sb.store(lds_b[cur ^ 1]);
+                    static_for<8>([&](auto) TF_LAMBDA_INLINE {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);  // DS write
+                    });
+                } else {
+                    static_for<8>([&](auto) TF_LAMBDA_INLINE {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                    });
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            });
+            if constexpr (store) __syncthreads();
+            if constexpr (load) load_block(kb_beg + kt + 2);
+            if constexpr (store) read(cur ^ 1, 0, f[0]);
+            big_mfma(f[1], acc);
+            if constexpr (load && store) {
+                static_for<8>([&](auto) TF_LAMBDA_INLINE {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM read
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                });
+            } else if constexpr (store) {
+                static_for<8>([&](auto) TF_LAMBDA_INLINE {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                });
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        using T = std::true_type;
+        using F = std::false_type;
+        load_block(kb_beg);
+        sa.store(lds_a[0]);
+        sb.store(lds_b[0]);
+        if (nk > 1) load_block(kb_beg + 1);
+        __syncthreads();
+        read(0, 0, f[0]);
+        int kt = 0;
+        for (; kt + 2 < nk; ++kt) block(kt, T{}, T{});
+        if (kt + 1 < nk) block(kt++, T{}, F{});
+        block(kt, F{}, F{});
+    }
+
+    big_epilogue<true>(p, acc, m0, n0, split, batch);
+}
+
+// Interior-tile kernel.  Per 32-deep block t (LDS buffer t % 5):
+//   step 0: MFMAs of k step 0 | fragment reads of step 1
+//   wait for block t+1's loads (vmcnt), barrier: block t+1 is visible and
+//     every wave holds all of block t's fragments
+//   step 1: MFMAs of step 1 | loads of block t+5 into buffer t % 5 |
+//     reads of block t+1's step 0
+// The five LDS buffers are separate objects and every access names its
+// buffer at compile time (block<B>), so the compiler can see that a load
+// into one buffer does not alias fragment reads from another.
+template <bool A_KMAJ, bool B_KMAJ>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_bf16_dl_kernel(GemmParams p) {
+    // One array per buffer (A block, then B block): the compiler tracks the
+    // targets of in-flight LDS loads per LDS object and only for a few
+    // objects; with more, every fragment read waits for all loads.
+    __shared__ u32x4 s0[2 * kDlVec], s1[2 * kDlVec], s2[2 * kDlVec], s3[2 * kDlVec], s4[2 * kDlVec];
+
+    int tm, tn;
+    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int split = blockIdx.y;
+    const int batch = blockIdx.z;
+    const int m0 = tm * kBigTile, n0 = tn * kBigTile;
+    const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A) + (int64_t)batch * p.stride_a;
+    const uint16_t* B = reinterpret_cast<const uint16_t*>(p.B) + (int64_t)batch * p.stride_b;
+    // Splits are counted in 64-deep blocks (K % 64 == 0 here): two of ours each.
+    const int kb64_total = (p.K / 64) * p.reduce_batch;
+    const int kb64_beg = split * p.kb_per_split;
+    const int nk = 2 * max(0, min(kb64_total, kb64_beg + p.kb_per_split) - kb64_beg);
+    const int kb_beg = 2 * kb64_beg;
+    const int kpb = p.K / kDlK;  // 32-deep blocks per batch element
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int half = lane >> 5;
+    v16f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = v16f{};
+
+    if (nk > 0) {
+        DlOperand<A_KMAJ> oa;
+        DlOperand<B_KMAJ> ob;
+        oa.init((wave >> 1) * 128);
+        ob.init((wave & 1) * 128);
+        uint32_t voff_a[kDlLoads], voff_b[kDlLoads];
+        dl_offsets<A_KMAJ>(p.lda, voff_a);
+        dl_offsets<B_KMAJ>(p.ldb, voff_b);
+        BigFrags f[2];
+        auto buf_a = [&](auto Bc) TF_LAMBDA_INLINE -> u32x4* {
+            constexpr int b = decltype(Bc)::value;
+            if constexpr (b == 0) return s0;
+            else if constexpr (b == 1) return s1;
+            else if constexpr (b == 2) return s2;
+            else if constexpr (b == 3) return s3;
+            else return s4;
+        };
+        auto buf_b = [&](auto Bc) TF_LAMBDA_INLINE -> u32x4* { return buf_a(Bc) + kDlVec; };
+        auto issue = [&](int kb, u32x4* la, u32x4* lb) TF_LAMBDA_INLINE {
+            const int b = kb / kpb;
+            const uint32_t k0 = (uint32_t)((kb - b * kpb) * kDlK);
+            const i32x4 ra = dl_rsrc(A + (int64_t)b * p.stride_a, p.a_bytes);
+            const i32x4 rb = dl_rsrc(B + (int64_t)b * p.stride_b, p.b_bytes);
+            const uint32_t ta =
+                2u * (A_KMAJ ? (uint32_t)m0 * (uint32_t)p.lda + k0 : k0 * (uint32_t)p.lda + (uint32_t)m0);
+            const uint32_t tb =
+                2u * (B_KMAJ ? (uint32_t)n0 * (uint32_t)p.ldb + k0 : k0 * (uint32_t)p.ldb + (uint32_t)n0);
+            dl_issue(ra, ta, voff_a, la);
+            dl_issue(rb, tb, voff_b, lb);
+        };
+        // Read order A0, B0..B3, A1..A3: the step's MFMAs (A_i x B_j,
+        // i-major) can start after 2 reads, each further one needs at most
+        // one more.
+        auto read = [&](const u32x4* la, const u32x4* lb, int s, BigFrags& dst) TF_LAMBDA_INLINE {
+            dst.a[0] = oa.frag(la, 0, s, half);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dst.b[j] = ob.frag(lb, j, s, half);
+#pragma unroll
+            for (int i = 1; i < 4; ++i) dst.a[i] = oa.frag(la, i, s, half);
+        };
+        constexpr int kReads = (A_KMAJ ? 4 : 8) + (B_KMAJ ? 4 : 8);  // LDS read instructions per k step
+        // Every block but the last loads block t+5 (clamped to the last real
+        // block: loads past the end land in buffers nobody reads again), so
+        // exactly three blocks of loads are outstanding behind block t+1's
+        // at each wait and all blocks have the same shape.  LAST: no next
+        // block, so no wait, barrier, loads or next-block reads.
+        auto block = [&](auto Bc, int t, auto LAST) TF_LAMBDA_INLINE {
+            constexpr int b = decltype(Bc)::value;
+            constexpr bool last = decltype(LAST)::value;
+            u32x4* la = buf_a(Bc);
+            u32x4* lb = buf_b(Bc);
+            u32x4* na = buf_a(std::integral_constant<int, (b + 1) % kDlBufs>{});
+            u32x4* nb = buf_b(std::integral_constant<int, (b + 1) % kDlBufs>{});
+            read(la, lb, 1, f[1]);
+            big_mfma(f[0], acc);
+            static_for<8>([&](auto) TF_LAMBDA_INLINE {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);           // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, kReads / 8, 0);  // DS read
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (!last) {
+                dl_barrier<3 * 2 * kDlLoads>();  // block t+1 has landed; block t fully read
+                issue(kb_beg + min(t + kDlBufs, nk - 1), la, lb);
+            }
+            big_mfma_part<0, 4>(f[1], acc);
+            if constexpr (!last) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x010, kDlLoads, 0);  // VMEM
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x010, kDlLoads, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (!last) read(na, nb, 0, f[0]);
+            big_mfma_part<4, 16>(f[1], acc);
+            if constexpr (!last) {
+                static_for<4>([&](auto) TF_LAMBDA_INLINE {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);           // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, kReads / 4, 0);  // DS read
+                });
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        // Prologue: blocks 0 .. 4 (clamped) into buffers 0 .. 4, wait for block 0.
+        static_for<kDlBufs>([&](auto Bc) TF_LAMBDA_INLINE {
+            issue(kb_beg + min((int)decltype(Bc)::value, nk - 1), buf_a(Bc), buf_b(Bc));
+        });
+        dl_barrier<(kDlBufs - 1) * 2 * kDlLoads>();  // block 0 has landed
+        read(s0, s0 + kDlVec, 0, f[0]);
+        // Blocks 0 .. nk-2, five per iteration (buffer = position in the group).
+        int t = 0;
+        bool stop = false;
+        while (!stop) {
+            static_for<kDlBufs>([&](auto Bc) TF_LAMBDA_INLINE {
+                if (stop) return;
+                if (t + 1 >= nk) {
+                    stop = true;
+                    return;
+                }
+                block(Bc, t, std::false_type{});
+                ++t;
+            });
+        }
+        // Block nk-1.
+        const int rlast = t % kDlBufs;
+        static_for<kDlBufs>([&](auto Bc) TF_LAMBDA_INLINE {
+            if (rlast == decltype(Bc)::value) block(Bc, t, std::true_type{});
+        });
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // drain the clamped loads before the waves end
+    }
+    big_epilogue<false>(p, acc, m0, n0, split, batch);
+}
+
+// Edge-tile kernel (or every tile when the direct path does not apply):
+// register-staged, bounds-checked 64-deep blocks.  Tiles: with an interior
+// grid of int_m x int_n, the tile rows from int_m on, then the tile columns
+// from int_n on of the rows above; without one, all tiles.
+template <bool A_KMAJ, bool B_KMAJ>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_bf16_big_kernel(GemmParams p) {
+    __shared__ u32x4 lds_a0[kBigTile * 8], lds_a1[kBigTile * 8];
+    __shared__ u32x4 lds_b0[kBigTile * 8], lds_b1[kBigTile * 8];
+
+    int tm, tn;
+    if (p.int_m * p.int_n == 0) {
+        tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    } else {
+        const int id = blockIdx.x;
+        const int below = (p.tiles_m - p.int_m) * p.tiles_n;
+        if (id < below) {
+            tm = p.int_m + id / p.tiles_n;
+            tn = id % p.tiles_n;
+        } else {
+            const int w = p.tiles_n - p.int_n, id2 = id - below;
+            tm = id2 / w;
+            tn = p.int_n + id2 % w;
+        }
+    }
+    const int split = blockIdx.y;
+    const int batch = blockIdx.z;
+    const int m0 = tm * kBigTile, n0 = tn * kBigTile;
+    const int kb_total = ((p.K + kBigK - 1) / kBigK) * p.reduce_batch;
+    const int kb_beg = split * p.kb_per_split;
+    const int nk = max(0, min(kb_total, kb_beg + p.kb_per_split) - kb_beg);
+    big_tile_guarded<A_KMAJ, B_KMAJ>(p, m0, n0, split, batch, kb_beg, nk, lds_a0, lds_a1, lds_b0, lds_b1);
+}
+
 // Split-K reduction: C = epi(alpha * sum_s partial[s] + beta * C), summing the
 // splits in ascending order (deterministic).
 __global__ void splitk_reduce_kernel(GemmParams p, int splits) {
@@ -506,7 +1165,29 @@ KernelFn pick_bf16(bool a_kmaj, bool b_kmaj) {
     return gemm_bf16_kernel<BN, false, false>;
 }
 
+KernelFn pick_bf16_big(bool a_kmaj, bool b_kmaj) {
+    if (a_kmaj && b_kmaj) return gemm_bf16_big_kernel<true, true>;
+    if (a_kmaj && !b_kmaj) return gemm_bf16_big_kernel<true, false>;
+    if (!a_kmaj && b_kmaj) return gemm_bf16_big_kernel<false, true>;
+    return gemm_bf16_big_kernel<false, false>;
+}
+
+KernelFn pick_bf16_dl(bool a_kmaj, bool b_kmaj) {
+    if (a_kmaj && b_kmaj) return gemm_bf16_dl_kernel<true, true>;
+    if (a_kmaj && !b_kmaj) return gemm_bf16_dl_kernel<true, false>;
+    if (!a_kmaj && b_kmaj) return gemm_bf16_dl_kernel<false, true>;
+    return gemm_bf16_dl_kernel<false, false>;
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Split count for a grid of `tiles` workgroups over `kblocks` k blocks:
+// enough slices for `target` workgroups, each slice >= min_per k blocks.
+int choose_splits(int64_t tiles, int64_t kblocks, int64_t target, int64_t min_per) {
+    if (tiles >= target || kblocks < 2 * min_per) return 1;
+    const int64_t want = (target + tiles - 1) / tiles;
+    return (int)std::max<int64_t>(1, std::min<int64_t>({want, kblocks / min_per, 256}));
+}
 
 tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                     const void* A, int64_t lda, int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b,
@@ -542,12 +1223,26 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
     p.stride_a = stride_a; p.stride_b = stride_b; p.stride_c = reduce_batch ? 0 : stride_c;
     p.M = (int)M; p.N = (int)N; p.K = (int)K;
-    // Tile width: 128 x 128 when that gives every CU at least two workgroups
-    // (two resident workgroups per CU hide each other's barrier and LDS
-    // latency), 128 x 64 otherwise and for narrow outputs.
-    const int64_t tiles_m = (M + BM - 1) / BM;
+    const int64_t ncu = ctx->num_cus;
+    // bf16 with enough work for one 256 x 256 tile per CU (directly, or with
+    // K split over at most 4 slices of >= 8 k blocks): the large-tile kernel.
+    bool big = false;
+    int splits = 1;
+    if (in_dtype == TF_BF16 && M >= 128 && N >= 128) {
+        const int64_t tb = ((M + kBigTile - 1) / kBigTile) * ((N + kBigTile - 1) / kBigTile) * grid_batch;
+        const int64_t kb = ((K + kBigK - 1) / kBigK) * (reduce_batch ? batch : 1);
+        const int s = grid_batch == 1 ? choose_splits(tb, kb, ncu, 8) : 1;
+        if (tb * s >= ncu && s <= 4) {
+            big = true;
+            splits = s;
+        }
+    }
+    // Otherwise: tile width 128 x 128 when that gives every CU at least two
+    // workgroups (two resident workgroups per CU hide each other's barrier
+    // and LDS latency), 128 x 64 otherwise and for narrow outputs.
+    const int64_t tiles_m = big ? (M + kBigTile - 1) / kBigTile : (M + BM - 1) / BM;
     const int64_t t128 = tiles_m * ((N + 127) / 128) * grid_batch;
-    const int BN = (N <= 64 || t128 < 2 * (int64_t)ctx->num_cus) ? 64 : 128;
+    const int BN = big ? kBigTile : (N <= 64 || t128 < 2 * ncu) ? 64 : 128;
     p.tiles_m = (int)tiles_m;
     p.tiles_n = (int)((N + BN - 1) / BN);
     p.alpha = alpha; p.beta = beta; p.epi = epi; p.row_bias = row_bias;
@@ -556,18 +1251,28 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     p.vec_a = aligned16(A) && (lda % vec_elems == 0) && (stride_a % vec_elems == 0);
     p.vec_b = aligned16(B) && (ldb % vec_elems == 0) && (stride_b % vec_elems == 0);
     p.pair_c = (reinterpret_cast<uintptr_t>(C) & 7) == 0 && (ldc % 2 == 0) && (p.stride_c % 2 == 0);
+    if (big) {
+        // Interior tiles take the direct-to-LDS kernel when the operands are
+        // 16-byte loadable, K is a whole number of 64-deep blocks (the split
+        // boundaries of both kernels then agree) and each operand's extent
+        // fits the buffer descriptor.
+        const int64_t ext_a = trans_a ? (K - 1) * lda + M : (M - 1) * lda + K;
+        const int64_t ext_b = trans_b ? (N - 1) * ldb + K : (K - 1) * ldb + N;
+        const int64_t lim = (int64_t)0x7fffffff;  // descriptor extent is passed as int
+        const bool direct = K > 0 && K % 64 == 0 && p.vec_a && p.vec_b && ext_a * esz <= lim && ext_b * esz <= lim;
+        p.a_bytes = direct ? (uint32_t)(ext_a * esz) : 0u;
+        p.b_bytes = direct ? (uint32_t)(ext_b * esz) : 0u;
+        p.int_m = direct ? (int)(M / kBigTile) : 0;
+        p.int_n = direct ? (int)(N / kBigTile) : 0;
+    }
 
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     TF_REQUIRE(tiles < (1LL << 31), "tf_gemm: too many tiles");
 
-    // Split the k blocks when the tiles leave most CUs idle and K is long.
+    // Split the k blocks when the tiles leave most CUs idle and K is long
+    // (target: two workgroups per CU, >= 4 k blocks per slice).
     const int64_t kblocks = ((K + BK - 1) / BK) * p.reduce_batch;
-    int splits = 1;
-    if (grid_batch == 1 && tiles * 2 <= ctx->num_cus && kblocks >= 8) {
-        int64_t want = (2 * (int64_t)ctx->num_cus + tiles - 1) / tiles;  // two workgroups per CU
-        int64_t max_by_k = kblocks / 4;                                  // >= 4 k blocks per split
-        splits = (int)std::max<int64_t>(1, std::min<int64_t>({want, max_by_k, 256}));
-    }
+    if (!big && grid_batch == 1 && tiles * 2 <= ncu && kblocks >= 8) splits = choose_splits(tiles, kblocks, 2 * ncu, 4);
     if (kblocks == 0) {
         splits = 1;
         p.kb_per_split = 0;
@@ -584,12 +1289,34 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
         p.partial = reinterpret_cast<float*>(ctx->ws);
     }
 
-    KernelFn fn = in_dtype == TF_F32 ? (BN == 128 ? pick_f32<128>(a_kmaj, b_kmaj) : pick_f32<64>(a_kmaj, b_kmaj))
-                                     : (BN == 128 ? pick_bf16<128>(a_kmaj, b_kmaj) : pick_bf16<64>(a_kmaj, b_kmaj));
-    dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)grid_batch);
-    fn<<<grid, kThreads, 0, ctx->stream>>>(p);
-    tf_status st = tfh::check_launch("gemm kernel");
-    if (st != TF_OK) return st;
+    tf_status st = TF_OK;
+    if (big) {
+        // Interior tiles: direct-to-LDS kernel over an int_m x int_n grid;
+        // the remaining edge tiles (or all tiles): the guarded kernel.
+        const int64_t n_int = (int64_t)p.int_m * p.int_n;
+        if (n_int > 0) {
+            GemmParams q = p;
+            q.tiles_m = p.int_m;
+            q.tiles_n = p.int_n;
+            dim3 grid((unsigned)n_int, (unsigned)splits, (unsigned)grid_batch);
+            pick_bf16_dl(a_kmaj, b_kmaj)<<<grid, kThreads, 0, ctx->stream>>>(q);
+            st = tfh::check_launch("gemm_bf16_dl_kernel");
+            if (st != TF_OK) return st;
+        }
+        if (tiles - n_int > 0) {
+            dim3 grid((unsigned)(tiles - n_int), (unsigned)splits, (unsigned)grid_batch);
+            pick_bf16_big(a_kmaj, b_kmaj)<<<grid, kThreads, 0, ctx->stream>>>(p);
+            st = tfh::check_launch("gemm_bf16_big_kernel");
+            if (st != TF_OK) return st;
+        }
+    } else {
+        KernelFn fn = in_dtype == TF_F32 ? (BN == 128 ? pick_f32<128>(a_kmaj, b_kmaj) : pick_f32<64>(a_kmaj, b_kmaj))
+                                         : (BN == 128 ? pick_bf16<128>(a_kmaj, b_kmaj) : pick_bf16<64>(a_kmaj, b_kmaj));
+        dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)grid_batch);
+        fn<<<grid, kThreads, 0, ctx->stream>>>(p);
+        st = tfh::check_launch("gemm kernel");
+        if (st != TF_OK) return st;
+    }
     if (splits > 1) {
         splitk_reduce_kernel<<<tfd::grid_for(M * N, 4), 256, 0, ctx->stream>>>(p, splits);
         st = tfh::check_launch("splitk_reduce_kernel");

@@ -160,6 +160,45 @@ def test_gemm_bf16_fp32_accumulate(ctx, ta, tb):
     assert_close(ta_mod.bf16_bits_to_f32(dc16.numpy()), truth, RTOL16, "bf16 in / bf16 out")
 
 
+# Shapes that select the 256 x 256 bf16 kernel: all-interior tiles; ragged
+# M/N edges with K a multiple of 64 (interior + guarded tiles in one grid);
+# ragged K (every tile guarded); few tiles with K split over 4 slices.
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 384), (4000, 4100, 256), (3900, 4352, 200), (2048, 2048, 2048)])
+def test_gemm_bf16_large_tile(ctx, ta, tb, M, N, K):
+    import tensors_amd as ta_mod
+    from tensors_amd import ops
+    seed = synth.seed(2, 9) + M + N + K
+    a16 = ta_mod.f32_to_bf16_bits(synth.normal(seed, (K, M) if ta else (M, K)))
+    b16 = ta_mod.f32_to_bf16_bits(synth.normal(seed + 1, (N, K) if tb else (K, N)))
+    truth = _gemm_truth(ta_mod.bf16_bits_to_f32(a16), ta_mod.bf16_bits_to_f32(b16), ta, tb)
+    da, db = ctx.array(a16, ta_mod.BF16), ctx.array(b16, ta_mod.BF16)
+    dc = ctx.zeros((M, N), np.float32)
+    ops.gemm(da, db, dc, trans_a=ta, trans_b=tb)
+    assert_close(dc.numpy(), truth, RTOL32, f"bf16 256-tile ta={ta} tb={tb} {M}x{N}x{K}")
+
+
+def test_gemm_bf16_large_tile_epilogues(ctx):
+    import tensors_amd as ta_mod
+    from tensors_amd import ops
+    M, N, K = 4096, 4000, 320
+    a16 = ta_mod.f32_to_bf16_bits(synth.normal(71, (M, K)))
+    b16 = ta_mod.f32_to_bf16_bits(synth.normal(72, (N, K)))
+    a, b = ta_mod.bf16_bits_to_f32(a16), ta_mod.bf16_bits_to_f32(b16)
+    bias = synth.normal(73, (N,))
+    c0 = synth.normal(74, (M, N))
+    da, db, dbias = ctx.array(a16, ta_mod.BF16), ctx.array(b16, ta_mod.BF16), ctx.array(bias)
+    # bf16 output with bias + ReLU (Linear forward in bf16 compute)
+    dc16 = ctx.zeros((M, N), ta_mod.BF16)
+    ops.gemm(da, db, dc16, trans_a=False, trans_b=True, bias=dbias, relu=True)
+    truth = _gemm_truth(a, b, False, True, bias=bias, relu=True)
+    assert_close(ta_mod.bf16_bits_to_f32(dc16.numpy()), truth, RTOL16, "bf16 out, bias+relu")
+    # fp32 output with alpha / beta
+    dc = ctx.array(c0)
+    ops.gemm(da, db, dc, trans_a=False, trans_b=True, alpha=0.5, beta=0.25)
+    assert_close(dc.numpy(), _gemm_truth(a, b, False, True, 0.5, 0.25, c0), RTOL32, "alpha/beta")
+
+
 def test_gemm_strided_batched(ctx):
     from tensors_amd._lib import TF_F32, call
     B, M, N, K = 5, 33, 47, 29
