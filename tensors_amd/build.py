@@ -37,7 +37,7 @@ HIP_FLAGS = [
     # Private arrays stay in registers or scratch; never silently in LDS (the
     # GEMM kernels size their LDS to one workgroup per CU).
     "-mllvm", "-disable-promote-alloca-to-lds",
-    "-Wno-unused-command-line-argument",
+    "-Wno-unused-command-line-argument", "-Wno-inline-asm",
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 

@@ -70,7 +70,7 @@ struct GemmParams {
     int vec_a, vec_b;      // 16-byte vector loads legal for A / B
     int pair_c;            // 8-byte paired stores legal for C
     uint32_t a_bytes, b_bytes;  // byte extent of one batch element of A / B (buffer loads)
-    int int_m, int_n;           // large-tile path: tile rows / columns covered by the interior kernel
+    int int_m, int_n;           // large-tile path: tile rows / columns covered by the direct kernel
 };
 
 // Remap a linear workgroup id so that the ids one XCD receives (id % 8 == x)
@@ -1087,7 +1087,7 @@ void gemm_bf16_dl_kernel(GemmParams p) {
         });
         __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // drain the clamped loads before the waves end
     }
-    big_epilogue<false>(p, acc, m0, n0, split, batch);
+    big_epilogue<true>(p, acc, m0, n0, split, batch);
 }
 
 // Edge-tile kernel (or every tile when the direct path does not apply):
@@ -1262,8 +1262,15 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
         const bool direct = K > 0 && K % 64 == 0 && p.vec_a && p.vec_b && ext_a * esz <= lim && ext_b * esz <= lim;
         p.a_bytes = direct ? (uint32_t)(ext_a * esz) : 0u;
         p.b_bytes = direct ? (uint32_t)(ext_b * esz) : 0u;
-        p.int_m = direct ? (int)(M / kBigTile) : 0;
-        p.int_n = direct ? (int)(N / kBigTile) : 0;
+        // Partial tiles at the M / N edges are fine for the direct kernel:
+        // rows past an operand's extent read as zero (buffer range check),
+        // rows past M or N inside it only feed outputs that are not stored.
+        // An MN-major operand needs its row count a multiple of 8 for that,
+        // so no 16-byte load straddles the end of its extent.
+        const bool part_m = trans_a == 0 || M % 8 == 0;
+        const bool part_n = trans_b != 0 || N % 8 == 0;
+        p.int_m = direct ? (int)(part_m ? (M + kBigTile - 1) / kBigTile : M / kBigTile) : 0;
+        p.int_n = direct ? (int)(part_n ? (N + kBigTile - 1) / kBigTile : N / kBigTile) : 0;
     }
 
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
@@ -1291,8 +1298,8 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
 
     tf_status st = TF_OK;
     if (big) {
-        // Interior tiles: direct-to-LDS kernel over an int_m x int_n grid;
-        // the remaining edge tiles (or all tiles): the guarded kernel.
+        // Direct-to-LDS kernel over an int_m x int_n grid of tiles; the
+        // remaining edge tiles (or all tiles): the guarded kernel.
         const int64_t n_int = (int64_t)p.int_m * p.int_n;
         if (n_int > 0) {
             GemmParams q = p;

@@ -164,7 +164,8 @@ def test_gemm_bf16_fp32_accumulate(ctx, ta, tb):
 # M/N edges with K a multiple of 64 (interior + guarded tiles in one grid);
 # ragged K (every tile guarded); few tiles with K split over 4 slices.
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
-@pytest.mark.parametrize("M,N,K", [(4096, 4096, 384), (4000, 4100, 256), (3900, 4352, 200), (2048, 2048, 2048)])
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 384), (4000, 4100, 256), (3900, 4352, 200), (2048, 2048, 2048),
+                                   (2048, 1000, 4096)])
 def test_gemm_bf16_large_tile(ctx, ta, tb, M, N, K):
     import tensors_amd as ta_mod
     from tensors_amd import ops
