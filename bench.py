@@ -230,14 +230,49 @@ def cpu_baseline_c2():
     }
 
 
+TRAFFIC_JSON = ROOT / "profiles" / "gemm_f32_c2_traffic.json"
+PROBE_CAL_N = 1 << 26      # calibration tf_add: reads 2 x 256 MB, writes 256 MB
+
+
 def load_traffic(name: str):
-    p = ROOT / "profiles" / "traffic.json"
-    if not p.exists():
+    """Calibrated HBM bytes per launch from the committed counter summary
+    (tensors_amd.profiling traffic), or None when it is absent."""
+    if not TRAFFIC_JSON.exists():
         return None
     try:
-        return json.loads(p.read_text()).get(name)
+        return json.loads(TRAFFIC_JSON.read_text()).get(name)
     except Exception:
         return None
+
+
+def probe(steps: int = 5) -> None:
+    """Launches for rocprofv3 counter runs: `steps` C2 steps (fwd GEMM, dX,
+    dW, colsum, SGD) and 3 calibration tf_add launches over PROBE_CAL_N
+    floats whose traffic is known.  No timing, no output but one line."""
+    import tensors_amd as ta
+    from tensors_amd import ops, synth
+
+    ctx = ta.Context(0)
+    X = ctx.array(synth.normal(synth.seed(2, 0), (N2, N2)))
+    W = ctx.array(synth.normal(synth.seed(2, 1), (N2, N2)))
+    dY = ctx.array(synth.normal(synth.seed(2, 2), (N2, N2)))
+    b = ctx.array(synth.normal(synth.seed(2, 3), (N2,)))
+    Y, dX, dW, db = ctx.empty((N2, N2)), ctx.empty((N2, N2)), ctx.empty((N2, N2)), ctx.empty((N2,))
+    vW, vb = ctx.zeros((N2, N2)), ctx.zeros((N2,))
+    for _ in range(steps):
+        ops.gemm(X, W, Y, trans_b=True, bias=b)
+        ops.gemm(dY, W, dX)
+        ops.gemm(dY, X, dW, trans_a=True)
+        ops.colsum(dY, db)
+        ops.sgd_momentum(W, dW, vW, 1e-3, 0.9)
+        ops.sgd_momentum(b, db, vb, 1e-3, 0.9)
+    ctx.sync()
+    ca, cb, cc = ctx.zeros((PROBE_CAL_N,)), ctx.zeros((PROBE_CAL_N,)), ctx.empty((PROBE_CAL_N,))
+    for _ in range(3):
+        ops.add(ca, cb, cc)
+    ctx.sync()
+    ctx.close()
+    print(f"probe: {steps} C2 steps, 3 calibration launches", flush=True)
 
 
 def main(argv=None):
@@ -247,7 +282,11 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-c2", action="store_true", help="skip the other configurations' measurements")
+    ap.add_argument("--probe", action="store_true", help="launch the C2 kernels for a profiler, then exit")
     args = ap.parse_args(argv)
+    if args.probe:
+        probe()
+        return 0
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
