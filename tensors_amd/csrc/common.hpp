@@ -31,6 +31,10 @@ tf_status hip_error(hipError_t e, const char* what);
 
 // Make sure ctx->ws holds at least `bytes`; returns TF_OK or an error.
 tf_status ensure_workspace(tf_ctx* ctx, size_t bytes);
+// out[j] = sum_k part[k * W + j] (fixed order) for j < W; columns j < split
+// go to out_lo[j], the rest to out_hi[j - split].  Launched on ctx->stream.
+tf_status partial_rows_sum(tf_ctx* ctx, const float* part, float* out_lo, float* out_hi, int64_t K, int64_t W,
+                           int64_t split);
 
 inline bool bad_ctx(tf_ctx* ctx) { return ctx == nullptr || ctx->stream == nullptr; }
 

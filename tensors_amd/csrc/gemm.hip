@@ -1163,6 +1163,40 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
     }
 }
 
+// Split-K reduction for many splits (>= 16) and small outputs: a block owns
+// 16 consecutive output elements (flat index row * N + col) x 16 split
+// groups; each thread adds splits g, g + 16, ... in ascending order with its
+// loads in flight together, and the 16 group sums are combined in a fixed
+// tree order before the epilogue (deterministic).
+__global__ __launch_bounds__(256) void splitk_reduce_wide_kernel(GemmParams p, int splits) {
+    __shared__ float red[16][17];
+    const int el = threadIdx.x & 15, g = threadIdx.x >> 4;
+    const int64_t plane = (int64_t)p.M * p.N;
+    const int64_t i = (int64_t)blockIdx.x * 16 + el;
+    float s = 0.0f;
+    if (i < plane) {
+#pragma unroll 8
+        for (int k = g; k < splits; k += 16) s += p.partial[k * plane + i];
+    }
+    red[g][el] = s;
+    __syncthreads();
+    if (threadIdx.x >= 16 || i >= plane) return;
+    float t[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) t[q] = red[2 * q][el] + red[2 * q + 1][el];
+    const float sum = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+    const int row = (int)(i / p.N), col = (int)(i - (int64_t)row * p.N);
+    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU || p.epi == TF_EPI_ROW_BIAS_RELU;
+    const bool has_bias = p.epi != TF_EPI_NONE && p.epi != TF_EPI_RELU;
+    const int64_t off = (int64_t)row * p.ldc + col;
+    float v = p.alpha * sum;
+    if (p.beta != 0.0f) v += p.beta * reinterpret_cast<const float*>(p.C)[off];
+    if (has_bias) v += p.row_bias ? p.bias[row] : p.bias[col];
+    if (relu) v = fmaxf(v, 0.0f);
+    if (p.out_bf16) reinterpret_cast<uint16_t*>(p.C)[off] = tfd::f32_to_bf16(v);
+    else reinterpret_cast<float*>(p.C)[off] = v;
+}
+
 using KernelFn = void (*)(GemmParams);
 
 template <int BN>
@@ -1341,8 +1375,12 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
         if (st != TF_OK) return st;
     }
     if (splits > 1) {
-        dim3 rgrid((unsigned)((N + 1023) / 1024), (unsigned)std::min<int64_t>(M, 65535));
-        splitk_reduce_kernel<<<rgrid, 256, 0, ctx->stream>>>(p, splits);
+        if (splits >= 16) {
+            splitk_reduce_wide_kernel<<<(unsigned)((M * N + 15) / 16), 256, 0, ctx->stream>>>(p, splits);
+        } else {
+            dim3 rgrid((unsigned)((N + 1023) / 1024), (unsigned)std::min<int64_t>(M, 65535));
+            splitk_reduce_kernel<<<rgrid, 256, 0, ctx->stream>>>(p, splits);
+        }
         st = tfh::check_launch("splitk_reduce_kernel");
     }
     return st;

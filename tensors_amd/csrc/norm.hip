@@ -13,8 +13,8 @@
 //
 // Rows of up to 2048 columns: one fused pass (one wave per row, the row held
 // in registers; each wave also accumulates its rows' dgamma/dbeta column
-// partials, combined per block in LDS and then across blocks by a second,
-// fixed-order kernel).  Wider rows: a streaming row kernel for dx and a
+// partials, combined per block in LDS and then across blocks by the shared
+// fixed-order reduction tfh::partial_rows_sum).  Wider rows: a streaming row kernel for dx and a
 // column kernel for dgamma/dbeta.
 #include "common.hpp"
 
@@ -279,27 +279,6 @@ __global__ __launch_bounds__(256) void ln_bwd_cols_kernel(const float* __restric
     }
 }
 
-// out_g[j] = sum_b part[b][0][j], out_b[j] = sum_b part[b][1][j] (fixed order).
-__global__ __launch_bounds__(256) void ln_partials_kernel(const float* __restrict__ part, float* __restrict__ dgamma,
-                                                          float* __restrict__ dbeta, int nparts, int cols) {
-    __shared__ float red[4][2][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int j = blockIdx.x * 64 + lane;
-    float g = 0.0f, b = 0.0f;
-    if (j < cols)
-        for (int k = wave; k < nparts; k += 4) {
-            g += part[(int64_t)k * 2 * cols + j];
-            b += part[(int64_t)k * 2 * cols + cols + j];
-        }
-    red[wave][0][lane] = g;
-    red[wave][1][lane] = b;
-    __syncthreads();
-    if (wave == 0 && j < cols) {
-        dgamma[j] = (red[0][0][lane] + red[1][0][lane]) + (red[2][0][lane] + red[3][0][lane]);
-        dbeta[j] = (red[0][1][lane] + red[1][1][lane]) + (red[2][1][lane] + red[3][1][lane]);
-    }
-}
-
 // Reference-compatible stub: dx = dy * gamma[col].
 __global__ void ln_bwd_stub_kernel(const float* __restrict__ dy, const float* __restrict__ gamma,
                                    float* __restrict__ dx, int64_t n, int cols) {
@@ -387,8 +366,8 @@ tf_status tf_layernorm_bwd(tf_ctx* ctx, const float* dy, const float* x, const f
 #undef TF_LN_BWD
         st = tfh::check_launch("ln_bwd_fused_kernel");
         if (st != TF_OK) return st;
-        ln_partials_kernel<<<(unsigned)((cols + 63) / 64), 256, 0, ctx->stream>>>(part, dgamma, dbeta, (int)nblocks, (int)cols);
-        return tfh::check_launch("ln_partials_kernel");
+        // part is [nblocks][dgamma cols | dbeta cols]: one [K][2 cols] reduction.
+        return tfh::partial_rows_sum(ctx, part, dgamma, dbeta, nblocks, 2 * cols, cols);
     }
     ln_bwd_dx_stream_kernel<<<row_grid(rows), 256, 0, ctx->stream>>>(dy, x, gamma, mean, rstd, dx, (int)rows, (int)cols);
     tf_status st = tfh::check_launch("ln_bwd_dx_stream_kernel");
@@ -404,8 +383,7 @@ tf_status tf_layernorm_bwd(tf_ctx* ctx, const float* dy, const float* x, const f
                                                                                (int)cols, rpc);
     st = tfh::check_launch("ln_bwd_cols_kernel");
     if (st != TF_OK) return st;
-    ln_partials_kernel<<<(unsigned)strips, 256, 0, ctx->stream>>>(part, dgamma, dbeta, (int)chunks, (int)cols);
-    return tfh::check_launch("ln_partials_kernel");
+    return tfh::partial_rows_sum(ctx, part, dgamma, dbeta, chunks, 2 * cols, cols);
 }
 
 }  // extern "C"

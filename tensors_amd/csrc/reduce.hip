@@ -2,7 +2,8 @@
 //   colsum : db[c] = sum_r dy[r, c]           (Linear bias grad)
 //   chansum: db[c] = sum_{n,p} dy[n, c, p]    (Conv2d bias grad, NCHW)
 // Stage 1 writes per-chunk partial sums to the context workspace, stage 2
-// adds the partials in ascending chunk order.  The reference's conv kernel
+// (tfh::partial_rows_sum, also used by the LayerNorm backward) adds them in a
+// fixed order.  The reference's conv kernel
 // lets every block overwrite out[c] with its own partial
 // (cuda/kernels/reduce_sum_axis.cu:60-97); this one reduces all of them.
 #include "common.hpp"
@@ -24,6 +25,7 @@ __global__ __launch_bounds__(256) void colsum_stage1(const float* __restrict__ d
     const int r1 = min(rows, r0 + rows_per_chunk);
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     if (vec && c0 + 4 <= cols) {
+#pragma unroll 4
         for (int r = r0 + wave; r < r1; r += 4) {
             float4 v = *reinterpret_cast<const float4*>(dy + (int64_t)r * cols + c0);
             acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
@@ -51,20 +53,33 @@ __global__ __launch_bounds__(256) void colsum_stage1(const float* __restrict__ d
     }
 }
 
-// Stage 2 (shared by colsum and chansum): out[c] = sum_k part[k, c].  A block
-// owns 64 columns; its 4 waves take chunks k = w, w + 4, ... and LDS adds the
-// four wave sums in a fixed order.
-__global__ __launch_bounds__(256) void partial_sum_stage2(const float* __restrict__ part, float* __restrict__ out,
-                                                          int chunks, int cols) {
-    __shared__ float red[4][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int c = blockIdx.x * 64 + lane;
+// Stage 2 of every two-stage reduction here (colsum, chansum, LayerNorm
+// dgamma/dbeta): out[j] = sum_k part[k][j] over a [K][W] partial matrix, the
+// first `split` columns to out_lo, the rest to out_hi.  A block owns 16
+// columns; its 256 threads are 16 columns x 16 k-groups (a group of 16 lanes
+// reads 64 contiguous bytes of one partial row), each thread adds k = g,
+// g + 16, ... in ascending order with its loads in flight together, and the
+// 16 group sums are added in a fixed tree order (deterministic).
+__global__ __launch_bounds__(256) void partial_rows_sum_kernel(const float* __restrict__ part, float* __restrict__ out_lo,
+                                                           float* __restrict__ out_hi, int K, int W, int split) {
+    __shared__ float red[16][17];
+    const int cl = threadIdx.x & 15, kg = threadIdx.x >> 4;
+    const int j = blockIdx.x * 16 + cl;
     float s = 0.0f;
-    if (c < cols)
-        for (int k = wave; k < chunks; k += 4) s += part[(int64_t)k * cols + c];
-    red[wave][lane] = s;
+    if (j < W) {
+#pragma unroll 8
+        for (int k = kg; k < K; k += 16) s += part[(int64_t)k * W + j];
+    }
+    red[kg][cl] = s;
     __syncthreads();
-    if (wave == 0 && c < cols) out[c] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+    if (threadIdx.x < 16 && j < W) {
+        float t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t[i] = red[2 * i][cl] + red[2 * i + 1][cl];
+        const float v = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+        if (j < split) out_lo[j] = v;
+        else out_hi[j - split] = v;
+    }
 }
 
 // Stage 1 of chansum: block (c, chunk) sums samples [chunk*npc, ...) of
@@ -95,6 +110,18 @@ __global__ __launch_bounds__(256) void chansum_stage1(const float* __restrict__ 
 
 }  // namespace
 
+namespace tfh {
+
+tf_status partial_rows_sum(tf_ctx* ctx, const float* part, float* out_lo, float* out_hi, int64_t K, int64_t W,
+                           int64_t split) {
+    if (W == 0) return TF_OK;
+    partial_rows_sum_kernel<<<(unsigned)((W + 15) / 16), 256, 0, ctx->stream>>>(part, out_lo, out_hi, (int)K, (int)W,
+                                                                               (int)split);
+    return check_launch("partial_rows_sum_kernel");
+}
+
+}  // namespace tfh
+
 extern "C" {
 
 tf_status tf_colsum(tf_ctx* ctx, const float* dy, float* db, int64_t rows, int64_t cols) {
@@ -117,8 +144,7 @@ tf_status tf_colsum(tf_ctx* ctx, const float* dy, float* db, int64_t rows, int64
     colsum_stage1<<<dim3(strips, (unsigned)chunks), 256, 0, ctx->stream>>>(dy, part, (int)rows, (int)cols, rpc, vec);
     st = tfh::check_launch("colsum_stage1");
     if (st != TF_OK) return st;
-    partial_sum_stage2<<<(unsigned)((cols + 63) / 64), 256, 0, ctx->stream>>>(part, db, (int)chunks, (int)cols);
-    return tfh::check_launch("partial_sum_stage2");
+    return tfh::partial_rows_sum(ctx, part, db, nullptr, chunks, cols, cols);
 }
 
 tf_status tf_chansum_nchw(tf_ctx* ctx, const float* dy, float* db, int64_t N, int64_t C, int64_t HW) {
@@ -139,8 +165,7 @@ tf_status tf_chansum_nchw(tf_ctx* ctx, const float* dy, float* db, int64_t N, in
                                                                                    (int)n_per_chunk, vec);
     st = tfh::check_launch("chansum_stage1");
     if (st != TF_OK) return st;
-    partial_sum_stage2<<<(unsigned)((C + 63) / 64), 256, 0, ctx->stream>>>(part, db, (int)chunks, (int)C);
-    return tfh::check_launch("partial_sum_stage2");
+    return tfh::partial_rows_sum(ctx, part, db, nullptr, chunks, C, C);
 }
 
 }  // extern "C"
