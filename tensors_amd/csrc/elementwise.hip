@@ -26,47 +26,85 @@ template <> struct Elem<uint16_t> {
 // Number of scalars in a 16-byte vector.
 template <typename T> constexpr int kVec = 16 / sizeof(T);
 
-// Binary elementwise: out = op(a, b).  Vector body when all three pointers
-// are 16-byte aligned, scalar loop otherwise / for the tail.
+// Streaming loops: a block works on chunks of kUnroll x 256 consecutive
+// 16-byte vectors (grid-stride over chunks); each thread loads its kUnroll
+// vectors of the chunk (256 vectors apart, so each load instruction is one
+// contiguous 4 KB piece per block) before any arithmetic or store.
+constexpr int kUnroll = 4;
+constexpr int kChunk = kUnroll * 256;  // vectors per block chunk
+
 template <typename T, typename Op>
-__global__ void binary_kernel(const T* __restrict__ a, const T* __restrict__ b,
-                              T* __restrict__ out, int64_t n, Op op, int vec_ok) {
+__device__ __forceinline__ uint4 apply2(const uint4& va, const uint4& vb, Op op) {
     constexpr int V = kVec<T>;
-    int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    int64_t nv = vec_ok ? n / V : 0;
-    for (int64_t i = tid; i < nv; i += stride) {
-        uint4 va = reinterpret_cast<const uint4*>(a)[i];
-        uint4 vb = reinterpret_cast<const uint4*>(b)[i];
-        uint4 vo;
-        const T* ea = reinterpret_cast<const T*>(&va);
-        const T* eb = reinterpret_cast<const T*>(&vb);
-        T* eo = reinterpret_cast<T*>(&vo);
+    uint4 vo;
+    const T* ea = reinterpret_cast<const T*>(&va);
+    const T* eb = reinterpret_cast<const T*>(&vb);
+    T* eo = reinterpret_cast<T*>(&vo);
 #pragma unroll
-        for (int j = 0; j < V; ++j)
-            Elem<T>::st(eo, j, op(Elem<T>::ld(ea, j), Elem<T>::ld(eb, j)));
-        reinterpret_cast<uint4*>(out)[i] = vo;
-    }
-    for (int64_t i = nv * V + tid; i < n; i += stride)
-        Elem<T>::st(out, i, op(Elem<T>::ld(a, i), Elem<T>::ld(b, i)));
+    for (int j = 0; j < V; ++j) Elem<T>::st(eo, j, op(Elem<T>::ld(ea, j), Elem<T>::ld(eb, j)));
+    return vo;
 }
 
 template <typename T, typename Op>
-__global__ void unary_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t n, Op op, int vec_ok) {
+__device__ __forceinline__ uint4 apply1(const uint4& vx, Op op) {
     constexpr int V = kVec<T>;
-    int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    int64_t nv = vec_ok ? n / V : 0;
-    for (int64_t i = tid; i < nv; i += stride) {
-        uint4 vx = reinterpret_cast<const uint4*>(x)[i];
-        uint4 vo;
-        const T* ex = reinterpret_cast<const T*>(&vx);
-        T* eo = reinterpret_cast<T*>(&vo);
+    uint4 vo;
+    const T* ex = reinterpret_cast<const T*>(&vx);
+    T* eo = reinterpret_cast<T*>(&vo);
 #pragma unroll
-        for (int j = 0; j < V; ++j) Elem<T>::st(eo, j, op(Elem<T>::ld(ex, j)));
-        reinterpret_cast<uint4*>(y)[i] = vo;
+    for (int j = 0; j < V; ++j) Elem<T>::st(eo, j, op(Elem<T>::ld(ex, j)));
+    return vo;
+}
+
+// Binary elementwise: out = op(a, b).  Vector body when all three pointers
+// are 16-byte aligned, scalar loop otherwise / for the tail.
+template <typename T, typename Op>
+__global__ __launch_bounds__(256) void binary_kernel(const T* __restrict__ a, const T* __restrict__ b,
+                                                     T* __restrict__ out, int64_t n, Op op, int vec_ok) {
+    constexpr int V = kVec<T>;
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t nv = vec_ok ? n / V : 0;
+    const uint4* A = reinterpret_cast<const uint4*>(a);
+    const uint4* B = reinterpret_cast<const uint4*>(b);
+    uint4* O = reinterpret_cast<uint4*>(out);
+    const int64_t full = nv / kChunk;
+    for (int64_t c = blockIdx.x; c < full; c += gridDim.x) {
+        const int64_t i = c * kChunk + threadIdx.x;
+        uint4 va[kUnroll], vb[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            va[u] = A[i + u * 256];
+            vb[u] = B[i + u * 256];
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) O[i + u * 256] = apply2<T>(va[u], vb[u], op);
     }
-    for (int64_t i = nv * V + tid; i < n; i += stride) Elem<T>::st(y, i, op(Elem<T>::ld(x, i)));
+    for (int64_t i = full * kChunk + tid; i < nv; i += stride) O[i] = apply2<T>(A[i], B[i], op);
+    for (int64_t j = nv * V + tid; j < n; j += stride)
+        Elem<T>::st(out, j, op(Elem<T>::ld(a, j), Elem<T>::ld(b, j)));
+}
+
+template <typename T, typename Op>
+__global__ __launch_bounds__(256) void unary_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t n, Op op,
+                                                    int vec_ok) {
+    constexpr int V = kVec<T>;
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t nv = vec_ok ? n / V : 0;
+    const uint4* X = reinterpret_cast<const uint4*>(x);
+    uint4* Y = reinterpret_cast<uint4*>(y);
+    const int64_t full = nv / kChunk;
+    for (int64_t c = blockIdx.x; c < full; c += gridDim.x) {
+        const int64_t i = c * kChunk + threadIdx.x;
+        uint4 vx[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) vx[u] = X[i + u * 256];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) Y[i + u * 256] = apply1<T>(vx[u], op);
+    }
+    for (int64_t i = full * kChunk + tid; i < nv; i += stride) Y[i] = apply1<T>(X[i], op);
+    for (int64_t j = nv * V + tid; j < n; j += stride) Elem<T>::st(y, j, op(Elem<T>::ld(x, j)));
 }
 
 // Operators.  The backward ones reproduce the reference's arithmetic order:
@@ -101,10 +139,10 @@ tf_status launch_binary(tf_ctx* ctx, const void* a, const void* b, void* out, in
     TF_REQUIRE(a && b && out, "null pointer");
     int vec_ok = aligned16<char>(a) && aligned16<char>(b) && aligned16<char>(out);
     if (dtype == TF_F32) {
-        binary_kernel<float, Op><<<tfd::grid_for(n, 4 * 4), 256, 0, ctx->stream>>>(
+        binary_kernel<float, Op><<<tfd::grid_for(n, 4 * kUnroll), 256, 0, ctx->stream>>>(
             (const float*)a, (const float*)b, (float*)out, n, op, vec_ok);
     } else if (dtype == TF_BF16) {
-        binary_kernel<uint16_t, Op><<<tfd::grid_for(n, 8 * 4), 256, 0, ctx->stream>>>(
+        binary_kernel<uint16_t, Op><<<tfd::grid_for(n, 8 * kUnroll), 256, 0, ctx->stream>>>(
             (const uint16_t*)a, (const uint16_t*)b, (uint16_t*)out, n, op, vec_ok);
     } else {
         return tfh::set_error(TF_ERR_UNSUPPORTED, std::string(name) + ": dtype must be Float32 or BFloat16");
@@ -120,10 +158,10 @@ tf_status launch_unary(tf_ctx* ctx, const void* x, void* y, int64_t n, int dtype
     TF_REQUIRE(x && y, "null pointer");
     int vec_ok = aligned16<char>(x) && aligned16<char>(y);
     if (dtype == TF_F32) {
-        unary_kernel<float, Op><<<tfd::grid_for(n, 4 * 4), 256, 0, ctx->stream>>>(
+        unary_kernel<float, Op><<<tfd::grid_for(n, 4 * kUnroll), 256, 0, ctx->stream>>>(
             (const float*)x, (float*)y, n, op, vec_ok);
     } else if (dtype == TF_BF16) {
-        unary_kernel<uint16_t, Op><<<tfd::grid_for(n, 8 * 4), 256, 0, ctx->stream>>>(
+        unary_kernel<uint16_t, Op><<<tfd::grid_for(n, 8 * kUnroll), 256, 0, ctx->stream>>>(
             (const uint16_t*)x, (uint16_t*)y, n, op, vec_ok);
     } else {
         return tfh::set_error(TF_ERR_UNSUPPORTED, std::string(name) + ": dtype must be Float32 or BFloat16");
@@ -144,74 +182,121 @@ __global__ void scale_by_kernel(const float* __restrict__ a, const float* __rest
 // (20 B/param; +2 B with the bf16 shadow).  Contraction is disabled so the
 // update rounds exactly like the host loop v*mu + g, p - v*lr (two roundings
 // each), the order of nn/optim/SGD.cpp:50-54.
-__global__ void sgd_momentum_kernel(float* __restrict__ p, const float* __restrict__ g,
-                                    float* __restrict__ v, uint16_t* __restrict__ p_bf16,
-                                    int64_t n, float lr, float mu, int vec_ok) {
+__device__ __forceinline__ void sgd4(float4& pp, const float4& gg, float4& vv, bool use_v, float lr, float mu) {
 #pragma clang fp contract(off)
-    int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    int64_t nv = vec_ok ? n / 4 : 0;
-    const bool use_v = mu != 0.0f;
-    for (int64_t i = tid; i < nv; i += stride) {
-        float4 pp = reinterpret_cast<float4*>(p)[i];
-        float4 gg = reinterpret_cast<const float4*>(g)[i];
-        float* pe = reinterpret_cast<float*>(&pp);
-        const float* ge = reinterpret_cast<const float*>(&gg);
+    float* pe = reinterpret_cast<float*>(&pp);
+    const float* ge = reinterpret_cast<const float*>(&gg);
+    float* ve = reinterpret_cast<float*>(&vv);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
         if (use_v) {
-            float4 vv = reinterpret_cast<float4*>(v)[i];
-            float* ve = reinterpret_cast<float*>(&vv);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float vm = ve[j] * mu;
-                ve[j] = vm + ge[j];
-                float step = ve[j] * lr;
-                pe[j] = pe[j] - step;
-            }
-            reinterpret_cast<float4*>(v)[i] = vv;
+            const float vm = ve[j] * mu;
+            ve[j] = vm + ge[j];
+            const float step = ve[j] * lr;
+            pe[j] = pe[j] - step;
         } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float step = lr * ge[j];
-                pe[j] = pe[j] - step;
-            }
-        }
-        reinterpret_cast<float4*>(p)[i] = pp;
-        if (p_bf16) {
-            ushort4 h;
-            h.x = f32_to_bf16(pe[0]);
-            h.y = f32_to_bf16(pe[1]);
-            h.z = f32_to_bf16(pe[2]);
-            h.w = f32_to_bf16(pe[3]);
-            reinterpret_cast<ushort4*>(p_bf16)[i] = h;
+            const float step = lr * ge[j];
+            pe[j] = pe[j] - step;
         }
     }
-    for (int64_t i = nv * 4 + tid; i < n; i += stride) {
-        float pv = p[i];
+}
+
+__global__ __launch_bounds__(256) void sgd_momentum_kernel(float* __restrict__ p, const float* __restrict__ g,
+                                                           float* __restrict__ v, uint16_t* __restrict__ p_bf16,
+                                                           int64_t n, float lr, float mu, int vec_ok) {
+#pragma clang fp contract(off)
+    constexpr int U = 2;  // iterations in flight (3 input streams)
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t nv = vec_ok ? n / 4 : 0;
+    const bool use_v = mu != 0.0f;
+    float4* P = reinterpret_cast<float4*>(p);
+    const float4* G = reinterpret_cast<const float4*>(g);
+    float4* Vv = reinterpret_cast<float4*>(v);
+    auto finish = [&](int64_t i, float4& pp, float4& vv) {
+        P[i] = pp;
+        if (use_v) Vv[i] = vv;
+        if (p_bf16) {
+            ushort4 h;
+            h.x = f32_to_bf16(pp.x);
+            h.y = f32_to_bf16(pp.y);
+            h.z = f32_to_bf16(pp.z);
+            h.w = f32_to_bf16(pp.w);
+            reinterpret_cast<ushort4*>(p_bf16)[i] = h;
+        }
+    };
+    const int64_t full = nv / (U * 256);
+    for (int64_t c = blockIdx.x; c < full; c += gridDim.x) {
+        const int64_t i = c * (U * 256) + threadIdx.x;
+        float4 pp[U], gg[U], vv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            pp[u] = P[i + u * 256];
+            gg[u] = G[i + u * 256];
+            vv[u] = use_v ? Vv[i + u * 256] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            sgd4(pp[u], gg[u], vv[u], use_v, lr, mu);
+            finish(i + u * 256, pp[u], vv[u]);
+        }
+    }
+    for (int64_t i = full * (U * 256) + tid; i < nv; i += stride) {
+        float4 pp = P[i], gg = G[i], vv = use_v ? Vv[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        sgd4(pp, gg, vv, use_v, lr, mu);
+        finish(i, pp, vv);
+    }
+    for (int64_t j = nv * 4 + tid; j < n; j += stride) {
+        float pv = p[j];
         if (use_v) {
-            float vm = v[i] * mu;
-            float vn = vm + g[i];
-            v[i] = vn;
+            float vm = v[j] * mu;
+            float vn = vm + g[j];
+            v[j] = vn;
             float step = vn * lr;
             pv = pv - step;
         } else {
-            float step = lr * g[i];
+            float step = lr * g[j];
             pv = pv - step;
         }
-        p[i] = pv;
-        if (p_bf16) p_bf16[i] = f32_to_bf16(pv);
+        p[j] = pv;
+        if (p_bf16) p_bf16[j] = f32_to_bf16(pv);
     }
 }
 
-__global__ void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, int64_t n) {
-    int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = tid; i < n; i += stride) y[i] = f32_to_bf16(x[i]);
+// Casts: 8 elements per iteration (two float4 <-> one 16-byte bf16 vector)
+// when both pointers are 16-byte aligned; scalar for the rest.
+__global__ __launch_bounds__(256) void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y,
+                                                            int64_t n, int vec_ok) {
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t nv = vec_ok ? n / 8 : 0;
+    for (int64_t i = tid; i < nv; i += stride) {
+        const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
+        const float4 b = reinterpret_cast<const float4*>(x)[2 * i + 1];
+        uint4 o;
+        o.x = (uint32_t)f32_to_bf16(a.x) | ((uint32_t)f32_to_bf16(a.y) << 16);
+        o.y = (uint32_t)f32_to_bf16(a.z) | ((uint32_t)f32_to_bf16(a.w) << 16);
+        o.z = (uint32_t)f32_to_bf16(b.x) | ((uint32_t)f32_to_bf16(b.y) << 16);
+        o.w = (uint32_t)f32_to_bf16(b.z) | ((uint32_t)f32_to_bf16(b.w) << 16);
+        reinterpret_cast<uint4*>(y)[i] = o;
+    }
+    for (int64_t j = nv * 8 + tid; j < n; j += stride) y[j] = f32_to_bf16(x[j]);
 }
 
-__global__ void cast_bf16_f32_kernel(const uint16_t* __restrict__ x, float* __restrict__ y, int64_t n) {
-    int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = tid; i < n; i += stride) y[i] = bf16_to_f32(x[i]);
+__global__ __launch_bounds__(256) void cast_bf16_f32_kernel(const uint16_t* __restrict__ x, float* __restrict__ y,
+                                                            int64_t n, int vec_ok) {
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t nv = vec_ok ? n / 8 : 0;
+    for (int64_t i = tid; i < nv; i += stride) {
+        const uint4 h = reinterpret_cast<const uint4*>(x)[i];
+        reinterpret_cast<float4*>(y)[2 * i] = make_float4(bf16_to_f32((uint16_t)h.x), bf16_to_f32((uint16_t)(h.x >> 16)),
+                                                          bf16_to_f32((uint16_t)h.y), bf16_to_f32((uint16_t)(h.y >> 16)));
+        reinterpret_cast<float4*>(y)[2 * i + 1] =
+            make_float4(bf16_to_f32((uint16_t)h.z), bf16_to_f32((uint16_t)(h.z >> 16)), bf16_to_f32((uint16_t)h.w),
+                        bf16_to_f32((uint16_t)(h.w >> 16)));
+    }
+    for (int64_t j = nv * 8 + tid; j < n; j += stride) y[j] = bf16_to_f32(x[j]);
 }
 
 }  // namespace
@@ -266,7 +351,7 @@ tf_status tf_sgd_momentum(tf_ctx* ctx, float* p, const float* g, float* v, void*
     TF_REQUIRE(mu >= 0.0f && mu < 1.0f, "tf_sgd_momentum: momentum must lie in [0, 1)");
     int vec_ok = aligned16<char>(p) && aligned16<char>(g) && (v == nullptr || aligned16<char>(v)) &&
                  (p_bf16 == nullptr || (reinterpret_cast<uintptr_t>(p_bf16) & 7) == 0);
-    sgd_momentum_kernel<<<tfd::grid_for(n, 4 * 4), 256, 0, ctx->stream>>>(
+    sgd_momentum_kernel<<<tfd::grid_for(n, 4 * 2), 256, 0, ctx->stream>>>(
         p, g, v, (uint16_t*)p_bf16, n, lr, mu, vec_ok);
     return tfh::check_launch("sgd_momentum_kernel");
 }
@@ -275,7 +360,8 @@ tf_status tf_cast_f32_bf16(tf_ctx* ctx, const float* x, void* y, int64_t n) {
     TF_CTX_CHECK(ctx);
     if (n == 0) return TF_OK;
     TF_REQUIRE(x && y && n > 0, "tf_cast_f32_bf16: bad argument");
-    cast_f32_bf16_kernel<<<tfd::grid_for(n, 4), 256, 0, ctx->stream>>>(x, (uint16_t*)y, n);
+    cast_f32_bf16_kernel<<<tfd::grid_for(n, 8), 256, 0, ctx->stream>>>(x, (uint16_t*)y, n,
+                                                                       aligned16<char>(x) && aligned16<char>(y));
     return tfh::check_launch("cast_f32_bf16_kernel");
 }
 
@@ -283,7 +369,8 @@ tf_status tf_cast_bf16_f32(tf_ctx* ctx, const void* x, float* y, int64_t n) {
     TF_CTX_CHECK(ctx);
     if (n == 0) return TF_OK;
     TF_REQUIRE(x && y && n > 0, "tf_cast_bf16_f32: bad argument");
-    cast_bf16_f32_kernel<<<tfd::grid_for(n, 4), 256, 0, ctx->stream>>>((const uint16_t*)x, y, n);
+    cast_bf16_f32_kernel<<<tfd::grid_for(n, 8), 256, 0, ctx->stream>>>((const uint16_t*)x, y, n,
+                                                                       aligned16<char>(x) && aligned16<char>(y));
     return tfh::check_launch("cast_bf16_f32_kernel");
 }
 

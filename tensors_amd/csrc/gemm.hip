@@ -237,126 +237,6 @@ __device__ __forceinline__ void store_wave(const GemmParams& p, const v16f (&acc
 }
 
 // ---------------------------------------------------------------------------
-// fp32 kernel: BK = 32, v_mfma_f32_32x32x2_f32.  Lane half h feeds k = 16h + s
-// to the s-th MFMA of a k block.
-// ---------------------------------------------------------------------------
-template <int BN, bool A_KMAJ, bool B_KMAJ>
-__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
-    constexpr int BK = 32;
-    constexpr int WN = BN / 2;
-    constexpr int NSUB = WN / 32;
-    constexpr bool A_PAIR = !A_KMAJ;
-    constexpr bool B_PAIR = !B_KMAJ && NSUB == 2;
-    using SA = Stage<float, BM, BK, A_KMAJ>;
-    using SB = Stage<float, BN, BK, B_KMAJ>;
-    __shared__ __attribute__((aligned(16))) float lds_a[2][SA::LDS_ELEMS];
-    __shared__ __attribute__((aligned(16))) float lds_b[2][SB::LDS_ELEMS];
-
-    int tm, tn;
-    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-    const int split = blockIdx.y;
-    const int batch = blockIdx.z;
-    const float* A = reinterpret_cast<const float*>(p.A) + (int64_t)batch * p.stride_a;
-    const float* B = reinterpret_cast<const float*>(p.B) + (int64_t)batch * p.stride_b;
-    const int m0 = tm * BM, n0 = tn * BN;
-    // k blocks of this split: block kb covers batch element kb / kb_per_b
-    // (only when reducing over the batch) and k range [(kb % kb_per_b) * BK, ...).
-    const int kb_per_b = (p.K + BK - 1) / BK;
-    const int kb_total = kb_per_b * p.reduce_batch;
-    const int kb_beg = split * p.kb_per_split;
-    const int nk = max(0, min(kb_total, kb_beg + p.kb_per_split) - kb_beg);
-
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int half = lane >> 5, l32 = lane & 31;
-
-    v16f acc[2][NSUB];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < NSUB; ++j) acc[i][j] = v16f{};
-
-    SA sa;
-    SB sb;
-    auto load_block = [&](int kb) {
-        const int b = kb / kb_per_b, k0 = (kb - b * kb_per_b) * BK;
-        sa.load(A + (int64_t)b * p.stride_a, p.lda, m0, p.M, k0, p.K, p.vec_a);
-        sb.load(B + (int64_t)b * p.stride_b, p.ldb, n0, p.N, k0, p.K, p.vec_b);
-    };
-    if (nk > 0) {
-        load_block(kb_beg);
-        sa.store(lds_a[0]);
-        sb.store(lds_b[0]);
-    }
-    __syncthreads();
-
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) load_block(kb_beg + kt + 1);
-        float fa[2][16], fb[NSUB][16];
-        const float* la = lds_a[cur];
-        const float* lb = lds_b[cur];
-        if (A_KMAJ) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const float* src = la + (wm * 64 + sub_row<false>(i, l32)) * SA::LD + 16 * half;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
-                    fa[i][4 * q + 0] = v.x; fa[i][4 * q + 1] = v.y;
-                    fa[i][4 * q + 2] = v.z; fa[i][4 * q + 3] = v.w;
-                }
-            }
-        } else {
-#pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                float2 v = *reinterpret_cast<const float2*>(la + (16 * half + s) * SA::LD + wm * 64 + 2 * l32);
-                fa[0][s] = v.x;
-                fa[1][s] = v.y;
-            }
-        }
-        if (B_KMAJ) {
-#pragma unroll
-            for (int j = 0; j < NSUB; ++j) {
-                const float* src = lb + (wn * WN + sub_row<false>(j, l32)) * SB::LD + 16 * half;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
-                    fb[j][4 * q + 0] = v.x; fb[j][4 * q + 1] = v.y;
-                    fb[j][4 * q + 2] = v.z; fb[j][4 * q + 3] = v.w;
-                }
-            }
-        } else if (B_PAIR) {
-#pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                float2 v = *reinterpret_cast<const float2*>(lb + (16 * half + s) * SB::LD + wn * WN + 2 * l32);
-                fb[0][s] = v.x;
-                fb[NSUB - 1][s] = v.y;
-            }
-        } else {
-#pragma unroll
-            for (int s = 0; s < 16; ++s) fb[0][s] = lb[(16 * half + s) * SB::LD + wn * WN + l32];
-        }
-#pragma unroll
-        for (int s = 0; s < 16; ++s)
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < NSUB; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
-        if (more) {
-            sa.store(lds_a[cur ^ 1]);
-            sb.store(lds_b[cur ^ 1]);
-        }
-        __syncthreads();
-    }
-
-    store_wave<NSUB, A_PAIR, B_PAIR>(p, acc, m0 + wm * 64, n0 + wn * WN, (int64_t)batch * p.stride_c, split);
-}
-
-// ---------------------------------------------------------------------------
 // bf16 kernel: BK = 64, v_mfma_f32_32x32x16_bf16 (lane half h supplies the 8
 // consecutive k 16s + 8h .. 16s + 8h + 7 to the s-th MFMA of a k block).
 // ---------------------------------------------------------------------------
@@ -1124,6 +1004,256 @@ void gemm_bf16_big_kernel(GemmParams p) {
     big_tile_guarded<A_KMAJ, B_KMAJ>(p, m0, n0, split, batch, kb_beg, nk, lds_a0, lds_a1, lds_b0, lds_b1);
 }
 
+// ---------------------------------------------------------------------------
+// fp32 kernel: 128 x BN x 32 per 256-thread workgroup (BN = 128, or 64 for
+// grids that would leave CUs idle), 4 waves in 2 x 2, each 64 x BN/2 =
+// 2 x NSUB accumulators of v_mfma_f32_32x32x2_f32.
+//
+// Both operands are staged K-major in LDS ([rows][32 + 4] floats: with the
+// 4-float pad the rows of a b128 fragment read hit distinct banks); an
+// MN-major operand is transposed in registers in 4 x 4 blocks while staged.
+// Lane half h feeds k = 16h + s to the s-th MFMA of a block (the sum order
+// within a block is permuted; the reference's sequential loop,
+// tensor/Tensor.cpp:356-360, differs only by rounding), so one b128 read
+// gives a lane four consecutive steps ("a quad").
+//
+// Pipeline (three LDS stages, one barrier per 32-deep block): while block k
+// is multiplied out of stage k%3, the registers holding block k+2 are written
+// to stage (k+2)%3, the global loads of block k+3 are issued into those
+// registers, and the first fragments of block k+1 (stage (k+1)%3, written a
+// block earlier) are read before the barrier, so no LDS latency follows it.
+// Loads past the last block are clamped to it (their writes land in a stage
+// nobody reads again).  Interior tiles take an unguarded load path with the
+// memory operations pinned between the MFMAs (sched_group_barrier); edge
+// tiles a bounds-checked one with zero fill (separate instantiations).
+// ---------------------------------------------------------------------------
+constexpr int kF32K = 32;
+constexpr int kF32LD = kF32K + 4;
+constexpr int kF32Stages = 3;
+// Native 4-float vector (HIP's float4 is a struct whose copies lower to
+// memcpy, which keeps staging arrays out of registers).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int ROWS, bool KMAJ, bool GUARD>
+struct F32Stage {
+    // K-major: vector i of thread t is row t/8 + 32i, k 4(t%8) .. +3 (a
+    // wave's 8-lane groups read 128 contiguous bytes of one row).
+    // MN-major: thread t < 8 * ROWS/4 owns the 4 x 4 block (k 4kb .. +3,
+    // rows 4mb .. +3); reg[kk] holds k row 4kb + kk.  Lanes 4i .. 4i+3 take
+    // consecutive mb (64 contiguous bytes of a k row) and the next four lanes
+    // the next kb, so a load reads whole 16 * ROWS-byte k rows, and the 8
+    // lanes of a group store at 8 distinct 16-byte bank groups (rows 4 apart
+    // are 144 words apart: 4 groups by mb, times 2 by kb).
+    static constexpr int NK = ROWS / 32;  // K-major 16-byte vectors per thread
+    static constexpr int NB = 8 * (ROWS / 4);  // MN-major blocks (threads with work)
+    static constexpr int N4 = KMAJ ? NK : 4;
+    static constexpr int MH = ROWS / 16;  // groups of 4 mb
+    f32x4 reg[N4];
+
+    __device__ __forceinline__ static void mn_block(int t, int& mb, int& kb) {
+        const int rest = t >> 3;
+        mb = (t & 3) + 4 * (rest % MH);
+        kb = ((t >> 2) & 1) + 2 * (rest / MH);
+    }
+
+    __device__ __forceinline__ static f32x4 load4(const float* __restrict__ p, int n, bool vec) {
+        if (!GUARD || (vec && n >= 4)) return *reinterpret_cast<const f32x4*>(p);
+        return f32x4{n > 0 ? p[0] : 0.0f, n > 1 ? p[1] : 0.0f, n > 2 ? p[2] : 0.0f, n > 3 ? p[3] : 0.0f};
+    }
+
+    __device__ __forceinline__ void load(const float* __restrict__ p, int64_t ld, int row0, int rows, int k0, int kend,
+                                         bool vec) {
+        const int t = threadIdx.x;
+        if (KMAJ) {
+            const int c = t & 7, r = t >> 3;
+            static_for<NK>([&](auto I) TF_LAMBDA_INLINE {
+                constexpr int i = decltype(I)::value;
+                const int row = row0 + r + 32 * i, k = k0 + 4 * c;
+                const float* src = p + (int64_t)row * ld + k;
+                if (!GUARD) reg[i] = *reinterpret_cast<const f32x4*>(src);
+                else reg[i] = row < rows ? load4(src, kend - k, vec) : f32x4{0.f, 0.f, 0.f, 0.f};
+            });
+        } else {
+            if (NB < kThreads && t >= NB) return;
+            int mb, kb;
+            mn_block(t, mb, kb);
+            const int m = row0 + 4 * mb;
+            static_for<4>([&](auto KK) TF_LAMBDA_INLINE {
+                constexpr int kk = decltype(KK)::value;
+                const int k = k0 + 4 * kb + kk;
+                const float* src = p + (int64_t)k * ld + m;
+                if (!GUARD) reg[kk] = *reinterpret_cast<const f32x4*>(src);
+                else reg[kk] = k < kend ? load4(src, rows - m, vec) : f32x4{0.f, 0.f, 0.f, 0.f};
+            });
+        }
+    }
+
+    __device__ __forceinline__ void store(float* __restrict__ lds) const {
+        const int t = threadIdx.x;
+        if (KMAJ) {
+            const int c = t & 7, r = t >> 3;
+            static_for<NK>([&](auto I) TF_LAMBDA_INLINE {
+                constexpr int i = decltype(I)::value;
+                *reinterpret_cast<f32x4*>(lds + (r + 32 * i) * kF32LD + 4 * c) = reg[i];
+            });
+        } else {
+            if (NB < kThreads && t >= NB) return;
+            int mb, kb;
+            mn_block(t, mb, kb);
+            // Row 4mb + j of the tile gets k 4kb .. +3 = element j of reg[0..3].
+            static_for<4>([&](auto J) TF_LAMBDA_INLINE {
+                constexpr int j = decltype(J)::value;
+                *reinterpret_cast<f32x4*>(lds + (4 * mb + j) * kF32LD + 4 * kb) =
+                    f32x4{reg[0][j], reg[1][j], reg[2][j], reg[3][j]};
+            });
+        }
+    }
+};
+
+template <int BN, bool A_KMAJ, bool B_KMAJ, bool GUARD>
+__device__ __forceinline__ void f32_tile(const GemmParams& p, int m0, int n0, int split, int batch, int kb_beg, int nk,
+                                         float* lds) {
+    constexpr int WN = BN / 2;
+    constexpr int NSUB = WN / 32;
+    constexpr int A_SZ = BM * kF32LD;          // floats of A per stage
+    constexpr int STAGE = (BM + BN) * kF32LD;  // floats per stage
+    const float* A = reinterpret_cast<const float*>(p.A) + (int64_t)batch * p.stride_a;
+    const float* B = reinterpret_cast<const float*>(p.B) + (int64_t)batch * p.stride_b;
+    const int kb_per_b = (p.K + kF32K - 1) / kF32K;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int half = lane >> 5, l32 = lane & 31;
+
+    v16f acc[2][NSUB];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NSUB; ++j) acc[i][j] = v16f{};
+
+    if (nk > 0) {
+        F32Stage<BM, A_KMAJ, GUARD> sa;
+        F32Stage<BN, B_KMAJ, GUARD> sb;
+        // Fragments of one quad (4 k steps): A sub-tiles 0,1 and B sub-tiles.
+        struct Quad {
+            f32x4 a[2], b[NSUB];
+        };
+        Quad f[2];
+        const int a_off = (wm * 64 + l32) * kF32LD + 16 * half;
+        const int b_off = A_SZ + (wn * WN + l32) * kF32LD + 16 * half;
+        // Block k of this slice (clamped to the last one).
+        auto load_block = [&](int k) TF_LAMBDA_INLINE {
+            const int kb = kb_beg + min(k, nk - 1);
+            const int b = kb / kb_per_b, k0 = (kb - b * kb_per_b) * kF32K;
+            sa.load(A + (int64_t)b * p.stride_a, p.lda, m0, p.M, k0, p.K, p.vec_a);
+            sb.load(B + (int64_t)b * p.stride_b, p.ldb, n0, p.N, k0, p.K, p.vec_b);
+        };
+        auto store_block = [&](float* st) TF_LAMBDA_INLINE {
+            sa.store(st);
+            sb.store(st + A_SZ);
+        };
+        auto read = [&](const float* st, int q, Quad& d) TF_LAMBDA_INLINE {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) d.a[i] = *reinterpret_cast<const f32x4*>(st + a_off + 32 * i * kF32LD + 4 * q);
+#pragma unroll
+            for (int j = 0; j < NSUB; ++j)
+                d.b[j] = *reinterpret_cast<const f32x4*>(st + b_off + 32 * j * kF32LD + 4 * q);
+        };
+        auto mfma_quad = [&](const Quad& d) TF_LAMBDA_INLINE {
+            static_for<4>([&](auto S) TF_LAMBDA_INLINE {
+                constexpr int s = decltype(S)::value;
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < NSUB; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(d.a[i][s], d.b[j][s], acc[i][j], 0, 0, 0);
+            });
+        };
+        constexpr int kMf = 4 * 2 * NSUB;  // MFMAs per quad
+        constexpr int kRd = 2 + NSUB;      // LDS reads per quad
+        // Interleave the quad's MFMAs with the kRd fragment reads issued
+        // before them (plus, in the first quad, the stage writes and loads).
+        auto pin_reads = [&]() TF_LAMBDA_INLINE {
+            static_for<kRd>([&](auto) TF_LAMBDA_INLINE {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+            });
+        };
+        constexpr int kWr = F32Stage<BM, A_KMAJ, GUARD>::N4 + F32Stage<BN, B_KMAJ, GUARD>::N4;  // stage writes per thread
+        constexpr bool kPinStage = !GUARD && F32Stage<BN, B_KMAJ, GUARD>::NB >= kThreads;
+
+        // Prologue: blocks 0 and 1 into stages 0 and 1, block 2 into registers.
+        load_block(0);
+        store_block(lds);
+        load_block(1);
+        store_block(lds + STAGE);
+        load_block(2);
+        dl_barrier<63>();
+        read(lds, 0, f[0]);
+        uint32_t s0 = 0, s1 = STAGE, s2 = 2 * STAGE;  // stage offsets of blocks k, k+1, k+2
+        for (int k = 0; k < nk; ++k) {
+            const float* cur = lds + s0;
+            // Quad 0: reads of quad 1, block k+2 to its stage, loads of block k+3.
+            read(cur, 1, f[1]);
+            store_block(lds + s2);
+            load_block(k + 3);
+            mfma_quad(f[0]);
+            if constexpr (kPinStage) {
+                pin_reads();
+                static_for<kWr / 2>([&](auto) TF_LAMBDA_INLINE {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);  // DS write
+                });
+                static_for<kWr / 2>([&](auto) TF_LAMBDA_INLINE {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM read
+                });
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // Quads 1 .. 3: each reads the fragments of the next quad; quad 3
+            // those of block k+1's quad 0.
+            read(cur, 2, f[0]);
+            mfma_quad(f[1]);
+            if constexpr (!GUARD) pin_reads();
+            __builtin_amdgcn_sched_barrier(0);
+            read(cur, 3, f[1]);
+            mfma_quad(f[0]);
+            if constexpr (!GUARD) pin_reads();
+            __builtin_amdgcn_sched_barrier(0);
+            read(lds + s1, 0, f[0]);
+            mfma_quad(f[1]);
+            if constexpr (!GUARD) pin_reads();
+            __builtin_amdgcn_sched_barrier(0);
+            // Block k+2's stage written and block k's stage fully read.
+            dl_barrier<63>();
+            const uint32_t t = s0;
+            s0 = s1;
+            s1 = s2;
+            s2 = t;
+        }
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // drain the clamped loads
+    }
+    store_wave<NSUB, false, false>(p, acc, m0 + wm * 64, n0 + wn * WN, (int64_t)batch * p.stride_c, split);
+}
+
+template <int BN, bool A_KMAJ, bool B_KMAJ>
+__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) float lds[kF32Stages * (BM + BN) * kF32LD];
+    int tm, tn;
+    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int split = blockIdx.y;
+    const int batch = blockIdx.z;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int kb_per_b = (p.K + kF32K - 1) / kF32K;
+    const int kb_total = kb_per_b * p.reduce_batch;
+    const int kb_beg = split * p.kb_per_split;
+    const int nk = max(0, min(kb_total, kb_beg + p.kb_per_split) - kb_beg);
+    const bool interior = p.vec_a && p.vec_b && m0 + BM <= p.M && n0 + BN <= p.N && p.K % kF32K == 0;
+    if (interior)
+        f32_tile<BN, A_KMAJ, B_KMAJ, false>(p, m0, n0, split, batch, kb_beg, nk, lds);
+    else
+        f32_tile<BN, A_KMAJ, B_KMAJ, true>(p, m0, n0, split, batch, kb_beg, nk, lds);
+}
+
 // Split-K reduction: C = epi(alpha * sum_s partial[s] + beta * C), summing the
 // splits in ascending order (deterministic).  Grid (ceil(N / 1024), M): a
 // block covers 1024 columns of one row, 4 per thread, with 16-byte loads of
@@ -1287,12 +1417,14 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
             splits = s;
         }
     }
-    // Otherwise: tile width 128 x 128 when that gives every CU at least two
-    // workgroups (two resident workgroups per CU hide each other's barrier
-    // and LDS latency), 128 x 64 otherwise and for narrow outputs.
+    // Otherwise: tile width 128 x 128 when that gives every CU at least its
+    // resident workgroup count (fp32: one, its three LDS stages take 108 KB;
+    // bf16: two, which hide each other's barrier and LDS latency), 128 x 64
+    // otherwise and for narrow outputs.
+    const int64_t per_cu = in_dtype == TF_F32 ? 1 : 2;
     const int64_t tiles_m = big ? (M + kBigTile - 1) / kBigTile : (M + BM - 1) / BM;
     const int64_t t128 = tiles_m * ((N + 127) / 128) * grid_batch;
-    const int BN = big ? kBigTile : (N <= 64 || t128 < 2 * ncu) ? 64 : 128;
+    const int BN = big ? kBigTile : (N <= 64 || t128 < per_cu * ncu) ? 64 : 128;
     p.tiles_m = (int)tiles_m;
     p.tiles_n = (int)((N + BN - 1) / BN);
     p.alpha = alpha; p.beta = beta; p.epi = epi; p.row_bias = row_bias;
@@ -1327,9 +1459,10 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     TF_REQUIRE(tiles < (1LL << 31), "tf_gemm: too many tiles");
 
     // Split the k blocks when the tiles leave most CUs idle and K is long
-    // (target: two workgroups per CU, >= 4 k blocks per slice).
+    // (target: the resident workgroups of every CU, >= 4 k blocks per slice).
     const int64_t kblocks = ((K + BK - 1) / BK) * p.reduce_batch;
-    if (!big && grid_batch == 1 && tiles * 2 <= ncu && kblocks >= 8) splits = choose_splits(tiles, kblocks, 2 * ncu, 4);
+    if (!big && grid_batch == 1 && tiles * 2 <= ncu && kblocks >= 8)
+        splits = choose_splits(tiles, kblocks, per_cu * ncu, 4);
     if (kblocks == 0) {
         splits = 1;
         p.kb_per_split = 0;
