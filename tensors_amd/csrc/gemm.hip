@@ -90,6 +90,26 @@ __device__ __forceinline__ void tile_coords(int wg, int tiles_m, int tiles_n, in
     tn = in_g / gm;
 }
 
+// Tile of an edge-kernel workgroup.  With an interior grid of int_m x int_n
+// tiles (taken by a direct-to-LDS kernel): the tile rows from int_m on, then
+// the tile columns from int_n on of the rows above; without one, all tiles.
+__device__ __forceinline__ void edge_coords(const GemmParams& p, int& tm, int& tn) {
+    if (p.int_m * p.int_n == 0) {
+        tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+        return;
+    }
+    const int id = blockIdx.x;
+    const int below = (p.tiles_m - p.int_m) * p.tiles_n;
+    if (id < below) {
+        tm = p.int_m + id / p.tiles_n;
+        tn = id % p.tiles_n;
+    } else {
+        const int w = p.tiles_n - p.int_n, id2 = id - below;
+        tm = id2 / w;
+        tn = p.int_n + id2 % w;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Operand staging.  ELEM = float (fp32 path) or uint16_t (bf16 bits).  A
 // tile is ROWS rows x BK k.  K-major LDS layout: [ROWS][BK + PADK];
@@ -190,10 +210,10 @@ __device__ __forceinline__ void emit(const GemmParams& p, int64_t off, float acc
 }
 
 // Write the wave's accumulators.  m_base/n_base: first row/column of the
-// wave block in C.
+// wave block in C.  i_only >= 0: only sub-tile row block i_only.
 template <int NSUB, bool A_PAIR, bool B_PAIR>
 __device__ __forceinline__ void store_wave(const GemmParams& p, const v16f (&acc)[2][NSUB], int m_base, int n_base,
-                                           int64_t batch_off_c, int split) {
+                                           int64_t batch_off_c, int split, int i_only = -1) {
     const int lane = threadIdx.x & 63;
     const int l32 = lane & 31, half = lane >> 5;
     const bool has_bias = p.epi != TF_EPI_NONE && p.epi != TF_EPI_RELU;
@@ -210,6 +230,7 @@ __device__ __forceinline__ void store_wave(const GemmParams& p, const v16f (&acc
         const float cb1 = (col_bias && c1) ? p.bias[col + 1] : 0.0f;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
+            if (i_only >= 0 && i != i_only) continue;  // the other sub-tile row block is another wave's
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m_base + sub_row<A_PAIR>(i, 8 * (r >> 2) + 4 * half + (r & 3));
@@ -971,9 +992,8 @@ void gemm_bf16_dl_kernel(GemmParams p) {
 }
 
 // Edge-tile kernel (or every tile when the direct path does not apply):
-// register-staged, bounds-checked 64-deep blocks.  Tiles: with an interior
-// grid of int_m x int_n, the tile rows from int_m on, then the tile columns
-// from int_n on of the rows above; without one, all tiles.
+// register-staged, bounds-checked 64-deep blocks over the tiles edge_coords
+// assigns.
 template <bool A_KMAJ, bool B_KMAJ>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_big_kernel(GemmParams p) {
@@ -981,20 +1001,7 @@ void gemm_bf16_big_kernel(GemmParams p) {
     __shared__ u32x4 lds_b0[kBigTile * 8], lds_b1[kBigTile * 8];
 
     int tm, tn;
-    if (p.int_m * p.int_n == 0) {
-        tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-    } else {
-        const int id = blockIdx.x;
-        const int below = (p.tiles_m - p.int_m) * p.tiles_n;
-        if (id < below) {
-            tm = p.int_m + id / p.tiles_n;
-            tn = id % p.tiles_n;
-        } else {
-            const int w = p.tiles_n - p.int_n, id2 = id - below;
-            tm = id2 / w;
-            tn = p.int_n + id2 % w;
-        }
-    }
+    edge_coords(p, tm, tn);
     const int split = blockIdx.y;
     const int batch = blockIdx.z;
     const int m0 = tm * kBigTile, n0 = tn * kBigTile;
@@ -1239,7 +1246,7 @@ template <int BN, bool A_KMAJ, bool B_KMAJ>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(16))) float lds[kF32Stages * (BM + BN) * kF32LD];
     int tm, tn;
-    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    edge_coords(p, tm, tn);
     const int split = blockIdx.y;
     const int batch = blockIdx.z;
     const int m0 = tm * BM, n0 = tn * BN;
@@ -1252,6 +1259,270 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmParams p) {
         f32_tile<BN, A_KMAJ, B_KMAJ, false>(p, m0, n0, split, batch, kb_beg, nk, lds);
     else
         f32_tile<BN, A_KMAJ, B_KMAJ, true>(p, m0, n0, split, batch, kb_beg, nk, lds);
+}
+
+// ---------------------------------------------------------------------------
+// fp32 direct-to-LDS kernel (tiles inside an int_m x int_n grid of 128 x 128,
+// K % 32 == 0, 16-byte loadable operands): the global loads write LDS
+// directly (buffer_load_dwordx4 ... lds, as in the bf16 direct kernel), so no
+// staging registers and no LDS stores; block k's loads are issued two blocks
+// ahead into a four-stage ring (128 KB).
+//
+// 512 threads: waves w and w + 4 share the 64 x 64 output block w & 3 (2 x 2
+// sub-tiles of v_mfma_f32_32x32x2_f32) and split every 32-deep block: group
+// g = w / 4 takes quads 2g and 2g + 1 (lane half h feeds k = 16h + 4q + s at
+// step s of quad q, the k order of the register-staged kernel).  Two waves
+// per SIMD keep its matrix core busy through each other's barrier and LDS
+// waits.  At the end each pair adds its halves through LDS (own + partner:
+// the same sum in both waves, fp addition commutes) and each wave stores one
+// 32-row sub-tile of the block.
+//
+// LDS layout per operand block (16 KB, written 1 KB per load instruction):
+//   K-major  [128 rows][8 chunks of 4 k]; chunk c of row r sits in slot
+//            c ^ f32dl_swz(r), so the b128 fragment reads of 16 consecutive
+//            rows hit 16 distinct 4-bank groups (rows 2 apart share banks);
+//   MN-major [32 k][128 rows], as in memory; a lane reads the row pair
+//            2c, 2c + 1 of one k with one ds_read_b64, so sub-tile 0 of a
+//            wave holds its rows 2c and sub-tile 1 its rows 2c + 1 (the
+//            epilogue writes those rows / columns interleaved).
+// ---------------------------------------------------------------------------
+constexpr int kF32DlThreads = 512;
+constexpr int kF32DlStages = 4;
+constexpr int kF32DlOp = BM * kF32K;                                     // floats of one operand block
+constexpr int kF32DlLoads = kF32DlOp * 4 / 1024 / (kF32DlThreads / 64);  // 1 KB loads per wave per block
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ int f32dl_swz(int row) { return (row >> 1) & 7; }
+
+// Byte offsets (from the tile origin) of this lane's direct loads of one
+// operand block; wave w fills 1 KB pieces kF32DlLoads*w .. of it.
+template <bool KMAJ>
+__device__ __forceinline__ void f32dl_offsets(int64_t ld, uint32_t (&voff)[kF32DlLoads]) {
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < kF32DlLoads; ++i) {
+        const int blk = w * kF32DlLoads + i;
+        if (KMAJ) {
+            const int row = blk * 8 + (l >> 3);  // lane l fills slot l & 7 of row
+            voff[i] = 4u * ((uint32_t)row * (uint32_t)ld + 4u * (uint32_t)((l & 7) ^ f32dl_swz(row)));
+        } else {
+            const int k = blk * 2 + (l >> 5);
+            voff[i] = 4u * ((uint32_t)k * (uint32_t)ld + 4u * (uint32_t)(l & 31));
+        }
+    }
+}
+
+// Issue this wave's direct loads of one operand block (M0 = the 1 KB LDS
+// destination; inline assembly for the reasons given at dl_issue).
+__device__ __forceinline__ void f32dl_issue(i32x4 rsrc, uint32_t tile_off, const uint32_t (&voff)[kF32DlLoads],
+                                            float* lds_block) {
+    const int w = threadIdx.x >> 6;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_ptr)(lds_block + w * kF32DlLoads * 256);
+    static_for<kF32DlLoads>([&](auto I) TF_LAMBDA_INLINE {
+        constexpr int i = decltype(I)::value;
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(lds0 + i * 1024u);
+        const uint32_t v = voff[i], so = tile_off;  // asm operands must be locals of the lambda
+        const i32x4 r = rsrc;
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                     :
+                     : "s"(dst), "v"(v), "s"(r), "s"(so)
+                     : "memory", "m0");
+    });
+}
+
+// One quad's fragments of one operand: the value of sub-tile i at step s.
+template <bool KMAJ>
+struct F32DlFrag;
+template <>
+struct F32DlFrag<true> {
+    f32x4 v[2];
+    __device__ __forceinline__ float at(int i, int s) const { return v[i][s]; }
+};
+template <>
+struct F32DlFrag<false> {
+    f32x2 v[4];
+    __device__ __forceinline__ float at(int i, int s) const { return v[s][i]; }
+};
+
+// Per-lane LDS word offsets of one operand's fragment reads (wave rows
+// wbase .. wbase + 63, quads 2g + qq).  K-major: sub-tile i's row for quad
+// qq (swizzled chunk 4h + 2g + qq).  MN-major: the lane's row pair in k row
+// 16h + 8g.
+template <bool KMAJ>
+struct F32DlOperand {
+    int off[KMAJ ? 4 : 1];
+    __device__ __forceinline__ void init(int wbase, int g) {
+        const int l = threadIdx.x & 63, h = l >> 5, l32 = l & 31;
+        if constexpr (KMAJ) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int r = wbase + 32 * i + l32;
+#pragma unroll
+                for (int qq = 0; qq < 2; ++qq)
+                    off[2 * i + qq] = r * kF32K + 4 * ((4 * h + 2 * g + qq) ^ f32dl_swz(r));
+            }
+        } else {
+            off[0] = (16 * h + 8 * g) * BM + wbase + 2 * l32;
+        }
+    }
+    __device__ __forceinline__ void read(const float* op, int qq, F32DlFrag<KMAJ>& d) const {
+        if constexpr (KMAJ) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) d.v[i] = *reinterpret_cast<const f32x4*>(op + off[2 * i + qq]);
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) d.v[s] = *reinterpret_cast<const f32x2*>(op + off[0] + (4 * qq + s) * BM);
+        }
+    }
+};
+
+template <bool A_KMAJ, bool B_KMAJ>
+__global__ __launch_bounds__(kF32DlThreads) void gemm_f32_dl_kernel(GemmParams p) {
+    constexpr int S = kF32DlStages;
+    __shared__ __attribute__((aligned(16))) float lds[S * 2 * kF32DlOp];
+    int tm, tn;
+    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int split = blockIdx.y;
+    const int batch = blockIdx.z;
+    const int m0 = tm * BM, n0 = tn * BM;
+    const int kpb = p.K / kF32K;
+    const int kb_total = kpb * p.reduce_batch;
+    const int kb_beg = split * p.kb_per_split;
+    const int nk = max(0, min(kb_total, kb_beg + p.kb_per_split) - kb_beg);
+    const float* A = reinterpret_cast<const float*>(p.A) + (int64_t)batch * p.stride_a;
+    const float* B = reinterpret_cast<const float*>(p.B) + (int64_t)batch * p.stride_b;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int g = wave >> 2, wm = (wave >> 1) & 1, wn = wave & 1;
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+
+    if (nk > 0) {
+        F32DlOperand<A_KMAJ> oa;
+        F32DlOperand<B_KMAJ> ob;
+        oa.init(wm * 64, g);
+        ob.init(wn * 64, g);
+        uint32_t voff_a[kF32DlLoads], voff_b[kF32DlLoads];
+        f32dl_offsets<A_KMAJ>(p.lda, voff_a);
+        f32dl_offsets<B_KMAJ>(p.ldb, voff_b);
+        struct Quad {
+            F32DlFrag<A_KMAJ> a;
+            F32DlFrag<B_KMAJ> b;
+        };
+        Quad f[2];
+        auto stage_a = [&](int st) TF_LAMBDA_INLINE { return lds + st * 2 * kF32DlOp; };
+        auto issue = [&](int kb, int st) TF_LAMBDA_INLINE {
+            const int b = kb / kpb;
+            const uint32_t k0 = (uint32_t)((kb - b * kpb) * kF32K);
+            const i32x4 ra = dl_rsrc(A + (int64_t)b * p.stride_a, p.a_bytes);
+            const i32x4 rb = dl_rsrc(B + (int64_t)b * p.stride_b, p.b_bytes);
+            const uint32_t ta =
+                4u * (A_KMAJ ? (uint32_t)m0 * (uint32_t)p.lda + k0 : k0 * (uint32_t)p.lda + (uint32_t)m0);
+            const uint32_t tb =
+                4u * (B_KMAJ ? (uint32_t)n0 * (uint32_t)p.ldb + k0 : k0 * (uint32_t)p.ldb + (uint32_t)n0);
+            f32dl_issue(ra, ta, voff_a, stage_a(st));
+            f32dl_issue(rb, tb, voff_b, stage_a(st) + kF32DlOp);
+        };
+        auto read = [&](int st, int qq, Quad& d) TF_LAMBDA_INLINE {
+            oa.read(stage_a(st), qq, d.a);
+            ob.read(stage_a(st) + kF32DlOp, qq, d.b);
+        };
+        auto mfma_quad = [&](const Quad& d) TF_LAMBDA_INLINE {
+            static_for<4>([&](auto Sc) TF_LAMBDA_INLINE {
+                constexpr int s = decltype(Sc)::value;
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(d.a.at(i, s), d.b.at(j, s), acc[i][j], 0, 0, 0);
+            });
+        };
+        constexpr int kRd = (A_KMAJ ? 2 : 4) + (B_KMAJ ? 2 : 4);  // LDS reads per quad
+        auto pin_reads = [&]() TF_LAMBDA_INLINE {
+            static_for<kRd>([&](auto) TF_LAMBDA_INLINE {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+            });
+        };
+        // Block t in stage b = t % S (this wave's two quads of it).  Every
+        // block but the last waits for block t+1 (S-3 newer blocks of loads
+        // stay in flight), which also guarantees every wave is done with block
+        // t-1's stage, loads block t+S-1 (clamped to the last block: loads
+        // past the end land in stages nobody reads again) into that stage and
+        // reads block t+1's first fragments.  LAST: no next block.
+        auto block = [&](auto Bc, int t, auto LAST) TF_LAMBDA_INLINE {
+            constexpr int b = decltype(Bc)::value;
+            constexpr bool last = decltype(LAST)::value;
+            read(b, 1, f[1]);
+            mfma_quad(f[0]);
+            pin_reads();
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (!last) {
+                dl_barrier<(S - 3) * 2 * kF32DlLoads>();
+                issue(kb_beg + min(t + S - 1, nk - 1), (b + S - 1) % S);
+                read((b + 1) % S, 0, f[0]);
+            }
+            mfma_quad(f[1]);
+            if constexpr (!last) pin_reads();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        // Prologue: blocks 0 .. S-2 (clamped) into stages 0 .. S-2, wait for block 0.
+        static_for<S - 1>([&](auto Bc) TF_LAMBDA_INLINE {
+            constexpr int b = decltype(Bc)::value;
+            issue(kb_beg + min(b, nk - 1), b);
+        });
+        dl_barrier<(S - 2) * 2 * kF32DlLoads>();
+        read(0, 0, f[0]);
+        // Blocks 0 .. nk-2, S per iteration (stage = position in the group).
+        int t = 0;
+        bool stop = false;
+        while (!stop) {
+            static_for<S>([&](auto Bc) TF_LAMBDA_INLINE {
+                if (stop) return;
+                if (t + 1 >= nk) {
+                    stop = true;
+                    return;
+                }
+                block(Bc, t, std::false_type{});
+                ++t;
+            });
+        }
+        // Block nk-1.
+        const int rlast = t % S;
+        static_for<S>([&](auto Bc) TF_LAMBDA_INLINE {
+            if (rlast == decltype(Bc)::value) block(Bc, t, std::true_type{});
+        });
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // drain the clamped loads
+    }
+    // Pair reduction through LDS: wave w hands sub-tile row block 1 - g to
+    // wave w ^ 4 and keeps block g (8 KB per wave, 1 KB per vector).
+    __syncthreads();  // every wave is done with the stages
+    f32x4* x = reinterpret_cast<f32x4*>(lds);
+    static_for<2>([&](auto I) TF_LAMBDA_INLINE {
+        constexpr int i = decltype(I)::value;
+        if (i == g) return;
+        static_for<8>([&](auto V) TF_LAMBDA_INLINE {
+            constexpr int v = decltype(V)::value, j = v >> 2, r = 4 * (v & 3);
+            x[(wave * 8 + v) * 64 + lane] = f32x4{acc[i][j][r], acc[i][j][r + 1], acc[i][j][r + 2], acc[i][j][r + 3]};
+        });
+    });
+    __syncthreads();
+    static_for<2>([&](auto I) TF_LAMBDA_INLINE {
+        constexpr int i = decltype(I)::value;
+        if (i != g) return;
+        static_for<8>([&](auto V) TF_LAMBDA_INLINE {
+            constexpr int v = decltype(V)::value, j = v >> 2, r = 4 * (v & 3);
+            const f32x4 y = x[((wave ^ 4) * 8 + v) * 64 + lane];
+            acc[i][j][r] += y[0];
+            acc[i][j][r + 1] += y[1];
+            acc[i][j][r + 2] += y[2];
+            acc[i][j][r + 3] += y[3];
+        });
+    });
+    store_wave<2, !A_KMAJ, !B_KMAJ>(p, acc, m0 + wm * 64, n0 + wn * 64, (int64_t)batch * p.stride_c, split, g);
 }
 
 // Split-K reduction: C = epi(alpha * sum_s partial[s] + beta * C), summing the
@@ -1343,6 +1614,13 @@ KernelFn pick_bf16(bool a_kmaj, bool b_kmaj) {
     if (a_kmaj && !b_kmaj) return gemm_bf16_kernel<BN, true, false>;
     if (!a_kmaj && b_kmaj) return gemm_bf16_kernel<BN, false, true>;
     return gemm_bf16_kernel<BN, false, false>;
+}
+
+KernelFn pick_f32_dl(bool a_kmaj, bool b_kmaj) {
+    if (a_kmaj && b_kmaj) return gemm_f32_dl_kernel<true, true>;
+    if (a_kmaj && !b_kmaj) return gemm_f32_dl_kernel<true, false>;
+    if (!a_kmaj && b_kmaj) return gemm_f32_dl_kernel<false, true>;
+    return gemm_f32_dl_kernel<false, false>;
 }
 
 KernelFn pick_bf16_big(bool a_kmaj, bool b_kmaj) {
@@ -1455,6 +1733,28 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
         p.int_n = direct ? (int)(part_n ? (N + kBigTile - 1) / kBigTile : N / kBigTile) : 0;
     }
 
+    // fp32 with 128 x 128 tiles: the tiles of an int_m x int_n grid take the
+    // direct-to-LDS kernel when K is a whole number of 32-deep blocks, the
+    // operands are 16-byte loadable and each extent fits the descriptor.
+    // Partial tiles at the M / N edges are fine for it as for the bf16 one;
+    // an MN-major operand needs its row count a multiple of 4 for that.
+    bool dl32 = false;
+    if (in_dtype == TF_F32 && BN == 128) {
+        const int64_t ext_a = trans_a ? (K - 1) * lda + M : (M - 1) * lda + K;
+        const int64_t ext_b = trans_b ? (N - 1) * ldb + K : (K - 1) * ldb + N;
+        const int64_t lim = (int64_t)0x7fffffff;
+        if (K > 0 && K % 32 == 0 && p.vec_a && p.vec_b && ext_a * 4 <= lim && ext_b * 4 <= lim) {
+            const bool part_m = trans_a == 0 || M % 4 == 0;
+            const bool part_n = trans_b != 0 || N % 4 == 0;
+            p.int_m = part_m ? p.tiles_m : (int)(M / BM);
+            p.int_n = part_n ? p.tiles_n : (int)(N / 128);
+            p.a_bytes = (uint32_t)(ext_a * 4);
+            p.b_bytes = (uint32_t)(ext_b * 4);
+            dl32 = p.int_m * p.int_n > 0;
+            if (!dl32) p.int_m = p.int_n = 0;
+        }
+    }
+
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     TF_REQUIRE(tiles < (1LL << 31), "tf_gemm: too many tiles");
 
@@ -1497,6 +1797,21 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
             dim3 grid((unsigned)(tiles - n_int), (unsigned)splits, (unsigned)grid_batch);
             pick_bf16_big(a_kmaj, b_kmaj)<<<grid, kThreads, 0, ctx->stream>>>(p);
             st = tfh::check_launch("gemm_bf16_big_kernel");
+            if (st != TF_OK) return st;
+        }
+    } else if (dl32) {
+        const int64_t n_int = (int64_t)p.int_m * p.int_n;
+        GemmParams q = p;
+        q.tiles_m = p.int_m;
+        q.tiles_n = p.int_n;
+        dim3 grid((unsigned)n_int, (unsigned)splits, (unsigned)grid_batch);
+        pick_f32_dl(a_kmaj, b_kmaj)<<<grid, kF32DlThreads, 0, ctx->stream>>>(q);
+        st = tfh::check_launch("gemm_f32_dl_kernel");
+        if (st != TF_OK) return st;
+        if (tiles - n_int > 0) {
+            dim3 egrid((unsigned)(tiles - n_int), (unsigned)splits, (unsigned)grid_batch);
+            pick_f32<128>(a_kmaj, b_kmaj)<<<egrid, kThreads, 0, ctx->stream>>>(p);
+            st = tfh::check_launch("gemm_f32_kernel");
             if (st != TF_OK) return st;
         }
     } else {

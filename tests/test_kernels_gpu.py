@@ -200,6 +200,47 @@ def test_gemm_bf16_large_tile_epilogues(ctx):
     assert_close(dc.numpy(), _gemm_truth(a, b, False, True, 0.5, 0.25, c0), RTOL32, "alpha/beta")
 
 
+# Shapes that select the fp32 128 x 128 tiles with the direct-to-LDS kernel:
+# all-interior tiles; ragged M/N that are multiples of 4 (partial tiles in the
+# direct kernel); ragged M/N that are not (the register-staged kernel takes
+# the edge tiles of MN-major operands); K not a multiple of 32 (no direct
+# path).
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(2048, 2048, 2048), (2000, 2100, 256), (2046, 2050, 96), (2048, 2304, 200)])
+def test_gemm_f32_large_tile(ctx, ta, tb, M, N, K):
+    seed = synth.seed(2, 10) + M + N + K
+    a = synth.normal(seed, (K, M) if ta else (M, K))
+    b = synth.normal(seed + 1, (N, K) if tb else (K, N))
+    got = _run_gemm(ctx, a, b, ta, tb, M, N)
+    assert_close(got, _gemm_truth(a, b, ta, tb), RTOL32, f"fp32 128-tile ta={ta} tb={tb} {M}x{N}x{K}")
+
+
+def test_gemm_f32_large_tile_epilogues(ctx):
+    M, N, K = 2048, 2176, 64
+    a = synth.normal(81, (M, K))
+    b = synth.normal(82, (N, K))
+    bias = synth.normal(83, (N,))
+    c0 = synth.normal(84, (M, N))
+    got = _run_gemm(ctx, a, b, False, True, M, N, bias=bias, relu=True)
+    assert_close(got, _gemm_truth(a, b, False, True, bias=bias, relu=True), RTOL32, "fp32 128-tile bias+relu")
+    got = _run_gemm(ctx, a, b, False, True, M, N, alpha=0.5, beta=0.25, c0=c0)
+    assert_close(got, _gemm_truth(a, b, False, True, 0.5, 0.25, c0), RTOL32, "fp32 128-tile alpha/beta")
+
+
+def test_gemm_f32_large_tile_reduce_batch(ctx):
+    # C = sum_b A_b^T B_b (weight-gradient form) with 128 x 128 tiles.
+    from tensors_amd import ops
+    nb, M, N, K = 3, 2048, 2048, 96
+    a = synth.normal(91, (nb, K, M))
+    b = synth.normal(92, (nb, K, N))
+    da, db = ctx.array(a), ctx.array(b)
+    dc = ctx.zeros((M, N))
+    ops.gemm_ex(da, db, dc, M, N, K, lda=M, ldb=N, ldc=N, trans_a=True, stride_a=K * M, stride_b=K * N,
+                batch=nb, reduce_batch=True)
+    truth = np.einsum("bkm,bkn->mn", a.astype(np.float64), b.astype(np.float64))
+    assert_close(dc.numpy(), truth, RTOL32, "fp32 128-tile batch reduction")
+
+
 def test_gemm_strided_batched(ctx):
     from tensors_amd._lib import TF_F32, call
     B, M, N, K = 5, 33, 47, 29
