@@ -25,9 +25,9 @@ from pathlib import Path
 # Kernels of bench.py --probe (C2 step): label -> (name substring, algorithmic bytes per launch)
 N2 = 2048
 C2_KERNELS = {
-    "gemm_f32_fwd_c2": ("gemm_f32_kernel<64, true, true>", 4 * (3 * N2 * N2 + N2)),
-    "gemm_f32_bwd_dx_c2": ("gemm_f32_kernel<64, true, false>", 4 * 3 * N2 * N2),
-    "gemm_f32_bwd_dw_c2": ("gemm_f32_kernel<64, false, false>", 4 * 3 * N2 * N2),
+    "gemm_f32_fwd_c2": ("gemm_f32_dl_kernel<true, true>", 4 * (3 * N2 * N2 + N2)),
+    "gemm_f32_bwd_dx_c2": ("gemm_f32_dl_kernel<true, false>", 4 * 3 * N2 * N2),
+    "gemm_f32_bwd_dw_c2": ("gemm_f32_dl_kernel<false, false>", 4 * 3 * N2 * N2),
 }
 CAL_NAME = "binary_kernel"
 
