@@ -144,18 +144,21 @@ __global__ __launch_bounds__(256) void ln_fwd_stream_kernel(const float* __restr
 }
 
 // ---------------------------------------------------------------------------
-// Fused backward for cols <= 256 * NC.  Block b handles rows
-// [b * rpb, (b+1) * rpb); each wave takes every 4th of them.  Column partial
-// sums of dy * xhat and dy go to part[b][0][:] and part[b][1][:].
+// Fused backward for cols <= 256 * NC.  Block b (WAVES waves) handles rows
+// [b * rpb, (b+1) * rpb); each wave takes every WAVES-th of them.  Column
+// partial sums of dy * xhat and dy go to part[b][0][:] and part[b][1][:].
+// Eight waves per block halve the partials (8 bytes per column per block)
+// against four while keeping one row per wave at 1024 rows.
 // ---------------------------------------------------------------------------
-template <int NC>
-__global__ __launch_bounds__(256) void ln_bwd_fused_kernel(const float* __restrict__ dy, const float* __restrict__ x,
-                                                           const float* __restrict__ gamma,
-                                                           const float* __restrict__ mean,
-                                                           const float* __restrict__ rstd, float* __restrict__ dx,
-                                                           float* __restrict__ part, int rows, int cols,
-                                                           int rows_per_block, int vec) {
-    __shared__ float red[4][2][NC * 256];
+template <int NC, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void ln_bwd_fused_kernel(const float* __restrict__ dy,
+                                                                  const float* __restrict__ x,
+                                                                  const float* __restrict__ gamma,
+                                                                  const float* __restrict__ mean,
+                                                                  const float* __restrict__ rstd, float* __restrict__ dx,
+                                                                  float* __restrict__ part, int rows, int cols,
+                                                                  int rows_per_block, int vec) {
+    __shared__ float red[WAVES][2][NC * 256];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r0 = blockIdx.x * rows_per_block;
     const int r1 = min(rows, r0 + rows_per_block);
@@ -173,7 +176,7 @@ __global__ __launch_bounds__(256) void ln_bwd_fused_kernel(const float* __restri
             const int j = col_of(c, lane, q, vec);
             gm[c][q] = j < cols ? gamma[j] : 0.0f;
         }
-    for (int r = r0 + wave; r < r1; r += 4) {
+    for (int r = r0 + wave; r < r1; r += WAVES) {
         float xv[NC][4], gv[NC][4];
         load_row<NC>(x + (int64_t)r * cols, cols, lane, vec, xv);
         load_row<NC>(dy + (int64_t)r * cols, cols, lane, vec, gv);
@@ -202,7 +205,7 @@ __global__ __launch_bounds__(256) void ln_bwd_fused_kernel(const float* __restri
             }
         store_row<NC>(dx + (int64_t)r * cols, cols, lane, vec, xv);
     }
-    // Block combine of the four waves' column partials (fixed order).
+    // Block combine of the waves' column partials (fixed order).
 #pragma unroll
     for (int c = 0; c < NC; ++c)
 #pragma unroll
@@ -212,13 +215,18 @@ __global__ __launch_bounds__(256) void ln_bwd_fused_kernel(const float* __restri
             red[wave][1][slot] = bacc[c][q];
         }
     __syncthreads();
-    for (int slot = threadIdx.x; slot < NC * 256; slot += 256) {
+    for (int slot = threadIdx.x; slot < NC * 256; slot += WAVES * 64) {
         const int c = slot / 256, rem = slot % 256, l = rem / 4, q = rem % 4;
         const int j = col_of(c, l, q, vec);
         if (j >= cols) continue;
         float* pg = part + (int64_t)blockIdx.x * 2 * cols;
-        pg[j] = (red[0][0][slot] + red[1][0][slot]) + (red[2][0][slot] + red[3][0][slot]);
-        pg[cols + j] = (red[0][1][slot] + red[1][1][slot]) + (red[2][1][slot] + red[3][1][slot]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float t = red[0][h][slot];
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) t += red[w][h][slot];
+            pg[h * cols + j] = t;
+        }
     }
 }
 
@@ -347,21 +355,24 @@ tf_status tf_layernorm_bwd(tf_ctx* ctx, const float* dy, const float* x, const f
     }
     const int nc = chunks_for(cols);
     if (nc > 0) {
-        // ~256 blocks of >= 4 rows each.
-        int64_t rpb = std::max<int64_t>(4, (rows + 255) / 256);
+        // 128 .. 256 blocks of 8 waves (4 for rows over 1024 columns, whose
+        // registers need the whole file), >= 1 row per wave.
+        const int waves = nc <= 4 ? 8 : 4;
+        const int64_t target = std::min<int64_t>(256, std::max<int64_t>(128, rows / (4 * waves)));
+        int64_t rpb = std::max<int64_t>(waves, (rows + target - 1) / target);
         int64_t nblocks = (rows + rpb - 1) / rpb;
         tf_status st = tfh::ensure_workspace(ctx, (size_t)nblocks * 2 * cols * sizeof(float));
         if (st != TF_OK) return st;
         float* part = reinterpret_cast<float*>(ctx->ws);
         const int vec = row_vec(x, cols) && row_vec(dy, cols) && row_vec(dx, cols);
         const dim3 grid((unsigned)nblocks);
-#define TF_LN_BWD(NC) ln_bwd_fused_kernel<NC><<<grid, 256, 0, ctx->stream>>>(dy, x, gamma, mean, rstd, dx, part, \
-                                                     (int)rows, (int)cols, (int)rpb, vec)
+#define TF_LN_BWD(NC, W) ln_bwd_fused_kernel<NC, W><<<grid, W * 64, 0, ctx->stream>>>(dy, x, gamma, mean, rstd, dx, \
+                                                     part, (int)rows, (int)cols, (int)rpb, vec)
         switch (nc) {
-        case 1: TF_LN_BWD(1); break;
-        case 2: TF_LN_BWD(2); break;
-        case 4: TF_LN_BWD(4); break;
-        default: TF_LN_BWD(kMaxCached); break;
+        case 1: TF_LN_BWD(1, 8); break;
+        case 2: TF_LN_BWD(2, 8); break;
+        case 4: TF_LN_BWD(4, 8); break;
+        default: TF_LN_BWD(kMaxCached, 4); break;
         }
 #undef TF_LN_BWD
         st = tfh::check_launch("ln_bwd_fused_kernel");
