@@ -222,6 +222,9 @@ tf_status tf_softmax_bwd(tf_ctx* ctx, const float* y, const float* dy, float* dx
 /* db[c] = sum_r dy[r, c]  (Linear bias grad; no reference counterpart, the
  * reference Linear drops its bias, nn/Linear.cpp:60-63) */
 tf_status tf_colsum(tf_ctx* ctx, const float* dy, float* db, int64_t rows, int64_t cols);
+/* The same for bf16 dy (bit patterns), summed in fp32; equal to tf_colsum of
+ * the widened tensor (the bf16 compute path's bias grad, no cast pass). */
+tf_status tf_colsum_bf16(tf_ctx* ctx, const void* dy, float* db, int64_t rows, int64_t cols);
 /* db[c] = sum_{n,hw} dy[n, c, hw]  (replaces launch_reduce_sum_axis_nchw,
  * cuda/kernels/reduce_sum_axis.cu:53-120, which is wrong for H*W > 256) */
 tf_status tf_chansum_nchw(tf_ctx* ctx, const float* dy, float* db,

@@ -81,6 +81,7 @@ SIGNATURES: dict[str, list] = {
     "tf_log_softmax_bwd": [_p, _p, _p, _p, _i64, _i64],
     "tf_softmax_bwd": [_p, _p, _p, _p, _i64, _i64],
     "tf_colsum": [_p, _p, _p, _i64, _i64],
+    "tf_colsum_bf16": [_p, _p, _p, _i64, _i64],
     "tf_chansum_nchw": [_p, _p, _p, _i64, _i64, _i64],
     "tf_sgd_momentum": [_p, _p, _p, _p, _p, _i64, _f, _f],
     "tf_cast_f32_bf16": [_p, _p, _p, _i64],

@@ -196,13 +196,7 @@ Tensor colsum(const Tensor& dy) {
     as_rows(dy, R, C);
     Tensor db = Tensor::empty(Shape{C}, Dtype::Float32, dy.device());
     if (gpu(dy)) {
-        if (dy.dtype() == Dtype::Float32) {
-            hip::colsum(dy, db);
-        } else {
-            Tensor f = Tensor::empty(dy.shape(), Dtype::Float32, dy.device());
-            hip::cast(dy, f);
-            hip::colsum(f, db);
-        }
+        hip::colsum(dy, db);  // Float32 or BFloat16 dy, fp32 sums
         return db;
     }
     cpu_f32(dy, "colsum");

@@ -227,12 +227,17 @@ void gemm_ex(int device, bool trans_a, bool trans_b, int64_t M, int64_t N, int64
 }
 
 namespace {
-void rows_cols(const Tensor& t, int64_t& rows, int64_t& cols, const char* what) {
+// [rows, cols] view of a contiguous tensor (cols = last dimension), any dtype.
+void rows_cols_any(const Tensor& t, int64_t& rows, int64_t& cols, const char* what) {
     require(t.shape().ndim() >= 1, std::string(what) + ": needs at least 1-D");
-    require(t.dtype() == Dtype::Float32, std::string(what) + ": Float32 only");
     require_contig(t, what);
     cols = t.shape()[t.shape().ndim() - 1];
     rows = cols ? t.numel() / cols : 0;
+}
+
+void rows_cols(const Tensor& t, int64_t& rows, int64_t& cols, const char* what) {
+    require(t.dtype() == Dtype::Float32, std::string(what) + ": Float32 only");
+    rows_cols_any(t, rows, cols, what);
 }
 }  // namespace
 
@@ -338,8 +343,13 @@ void transpose2d(const Tensor& x, Tensor& out, int64_t batch, int64_t rows, int6
 
 void colsum(const Tensor& dy, Tensor& db) {
     require_gpu(dy, "hip::colsum");
-    int64_t r, c; rows_cols(dy, r, c, "hip::colsum");
-    require(db.numel() == c, "hip::colsum: db size");
+    int64_t r, c; rows_cols_any(dy, r, c, "hip::colsum");
+    require(db.numel() == c && db.dtype() == Dtype::Float32, "hip::colsum: db size");
+    if (dy.dtype() == Dtype::BFloat16) {
+        check(tf_colsum_bf16(ctx_of(dy), dy.data(), static_cast<float*>(db.data()), r, c), "hip::colsum");
+        return;
+    }
+    require(dy.dtype() == Dtype::Float32, "hip::colsum: dy must be Float32 or BFloat16");
     check(tf_colsum(ctx_of(dy), static_cast<const float*>(dy.data()), static_cast<float*>(db.data()), r, c), "hip::colsum");
 }
 

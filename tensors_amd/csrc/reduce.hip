@@ -1,5 +1,5 @@
 // Bias-gradient reductions, deterministic two-stage (no atomics):
-//   colsum : db[c] = sum_r dy[r, c]           (Linear bias grad)
+//   colsum : db[c] = sum_r dy[r, c]           (Linear bias grad; fp32 or bf16 dy)
 //   chansum: db[c] = sum_{n,p} dy[n, c, p]    (Conv2d bias grad, NCHW)
 // Stage 1 writes per-chunk partial sums to the context workspace, stage 2
 // (tfh::partial_rows_sum, also used by the LayerNorm backward) adds them in a
@@ -14,9 +14,22 @@ namespace {
 
 constexpr int kColsPerBlock = 256;  // 64 lanes x float4
 
+// Element loads as fp32: float, or bf16 bit patterns (uint16_t; widening is
+// exact, so the bf16 sums equal those of the cast fp32 tensor).
+__device__ __forceinline__ float elem_f32(const float* p, int64_t i) { return p[i]; }
+__device__ __forceinline__ float elem_f32(const uint16_t* p, int64_t i) { return __uint_as_float((uint32_t)p[i] << 16); }
+// Four consecutive elements (16-byte / 8-byte aligned).
+__device__ __forceinline__ float4 vec4_f32(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 vec4_f32(const uint16_t* p) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xffff0000u));
+}
+
 // Stage 1 of colsum: block (strip, chunk) sums rows [chunk*rpc, ...) of the
 // 256-column strip.  The four waves take interleaved rows; LDS combines them.
-__global__ __launch_bounds__(256) void colsum_stage1(const float* __restrict__ dy, float* __restrict__ part,
+template <typename T>
+__global__ __launch_bounds__(256) void colsum_stage1(const T* __restrict__ dy, float* __restrict__ part,
                                                      int rows, int cols, int rows_per_chunk, int vec) {
     __shared__ float4 red[4][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -27,16 +40,16 @@ __global__ __launch_bounds__(256) void colsum_stage1(const float* __restrict__ d
     if (vec && c0 + 4 <= cols) {
 #pragma unroll 4
         for (int r = r0 + wave; r < r1; r += 4) {
-            float4 v = *reinterpret_cast<const float4*>(dy + (int64_t)r * cols + c0);
+            float4 v = vec4_f32(dy + (int64_t)r * cols + c0);
             acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
         }
     } else {
         for (int r = r0 + wave; r < r1; r += 4) {
-            const float* row = dy + (int64_t)r * cols;
-            if (c0 + 0 < cols) acc.x += row[c0 + 0];
-            if (c0 + 1 < cols) acc.y += row[c0 + 1];
-            if (c0 + 2 < cols) acc.z += row[c0 + 2];
-            if (c0 + 3 < cols) acc.w += row[c0 + 3];
+            const T* row = dy + (int64_t)r * cols;
+            if (c0 + 0 < cols) acc.x += elem_f32(row, c0 + 0);
+            if (c0 + 1 < cols) acc.y += elem_f32(row, c0 + 1);
+            if (c0 + 2 < cols) acc.z += elem_f32(row, c0 + 2);
+            if (c0 + 3 < cols) acc.w += elem_f32(row, c0 + 3);
         }
     }
     red[wave][lane] = acc;
@@ -122,9 +135,10 @@ tf_status partial_rows_sum(tf_ctx* ctx, const float* part, float* out_lo, float*
 
 }  // namespace tfh
 
-extern "C" {
+namespace {
 
-tf_status tf_colsum(tf_ctx* ctx, const float* dy, float* db, int64_t rows, int64_t cols) {
+template <typename T>
+tf_status colsum_impl(tf_ctx* ctx, const T* dy, float* db, int64_t rows, int64_t cols) {
     TF_CTX_CHECK(ctx);
     TF_REQUIRE(rows >= 0 && cols >= 0 && rows < (1LL << 31) && cols < (1LL << 31), "tf_colsum: bad extent");
     if (cols == 0) return TF_OK;
@@ -140,11 +154,24 @@ tf_status tf_colsum(tf_ctx* ctx, const float* dy, float* db, int64_t rows, int64
     tf_status st = tfh::ensure_workspace(ctx, (size_t)chunks * cols * sizeof(float));
     if (st != TF_OK) return st;
     float* part = reinterpret_cast<float*>(ctx->ws);
-    int vec = (reinterpret_cast<uintptr_t>(dy) & 15) == 0 && cols % 4 == 0;
-    colsum_stage1<<<dim3(strips, (unsigned)chunks), 256, 0, ctx->stream>>>(dy, part, (int)rows, (int)cols, rpc, vec);
+    int vec = (reinterpret_cast<uintptr_t>(dy) & (4 * sizeof(T) - 1)) == 0 && cols % 4 == 0;
+    colsum_stage1<T><<<dim3(strips, (unsigned)chunks), 256, 0, ctx->stream>>>(dy, part, (int)rows, (int)cols, rpc,
+                                                                             vec);
     st = tfh::check_launch("colsum_stage1");
     if (st != TF_OK) return st;
     return tfh::partial_rows_sum(ctx, part, db, nullptr, chunks, cols, cols);
+}
+
+}  // namespace
+
+extern "C" {
+
+tf_status tf_colsum(tf_ctx* ctx, const float* dy, float* db, int64_t rows, int64_t cols) {
+    return colsum_impl(ctx, dy, db, rows, cols);
+}
+
+tf_status tf_colsum_bf16(tf_ctx* ctx, const void* dy, float* db, int64_t rows, int64_t cols) {
+    return colsum_impl(ctx, static_cast<const uint16_t*>(dy), db, rows, cols);
 }
 
 tf_status tf_chansum_nchw(tf_ctx* ctx, const float* dy, float* db, int64_t N, int64_t C, int64_t HW) {

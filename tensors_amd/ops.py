@@ -153,7 +153,8 @@ def colsum(dy, db):
     rows, cols = _rows_cols(dy)
     if db.size != cols:
         raise ValueError("colsum: db must have one entry per column")
-    call("tf_colsum", _ctx(dy), dy.ptr, db.ptr, rows, cols)
+    fn = "tf_colsum_bf16" if dy.tf_dtype == _lib.TF_BF16 else "tf_colsum"
+    call(fn, _ctx(dy), dy.ptr, db.ptr, rows, cols)
     return db
 
 

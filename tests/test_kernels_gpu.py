@@ -435,6 +435,22 @@ def test_colsum(ctx, R, Cc):
     assert_close(db.numpy(), oracle.colsum(dy), RTOL32, "colsum vs oracle")
 
 
+@pytest.mark.parametrize("R,Cc", [(2048, 2048), (4096, 8192), (17, 19), (1, 5), (3, 1001), (64, 258)])
+def test_colsum_bf16(ctx, R, Cc):
+    # bf16 dy summed in fp32: bit-exact against the fp32 colsum of the widened
+    # tensor (same order; widening is exact), and within fp32 tolerance of
+    # float64.
+    import tensors_amd as ta_mod
+    ops = _ops()
+    bits = ta_mod.f32_to_bf16_bits(synth.normal(171 + R, (R, Cc)))
+    wide = ta_mod.bf16_bits_to_f32(bits)
+    db16, db32 = ctx.empty((Cc,)), ctx.empty((Cc,))
+    ops.colsum(ctx.array(bits, ta_mod.BF16), db16)
+    ops.colsum(ctx.array(wide), db32)
+    assert np.array_equal(db16.numpy(), db32.numpy()), f"colsum_bf16 {R}x{Cc}"
+    assert_close(db16.numpy(), wide.astype(np.float64).sum(0), RTOL32, f"colsum_bf16 {R}x{Cc} vs float64")
+
+
 def test_colsum_zero_rows(ctx):
     ops = _ops()
     db = ctx.array(np.full(7, 3.0, np.float32))
