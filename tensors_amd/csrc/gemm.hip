@@ -43,6 +43,10 @@
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+// Native 4- and 2-float vectors (HIP's float4 is a struct whose copies lower
+// to memcpy, which keeps staging arrays out of registers).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 // Native 16-byte vector (HIP's uint4 is a struct whose copies lower to
 // memcpy, which keeps staging arrays out of registers).
@@ -69,6 +73,7 @@ struct GemmParams {
     int out_bf16;
     int vec_a, vec_b;      // 16-byte vector loads legal for A / B
     int pair_c;            // 8-byte paired stores legal for C
+    int vec_c4;            // 4-element vector stores legal for C (16 bytes fp32, 8 bytes bf16)
     uint32_t a_bytes, b_bytes;  // byte extent of one batch element of A / B (buffer loads)
     int int_m, int_n;           // large-tile path: tile rows / columns covered by the direct kernel
 };
@@ -669,62 +674,129 @@ struct DlOperand {
 };
 
 // Writes a 256 x 256 accumulator tile (bounds-checked when GUARD).
-template <bool GUARD>
+// Epilogue of the 256 x 256 kernels, staged through LDS: each wave writes
+// its raw accumulators, 64 rows x 128 columns at a time, into its own 32 KB
+// of LDS, then copies them out by whole rows (a lane takes 4 consecutive
+// columns, 32 lanes a row), applying alpha, beta * C, bias and ReLU per
+// 4-column vector, so C is written with 16-byte (fp32) or 8-byte (bf16)
+// stores of contiguous rows.  The copy loop is a run-time loop, so its body
+// (every output variant) exists twice in the code rather than once per row
+// group: writing the accumulators element by element from fully unrolled
+// code instead made the epilogue tens of kilobytes of straight-line code and
+// slower than the k loop of a 1000-deep GEMM.  Lane l, register r of
+// acc[i][j] is row 32i + 8(r/4) + 4(l/32) + r%4, column 32j + l%32 of the
+// wave block; static_for keeps every accumulator index a compile-time
+// constant (a runtime index would move the accumulators to scratch).  The
+// caller has synchronised the workgroup: `stage` (8192 floats) may alias
+// buffers the main loop used.
 __device__ __forceinline__ void big_epilogue(const GemmParams& p, v16f (&acc)[4][4], int m0, int n0, int split,
-                                             int batch) {
+                                             int batch, float* __restrict__ stage) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int wm = wave >> 1, wn = wave & 1;
     const int half = lane >> 5, l32 = lane & 31;
-    // Epilogue: lane l, register r of acc[i][j] is row 32i + 8(r/4) + 4(l/32)
-    // + r%4, column 32j + l%32 of the wave block.  static_for keeps every
-    // accumulator index a compile-time constant (a runtime index would move
-    // the accumulators to scratch memory); the output variant is chosen once
-    // outside the unrolled loops.
-    const int m_base = m0 + wm * 128 + 4 * half, n_base = n0 + wn * 128 + l32;
-    auto for_each = [&](auto&& st) TF_LAMBDA_INLINE {
-        static_for<4>([&](auto J) TF_LAMBDA_INLINE {
-            constexpr int j = decltype(J)::value;
-            const int col = n_base + 32 * j;
-            if (GUARD && col >= p.N) return;
-            static_for<4>([&](auto I) TF_LAMBDA_INLINE {
-                constexpr int i = decltype(I)::value;
+    const int lc = 4 * l32;  // this lane's 4 columns of a staged row
+    const int col = n0 + wn * 128 + lc;
+    float* part = p.partial ? p.partial + (int64_t)split * p.M * p.N : nullptr;
+    const bool has_bias = p.epi != TF_EPI_NONE && p.epi != TF_EPI_RELU;
+    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU || p.epi == TF_EPI_ROW_BIAS_RELU;
+    const float* row_bias = has_bias && p.row_bias ? p.bias : nullptr;
+    const bool vec = (part ? (p.N % 4 == 0) : p.vec_c4 != 0) && col + 4 <= p.N;
+    float cb[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) cb[e] = (has_bias && !p.row_bias && col + e < p.N) ? p.bias[col + e] : 0.0f;
+    const float alpha = p.alpha, beta = p.beta;
+    const int64_t ldc = p.ldc, boff = (int64_t)batch * p.stride_c;
+
+    // One staged vector: columns col .. col+3 of `row`.  LOADS: the general
+    // form (beta * C, row bias).  Without it the copy loop holds no global
+    // load: this GPU counts loads and stores in one counter, so any load in
+    // the loop makes the compiler wait for every store issued before it and
+    // serialises the loop on store latency.
+    auto out4 = [&](int row, f32x4 v, auto LOADS) TF_LAMBDA_INLINE {
+        constexpr bool loads = decltype(LOADS)::value;
+        if (part) {
+            float* dst = part + (int64_t)row * p.N + col;
+            if (vec) {
+                *reinterpret_cast<f32x4*>(dst) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (col + e < p.N) dst[e] = v[e];
+            }
+            return;
+        }
+        float rb = 0.0f;
+        if constexpr (loads) rb = row_bias ? row_bias[row] : 0.0f;
+        const int64_t off = boff + (int64_t)row * ldc + col;
+        f32x4 old = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (loads) {
+            if (beta != 0.0f) {
+                const float* c = reinterpret_cast<const float*>(p.C) + off;
+                if (vec) {
+                    old = *reinterpret_cast<const f32x4*>(c);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) old[e] = col + e < p.N ? c[e] : 0.0f;
+                }
+            }
+        }
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float t = alpha * v[e];
+            if (loads && beta != 0.0f) t += beta * old[e];
+            t += cb[e] + rb;
+            o[e] = relu ? fmaxf(t, 0.0f) : t;
+        }
+        if (p.out_bf16) {
+            uint16_t* c = reinterpret_cast<uint16_t*>(p.C) + off;
+            if (vec) {
+                const uint32_t lo = (uint32_t)tfd::f32_to_bf16(o[0]) | ((uint32_t)tfd::f32_to_bf16(o[1]) << 16);
+                const uint32_t hi = (uint32_t)tfd::f32_to_bf16(o[2]) | ((uint32_t)tfd::f32_to_bf16(o[3]) << 16);
+                *reinterpret_cast<uint2*>(c) = make_uint2(lo, hi);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (col + e < p.N) c[e] = tfd::f32_to_bf16(o[e]);
+            }
+        } else {
+            float* c = reinterpret_cast<float*>(p.C) + off;
+            if (vec) {
+                *reinterpret_cast<f32x4*>(c) = o;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (col + e < p.N) c[e] = o[e];
+            }
+        }
+    };
+    const bool general = !part && (beta != 0.0f || row_bias != nullptr);
+    static_for<2>([&](auto RND) TF_LAMBDA_INLINE {
+        constexpr int rnd = decltype(RND)::value;
+        // Sub-tile row blocks 2rnd, 2rnd + 1 -> staged rows 0 .. 63.
+        static_for<2>([&](auto II) TF_LAMBDA_INLINE {
+            constexpr int ii = decltype(II)::value;
+            static_for<4>([&](auto J) TF_LAMBDA_INLINE {
+                constexpr int j = decltype(J)::value;
                 static_for<16>([&](auto R) TF_LAMBDA_INLINE {
                     constexpr int r = decltype(R)::value;
-                    const int row = m_base + 32 * i + 8 * (r >> 2) + (r & 3);
-                    if (GUARD && row >= p.M) return;
-                    st(row, col, acc[i][j][r]);
+                    const int lrow = 32 * ii + 8 * (r >> 2) + 4 * half + (r & 3);
+                    stage[lrow * 128 + 32 * j + l32] = acc[2 * rnd + ii][j][r];
                 });
             });
         });
-    };
-    if (p.partial) {
-        float* part = p.partial + (int64_t)split * p.M * p.N;
-        for_each([&](int row, int col, float v) TF_LAMBDA_INLINE { part[(int64_t)row * p.N + col] = v; });
-        return;
-    }
-    const bool has_bias = p.epi != TF_EPI_NONE && p.epi != TF_EPI_RELU;
-    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU || p.epi == TF_EPI_ROW_BIAS_RELU;
-    const float* col_bias = has_bias && !p.row_bias ? p.bias : nullptr;
-    const float* row_bias = has_bias && p.row_bias ? p.bias : nullptr;
-    const float alpha = p.alpha;
-    const int64_t ldc = p.ldc;
-    if (p.beta == 0.0f && !p.out_bf16 && !has_bias && !relu) {
-        float* C = reinterpret_cast<float*>(p.C) + (int64_t)batch * p.stride_c;
-        for_each([&](int row, int col, float v) TF_LAMBDA_INLINE { C[(int64_t)row * ldc + col] = alpha * v; });
-    } else if (p.beta == 0.0f && p.out_bf16) {
-        uint16_t* C = reinterpret_cast<uint16_t*>(p.C) + (int64_t)batch * p.stride_c;
-        for_each([&](int row, int col, float v) TF_LAMBDA_INLINE {
-            v = alpha * v + (col_bias ? col_bias[col] : 0.0f) + (row_bias ? row_bias[row] : 0.0f);
-            if (relu) v = fmaxf(v, 0.0f);
-            C[(int64_t)row * ldc + col] = tfd::f32_to_bf16(v);
-        });
-    } else {
-        const int64_t batch_off_c = (int64_t)batch * p.stride_c;
-        for_each([&](int row, int col, float v) TF_LAMBDA_INLINE {
-            const float b = (col_bias ? col_bias[col] : 0.0f) + (row_bias ? row_bias[row] : 0.0f);
-            emit(p, batch_off_c + (int64_t)row * ldc + col, v, b, relu);
-        });
-    }
+        const int row0 = m0 + wm * 128 + 64 * rnd + half;
+        auto copy_out = [&](auto LOADS) TF_LAMBDA_INLINE {
+#pragma unroll 1
+            for (int pass = 0; pass < 32; ++pass) {
+                const int row = row0 + 2 * pass;
+                const f32x4 v = *reinterpret_cast<const f32x4*>(stage + (2 * pass + half) * 128 + lc);
+                if (row < p.M && col < p.N) out4(row, v, LOADS);
+            }
+        };
+        if (general) copy_out(std::true_type{});
+        else copy_out(std::false_type{});
+    });
 }
 
 // One 256 x 256 tile with register-staged, bounds-checked 64-deep blocks.
@@ -836,7 +908,9 @@ __device__ __forceinline__ void big_tile_guarded(const GemmParams& p, int m0, in
         block(kt, F{}, F{});
     }
 
-    big_epilogue<true>(p, acc, m0, n0, split, batch);
+    __syncthreads();  // the epilogue stages through the operand buffers (one 32 KB buffer per wave)
+    big_epilogue(p, acc, m0, n0, split, batch,
+                 reinterpret_cast<float*>(wave == 0 ? a0 : wave == 1 ? a1 : wave == 2 ? b0 : b1));
 }
 
 // Interior-tile kernel.  Per 32-deep block t (LDS buffer t % 5):
@@ -981,14 +1055,22 @@ void gemm_bf16_dl_kernel(GemmParams p) {
                 ++t;
             });
         }
-        // Block nk-1.
-        const int rlast = t % kDlBufs;
-        static_for<kDlBufs>([&](auto Bc) TF_LAMBDA_INLINE {
-            if (rlast == decltype(Bc)::value) block(Bc, t, std::true_type{});
-        });
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // drain the clamped loads before the waves end
+        // Block nk-1: one copy with its buffer chosen at run time (five
+        // unrolled copies, one per buffer, made the register allocator
+        // spill accumulators around them).
+        {
+            const int rlast = t % kDlBufs;
+            const u32x4* la = rlast == 0 ? s0 : rlast == 1 ? s1 : rlast == 2 ? s2 : rlast == 3 ? s3 : s4;
+            read(la, la + kDlVec, 1, f[1]);
+            big_mfma(f[0], acc);
+            __builtin_amdgcn_sched_barrier(0);
+            big_mfma(f[1], acc);
+        }
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // drain the clamped loads before the epilogue
     }
-    big_epilogue<true>(p, acc, m0, n0, split, batch);
+    __syncthreads();  // the epilogue stages through the ring buffers (one 32 KB buffer per wave)
+    big_epilogue(p, acc, m0, n0, split, batch,
+                 reinterpret_cast<float*>(wave == 0 ? s0 : wave == 1 ? s1 : wave == 2 ? s2 : s3));
 }
 
 // Edge-tile kernel (or every tile when the direct path does not apply):
@@ -1037,9 +1119,6 @@ void gemm_bf16_big_kernel(GemmParams p) {
 constexpr int kF32K = 32;
 constexpr int kF32LD = kF32K + 4;
 constexpr int kF32Stages = 3;
-// Native 4-float vector (HIP's float4 is a struct whose copies lower to
-// memcpy, which keeps staging arrays out of registers).
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <int ROWS, bool KMAJ, bool GUARD>
 struct F32Stage {
@@ -1290,7 +1369,6 @@ constexpr int kF32DlThreads = 512;
 constexpr int kF32DlStages = 4;
 constexpr int kF32DlOp = BM * kF32K;                                     // floats of one operand block
 constexpr int kF32DlLoads = kF32DlOp * 4 / 1024 / (kF32DlThreads / 64);  // 1 KB loads per wave per block
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ int f32dl_swz(int row) { return (row >> 1) & 7; }
 
@@ -1711,6 +1789,8 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     p.vec_a = aligned16(A) && (lda % vec_elems == 0) && (stride_a % vec_elems == 0);
     p.vec_b = aligned16(B) && (ldb % vec_elems == 0) && (stride_b % vec_elems == 0);
     p.pair_c = (reinterpret_cast<uintptr_t>(C) & 7) == 0 && (ldc % 2 == 0) && (p.stride_c % 2 == 0);
+    const uintptr_t c_vec_bytes = out_dtype == TF_BF16 ? 8 : 16;
+    p.vec_c4 = (reinterpret_cast<uintptr_t>(C) & (c_vec_bytes - 1)) == 0 && (ldc % 4 == 0) && (p.stride_c % 4 == 0);
     if (big) {
         // Interior tiles take the direct-to-LDS kernel when the operands are
         // 16-byte loadable, K is a whole number of 64-deep blocks (the split
