@@ -55,6 +55,20 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int BM = 128;
 constexpr int kThreads = 256;
 
+// Lambdas in the kernels must inline: an out-of-line lambda takes its
+// captures (accumulators, staging registers) through memory.
+#define TF_LAMBDA_INLINE __attribute__((always_inline))
+
+// Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 (compile-time unroll).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 struct GemmParams {
     const void* A;
     const void* B;
@@ -224,42 +238,63 @@ __device__ __forceinline__ void store_wave(const GemmParams& p, const v16f (&acc
     const bool has_bias = p.epi != TF_EPI_NONE && p.epi != TF_EPI_RELU;
     const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU || p.epi == TF_EPI_ROW_BIAS_RELU;
     float* part = p.partial ? p.partial + (int64_t)split * p.M * p.N : nullptr;
+    // LOADS: the general form (beta * C, row bias).  Without it no global
+    // load sits among the stores: this GPU counts loads and stores in one
+    // counter, so a wait for any load also waits for every earlier store.
+    auto body = [&](auto LOADS) TF_LAMBDA_INLINE {
+        constexpr bool loads = decltype(LOADS)::value;
 #pragma unroll
-    for (int j = 0; j < NSUB; ++j) {
-        if (B_PAIR && j == 1) break;  // paired columns are written together with j == 0
-        const int col = n_base + sub_row<B_PAIR>(j, l32);
-        const bool c0 = col < p.N, c1 = B_PAIR && col + 1 < p.N;
-        if (!c0) continue;
-        const bool col_bias = has_bias && !p.row_bias;
-        const float cb0 = col_bias ? p.bias[col] : 0.0f;
-        const float cb1 = (col_bias && c1) ? p.bias[col + 1] : 0.0f;
+        for (int j = 0; j < NSUB; ++j) {
+            if (B_PAIR && j == 1) break;  // paired columns are written together with j == 0
+            const int col = n_base + sub_row<B_PAIR>(j, l32);
+            const bool c0 = col < p.N, c1 = B_PAIR && col + 1 < p.N;
+            if (!c0) continue;
+            const bool col_bias = has_bias && !p.row_bias;
+            const float cb0 = col_bias ? p.bias[col] : 0.0f;
+            const float cb1 = (col_bias && c1) ? p.bias[col + 1] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            if (i_only >= 0 && i != i_only) continue;  // the other sub-tile row block is another wave's
+            for (int i = 0; i < 2; ++i) {
+                if (i_only >= 0 && i != i_only) continue;  // the other sub-tile row block is another wave's
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m_base + sub_row<A_PAIR>(i, 8 * (r >> 2) + 4 * half + (r & 3));
-                if (row >= p.M) continue;
-                const float rb = (has_bias && p.row_bias) ? p.bias[row] : 0.0f;
-                const float b0 = cb0 + rb, b1 = cb1 + rb;
-                if (part) {
-                    float* dst = part + (int64_t)row * p.N + col;
-                    dst[0] = acc[i][j][r];
-                    if (B_PAIR && c1) dst[1] = acc[i][1][r];
-                    continue;
-                }
-                const int64_t off = batch_off_c + (int64_t)row * p.ldc + col;
-                if (B_PAIR && c1 && p.pair_c && p.beta == 0.0f && !p.out_bf16) {
-                    float v0 = p.alpha * acc[i][0][r] + b0, v1 = p.alpha * acc[i][1][r] + b1;
-                    if (relu) { v0 = fmaxf(v0, 0.0f); v1 = fmaxf(v1, 0.0f); }
-                    *reinterpret_cast<float2*>(reinterpret_cast<float*>(p.C) + off) = make_float2(v0, v1);
-                } else {
-                    emit(p, off, acc[i][j][r], b0, relu);
-                    if (B_PAIR && c1) emit(p, off + 1, acc[i][1][r], b1, relu);
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m_base + sub_row<A_PAIR>(i, 8 * (r >> 2) + 4 * half + (r & 3));
+                    if (row >= p.M) continue;
+                    if (part) {
+                        float* dst = part + (int64_t)row * p.N + col;
+                        dst[0] = acc[i][j][r];
+                        if (B_PAIR && c1) dst[1] = acc[i][1][r];
+                        continue;
+                    }
+                    const int64_t off = batch_off_c + (int64_t)row * p.ldc + col;
+                    if constexpr (loads) {
+                        const float rb = (has_bias && p.row_bias) ? p.bias[row] : 0.0f;
+                        emit(p, off, acc[i][j][r], cb0 + rb, relu);
+                        if (B_PAIR && c1) emit(p, off + 1, acc[i][1][r], cb1 + rb, relu);
+                    } else {
+                        float v0 = p.alpha * acc[i][j][r] + cb0;
+                        float v1 = B_PAIR ? p.alpha * acc[i][1][r] + cb1 : 0.0f;
+                        if (relu) {
+                            v0 = fmaxf(v0, 0.0f);
+                            v1 = fmaxf(v1, 0.0f);
+                        }
+                        if (p.out_bf16) {
+                            uint16_t* c = reinterpret_cast<uint16_t*>(p.C) + off;
+                            c[0] = tfd::f32_to_bf16(v0);
+                            if (B_PAIR && c1) c[1] = tfd::f32_to_bf16(v1);
+                        } else if (B_PAIR && c1 && p.pair_c) {
+                            *reinterpret_cast<float2*>(reinterpret_cast<float*>(p.C) + off) = make_float2(v0, v1);
+                        } else {
+                            float* c = reinterpret_cast<float*>(p.C) + off;
+                            c[0] = v0;
+                            if (B_PAIR && c1) c[1] = v1;
+                        }
+                    }
                 }
             }
         }
-    }
+    };
+    if (p.partial == nullptr && (p.beta != 0.0f || (has_bias && p.row_bias))) body(std::true_type{});
+    else body(std::false_type{});
 }
 
 // ---------------------------------------------------------------------------
@@ -399,21 +434,7 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(GemmParams p) {
 constexpr int kBigTile = 256;
 constexpr int kBigK = 64;
 
-// Lambdas in the large-tile kernel must inline: an out-of-line lambda takes
-// its captures (accumulators, staging registers) through memory.
-#define TF_LAMBDA_INLINE __attribute__((always_inline))
-
 __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
-
-// Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 (compile-time unroll).
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
 
 // One 16-byte chunk of bf16 values at p[0 .. 7] with elements i >= n read as
 // zero (n <= 0: all zero).
