@@ -85,11 +85,12 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // bf16 <-> f32, round to nearest even; NaN stays NaN (quiet bit forced).
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
-    uint32_t lsb = (u >> 16) & 1u;
-    u += 0x7fffu + lsb;
-    return (uint16_t)(u >> 16);
+    // Round to nearest even; a NaN keeps its top bits and is made quiet.
+    // Written as a select so the compiler emits no branch.
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t quiet = (u >> 16) | 0x40u;
+    return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {

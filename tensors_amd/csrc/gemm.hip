@@ -728,14 +728,17 @@ __device__ __forceinline__ void big_epilogue(const GemmParams& p, v16f (&acc)[4]
     const float alpha = p.alpha, beta = p.beta;
     const int64_t ldc = p.ldc, boff = (int64_t)batch * p.stride_c;
 
-    // One staged vector: columns col .. col+3 of `row`.  LOADS: the general
-    // form (beta * C, row bias).  Without it the copy loop holds no global
+    // One staged vector: columns col .. col+3 of `row`.  The output form is
+    // fixed per loop (template flags) so the copy loop carries no branches on
+    // it.  PART: split-K partial (fp32, leading dimension N).  LOADS: the
+    // general form (beta * C, row bias); without it the loop holds no global
     // load: this GPU counts loads and stores in one counter, so any load in
     // the loop makes the compiler wait for every store issued before it and
     // serialises the loop on store latency.
-    auto out4 = [&](int row, f32x4 v, auto LOADS) TF_LAMBDA_INLINE {
+    auto out4 = [&](int row, f32x4 v, auto PART, auto BF16, auto LOADS) TF_LAMBDA_INLINE {
+        constexpr bool is_part = decltype(PART)::value, bf16 = decltype(BF16)::value;
         constexpr bool loads = decltype(LOADS)::value;
-        if (part) {
+        if constexpr (is_part) {
             float* dst = part + (int64_t)row * p.N + col;
             if (vec) {
                 *reinterpret_cast<f32x4*>(dst) = v;
@@ -765,11 +768,11 @@ __device__ __forceinline__ void big_epilogue(const GemmParams& p, v16f (&acc)[4]
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             float t = alpha * v[e];
-            if (loads && beta != 0.0f) t += beta * old[e];
+            if (loads) t += beta * old[e];
             t += cb[e] + rb;
             o[e] = relu ? fmaxf(t, 0.0f) : t;
         }
-        if (p.out_bf16) {
+        if constexpr (bf16) {
             uint16_t* c = reinterpret_cast<uint16_t*>(p.C) + off;
             if (vec) {
                 const uint32_t lo = (uint32_t)tfd::f32_to_bf16(o[0]) | ((uint32_t)tfd::f32_to_bf16(o[1]) << 16);
@@ -792,6 +795,8 @@ __device__ __forceinline__ void big_epilogue(const GemmParams& p, v16f (&acc)[4]
         }
     };
     const bool general = !part && (beta != 0.0f || row_bias != nullptr);
+    using T_ = std::true_type;
+    using F_ = std::false_type;
     static_for<2>([&](auto RND) TF_LAMBDA_INLINE {
         constexpr int rnd = decltype(RND)::value;
         // Sub-tile row blocks 2rnd, 2rnd + 1 -> staged rows 0 .. 63.
@@ -807,16 +812,24 @@ __device__ __forceinline__ void big_epilogue(const GemmParams& p, v16f (&acc)[4]
             });
         });
         const int row0 = m0 + wm * 128 + 64 * rnd + half;
-        auto copy_out = [&](auto LOADS) TF_LAMBDA_INLINE {
-#pragma unroll 1
+        // The LDS read of pass + 1 is issued before pass is written out, so
+        // its latency overlaps the conversion and store.
+        const float* src = stage + half * 128 + lc;
+        auto copy_out = [&](auto PART, auto BF16, auto LOADS) TF_LAMBDA_INLINE {
+            f32x4 next = *reinterpret_cast<const f32x4*>(src);
+#pragma unroll 2
             for (int pass = 0; pass < 32; ++pass) {
+                const f32x4 v = next;
+                next = *reinterpret_cast<const f32x4*>(src + min(pass + 1, 31) * 256);
                 const int row = row0 + 2 * pass;
-                const f32x4 v = *reinterpret_cast<const f32x4*>(stage + (2 * pass + half) * 128 + lc);
-                if (row < p.M && col < p.N) out4(row, v, LOADS);
+                if (row < p.M && col < p.N) out4(row, v, PART, BF16, LOADS);
             }
         };
-        if (general) copy_out(std::true_type{});
-        else copy_out(std::false_type{});
+        if (part) copy_out(T_{}, F_{}, F_{});
+        else if (general && p.out_bf16) copy_out(F_{}, T_{}, T_{});  // row bias (beta != 0 needs an fp32 C)
+        else if (general) copy_out(F_{}, F_{}, T_{});
+        else if (p.out_bf16) copy_out(F_{}, T_{}, F_{});
+        else copy_out(F_{}, F_{}, F_{});
     });
 }
 
