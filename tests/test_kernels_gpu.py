@@ -227,6 +227,58 @@ def test_gemm_f32_large_tile_epilogues(ctx):
     assert_close(got, _gemm_truth(a, b, False, True, 0.5, 0.25, c0), RTOL32, "fp32 128-tile alpha/beta")
 
 
+def _row_bias_truth(a, b, ta, tb, bias, relu):
+    out = _gemm_truth(a, b, ta, tb) + bias.astype(np.float64)[:, None]
+    return np.maximum(out, 0.0) if relu else out
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_gemm_large_tile_row_bias(ctx, dt):
+    # Row-bias epilogue (conv-forward form) on the large-tile kernels: the
+    # fp32 direct kernel, and the general copy path of the 256 x 256 bf16
+    # kernel with bf16 and fp32 output; ragged N for the edge tiles.
+    import tensors_amd as ta_mod
+    from tensors_amd import ops
+    from tensors_amd._lib import TF_EPI_ROW_BIAS_RELU
+    M, N, K = (2048, 2052, 128) if dt == "f32" else (4096, 4100, 128)
+    a = synth.normal(101, (M, K))
+    b = synth.normal(102, (N, K))
+    bias = synth.normal(103, (M,))
+    if dt == "bf16":
+        a16, b16 = ta_mod.f32_to_bf16_bits(a), ta_mod.f32_to_bf16_bits(b)
+        a, b = ta_mod.bf16_bits_to_f32(a16), ta_mod.bf16_bits_to_f32(b16)
+        da, db = ctx.array(a16, ta_mod.BF16), ctx.array(b16, ta_mod.BF16)
+        outs = [np.float32, ta_mod.BF16]
+    else:
+        da, db = ctx.array(a), ctx.array(b)
+        outs = [np.float32]
+    dbias = ctx.array(bias)
+    truth = _row_bias_truth(a, b, False, True, bias, True)
+    for odt in outs:
+        dc = ctx.zeros((M, N), odt)
+        ops.gemm_ex(da, db, dc, M, N, K, lda=K, ldb=K, ldc=N, trans_b=True, epilogue=TF_EPI_ROW_BIAS_RELU,
+                    bias=dbias)
+        f32_out = odt is np.float32
+        got = dc.numpy() if f32_out else ta_mod.bf16_bits_to_f32(dc.numpy())
+        assert_close(got, truth, RTOL32 if f32_out else RTOL16,
+                     f"{dt} in, {'fp32' if f32_out else 'bf16'} out, row bias + relu")
+
+
+def test_gemm_bf16_large_tile_beta_split(ctx):
+    # alpha / beta with an fp32 C on the 256 x 256 kernel when K is split
+    # (few tiles, long K): partial sums, then the reduction's epilogue.
+    import tensors_amd as ta_mod
+    from tensors_amd import ops
+    M, N, K = 512, 512, 8192
+    a16 = ta_mod.f32_to_bf16_bits(synth.normal(111, (M, K)))
+    b16 = ta_mod.f32_to_bf16_bits(synth.normal(112, (K, N)))
+    a, b = ta_mod.bf16_bits_to_f32(a16), ta_mod.bf16_bits_to_f32(b16)
+    c0 = synth.normal(113, (M, N))
+    dc = ctx.array(c0)
+    ops.gemm(ctx.array(a16, ta_mod.BF16), ctx.array(b16, ta_mod.BF16), dc, alpha=0.5, beta=0.25)
+    assert_close(dc.numpy(), _gemm_truth(a, b, False, False, 0.5, 0.25, c0), RTOL32, "bf16 split-K alpha/beta")
+
+
 def test_gemm_f32_large_tile_reduce_batch(ctx):
     # C = sum_b A_b^T B_b (weight-gradient form) with 128 x 128 tiles.
     from tensors_amd import ops
