@@ -1030,11 +1030,10 @@ void gemm_bf16_dl_kernel(GemmParams p) {
         // Every block but the last loads block t+5 (clamped to the last real
         // block: loads past the end land in buffers nobody reads again), so
         // exactly three blocks of loads are outstanding behind block t+1's
-        // at each wait and all blocks have the same shape.  LAST: no next
-        // block, so no wait, barrier, loads or next-block reads.
-        auto block = [&](auto Bc, int t, auto LAST) TF_LAMBDA_INLINE {
+        // at each wait and all blocks have the same shape.  The last block
+        // (no wait, barrier, loads or next-block reads) follows the loop.
+        auto block = [&](auto Bc, int t) TF_LAMBDA_INLINE {
             constexpr int b = decltype(Bc)::value;
-            constexpr bool last = decltype(LAST)::value;
             u32x4* la = buf_a(Bc);
             u32x4* lb = buf_b(Bc);
             u32x4* na = buf_a(std::integral_constant<int, (b + 1) % kDlBufs>{});
@@ -1046,27 +1045,21 @@ void gemm_bf16_dl_kernel(GemmParams p) {
                 __builtin_amdgcn_sched_group_barrier(0x100, kReads / 8, 0);  // DS read
             });
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (!last) {
-                dl_barrier<3 * 2 * kDlLoads>();  // block t+1 has landed; block t fully read
-                issue(kb_beg + min(t + kDlBufs, nk - 1), la, lb);
-            }
+            dl_barrier<3 * 2 * kDlLoads>();  // block t+1 has landed; block t fully read
+            issue(kb_beg + min(t + kDlBufs, nk - 1), la, lb);
             big_mfma_part<0, 4>(f[1], acc);
-            if constexpr (!last) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x010, kDlLoads, 0);  // VMEM
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x010, kDlLoads, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x010, kDlLoads, 0);  // VMEM
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x010, kDlLoads, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (!last) read(na, nb, 0, f[0]);
+            read(na, nb, 0, f[0]);
             big_mfma_part<4, 16>(f[1], acc);
-            if constexpr (!last) {
-                static_for<4>([&](auto) TF_LAMBDA_INLINE {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);           // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x100, kReads / 4, 0);  // DS read
-                });
-            }
+            static_for<4>([&](auto) TF_LAMBDA_INLINE {
+                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);           // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, kReads / 4, 0);  // DS read
+            });
             __builtin_amdgcn_sched_barrier(0);
         };
         // Prologue: blocks 0 .. 4 (clamped) into buffers 0 .. 4, wait for block 0.
@@ -1085,7 +1078,7 @@ void gemm_bf16_dl_kernel(GemmParams p) {
                     stop = true;
                     return;
                 }
-                block(Bc, t, std::false_type{});
+                block(Bc, t);
                 ++t;
             });
         }
