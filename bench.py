@@ -69,8 +69,7 @@ def bench_c2(steps: int, warmup: int):
         rec(3)
         ops.colsum(dY, db)
         rec(4)
-        ops.sgd_momentum(W, dW, vW, lr, mu)
-        ops.sgd_momentum(b, db, vb, lr, mu)
+        ops.sgd_momentum_multi([W, b], [dW, db], [vW, vb], lr, mu)
         rec(5)
 
     for _ in range(warmup):
@@ -264,8 +263,7 @@ def probe(steps: int = 5) -> None:
         ops.gemm(dY, W, dX)
         ops.gemm(dY, X, dW, trans_a=True)
         ops.colsum(dY, db)
-        ops.sgd_momentum(W, dW, vW, 1e-3, 0.9)
-        ops.sgd_momentum(b, db, vb, 1e-3, 0.9)
+        ops.sgd_momentum_multi([W, b], [dW, db], [vW, vb], 1e-3, 0.9)
     ctx.sync()
     ca, cb, cc = ctx.zeros((PROBE_CAL_N,)), ctx.zeros((PROBE_CAL_N,)), ctx.empty((PROBE_CAL_N,))
     for _ in range(3):

@@ -277,6 +277,13 @@ tf_status tf_transpose2d(tf_ctx* ctx, const void* x, void* out, int64_t batch, i
  * ------------------------------------------------------------------------- */
 tf_status tf_sgd_momentum(tf_ctx* ctx, float* p, const float* g, float* v,
                           void* p_bf16, int64_t n, float lr, float mu);
+/* The same update for `count` parameters in one launch (the per-parameter
+ * loop of nn/optim/SGD.cpp:50-56): entry i is (p[i], g[i], v[i], p_bf16[i],
+ * n[i]); v and p_bf16 may be NULL arrays (no velocity / no shadows) or hold
+ * NULL entries.  Each parameter ends up as tf_sgd_momentum leaves it. */
+#define TF_SGD_MULTI_MAX 32
+tf_status tf_sgd_momentum_multi(tf_ctx* ctx, int count, float* const* p, const float* const* g,
+                                float* const* v, void* const* p_bf16, const int64_t* n, float lr, float mu);
 
 /* float32 <-> bf16 conversion (round to nearest even). */
 tf_status tf_cast_f32_bf16(tf_ctx* ctx, const float* x, void* y, int64_t n);

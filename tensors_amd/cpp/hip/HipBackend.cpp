@@ -394,4 +394,34 @@ void sgd_momentum(Tensor& p, const Tensor& g, Tensor* v, Tensor* shadow, float l
           "hip::sgd");
 }
 
+void sgd_momentum_multi(std::vector<SgdItem>& items, float lr, float mu) {
+    size_t i = 0;
+    while (i < items.size()) {
+        // A run of up to TF_SGD_MULTI_MAX parameters on one device.
+        tf_ctx* ctx = ctx_of(*items[i].p);
+        float* ps[TF_SGD_MULTI_MAX];
+        const float* gs[TF_SGD_MULTI_MAX];
+        float* vs[TF_SGD_MULTI_MAX];
+        void* ss[TF_SGD_MULTI_MAX];
+        int64_t ns[TF_SGD_MULTI_MAX];
+        int count = 0;
+        for (; i < items.size() && count < TF_SGD_MULTI_MAX && ctx_of(*items[i].p) == ctx; ++i, ++count) {
+            SgdItem& it = items[i];
+            Tensor& p = *it.p;
+            require_gpu(p, "hip::sgd"); require_gpu(it.g, "hip::sgd");
+            require(p.dtype() == Dtype::Float32 && it.g.dtype() == Dtype::Float32 && p.numel() == it.g.numel(),
+                    "hip::sgd: p and g must be Float32 of equal size");
+            if (it.v) require(it.v->numel() == p.numel() && it.v->dtype() == Dtype::Float32, "hip::sgd: velocity size");
+            if (it.shadow.numel())
+                require(it.shadow.numel() == p.numel() && it.shadow.dtype() == Dtype::BFloat16, "hip::sgd: shadow");
+            ps[count] = static_cast<float*>(p.data());
+            gs[count] = static_cast<const float*>(it.g.data());
+            vs[count] = it.v ? static_cast<float*>(it.v->data()) : nullptr;
+            ss[count] = it.shadow.numel() ? it.shadow.data() : nullptr;
+            ns[count] = p.numel();
+        }
+        check(tf_sgd_momentum_multi(ctx, count, ps, gs, vs, ss, ns, lr, mu), "hip::sgd");
+    }
+}
+
 }  // namespace tensorforge::hip

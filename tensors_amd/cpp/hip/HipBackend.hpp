@@ -13,6 +13,8 @@
 #include "tensor/CPUStorageAllocator.hpp"
 #include "tensor/Tensor.hpp"
 
+#include <vector>
+
 #include <cstddef>
 #include <cstdint>
 
@@ -92,5 +94,14 @@ void col2im(const Tensor& col, Tensor& dx, int64_t kH, int64_t kW, int64_t sh, i
 // Fused v = mu*v + g; p -= lr*v (mu == 0: p -= lr*g); shadow (BFloat16, may
 // be nullptr) receives bf16(p).
 void sgd_momentum(Tensor& p, const Tensor& g, Tensor* v, Tensor* shadow, float lr, float mu);
+// The same update for several parameters, one launch per 32 parameters of
+// one device (tf_sgd_momentum_multi).  v / shadow: nullptr or as above.
+struct SgdItem {
+    Tensor* p;
+    Tensor g;
+    Tensor* v;
+    Tensor shadow;  // empty: none
+};
+void sgd_momentum_multi(std::vector<SgdItem>& items, float lr, float mu);
 
 }  // namespace tensorforge::hip

@@ -20,6 +20,11 @@ SGD::SGD(std::vector<Tensor*> parameters, float lr, float momentum)
 }
 
 void SGD::step() {
+    // GPU parameters are updated together (one launch per 32 parameters of a
+    // device, hip::sgd_momentum_multi); nn/optim/SGD.cpp:50-56 updates them one
+    // by one, and each ends up the same either way.
+    std::vector<hip::SgdItem> batch;
+    batch.reserve(parameters_.size());
     for (size_t i = 0; i < parameters_.size(); ++i) {
         Tensor& p = *parameters_[i];
         Tensor g = p.grad();
@@ -34,10 +39,7 @@ void SGD::step() {
             v = &velocity_[i];
         }
         if (p.device().type == DeviceType::CUDA) {
-            Tensor shadow = hip::find_shadow(p);
-            hip::sgd_momentum(p, g, v, shadow.numel() ? &shadow : nullptr, lr_, momentum_);
-            (void)p.bump_version();
-            if (shadow.numel()) hip::mark_shadow_current(p);
+            batch.push_back(hip::SgdItem{&p, g, v, hip::find_shadow(p)});
         } else {
             float* pp = static_cast<float*>(p.data());
             const float* gp = static_cast<const float*>(g.data());
@@ -54,6 +56,13 @@ void SGD::step() {
                 }
             }
             (void)p.bump_version();
+        }
+    }
+    if (!batch.empty()) {
+        hip::sgd_momentum_multi(batch, lr_, momentum_);
+        for (const hip::SgdItem& it : batch) {
+            (void)it.p->bump_version();
+            if (it.shadow.numel()) hip::mark_shadow_current(*it.p);
         }
     }
 }

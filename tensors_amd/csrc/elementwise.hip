@@ -263,6 +263,94 @@ __global__ __launch_bounds__(256) void sgd_momentum_kernel(float* __restrict__ p
     }
 }
 
+// Scalar SGD step of one element (the tail of the vector kernels).
+__device__ __forceinline__ float sgd1(float pv, float gv, float* vp, bool use_v, float lr, float mu) {
+#pragma clang fp contract(off)
+    if (use_v) {
+        const float vm = *vp * mu;
+        const float vn = vm + gv;
+        *vp = vn;
+        const float step = vn * lr;
+        return pv - step;
+    }
+    const float step = lr * gv;
+    return pv - step;
+}
+
+// Several parameters in one launch (an optimiser's whole step).  Work units
+// of kSgdUnit consecutive elements of one tensor; unit u belongs to tensor t
+// with unit_start[t] <= u < unit_start[t + 1].  The element update is the
+// one of sgd_momentum_kernel (sgd4 / sgd1), so each tensor ends up exactly
+// as tf_sgd_momentum would leave it.
+constexpr int kSgdUnit = 2048;  // 256 threads x 2 float4
+struct SgdMultiArgs {
+    float* p[TF_SGD_MULTI_MAX];
+    const float* g[TF_SGD_MULTI_MAX];
+    float* v[TF_SGD_MULTI_MAX];
+    uint16_t* s[TF_SGD_MULTI_MAX];
+    int64_t n[TF_SGD_MULTI_MAX];
+    int64_t unit_start[TF_SGD_MULTI_MAX + 1];
+    int vec_ok[TF_SGD_MULTI_MAX];
+    int count;
+};
+
+__global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdMultiArgs a, float lr, float mu) {
+#pragma clang fp contract(off)
+    const bool use_v = mu != 0.0f;
+    const int64_t units = a.unit_start[a.count];
+    for (int64_t u = blockIdx.x; u < units; u += gridDim.x) {
+        int t = 0;
+        while (u >= a.unit_start[t + 1]) ++t;
+        const int64_t e0 = (u - a.unit_start[t]) * kSgdUnit;
+        const int64_t e1 = min(a.n[t], e0 + kSgdUnit);
+        float* p = a.p[t];
+        const float* g = a.g[t];
+        float* v = a.v[t];
+        uint16_t* s = a.s[t];
+        int64_t js = e0;  // first element of the scalar part
+        if (a.vec_ok[t]) {
+            float4* P = reinterpret_cast<float4*>(p);
+            const float4* G = reinterpret_cast<const float4*>(g);
+            float4* V = reinterpret_cast<float4*>(v);
+            const int64_t vend = e1 / 4;  // e0 is a multiple of 4
+            const int64_t i0 = e0 / 4 + threadIdx.x, i1 = i0 + 256;
+            const bool ok0 = i0 < vend, ok1 = i1 < vend;
+            float4 pp0, gg0, vv0 = make_float4(0.f, 0.f, 0.f, 0.f), pp1, gg1, vv1 = vv0;
+            if (ok0) {
+                pp0 = P[i0];
+                gg0 = G[i0];
+                if (use_v) vv0 = V[i0];
+            }
+            if (ok1) {
+                pp1 = P[i1];
+                gg1 = G[i1];
+                if (use_v) vv1 = V[i1];
+            }
+            auto finish = [&](int64_t i, float4& pp, const float4& gg, float4& vv) {
+                sgd4(pp, gg, vv, use_v, lr, mu);
+                P[i] = pp;
+                if (use_v) V[i] = vv;
+                if (s) {
+                    ushort4 h;
+                    h.x = f32_to_bf16(pp.x);
+                    h.y = f32_to_bf16(pp.y);
+                    h.z = f32_to_bf16(pp.z);
+                    h.w = f32_to_bf16(pp.w);
+                    reinterpret_cast<ushort4*>(s)[i] = h;
+                }
+            };
+            if (ok0) finish(i0, pp0, gg0, vv0);
+            if (ok1) finish(i1, pp1, gg1, vv1);
+            js = vend * 4;
+        }
+        for (int64_t j = js + threadIdx.x; j < e1; j += 256) {
+            const float pv = sgd1(p[j], g[j], use_v ? v + j : nullptr, use_v, lr, mu);
+            p[j] = pv;
+            if (s) s[j] = f32_to_bf16(pv);
+        }
+    }
+}
+
 // Casts: 8 elements per iteration (two float4 <-> one 16-byte bf16 vector)
 // when both pointers are 16-byte aligned; scalar for the rest.
 __global__ __launch_bounds__(256) void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y,
@@ -354,6 +442,41 @@ tf_status tf_sgd_momentum(tf_ctx* ctx, float* p, const float* g, float* v, void*
     sgd_momentum_kernel<<<tfd::grid_for(n, 4 * 2), 256, 0, ctx->stream>>>(
         p, g, v, (uint16_t*)p_bf16, n, lr, mu, vec_ok);
     return tfh::check_launch("sgd_momentum_kernel");
+}
+
+tf_status tf_sgd_momentum_multi(tf_ctx* ctx, int count, float* const* p, const float* const* g, float* const* v,
+                                void* const* p_bf16, const int64_t* n, float lr, float mu) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(count >= 0 && count <= TF_SGD_MULTI_MAX, "tf_sgd_momentum_multi: count must lie in [0, 32]");
+    if (count == 0) return TF_OK;
+    TF_REQUIRE(p && g && n, "tf_sgd_momentum_multi: null p, g or n array");
+    TF_REQUIRE(mu >= 0.0f && mu < 1.0f, "tf_sgd_momentum_multi: momentum must lie in [0, 1)");
+    SgdMultiArgs a{};
+    int64_t units = 0;
+    int m = 0;
+    for (int i = 0; i < count; ++i) {
+        TF_REQUIRE(n[i] >= 0, "tf_sgd_momentum_multi: negative n");
+        if (n[i] == 0) continue;
+        TF_REQUIRE(p[i] && g[i], "tf_sgd_momentum_multi: null p or g");
+        float* vi = v ? v[i] : nullptr;
+        TF_REQUIRE(mu == 0.0f || vi != nullptr, "tf_sgd_momentum_multi: momentum needs a velocity buffer");
+        void* si = p_bf16 ? p_bf16[i] : nullptr;
+        a.p[m] = p[i];
+        a.g[m] = g[i];
+        a.v[m] = vi;
+        a.s[m] = static_cast<uint16_t*>(si);
+        a.n[m] = n[i];
+        a.vec_ok[m] = aligned16<char>(p[i]) && aligned16<char>(g[i]) && (vi == nullptr || aligned16<char>(vi)) &&
+                      (si == nullptr || (reinterpret_cast<uintptr_t>(si) & 7) == 0);
+        a.unit_start[m] = units;
+        units += (n[i] + kSgdUnit - 1) / kSgdUnit;
+        ++m;
+    }
+    a.unit_start[m] = units;
+    a.count = m;
+    if (units == 0) return TF_OK;
+    sgd_multi_kernel<<<(unsigned)std::min<int64_t>(units, 16384), 256, 0, ctx->stream>>>(a, lr, mu);
+    return tfh::check_launch("sgd_multi_kernel");
 }
 
 tf_status tf_cast_f32_bf16(tf_ctx* ctx, const float* x, void* y, int64_t n) {

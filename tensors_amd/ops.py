@@ -175,6 +175,31 @@ def sgd_momentum(p, g, v, lr, mu, p_bf16=None):
     return p
 
 
+SGD_MULTI_MAX = 32
+
+
+def sgd_momentum_multi(ps, gs, vs, lr, mu, shadows=None):
+    """One launch for several parameters: entry i as sgd_momentum(ps[i], gs[i],
+    vs[i], lr, mu, shadows[i]); vs / shadows may be None or hold None."""
+    import ctypes as C
+    count = len(ps)
+    if count > SGD_MULTI_MAX or len(gs) != count or (vs is not None and len(vs) != count) or \
+            (shadows is not None and len(shadows) != count):
+        raise ValueError("sgd_momentum_multi: mismatched or too many parameter lists")
+    if count == 0:
+        return ps
+    ns = [(_same(p, g) if vs is None or vs[i] is None else _same(p, g, vs[i])) for i, (p, g) in enumerate(zip(ps, gs))]
+    arr = lambda xs: (C.c_void_p * count)(*[x.ptr if x is not None else None for x in xs])
+    p_arr, g_arr = arr(ps), arr(gs)
+    v_arr = arr(vs) if vs is not None else None
+    s_arr = arr(shadows) if shadows is not None else None
+    n_arr = (C.c_int64 * count)(*ns)
+    call("tf_sgd_momentum_multi", _ctx(ps[0]), count, C.cast(p_arr, C.c_void_p), C.cast(g_arr, C.c_void_p),
+         C.cast(v_arr, C.c_void_p) if v_arr is not None else None,
+         C.cast(s_arr, C.c_void_p) if s_arr is not None else None, C.cast(n_arr, C.c_void_p), lr, mu)
+    return ps
+
+
 def gemm_ex(a, b, c, M, N, K, *, lda, ldb, ldc, trans_a=False, trans_b=False, stride_a=0, stride_b=0, stride_c=0,
             batch=1, reduce_batch=False, alpha=1.0, beta=0.0, epilogue=_lib.TF_EPI_NONE, bias=None):
     """Raw tf_gemm_ex on DeviceArrays (extents and strides in elements; the

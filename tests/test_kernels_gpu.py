@@ -537,3 +537,45 @@ def test_sgd_momentum_bitexact(ctx, n, mu):
     assert_bitexact(dp.numpy(), p, "sgd p")
     assert_bitexact(dv.numpy(), v, "sgd v")
     assert_bitexact(sh.numpy(), ta_mod.f32_to_bf16_bits(p), "bf16 shadow")
+
+
+class _OffsetView:
+    """n float32 elements `offset` elements into a DeviceArray (not owned)."""
+
+    def __init__(self, base, offset, n):
+        from tensors_amd.device import DeviceArray
+        self._base = base
+        self.ctx, self.shape, self.dtype, self.size = base.ctx, (n,), np.float32, n
+        self.nbytes = 4 * n
+        self.ptr = base.ptr + 4 * offset
+        self.tf_dtype = base.tf_dtype
+        self.numpy = lambda: DeviceArray.numpy(self)
+
+
+@pytest.mark.parametrize("mu", [0.9, 0.0])
+def test_sgd_momentum_multi_bitexact(ctx, mu):
+    # One launch over several parameters (ragged sizes, an unaligned one,
+    # with and without a bf16 shadow) equals the oracle step of each.
+    import tensors_amd as ta_mod
+    ops = _ops()
+    sizes = [2048, 7, 1, 235146, 2049, 1 << 20, 0]
+    ps = [synth.normal(181 + i, (n,)) for i, n in enumerate(sizes)]
+    gs = [synth.normal(191 + i, (n,)) for i, n in enumerate(sizes)]
+    vs = [synth.normal(201 + i, (n,)) for i, n in enumerate(sizes)]
+    dps = [ctx.array(x) for x in ps]
+    dgs = [ctx.array(x) for x in gs]
+    dvs = [ctx.array(x) for x in vs]
+    # An unaligned parameter: a view one float into a larger buffer.
+    base = ctx.array(np.concatenate([np.zeros(1, np.float32), ps[1]]))
+    dps[1] = _OffsetView(base, 1, sizes[1])
+    shs = [ctx.empty((n,), ta_mod.BF16) if i % 2 == 0 else None for i, n in enumerate(sizes)]
+    for _ in range(3):
+        ops.sgd_momentum_multi(dps, dgs, dvs if mu != 0.0 else None, 0.1, mu, shadows=shs)
+        for i in range(len(sizes)):
+            ps[i], vs[i] = oracle.sgd_momentum(ps[i], gs[i], vs[i], 0.1, mu)
+    for i, n in enumerate(sizes):
+        assert_bitexact(dps[i].numpy(), ps[i], f"multi sgd p[{i}] n={n}")
+        if mu != 0.0:
+            assert_bitexact(dvs[i].numpy(), vs[i], f"multi sgd v[{i}] n={n}")
+        if shs[i] is not None:
+            assert_bitexact(shs[i].numpy(), ta_mod.f32_to_bf16_bits(ps[i]), f"multi sgd shadow[{i}]")
