@@ -97,6 +97,55 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return __uint_as_float(((uint32_t)h) << 16);
 }
 
+// Streaming accesses (global_load / global_store ... nt) for data a kernel
+// touches once.  The non-temporal hint lets the caches evict these lines
+// first.  On this GPU it raised a 16 MB copy from 4.5 to 4.9 TB/s, two reads
+// plus a write from 4.7 to 5.5 TB/s, and three reads plus two writes (SGD)
+// from 4.8 to 5.6 TB/s.  The event-timed microbenchmark rotated buffers past
+// the 256 MB last-level cache.
+typedef unsigned int nt_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int nt_u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ld_nt(const uint4* p) {
+    const nt_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_nt(uint4* p, const uint4& v) {
+    __builtin_nontemporal_store(nt_u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<nt_u32x4*>(p));
+}
+__device__ __forceinline__ float4 ld_nt(const float4* p) {
+    const nt_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4*>(p));
+    return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+__device__ __forceinline__ void st_nt(float4* p, const float4& v) {
+    __builtin_nontemporal_store(nt_u32x4{__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
+                                         __float_as_uint(v.w)},
+                                reinterpret_cast<nt_u32x4*>(p));
+}
+__device__ __forceinline__ uint2 ld_nt(const uint2* p) {
+    const nt_u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x2*>(p));
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ void st_nt(uint2* p, const uint2& v) {
+    __builtin_nontemporal_store(nt_u32x2{v.x, v.y}, reinterpret_cast<nt_u32x2*>(p));
+}
+// The same with the hint chosen at compile time.
+template <bool NT, typename V>
+__device__ __forceinline__ V ld_v(const V* p) {
+    if constexpr (NT) return ld_nt(p);
+    else return *p;
+}
+template <bool NT, typename V>
+__device__ __forceinline__ void st_v(V* p, const V& v) {
+    if constexpr (NT) st_nt(p, v);
+    else *p = v;
+}
+// Launches that move more than this many bytes cannot keep their data in the
+// 256 MB last-level cache between uses; below it (e.g. a small model's
+// parameters, read again every step) cached accesses are faster: the SGD
+// update of 4 M parameters (84 MB) took 12.9 us with warm data and cached
+// accesses, 13.5 us with non-temporal ones; 24.2 vs 26.7 us with cold data.
+constexpr int64_t kStreamMinBytes = 256ll << 20;
+
 // Grid size for a grid-stride elementwise kernel over n items with 256
 // threads per block: enough blocks to fill 256 CUs several times over.
 inline int grid_for(int64_t n_items, int per_thread = 1, int max_blocks = 8192) {

@@ -4,13 +4,17 @@
 //
 // Every kernel is a grid-stride loop over 16-byte vectors (4 x f32 or
 // 8 x bf16) with a scalar tail, 256 threads per block.  They are HBM-bound:
-// the algorithmic traffic per element is listed beside each one.
+// the algorithmic traffic per element is listed beside each one.  The
+// streaming kernels (activations, their backward, SGD) read and write their
+// vectors with non-temporal accesses (tfd::ld_nt / st_nt).
 #include "common.hpp"
 
 namespace {
 
 using tfd::bf16_to_f32;
 using tfd::f32_to_bf16;
+using tfd::ld_nt;
+using tfd::st_nt;
 
 // ----- element access for f32 / bf16 storage with f32 math ----------------
 template <typename T> struct Elem;
@@ -74,13 +78,13 @@ __global__ __launch_bounds__(256) void binary_kernel(const T* __restrict__ a, co
         uint4 va[kUnroll], vb[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            va[u] = A[i + u * 256];
-            vb[u] = B[i + u * 256];
+            va[u] = ld_nt(A + i + u * 256);
+            vb[u] = ld_nt(B + i + u * 256);
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) O[i + u * 256] = apply2<T>(va[u], vb[u], op);
+        for (int u = 0; u < kUnroll; ++u) st_nt(O + i + u * 256, apply2<T>(va[u], vb[u], op));
     }
-    for (int64_t i = full * kChunk + tid; i < nv; i += stride) O[i] = apply2<T>(A[i], B[i], op);
+    for (int64_t i = full * kChunk + tid; i < nv; i += stride) st_nt(O + i, apply2<T>(ld_nt(A + i), ld_nt(B + i), op));
     for (int64_t j = nv * V + tid; j < n; j += stride)
         Elem<T>::st(out, j, op(Elem<T>::ld(a, j), Elem<T>::ld(b, j)));
 }
@@ -99,11 +103,11 @@ __global__ __launch_bounds__(256) void unary_kernel(const T* __restrict__ x, T* 
         const int64_t i = c * kChunk + threadIdx.x;
         uint4 vx[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) vx[u] = X[i + u * 256];
+        for (int u = 0; u < kUnroll; ++u) vx[u] = ld_nt(X + i + u * 256);
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) Y[i + u * 256] = apply1<T>(vx[u], op);
+        for (int u = 0; u < kUnroll; ++u) st_nt(Y + i + u * 256, apply1<T>(vx[u], op));
     }
-    for (int64_t i = full * kChunk + tid; i < nv; i += stride) Y[i] = apply1<T>(X[i], op);
+    for (int64_t i = full * kChunk + tid; i < nv; i += stride) st_nt(Y + i, apply1<T>(ld_nt(X + i), op));
     for (int64_t j = nv * V + tid; j < n; j += stride) Elem<T>::st(y, j, op(Elem<T>::ld(x, j)));
 }
 
@@ -182,6 +186,12 @@ __global__ void scale_by_kernel(const float* __restrict__ a, const float* __rest
 // (20 B/param; +2 B with the bf16 shadow).  Contraction is disabled so the
 // update rounds exactly like the host loop v*mu + g, p - v*lr (two roundings
 // each), the order of nn/optim/SGD.cpp:50-54.
+// Four bf16 (round to nearest even) packed as they lie in memory.
+__device__ __forceinline__ uint2 bf16x4(const float4& v) {
+    return make_uint2((uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16),
+                      (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16));
+}
+
 __device__ __forceinline__ void sgd4(float4& pp, const float4& gg, float4& vv, bool use_v, float lr, float mu) {
 #pragma clang fp contract(off)
     float* pe = reinterpret_cast<float*>(&pp);
@@ -201,6 +211,9 @@ __device__ __forceinline__ void sgd4(float4& pp, const float4& gg, float4& vv, b
     }
 }
 
+// NT: non-temporal accesses, for parameter sets too large to stay in the
+// last-level cache between steps (tfd::kStreamMinBytes).
+template <bool NT>
 __global__ __launch_bounds__(256) void sgd_momentum_kernel(float* __restrict__ p, const float* __restrict__ g,
                                                            float* __restrict__ v, uint16_t* __restrict__ p_bf16,
                                                            int64_t n, float lr, float mu, int vec_ok) {
@@ -214,16 +227,9 @@ __global__ __launch_bounds__(256) void sgd_momentum_kernel(float* __restrict__ p
     const float4* G = reinterpret_cast<const float4*>(g);
     float4* Vv = reinterpret_cast<float4*>(v);
     auto finish = [&](int64_t i, float4& pp, float4& vv) {
-        P[i] = pp;
-        if (use_v) Vv[i] = vv;
-        if (p_bf16) {
-            ushort4 h;
-            h.x = f32_to_bf16(pp.x);
-            h.y = f32_to_bf16(pp.y);
-            h.z = f32_to_bf16(pp.z);
-            h.w = f32_to_bf16(pp.w);
-            reinterpret_cast<ushort4*>(p_bf16)[i] = h;
-        }
+        tfd::st_v<NT>(P + i, pp);
+        if (use_v) tfd::st_v<NT>(Vv + i, vv);
+        if (p_bf16) tfd::st_v<NT>(reinterpret_cast<uint2*>(p_bf16) + i, bf16x4(pp));
     };
     const int64_t full = nv / (U * 256);
     for (int64_t c = blockIdx.x; c < full; c += gridDim.x) {
@@ -231,9 +237,9 @@ __global__ __launch_bounds__(256) void sgd_momentum_kernel(float* __restrict__ p
         float4 pp[U], gg[U], vv[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            pp[u] = P[i + u * 256];
-            gg[u] = G[i + u * 256];
-            vv[u] = use_v ? Vv[i + u * 256] : make_float4(0.f, 0.f, 0.f, 0.f);
+            pp[u] = tfd::ld_v<NT>(P + i + u * 256);
+            gg[u] = tfd::ld_v<NT>(G + i + u * 256);
+            vv[u] = use_v ? tfd::ld_v<NT>(Vv + i + u * 256) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -294,6 +300,7 @@ struct SgdMultiArgs {
     int count;
 };
 
+template <bool NT>
 __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdMultiArgs a, float lr, float mu) {
 #pragma clang fp contract(off)
     const bool use_v = mu != 0.0f;
@@ -317,27 +324,20 @@ __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdMultiArgs a, fl
             const bool ok0 = i0 < vend, ok1 = i1 < vend;
             float4 pp0, gg0, vv0 = make_float4(0.f, 0.f, 0.f, 0.f), pp1, gg1, vv1 = vv0;
             if (ok0) {
-                pp0 = P[i0];
-                gg0 = G[i0];
-                if (use_v) vv0 = V[i0];
+                pp0 = tfd::ld_v<NT>(P + i0);
+                gg0 = tfd::ld_v<NT>(G + i0);
+                if (use_v) vv0 = tfd::ld_v<NT>(V + i0);
             }
             if (ok1) {
-                pp1 = P[i1];
-                gg1 = G[i1];
-                if (use_v) vv1 = V[i1];
+                pp1 = tfd::ld_v<NT>(P + i1);
+                gg1 = tfd::ld_v<NT>(G + i1);
+                if (use_v) vv1 = tfd::ld_v<NT>(V + i1);
             }
             auto finish = [&](int64_t i, float4& pp, const float4& gg, float4& vv) {
                 sgd4(pp, gg, vv, use_v, lr, mu);
-                P[i] = pp;
-                if (use_v) V[i] = vv;
-                if (s) {
-                    ushort4 h;
-                    h.x = f32_to_bf16(pp.x);
-                    h.y = f32_to_bf16(pp.y);
-                    h.z = f32_to_bf16(pp.z);
-                    h.w = f32_to_bf16(pp.w);
-                    reinterpret_cast<ushort4*>(s)[i] = h;
-                }
+                tfd::st_v<NT>(P + i, pp);
+                if (use_v) tfd::st_v<NT>(V + i, vv);
+                if (s) tfd::st_v<NT>(reinterpret_cast<uint2*>(s) + i, bf16x4(pp));
             };
             if (ok0) finish(i0, pp0, gg0, vv0);
             if (ok1) finish(i1, pp1, gg1, vv1);
@@ -439,8 +439,9 @@ tf_status tf_sgd_momentum(tf_ctx* ctx, float* p, const float* g, float* v, void*
     TF_REQUIRE(mu >= 0.0f && mu < 1.0f, "tf_sgd_momentum: momentum must lie in [0, 1)");
     int vec_ok = aligned16<char>(p) && aligned16<char>(g) && (v == nullptr || aligned16<char>(v)) &&
                  (p_bf16 == nullptr || (reinterpret_cast<uintptr_t>(p_bf16) & 7) == 0);
-    sgd_momentum_kernel<<<tfd::grid_for(n, 4 * 2), 256, 0, ctx->stream>>>(
-        p, g, v, (uint16_t*)p_bf16, n, lr, mu, vec_ok);
+    const int64_t bytes = n * (12 + (mu != 0.0f ? 8 : 0) + (p_bf16 ? 2 : 0));
+    auto kernel = bytes > tfd::kStreamMinBytes ? sgd_momentum_kernel<true> : sgd_momentum_kernel<false>;
+    kernel<<<tfd::grid_for(n, 4 * 2), 256, 0, ctx->stream>>>(p, g, v, (uint16_t*)p_bf16, n, lr, mu, vec_ok);
     return tfh::check_launch("sgd_momentum_kernel");
 }
 
@@ -452,7 +453,7 @@ tf_status tf_sgd_momentum_multi(tf_ctx* ctx, int count, float* const* p, const f
     TF_REQUIRE(p && g && n, "tf_sgd_momentum_multi: null p, g or n array");
     TF_REQUIRE(mu >= 0.0f && mu < 1.0f, "tf_sgd_momentum_multi: momentum must lie in [0, 1)");
     SgdMultiArgs a{};
-    int64_t units = 0;
+    int64_t units = 0, bytes = 0;
     int m = 0;
     for (int i = 0; i < count; ++i) {
         TF_REQUIRE(n[i] >= 0, "tf_sgd_momentum_multi: negative n");
@@ -470,12 +471,14 @@ tf_status tf_sgd_momentum_multi(tf_ctx* ctx, int count, float* const* p, const f
                       (si == nullptr || (reinterpret_cast<uintptr_t>(si) & 7) == 0);
         a.unit_start[m] = units;
         units += (n[i] + kSgdUnit - 1) / kSgdUnit;
+        bytes += n[i] * (12 + (mu != 0.0f ? 8 : 0) + (si ? 2 : 0));
         ++m;
     }
     a.unit_start[m] = units;
     a.count = m;
     if (units == 0) return TF_OK;
-    sgd_multi_kernel<<<(unsigned)std::min<int64_t>(units, 16384), 256, 0, ctx->stream>>>(a, lr, mu);
+    auto kernel = bytes > tfd::kStreamMinBytes ? sgd_multi_kernel<true> : sgd_multi_kernel<false>;
+    kernel<<<(unsigned)std::min<int64_t>(units, 16384), 256, 0, ctx->stream>>>(a, lr, mu);
     return tfh::check_launch("sgd_multi_kernel");
 }
 

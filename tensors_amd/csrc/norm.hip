@@ -29,6 +29,8 @@ __device__ __forceinline__ int col_of(int c, int lane, int q, bool vec) {
     return vec ? 256 * c + 4 * lane + q : 256 * c + lane + 64 * q;
 }
 
+// Whole rows held in registers, read and written once: non-temporal vector
+// accesses.
 template <int NC>
 __device__ __forceinline__ void load_row(const float* __restrict__ row, int cols, int lane, bool vec,
                                          float (&v)[NC][4]) {
@@ -36,7 +38,7 @@ __device__ __forceinline__ void load_row(const float* __restrict__ row, int cols
     for (int c = 0; c < NC; ++c) {
         int base = 256 * c + 4 * lane;
         if (vec && base + 4 <= cols) {
-            float4 t = *reinterpret_cast<const float4*>(row + base);
+            float4 t = tfd::ld_nt(reinterpret_cast<const float4*>(row + base));
             v[c][0] = t.x; v[c][1] = t.y; v[c][2] = t.z; v[c][3] = t.w;
         } else {
 #pragma unroll
@@ -55,7 +57,7 @@ __device__ __forceinline__ void store_row(float* __restrict__ row, int cols, int
     for (int c = 0; c < NC; ++c) {
         int base = 256 * c + 4 * lane;
         if (vec && base + 4 <= cols) {
-            *reinterpret_cast<float4*>(row + base) = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+            tfd::st_nt(reinterpret_cast<float4*>(row + base), make_float4(v[c][0], v[c][1], v[c][2], v[c][3]));
         } else {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {

@@ -18,10 +18,11 @@ constexpr int kColsPerBlock = 256;  // 64 lanes x float4
 // exact, so the bf16 sums equal those of the cast fp32 tensor).
 __device__ __forceinline__ float elem_f32(const float* p, int64_t i) { return p[i]; }
 __device__ __forceinline__ float elem_f32(const uint16_t* p, int64_t i) { return __uint_as_float((uint32_t)p[i] << 16); }
-// Four consecutive elements (16-byte / 8-byte aligned).
-__device__ __forceinline__ float4 vec4_f32(const float* p) { return *reinterpret_cast<const float4*>(p); }
+// Four consecutive elements (16-byte / 8-byte aligned), read once:
+// non-temporal loads.
+__device__ __forceinline__ float4 vec4_f32(const float* p) { return tfd::ld_nt(reinterpret_cast<const float4*>(p)); }
 __device__ __forceinline__ float4 vec4_f32(const uint16_t* p) {
-    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    const uint2 u = tfd::ld_nt(reinterpret_cast<const uint2*>(p));
     return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
                        __uint_as_float(u.y & 0xffff0000u));
 }

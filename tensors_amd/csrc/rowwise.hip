@@ -20,14 +20,18 @@ __device__ __forceinline__ int col_of(int c, int lane, int q, bool vec) {
     return vec ? 256 * c + 4 * lane + q : 256 * c + lane + 64 * q;
 }
 
-template <int NC>
+// NT: non-temporal vector accesses, for rows read or written once (the
+// register-cached path); the streamed path reads its row twice and keeps the
+// default policy so the second read can hit the cache.
+template <int NC, bool NT = false>
 __device__ __forceinline__ void load_row(const float* __restrict__ row, int cols, int lane, bool vec,
                                          float (&v)[NC][4], float fill) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         int base = 256 * c + 4 * lane;
         if (vec && base + 4 <= cols) {
-            float4 t = *reinterpret_cast<const float4*>(row + base);
+            const float4* src = reinterpret_cast<const float4*>(row + base);
+            float4 t = NT ? tfd::ld_nt(src) : *src;
             v[c][0] = t.x; v[c][1] = t.y; v[c][2] = t.z; v[c][3] = t.w;
         } else {
 #pragma unroll
@@ -39,14 +43,17 @@ __device__ __forceinline__ void load_row(const float* __restrict__ row, int cols
     }
 }
 
-template <int NC>
+template <int NC, bool NT = false>
 __device__ __forceinline__ void store_row(float* __restrict__ row, int cols, int lane, bool vec,
                                           const float (&v)[NC][4]) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         int base = 256 * c + 4 * lane;
         if (vec && base + 4 <= cols) {
-            *reinterpret_cast<float4*>(row + base) = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+            float4* dst = reinterpret_cast<float4*>(row + base);
+            const float4 t = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+            if (NT) tfd::st_nt(dst, t);
+            else *dst = t;
         } else {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -108,7 +115,7 @@ __global__ __launch_bounds__(256) void ce_kernel(const float* __restrict__ logit
     float lse;
     float v[NCC][4];
     if constexpr (NC > 0) {
-        load_row<NCC>(x, cols, lane, vec, v, -INFINITY);
+        load_row<NCC, true>(x, cols, lane, vec, v, -INFINITY);
     }
     if (MODE == 1 && lse_in != nullptr) {
         lse = lse_in[r];
@@ -151,7 +158,7 @@ __global__ __launch_bounds__(256) void ce_kernel(const float* __restrict__ logit
                     float pj = __expf(v[c][q] - lse);
                     v[c][q] = pj * scale - (j == t ? scale : 0.0f);
                 }
-            store_row<NCC>(dx, cols, lane, vec, v);
+            store_row<NCC, true>(dx, cols, lane, vec, v);
         } else {
             for (int c = 0; 256 * c < cols; ++c) {
                 float w[1][4];
@@ -196,7 +203,7 @@ __global__ __launch_bounds__(256) void softmax_fwd_kernel(const float* __restric
     float* y = ys + (int64_t)r * cols;
     if constexpr (NC > 0) {
         float v[NCC][4];
-        load_row<NCC>(x, cols, lane, vec, v, -INFINITY);
+        load_row<NCC, true>(x, cols, lane, vec, v, -INFINITY);
         float m = -INFINITY;
 #pragma unroll
         for (int c = 0; c < NC; ++c)
@@ -214,7 +221,7 @@ __global__ __launch_bounds__(256) void softmax_fwd_kernel(const float* __restric
         for (int c = 0; c < NC; ++c)
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[c][q] = KIND == 0 ? v[c][q] - lz : __expf(v[c][q] - m) * inv;
-        store_row<NCC>(y, cols, lane, vec, v);
+        store_row<NCC, true>(y, cols, lane, vec, v);
     } else {
         float m, s;
         stream_stats(x, cols, lane, vec, m, s);
@@ -243,8 +250,8 @@ __global__ __launch_bounds__(256) void softmax_bwd_kernel(const float* __restric
     float* dx = dxs + (int64_t)r * cols;
     if constexpr (NC > 0) {
         float yv[NCC][4], gv[NCC][4];
-        load_row<NCC>(y, cols, lane, vec, yv, 0.0f);
-        load_row<NCC>(dy, cols, lane, vec, gv, 0.0f);
+        load_row<NCC, true>(y, cols, lane, vec, yv, 0.0f);
+        load_row<NCC, true>(dy, cols, lane, vec, gv, 0.0f);
         float s = 0.0f;
 #pragma unroll
         for (int c = 0; c < NC; ++c)
@@ -256,7 +263,7 @@ __global__ __launch_bounds__(256) void softmax_bwd_kernel(const float* __restric
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 gv[c][q] = KIND == 0 ? gv[c][q] - expf(yv[c][q]) * s : yv[c][q] * (gv[c][q] - s);
-        store_row<NCC>(dx, cols, lane, vec, gv);
+        store_row<NCC, true>(dx, cols, lane, vec, gv);
     } else {
         float s = 0.0f;
         for (int c = 0; 256 * c < cols; ++c) {
