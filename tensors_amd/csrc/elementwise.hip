@@ -188,8 +188,7 @@ __global__ void scale_by_kernel(const float* __restrict__ a, const float* __rest
 // each), the order of nn/optim/SGD.cpp:50-54.
 // Four bf16 (round to nearest even) packed as they lie in memory.
 __device__ __forceinline__ uint2 bf16x4(const float4& v) {
-    return make_uint2((uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16),
-                      (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16));
+    return make_uint2(tfd::bf16x2_rne(v.x, v.y), tfd::bf16x2_rne(v.z, v.w));
 }
 
 __device__ __forceinline__ void sgd4(float4& pp, const float4& gg, float4& vv, bool use_v, float lr, float mu) {
@@ -362,10 +361,10 @@ __global__ __launch_bounds__(256) void cast_f32_bf16_kernel(const float* __restr
         const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
         const float4 b = reinterpret_cast<const float4*>(x)[2 * i + 1];
         uint4 o;
-        o.x = (uint32_t)f32_to_bf16(a.x) | ((uint32_t)f32_to_bf16(a.y) << 16);
-        o.y = (uint32_t)f32_to_bf16(a.z) | ((uint32_t)f32_to_bf16(a.w) << 16);
-        o.z = (uint32_t)f32_to_bf16(b.x) | ((uint32_t)f32_to_bf16(b.y) << 16);
-        o.w = (uint32_t)f32_to_bf16(b.z) | ((uint32_t)f32_to_bf16(b.w) << 16);
+        o.x = tfd::bf16x2_rne(a.x, a.y);
+        o.y = tfd::bf16x2_rne(a.z, a.w);
+        o.z = tfd::bf16x2_rne(b.x, b.y);
+        o.w = tfd::bf16x2_rne(b.z, b.w);
         reinterpret_cast<uint4*>(y)[i] = o;
     }
     for (int64_t j = nv * 8 + tid; j < n; j += stride) y[j] = f32_to_bf16(x[j]);

@@ -775,9 +775,7 @@ __device__ __forceinline__ void big_epilogue(const GemmParams& p, v16f (&acc)[4]
         if constexpr (bf16) {
             uint16_t* c = reinterpret_cast<uint16_t*>(p.C) + off;
             if (vec) {
-                const uint32_t lo = (uint32_t)tfd::f32_to_bf16(o[0]) | ((uint32_t)tfd::f32_to_bf16(o[1]) << 16);
-                const uint32_t hi = (uint32_t)tfd::f32_to_bf16(o[2]) | ((uint32_t)tfd::f32_to_bf16(o[3]) << 16);
-                *reinterpret_cast<uint2*>(c) = make_uint2(lo, hi);
+                *reinterpret_cast<uint2*>(c) = make_uint2(tfd::bf16x2_rne(o[0], o[1]), tfd::bf16x2_rne(o[2], o[3]));
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
@@ -825,7 +823,56 @@ __device__ __forceinline__ void big_epilogue(const GemmParams& p, v16f (&acc)[4]
                 if (row < p.M && col < p.N) out4(row, v, PART, BF16, LOADS);
             }
         };
-        if (part) copy_out(T_{}, F_{}, F_{});
+        // Interior blocks (the wave's 64 x 128 staged block inside C, every
+        // 4-column vector aligned) without beta * C or a row bias: no bounds
+        // checks, a pointer advanced by two rows per pass, and the transform
+        // fixed at compile time (XF 0: copy, 1: alpha * v + bias, 2: the same
+        // then ReLU).  OUT 0: split-K partial, 1: bf16 C, 2: fp32 C.  The
+        // generic loop above spent most of its time on per-pass address
+        // arithmetic, bounds and form checks, and software bf16 rounding.
+        auto copy_fast = [&](auto OUT, auto XF) TF_LAMBDA_INLINE {
+            constexpr int out = decltype(OUT)::value, xf = decltype(XF)::value;
+            using Dst = std::conditional_t<out == 1, uint16_t, float>;
+            const int64_t ld = out == 0 ? (int64_t)p.N : ldc;
+            Dst* dst = out == 0 ? reinterpret_cast<Dst*>(part) + (int64_t)row0 * ld + col
+                                : reinterpret_cast<Dst*>(p.C) + boff + (int64_t)row0 * ld + col;
+            f32x4 next = *reinterpret_cast<const f32x4*>(src);
+#pragma unroll 2
+            for (int pass = 0; pass < 32; ++pass) {
+                f32x4 o = next;
+                next = *reinterpret_cast<const f32x4*>(src + min(pass + 1, 31) * 256);
+                if constexpr (xf != 0) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float t = alpha * o[e] + cb[e];
+                        o[e] = xf == 2 ? fmaxf(t, 0.0f) : t;
+                    }
+                }
+                if constexpr (out == 1)
+                    *reinterpret_cast<uint2*>(dst) = make_uint2(tfd::bf16x2_rne(o[0], o[1]), tfd::bf16x2_rne(o[2], o[3]));
+                else
+                    *reinterpret_cast<f32x4*>(dst) = o;
+                dst += 2 * ld;
+            }
+        };
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        const bool interior = !general && (part ? p.N % 4 == 0 : p.vec_c4 != 0) &&
+                              m0 + wm * 128 + 64 * rnd + 64 <= p.M && n0 + wn * 128 + 128 <= p.N;
+        const bool plain = alpha == 1.0f && !has_bias && !relu;
+        if (interior) {
+            if (part) copy_fast(I0{}, I0{});
+            else if (p.out_bf16) {
+                if (plain) copy_fast(I1{}, I0{});
+                else if (relu) copy_fast(I1{}, I2{});
+                else copy_fast(I1{}, I1{});
+            } else {
+                if (plain) copy_fast(I2{}, I0{});
+                else if (relu) copy_fast(I2{}, I2{});
+                else copy_fast(I2{}, I1{});
+            }
+        } else if (part) copy_out(T_{}, F_{}, F_{});
         else if (general && p.out_bf16) copy_out(F_{}, T_{}, T_{});  // row bias (beta != 0 needs an fp32 C)
         else if (general) copy_out(F_{}, F_{}, T_{});
         else if (p.out_bf16) copy_out(F_{}, T_{}, F_{});

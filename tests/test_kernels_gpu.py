@@ -579,3 +579,34 @@ def test_sgd_momentum_multi_bitexact(ctx, mu):
             assert_bitexact(dvs[i].numpy(), vs[i], f"multi sgd v[{i}] n={n}")
         if shs[i] is not None:
             assert_bitexact(shs[i].numpy(), ta_mod.f32_to_bf16_bits(ps[i]), f"multi sgd shadow[{i}]")
+
+
+def _bf16_special_inputs():
+    """float32 bit patterns that exercise every branch of round-to-nearest-even
+    to bf16: signed zeros, denormals, exact ties with even and odd kept bits,
+    values just above and below a tie, the largest finite values (some round
+    to infinity), infinities, and NaNs whose payload lies in the kept bits,
+    only in the dropped bits, or both."""
+    pats = [0x00000000, 0x80000000, 0x00000001, 0x807FFFFF, 0x00008000, 0x00018000, 0x00400000,
+            0x3F808000, 0x3F818000, 0x3F807FFF, 0x3F808001, 0x3F800000, 0xBF808000, 0xBF818000,
+            0x7F7F7FFF, 0x7F7F8000, 0x7F7FFFFF, 0xFF7FFFFF, 0x7F800000, 0xFF800000,
+            0x7FC00000, 0xFFC00000, 0x7F800001, 0xFF800001, 0x7FA00000, 0x7F80FFFF, 0x7FFFFFFF, 0xFFFFFFFF]
+    rnd = synth.uniform_int(221, (4096,), 1 << 31).astype(np.uint32) * 2 + 1
+    u = np.concatenate([np.array(pats, np.uint32), rnd, np.arange(0x3F800000, 0x3F800000 + 4096, dtype=np.uint32)])
+    return u[: (u.size // 8) * 8 + 5]   # a scalar tail as well as the vector body
+
+
+def test_cast_f32_bf16_hw_rounding(ctx):
+    # Every f32 -> bf16 store in the library goes through the hardware
+    # conversion (v_cvt_pk_bf16_f32: the cast's vector body converts pairs,
+    # its scalar tail single values).  Both must equal the oracle's rule bit
+    # for bit: round to nearest even, and a NaN keeps its sign and top
+    # payload bits with the quiet bit set.
+    import tensors_amd as ta_mod
+    from tensors_amd._lib import call
+    u = _bf16_special_inputs()
+    x = u.view(np.float32)
+    dx = ctx.array(x)
+    dy = ctx.empty(x.shape, ta_mod.BF16)
+    call("tf_cast_f32_bf16", ctx.handle, dx.ptr, dy.ptr, x.size)
+    assert_bitexact(dy.numpy(), ta_mod.f32_to_bf16_bits(x), "bf16 rounding (incl. NaN payloads)")
