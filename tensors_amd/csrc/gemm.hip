@@ -1528,6 +1528,96 @@ struct F32DlOperand {
     }
 };
 
+constexpr int kF32DlPairFloats = 8 * 8 * 64 * 4;  // LDS floats of the pair reduction (8 KB per wave)
+
+// Epilogue of the direct fp32 kernel for interior blocks without beta * C or
+// a row bias.  The wave's 32 x 64 block (sub-tile row block g after the pair
+// reduction) is staged in its own 8 KB of LDS (`stage`, 32 rows x 64
+// floats) and written by whole rows: a lane takes 4 consecutive columns
+// (16-byte stores; 16 lanes per row, 4 rows per pass), the pointer advances
+// by 4 staged rows per pass, and the output form (OUT 0: split-K partial,
+// 1: bf16, 2: fp32) and transform (XF 0: copy, 1: alpha * v + bias, 2: the
+// same then ReLU) are fixed at compile time.  Writing element by element
+// (store_wave) spends more time on address arithmetic and checks than on the
+// stores.  Staged row rl of block g is row rl (A_PAIR: 2 rl + g; otherwise
+// 32 g + rl) of the wave block; its column c is column c of the wave block
+// (B_PAIR: accumulator j holds columns 2 l + j, so a lane's pair of
+// accumulators is one 8-byte LDS write).  Returns false, having written
+// nothing, when the block does not qualify.
+template <bool A_PAIR, bool B_PAIR>
+__device__ __forceinline__ bool f32dl_store_fast(const GemmParams& p, const v16f (&acc)[2][2], int g, int m_base,
+                                                 int n_base, int64_t boff, int split, float* __restrict__ stage) {
+    const bool has_bias = p.epi != TF_EPI_NONE && p.epi != TF_EPI_RELU;
+    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU || p.epi == TF_EPI_ROW_BIAS_RELU;
+    float* part = p.partial ? p.partial + (int64_t)split * p.M * p.N : nullptr;
+    if (!part && (p.beta != 0.0f || (has_bias && p.row_bias))) return false;
+    if (part ? p.N % 4 != 0 : p.vec_c4 == 0) return false;
+    if (m_base + 64 > p.M || n_base + 64 > p.N) return false;
+    const int lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
+    // The kept block, chosen by value: indexing acc with the run-time g
+    // (even under a branch per candidate) made the compiler keep all
+    // accumulators in scratch memory.
+    const v16f k0 = g ? acc[1][0] : acc[0][0];
+    const v16f k1 = g ? acc[1][1] : acc[0][1];
+    static_for<16>([&](auto R) TF_LAMBDA_INLINE {
+        constexpr int r = decltype(R)::value;
+        float* row = stage + (8 * (r >> 2) + 4 * half + (r & 3)) * 64;
+        if constexpr (B_PAIR) {
+            *reinterpret_cast<f32x2*>(row + 2 * l32) = f32x2{k0[r], k1[r]};
+        } else {
+            row[l32] = k0[r];
+            row[32 + l32] = k1[r];
+        }
+    });
+    const int rsub = lane >> 4, c4 = 4 * (lane & 15);
+    const int col = n_base + c4;
+    float cb[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) cb[e] = has_bias ? p.bias[col + e] : 0.0f;
+    const float alpha = p.alpha;
+    const int row_step = A_PAIR ? 2 : 1;  // rows of C per staged row
+    const int row0 = m_base + (A_PAIR ? g : 32 * g) + row_step * rsub;
+    const float* src = stage + rsub * 64 + c4;
+    auto copy = [&](auto OUT, auto XF) TF_LAMBDA_INLINE {
+        constexpr int out = decltype(OUT)::value, xf = decltype(XF)::value;
+        using Dst = std::conditional_t<out == 1, uint16_t, float>;
+        const int64_t ld = out == 0 ? (int64_t)p.N : (int64_t)p.ldc;
+        Dst* dst = out == 0 ? reinterpret_cast<Dst*>(part) + (int64_t)row0 * ld + col
+                            : reinterpret_cast<Dst*>(p.C) + boff + (int64_t)row0 * ld + col;
+#pragma unroll
+        for (int pass = 0; pass < 8; ++pass) {
+            f32x4 o = *reinterpret_cast<const f32x4*>(src + pass * 4 * 64);
+            if constexpr (xf != 0) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float t = alpha * o[e] + cb[e];
+                    o[e] = xf == 2 ? fmaxf(t, 0.0f) : t;
+                }
+            }
+            if constexpr (out == 1)
+                *reinterpret_cast<uint2*>(dst) = make_uint2(tfd::bf16x2_rne(o[0], o[1]), tfd::bf16x2_rne(o[2], o[3]));
+            else
+                *reinterpret_cast<f32x4*>(dst) = o;
+            dst += 4 * row_step * ld;
+        }
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    const bool plain = alpha == 1.0f && !has_bias && !relu;
+    if (part) copy(I0{}, I0{});
+    else if (p.out_bf16) {
+        if (plain) copy(I1{}, I0{});
+        else if (relu) copy(I1{}, I2{});
+        else copy(I1{}, I1{});
+    } else {
+        if (plain) copy(I2{}, I0{});
+        else if (relu) copy(I2{}, I2{});
+        else copy(I2{}, I1{});
+    }
+    return true;
+}
+
 template <bool A_KMAJ, bool B_KMAJ>
 __global__ __launch_bounds__(kF32DlThreads) void gemm_f32_dl_kernel(GemmParams p) {
     constexpr int S = kF32DlStages;
@@ -1674,7 +1764,11 @@ __global__ __launch_bounds__(kF32DlThreads) void gemm_f32_dl_kernel(GemmParams p
             acc[i][j][r + 3] += y[3];
         });
     });
-    store_wave<2, !A_KMAJ, !B_KMAJ>(p, acc, m0 + wm * 64, n0 + wn * 64, (int64_t)batch * p.stride_c, split, g);
+    static_assert(kF32DlPairFloats + 8 * 32 * 64 <= S * 2 * kF32DlOp, "epilogue staging must fit in the ring");
+    float* stage = lds + kF32DlPairFloats + wave * 32 * 64;  // past the pair-reduction area
+    if (!f32dl_store_fast<!A_KMAJ, !B_KMAJ>(p, acc, g, m0 + wm * 64, n0 + wn * 64, (int64_t)batch * p.stride_c,
+                                            split, stage))
+        store_wave<2, !A_KMAJ, !B_KMAJ>(p, acc, m0 + wm * 64, n0 + wn * 64, (int64_t)batch * p.stride_c, split, g);
 }
 
 // Split-K reduction: C = epi(alpha * sum_s partial[s] + beta * C), summing the
