@@ -227,6 +227,47 @@ def test_gemm_f32_large_tile_epilogues(ctx):
     assert_close(got, _gemm_truth(a, b, False, True, 0.5, 0.25, c0), RTOL32, "fp32 128-tile alpha/beta")
 
 
+# Every epilogue form the large-tile kernels compile separately (copy, alpha,
+# bias, bias + ReLU, ReLU alone) with fp32 and bf16 outputs, on shapes whose
+# blocks are all interior (the staged whole-row store path), split over K
+# (split-K partials), and ragged (the bounds-checked path).  The product is
+# computed once per shape in float64; each form is applied to it.
+_EPI_FORMS = [("plain", 1.0, False, False), ("alpha", 0.75, False, False), ("bias", 1.0, True, False),
+              ("bias_relu", 1.0, True, True), ("relu", 1.0, False, True), ("alpha_bias_relu", -1.5, True, True)]
+
+
+@pytest.mark.parametrize("dt,M,N,K,ta,tb", [
+    ("f32", 2048, 2048, 128, False, True), ("f32", 2048, 2048, 96, True, False), ("f32", 512, 512, 8192, False, False),
+    ("f32", 2000, 2052, 96, False, True),
+    ("bf16", 4096, 4096, 256, False, True), ("bf16", 4096, 4096, 192, True, False),
+    ("bf16", 1024, 1024, 8192, False, False), ("bf16", 3900, 4100, 128, False, True)])
+def test_gemm_large_tile_epilogue_forms(ctx, dt, M, N, K, ta, tb):
+    import tensors_amd as ta_mod
+    from tensors_amd import ops
+    seed = synth.seed(2, 30) + M + K
+    a = synth.normal(seed, (K, M) if ta else (M, K))
+    b = synth.normal(seed + 1, (N, K) if tb else (K, N))
+    if dt == "bf16":
+        a16, b16 = ta_mod.f32_to_bf16_bits(a), ta_mod.f32_to_bf16_bits(b)
+        a, b = ta_mod.bf16_bits_to_f32(a16), ta_mod.bf16_bits_to_f32(b16)
+        da, db = ctx.array(a16, ta_mod.BF16), ctx.array(b16, ta_mod.BF16)
+    else:
+        da, db = ctx.array(a), ctx.array(b)
+    prod = _gemm_truth(a, b, ta, tb)
+    bias = synth.normal(seed + 2, (N,))
+    dbias = ctx.array(bias)
+    for name, alpha, use_bias, relu in _EPI_FORMS:
+        want = alpha * prod + (bias.astype(np.float64) if use_bias else 0.0)
+        if relu:
+            want = np.maximum(want, 0.0)
+        for out in ("f32", "bf16"):
+            dc = ctx.zeros((M, N), np.float32 if out == "f32" else ta_mod.BF16)
+            ops.gemm(da, db, dc, trans_a=ta, trans_b=tb, alpha=alpha, bias=dbias if use_bias else None, relu=relu)
+            got = dc.numpy() if out == "f32" else ta_mod.bf16_bits_to_f32(dc.numpy())
+            tol = RTOL16 if (dt == "bf16" or out == "bf16") else RTOL32
+            assert_close(got, want, tol, f"{dt} in, {out} out, {name}, {M}x{N}x{K} ta={ta} tb={tb}")
+
+
 def _row_bias_truth(a, b, ta, tb, bias, relu):
     out = _gemm_truth(a, b, ta, tb) + bias.astype(np.float64)[:, None]
     return np.maximum(out, 0.0) if relu else out
