@@ -12,8 +12,11 @@ all on device-resident inputs.  Prints ONE JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 
-Per-kernel durations come from HIP events recorded on the context's stream
-around each launch inside the timed steps.  The roofline entry is for the
+`value` is the wall time of the K timed steps (nothing but the step's
+kernels on the stream, synchronised before and after) divided by K.
+Per-kernel durations come from a second, untimed pass of K steps with HIP
+events recorded on the context's stream between consecutive launches.  The
+roofline entry is for the
 backward GEMMs (dominant kernel): 2*M*N*K = 17,179,869,184 FLOP per launch
 against the 157.3 TFLOP/s fp32 MFMA peak.  ``traffic`` is read from the
 committed rocprofv3 counter summary when present.
@@ -74,12 +77,18 @@ def bench_c2(steps: int, warmup: int):
 
     for _ in range(warmup):
         step()
+    # Timed region: exactly `steps` steps with nothing else on the stream.
     ctx.sync()
     t0 = time.perf_counter()
     for s in range(steps):
-        step(events[s])
+        step()
     ctx.sync()
     wall_ms = (time.perf_counter() - t0) * 1e3
+    # Per-kernel breakdown (and the roofline figure) from a second, untimed
+    # pass with an event between consecutive kernels.
+    for s in range(steps):
+        step(events[s])
+    ctx.sync()
 
     per = {"fwd_gemm": [], "bwd_gemm_dx": [], "bwd_gemm_dw": [], "colsum": [], "sgd": [], "step_dev": []}
     for s in range(steps):
@@ -276,8 +285,11 @@ def probe(steps: int = 5) -> None:
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    # 50 warmup steps (~20 ms): the GPU's clocks need more than ~10 ms of load
+    # to settle after the host-side input generation; with 5 warmup steps the
+    # timed C2 steps ran ~5 % slower than in steady state.
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-c2", action="store_true", help="skip the other configurations' measurements")
     ap.add_argument("--probe", action="store_true", help="launch the C2 kernels for a profiler, then exit")

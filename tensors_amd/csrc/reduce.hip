@@ -1,9 +1,10 @@
-// Bias-gradient reductions, deterministic two-stage (no atomics):
+// Bias-gradient reductions, deterministic (no atomics, fixed summation order):
 //   colsum : db[c] = sum_r dy[r, c]           (Linear bias grad; fp32 or bf16 dy)
 //   chansum: db[c] = sum_{n,p} dy[n, c, p]    (Conv2d bias grad, NCHW)
-// Stage 1 writes per-chunk partial sums to the context workspace, stage 2
-// (tfh::partial_rows_sum, also used by the LayerNorm backward) adds them in a
-// fixed order.  The reference's conv kernel
+// Wide colsums (>= 2048 columns) run as one launch of column strips.  The
+// others are two-stage: stage 1 writes per-chunk partial sums to the context
+// workspace, stage 2 (tfh::partial_rows_sum, also used by the LayerNorm
+// backward) adds them in a fixed order.  The reference's conv kernel
 // lets every block overwrite out[c] with its own partial
 // (cuda/kernels/reduce_sum_axis.cu:60-97); this one reduces all of them.
 #include "common.hpp"
@@ -64,6 +65,63 @@ __global__ __launch_bounds__(256) void colsum_stage1(const T* __restrict__ dy, f
         if (c0 + 1 < cols) out[c0 + 1] = s.y;
         if (c0 + 2 < cols) out[c0 + 2] = s.z;
         if (c0 + 3 < cols) out[c0 + 3] = s.w;
+    }
+}
+
+// Single-launch colsum for wide matrices: block b owns a strip of W
+// consecutive columns and sums every row of it (no partials, no second
+// launch).  A lane takes 4 columns (one 16- or 8-byte load per row), W / 4
+// lanes cover a row of the strip, and the block's 256 / (W / 4) row groups
+// take rows g, g + groups, ... in ascending order, sixteen loads in flight.
+// The row groups are then added in a fixed order: a butterfly across the
+// lanes of a wave that hold the same columns, then the four waves in order
+// through LDS.  Strips are assigned XCD by XCD: workgroups are dispatched
+// round-robin over the 8 XCDs (block b on XCD b % 8), so strip
+// (b % 8) * (strips / 8) + b / 8 gives each XCD a contiguous column range,
+// and the strips that share a cache line share an L2.
+template <typename T, int W>
+__global__ __launch_bounds__(256) void colsum_strip_kernel(const T* __restrict__ dy, float* __restrict__ db, int rows,
+                                                           int cols, int strips) {
+    constexpr int LPR = W / 4;      // lanes per row of the strip
+    constexpr int RG = 256 / LPR;   // row groups
+    constexpr int U = 16;           // loads in flight per lane
+    __shared__ float4 red[4][LPR];
+    const int b = blockIdx.x;
+    const int strip = (b % 8) * (strips / 8) + b / 8;
+    const int cg = threadIdx.x % LPR, rg = threadIdx.x / LPR;
+    const int c0 = strip * W + 4 * cg;
+    const T* base = dy + c0;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    int r = rg;
+    for (; r + (U - 1) * RG < rows; r += U * RG) {
+        float4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = vec4_f32(base + (int64_t)(r + u * RG) * cols);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
+        }
+    }
+    for (; r < rows; r += RG) {
+        const float4 v = vec4_f32(base + (int64_t)r * cols);
+        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1) {
+        acc.x += __shfl_xor(acc.x, off, 64);
+        acc.y += __shfl_xor(acc.y, off, 64);
+        acc.z += __shfl_xor(acc.z, off, 64);
+        acc.w += __shfl_xor(acc.w, off, 64);
+    }
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane < LPR) red[wave][lane] = acc;
+    __syncthreads();
+    if (threadIdx.x < LPR) {
+        const float4 a = red[0][cg], b1 = red[1][cg], c = red[2][cg], d = red[3][cg];
+        db[c0 + 0] = (a.x + b1.x) + (c.x + d.x);
+        db[c0 + 1] = (a.y + b1.y) + (c.y + d.y);
+        db[c0 + 2] = (a.z + b1.z) + (c.z + d.z);
+        db[c0 + 3] = (a.w + b1.w) + (c.w + d.w);
     }
 }
 
@@ -145,6 +203,23 @@ tf_status colsum_impl(tf_ctx* ctx, const T* dy, float* db, int64_t rows, int64_t
     if (cols == 0) return TF_OK;
     TF_REQUIRE(db != nullptr && (rows == 0 || dy != nullptr), "tf_colsum: null pointer");
     if (rows == 0) return tf_hip_fill_f32(ctx, db, 0.0f, cols);
+    const int vec = (reinterpret_cast<uintptr_t>(dy) & (4 * sizeof(T) - 1)) == 0 && cols % 4 == 0;
+    // Wide matrices: one launch of column strips (about one per CU), W = 8,
+    // 16 or 32 columns each.  The strip width depends only on cols, so an
+    // fp32 and a bf16 input of the same shape are summed in the same order.
+    if (vec && cols >= 2048) {
+        int w = 8;
+        while (w < 32 && cols / w > 256) w *= 2;
+        const int nstrips = (int)(cols / w);
+        if (cols % w == 0 && nstrips % 8 == 0) {
+            switch (w) {
+            case 8: colsum_strip_kernel<T, 8><<<nstrips, 256, 0, ctx->stream>>>(dy, db, (int)rows, (int)cols, nstrips); break;
+            case 16: colsum_strip_kernel<T, 16><<<nstrips, 256, 0, ctx->stream>>>(dy, db, (int)rows, (int)cols, nstrips); break;
+            default: colsum_strip_kernel<T, 32><<<nstrips, 256, 0, ctx->stream>>>(dy, db, (int)rows, (int)cols, nstrips); break;
+            }
+            return tfh::check_launch("colsum_strip_kernel");
+        }
+    }
     const int strips = (int)((cols + kColsPerBlock - 1) / kColsPerBlock);
     // Aim for ~512 stage-1 blocks (two per CU) with at least 16 rows each.
     int64_t chunks = (512 + strips - 1) / strips;
@@ -155,7 +230,6 @@ tf_status colsum_impl(tf_ctx* ctx, const T* dy, float* db, int64_t rows, int64_t
     tf_status st = tfh::ensure_workspace(ctx, (size_t)chunks * cols * sizeof(float));
     if (st != TF_OK) return st;
     float* part = reinterpret_cast<float*>(ctx->ws);
-    int vec = (reinterpret_cast<uintptr_t>(dy) & (4 * sizeof(T) - 1)) == 0 && cols % 4 == 0;
     colsum_stage1<T><<<dim3(strips, (unsigned)chunks), 256, 0, ctx->stream>>>(dy, part, (int)rows, (int)cols, rpc,
                                                                              vec);
     st = tfh::check_launch("colsum_stage1");

@@ -92,6 +92,29 @@ def stats_table(path: str | Path, top: int = 25) -> str:
     return "\n".join(lines)
 
 
+def phase_table(trace_csv: str | Path, phases: list[tuple[str, int]], match: list[str]) -> str:
+    """Mean duration per bench phase of each kernel matching a substring in
+    `match`: its dispatches in launch order are split into consecutive groups
+    of the given sizes (e.g. warmup, timed, per-kernel events)."""
+    per: dict[str, list[tuple[int, int]]] = defaultdict(list)
+    with open(trace_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            per[r["Kernel_Name"]].append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    head = "| kernel | " + " | ".join(f"{p} (n={n}) avg us" for p, n in phases) + " |"
+    lines = [head, "|---|" + "---:|" * len(phases)]
+    for sub in match:
+        for kname in sorted(n for n in per if sub in n):
+            spans = sorted(per[kname])
+            cells, i = [], 0
+            for _, n in phases:
+                group = spans[i:i + n]
+                i += n
+                cells.append(f"{sum(e - s for s, e in group) / len(group) / 1e3:.2f}" if group else "—")
+            name = kname.replace("(anonymous namespace)::", "").replace("|", "\\|")
+            lines.append(f"| `{name[:110]}` | " + " | ".join(cells) + " |")
+    return "\n".join(lines)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(prog="python -m tensors_amd.profiling")
     sub = ap.add_subparsers(dest="action", required=True)
@@ -100,6 +123,9 @@ def main(argv=None) -> int:
     s.add_argument("--title", required=True)
     s.add_argument("--cmd", required=True, help="the rocprofv3 command that produced the CSV")
     s.add_argument("--out")
+    s.add_argument("--trace", help="the run's kernel_trace.csv, for a per-phase table")
+    s.add_argument("--phases", help="phase sizes in dispatches per kernel, e.g. warmup=50,timed=100,events=100")
+    s.add_argument("--match", nargs="*", default=[], help="kernel-name substrings for the per-phase table")
     t = sub.add_parser("traffic")
     t.add_argument("--fetch", required=True)
     t.add_argument("--write", required=True)
@@ -109,6 +135,10 @@ def main(argv=None) -> int:
     a = ap.parse_args(argv)
     if a.action == "stats":
         text = f"# {a.title}\n\nCommand (repo root):\n\n```\n{a.cmd}\n```\n\n{stats_table(a.csv)}\n"
+        if a.trace and a.phases:
+            phases = [(p.split("=")[0], int(p.split("=")[1])) for p in a.phases.split(",")]
+            text += ("\nPer phase (each kernel's dispatches in launch order, split into the bench's phases):\n\n"
+                     f"{phase_table(a.trace, phases, a.match)}\n")
         if a.out:
             Path(a.out).write_text(text)
         else:
