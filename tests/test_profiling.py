@@ -1,0 +1,77 @@
+"""Host logic of tensors_amd.profiling (the summaries under profiles/): the
+traffic calibration arithmetic, the stats table and the per-phase split, on
+synthetic rocprofv3 CSV files."""
+from __future__ import annotations
+
+import csv
+import json
+
+from tensors_amd import profiling
+
+
+def _write_counters(path, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for r in rows:
+            w.writerow(r)
+
+
+def test_traffic_calibration(tmp_path):
+    # The copy kernel reads 2 x 4 x N and writes 4 x N bytes; the counter
+    # reports half the fetch bytes (scale 2) and the exact write bytes.  A GEMM
+    # dispatch whose raw FETCH_SIZE is 50,000 KiB must come out as 100,000 KiB.
+    n = 1 << 20
+    cal_f_kib = 2 * 4 * n / 1024 / 2
+    cal_w_kib = 4 * n / 1024
+    fetch, write = [], []
+    d = 0
+    for name, f_kib, w_kib in [("binary_kernel<float, AddOp>", cal_f_kib, cal_w_kib)] + \
+            [(k, 50000.0, 16384.0) for k, _ in profiling.C2_KERNELS.values()]:
+        d += 1
+        # two counter instances per dispatch (summed by per_dispatch)
+        for part in (0.25, 0.75):
+            fetch.append({"Dispatch_Id": d, "Kernel_Name": name, "Counter_Name": "FETCH_SIZE",
+                          "Counter_Value": f_kib * part})
+            write.append({"Dispatch_Id": d, "Kernel_Name": name, "Counter_Name": "WRITE_SIZE",
+                          "Counter_Value": w_kib * part})
+    fp, wp = tmp_path / "f.csv", tmp_path / "w.csv"
+    _write_counters(fp, fetch)
+    _write_counters(wp, write)
+    res = profiling.traffic(fp, wp, n)
+    assert abs(res["calibration"]["fetch_scale"] - 2.0) < 1e-6
+    assert abs(res["calibration"]["write_scale"] - 1.0) < 1e-6
+    dx = res["gemm_f32_bwd_dx_c2"]
+    assert dx["fetch_bytes"] == 100000 * 1024 and dx["write_bytes"] == 16384 * 1024
+    assert dx["traffic_bytes"] == dx["fetch_bytes"] + dx["write_bytes"]
+    assert res["gemm_f32_bwd_c2"] == dx["traffic_bytes"]
+    json.dumps(res)
+
+
+def test_stats_and_phase_tables(tmp_path):
+    stats = tmp_path / "s.csv"
+    with open(stats, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Name", "Calls", "TotalDurationNs", "AverageNs", "MinNs", "MaxNs",
+                                          "Percentage"])
+        w.writeheader()
+        w.writerow({"Name": "void (anonymous namespace)::k_a<1>(int)", "Calls": 6, "TotalDurationNs": 6000,
+                    "AverageNs": 1000, "MinNs": 500, "MaxNs": 2000, "Percentage": 75.0})
+        w.writerow({"Name": "k_b(float|int)", "Calls": 2, "TotalDurationNs": 2000, "AverageNs": 1000,
+                    "MinNs": 1000, "MaxNs": 1000, "Percentage": 25.0})
+    table = profiling.stats_table(stats)
+    assert table.splitlines()[2].startswith("| `void k_a<1>(int)` | 6 | 0.006 | 1.00 |")
+    assert "k_b(float\\|int)" in table          # pipes escaped for markdown
+    trace = tmp_path / "t.csv"
+    with open(trace, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        # k_a: durations 4, 4 (warmup), 2, 2 (timed), 1, 1 (events) microseconds, written out of order
+        t = 0
+        rows = []
+        for dur in (4000, 4000, 2000, 2000, 1000, 1000):
+            rows.append({"Kernel_Name": "k_a<1>", "Start_Timestamp": t, "End_Timestamp": t + dur})
+            t += 10000
+        for r in reversed(rows):
+            w.writerow(r)
+    out = profiling.phase_table(trace, [("warmup", 2), ("timed", 2), ("events", 2)], ["k_a"])
+    assert out.splitlines()[-1] == "| `k_a<1>` | 4.00 | 2.00 | 1.00 |"
