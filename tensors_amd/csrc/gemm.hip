@@ -592,6 +592,17 @@ constexpr int kDlLoads = kBigTile * kDlK * 2 / 1024 / 4;  // 1 KB loads per wave
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(lds_void_ptr)const_cast<void*>(p);
+}
+// LDS byte offset of this wave's 1 KB pieces of a direct-load block (wave w
+// fills pieces loads*w ..), as a scalar.
+template <int LOADS>
+__device__ __forceinline__ uint32_t dl_wave_offset() {
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6) * LOADS * 1024);
+}
+
 __device__ __forceinline__ int swz32(int row) { return (row >> 2) & 3; }
 
 // s_waitcnt immediate (gfx9 encoding) waiting for at most n outstanding
@@ -682,13 +693,14 @@ struct KWalk {
 // then makes fragment reads wait for every load in flight, draining the
 // pipeline.  The kernel waits for these loads itself (dl_barrier, and a
 // final vmcnt(0)), and nothing else in it uses M0.
+// `lds_wave`: LDS byte address of this wave's first 1 KB of the block (a
+// scalar computed once per kernel: deriving it per load from the generic
+// pointer cost a readfirstlane and a null-check select per load).
 __device__ __forceinline__ void dl_issue(i32x4 rsrc, uint32_t tile_off, const uint32_t (&voff)[kDlLoads],
-                                         u32x4* lds_block) {
-    const int w = threadIdx.x >> 6;
-    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_ptr)(lds_block + w * kDlLoads * 64);
+                                         uint32_t lds_wave) {
     static_for<kDlLoads>([&](auto I) TF_LAMBDA_INLINE {
         constexpr int i = decltype(I)::value;
-        const uint32_t dst = __builtin_amdgcn_readfirstlane(lds0 + i * 1024u);
+        const uint32_t dst = lds_wave + i * 1024u;
         const uint32_t v = voff[i], so = tile_off;  // asm operands must be locals of the lambda
         const i32x4 r = rsrc;
         asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
@@ -1096,9 +1108,12 @@ void gemm_bf16_dl_kernel(GemmParams p) {
         const uint32_t tb0 = 2u * (B_KMAJ ? (uint32_t)n0 * (uint32_t)p.ldb : (uint32_t)n0);
         const uint32_t a_kstep = 2u * kDlK * (A_KMAJ ? 1u : (uint32_t)p.lda);
         const uint32_t b_kstep = 2u * kDlK * (B_KMAJ ? 1u : (uint32_t)p.ldb);
+        const uint32_t wave_lds = dl_wave_offset<kDlLoads>();
         auto issue_next = [&](u32x4* la, u32x4* lb) TF_LAMBDA_INLINE {
-            dl_issue(dl_rsrc(walk.a_base, p.a_bytes), ta0 + (uint32_t)walk.kin * a_kstep, voff_a, la);
-            dl_issue(dl_rsrc(walk.b_base, p.b_bytes), tb0 + (uint32_t)walk.kin * b_kstep, voff_b, lb);
+            dl_issue(dl_rsrc(walk.a_base, p.a_bytes), ta0 + (uint32_t)walk.kin * a_kstep, voff_a,
+                     lds_addr(la) + wave_lds);
+            dl_issue(dl_rsrc(walk.b_base, p.b_bytes), tb0 + (uint32_t)walk.kin * b_kstep, voff_b,
+                     lds_addr(lb) + wave_lds);
             walk.advance();
         };
         // Read order A0, B0..B3, A1..A3: the step's MFMAs (A_i x B_j,
@@ -1504,13 +1519,12 @@ __device__ __forceinline__ void f32dl_offsets(int64_t ld, uint32_t (&voff)[kF32D
 
 // Issue this wave's direct loads of one operand block (M0 = the 1 KB LDS
 // destination; inline assembly for the reasons given at dl_issue).
+// `lds_wave`: LDS byte address of this wave's first 1 KB of the block.
 __device__ __forceinline__ void f32dl_issue(i32x4 rsrc, uint32_t tile_off, const uint32_t (&voff)[kF32DlLoads],
-                                            float* lds_block) {
-    const int w = threadIdx.x >> 6;
-    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_ptr)(lds_block + w * kF32DlLoads * 256);
+                                            uint32_t lds_wave) {
     static_for<kF32DlLoads>([&](auto I) TF_LAMBDA_INLINE {
         constexpr int i = decltype(I)::value;
-        const uint32_t dst = __builtin_amdgcn_readfirstlane(lds0 + i * 1024u);
+        const uint32_t dst = lds_wave + i * 1024u;
         const uint32_t v = voff[i], so = tile_off;  // asm operands must be locals of the lambda
         const i32x4 r = rsrc;
         asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
@@ -1701,10 +1715,12 @@ __global__ __launch_bounds__(kF32DlThreads) void gemm_f32_dl_kernel(GemmParams p
         const uint32_t tb0 = 4u * (B_KMAJ ? (uint32_t)n0 * (uint32_t)p.ldb : (uint32_t)n0);
         const uint32_t a_kstep = 4u * kF32K * (A_KMAJ ? 1u : (uint32_t)p.lda);
         const uint32_t b_kstep = 4u * kF32K * (B_KMAJ ? 1u : (uint32_t)p.ldb);
+        const uint32_t wave_lds = lds_addr(lds) + dl_wave_offset<kF32DlLoads>();
         auto issue_next = [&](int st) TF_LAMBDA_INLINE {
-            f32dl_issue(dl_rsrc(walk.a_base, p.a_bytes), ta0 + (uint32_t)walk.kin * a_kstep, voff_a, stage_a(st));
+            const uint32_t dst = wave_lds + (uint32_t)(st * 2 * kF32DlOp * 4);
+            f32dl_issue(dl_rsrc(walk.a_base, p.a_bytes), ta0 + (uint32_t)walk.kin * a_kstep, voff_a, dst);
             f32dl_issue(dl_rsrc(walk.b_base, p.b_bytes), tb0 + (uint32_t)walk.kin * b_kstep, voff_b,
-                        stage_a(st) + kF32DlOp);
+                        dst + kF32DlOp * 4);
             walk.advance();
         };
         auto read = [&](int st, int qq, Quad& d) TF_LAMBDA_INLINE {
