@@ -334,6 +334,29 @@ def test_gemm_f32_large_tile_reduce_batch(ctx):
     assert_close(dc.numpy(), truth, RTOL32, "fp32 128-tile batch reduction")
 
 
+@pytest.mark.parametrize("dt,nb,M,N,K", [("bf16", 3, 4096, 4096, 128), ("f32", 8, 512, 512, 96),
+                                         ("bf16", 8, 512, 512, 128), ("f32", 5, 256, 384, 64)])
+def test_gemm_reduce_batch_walk(ctx, dt, nb, M, N, K):
+    # C = sum_b A_b^T B_b through the direct kernels' k-block walk: the walk
+    # crosses batch elements (wraps) and, where few tiles make the GEMM split
+    # over K, starts and ends inside an element.
+    import tensors_amd as ta_mod
+    from tensors_amd import ops
+    a = synth.normal(231 + nb, (nb, K, M))
+    b = synth.normal(232 + nb, (nb, K, N))
+    if dt == "bf16":
+        a16, b16 = ta_mod.f32_to_bf16_bits(a), ta_mod.f32_to_bf16_bits(b)
+        a, b = ta_mod.bf16_bits_to_f32(a16), ta_mod.bf16_bits_to_f32(b16)
+        da, db = ctx.array(a16, ta_mod.BF16), ctx.array(b16, ta_mod.BF16)
+    else:
+        da, db = ctx.array(a), ctx.array(b)
+    dc = ctx.zeros((M, N))
+    ops.gemm_ex(da, db, dc, M, N, K, lda=M, ldb=N, ldc=N, trans_a=True, stride_a=K * M, stride_b=K * N,
+                batch=nb, reduce_batch=True)
+    truth = np.einsum("bkm,bkn->mn", a.astype(np.float64), b.astype(np.float64))
+    assert_close(dc.numpy(), truth, RTOL16 if dt == "bf16" else RTOL32, f"{dt} batch reduction {nb}x{M}x{N}x{K}")
+
+
 def test_gemm_strided_batched(ctx):
     from tensors_amd._lib import TF_F32, call
     B, M, N, K = 5, 33, 47, 29
