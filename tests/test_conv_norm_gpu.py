@@ -18,7 +18,11 @@ def _ops():
     return ops
 
 
-@pytest.mark.parametrize("R,Cc", [(1024, 1024), (64, 128), (7, 3000), (33, 1001), (1, 1), (300, 2048)])
+# Backward paths: rows cached in registers with column partials (up to 2048
+# columns, incl. partly filled row chunks: 520, 264, 1536, 1001, 1) and
+# streamed wide rows (3000).
+@pytest.mark.parametrize("R,Cc", [(1024, 1024), (64, 128), (7, 3000), (33, 1001), (1, 1), (300, 2048), (4096, 1024),
+                                  (2, 520), (5, 264), (1000, 1536)])
 def test_layernorm_fwd_bwd(ctx, R, Cc):
     ops = _ops()
     x = synth.normal(201 + Cc, (R, Cc))
