@@ -662,8 +662,29 @@ __device__ __forceinline__ void dl_offsets(int64_t ld, uint32_t (&voff)[LOADS]) 
     }
 }
 
+// First k (within the 32-deep block) of each of this lane's LOADS direct
+// loads, in the layout of dl_offsets: a K-major 16-byte load holds k .. k+7
+// of one row, an MN-major one holds row k.  With K % 8 == 0 a load is
+// wholly inside or wholly past K.
+template <bool KMAJ, int LOADS = kDlLoads>
+__device__ __forceinline__ void dl_klane(int (&kl)[LOADS]) {
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int blk = w * LOADS + i;
+        kl[i] = KMAJ ? 8 * ((l & 3) ^ swz32(blk * 16 + (l >> 2))) : blk * 2 + (l >> 5);
+    }
+}
+
+// Lane offset of a load past K: above any descriptor extent (< 2^31), so the
+// buffer range check returns zeros (the lane offset alone is out of range).
+constexpr uint32_t kDlOob = 0x80000000u;
+
 // Buffer resource descriptor for raw 16-byte loads from `base` (gfx9-family
-// word 3: raw dword access; reads beyond `bytes` return zero).
+// word 3: raw dword access; reads beyond `bytes` return zero).  The range
+// check covers the lane offset plus the scalar offset: measured on gfx950,
+// a load at scalar offset 2048, lane offset 0 of a 1024-byte descriptor
+// returns zeros.
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ i32x4 dl_rsrc(uint64_t a, uint32_t bytes) {
     return i32x4{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), (int)bytes, 0x00020000};
@@ -1233,7 +1254,10 @@ void gemm_bf16_dl_kernel(GemmParams p) {
 // registers each) so that one wave's stalls (barrier skew, fragment-read and
 // scalar latency) can be covered by the other wave's MFMAs; each wave issues
 // half as many direct loads.
-template <bool A_KMAJ, bool B_KMAJ>
+// KTAIL: K % 64 != 0 (K % 8 == 0).  Each batch element spans 2 * ceil(K / 64)
+// blocks of 32; the loads of k >= K get an offset past the descriptor and
+// read zero (a compare and a select per load).
+template <bool A_KMAJ, bool B_KMAJ, bool KTAIL = false>
 __global__ __launch_bounds__(2 * kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_bf16_dl8_kernel(GemmParams p) {
     // One array per buffer (A block, then B block): the compiler tracks the
@@ -1248,12 +1272,14 @@ void gemm_bf16_dl8_kernel(GemmParams p) {
     const int m0 = tm * kBigTile, n0 = tn * kBigTile;
     const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A) + (int64_t)batch * p.stride_a;
     const uint16_t* B = reinterpret_cast<const uint16_t*>(p.B) + (int64_t)batch * p.stride_b;
-    // Splits are counted in 64-deep blocks (K % 64 == 0 here): two of ours each.
-    const int kb64_total = (p.K / 64) * p.reduce_batch;
+    // Splits are counted in 64-deep blocks (the last one partly past K
+    // with KTAIL): two of ours each.
+    const int kb64_elem = KTAIL ? (p.K + 63) / 64 : p.K / 64;
+    const int kb64_total = kb64_elem * p.reduce_batch;
     const int kb64_beg = split * p.kb_per_split;
     const int nk = 2 * max(0, min(kb64_total, kb64_beg + p.kb_per_split) - kb64_beg);
     const int kb_beg = 2 * kb64_beg;
-    const int kpb = p.K / kDlK;  // 32-deep blocks per batch element
+    const int kpb = 2 * kb64_elem;  // 32-deep blocks per batch element
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int half = lane >> 5;
@@ -1290,11 +1316,27 @@ void gemm_bf16_dl8_kernel(GemmParams p) {
         const uint32_t a_kstep = 2u * kDlK * (A_KMAJ ? 1u : (uint32_t)p.lda);
         const uint32_t b_kstep = 2u * kDlK * (B_KMAJ ? 1u : (uint32_t)p.ldb);
         const uint32_t wave_lds = dl_wave_offset<kDl8Loads>();
+        int kl_a[kDl8Loads], kl_b[kDl8Loads];
+        if constexpr (KTAIL) {
+            dl_klane<A_KMAJ, kDl8Loads>(kl_a);
+            dl_klane<B_KMAJ, kDl8Loads>(kl_b);
+        }
         auto issue_next = [&](u32x4* la, u32x4* lb) TF_LAMBDA_INLINE {
-            dl_issue<kDl8Loads>(dl_rsrc(walk.a_base, p.a_bytes), ta0 + (uint32_t)walk.kin * a_kstep, voff_a,
-                     lds_addr(la) + wave_lds);
-            dl_issue<kDl8Loads>(dl_rsrc(walk.b_base, p.b_bytes), tb0 + (uint32_t)walk.kin * b_kstep, voff_b,
-                     lds_addr(lb) + wave_lds);
+            const uint32_t so_a = ta0 + (uint32_t)walk.kin * a_kstep, so_b = tb0 + (uint32_t)walk.kin * b_kstep;
+            if constexpr (KTAIL) {
+                const int rem = p.K - walk.kin * kDlK;  // k of this block still inside K
+                uint32_t va[kDl8Loads], vb[kDl8Loads];
+#pragma unroll
+                for (int i = 0; i < kDl8Loads; ++i) {
+                    va[i] = kl_a[i] < rem ? voff_a[i] : kDlOob;
+                    vb[i] = kl_b[i] < rem ? voff_b[i] : kDlOob;
+                }
+                dl_issue<kDl8Loads>(dl_rsrc(walk.a_base, p.a_bytes), so_a, va, lds_addr(la) + wave_lds);
+                dl_issue<kDl8Loads>(dl_rsrc(walk.b_base, p.b_bytes), so_b, vb, lds_addr(lb) + wave_lds);
+            } else {
+                dl_issue<kDl8Loads>(dl_rsrc(walk.a_base, p.a_bytes), so_a, voff_a, lds_addr(la) + wave_lds);
+                dl_issue<kDl8Loads>(dl_rsrc(walk.b_base, p.b_bytes), so_b, voff_b, lds_addr(lb) + wave_lds);
+            }
             walk.advance();
         };
         // Read order A0, B0..B3, A1..A3: the step's MFMAs (A_i x B_j,
@@ -2120,8 +2162,14 @@ KernelFn pick_bf16_big(bool a_kmaj, bool b_kmaj) {
 #endif
 constexpr bool kBf16Dl8 = TF_BF16_DL8 != 0;
 constexpr int kBf16DlThreads = kBf16Dl8 ? 2 * kThreads : kThreads;
-KernelFn pick_bf16_dl(bool a_kmaj, bool b_kmaj) {
+KernelFn pick_bf16_dl(bool a_kmaj, bool b_kmaj, bool ktail) {
     if constexpr (kBf16Dl8) {
+        if (ktail) {
+            if (a_kmaj && b_kmaj) return gemm_bf16_dl8_kernel<true, true, true>;
+            if (a_kmaj && !b_kmaj) return gemm_bf16_dl8_kernel<true, false, true>;
+            if (!a_kmaj && b_kmaj) return gemm_bf16_dl8_kernel<false, true, true>;
+            return gemm_bf16_dl8_kernel<false, false, true>;
+        }
         if (a_kmaj && b_kmaj) return gemm_bf16_dl8_kernel<true, true>;
         if (a_kmaj && !b_kmaj) return gemm_bf16_dl8_kernel<true, false>;
         if (!a_kmaj && b_kmaj) return gemm_bf16_dl8_kernel<false, true>;
@@ -2211,13 +2259,15 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     p.vec_c4 = (reinterpret_cast<uintptr_t>(C) & (c_vec_bytes - 1)) == 0 && (ldc % 4 == 0) && (p.stride_c % 4 == 0);
     if (big) {
         // Interior tiles take the direct-to-LDS kernel when the operands are
-        // 16-byte loadable, K is a whole number of 64-deep blocks (the split
-        // boundaries of both kernels then agree) and each operand's extent
-        // fits the buffer descriptor.
+        // 16-byte loadable, K is a whole number of 16-byte loads (both
+        // kernels count splits in 64-deep blocks, the last one partial when
+        // K % 64 != 0, so their split boundaries agree) and each operand's
+        // extent fits the buffer descriptor.
         const int64_t ext_a = trans_a ? (K - 1) * lda + M : (M - 1) * lda + K;
         const int64_t ext_b = trans_b ? (N - 1) * ldb + K : (K - 1) * ldb + N;
         const int64_t lim = (int64_t)0x7fffffff;  // descriptor extent is passed as int
-        const bool direct = K > 0 && K % 64 == 0 && p.vec_a && p.vec_b && ext_a * esz <= lim && ext_b * esz <= lim;
+        const int64_t k_unit = kBf16Dl8 ? 8 : 64;   // the four-wave kernel has no K tail
+        const bool direct = K > 0 && K % k_unit == 0 && p.vec_a && p.vec_b && ext_a * esz <= lim && ext_b * esz <= lim;
         p.a_bytes = direct ? (uint32_t)(ext_a * esz) : 0u;
         p.b_bytes = direct ? (uint32_t)(ext_b * esz) : 0u;
         // Partial tiles at the M / N edges are fine for the direct kernel:
@@ -2287,7 +2337,7 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
             q.tiles_m = p.int_m;
             q.tiles_n = p.int_n;
             dim3 grid((unsigned)n_int, (unsigned)splits, (unsigned)grid_batch);
-            pick_bf16_dl(a_kmaj, b_kmaj)<<<grid, kBf16DlThreads, 0, ctx->stream>>>(q);
+            pick_bf16_dl(a_kmaj, b_kmaj, K % 64 != 0)<<<grid, kBf16DlThreads, 0, ctx->stream>>>(q);
             st = tfh::check_launch("gemm_bf16_dl_kernel");
             if (st != TF_OK) return st;
         }

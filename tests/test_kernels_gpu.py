@@ -357,6 +357,39 @@ def test_gemm_reduce_batch_walk(ctx, dt, nb, M, N, K):
     assert_close(dc.numpy(), truth, RTOL16 if dt == "bf16" else RTOL32, f"{dt} batch reduction {nb}x{M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("ta,tb,nb,M,N,K,pad", [
+    (False, False, 1, 4096, 4096, 1000, 0),   # last 32-deep block holds 8 of K
+    (False, True, 1, 4096, 2048, 968, 8),     # whole last block past K; split in two; padded rows
+    (True, False, 1, 4096, 4096, 200, 0),
+    (True, True, 1, 4096, 4096, 8, 0),        # one 64-deep block, 56 of it masked
+    (True, False, 3, 4096, 4096, 200, 0),     # batch reduction: the walk wraps after a partial block
+    (False, False, 2, 2048, 2048, 1000, 8),   # batch reduction split over K, slices start mid-element
+])
+def test_gemm_bf16_direct_k_tail(ctx, ta, tb, nb, M, N, K, pad):
+    # K % 64 != 0 on the direct large-tile kernel: the loads of k >= K must
+    # read zero.  Past K lie the padding of K-major rows (random here), the
+    # next row, or the next batch element, so a leak changes the result.
+    import tensors_amd as ta_mod
+    from tensors_amd import ops
+    lda = (M if ta else K) + pad
+    ldb = (K if tb else N) + pad
+    a_shape = (nb, K, lda) if ta else (nb, M, lda)
+    b_shape = (nb, N, ldb) if tb else (nb, K, ldb)
+    a16 = ta_mod.f32_to_bf16_bits(synth.normal(241 + K, a_shape))
+    b16 = ta_mod.f32_to_bf16_bits(synth.normal(242 + K, b_shape))
+    a, b = ta_mod.bf16_bits_to_f32(a16), ta_mod.bf16_bits_to_f32(b16)
+    dc = ctx.zeros((M, N))
+    ops.gemm_ex(ctx.array(a16, ta_mod.BF16), ctx.array(b16, ta_mod.BF16), dc, M, N, K, lda=lda, ldb=ldb, ldc=N,
+                trans_a=ta, trans_b=tb, stride_a=a_shape[1] * lda, stride_b=b_shape[1] * ldb, batch=nb,
+                reduce_batch=nb > 1)
+    truth = np.zeros((M, N))
+    for e in range(nb):
+        ae = a[e][:, :M] if ta else a[e][:, :K]
+        be = b[e][:, :K] if tb else b[e][:, :N]
+        truth += _gemm_truth(ae, be, ta, tb)
+    assert_close(dc.numpy(), truth, RTOL16, f"bf16 K tail ta={ta} tb={tb} {nb}x{M}x{N}x{K} pad={pad}")
+
+
 def test_gemm_strided_batched(ctx):
     from tensors_amd._lib import TF_F32, call
     B, M, N, K = 5, 33, 47, 29
