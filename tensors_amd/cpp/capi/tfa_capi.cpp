@@ -414,6 +414,52 @@ void t_linear_grads(Device d) {
     }
 }
 
+// Linear::forward_relu = relu(Linear::forward): the same layer and upstream
+// as t_linear_grads, rows with a negative pre-activation masked out.
+void t_linear_relu_fused(Device d) {
+    nn::Linear fc(3, 2);
+    fc.to(d);
+    Tensor W = from_vals({1, 2, 3, 4, 5, 6}, {2, 3}, d);
+    Tensor b = from_vals({0.5f, -1.0f}, {2}, d);
+    for (auto& np : fc.named_parameters()) {
+        np.second->data_ = np.first == "weight" ? W : b;
+        np.second->data_.requires_grad(true);
+    }
+    Tensor x = from_vals({1, 0, -1, 2, 1, 0}, {2, 3}, d);
+    x.requires_grad(true);
+    Tensor y = fc.forward_relu(x);
+    check_vec(y, {0.0f, 0.0f, 4.5f, 12.0f}, "y");
+    Tensor up = from_vals({1, 2, 3, 4}, {2, 2}, d);
+    Engine().execute(y.autograd_meta()->grad_fn_, up, false);
+    // dZ = up * (y > 0) = [[0, 0], [3, 4]].
+    check_vec(x.grad(), {0, 0, 0, 19, 26, 33}, "dX");
+    for (auto& np : fc.named_parameters()) {
+        if (np.first == "weight") check_vec(np.second->data_.grad(), {6, 3, 0, 8, 4, 0}, "dW");
+        if (np.first == "bias") check_vec(np.second->data_.grad(), {3, 4}, "db");
+    }
+}
+
+// Conv2dModule::forward_relu on a 1x1 convolution (w = 2, b = 0).
+void t_conv_relu_fused(Device d) {
+    Tensor x = from_vals({1, -2, 3, -4}, {1, 1, 2, 2}, d);
+    x.requires_grad(true);
+    nn::Conv2dModule conv(1, 1, 1);
+    conv.to(d);
+    for (auto& np : conv.named_parameters()) {
+        if (np.first == "weight") np.second->data_ = from_vals({2.0f}, {1, 1, 1, 1}, d);
+        np.second->data_.requires_grad(true);
+    }
+    Tensor y = conv.forward_relu(x);
+    check_vec(y, {2, 0, 6, 0}, "y");
+    Tensor up = from_vals({0.1f, 0.2f, 0.3f, 0.4f}, {1, 1, 2, 2}, d);
+    Engine().execute(y.autograd_meta()->grad_fn_, up, false);
+    check_vec(x.grad(), {0.2f, 0.0f, 0.6f, 0.0f}, "dX");
+    for (auto& np : conv.named_parameters()) {
+        if (np.first == "weight") check_vec(np.second->data_.grad(), {1.0f}, "dW");
+        if (np.first == "bias") check_vec(np.second->data_.grad(), {0.4f}, "db");
+    }
+}
+
 // optim::SGD momentum rule v = mu v + g; p = p - lr v (nn/optim/SGD.hpp:3-6).
 void t_sgd_momentum_rule(Device d) {
     Tensor p = from_vals({1.0f, -2.0f}, {2}, d);
@@ -467,6 +513,8 @@ const std::map<std::string, std::function<void(Device)>>& registry() {
         {"conv_1x1_golden", t_conv_1x1_golden},
         {"conv2d_explicit_backward", t_conv2d_module_explicit_backward},
         {"linear_grads", t_linear_grads},
+        {"linear_relu_fused", t_linear_relu_fused},
+        {"conv_relu_fused", t_conv_relu_fused},
         {"sgd_momentum_rule", t_sgd_momentum_rule},
         {"reshape_grad", t_reshape_grad},
         {"sum_broadcast", t_sum_broadcast},
@@ -524,7 +572,6 @@ int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t ste
         for (auto& fc : layers)
             for (auto* p : fc->parameters()) params.push_back(&p->data_);
         nn::optim::SGD opt(params, lr, mu);
-        nn::ReLU relu;
         nn::CrossEntropyLoss ce;
 
         std::vector<Tensor> xb, yb;
@@ -536,10 +583,9 @@ int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t ste
         loss_t.reserve(static_cast<size_t>(steps));
         auto run_step = [&](int64_t s) {
             Tensor h = xb[s % n_batches];
-            for (size_t l = 0; l < layers.size(); ++l) {
-                h = layers[l]->forward(h);
-                if (l + 1 < layers.size()) h = relu.forward(h);
-            }
+            // Hidden layers: Linear then ReLU, fused into one GEMM on the GPU.
+            for (size_t l = 0; l < layers.size(); ++l)
+                h = l + 1 < layers.size() ? layers[l]->forward_relu(h) : layers[l]->forward(h);
             Tensor loss = ce.forward(h, yb[s % n_batches]);
             loss.backward();
             opt.step();
@@ -600,7 +646,6 @@ int tfa_cnn_train(int64_t batch, int64_t H, int64_t W, int64_t steps, int64_t wa
         for (nn::Module* m : std::initializer_list<nn::Module*>{&conv1, &conv2, &fc})
             for (auto* p : m->parameters()) params.push_back(&p->data_);
         nn::optim::SGD opt(params, lr, mu);
-        nn::ReLU relu;
         nn::CrossEntropyLoss ce;
         std::vector<Tensor> xb, yb;
         for (int64_t i = 0; i < n_batches; ++i) {
@@ -609,8 +654,9 @@ int tfa_cnn_train(int64_t batch, int64_t H, int64_t W, int64_t steps, int64_t wa
         }
         std::vector<Tensor> loss_t;
         auto run_step = [&](int64_t s) {
-            Tensor h = relu.forward(conv1.forward(xb[s % n_batches]));
-            h = relu.forward(conv2.forward(h));
+            // Conv then ReLU, fused into one GEMM on the GPU.
+            Tensor h = conv1.forward_relu(xb[s % n_batches]);
+            h = conv2.forward_relu(h);
             h = reshape(h, Shape{batch, flat});
             Tensor loss = ce.forward(fc.forward(h), yb[s % n_batches]);
             loss.backward();

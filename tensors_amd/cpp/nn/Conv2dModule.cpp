@@ -1,6 +1,7 @@
 #include "nn/Conv2dModule.hpp"
 
 #include "autograd/Wiring.hpp"
+#include "autograd/ops/ReluBackward.hpp"
 #include "hip/HipBackend.hpp"
 #include "nn/ConvCommon.hpp"
 #include "tensor/factory.hpp"
@@ -15,7 +16,7 @@ namespace tensorforge::nn {
 namespace detail {
 
 Tensor conv2d_forward(const Tensor& x, const Tensor& w, const Tensor* bias, int64_t sh, int64_t sw, int64_t ph,
-                      int64_t pw, int64_t dh, int64_t dw) {
+                      int64_t pw, int64_t dh, int64_t dw, bool relu) {
     if (x.shape().ndim() != 4) throw std::invalid_argument("Conv2d.forward expects [N, Cin, H, W]");
     if (x.dtype() != Dtype::Float32) throw std::invalid_argument("Conv2d.forward: only Float32 supported");
     if (x.device() != w.device()) throw std::invalid_argument("Conv2d.forward: input and weight on different devices");
@@ -41,10 +42,12 @@ Tensor conv2d_forward(const Tensor& x, const Tensor& w, const Tensor* bias, int6
         Tensor col = Tensor::empty(Shape{g.N, KK, P}, Dtype::Float32, x.device());
         hip::im2col(x, col, g.kH, g.kW, sh, sw, ph, pw, dh, dw);
         hip::gemm_ex(x.device().index, false, false, g.Cout, P, KK, w.data(), KK, 0, col.data(), P, KK * P, y.data(), P,
-                     g.Cout * P, g.N, false, Dtype::Float32, Dtype::Float32, bias ? TF_EPI_ROW_BIAS : TF_EPI_NONE,
+                     g.Cout * P, g.N, false, Dtype::Float32, Dtype::Float32,
+                     bias ? (relu ? TF_EPI_ROW_BIAS_RELU : TF_EPI_ROW_BIAS) : (relu ? TF_EPI_RELU : TF_EPI_NONE),
                      bias ? static_cast<const float*>(bias->data()) : nullptr);
         saved = col;
     } else {
+        if (relu) throw std::invalid_argument("conv2d_forward: fused ReLU is a GPU path");
         // Direct loop in the reference's order (nn/Conv2dModule.cpp:26-70).
         const float* in = static_cast<const float*>(x.data());
         const float* wt = static_cast<const float*>(w.data());
@@ -70,9 +73,16 @@ Tensor conv2d_forward(const Tensor& x, const Tensor& w, const Tensor* bias, int6
     }
     if (x.requires_grad() || w.requires_grad() || (bias && bias->requires_grad())) {
         auto node = std::make_shared<Conv2dBackward>(saved, w, bias != nullptr, g);
-        wiring::attach(y, node,
-                       {wiring::accumulator_edge(x), wiring::accumulator_edge(w),
-                        bias ? wiring::accumulator_edge(*bias) : Edge(nullptr, 0)});
+        std::vector<Edge> edges = {wiring::accumulator_edge(x), wiring::accumulator_edge(w),
+                                   bias ? wiring::accumulator_edge(*bias) : Edge(nullptr, 0)};
+        if (relu) {
+            // The graph of the convolution then relu(), without the
+            // pre-activation tensor; the ReLU mask is y > 0.
+            node->next_edges_ = std::move(edges);
+            wiring::attach(y, std::make_shared<ReluBackward>(y), {Edge(node, 0)});
+        } else {
+            wiring::attach(y, node, std::move(edges));
+        }
     }
     return y;
 }
@@ -95,14 +105,21 @@ Conv2dModule::Conv2dModule(int in_channels, int out_channels, int kernel_size, i
     if (bias_enabled_) register_parameter("bias", Parameter(zeros(Shape{out_channels}, Dtype::Float32, Device::cpu())));
 }
 
-Tensor Conv2dModule::forward(Tensor x) {
+Tensor Conv2dModule::forward(Tensor x) { return forward_impl(std::move(x), false); }
+
+Tensor Conv2dModule::forward_relu(Tensor x) {
+    if (x.device().type != DeviceType::CUDA) return forward_impl(std::move(x), false).relu();
+    return forward_impl(std::move(x), true);
+}
+
+Tensor Conv2dModule::forward_impl(Tensor x, bool relu) {
     if (x.shape().ndim() != 4) throw std::invalid_argument("Conv2dModule.forward expects [N, Cin, H, W]");
     if (x.shape()[1] != in_channels_) throw std::invalid_argument("Conv2dModule.forward: Cin mismatch");
     if (kernel_size_ <= 0 || stride_ <= 0 || dilation_ <= 0)
         throw std::invalid_argument("Conv2dModule.forward: non-positive stride/dilation/kernel");
     const Tensor& w = parameters_.at("weight").data_;
     const Tensor* b = bias_enabled_ ? &parameters_.at("bias").data_ : nullptr;
-    return detail::conv2d_forward(x, w, b, stride_, stride_, padding_, padding_, dilation_, dilation_);
+    return detail::conv2d_forward(x, w, b, stride_, stride_, padding_, padding_, dilation_, dilation_, relu);
 }
 
 }  // namespace tensorforge::nn

@@ -16,8 +16,14 @@ public:
                  int dilation = 1, bool bias = true);
 
     [[nodiscard]] Tensor forward(Tensor x) override;
+    // relu(forward(x)) with the ReLU in the GEMM epilogue on the GPU; same
+    // values and backward graph as the two calls (no counterpart in the
+    // reference, which has only the separate modules).
+    [[nodiscard]] Tensor forward_relu(Tensor x);
 
 private:
+    [[nodiscard]] Tensor forward_impl(Tensor x, bool relu);
+
     int in_channels_;
     int out_channels_;
     int kernel_size_;

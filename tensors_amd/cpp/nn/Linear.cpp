@@ -2,6 +2,7 @@
 
 #include "autograd/Wiring.hpp"
 #include "autograd/ops/LinearBackward.hpp"
+#include "autograd/ops/ReluBackward.hpp"
 #include "hip/HipBackend.hpp"
 #include "hip/Shadow.hpp"
 #include "tensor/Compat.hpp"
@@ -34,7 +35,14 @@ void Linear::set_compute_dtype(Dtype dtype) {
     compute_dtype_ = dtype;
 }
 
-Tensor Linear::forward(Tensor x) {
+Tensor Linear::forward(Tensor x) { return forward_impl(std::move(x), false); }
+
+Tensor Linear::forward_relu(Tensor x) {
+    if (x.device().type != DeviceType::CUDA) return forward_impl(std::move(x), false).relu();
+    return forward_impl(std::move(x), true);
+}
+
+Tensor Linear::forward_impl(Tensor x, bool relu) {
     if (x.shape().ndim() != 2) throw std::invalid_argument("Linear.forward expects 2D input [N, in_features]");
     if (x.shape()[1] != in_features_) throw std::invalid_argument("Linear.forward: in_features mismatch");
     const Tensor& W = parameters_.at("weight").data_;
@@ -50,13 +58,13 @@ Tensor Linear::forward(Tensor x) {
             if (x.dtype() != Dtype::BFloat16) x = x.to(Dtype::BFloat16);
             Tensor w16 = hip::shadow_for(W);
             y = Tensor::empty(Shape{B, out_features_}, Dtype::BFloat16, x.device());
-            hip::gemm(x, false, w16, true, y, 1.0f, 0.0f, b);
+            hip::gemm(x, false, w16, true, y, 1.0f, 0.0f, b, relu);
             if (x.requires_grad() || W.requires_grad() || (b && b->requires_grad()))
                 node = std::make_shared<LinearBackward>(x, w16, use_bias, Dtype::Float32);
         } else {
             if (x.dtype() != Dtype::Float32) throw std::invalid_argument("Linear.forward: Float32 input expected");
             y = Tensor::empty(Shape{B, out_features_}, Dtype::Float32, x.device());
-            hip::gemm(x, false, W, true, y, 1.0f, 0.0f, b);
+            hip::gemm(x, false, W, true, y, 1.0f, 0.0f, b, relu);
             if (x.requires_grad() || W.requires_grad() || (b && b->requires_grad()))
                 node = std::make_shared<LinearBackward>(x, W, use_bias, Dtype::Float32);
         }
@@ -83,9 +91,17 @@ Tensor Linear::forward(Tensor x) {
             node = std::make_shared<LinearBackward>(x, W, use_bias, Dtype::Float32);
     }
     if (node) {
-        wiring::attach(y, node,
-                       {wiring::accumulator_edge(x), wiring::accumulator_edge(W),
-                        b ? wiring::accumulator_edge(*b) : Edge(nullptr, 0)});
+        std::vector<Edge> edges = {wiring::accumulator_edge(x), wiring::accumulator_edge(W),
+                                   b ? wiring::accumulator_edge(*b) : Edge(nullptr, 0)};
+        if (relu) {
+            // The graph of forward() then relu(): ReluBackward -> LinearBackward,
+            // without the pre-activation tensor.  The ReLU node's mask is taken
+            // from y (y > 0 exactly where the pre-activation is > 0).
+            node->next_edges_ = std::move(edges);
+            wiring::attach(y, std::make_shared<ReluBackward>(y), {Edge(node, 0)});
+        } else {
+            wiring::attach(y, node, std::move(edges));
+        }
     }
     return y;
 }

@@ -20,6 +20,11 @@ public:
     Linear(int in_features, int out_features, bool bias = true);
 
     [[nodiscard]] Tensor forward(Tensor x) override;
+    // relu(forward(x)) with the ReLU in the GEMM epilogue on the GPU (one
+    // launch, no pre-activation tensor).  Same values and the same backward
+    // graph (ReluBackward -> LinearBackward) as the two calls; no counterpart
+    // in the reference, which has only the separate modules.
+    [[nodiscard]] Tensor forward_relu(Tensor x);
 
     [[nodiscard]] int in_features() const noexcept { return in_features_; }
     [[nodiscard]] int out_features() const noexcept { return out_features_; }
@@ -28,6 +33,8 @@ public:
     [[nodiscard]] Dtype compute_dtype() const noexcept { return compute_dtype_; }
 
 private:
+    [[nodiscard]] Tensor forward_impl(Tensor x, bool relu);
+
     int in_features_;
     int out_features_;
     bool bias_enabled_;
