@@ -12,6 +12,8 @@
 //   dx[n][c][ih][iw] = sum_{ki,kj : (ih + ph - ki*dh) % sh == 0, ...} col[...]
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace {
 
 struct ConvGeom {
@@ -90,6 +92,82 @@ __global__ void col2im_kernel(const T* __restrict__ col, T* __restrict__ dx, Con
     }
 }
 
+// Plane forms, used when a channel plane and its kH*kW column rows fit in
+// LDS (the common case): one block per (n, c) plane or part of its rows.
+// col[n][c*kH*kW + r][o] for fixed (n, c) is one contiguous run of
+// kH*kW*outH*outW elements, so the block's stores (im2col) or loads
+// (col2im) are a single coalesced stream, the other side goes through LDS,
+// and the index arithmetic is 32-bit.  Same values as the element forms:
+// im2col copies, col2im sums the taps in the same (ki, kj) order.
+constexpr int kPlaneLdsFloats = 16384;  // 64 KB of LDS per block
+
+// Rows r0 .. r0 + rows_per_block - 1 of plane blockIdx.x.
+template <typename T>
+__global__ __launch_bounds__(256) void im2col_plane_kernel(const T* __restrict__ x, T* __restrict__ col, ConvGeom g64,
+                                                           int rows_per_block) {
+    extern __shared__ float plane[];
+    const int H = (int)g64.H, W = (int)g64.W, kW = (int)g64.kW, outW = (int)g64.outW;
+    const int sh = (int)g64.sh, sw = (int)g64.sw, dh = (int)g64.dh, dw = (int)g64.dw;
+    const int kk = (int)(g64.kH * g64.kW), sp = (int)(g64.outH * g64.outW), hw = H * W;
+    const int64_t nc = blockIdx.x;
+    const T* xp = x + nc * hw;
+    for (int i = threadIdx.x; i < hw; i += 256) plane[i] = ldf(xp, i);
+    __syncthreads();
+    const int r0 = blockIdx.y * rows_per_block, r1 = min(kk, r0 + rows_per_block);
+    T* cp = col + nc * kk * sp;
+    for (int r = r0; r < r1; ++r) {
+        const int ki = r / kW, kj = r - ki * kW;
+        const int ih0 = ki * dh - (int)g64.ph, iw0 = kj * dw - (int)g64.pw;
+        for (int o = threadIdx.x; o < sp; o += 256) {
+            const int oh = o / outW, ow = o - oh * outW;
+            const int ih = oh * sh + ih0, iw = ow * sw + iw0;
+            float v = 0.0f;
+            if ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) v = plane[ih * W + iw];
+            stf(cp, (int64_t)r * sp + o, v);
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void col2im_plane_kernel(const T* __restrict__ col, T* __restrict__ dx, ConvGeom g64) {
+    extern __shared__ float cols[];
+    const int H = (int)g64.H, W = (int)g64.W, kH = (int)g64.kH, kW = (int)g64.kW;
+    const int outH = (int)g64.outH, outW = (int)g64.outW, sh = (int)g64.sh, sw = (int)g64.sw;
+    const int ph = (int)g64.ph, pw = (int)g64.pw, dh = (int)g64.dh, dw = (int)g64.dw;
+    const int sp = outH * outW, n_col = kH * kW * sp, hw = H * W;
+    const int64_t nc = blockIdx.x;
+    const T* cp = col + nc * n_col;
+    for (int i = threadIdx.x; i < n_col; i += 256) cols[i] = ldf(cp, i);
+    __syncthreads();
+    T* dp = dx + nc * hw;
+    for (int p = threadIdx.x; p < hw; p += 256) {
+        const int ih = p / W, iw = p - ih * W;
+        float acc = 0.0f;
+        for (int ki = 0; ki < kH; ++ki) {
+            const int hh = ih + ph - ki * dh;
+            if (hh < 0 || hh % sh != 0) continue;
+            const int oh = hh / sh;
+            if (oh >= outH) continue;
+            for (int kj = 0; kj < kW; ++kj) {
+                const int ww = iw + pw - kj * dw;
+                if (ww < 0 || ww % sw != 0) continue;
+                const int ow = ww / sw;
+                if (ow >= outW) continue;
+                acc += cols[(ki * kW + kj) * sp + oh * outW + ow];
+            }
+        }
+        stf(dp, p, acc);
+    }
+}
+
+// The plane forms' 32-bit index arithmetic stays in range: every input
+// coordinate they form lies within +-2^24.
+bool plane_indices_fit(const ConvGeom& g) {
+    const int64_t lim = 1LL << 24;
+    return (g.outH - 1) * g.sh + (g.kH - 1) * g.dh < lim && (g.outW - 1) * g.sw + (g.kW - 1) * g.dw < lim &&
+           g.ph < lim && g.pw < lim && g.H < lim && g.W < lim;
+}
+
 tf_status make_geom(ConvGeom& g, int64_t N, int64_t C, int64_t H, int64_t W, int64_t kH, int64_t kW, int64_t sh,
                     int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw) {
     TF_REQUIRE(N >= 0 && C >= 0 && H >= 0 && W >= 0, "conv: negative extent");
@@ -115,6 +193,21 @@ tf_status tf_im2col(tf_ctx* ctx, const void* x, void* col, int64_t N, int64_t C,
     const int64_t total = N * C * kH * kW * g.outH * g.outW;
     if (total == 0) return TF_OK;
     TF_REQUIRE(x && col, "tf_im2col: null pointer");
+    TF_REQUIRE(dtype == TF_F32 || dtype == TF_BF16, "tf_im2col: dtype must be Float32 or BFloat16");
+    const int64_t planes = N * C, sp = g.outH * g.outW, kk = kH * kW;
+    if (H * W <= kPlaneLdsFloats && kk * sp <= (1LL << 30) && planes >= 256 && planes < (1LL << 31) &&
+        plane_indices_fit(g)) {
+        // Row groups of about 4096 outputs per block.
+        const int64_t groups = std::min<int64_t>({kk, std::max<int64_t>(1, (kk * sp) / 4096), 1024});
+        const int rpb = (int)((kk + groups - 1) / groups);
+        const dim3 grid((unsigned)planes, (unsigned)((kk + rpb - 1) / rpb));
+        const size_t lds = (size_t)(H * W) * sizeof(float);
+        if (dtype == TF_F32)
+            im2col_plane_kernel<float><<<grid, 256, lds, ctx->stream>>>((const float*)x, (float*)col, g, rpb);
+        else
+            im2col_plane_kernel<uint16_t><<<grid, 256, lds, ctx->stream>>>((const uint16_t*)x, (uint16_t*)col, g, rpb);
+        return tfh::check_launch("im2col_plane_kernel");
+    }
     if (dtype == TF_F32) {
         im2col_kernel<float><<<tfd::grid_for(total, 4), 256, 0, ctx->stream>>>((const float*)x, (float*)col, g);
     } else if (dtype == TF_BF16) {
@@ -134,6 +227,18 @@ tf_status tf_col2im(tf_ctx* ctx, const void* col, void* dx, int64_t N, int64_t C
     const int64_t total = N * C * H * W;
     if (total == 0) return TF_OK;
     TF_REQUIRE(col && dx, "tf_col2im: null pointer");
+    TF_REQUIRE(dtype == TF_F32 || dtype == TF_BF16, "tf_col2im: dtype must be Float32 or BFloat16");
+    const int64_t planes = N * C, n_col = kH * kW * g.outH * g.outW;
+    if (n_col <= kPlaneLdsFloats && H * W < (1LL << 30) && planes >= 256 && planes < (1LL << 31) &&
+        plane_indices_fit(g)) {
+        const size_t lds = (size_t)n_col * sizeof(float);
+        if (dtype == TF_F32)
+            col2im_plane_kernel<float><<<(unsigned)planes, 256, lds, ctx->stream>>>((const float*)col, (float*)dx, g);
+        else
+            col2im_plane_kernel<uint16_t><<<(unsigned)planes, 256, lds, ctx->stream>>>((const uint16_t*)col,
+                                                                                     (uint16_t*)dx, g);
+        return tfh::check_launch("col2im_plane_kernel");
+    }
     if (dtype == TF_F32) {
         col2im_kernel<float><<<tfd::grid_for(total, 2), 256, 0, ctx->stream>>>((const float*)col, (float*)dx, g);
     } else if (dtype == TF_BF16) {

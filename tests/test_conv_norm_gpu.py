@@ -65,6 +65,14 @@ IM2COL_CASES = [
     (3, 1, 5, 6, 1, 1, 0, 1),
     (128, 3, 32, 32, 3, 1, 1, 1),       # C4 conv1
     (16, 32, 32, 32, 3, 2, 1, 1),       # C4 conv2 geometry (reduced batch)
+    # >= 256 planes: the LDS plane forms (im2col in row groups, col2im per plane)
+    (128, 32, 32, 32, 3, 2, 1, 1),      # C4 conv2 at full size
+    (64, 8, 9, 7, 3, 2, 1, 1),          # odd plane, stride 2
+    (32, 16, 10, 10, 3, 1, 2, 2),       # dilation 2
+    (256, 1, 5, 6, 1, 1, 0, 1),         # 1x1
+    (32, 8, 13, 11, 5, 3, 2, 1),        # stride 3, 5x5
+    (16, 16, 64, 64, 5, 1, 2, 1),       # im2col in 25 row groups; col2im column chunk too big for LDS
+    (2, 128, 130, 130, 3, 1, 1, 1),     # plane too big for LDS: element forms
 ]
 
 
