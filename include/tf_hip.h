@@ -99,9 +99,13 @@ tf_status tf_hip_sync(tf_ctx* ctx);
  * bytes == 0 allocates 1 byte, as the reference does
  * (cuda/memory/storage_allocator_test.cpp:42-48). */
 tf_status tf_hip_alloc(tf_ctx* ctx, size_t bytes, void** out);
-/* Stream-ordered free back into the pool. NULL is a no-op. */
+/* Stream-ordered free: the block waits in the context's cache for the next
+ * allocation of its size class (512-byte steps to 1 MB, 2 MB steps above)
+ * on the context's stream.  NULL is a no-op; a pointer this context did not
+ * allocate (or already freed) is an error. */
 tf_status tf_hip_free(tf_ctx* ctx, void* ptr);
-/* Return cached pool memory above `keep_bytes` to the device. */
+/* Hand the context's cached blocks back to the pool and return pool memory
+ * above `keep_bytes` to the device. */
 tf_status tf_hip_trim(tf_ctx* ctx, size_t keep_bytes);
 /* Bytes currently reserved by the pool and in use by live allocations. */
 tf_status tf_hip_pool_stats(tf_ctx* ctx, uint64_t* reserved, uint64_t* used);

@@ -7,7 +7,10 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
+#include <unordered_map>
+#include <vector>
 
 #include "tf_hip.h"
 
@@ -21,6 +24,15 @@ struct tf_ctx {
     // per-row losses).  Grown on demand from the pool; stream-ordered.
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    // Block cache in front of the pool (tf_hip_alloc / tf_hip_free): freed
+    // blocks wait here by size class and go to the next request of that
+    // class, stream-ordered on `stream` like the pool's own reuse.  A pool
+    // round trip (hipFreeAsync + hipMallocFromPoolAsync) costs 30-70 us of
+    // host time per block on this runtime; a cache hit costs a map lookup.
+    std::mutex cache_mu;
+    std::unordered_map<size_t, std::vector<void*>> cached;  // size class -> free blocks
+    std::unordered_map<void*, size_t> live;                  // block -> size class
+    size_t cached_bytes = 0;
 };
 
 namespace tfh {
