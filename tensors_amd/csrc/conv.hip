@@ -101,6 +101,22 @@ __global__ void col2im_kernel(const T* __restrict__ col, T* __restrict__ dx, Con
 // im2col copies, col2im sums the taps in the same (ki, kj) order.
 constexpr int kPlaneLdsFloats = 16384;  // 64 KB of LDS per block
 
+// dst[0 .. n) = src[0 .. n) as floats, by the whole block: eight loads in
+// flight per thread before their LDS stores (a plain strided loop waits for
+// each load in turn).
+template <typename T>
+__device__ __forceinline__ void stage_to_lds(const T* __restrict__ src, float* dst, int n) {
+    int i = threadIdx.x;
+    for (; i + 7 * 256 < n; i += 8 * 256) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = ldf(src, i + u * 256);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) dst[i + u * 256] = v[u];
+    }
+    for (; i < n; i += 256) dst[i] = ldf(src, i);
+}
+
 // Rows r0 .. r0 + rows_per_block - 1 of plane blockIdx.x.
 template <typename T>
 __global__ __launch_bounds__(256) void im2col_plane_kernel(const T* __restrict__ x, T* __restrict__ col, ConvGeom g64,
@@ -111,19 +127,26 @@ __global__ __launch_bounds__(256) void im2col_plane_kernel(const T* __restrict__
     const int kk = (int)(g64.kH * g64.kW), sp = (int)(g64.outH * g64.outW), hw = H * W;
     const int64_t nc = blockIdx.x;
     const T* xp = x + nc * hw;
-    for (int i = threadIdx.x; i < hw; i += 256) plane[i] = ldf(xp, i);
+    stage_to_lds(xp, plane, hw);
     __syncthreads();
     const int r0 = blockIdx.y * rows_per_block, r1 = min(kk, r0 + rows_per_block);
     T* cp = col + nc * kk * sp;
-    for (int r = r0; r < r1; ++r) {
-        const int ki = r / kW, kj = r - ki * kW;
-        const int ih0 = ki * dh - (int)g64.ph, iw0 = kj * dw - (int)g64.pw;
-        for (int o = threadIdx.x; o < sp; o += 256) {
-            const int oh = o / outW, ow = o - oh * outW;
-            const int ih = oh * sh + ih0, iw = ow * sw + iw0;
+    const int ph = (int)g64.ph, pw = (int)g64.pw;
+    // Output pixel outer (one division per pixel), rows inner: for each row
+    // the wave's lanes still store consecutive pixels.
+    for (int o = threadIdx.x; o < sp; o += 256) {
+        const int oh = o / outW, ow = o - oh * outW;
+        const int ihb = oh * sh - ph, iwb = ow * sw - pw;
+        int ki = r0 / kW, kj = r0 - (r0 / kW) * kW;
+        for (int r = r0; r < r1; ++r) {
+            const int ih = ihb + ki * dh, iw = iwb + kj * dw;
             float v = 0.0f;
             if ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) v = plane[ih * W + iw];
             stf(cp, (int64_t)r * sp + o, v);
+            if (++kj == kW) {
+                kj = 0;
+                ++ki;
+            }
         }
     }
 }
@@ -137,23 +160,39 @@ __global__ __launch_bounds__(256) void col2im_plane_kernel(const T* __restrict__
     const int sp = outH * outW, n_col = kH * kW * sp, hw = H * W;
     const int64_t nc = blockIdx.x;
     const T* cp = col + nc * n_col;
-    for (int i = threadIdx.x; i < n_col; i += 256) cols[i] = ldf(cp, i);
+    stage_to_lds(cp, cols, n_col);
     __syncthreads();
     T* dp = dx + nc * hw;
+    // Tap (ki, kj) reaches output row oh = (ih + ph - ki*dh) / sh when that
+    // is a whole number in [0, outH); the quotient and remainder are carried
+    // from tap to tap (one division per pixel and axis instead of per tap).
+    const int dqh = dh / sh, drh = dh - dqh * sh, dqw = dw / sw, drw = dw - dqw * sw;
     for (int p = threadIdx.x; p < hw; p += 256) {
         const int ih = p / W, iw = p - ih * W;
+        const int qw0 = (iw + pw) / sw, rw0 = (iw + pw) - qw0 * sw;
+        int qh = (ih + ph) / sh, rh = (ih + ph) - qh * sh;
         float acc = 0.0f;
         for (int ki = 0; ki < kH; ++ki) {
-            const int hh = ih + ph - ki * dh;
-            if (hh < 0 || hh % sh != 0) continue;
-            const int oh = hh / sh;
-            if (oh >= outH) continue;
-            for (int kj = 0; kj < kW; ++kj) {
-                const int ww = iw + pw - kj * dw;
-                if (ww < 0 || ww % sw != 0) continue;
-                const int ow = ww / sw;
-                if (ow >= outW) continue;
-                acc += cols[(ki * kW + kj) * sp + oh * outW + ow];
+            if (qh < 0) break;  // hh < 0 here and for every later ki
+            if (rh == 0 && qh < outH) {
+                const float* crow = cols + ki * kW * sp + qh * outW;
+                int qw = qw0, rw = rw0;
+                for (int kj = 0; kj < kW; ++kj) {
+                    if (qw < 0) break;
+                    if (rw == 0 && qw < outW) acc += crow[kj * sp + qw];
+                    rw -= drw;
+                    qw -= dqw;
+                    if (rw < 0) {
+                        rw += sw;
+                        --qw;
+                    }
+                }
+            }
+            rh -= drh;
+            qh -= dqh;
+            if (rh < 0) {
+                rh += sh;
+                --qh;
             }
         }
         stf(dp, p, acc);
