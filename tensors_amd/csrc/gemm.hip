@@ -2124,6 +2124,52 @@ __global__ __launch_bounds__(256) void splitk_reduce_wide_kernel(GemmParams p, i
 
 using KernelFn = void (*)(GemmParams);
 
+// fp32 GEMM with a short K (<= 32) and few rows (<= 64), A K-major and B
+// MN-major: a convolution over few input channels (W [Cout x Cin*k*k] times
+// each image's im2col block).  An MFMA tile would be mostly padding and one
+// latency-bound k block, so one VALU thread per output column n (of one
+// batch element) keeps its K values of B in registers and produces all M
+// rows.  A sits in LDS zero-padded to 32 columns (the reads are uniform, so
+// they broadcast), which makes every row 32 unconditional FMAs, and the B
+// loads are unconditional too (rows past K re-read row K-1 and are then
+// replaced by zeros).  Sums run over k ascending.
+__global__ __launch_bounds__(256) void gemm_f32_smallk_kernel(GemmParams p) {
+    __shared__ float As[64 * 32];
+    const int64_t b = blockIdx.y;
+    const float* A = reinterpret_cast<const float*>(p.A) + b * p.stride_a;
+    for (int i = threadIdx.x; i < 64 * 32; i += 256) {
+        const int m = i >> 5, k = i & 31;
+        As[i] = (m < p.M && k < p.K) ? A[(int64_t)m * p.lda + k] : 0.0f;
+    }
+    __syncthreads();
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= p.N) return;
+    float bk[32];
+    if (p.K > 0) {
+        const float* B = reinterpret_cast<const float*>(p.B) + b * p.stride_b + n;
+        const int klast = p.K - 1;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            const float v = B[(int64_t)min(k, klast) * p.ldb];
+            bk[k] = k <= klast ? v : 0.0f;  // a select, not a branch: an inf in row K-1 must not meet a 0
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 32; ++k) bk[k] = 0.0f;
+    }
+    const bool has_bias = p.epi != TF_EPI_NONE && p.epi != TF_EPI_RELU;
+    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU || p.epi == TF_EPI_ROW_BIAS_RELU;
+    const float col_bias = (has_bias && !p.row_bias) ? p.bias[n] : 0.0f;
+    const int64_t c0 = b * p.stride_c + n;
+    for (int m = 0; m < p.M; ++m) {
+        const float* a = As + m * 32;
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) acc = fmaf(a[k], bk[k], acc);
+        emit(p, c0 + (int64_t)m * p.ldc, acc, has_bias ? (p.row_bias ? p.bias[m] : col_bias) : 0.0f, relu);
+    }
+}
+
 template <int BN>
 KernelFn pick_f32(bool a_kmaj, bool b_kmaj) {
     if (a_kmaj && b_kmaj) return gemm_f32_kernel<BN, true, true>;
@@ -2257,6 +2303,11 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     p.pair_c = (reinterpret_cast<uintptr_t>(C) & 7) == 0 && (ldc % 2 == 0) && (p.stride_c % 2 == 0);
     const uintptr_t c_vec_bytes = out_dtype == TF_BF16 ? 8 : 16;
     p.vec_c4 = (reinterpret_cast<uintptr_t>(C) & (c_vec_bytes - 1)) == 0 && (ldc % 4 == 0) && (p.stride_c % 4 == 0);
+    if (in_dtype == TF_F32 && !trans_a && !trans_b && !reduce_batch && K <= 32 && M <= 64 && N >= 256) {
+        const dim3 grid((unsigned)((N + 255) / 256), (unsigned)batch);
+        gemm_f32_smallk_kernel<<<grid, 256, 0, ctx->stream>>>(p);
+        return tfh::check_launch("gemm_f32_smallk_kernel");
+    }
     if (big) {
         // Interior tiles take the direct-to-LDS kernel when the operands are
         // 16-byte loadable, K is a whole number of 16-byte loads (both

@@ -390,6 +390,41 @@ def test_gemm_bf16_direct_k_tail(ctx, ta, tb, nb, M, N, K, pad):
     assert_close(dc.numpy(), truth, RTOL16, f"bf16 K tail ta={ta} tb={tb} {nb}x{M}x{N}x{K} pad={pad}")
 
 
+@pytest.mark.parametrize("M,N,K,nb,shared_a,epi,out_bf16,beta", [
+    (32, 1024, 27, 4, True, "row_bias_relu", False, 0.0),   # convolution over 3 channels, 3x3
+    (64, 300, 32, 2, False, "bias", False, 0.0),            # ragged N, column bias, A per element
+    (1, 256, 1, 1, True, "none", False, 0.0),
+    (17, 777, 9, 3, True, "relu", True, 0.0),               # bf16 output
+    (8, 512, 16, 2, False, "none", False, 0.5),             # beta * C
+    (64, 4096, 32, 1, True, "row_bias", False, 0.0),
+])
+def test_gemm_f32_short_k(ctx, M, N, K, nb, shared_a, epi, out_bf16, beta):
+    # K <= 32, M <= 64, N >= 256, A K-major, B MN-major: the VALU path.
+    import tensors_amd as ta_mod
+    from tensors_amd import ops
+    from tensors_amd._lib import TF_EPI_BIAS, TF_EPI_NONE, TF_EPI_RELU, TF_EPI_ROW_BIAS, TF_EPI_ROW_BIAS_RELU
+    codes = {"none": TF_EPI_NONE, "bias": TF_EPI_BIAS, "relu": TF_EPI_RELU, "row_bias": TF_EPI_ROW_BIAS,
+             "row_bias_relu": TF_EPI_ROW_BIAS_RELU}
+    a = synth.normal(261 + K, (1 if shared_a else nb, M, K))
+    b = synth.normal(262 + K, (nb, K, N))
+    c0 = synth.normal(263 + K, (nb, M, N))
+    bias = synth.normal(264 + K, (M if epi.startswith("row") else N,))
+    dc = ctx.empty((nb, M, N), ta_mod.BF16) if out_bf16 else ctx.array(c0)
+    ops.gemm_ex(ctx.array(a), ctx.array(b), dc, M, N, K, lda=K, ldb=N, ldc=N, stride_a=0 if shared_a else M * K,
+                stride_b=K * N, stride_c=M * N, batch=nb, beta=beta, epilogue=codes[epi],
+                bias=ctx.array(bias) if epi in ("bias", "row_bias", "row_bias_relu") else None)
+    truth = np.einsum("bmk,bkn->bmn", np.broadcast_to(a, (nb, M, K)).astype(np.float64), b.astype(np.float64))
+    truth += beta * c0.astype(np.float64)
+    if epi == "bias":
+        truth += bias.astype(np.float64)[None, None, :]
+    if epi.startswith("row"):
+        truth += bias.astype(np.float64)[None, :, None]
+    if epi in ("relu", "row_bias_relu"):
+        truth = np.maximum(truth, 0.0)
+    got = ta_mod.bf16_bits_to_f32(dc.numpy()) if out_bf16 else dc.numpy()
+    assert_close(got, truth, RTOL16 if out_bf16 else RTOL32, f"short-K GEMM {M}x{N}x{K} b{nb} {epi}")
+
+
 def test_gemm_strided_batched(ctx):
     from tensors_amd._lib import TF_F32, call
     B, M, N, K = 5, 33, 47, 29
