@@ -42,6 +42,35 @@ def test_memcpy_roundtrip_and_fill(ctx):
     assert r >= u > 0
 
 
+def test_block_cache_reuse_and_errors(ctx):
+    import ctypes as C
+    from tensors_amd._lib import TFError, call
+    def alloc(n):
+        p = C.c_void_p()
+        call("tf_hip_alloc", ctx.handle, n, C.byref(p))
+        return p.value
+    a = alloc(3000)                  # size class 3072
+    call("tf_hip_free", ctx.handle, a)
+    assert alloc(3001) == a          # same class: the cached block comes back
+    b = alloc(3 << 20)               # 4 MB class
+    call("tf_hip_free", ctx.handle, b)
+    c = alloc(5 << 20)               # 6 MB class: not the cached 4 MB block
+    assert c != b
+    with pytest.raises(TFError):
+        call("tf_hip_free", ctx.handle, b)   # already freed (it sits in the cache)
+    call("tf_hip_free", ctx.handle, c)
+    call("tf_hip_free", ctx.handle, a)
+    call("tf_hip_trim", ctx.handle, 0)       # hands the cache back to the pool
+    d = alloc(1 << 20)
+    x = np.arange(1 << 18, dtype=np.float32)
+    from tensors_amd import _lib
+    call("tf_hip_memcpy", ctx.handle, d, x.ctypes.data, x.nbytes, _lib.TF_COPY_H2D)
+    y = np.empty_like(x)
+    call("tf_hip_memcpy", ctx.handle, y.ctypes.data, d, x.nbytes, _lib.TF_COPY_D2H)
+    assert_bitexact(y, x, "round trip through a block after trim")
+    call("tf_hip_free", ctx.handle, d)
+
+
 def test_zero_size_alloc_and_event_timing(ctx):
     e = ctx.empty((0,), np.float32)
     assert e.ptr is not None            # zero bytes allocates 1 byte
