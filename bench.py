@@ -151,6 +151,16 @@ def bench_c3():
     algo = R * Cc * 4 * 3
     out["c3b_relu_bwd"] = {"us": round(ms * 1e3, 2), "bytes": algo, "gbps": round(algo / ms / 1e6, 1),
                            "frac_hbm": round(algo / ms / 1e6 / PEAK_HBM_GBPS, 3)}
+    # The other backward kernels of the path at the same shape (two reads and
+    # one write of 16 MB each); the values do not affect their speed.
+    for name, fn in (("sigmoid_bwd", lambda i: ops.sigmoid_bwd(dys[i], xs[i], dxs[i])),
+                     ("tanh_bwd", lambda i: ops.tanh_bwd(dys[i], xs[i], dxs[i])),
+                     ("softmax_bwd", lambda i: ops.softmax_bwd(xs[i], dys[i], dxs[i])),
+                     ("mul", lambda i: ops.mul(dys[i], xs[i], dxs[i])),
+                     ("add", lambda i: ops.add(dys[i], xs[i], dxs[i]))):
+        ms = _rotating_bench(ctx, sets, fn)
+        out[f"c3_more_{name}"] = {"us": round(ms * 1e3, 2), "bytes": algo, "gbps": round(algo / ms / 1e6, 1),
+                                  "frac_hbm": round(algo / ms / 1e6 / PEAK_HBM_GBPS, 3)}
     del xs, dys, dxs
     R = Cc = 1024
     sets = 24
