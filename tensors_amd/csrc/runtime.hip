@@ -79,7 +79,22 @@ tf_status ensure_workspace(tf_ctx* ctx, size_t bytes) {
         ctx->ws_bytes = 0;
     }
     size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-    TF_HIP_CHECK(hipMallocFromPoolAsync(&ctx->ws, want, ctx->pool, ctx->stream));
+    hipError_t e = hipMallocFromPoolAsync(&ctx->ws, want, ctx->pool, ctx->stream);
+    if (e == hipErrorOutOfMemory) {
+        // The block cache may hold the memory: hand it back and retry once.
+        (void)hipGetLastError();
+        std::lock_guard<std::mutex> lock(ctx->cache_mu);
+        if (ctx->cached_bytes > 0) {
+            tf_status st = release_cached(ctx);
+            if (st != TF_OK) return st;
+            TF_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+            e = hipMallocFromPoolAsync(&ctx->ws, want, ctx->pool, ctx->stream);
+        }
+    }
+    if (e != hipSuccess) {
+        ctx->ws = nullptr;
+        return hip_error(e, "ensure_workspace: hipMallocFromPoolAsync");
+    }
     ctx->ws_bytes = want;
     return TF_OK;
 }
