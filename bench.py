@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the training hot path on one MI355X.
 
-Default workload ("Isolated Linear backward, fp32"):
+Default workload (the headline benchmark configuration, "Isolated Linear backward, fp32"):
 X, W, dY [2048 x 2048] ~ N(0,1), b [2048] ~ N(0,1); one step is
     Y  = X W^T + b          (fwd GEMM, bias epilogue)
     dX = dY W               (bwd GEMM, NN)
