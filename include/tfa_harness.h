@@ -42,10 +42,11 @@ int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t ste
 /* CNN training (the config-4 network): Conv2dModule(3,32,3,1,1) - ReLU -
  * Conv2dModule(32,64,3,2,1) - ReLU - flatten - Linear(64*(H/2)*(W/2), 10) -
  * CrossEntropyLoss, optim::SGD.  xs [n_batches][batch][3][H][W]; init_params
- * NULL or {conv1.w, conv1.b, conv2.w, conv2.b, fc.w, fc.b} concatenated. */
+ * NULL or {conv1.w, conv1.b, conv2.w, conv2.b, fc.w, fc.b} concatenated;
+ * final_params NULL or out: the same six tensors after the last step. */
 int tfa_cnn_train(int64_t batch, int64_t H, int64_t W, int64_t steps, int64_t warmup, int64_t n_batches,
                   const float* xs, const int64_t* ys, float lr, float mu, int32_t on_gpu, const float* init_params,
-                  float* losses, double* ms_per_step);
+                  float* losses, float* final_params, double* ms_per_step);
 
 /* Runs one of the C++ self-tests (`name`, see tfa_selftest_names) on the CPU
  * (on_gpu = 0) or on GPU 0 (on_gpu = 1). */

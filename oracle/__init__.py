@@ -335,6 +335,94 @@ def mlp_step(weights, vels, x, labels, lr, mu):
     return loss
 
 
+def bf16_round(x):
+    """Nearest bfloat16 value of each float32 (ties to even), as float32.
+
+    bfloat16 keeps the top 16 bits of a float32; rounding adds 0x7FFF plus
+    the lowest kept bit and truncates.  Finite inputs only: a finite value
+    never carries past +/-inf (0x7F7FFFFF + 0x8000 = 0x7F807FFF -> inf).
+    """
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    with np.errstate(over="ignore"):
+        r = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    return r.view(np.float32)
+
+
+def _no_round(x):
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def mlp_step_mixed(weights, biases, vels, bvels, x, labels, lr, mu, rounding=True):
+    """One step of the mixed-precision MLP (config 5): bf16 operands and
+    activations, float32 accumulation, float32 master weights.
+
+    The reference has no bf16 path (tensor/Tensor.cpp:344-346); this restates
+    its graph (nn/Linear.cpp:45-64 forward, Linear+ReLU layers, the
+    cross-entropy of examples/train_mlp.cpp:54-76, the momentum rule of
+    nn/optim/SGD.hpp:3-6) with a bf16 rounding at each point where the mixed
+    precision step stores a bf16 tensor:
+      * the input and each weight's working copy: bf16(x), bf16(W);
+      * each layer's output: bf16(relu(acc + b)) (the last layer without
+        the ReLU); acc is the float32 sum over bf16 products;
+      * the loss gradient: dlogits = (softmax - onehot)/N in float32, then
+        bf16 for the backward GEMMs;
+      * dX = bf16(dY16 @ W16), masked by the layer input's ReLU (y > 0);
+      * dW = dY16^T @ X16 and db = colsum(dY16), both kept in float32;
+      * SGD on the float32 masters: v = mu*v + g, p = p - lr*v, each
+        operation rounded to float32.
+    `rounding=False` turns every bf16 rounding into the identity, which
+    leaves the float32 step (then equal to mlp_step up to summation order).
+    Products run through numpy's float32 BLAS (float32 accumulation, in
+    another order than the GPU).  weights/biases/vels/bvels are updated in
+    place (biases[l] may be None: no bias); returns the loss.
+    """
+    rnd = bf16_round if rounding else _no_round
+    L = len(weights)
+    w16 = [rnd(w) for w in weights]
+    h = rnd(x)
+    acts = [h]
+    for li in range(L):
+        z = h @ w16[li].T
+        if biases[li] is not None:
+            z = z + _f32(biases[li])
+        if li + 1 < L:
+            z = np.maximum(z, np.float32(0))
+        h = rnd(z)
+        acts.append(h)
+    logits = acts[-1].astype(np.float64)
+    labels = np.asarray(labels, dtype=np.int64)
+    N = logits.shape[0]
+    rows = np.arange(N)
+    mx = logits.max(axis=1, keepdims=True)
+    e = np.exp(logits - mx)
+    s = e.sum(axis=1, keepdims=True)
+    lse = mx[:, 0] + np.log(s[:, 0])
+    loss = float(np.mean(lse - logits[rows, labels]))
+    g = e / s
+    g[rows, labels] -= 1.0
+    g /= N
+    g = rnd(g.astype(np.float32))
+    f_lr, f_mu = np.float32(lr), np.float32(mu)
+
+    def sgd(p, grad, v):
+        if mu != 0.0:
+            v[...] = f_mu * v + grad
+            p[...] = p - f_lr * v
+        else:
+            p[...] = p - f_lr * grad
+
+    for li in range(L - 1, -1, -1):
+        dw = (g.T @ acts[li]).astype(np.float32)
+        db = g.astype(np.float64).sum(axis=0).astype(np.float32)
+        if li > 0:
+            dh = rnd(g @ w16[li])
+            g = np.where(acts[li] > 0, dh, np.float32(0)).astype(np.float32)
+        sgd(weights[li], dw, vels[li])
+        if biases[li] is not None:
+            sgd(biases[li], db, bvels[li])
+    return loss
+
+
 def cnn_step(params, vels, x, labels, lr, mu):
     """One config-4 training step in reference order: Conv(3->32, s1 p1) +
     ReLU, Conv(32->64, s2 p1) + ReLU, flatten, Linear(+bias), CE chain;

@@ -30,7 +30,7 @@ def _load() -> C.CDLL:
     p, i64, i32, f = C.c_void_p, C.c_int64, C.c_int32, C.c_float
     lib.tfa_mlp_train.argtypes = [p, i32, i64, i64, i64, i64, p, p, f, f, i32, i32, i32, p, p, p, p]
     lib.tfa_mlp_train.restype = C.c_int
-    lib.tfa_cnn_train.argtypes = [i64, i64, i64, i64, i64, i64, p, p, f, f, i32, p, p, p]
+    lib.tfa_cnn_train.argtypes = [i64, i64, i64, i64, i64, i64, p, p, f, f, i32, p, p, p, p]
     lib.tfa_cnn_train.restype = C.c_int
     return lib
 
@@ -76,14 +76,21 @@ def mlp_train(dims, xs, ys, *, steps, lr, mu, on_gpu, reference_compat=False, bf
     return losses, fw, ms.value
 
 
-def cnn_train(xs, ys, *, steps, lr, mu, on_gpu, init_params=None, warmup=0):
-    """xs [n_batches, B, 3, H, W]; returns (losses, ms_per_step)."""
+def cnn_train(xs, ys, *, steps, lr, mu, on_gpu, init_params=None, warmup=0, want_params=False):
+    """xs [n_batches, B, 3, H, W]; returns (losses, ms_per_step), or
+    (losses, final_params, ms_per_step) with want_params (the six parameters
+    concatenated: conv1.w, conv1.b, conv2.w, conv2.b, fc.w, fc.b)."""
     xs = np.ascontiguousarray(xs, dtype=np.float32)
     ys = np.ascontiguousarray(ys, dtype=np.int64)
     n_batches, batch, _, H, W = xs.shape
     losses = np.zeros(steps, np.float32)
     ip = None if init_params is None else np.ascontiguousarray(init_params, dtype=np.float32)
+    flat = 64 * (H // 2) * (W // 2)
+    n_params = 32 * 27 + 32 + 64 * 288 + 64 + 10 * flat + 10
+    fp = np.zeros(n_params, np.float32) if want_params else None
+    if ip is not None:
+        assert ip.size == n_params
     ms = C.c_double(0.0)
     _check(lib.tfa_cnn_train(batch, H, W, steps, warmup, n_batches, _ptr(xs), _ptr(ys), lr, mu, int(on_gpu), _ptr(ip),
-                             _ptr(losses), C.byref(ms)))
-    return losses, ms.value
+                             _ptr(losses), _ptr(fp), C.byref(ms)))
+    return (losses, fp, ms.value) if want_params else (losses, ms.value)

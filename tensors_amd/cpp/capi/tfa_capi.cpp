@@ -616,7 +616,7 @@ int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t ste
 
 int tfa_cnn_train(int64_t batch, int64_t H, int64_t W, int64_t steps, int64_t warmup, int64_t n_batches, const float* xs,
                   const int64_t* ys, float lr, float mu, int32_t on_gpu, const float* init_params, float* losses,
-                  double* ms_per_step) {
+                  float* final_params, double* ms_per_step) {
     return guarded([&] {
         if (batch <= 0 || steps < 0 || n_batches <= 0 || warmup < 0 || warmup > steps || H % 2 || W % 2)
             throw std::invalid_argument("tfa_cnn_train: bad sizes");
@@ -625,19 +625,21 @@ int tfa_cnn_train(int64_t batch, int64_t H, int64_t W, int64_t steps, int64_t wa
         nn::Conv2dModule conv1(3, 32, 3, 1, 1), conv2(32, 64, 3, 2, 1);
         const int64_t flat = 64 * (H / 2) * (W / 2);
         nn::Linear fc(static_cast<int>(flat), 10);
+        // The six parameters in the order of init_params / final_params.
+        const std::pair<nn::Module*, const char*> order[6] = {{&conv1, "weight"}, {&conv1, "bias"}, {&conv2, "weight"},
+                                                              {&conv2, "bias"},   {&fc, "weight"},    {&fc, "bias"}};
+        auto param = [](nn::Module* m, const char* name) -> Tensor& {
+            for (auto& np : m->named_parameters())
+                if (np.first == name) return np.second->data_;
+            throw std::logic_error(std::string("tfa_cnn_train: no parameter ") + name);
+        };
         if (init_params) {
             size_t off = 0;
-            auto load = [&](nn::Module& m, const char* name, int64_t n) {
-                for (auto& np : m.named_parameters())
-                    if (np.first == name) std::memcpy(np.second->data_.data(), init_params + off, sizeof(float) * n);
-                off += static_cast<size_t>(n);
-            };
-            load(conv1, "weight", 32 * 3 * 9);
-            load(conv1, "bias", 32);
-            load(conv2, "weight", 64 * 32 * 9);
-            load(conv2, "bias", 64);
-            load(fc, "weight", 10 * flat);
-            load(fc, "bias", 10);
+            for (const auto& o : order) {
+                Tensor& t = param(o.first, o.second);
+                std::memcpy(t.data(), init_params + off, sizeof(float) * static_cast<size_t>(t.numel()));
+                off += static_cast<size_t>(t.numel());
+            }
         }
         conv1.to(d);
         conv2.to(d);
@@ -673,6 +675,14 @@ int tfa_cnn_train(int64_t batch, int64_t H, int64_t W, int64_t steps, int64_t wa
             *ms_per_step = steps > warmup ? std::chrono::duration<double, std::milli>(t1 - t0).count() / double(steps - warmup) : 0.0;
         if (losses)
             for (int64_t s = 0; s < steps; ++s) losses[s] = to_host(loss_t[static_cast<size_t>(s)])[0];
+        if (final_params) {
+            size_t off = 0;
+            for (const auto& o : order) {
+                auto v = to_host(param(o.first, o.second));
+                std::memcpy(final_params + off, v.data(), sizeof(float) * v.size());
+                off += v.size();
+            }
+        }
     });
 }
 

@@ -478,3 +478,106 @@ def _conv64(x, w, b, s, p):
 def test_argmax_first_max_wins():
     x = np.array([[1, 3, 3, 2], [5, 5, 5, 5], [-1, -2, -0.5, -0.5]], np.float32)
     assert list(oracle.argmax_rows(x)) == [1, 0, 2]
+
+
+# ---------------------------------------------------------------------------
+# mixed-precision (bf16) step of config 5
+# ---------------------------------------------------------------------------
+def test_bf16_round_known_answers_and_package_rule():
+    """Ties go to the even neighbour; one bf16 ulp at 1.0 is 2^-7."""
+    one = 1.0
+    x = np.array([one, one + 2 ** -8, one + 3 * 2 ** -8, one + 2 ** -8 + 2 ** -20, -(one + 2 ** -8),
+                  2 ** -130, 3.0e38, -3.4e38, np.inf, -np.inf, 0.0, -0.0], np.float32)
+    want = np.array([one, one, one + 2 ** -6, one + 2 ** -7, -one, 2 ** -130], np.float32)
+    got = oracle.bf16_round(x)
+    # -3.4e38 lies above the largest bf16 (3.3895e38) past the midpoint to 2^128
+    assert np.array_equal(got[:6], want) and got[7] == -np.inf and np.isinf(got[8])
+    assert np.signbit(got[11]) and not np.signbit(got[10])
+    # 3.0e38 lies between bf16 neighbours 2.9909e38 and 3.0042e38
+    assert abs(float(got[6]) - 3.0e38) <= 2 ** 120
+    # Same rule as the package's bit conversion (which the GPU's hardware
+    # conversion is compared with bit for bit).
+    from tensors_amd import bf16_bits_to_f32, f32_to_bf16_bits
+    r = np.concatenate([synth.normal(700, (20000,)), synth.normal(701, (2000,), std=1e-38),
+                        synth.normal(702, (2000,), std=1e30)])
+    assert_bitexact(oracle.bf16_round(r), bf16_bits_to_f32(f32_to_bf16_bits(r)), "bf16 rule")
+
+
+def _mixed_init(dims, seed0, bias):
+    ws = [synth.normal(seed0 + i, (dims[i + 1], dims[i]), std=float(dims[i]) ** -0.5) for i in range(len(dims) - 1)]
+    bs = [synth.normal(seed0 + 50 + i, (dims[i + 1],), std=0.1) if bias else None for i in range(len(dims) - 1)]
+    return ws, bs
+
+
+def test_mixed_step_without_rounding_is_the_reference_order_step():
+    """With the bf16 roundings turned off and no bias, three steps equal the
+    reference-order fp32 step (mlp_step, pinned bit-exact to the compiled
+    reference's 100-step trajectory) up to summation order."""
+    dims = [40, 32, 24, 10]
+    ws, _ = _mixed_init(dims, 710, False)
+    ws_ref = [w.copy() for w in ws]
+    vs = [np.zeros_like(w) for w in ws]
+    vs_ref = [np.zeros_like(w) for w in ws]
+    for s in range(3):
+        x = synth.normal(720 + s, (16, dims[0]))
+        y = synth.uniform_int(730 + s, (16,), dims[-1])
+        l_mix = oracle.mlp_step_mixed(ws, [None] * 3, vs, [None] * 3, x, y, 0.1, 0.9, rounding=False)
+        l_ref = oracle.mlp_step(ws_ref, vs_ref, x, y, 0.1, 0.9)
+        assert abs(l_mix - l_ref) <= 1e-5 * max(1.0, abs(l_ref)), (s, l_mix, l_ref)
+    for i in range(3):
+        assert_close(ws[i], ws_ref[i], 1e-5, f"W{i} after 3 steps")
+        assert_close(vs[i], vs_ref[i], 1e-4, f"v{i} after 3 steps")
+
+
+def _mlp_loss64(ws, bs, x, y):
+    h = x.astype(np.float64)
+    for i, (w, b) in enumerate(zip(ws, bs)):
+        h = h @ w.astype(np.float64).T + b.astype(np.float64)
+        if i + 1 < len(ws):
+            h = np.maximum(h, 0.0)
+    m = h.max(1, keepdims=True)
+    lse = m[:, 0] + np.log(np.exp(h - m).sum(1))
+    return float(np.mean(lse - h[np.arange(len(y)), y]))
+
+
+def test_mixed_step_gradients_are_derivatives_of_the_loss():
+    """Without rounding, mu = 0 and lr = 1, the update p_old - p_new is the
+    gradient: it must equal central differences of a float64 forward, for
+    the weights and the biases of every layer (a dropped bias gradient, a
+    mask taken from the wrong tensor or a transposed operand fails this)."""
+    dims = [12, 9, 7, 5]
+    ws, bs = _mixed_init(dims, 740, True)
+    x = synth.normal(760, (6, dims[0]))
+    y = synth.uniform_int(761, (6,), dims[-1])
+    w0 = [w.astype(np.float64) for w in ws]
+    b0 = [b.astype(np.float64) for b in bs]
+    loss = oracle.mlp_step_mixed(ws, bs, [np.zeros_like(w) for w in ws], [np.zeros_like(b) for b in bs], x, y,
+                                 1.0, 0.0, rounding=False)
+    assert abs(loss - _mlp_loss64(w0, b0, x, y)) < 1e-5
+    h = 1e-5
+    for li in range(3):
+        for arr0, new, is_w in ((w0[li], ws[li], True), (b0[li], bs[li], False)):
+            g = arr0 - new.astype(np.float64)
+            cd = np.zeros_like(arr0)
+            for idx in np.ndindex(arr0.shape):
+                p, m = [a.copy() for a in w0], [a.copy() for a in w0]
+                pb, mb = [a.copy() for a in b0], [a.copy() for a in b0]
+                (p if is_w else pb)[li][idx] += h
+                (m if is_w else mb)[li][idx] -= h
+                cd[idx] = (_mlp_loss64(p, pb, x, y) - _mlp_loss64(m, mb, x, y)) / (2 * h)
+            assert_close(g, cd, 1e-3, f"layer {li} {'W' if is_w else 'b'} gradient", atol=1e-5)
+
+
+def test_mixed_step_rounding_changes_results_by_bf16_amounts():
+    """With rounding on, the loss moves by about a bf16 ulp from the float32
+    step, not by zero (the roundings are applied) and not by more than the
+    bf16 bar (they are applied to the right tensors)."""
+    dims = [64, 48, 32, 10]
+    ws, bs = _mixed_init(dims, 780, True)
+    x = synth.normal(790, (32, dims[0]))
+    y = synth.uniform_int(791, (32,), dims[-1])
+    args = lambda: ([w.copy() for w in ws], [b.copy() for b in bs], [np.zeros_like(w) for w in ws],
+                    [np.zeros_like(b) for b in bs])
+    l16 = oracle.mlp_step_mixed(*args()[:2], *args()[2:], x, y, 0.1, 0.9, rounding=True)
+    l32 = oracle.mlp_step_mixed(*args()[:2], *args()[2:], x, y, 0.1, 0.9, rounding=False)
+    assert 0 < abs(l16 - l32) < 2e-2 * abs(l32)
