@@ -145,6 +145,21 @@ tf_status tf_gemm(tf_ctx* ctx, int trans_a, int trans_b,
                   float beta, void* C, int64_t ldc,
                   int in_dtype, int out_dtype, int epilogue, const float* bias);
 
+/* tf_gemm without any allocation: no counterpart in the reference; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * kernels and results as tf_gemm; the split-K partials, which tf_gemm keeps
+ * in the context's pool-grown workspace, go to a fixed 64 MiB device array
+ * instead (one per GPU, held until the process ends).  A shape whose
+ * partials need more is rejected with TF_ERR_INVALID.  Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams, two
+ * threads) race and must be ordered by the caller. */
+tf_status tf_gemm_noalloc(tf_ctx* ctx, int trans_a, int trans_b,
+                          int64_t M, int64_t N, int64_t K, float alpha,
+                          const void* A, int64_t lda, const void* B, int64_t ldb,
+                          float beta, void* C, int64_t ldc,
+                          int in_dtype, int out_dtype, int epilogue, const float* bias);
+
 /* Strided-batched GEMM: for b < batch, the same op on A + b*stride_a,
  * B + b*stride_b, C + b*stride_c (strides in elements).  Used by Conv2d
  * forward/backward in place of the reference's per-sample launches

@@ -2237,10 +2237,43 @@ int choose_splits(int64_t tiles, int64_t kblocks, int64_t target, int64_t min_pe
     return (int)std::max<int64_t>(1, std::min<int64_t>({want, kblocks / min_per, 256}));
 }
 
+// Split-K partials of tf_gemm_noalloc: a fixed device array instead of the
+// context's pool-grown workspace.  64 MiB covers every split this library
+// chooses for the benchmark configurations (the largest, config 5's
+// 4096 x 1000 products over 4 K slices, needs 65.5 MB); a split that needs
+// more is rejected.  Each GPU the library runs on holds its own copy until
+// the process ends.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// Device address of `scratch` on `device`, looked up once per device with
+// that device current.  The array's name is only a host-side stand-in.
+tf_status scratch_address(int device, float** out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    TF_REQUIRE(device >= 0 && device < kMaxDevices, "tf_gemm_noalloc: device index out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (addr[device] == nullptr) {
+        int cur = -1;
+        TF_HIP_CHECK(hipGetDevice(&cur));
+        if (cur != device) TF_HIP_CHECK(hipSetDevice(device));
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != device) (void)hipSetDevice(cur);
+        if (e != hipSuccess) return tfh::hip_error(e, "tf_gemm_noalloc: hipGetSymbolAddress(scratch)");
+        TF_REQUIRE(p != nullptr, "tf_gemm_noalloc: null scratch address");
+        addr[device] = p;
+    }
+    *out = static_cast<float*>(addr[device]);
+    return TF_OK;
+}
+
+// `noalloc`: split-K partials go to the fixed scratch array (no pool call).
 tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                     const void* A, int64_t lda, int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b,
                     float beta, void* C, int64_t ldc, int64_t stride_c, int64_t batch, int reduce_batch,
-                    int in_dtype, int out_dtype, int epi, const float* bias) {
+                    int in_dtype, int out_dtype, int epi, const float* bias, bool noalloc = false) {
     TF_CTX_CHECK(ctx);
     TF_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "tf_gemm: negative extent");
     TF_REQUIRE(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31), "tf_gemm: extent exceeds 2^31");
@@ -2373,9 +2406,19 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
 
     if (splits > 1) {
         size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(float);
-        tf_status st = tfh::ensure_workspace(ctx, need);
-        if (st != TF_OK) return st;
-        p.partial = reinterpret_cast<float*>(ctx->ws);
+        if (noalloc) {
+            if (need > kNoAllocScratchBytes)
+                return tfh::set_error(TF_ERR_INVALID,
+                                      "tf_gemm_noalloc: this shape's split-K partials need " + std::to_string(need) +
+                                          " bytes, more than the fixed scratch of " +
+                                          std::to_string(kNoAllocScratchBytes) + " bytes (use tf_gemm)");
+            tf_status st = scratch_address(ctx->device, &p.partial);
+            if (st != TF_OK) return st;
+        } else {
+            tf_status st = tfh::ensure_workspace(ctx, need);
+            if (st != TF_OK) return st;
+            p.partial = reinterpret_cast<float*>(ctx->ws);
+        }
     }
 
     tf_status st = TF_OK;
@@ -2442,6 +2485,13 @@ tf_status tf_gemm(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, i
                   int in_dtype, int out_dtype, int epilogue, const float* bias) {
     return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1, 0,
                      in_dtype, out_dtype, epilogue, bias);
+}
+
+tf_status tf_gemm_noalloc(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                          const void* A, int64_t lda, const void* B, int64_t ldb, float beta, void* C, int64_t ldc,
+                          int in_dtype, int out_dtype, int epilogue, const float* bias) {
+    return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1, 0,
+                     in_dtype, out_dtype, epilogue, bias, /*noalloc=*/true);
 }
 
 tf_status tf_gemm_strided_batched(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
