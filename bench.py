@@ -1,25 +1,26 @@
 #!/usr/bin/env python3
 """Benchmark of the training hot path on one MI355X.
 
-Default workload (the headline benchmark configuration, "Isolated Linear backward, fp32"):
-X, W, dY [2048 x 2048] ~ N(0,1), b [2048] ~ N(0,1); one step is
-    Y  = X W^T + b          (fwd GEMM, bias epilogue)
-    dX = dY W               (bwd GEMM, NN)
-    dW = dY^T X             (bwd GEMM, TN)
-    db = sum_rows(dY)       (bias-grad column reduction)
-    W, b <- SGD momentum    (fused update, lr 1e-3, mu 0.9)
-all on device-resident inputs.  Prints ONE JSON line.
+Headline workload, config 5 (the largest configuration, which fits one GPU):
+the wide MLP 4096-8192-8192-4096-1000 at batch 4096, bf16 weights and
+activations with fp32 accumulation and fp32 master weights, ReLU,
+CrossEntropy over 1000 labels, SGD with momentum.  One step is the whole
+fwd + bwd + SGD step through the C++20 tensorforge API (nn::Linear,
+nn::CrossEntropyLoss, Tensor::backward, optim::SGD) on device-resident
+inputs, host launch work included.  Prints ONE JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 
-`value` is the wall time of the K timed steps (nothing but the step's
-kernels on the stream, synchronised before and after) divided by K.
-Per-kernel durations come from a second, untimed pass of K steps with HIP
-events recorded on the context's stream between consecutive launches.  The
-roofline entry is for the
-backward GEMMs (dominant kernel): 2*M*N*K = 17,179,869,184 FLOP per launch
-against the 157.3 TFLOP/s fp32 MFMA peak.  ``traffic`` is read from the
-committed rocprofv3 counter summary when present.
+`value` is the wall time of the K timed steps (the device drained before and
+after) divided by K.  The roofline entry is for the backward GEMMs (the
+dominant kernels): a second pass of the same step with the library's launch
+timing on (tf_hip_timing_*: a HIP event before and after every GEMM on the
+stream it runs on) gives each GEMM's duration; `achieved` is the backward
+GEMMs' 2*M*N*K FLOP per step over their summed duration, against the
+2.5 PFLOP/s dense bf16 MFMA peak.  ``traffic`` is read from the committed
+rocprofv3 counter summary when present.  The other configurations (C2's
+isolated fp32 Linear step with its own fp32 roofline, the C3 bandwidth
+kernels, the C1 and C4 training steps) are reported under `other_configs`.
 """
 from __future__ import annotations
 
@@ -36,7 +37,10 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_FP32_TFLOPS = 157.3
+PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBPS = 8000.0
+C5_DIMS = [4096, 8192, 8192, 4096, 1000]
+C5_BATCH = 4096
 N2 = 2048
 GEMM_FLOP = 2 * N2 * N2 * N2          # 17,179,869,184
 
@@ -184,7 +188,8 @@ def bench_c3():
 
 
 def bench_api_steps():
-    """Whole training steps through the C++ API (host launch work included)."""
+    """Configs 1 and 4: whole training steps through the C++ API (host launch
+    work included)."""
     from tensors_amd import api, synth
     out = {}
     xs = synth.mnist_like(synth.seed(1, 0), (100, 64, 784))
@@ -196,14 +201,139 @@ def bench_api_steps():
     ys = synth.uniform_int(synth.seed(4, 1), (1, 128), 10)
     _, ms = api.cnn_train(xs, ys, steps=23, warmup=3, lr=0.01, mu=0.9, on_gpu=True)
     out["c4_cnn_step_ms"] = round(ms, 4)
-    dims = [4096, 8192, 8192, 4096, 1000]
-    xs = synth.normal(synth.seed(5, 0), (1, 4096, 4096))
-    ys = synth.uniform_int(synth.seed(5, 1), (1, 4096), 1000)
-    _, _, ms = api.mlp_train(dims, xs, ys, steps=13, warmup=3, lr=0.01, mu=0.9, on_gpu=True, bf16=True)
-    flop = 2 * 4096 * sum(dims[i] * dims[i + 1] for i in range(4)) * 3 - 2 * 4096 * dims[0] * dims[1]
-    out["c5_bf16_mlp_step_ms"] = round(ms, 4)
-    out["c5_bf16_step_tflops"] = round(flop / (ms * 1e-3) / 1e12, 1)
     return out
+
+
+def _c5_inputs():
+    from tensors_amd import synth
+    xs = synth.normal(synth.seed(5, 0), (1, C5_BATCH, C5_DIMS[0]))
+    ys = synth.uniform_int(synth.seed(5, 1), (1, C5_BATCH), C5_DIMS[-1])
+    return xs, ys
+
+
+def _gemm_kind(ta, tb):
+    return {(0, 1): "fwd", (0, 0): "dX", (1, 0): "dW"}.get((ta, tb), f"ta{ta}tb{tb}")
+
+
+def bench_c5(steps: int, warmup: int, timing_steps: int = 12, timing_warmup: int = 5):
+    """Config-5 step through the C++ API: timed steps, then a second pass with
+    the launch timing on for the per-GEMM durations.  The second pass builds
+    its model anew (a second or two of host work, while the GPU idles and its
+    clocks drop), so its first `timing_warmup` steps (16 ms) are not used."""
+    from tensors_amd import api
+    from tensors_amd._lib import call
+    import ctypes as C
+
+    xs, ys = _c5_inputs()
+    kw = dict(lr=0.01, mu=0.9, on_gpu=True, bf16=True)
+    losses, _, ms = api.mlp_train(C5_DIMS, xs, ys, steps=warmup + steps, warmup=warmup, **kw)
+    per_step = 3 * (len(C5_DIMS) - 1) - 1     # 4 forward, 4 dW, 3 dX (the input needs no gradient)
+    call("tf_hip_timing_start", per_step * timing_steps + 64)
+    try:
+        api.mlp_train(C5_DIMS, xs, ys, steps=timing_steps, warmup=0, **kw)
+    finally:
+        n = C.c_int(0)
+        call("tf_hip_timing_stop", C.byref(n))
+    shape = (C.c_int64 * 4)()
+    meta = (C.c_int * 4)()
+    t = C.c_float()
+    recs = []
+    for i in range(n.value):
+        call("tf_hip_timing_record", i, shape, meta, C.byref(t))
+        recs.append((tuple(shape), tuple(meta), t.value))
+    if len(recs) != per_step * timing_steps:
+        raise RuntimeError(f"C5 timing pass: {len(recs)} GEMM records, expected {per_step * timing_steps}")
+    recs = recs[per_step * timing_warmup:]
+    nsteps = timing_steps - timing_warmup
+    gemms = {}
+    for (M, N, K, _), (ta, tb, _, _), ms_k in recs:
+        key = (_gemm_kind(ta, tb), M, N, K)
+        g = gemms.setdefault(key, {"ms": [], "flop": 2 * M * N * K})
+        g["ms"].append(ms_k)
+    per_gemm = []
+    bwd_flop = bwd_ms = fwd_flop = fwd_ms = 0.0
+    for (kind, M, N, K), g in gemms.items():
+        mean = float(np.mean(g["ms"]))
+        calls = len(g["ms"]) / nsteps
+        per_gemm.append({"kind": kind, "M": M, "N": N, "K": K, "per_step": calls, "us": round(mean * 1e3, 1),
+                         "tflops": round(g["flop"] / (mean * 1e-3) / 1e12, 1)})
+        if kind == "fwd":
+            fwd_flop += g["flop"] * calls
+            fwd_ms += mean * calls
+        else:
+            bwd_flop += g["flop"] * calls
+            bwd_ms += mean * calls
+    return {"ms_step": ms, "losses_finite": bool(np.all(np.isfinite(losses))), "per_gemm": per_gemm,
+            "bwd_flop_step": bwd_flop, "bwd_ms_step": bwd_ms, "fwd_flop_step": fwd_flop, "fwd_ms_step": fwd_ms,
+            "bwd_launches_step": int(round(sum(p["per_step"] for p in per_gemm if p["kind"] != "fwd")))}
+
+
+def _host_info():
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, os.cpu_count()
+
+
+def cpu_baseline_c5():
+    """Reference CPU path on a bounded sample of config 5, extrapolated.
+
+    The reference has no bf16 path and no threads; its fp32 nn::Linear
+    forward + engine backward (naive GEMMs plus transpose copies of W) is
+    timed for the middle layer shape 4096 -> 8192 at batch rows B = 2 and 6
+    (the module constructor timed apart and removed).  Time is linear in B
+    plus a fixed part (the copies of W); both scale with in*out, so the
+    step estimate is (fixed + slope * 4096) * sum(in*out) / (4096*8192).
+    Uses oracle/_ref (the reference compiled from its sources) when present,
+    else the C restatement.
+    """
+    import oracle
+    inn, out = 4096, 8192
+    rng = np.random.default_rng(0x7E45)
+    W = rng.standard_normal((out, inn), dtype=np.float32) * np.float32(inn ** -0.5)
+    kind = "reference" if oracle.ref_available() else "port"
+    times = {}
+    init_s = 0.0
+    if kind == "reference":
+        w0 = np.empty((out, inn), np.float32)
+        t0 = time.perf_counter()
+        oracle.ref_call("ref_linear_init", inn, out, w0)
+        init_s = time.perf_counter() - t0
+    for B in (2, 6):
+        X = rng.standard_normal((B, inn), dtype=np.float32)
+        dY = rng.standard_normal((B, out), dtype=np.float32)
+        t0 = time.perf_counter()
+        if kind == "reference":
+            y = np.empty((B, out), np.float32)
+            dx = np.empty((B, inn), np.float32)
+            dw = np.empty((out, inn), np.float32)
+            oracle.ref_call("ref_linear", X, W, dY, y, dx, dw, B, inn, out)
+        else:
+            oracle.linear_fwd(X, W)
+            oracle.linear_bwd(X, W, dY)
+        times[B] = time.perf_counter() - t0 - init_s
+    slope = (times[6] - times[2]) / 4.0
+    fixed = max(times[2] - 2 * slope, 0.0)
+    layer_ms = (fixed + slope * C5_BATCH) * 1e3
+    scale = sum(C5_DIMS[i] * C5_DIMS[i + 1] for i in range(len(C5_DIMS) - 1)) / (inn * out)
+    model, ncpu = _host_info()
+    return {
+        "value": round(layer_ms * scale, 1),
+        "unit": "ms/step",
+        "cores": 1,
+        "kind": kind,
+        "extrapolated": True,
+        "host": f"{model}, {ncpu} logical CPUs visible; the reference is single-threaded",
+        "sample": (f"fp32 Linear 4096->8192 fwd+bwd (reference order) at batch 2 and 6 rows "
+                   f"({times[2]:.2f} s, {times[6]:.2f} s after {init_s:.2f} s of module init), extrapolated "
+                   f"linearly to 4096 rows and by weight count to the 4 layers (x{scale:.3f}); "
+                   f"fp32 stands in for bf16, which the reference lacks"),
+    }
 
 
 def cpu_baseline_c2():
@@ -248,22 +378,32 @@ def cpu_baseline_c2():
     }
 
 
-TRAFFIC_JSON = ROOT / "profiles" / "gemm_f32_c2_traffic.json"
+TRAFFIC_JSON = {"c2": ROOT / "profiles" / "gemm_f32_c2_traffic.json",
+                "c5": ROOT / "profiles" / "gemm_bf16_c5_traffic.json"}
 PROBE_CAL_N = 1 << 26      # calibration tf_add: reads 2 x 256 MB, writes 256 MB
 
 
-def load_traffic(name: str):
+def load_traffic(config: str, name: str):
     """Calibrated HBM bytes per launch from the committed counter summary
     (tensors_amd.profiling traffic), or None when it is absent."""
-    if not TRAFFIC_JSON.exists():
+    path = TRAFFIC_JSON[config]
+    if not path.exists():
         return None
     try:
-        return json.loads(TRAFFIC_JSON.read_text()).get(name)
+        return json.loads(path.read_text()).get(name)
     except Exception:
         return None
 
 
-def probe(steps: int = 5) -> None:
+def _probe_calibration(ctx):
+    from tensors_amd import ops
+    ca, cb, cc = ctx.zeros((PROBE_CAL_N,)), ctx.zeros((PROBE_CAL_N,)), ctx.empty((PROBE_CAL_N,))
+    for _ in range(3):
+        ops.add(ca, cb, cc)
+    ctx.sync()
+
+
+def probe_c2(steps: int = 5) -> None:
     """Launches for rocprofv3 counter runs: `steps` C2 steps (fwd GEMM, dX,
     dW, colsum, SGD) and 3 calibration tf_add launches over PROBE_CAL_N
     floats whose traffic is known.  No timing, no output but one line."""
@@ -284,28 +424,88 @@ def probe(steps: int = 5) -> None:
         ops.colsum(dY, db)
         ops.sgd_momentum_multi([W, b], [dW, db], [vW, vb], 1e-3, 0.9)
     ctx.sync()
-    ca, cb, cc = ctx.zeros((PROBE_CAL_N,)), ctx.zeros((PROBE_CAL_N,)), ctx.empty((PROBE_CAL_N,))
-    for _ in range(3):
-        ops.add(ca, cb, cc)
-    ctx.sync()
+    _probe_calibration(ctx)
     ctx.close()
     print(f"probe: {steps} C2 steps, 3 calibration launches", flush=True)
+
+
+def probe_c5(steps: int = 3) -> None:
+    """Launches for rocprofv3 counter runs: the config-5 step's GEMMs at their
+    shapes, layouts and output types (forward with bias + ReLU in bf16, dX in
+    bf16, dW in fp32), `steps` times over, then the calibration launches."""
+    import tensors_amd as ta
+    from tensors_amd import ops
+
+    ctx = ta.Context(0)
+    rng = np.random.default_rng(0x7E45)
+    B, d = C5_BATCH, C5_DIMS
+    bf = lambda shape, sd=1.0: ctx.array(ta.f32_to_bf16_bits(rng.standard_normal(shape, dtype=np.float32)
+                                                             * np.float32(sd)), ta.BF16)
+    acts = [bf((B, d[i])) for i in range(4)]
+    ws = [bf((d[i + 1], d[i]), d[i] ** -0.5) for i in range(4)]
+    grads = [bf((B, d[i + 1]), 1e-3) for i in range(4)]
+    biases = [ctx.zeros((d[i + 1],)) for i in range(4)]
+    outs = [ctx.empty((B, d[i + 1]), ta.BF16) for i in range(4)]
+    dxs = [ctx.empty((B, d[i]), ta.BF16) for i in range(4)]
+    dws = [ctx.empty((d[i + 1], d[i])) for i in range(4)]
+    for _ in range(steps):
+        for i in range(4):
+            ops.gemm(acts[i], ws[i], outs[i], trans_b=True, bias=biases[i], relu=i < 3)
+        for i in range(3, -1, -1):
+            ops.gemm(grads[i], acts[i], dws[i], trans_a=True)
+            if i > 0:
+                ops.gemm(grads[i], ws[i], dxs[i])
+    ctx.sync()
+    _probe_calibration(ctx)
+    ctx.close()
+    print(f"probe: {steps} x the C5 step's GEMMs, 3 calibration launches", flush=True)
+
+
+def c2_report(steps: int, warmup: int) -> dict:
+    ms_step, mean, per = bench_c2(steps, warmup)
+    bwd_ms = 0.5 * (mean["bwd_gemm_dx"] + mean["bwd_gemm_dw"])
+    bwd_tflops = GEMM_FLOP / (bwd_ms * 1e-3) / 1e12
+    fwd_tflops = GEMM_FLOP / (mean["fwd_gemm"] * 1e-3) / 1e12
+    colsum_gbps = (N2 * N2 * 4 + N2 * 4) / (mean["colsum"] * 1e-3) / 1e9
+    sgd_gbps = (N2 * N2 + N2) * 20 / (mean["sgd"] * 1e-3) / 1e9
+    return {
+        "workload": "C2 isolated Linear 2048x2048 fp32: fwd GEMM+bias, bwd dX/dW GEMMs, bias colsum, "
+                    "fused SGD-momentum on W and b (ops level, device-resident)",
+        "ms_per_step": round(ms_step, 4),
+        "steps": steps,
+        "warmup": warmup,
+        "dtype": "f32",
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "gemm_f32 (bwd dX NN + dW TN, mean of both)",
+            "achieved": round(bwd_tflops, 2),
+            "peak": PEAK_FP32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(bwd_tflops / PEAK_FP32_TFLOPS, 4),
+            "traffic": load_traffic("c2", "gemm_f32_bwd_c2"),
+            "algorithmic_flop_per_launch": GEMM_FLOP,
+        },
+        "kernels_ms": {k: round(v, 5) for k, v in mean.items()},
+        "fwd_gemm_tflops": round(fwd_tflops, 2),
+        "colsum_gbps": round(colsum_gbps, 1),
+        "sgd_gbps": round(sgd_gbps, 1),
+        "step_ms_device_median": round(_median(per["step_dev"]), 4),
+    }
 
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    # 50 warmup steps (~20 ms): the GPU's clocks need more than ~10 ms of load
-    # to settle after the host-side input generation; with 5 warmup steps the
-    # timed C2 steps ran ~5 % slower than in steady state.
-    ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only-c2", action="store_true", help="skip the other configurations' measurements")
-    ap.add_argument("--probe", action="store_true", help="launch the C2 kernels for a profiler, then exit")
+    ap.add_argument("--steps", type=int, default=20)
+    # The GPU's clocks need more than ~10 ms of load to settle after the
+    # host-side input generation: 5 warmup steps of config 5 are ~16 ms.
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--only-headline", action="store_true", help="skip the other configurations' measurements")
+    ap.add_argument("--probe", choices=["c2", "c5"], help="launch a config's kernels for a profiler, then exit")
     args = ap.parse_args(argv)
     if args.probe:
-        probe()
+        (probe_c2 if args.probe == "c2" else probe_c5)()
         return 0
 
     if args.gpus != 1:
@@ -314,14 +514,10 @@ def main(argv=None):
         return 2
     rank = int(os.environ.get("RANK", "0"))
 
-    ms_step, mean, per = bench_c2(args.steps, args.warmup)
-    bwd_ms = 0.5 * (mean["bwd_gemm_dx"] + mean["bwd_gemm_dw"])
-    bwd_tflops = GEMM_FLOP / (bwd_ms * 1e-3) / 1e12
-    fwd_tflops = GEMM_FLOP / (mean["fwd_gemm"] * 1e-3) / 1e12
-    colsum_gbps = (N2 * N2 * 4 + N2 * 4) / (mean["colsum"] * 1e-3) / 1e9
-    sgd_bytes = (N2 * N2 + N2) * 20
-    sgd_gbps = sgd_bytes / (mean["sgd"] * 1e-3) / 1e9
-
+    c5 = bench_c5(args.steps, args.warmup)
+    ms_step = c5["ms_step"]
+    bwd_tflops = c5["bwd_flop_step"] / (c5["bwd_ms_step"] * 1e-3) / 1e12
+    step_flop = c5["fwd_flop_step"] + c5["bwd_flop_step"]
     line = {
         "metric": "fwd+bwd+SGD step ms; bwd GEMM TFLOPS & bwd kernel GB/s as % MI355X peak",
         "value": round(ms_step, 4),
@@ -333,31 +529,35 @@ def main(argv=None):
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seeded N(0,1), counter-based generator)",
-        "config": {"workload": "C2 isolated Linear 2048x2048 fp32: fwd GEMM+bias, bwd dX/dW GEMMs, "
-                               "bias colsum, fused SGD-momentum on W and b",
-                   "M": N2, "N": N2, "K": N2},
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) inputs, uniform labels; Kaiming-uniform init from the reference's seed)",
+        "config": {"workload": "C5 wide MLP 4096-8192-8192-4096-1000, batch 4096, bf16 weights/activations with "
+                               "fp32 accumulate and fp32 master weights, ReLU, CrossEntropy over 1000 labels, "
+                               "SGD momentum (lr 0.01, mu 0.9); full fwd+bwd+SGD step through the C++ API",
+                   "dims": C5_DIMS, "batch": C5_BATCH},
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_f32 (bwd dX NN + dW TN, mean of both)",
-            "achieved": round(bwd_tflops, 2),
-            "peak": PEAK_FP32_TFLOPS,
+            "kernel": f"bf16 backward GEMMs ({c5['bwd_launches_step']} launches per step: 4 dW, 3 dX), "
+                      "FLOP over summed event-timed durations",
+            "achieved": round(bwd_tflops, 1),
+            "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(bwd_tflops / PEAK_FP32_TFLOPS, 4),
-            "traffic": load_traffic("gemm_f32_bwd_c2"),
-            "algorithmic_flop_per_launch": GEMM_FLOP,
+            "frac": round(bwd_tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": load_traffic("c5", "gemm_bf16_bwd_c5"),
+            "algorithmic_flop_per_step": int(c5["bwd_flop_step"]),
         },
-        "kernels_ms": {k: round(v, 5) for k, v in mean.items()},
-        "fwd_gemm_tflops": round(fwd_tflops, 2),
-        "colsum_gbps": round(colsum_gbps, 1),
-        "sgd_gbps": round(sgd_gbps, 1),
-        "step_ms_device_median": round(_median(per["step_dev"]), 4),
+        "step_tflops": round(step_flop / (ms_step * 1e-3) / 1e12, 1),
+        "gemm_ms_per_step": {"fwd": round(c5["fwd_ms_step"], 4), "bwd": round(c5["bwd_ms_step"], 4)},
+        "fwd_gemm_tflops": round(c5["fwd_flop_step"] / (c5["fwd_ms_step"] * 1e-3) / 1e12, 1),
+        "per_gemm": c5["per_gemm"],
+        "losses_finite": c5["losses_finite"],
     }
-    if not args.only_c2:
-        line["other_configs"] = {"c3": bench_c3(), **bench_api_steps()}
+    if not args.only_headline:
+        line["other_configs"] = {"c2": c2_report(100, 50), "c3": bench_c3(), **bench_api_steps()}
     if rank == 0 and not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline_c2()
+        line["cpu_baseline"] = cpu_baseline_c5()
+        if "other_configs" in line:
+            line["other_configs"]["c2"]["cpu_baseline"] = cpu_baseline_c2()
     if rank == 0:
         print(json.dumps(line), flush=True)
     return 0

@@ -127,6 +127,20 @@ tf_status tf_hip_event_record(tf_ctx* ctx, void* event);
 tf_status tf_hip_event_elapsed(void* start, void* end, float* ms);
 tf_status tf_hip_event_destroy(void* event);
 
+/* Launch timing, for measurement (no counterpart in the reference, whose
+ * benchmarks time from outside).  tf_hip_timing_start creates `max_records`
+ * event pairs and starts recording: from then on every GEMM call
+ * (tf_gemm, tf_gemm_noalloc, tf_gemm_strided_batched, tf_gemm_ex) on any
+ * context records one event before its kernels and one after them on that
+ * context's stream, until the records are used up or tf_hip_timing_stop.
+ * The events add two stream packets per GEMM: time a step without them.
+ * tf_hip_timing_record returns record i: shape = {M, N, K, batch},
+ * meta = {trans_a, trans_b, in_dtype, out_dtype}, and the milliseconds
+ * between its events (this waits for the second one). */
+tf_status tf_hip_timing_start(int max_records);
+tf_status tf_hip_timing_stop(int* count);
+tf_status tf_hip_timing_record(int i, int64_t* shape, int* meta, float* ms);
+
 /* ---------------------------------------------------------------------------
  * GEMM on MFMA.  C[m,n] = epi(alpha * sum_k op(A)[m,k] * op(B)[k,n] + beta*C[m,n])
  *   op(A) is M x K: trans_a == 0 -> A[m*lda + k], trans_a == 1 -> A[k*lda + m]

@@ -52,6 +52,9 @@ SIGNATURES: dict[str, list] = {
     "tf_hip_event_elapsed": [_p, _p, C.POINTER(_f)],
     "tf_hip_event_destroy": [_p],
     "tf_gemm": [_p, _i, _i, _i64, _i64, _i64, _f, _p, _i64, _p, _i64, _f, _p, _i64, _i, _i, _i, _p],
+    "tf_hip_timing_start": [_i],
+    "tf_hip_timing_stop": [_p],
+    "tf_hip_timing_record": [_i, _p, _p, _p],
     "tf_gemm_noalloc": [_p, _i, _i, _i64, _i64, _i64, _f, _p, _i64, _p, _i64, _f, _p, _i64, _i, _i, _i, _p],
     "tf_gemm_strided_batched": [_p, _i, _i, _i64, _i64, _i64, _f, _p, _i64, _i64, _p, _i64, _i64,
                                 _f, _p, _i64, _i64, _i64, _i, _i],

@@ -50,6 +50,22 @@ tf_status partial_rows_sum(tf_ctx* ctx, const float* part, float* out_lo, float*
 
 inline bool bad_ctx(tf_ctx* ctx) { return ctx == nullptr || ctx->stream == nullptr; }
 
+// Launch timing (tf_hip_timing_*): a GEMM entry point constructs one of
+// these around its launches; while recording is on it records an event on
+// the context's stream at construction and another at destruction.
+class TimedLaunch {
+public:
+    TimedLaunch(tf_ctx* ctx, int64_t M, int64_t N, int64_t K, int64_t batch, int trans_a, int trans_b, int in_dtype,
+                int out_dtype);
+    ~TimedLaunch();
+    TimedLaunch(const TimedLaunch&) = delete;
+    TimedLaunch& operator=(const TimedLaunch&) = delete;
+
+private:
+    tf_ctx* ctx_;
+    int slot_ = -1;
+};
+
 // Launch-error check after every <<<>>>: catches bad launch shapes early.
 inline tf_status check_launch(const char* what) {
     hipError_t e = hipGetLastError();

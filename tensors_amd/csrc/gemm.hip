@@ -2483,6 +2483,7 @@ extern "C" {
 tf_status tf_gemm(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                   const void* A, int64_t lda, const void* B, int64_t ldb, float beta, void* C, int64_t ldc,
                   int in_dtype, int out_dtype, int epilogue, const float* bias) {
+    tfh::TimedLaunch timed(ctx, M, N, K, 1, trans_a, trans_b, in_dtype, out_dtype);
     return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1, 0,
                      in_dtype, out_dtype, epilogue, bias);
 }
@@ -2490,6 +2491,7 @@ tf_status tf_gemm(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, i
 tf_status tf_gemm_noalloc(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                           const void* A, int64_t lda, const void* B, int64_t ldb, float beta, void* C, int64_t ldc,
                           int in_dtype, int out_dtype, int epilogue, const float* bias) {
+    tfh::TimedLaunch timed(ctx, M, N, K, 1, trans_a, trans_b, in_dtype, out_dtype);
     return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1, 0,
                      in_dtype, out_dtype, epilogue, bias, /*noalloc=*/true);
 }
@@ -2498,6 +2500,7 @@ tf_status tf_gemm_strided_batched(tf_ctx* ctx, int trans_a, int trans_b, int64_t
                                   float alpha, const void* A, int64_t lda, int64_t stride_a, const void* B,
                                   int64_t ldb, int64_t stride_b, float beta, void* C, int64_t ldc,
                                   int64_t stride_c, int64_t batch, int in_dtype, int out_dtype) {
+    tfh::TimedLaunch timed(ctx, M, N, K, batch, trans_a, trans_b, in_dtype, out_dtype);
     return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
                      stride_c, batch, 0, in_dtype, out_dtype, TF_EPI_NONE, nullptr);
 }
@@ -2506,6 +2509,7 @@ tf_status tf_gemm_ex(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N
                      const void* A, int64_t lda, int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b,
                      float beta, void* C, int64_t ldc, int64_t stride_c, int64_t batch, int reduce_batch,
                      int in_dtype, int out_dtype, int epilogue, const float* bias) {
+    tfh::TimedLaunch timed(ctx, M, N, K, reduce_batch ? -batch : batch, trans_a, trans_b, in_dtype, out_dtype);
     return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
                      stride_c, batch, reduce_batch, in_dtype, out_dtype, epilogue, bias);
 }

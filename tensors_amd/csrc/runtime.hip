@@ -57,9 +57,44 @@ tf_status release_cached(tf_ctx* ctx) {
     return TF_OK;
 }
 
+// Launch-timing records (tf_hip_timing_*), process-wide.
+struct TimingRecord {
+    int64_t shape[4];
+    int meta[4];
+};
+struct TimingState {
+    std::mutex mu;
+    bool on = false;
+    std::vector<hipEvent_t> events;   // 2 per record
+    std::vector<TimingRecord> records;
+    size_t used = 0;
+};
+TimingState& timing() {
+    static TimingState t;
+    return t;
+}
+
 }  // namespace
 
 namespace tfh {
+
+TimedLaunch::TimedLaunch(tf_ctx* ctx, int64_t M, int64_t N, int64_t K, int64_t batch, int trans_a, int trans_b,
+                         int in_dtype, int out_dtype)
+    : ctx_(ctx) {
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lock(t.mu);
+    if (!t.on || ctx == nullptr || t.used >= t.records.size()) return;
+    slot_ = (int)t.used++;
+    t.records[slot_] = TimingRecord{{M, N, K, batch}, {trans_a, trans_b, in_dtype, out_dtype}};
+    (void)hipEventRecord(t.events[2 * slot_], ctx->stream);
+}
+
+TimedLaunch::~TimedLaunch() {
+    if (slot_ < 0) return;
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lock(t.mu);
+    (void)hipEventRecord(t.events[2 * slot_ + 1], ctx_->stream);
+}
 
 tf_status set_error(tf_status code, const std::string& msg) {
     g_last_error = msg;
@@ -282,6 +317,45 @@ tf_status tf_hip_zero(tf_ctx* ctx, void* p, size_t bytes) {
     TF_REQUIRE(p != nullptr, "tf_hip_zero: null pointer");
     zero_bytes_kernel<<<tfd::grid_for((int64_t)bytes, 16), 256, 0, ctx->stream>>>((uint8_t*)p, bytes);
     return tfh::check_launch("zero_bytes_kernel");
+}
+
+tf_status tf_hip_timing_start(int max_records) {
+    TF_REQUIRE(max_records > 0 && max_records <= (1 << 20), "tf_hip_timing_start: max_records out of range");
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lock(t.mu);
+    while (t.events.size() < 2 * (size_t)max_records) {
+        hipEvent_t e;
+        TF_HIP_CHECK(hipEventCreate(&e));
+        t.events.push_back(e);
+    }
+    t.records.assign((size_t)max_records, TimingRecord{});
+    t.used = 0;
+    t.on = true;
+    return TF_OK;
+}
+
+tf_status tf_hip_timing_stop(int* count) {
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lock(t.mu);
+    t.on = false;
+    if (count) *count = (int)t.used;
+    return TF_OK;
+}
+
+tf_status tf_hip_timing_record(int i, int64_t* shape, int* meta, float* ms) {
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lock(t.mu);
+    TF_REQUIRE(!t.on, "tf_hip_timing_record: stop recording first");
+    TF_REQUIRE(i >= 0 && (size_t)i < t.used, "tf_hip_timing_record: no such record");
+    if (shape)
+        for (int j = 0; j < 4; ++j) shape[j] = t.records[i].shape[j];
+    if (meta)
+        for (int j = 0; j < 4; ++j) meta[j] = t.records[i].meta[j];
+    if (ms) {
+        TF_HIP_CHECK(hipEventSynchronize(t.events[2 * i + 1]));
+        TF_HIP_CHECK(hipEventElapsedTime(ms, t.events[2 * i], t.events[2 * i + 1]));
+    }
+    return TF_OK;
 }
 
 tf_status tf_hip_event_create(tf_ctx* ctx, void** event) {

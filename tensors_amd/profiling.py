@@ -4,7 +4,8 @@
     python -m tensors_amd.profiling stats <dir>/run_kernel_stats.csv --title "..." --cmd "..."
 
     # per-launch HBM traffic from two --pmc runs (FETCH_SIZE, then WRITE_SIZE)
-    # of ``bench.py --probe``, calibrated against the probe's copy kernel
+    # of ``bench.py --probe c2`` (or ``--probe c5`` with ``--config c5``),
+    # calibrated against the probe's copy kernel
     python -m tensors_amd.profiling traffic --fetch <dir>/run_counter_collection.csv \
         --write <dir>/run_counter_collection.csv --json profiles/<name>.json --cmd "..."
 
@@ -78,6 +79,158 @@ def traffic(fetch_csv, write_csv, cal_n: int) -> dict:
     return res
 
 
+# Config 5 (bench.py --probe c5): the step's GEMMs in launch order per step,
+# (kind, M, N, K, output bytes per element): forward L1..L4, then per layer
+# from the last: dW, dX (no dX for layer 1).  A split-K reduction dispatch
+# belongs to the GEMM launched right before it.
+C5_DIMS = [4096, 8192, 8192, 4096, 1000]
+C5_B = 4096
+
+
+def c5_gemm_order() -> list[tuple[str, int, int, int, int]]:
+    d, B = C5_DIMS, C5_B
+    seq = [("fwd", B, d[i + 1], d[i], 2) for i in range(4)]
+    for i in range(3, -1, -1):
+        seq.append(("dW", d[i + 1], d[i], B, 4))
+        if i > 0:
+            seq.append(("dX", B, d[i], d[i + 1], 2))
+    return seq
+
+
+def _ordered(path: str | Path, counter: str) -> list[tuple[str, float]]:
+    """(kernel name, value of `counter` summed over instances) per dispatch, in
+    dispatch order."""
+    sums: dict[int, float] = defaultdict(float)
+    names: dict[int, str] = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            d = int(r["Dispatch_Id"])
+            sums[d] += float(r["Counter_Value"])
+            names[d] = r["Kernel_Name"]
+    return [(names[d], sums[d]) for d in sorted(sums)]
+
+
+def traffic_c5(fetch_csv, write_csv, cal_n: int) -> dict:
+    """Calibrated HBM bytes of config 5's GEMMs, by kind (fwd / dX / dW) per
+    step and per launch, from two counter runs of ``bench.py --probe c5``."""
+    fetch, write = _ordered(fetch_csv, "FETCH_SIZE"), _ordered(write_csv, "WRITE_SIZE")
+    cal_read, cal_write = 2 * 4 * cal_n, 4 * cal_n
+    cal_f = [v for n, v in fetch if CAL_NAME in n]
+    cal_w = [v for n, v in write if CAL_NAME in n]
+    if not cal_f or not cal_w:
+        raise SystemExit("no calibration dispatch")
+    f_scale = cal_read / (sum(cal_f) / len(cal_f) * 1024.0)
+    w_scale = cal_write / (sum(cal_w) / len(cal_w) * 1024.0)
+    order = c5_gemm_order()
+    totals = {k: {"fetch_bytes": 0.0, "write_bytes": 0.0, "algorithmic_bytes": 0, "launches": 0}
+              for k in ("fwd", "dX", "dW")}
+    steps = 0
+    for stream, key, scale in ((fetch, "fetch_bytes", f_scale), (write, "write_bytes", w_scale)):
+        pos, count = -1, 0
+        for name, v in stream:
+            if "gemm_" in name:
+                pos += 1
+                count += 1
+                kind, M, N, K, ob = order[pos % len(order)]
+                totals[kind][key] += v * 1024.0 * scale
+                if key == "fetch_bytes":
+                    totals[kind]["algorithmic_bytes"] += 2 * (M * K + K * N) + ob * M * N
+                    totals[kind]["launches"] += 1
+            elif "splitk_reduce" in name and pos >= 0:
+                totals[order[pos % len(order)][0]][key] += v * 1024.0 * scale
+        if count % len(order):
+            raise SystemExit(f"{count} GEMM dispatches is not a whole number of C5 steps")
+        steps = count // len(order)
+    res = {"calibration": {"kernel": f"tf_add over {cal_n} floats", "known_read_bytes": cal_read,
+                           "known_write_bytes": cal_write, "fetch_scale": round(f_scale, 4),
+                           "write_scale": round(w_scale, 4)},
+           "steps": steps}
+    for kind, t in totals.items():
+        tb = t["fetch_bytes"] + t["write_bytes"]
+        res[f"gemm_bf16_{kind}_c5"] = {
+            "launches_per_step": t["launches"] // steps,
+            "fetch_bytes_per_step": round(t["fetch_bytes"] / steps),
+            "write_bytes_per_step": round(t["write_bytes"] / steps),
+            "traffic_bytes_per_step": round(tb / steps),
+            "algorithmic_bytes_per_step": t["algorithmic_bytes"] // steps,
+            "traffic_over_algorithmic": round(tb / t["algorithmic_bytes"], 3)}
+    bwd = [res["gemm_bf16_dX_c5"], res["gemm_bf16_dW_c5"]]
+    n_bwd = sum(r["launches_per_step"] for r in bwd)
+    res["gemm_bf16_bwd_c5"] = round(sum(r["traffic_bytes_per_step"] for r in bwd) / n_bwd)  # bench roofline.traffic
+    return res
+
+
+def c5_api_order() -> list[tuple[str, int, int, int]]:
+    """The config-5 step's GEMMs in the order the C++ API launches them:
+    forward L1..L4, then the engine's backward from the last layer, each
+    LinearBackward computing dX before dW (no dX for layer 1)."""
+    d, B = C5_DIMS, C5_B
+    seq = [("fwd", B, d[i + 1], d[i]) for i in range(4)]
+    for i in range(3, -1, -1):
+        if i > 0:
+            seq.append(("dX", B, d[i], d[i + 1]))
+        seq.append(("dW", d[i + 1], d[i], B))
+    return seq
+
+
+def c5_gemm_table(trace_csv: str | Path, bench_line: dict | None = None, tail_steps: int = 0) -> str:
+    """Mean kernel time of each GEMM of the config-5 step from a kernel trace
+    of the C++ API step (GEMM dispatches in launch order, 11 per step; a
+    split-K reduction counts with the GEMM before it: from the GEMM's start
+    to the reduction's end), over all steps and over the last `tail_steps`
+    (the bench's event-timed steps), beside the bench's event timing of the
+    same GEMM when its JSON line is given."""
+    rows = []
+    with open(trace_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            n = r["Kernel_Name"]
+            if "gemm_" in n or "splitk_reduce" in n:
+                rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), "splitk_reduce" in n))
+    rows.sort()
+    order = c5_api_order()
+    spans: list[list[float]] = []      # per GEMM dispatch: [start, end]
+    for start, end, is_reduce in rows:
+        if not is_reduce:
+            spans.append([start, end])
+        elif spans:
+            spans[-1][1] = end
+    if len(spans) % len(order):
+        raise SystemExit(f"{len(spans)} GEMM dispatches is not a whole number of config-5 steps")
+    nsteps = len(spans) // len(order)
+    tail = min(tail_steps, nsteps)
+
+    def avg(i, first):
+        v = [(spans[s * len(order) + i][1] - spans[s * len(order) + i][0]) / 1e3 for s in range(first, nsteps)]
+        return sum(v) / len(v)
+
+    ev = {}
+    if bench_line:
+        for g in bench_line.get("per_gemm", []):
+            ev[(g["kind"], g["M"], g["N"], g["K"])] = g["us"]
+    lines = [f"| GEMM | M x N x K | kernel avg us, all {nsteps} steps | kernel avg us, last {tail} steps | "
+             "event avg us (bench) | TFLOP/s (all steps) |", "|---|---|---:|---:|---:|---:|"]
+    tot = {"fwd": [0.0, 0.0, 0.0, 0.0], "bwd": [0.0, 0.0, 0.0, 0.0]}
+    for i, (kind, M, N, K) in enumerate(order):
+        a_all = avg(i, 0)
+        a_tail = avg(i, nsteps - tail) if tail else float("nan")
+        flop = 2.0 * M * N * K
+        e = ev.get((kind, M, N, K))
+        lines.append(f"| {kind} | {M} x {N} x {K} | {a_all:.1f} | {a_tail:.1f} | "
+                     f"{'' if e is None else f'{e:.1f}'} | {flop / (a_all * 1e-6) / 1e12:.0f} |")
+        t = tot["fwd" if kind == "fwd" else "bwd"]
+        t[0] += a_all
+        t[1] += a_tail
+        t[2] += e if e is not None else float("nan")
+        t[3] += flop
+    for name, n in (("bwd", 7), ("fwd", 4)):
+        t = tot[name]
+        lines.append(f"| {name} sum ({n}) | | {t[0]:.1f} | {t[1]:.1f} | {t[2]:.1f} | "
+                     f"{t[3] / (t[0] * 1e-6) / 1e12:.0f} |")
+    return "\n".join(lines)
+
+
 def stats_table(path: str | Path, top: int = 25) -> str:
     rows = list(csv.DictReader(open(path, newline="")))
     rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
@@ -126,10 +279,14 @@ def main(argv=None) -> int:
     s.add_argument("--trace", help="the run's kernel_trace.csv, for a per-phase table")
     s.add_argument("--phases", help="phase sizes in dispatches per kernel, e.g. warmup=50,timed=100,events=100")
     s.add_argument("--match", nargs="*", default=[], help="kernel-name substrings for the per-phase table")
+    s.add_argument("--c5-gemms", help="the run's kernel_trace.csv: add the per-GEMM table of the config-5 step")
+    s.add_argument("--bench-log", help="file holding the bench's JSON line (event timings for that table)")
+    s.add_argument("--tail-steps", type=int, default=7, help="steps of the bench's event-timed pass")
     t = sub.add_parser("traffic")
     t.add_argument("--fetch", required=True)
     t.add_argument("--write", required=True)
     t.add_argument("--cal-n", type=int, default=1 << 26)
+    t.add_argument("--config", choices=["c2", "c5"], default="c2")
     t.add_argument("--json", required=True)
     t.add_argument("--cmd", required=True, nargs="+", help="the two rocprofv3 commands")
     a = ap.parse_args(argv)
@@ -139,12 +296,20 @@ def main(argv=None) -> int:
             phases = [(p.split("=")[0], int(p.split("=")[1])) for p in a.phases.split(",")]
             text += ("\nPer phase (each kernel's dispatches in launch order, split into the bench's phases):\n\n"
                      f"{phase_table(a.trace, phases, a.match)}\n")
+        if a.c5_gemms:
+            line = None
+            if a.bench_log:
+                for ln in Path(a.bench_log).read_text().splitlines():
+                    if ln.startswith("{") and '"metric"' in ln:
+                        line = json.loads(ln)
+            text += ("\nConfig-5 GEMMs (dispatches of the C++ API step in launch order; split-K reductions "
+                     "counted with their GEMM):\n\n" + c5_gemm_table(a.c5_gemms, line, a.tail_steps) + "\n")
         if a.out:
             Path(a.out).write_text(text)
         else:
             sys.stdout.write(text)
     else:
-        res = traffic(a.fetch, a.write, a.cal_n)
+        res = (traffic if a.config == "c2" else traffic_c5)(a.fetch, a.write, a.cal_n)
         res["commands"] = a.cmd
         Path(a.json).write_text(json.dumps(res, indent=2) + "\n")
         print(json.dumps(res, indent=2))

@@ -75,3 +75,39 @@ def test_stats_and_phase_tables(tmp_path):
             w.writerow(r)
     out = profiling.phase_table(trace, [("warmup", 2), ("timed", 2), ("events", 2)], ["k_a"])
     assert out.splitlines()[-1] == "| `k_a<1>` | 4.00 | 2.00 | 1.00 |"
+
+
+def test_traffic_c5_attributes_split_reductions_to_their_gemm(tmp_path):
+    """Two probe steps: each GEMM dispatch reads 1000 KiB and writes 100 KiB
+    (raw); the split-K reductions after the L4 forward and L4 dW add 10 KiB
+    each to those GEMMs' kinds.  The copy kernel calibrates fetch x2, write x1."""
+    n = 1 << 20
+    order = profiling.c5_gemm_order()
+    rows_f, rows_w = [], []
+    d = 0
+
+    def add(name, f, w):
+        nonlocal d
+        d += 1
+        rows_f.append({"Dispatch_Id": d, "Kernel_Name": name, "Counter_Name": "FETCH_SIZE", "Counter_Value": f})
+        rows_w.append({"Dispatch_Id": d, "Kernel_Name": name, "Counter_Name": "WRITE_SIZE", "Counter_Value": w})
+
+    for _ in range(2):
+        for i, (kind, M, N, K, ob) in enumerate(order):
+            add("gemm_bf16_dl8_kernel<...>", 1000.0, 100.0)
+            if i in (3, 4):           # L4 forward, L4 dW
+                add("splitk_reduce_kernel(GemmParams, int)", 10.0, 10.0)
+    add("binary_kernel<float, AddOp>", 2 * 4 * n / 1024 / 2, 4 * n / 1024)
+    fp, wp = tmp_path / "f.csv", tmp_path / "w.csv"
+    _write_counters(fp, rows_f)
+    _write_counters(wp, rows_w)
+    res = profiling.traffic_c5(fp, wp, n)
+    assert res["steps"] == 2
+    fwd, dx, dw = res["gemm_bf16_fwd_c5"], res["gemm_bf16_dX_c5"], res["gemm_bf16_dW_c5"]
+    assert (fwd["launches_per_step"], dx["launches_per_step"], dw["launches_per_step"]) == (4, 3, 4)
+    assert fwd["fetch_bytes_per_step"] == (4 * 1000 + 10) * 2 * 1024
+    assert dw["write_bytes_per_step"] == (4 * 100 + 10) * 1024
+    assert dx["traffic_bytes_per_step"] == 3 * (2000 + 100) * 1024
+    assert res["gemm_bf16_bwd_c5"] == round((dx["traffic_bytes_per_step"] + dw["traffic_bytes_per_step"]) / 7)
+    # algorithmic bytes of the L2 dW (8192 x 8192 x 4096, bf16 in, fp32 out) are part of dW's total
+    assert dw["algorithmic_bytes_per_step"] >= 2 * (8192 * 4096 * 2) + 4 * 8192 * 8192
