@@ -210,6 +210,9 @@ tf_status tf_mul(tf_ctx* ctx, const void* a, const void* b, void* out, int64_t n
 /* out = a * s[0] where s is a device scalar. */
 tf_status tf_scale_by(tf_ctx* ctx, const void* a, const float* s, void* out, int64_t n, int dtype);
 tf_status tf_relu_fwd(tf_ctx* ctx, const void* x, void* y, int64_t n, int dtype);
+/* y = x > 0 ? x : alpha * x  (the registry's LeakyReluFn slot,
+ * cuda/CudaKernelRegistry.hpp:17,24, filled by cuda/kernels/elementwise.cu:299-301,325) */
+tf_status tf_leaky_relu_fwd(tf_ctx* ctx, const void* x, void* y, int64_t n, float alpha, int dtype);
 tf_status tf_sigmoid_fwd(tf_ctx* ctx, const void* x, void* y, int64_t n, int dtype);
 tf_status tf_tanh_fwd(tf_ctx* ctx, const void* x, void* y, int64_t n, int dtype);
 
@@ -224,10 +227,17 @@ tf_status tf_tanh_bwd(tf_ctx* ctx, const void* dy, const void* y, void* dx, int6
  * Row kernels (one wave64 per row).
  * ------------------------------------------------------------------------- */
 /* Cross-entropy forward: lse[r] = logsumexp(logits[r,:]) (may be NULL) and
- * loss[0] = mean_r (lse[r] - logits[r, t_r]).  targets are int64 in [0, cols).
- * Equals the loss of the train_mlp chain (examples/train_mlp.cpp:54-76). */
+ * loss[0] = mean_r nll[r], nll[r] = lse[r] - logits[r, t_r].  flags:
+ *   0 (TF_CE_CHAIN): the train_mlp chain (examples/train_mlp.cpp:54-76): a
+ *     target outside [0, cols) contributes nll 0 (its one-hot row is empty);
+ *   TF_CE_STRICT: such a target makes its nll, and so the loss, NaN (the
+ *     module throws for it, nn/CrossEntropyLoss.cpp:47-53; no host check);
+ *   TF_CE_CLAMP: nll[r] <= -logf(1e-9f), the module's clamp of the
+ *     probability at 1e-9 (nn/CrossEntropyLoss.cpp:54-55);
+ *   TF_CE_MODULE = both: nn::CrossEntropyLoss::forward's loss. */
+enum { TF_CE_CHAIN = 0, TF_CE_STRICT = 1, TF_CE_CLAMP = 2, TF_CE_MODULE = 3 };
 tf_status tf_ce_fwd(tf_ctx* ctx, const float* logits, const int64_t* targets,
-                    float* loss, float* lse, int64_t rows, int64_t cols);
+                    float* loss, float* lse, int64_t rows, int64_t cols, int flags);
 /* Fused LogSoftmax+NLL backward: dlogits = g * (softmax(logits) - onehot) / rows
  * where g = grad_loss[0] (NULL means 1).  With lse from tf_ce_fwd the kernel
  * is a single streaming pass; with lse == NULL it recomputes row statistics.
@@ -236,9 +246,18 @@ tf_status tf_ce_fwd(tf_ctx* ctx, const float* logits, const int64_t* targets,
 tf_status tf_ce_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets,
                     const float* lse, const float* grad_loss, float* dlogits,
                     int64_t rows, int64_t cols);
-/* Forward and backward in one pass over logits (upstream gradient 1). */
+/* Forward and backward in one pass over logits (upstream gradient 1); flags
+ * as tf_ce_fwd's (they change the loss only). */
 tf_status tf_ce_fwd_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets,
-                        float* loss, float* dlogits, int64_t rows, int64_t cols);
+                        float* loss, float* dlogits, int64_t rows, int64_t cols, int flags);
+/* pred[r] = first column of row r holding its largest value, with the
+ * reference's scan (examples/train_mlp.cpp:95-100: running maximum from
+ * -1e30, strict '>', prediction 0 when no value exceeds it).  With labels
+ * (int64[rows]) and correct (int64[1]) both non-NULL, also
+ * correct[0] = #{r : pred[r] == labels[r]} (the accuracy count of
+ * eval_accuracy, examples/train_mlp.cpp:101), without a host copy. */
+tf_status tf_argmax_rows(tf_ctx* ctx, const float* x, int64_t* pred, const int64_t* labels, int64_t* correct,
+                         int64_t rows, int64_t cols);
 /* Row log_softmax / softmax forward (tensor/Tensor.cpp:370-447). */
 tf_status tf_log_softmax_fwd(tf_ctx* ctx, const float* x, float* y, int64_t rows, int64_t cols);
 tf_status tf_softmax_fwd(tf_ctx* ctx, const float* x, float* y, int64_t rows, int64_t cols);
@@ -278,8 +297,10 @@ tf_status tf_layernorm_bwd(tf_ctx* ctx, const float* dy, const float* x, const f
                            float* dbeta, int64_t rows, int64_t cols, int reference_compat);
 
 /* ---------------------------------------------------------------------------
- * Conv2d index maps, NCHW (same parameter list as launch_im2col /
- * launch_col2im, cuda/kernels/im2col.cuh:37-43, cuda/kernels/col2im.cuh:22-29).
+ * Conv2d index maps, NCHW, with the parameter lists of launch_im2col
+ * (cuda/kernels/im2col.cuh:37-43) and launch_col2im (cuda/kernels/col2im.cuh:22-29,
+ * including its outH/outW, which must equal the geometry's) after the
+ * context; the dtype is last and the stream is the context's.
  * col is [N][C*kH*kW][outH*outW].  col2im gathers (deterministic).
  * ------------------------------------------------------------------------- */
 tf_status tf_im2col(tf_ctx* ctx, const void* x, void* col, int64_t N, int64_t C, int64_t H, int64_t W,
@@ -287,7 +308,8 @@ tf_status tf_im2col(tf_ctx* ctx, const void* x, void* col, int64_t N, int64_t C,
                     int64_t pad_w, int64_t dilation_h, int64_t dilation_w, int dtype);
 tf_status tf_col2im(tf_ctx* ctx, const void* col, void* dx, int64_t N, int64_t C, int64_t H, int64_t W,
                     int64_t kH, int64_t kW, int64_t stride_h, int64_t stride_w, int64_t pad_h,
-                    int64_t pad_w, int64_t dilation_h, int64_t dilation_w, int dtype);
+                    int64_t pad_w, int64_t dilation_h, int64_t dilation_w, int64_t outH, int64_t outW,
+                    int dtype);
 
 /* ---------------------------------------------------------------------------
  * Layout kernels over contiguous data viewed as [outer][reduce][inner].

@@ -33,11 +33,14 @@ const char* tfa_last_error(void);
  *   losses[steps]      out: loss of every step (read back after the loop)
  *   final_weights      NULL or out: concatenated weights after the last step
  *   ms_per_step        NULL or out: wall time per timed step (steps after `warmup`),
- *                      host launch work included, device drained at both ends. */
+ *                      host launch work included, device drained at both ends.
+ *   pool_used          NULL or out [steps]: the device pool's bytes in use after each
+ *                      step (the device drained first; GPU only, and then the steps
+ *                      are not timed). */
 int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t steps, int64_t warmup,
                   int64_t n_batches, const float* xs, const int64_t* ys, float lr, float mu, int32_t on_gpu,
                   int32_t reference_compat, int32_t bf16, const float* init_weights, float* losses,
-                  float* final_weights, double* ms_per_step);
+                  float* final_weights, double* ms_per_step, uint64_t* pool_used);
 
 /* CNN training (the config-4 network): Conv2dModule(3,32,3,1,1) - ReLU -
  * Conv2dModule(32,64,3,2,1) - ReLU - flatten - Linear(64*(H/2)*(W/2), 10) -

@@ -48,6 +48,7 @@ def _load_oracle() -> C.CDLL:
         "orc_add": [_f32p, _f32p, _f32p, _i64],
         "orc_mul": [_f32p, _f32p, _f32p, _i64],
         "orc_relu_fwd": [_f32p, _f32p, _i64],
+        "orc_leaky_relu_fwd": [_f32p, _f32p, _i64, _f],
         "orc_sigmoid_fwd": [_f32p, _f32p, _i64],
         "orc_tanh_fwd": [_f32p, _f32p, _i64],
         "orc_relu_bwd": [_f32p, _f32p, _f32p, _i64],
@@ -69,7 +70,10 @@ def _load_oracle() -> C.CDLL:
         "orc_conv2d_fwd": [_f32p, _f32p, C.c_void_p, _f32p] + [_i64] * 10,
         "orc_conv2d_bwd": [_f32p, _f32p, C.c_int, _f32p, _f32p, _f32p, _f32p] + [_i64] * 13,
         "orc_argmax_rows": [_f32p, _i64p, _i64, _i64],
+        "orc_sum_dim": [_f32p, _f32p, _i64, _i64, _i64],
     }
+    lib.orc_ce_module.argtypes = [_f32p, _i64p, _i64, _i64, _f32p, _f32p]
+    lib.orc_ce_module.restype = C.c_int
     for name, args in sig.items():
         fn = getattr(lib, name)
         fn.argtypes = args
@@ -125,6 +129,13 @@ def _unary(fn, x):
 
 def relu(x):
     return _unary(lib.orc_relu_fwd, x)
+
+
+def leaky_relu(x, alpha):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib.orc_leaky_relu_fwd(x.reshape(-1), y.reshape(-1), x.size, alpha)
+    return y
 
 
 def sigmoid(x):
@@ -195,6 +206,18 @@ def ce_chain(logits, labels):
     d = np.empty_like(logits)
     lib.orc_ce_chain(logits, labels, logits.shape[0], logits.shape[1], loss, d, None)
     return float(loss[0]), d
+
+
+def ce_module(logits, labels):
+    """Loss of nn::CrossEntropyLoss::forward (probability clamped at 1e-9);
+    raises IndexError for a target outside [0, C), as the reference throws."""
+    logits = _f32(logits)
+    labels = np.ascontiguousarray(labels, dtype=np.int64)
+    loss = np.zeros(1, np.float32)
+    probs = np.empty_like(logits)
+    if lib.orc_ce_module(logits, labels, logits.shape[0], logits.shape[1], loss, probs) != 0:
+        raise IndexError("CrossEntropyLoss: target index out of range")
+    return float(loss[0])
 
 
 def colsum(dy):
@@ -293,6 +316,15 @@ def conv2d_bwd(x, w, gout, stride=(1, 1), pad=(0, 0), dil=(1, 1), has_bias=True)
     lib.orc_conv2d_bwd(x, w, int(has_bias), gout, gin, gw, gb, N, Cin, H, W, Cout, kH, kW,
                        stride[0], stride[1], pad[0], pad[1], dil[0], dil[1])
     return gin, gw, gb
+
+
+def sum_dim(x, outer, reduce, inner):
+    """Tensor::sum along the middle dim of x viewed as [outer][reduce][inner]."""
+    x = _f32(x).reshape(-1)
+    assert x.size == outer * reduce * inner
+    out = np.empty(outer * inner, np.float32)
+    lib.orc_sum_dim(x, out, outer, reduce, inner)
+    return out.reshape(outer, inner)
 
 
 def argmax_rows(x):
@@ -471,7 +503,7 @@ def ref():
         r = C.CDLL(str(REF_SO), mode=os.RTLD_NOW | os.RTLD_LOCAL)
         r.ref_last_error.restype = C.c_char_p
         for name in ("ref_matmul", "ref_transpose2d", "ref_matmul_backward", "ref_linear", "ref_linear_init",
-                     "ref_conv2d_init", "ref_relu_fwd", "ref_sigmoid_fwd", "ref_tanh_fwd", "ref_relu_bwd",
+                     "ref_conv2d_init", "ref_relu_fwd", "ref_leaky_relu_fwd", "ref_sigmoid_fwd", "ref_tanh_fwd", "ref_relu_bwd",
                      "ref_log_softmax_fwd", "ref_softmax_fwd", "ref_log_softmax_bwd", "ref_softmax_bwd",
                      "ref_sum", "ref_add", "ref_layernorm_fwd", "ref_layernorm_bwd", "ref_ce_chain",
                      "ref_ce_module", "ref_conv2d_fwd", "ref_mlp_train"):

@@ -152,6 +152,9 @@ int ref_conv2d_init(int64_t cin, int64_t cout, int64_t k, float* w) {
 int ref_relu_fwd(const float* x, float* y, int64_t n) {
     return guarded([&] { copy_out(host_tensor(x, Shape{n}).relu(), y); });
 }
+int ref_leaky_relu_fwd(const float* x, float* y, int64_t n, float alpha) {
+    return guarded([&] { copy_out(host_tensor(x, Shape{n}).leaky_relu(alpha), y); });
+}
 int ref_sigmoid_fwd(const float* x, float* y, int64_t n) {
     return guarded([&] { copy_out(host_tensor(x, Shape{n}).sigmoid(), y); });
 }

@@ -46,6 +46,10 @@ void orc_mul(const float* a, const float* b, float* out, int64_t n) {
 void orc_relu_fwd(const float* x, float* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = x[i] > 0.0f ? x[i] : 0.0f;
 }
+/* Tensor::leaky_relu, CPU loop (tensor/Tensor.cpp:306-311): x > 0 ? x : alpha * x. */
+void orc_leaky_relu_fwd(const float* x, float* y, int64_t n, float alpha) {
+    for (int64_t i = 0; i < n; ++i) y[i] = x[i] > 0.0f ? x[i] : alpha * x[i];
+}
 void orc_sigmoid_fwd(const float* x, float* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = 1.0f / (1.0f + expf(-x[i]));
 }
@@ -382,6 +386,34 @@ void orc_conv2d_bwd(const float* in, const float* w, int has_bias, const float* 
             for (int64_t co = 0; co < Cout; ++co)
                 for (int64_t oh = 0; oh < outH; ++oh)
                     for (int64_t ow = 0; ow < outW; ++ow) gb[co] += gout[((n * Cout + co) * outH + oh) * outW + ow];
+}
+
+/* Tensor::sum along one dim (tensor/Tensor.cpp:513-561) on data viewed as
+ * [outer][reduce][inner]: out[o][i] = sum_d x[o][d][i], d ascending from 0.0f. */
+void orc_sum_dim(const float* x, float* out, int64_t outer, int64_t reduce, int64_t inner) {
+    for (int64_t oi = 0; oi < outer * inner; ++oi) {
+        const int64_t o = oi / inner, i = oi % inner;
+        float s = 0.0f;
+        for (int64_t d = 0; d < reduce; ++d) s += x[(o * reduce + d) * inner + i];
+        out[oi] = s;
+    }
+}
+
+/* nn::CrossEntropyLoss::forward (nn/CrossEntropyLoss.cpp:36-62): softmax
+ * rows, p = probs[r][t_r] clamped below at 1e-9f, loss_r = -log(p), then
+ * Tensor::mean (tensor/Tensor.cpp:562-576: sequential sum / n).  Returns -1
+ * when a target lies outside [0, C) (the reference throws), else 0. */
+int orc_ce_module(const float* logits, const int64_t* t, int64_t R, int64_t C, float* loss, float* probs) {
+    orc_softmax_fwd(logits, probs, R, C);
+    float s = 0.0f;
+    for (int64_t r = 0; r < R; ++r) {
+        if (t[r] < 0 || t[r] >= C) return -1;
+        const float p = probs[r * C + t[r]];
+        const float clamped = p < 1e-9f ? 1e-9f : p;
+        s += -logf(clamped);
+    }
+    loss[0] = s / (float)R;
+    return 0;
 }
 
 /* First-max argmax with strict '>' (examples/train_mlp.cpp:95-100). */

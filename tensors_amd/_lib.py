@@ -16,6 +16,7 @@ TF_OK, TF_ERR_INVALID, TF_ERR_HIP, TF_ERR_UNSUPPORTED, TF_ERR_OOM = range(5)
 TF_F32, TF_F16, TF_BF16, TF_I32, TF_I64, TF_BOOL = range(6)
 TF_COPY_H2H, TF_COPY_H2D, TF_COPY_D2H, TF_COPY_D2D = range(4)
 TF_EPI_NONE, TF_EPI_BIAS, TF_EPI_BIAS_RELU, TF_EPI_RELU, TF_EPI_ROW_BIAS, TF_EPI_ROW_BIAS_RELU = range(6)
+TF_CE_CHAIN, TF_CE_STRICT, TF_CE_CLAMP, TF_CE_MODULE = range(4)
 
 
 class TFError(RuntimeError):
@@ -63,7 +64,7 @@ SIGNATURES: dict[str, list] = {
     "tf_layernorm_fwd": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _f],
     "tf_layernorm_bwd": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i],
     "tf_im2col": [_p, _p, _p] + [_i64] * 12 + [_i],
-    "tf_col2im": [_p, _p, _p] + [_i64] * 12 + [_i],
+    "tf_col2im": [_p, _p, _p] + [_i64] * 14 + [_i],
     "tf_add": [_p, _p, _p, _p, _i64, _i],
     "tf_sub": [_p, _p, _p, _p, _i64, _i],
     "tf_sum_dim": [_p, _p, _p, _i64, _i64, _i64],
@@ -77,11 +78,13 @@ SIGNATURES: dict[str, list] = {
     "tf_relu_bwd": [_p, _p, _p, _p, _i64, _i],
     "tf_sigmoid_bwd": [_p, _p, _p, _p, _i64, _i],
     "tf_tanh_bwd": [_p, _p, _p, _p, _i64, _i],
-    "tf_ce_fwd": [_p, _p, _p, _p, _p, _i64, _i64],
+    "tf_ce_fwd": [_p, _p, _p, _p, _p, _i64, _i64, _i],
     "tf_ce_bwd": [_p, _p, _p, _p, _p, _p, _i64, _i64],
-    "tf_ce_fwd_bwd": [_p, _p, _p, _p, _p, _i64, _i64],
+    "tf_ce_fwd_bwd": [_p, _p, _p, _p, _p, _i64, _i64, _i],
     "tf_log_softmax_fwd": [_p, _p, _p, _i64, _i64],
     "tf_softmax_fwd": [_p, _p, _p, _i64, _i64],
+    "tf_argmax_rows": [_p, _p, _p, _p, _p, _i64, _i64],
+    "tf_leaky_relu_fwd": [_p, _p, _p, _i64, _f, _i],
     "tf_log_softmax_bwd": [_p, _p, _p, _p, _i64, _i64],
     "tf_softmax_bwd": [_p, _p, _p, _p, _i64, _i64],
     "tf_colsum": [_p, _p, _p, _i64, _i64],

@@ -28,7 +28,7 @@ def _load() -> C.CDLL:
     lib.tfa_selftest.argtypes = [C.c_char_p, C.c_int32]
     lib.tfa_selftest.restype = C.c_int
     p, i64, i32, f = C.c_void_p, C.c_int64, C.c_int32, C.c_float
-    lib.tfa_mlp_train.argtypes = [p, i32, i64, i64, i64, i64, p, p, f, f, i32, i32, i32, p, p, p, p]
+    lib.tfa_mlp_train.argtypes = [p, i32, i64, i64, i64, i64, p, p, f, f, i32, i32, i32, p, p, p, p, p]
     lib.tfa_mlp_train.restype = C.c_int
     lib.tfa_cnn_train.argtypes = [i64, i64, i64, i64, i64, i64, p, p, f, f, i32, p, p, p, p]
     lib.tfa_cnn_train.restype = C.c_int
@@ -56,8 +56,10 @@ def selftest(name: str, on_gpu: bool) -> None:
 
 
 def mlp_train(dims, xs, ys, *, steps, lr, mu, on_gpu, reference_compat=False, bf16=False, init_weights=None,
-              warmup=0, want_weights=False):
-    """Returns (losses[steps], final_weights or None, ms_per_step)."""
+              warmup=0, want_weights=False, pool_trace=None):
+    """Returns (losses[steps], final_weights or None, ms_per_step).  With
+    pool_trace a uint64 array [steps], it receives the device pool's bytes in
+    use after each step (GPU only)."""
     dims_a = np.ascontiguousarray(dims, dtype=np.int32)
     xs = np.ascontiguousarray(xs, dtype=np.float32)
     ys = np.ascontiguousarray(ys, dtype=np.int64)
@@ -70,9 +72,11 @@ def mlp_train(dims, xs, ys, *, steps, lr, mu, on_gpu, reference_compat=False, bf
     if iw is not None:
         assert iw.size == nw
     ms = C.c_double(0.0)
+    if pool_trace is not None:
+        assert pool_trace.dtype == np.uint64 and pool_trace.size == steps and pool_trace.flags["C_CONTIGUOUS"]
     _check(lib.tfa_mlp_train(_ptr(dims_a), len(dims_a), batch, steps, warmup, n_batches, _ptr(xs), _ptr(ys), lr, mu,
                              int(on_gpu), int(reference_compat), int(bf16), _ptr(iw), _ptr(losses), _ptr(fw),
-                             C.byref(ms)))
+                             C.byref(ms), _ptr(pool_trace)))
     return losses, fw, ms.value
 
 

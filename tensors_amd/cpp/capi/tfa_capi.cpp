@@ -209,6 +209,13 @@ void t_relu_mask(Device d) {
     check_vec(x.grad(), {0, 0, 0, 1, 1, 1}, "relu grad");
 }
 
+// Tensor::leaky_relu through the registry's LeakyReluFn slot on the GPU
+// (tensor/Tensor.cpp:303-327): x > 0 ? x : alpha * x.
+void t_leaky_relu(Device d) {
+    Tensor x = from_vals({-2, -0.5f, 0, 0.5f, 3}, {5}, d);
+    check_vec(x.leaky_relu(0.1f), {0.1f * -2.0f, 0.1f * -0.5f, 0, 0.5f, 3}, "leaky_relu", 0.0f);
+}
+
 // autograd/ops/autograd_all_ops_test.cpp:108-121 — uniform softmax, grad 0.
 void t_softmax_uniform(Device d) {
     Tensor x = filled({2, 4}, 0.3f, d);
@@ -518,6 +525,7 @@ const std::map<std::string, std::function<void(Device)>>& registry() {
         {"sgd_momentum_rule", t_sgd_momentum_rule},
         {"reshape_grad", t_reshape_grad},
         {"sum_broadcast", t_sum_broadcast},
+        {"leaky_relu", t_leaky_relu},
     };
     return r;
 }
@@ -547,11 +555,13 @@ int tfa_selftest(const char* name, int32_t on_gpu) {
 
 int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t steps, int64_t warmup, int64_t n_batches,
                   const float* xs, const int64_t* ys, float lr, float mu, int32_t on_gpu, int32_t reference_compat,
-                  int32_t bf16, const float* init_weights, float* losses, float* final_weights, double* ms_per_step) {
+                  int32_t bf16, const float* init_weights, float* losses, float* final_weights, double* ms_per_step,
+                  uint64_t* pool_used) {
     return guarded([&] {
         if (ndims < 2 || batch <= 0 || steps < 0 || n_batches <= 0 || warmup < 0 || warmup > steps)
             throw std::invalid_argument("tfa_mlp_train: bad sizes");
         if (bf16 && !on_gpu) throw std::invalid_argument("tfa_mlp_train: bf16 needs the GPU");
+        if (pool_used && !on_gpu) throw std::invalid_argument("tfa_mlp_train: pool_used needs the GPU");
         CompatScope scope(reference_compat != 0);
         const Device d = dev_of(on_gpu);
         std::vector<std::shared_ptr<nn::Linear>> layers;
@@ -590,6 +600,10 @@ int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t ste
             loss.backward();
             opt.step();
             loss_t.push_back(loss);
+            if (pool_used) {
+                hip::synchronize(0);
+                hip::pool_stats(0, nullptr, &pool_used[s]);
+            }
         };
         for (int64_t s = 0; s < warmup; ++s) run_step(s);
         sync_if_gpu(on_gpu);

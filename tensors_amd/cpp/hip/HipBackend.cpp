@@ -74,6 +74,9 @@ void slot_sigmoid(const void* x, void* y, int64_t n, Dtype d, void*) {
     check(tf_sigmoid_fwd(context(0), x, y, n, tf_code(d)), "sigmoid");
 }
 void slot_tanh(const void* x, void* y, int64_t n, Dtype d, void*) { check(tf_tanh_fwd(context(0), x, y, n, tf_code(d)), "tanh"); }
+void slot_leaky_relu(const void* x, void* y, int64_t n, Dtype d, float alpha, void*) {
+    check(tf_leaky_relu_fwd(context(0), x, y, n, alpha, tf_code(d)), "leaky_relu");
+}
 
 struct AutoRegister {
     AutoRegister() { register_backend(); }
@@ -111,10 +114,15 @@ void register_backend() {
         register_cuda_relu(slot_relu);
         register_cuda_sigmoid(slot_sigmoid);
         register_cuda_tanh(slot_tanh);
+        register_cuda_leaky_relu(slot_leaky_relu);
     });
 }
 
 void synchronize(int device) { check(tf_hip_sync(context(device)), "hip::synchronize"); }
+
+void pool_stats(int device, uint64_t* reserved, uint64_t* used) {
+    check(tf_hip_pool_stats(context(device), reserved, used), "hip::pool_stats");
+}
 
 void set_stream(void* stream, int device) { check(tf_hip_set_stream(context(device), stream), "hip::set_stream"); }
 
@@ -269,7 +277,7 @@ void log_softmax_backward(const Tensor& y, const Tensor& dy, Tensor& dx) {
                              static_cast<float*>(dx.data()), r, c), "hip::log_softmax_backward");
 }
 
-void cross_entropy_forward(const Tensor& logits, const Tensor& targets, Tensor& loss, Tensor* lse) {
+void cross_entropy_forward(const Tensor& logits, const Tensor& targets, Tensor& loss, Tensor* lse, int flags) {
     require_gpu(logits, "hip::cross_entropy"); require_gpu(targets, "hip::cross_entropy"); require_gpu(loss, "hip::cross_entropy");
     require(logits.shape().ndim() == 2, "hip::cross_entropy: logits must be 2-D");
     int64_t r, c; rows_cols(logits, r, c, "hip::cross_entropy");
@@ -277,7 +285,7 @@ void cross_entropy_forward(const Tensor& logits, const Tensor& targets, Tensor& 
     require(loss.dtype() == Dtype::Float32 && loss.numel() >= 1, "hip::cross_entropy: loss must be Float32");
     if (lse) require(lse->numel() == r && lse->dtype() == Dtype::Float32, "hip::cross_entropy: lse must be Float32 [N]");
     check(tf_ce_fwd(ctx_of(logits), static_cast<const float*>(logits.data()), static_cast<const int64_t*>(targets.data()),
-                    static_cast<float*>(loss.data()), lse ? static_cast<float*>(lse->data()) : nullptr, r, c),
+                    static_cast<float*>(loss.data()), lse ? static_cast<float*>(lse->data()) : nullptr, r, c, flags),
           "hip::cross_entropy");
 }
 
@@ -377,7 +385,8 @@ void col2im(const Tensor& col, Tensor& dx, int64_t kH, int64_t kW, int64_t sh, i
     require_gpu(col, "hip::col2im"); require_gpu(dx, "hip::col2im");
     require(dx.shape().ndim() == 4, "hip::col2im: NCHW");
     const auto& s = dx.shape();
-    check(tf_col2im(ctx_of(col), col.data(), dx.data(), s[0], s[1], s[2], s[3], kH, kW, sh, sw, ph, pw, dh, dw,
+    const int64_t oh = (s[2] + 2 * ph - dh * (kH - 1) - 1) / sh + 1, ow = (s[3] + 2 * pw - dw * (kW - 1) - 1) / sw + 1;
+    check(tf_col2im(ctx_of(col), col.data(), dx.data(), s[0], s[1], s[2], s[3], kH, kW, sh, sw, ph, pw, dh, dw, oh, ow,
                     tf_code(col.dtype())),
           "hip::col2im");
 }

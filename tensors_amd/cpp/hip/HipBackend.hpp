@@ -25,6 +25,8 @@ namespace tensorforge::hip {
 // The context of GPU `device` (created on first use; one stream and the
 // device's memory pool).  Throws when no GPU is visible.
 tf_ctx* context(int device = 0);
+// Pool bytes reserved and in use on `device` (tf_hip_pool_stats).
+void pool_stats(int device, uint64_t* reserved, uint64_t* used);
 // Throws std::runtime_error("<what>: <tf_last_error()>") when status != 0.
 void check(int status, const char* what);
 // Registers the GPU allocator, copy callback and elementwise slots (idempotent;
@@ -69,7 +71,8 @@ void softmax(const Tensor& x, Tensor& y);
 void log_softmax(const Tensor& x, Tensor& y);
 void softmax_backward(const Tensor& y, const Tensor& dy, Tensor& dx);
 void log_softmax_backward(const Tensor& y, const Tensor& dy, Tensor& dx);
-void cross_entropy_forward(const Tensor& logits, const Tensor& targets, Tensor& loss, Tensor* lse);
+// flags: TF_CE_* of tf_ce_fwd (TF_CE_MODULE for nn::CrossEntropyLoss).
+void cross_entropy_forward(const Tensor& logits, const Tensor& targets, Tensor& loss, Tensor* lse, int flags);
 void cross_entropy_backward(const Tensor& logits, const Tensor& targets, const Tensor* lse, const Tensor* grad_loss,
                             Tensor& dlogits);
 void layernorm_forward(const Tensor& x, const Tensor& gamma, const Tensor& beta, Tensor& y, Tensor& mean,

@@ -3,6 +3,7 @@
 #include "autograd/Wiring.hpp"
 #include "autograd/ops/CrossEntropyBackward.hpp"
 #include "hip/HipBackend.hpp"
+#include "tf_hip.h"
 
 #include <cmath>
 #include <stdexcept>
@@ -22,12 +23,13 @@ Tensor CrossEntropyLoss::forward(Tensor logits, Tensor targets) {
     Tensor loss = Tensor::empty(Shape{1}, Dtype::Float32, logits.device());
     NodePtr<CrossEntropyBackward> node;
     if (on_gpu) {
-        // Target indices outside [0, C) contribute neither loss nor gradient
-        // (the train_mlp chain's one-hot mask skips them); they are not
-        // checked on the host, which would need a device->host copy per step.
+        // The module's loss (nn/CrossEntropyLoss.cpp:47-58 of the reference):
+        // the probability clamped at 1e-9, and a target outside [0, C) makes
+        // the loss NaN instead of throwing (a host check would need a
+        // device->host copy per step); such a row gets a zero gradient.
         Tensor lf = logits.dtype() == Dtype::Float32 ? logits : logits.to(Dtype::Float32);
         Tensor lse = Tensor::empty(Shape{N}, Dtype::Float32, logits.device());
-        hip::cross_entropy_forward(lf, targets, loss, &lse);
+        hip::cross_entropy_forward(lf, targets, loss, &lse, TF_CE_MODULE);
         if (logits.requires_grad()) node = std::make_shared<CrossEntropyBackward>(lf, targets, lse);
     } else {
         // softmax -> gather -> clamp(1e-9) -> -log -> mean, as

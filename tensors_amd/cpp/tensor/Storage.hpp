@@ -4,7 +4,9 @@
 // destructor is defaulted and drops the raw pointer, so no storage is ever
 // freed): the allocator that created the block installs a release callback,
 // run once when the last Storage reference goes away.  For GPU storage that
-// returns the block to the stream-ordered pool (hipFreeAsync).
+// is tf_hip_free: the block goes to its context's cache of freed blocks,
+// from which the next allocation of its size class on the same stream takes
+// it (stream-ordered, like the pool's own reuse).
 #pragma once
 
 #include "tensor/Device.hpp"

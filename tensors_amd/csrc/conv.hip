@@ -258,11 +258,14 @@ tf_status tf_im2col(tf_ctx* ctx, const void* x, void* col, int64_t N, int64_t C,
 }
 
 tf_status tf_col2im(tf_ctx* ctx, const void* col, void* dx, int64_t N, int64_t C, int64_t H, int64_t W, int64_t kH,
-                    int64_t kW, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw, int dtype) {
+                    int64_t kW, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw, int64_t outH,
+                    int64_t outW, int dtype) {
     TF_CTX_CHECK(ctx);
     ConvGeom g;
     tf_status st = make_geom(g, N, C, H, W, kH, kW, sh, sw, ph, pw, dh, dw);
     if (st != TF_OK) return st;
+    TF_REQUIRE(outH == g.outH && outW == g.outW,
+               "tf_col2im: outH/outW do not match the geometry ((H + 2p - d(k-1) - 1) / s + 1)");
     const int64_t total = N * C * H * W;
     if (total == 0) return TF_OK;
     TF_REQUIRE(col && dx, "tf_col2im: null pointer");

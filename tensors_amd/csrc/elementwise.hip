@@ -128,6 +128,12 @@ struct TanhBwdOp {
     __device__ float operator()(float dy, float y) const { return dy * (1.0f - y * y); }
 };
 struct ReluOp { __device__ float operator()(float x) const { return x > 0.0f ? x : 0.0f; } };
+// x > 0 ? x : alpha * x, one rounding (the reference's LeakyReluOp,
+// cuda/kernels/elementwise.cu:116-121, and its CPU loop).
+struct LeakyReluOp {
+    float alpha;
+    __device__ float operator()(float x) const { return x > 0.0f ? x : alpha * x; }
+};
 struct SigmoidOp { __device__ float operator()(float x) const { return 1.0f / (1.0f + expf(-x)); } };
 struct TanhOp { __device__ float operator()(float x) const { return tanhf(x); } };
 
@@ -410,6 +416,9 @@ tf_status tf_tanh_bwd(tf_ctx* ctx, const void* dy, const void* y, void* dx, int6
 }
 tf_status tf_relu_fwd(tf_ctx* ctx, const void* x, void* y, int64_t n, int dtype) {
     return launch_unary(ctx, x, y, n, dtype, ReluOp{}, "tf_relu_fwd");
+}
+tf_status tf_leaky_relu_fwd(tf_ctx* ctx, const void* x, void* y, int64_t n, float alpha, int dtype) {
+    return launch_unary(ctx, x, y, n, dtype, LeakyReluOp{alpha}, "tf_leaky_relu_fwd");
 }
 tf_status tf_sigmoid_fwd(tf_ctx* ctx, const void* x, void* y, int64_t n, int dtype) {
     return launch_unary(ctx, x, y, n, dtype, SigmoidOp{}, "tf_sigmoid_fwd");

@@ -93,9 +93,12 @@ __device__ __forceinline__ void stream_stats(const float* __restrict__ row, int 
 // ---------------------------------------------------------------------------
 // Cross entropy.  MODE 0: forward only (lse, per-row nll).  MODE 1: backward
 // only (dlogits).  MODE 2: fused forward + backward.
-// nll[r] = lse_r - x[r, t_r] (0 for a target outside [0, cols), whose row
-// also receives a zero gradient: the train_mlp chain's one-hot mask skips
-// such labels, examples/train_mlp.cpp:60-66).
+// nll[r] = lse_r - x[r, t_r].  A target outside [0, cols) gives nll 0 and a
+// zero gradient row (the train_mlp chain's one-hot mask skips such labels,
+// examples/train_mlp.cpp:60-66), or NaN with `strict` (the module throws
+// for them, nn/CrossEntropyLoss.cpp:47-53; NaN makes the mean loss NaN
+// without a host check).  nll is capped at nll_max (the module's clamp of
+// the probability at 1e-9, nn/CrossEntropyLoss.cpp:54-55; +inf: no cap).
 // dlogits = scale * (exp(x - lse) - onehot), scale = g / rows.
 // ---------------------------------------------------------------------------
 template <int NC, int MODE>
@@ -103,7 +106,7 @@ __global__ __launch_bounds__(256) void ce_kernel(const float* __restrict__ logit
                                                  const float* __restrict__ lse_in, const float* __restrict__ grad_loss,
                                                  float* __restrict__ lse_out, float* __restrict__ nll,
                                                  float* __restrict__ dlogits, int rows, int cols, float inv_rows,
-                                                 int vec) {
+                                                 int vec, float nll_max, int strict) {
     constexpr int NCC = NC > 0 ? NC : 1;
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
@@ -142,7 +145,8 @@ __global__ __launch_bounds__(256) void ce_kernel(const float* __restrict__ logit
     if (MODE != 1) {
         if (lane == 0) {
             if (lse_out) lse_out[r] = lse;
-            nll[r] = t_ok ? lse - x[t] : 0.0f;
+            float nl = t_ok ? lse - x[t] : (strict ? __builtin_nanf("") : 0.0f);
+            nll[r] = nl > nll_max ? nll_max : nl;   // NaN stays NaN
         }
     }
     if (MODE != 0) {
@@ -301,13 +305,18 @@ int chunks_for(int64_t cols) {
 
 template <int MODE>
 tf_status launch_ce(tf_ctx* ctx, const float* logits, const int64_t* targets, const float* lse_in,
-                    const float* grad_loss, float* lse_out, float* nll, float* dlogits, int64_t rows, int64_t cols) {
+                    const float* grad_loss, float* lse_out, float* nll, float* dlogits, int64_t rows, int64_t cols,
+                    int flags = 0) {
+    // -log(1e-9f) with the host's logf, as the module computes it.
+    const float nll_max = (flags & TF_CE_CLAMP) ? -std::log(1e-9f) : INFINITY;
+    const int strict = (flags & TF_CE_STRICT) ? 1 : 0;
     const int vec = row_vec_ok(logits, cols) && (dlogits == nullptr || row_vec_ok(dlogits, cols));
     const float inv_rows = (float)(1.0 / (double)rows);
     dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
 #define TF_CE_LAUNCH(NC)                                                                              \
     ce_kernel<NC, MODE><<<grid, 256, 0, ctx->stream>>>(logits, targets, lse_in, grad_loss, lse_out, nll, \
-                                                         dlogits, (int)rows, (int)cols, inv_rows, vec)
+                                                         dlogits, (int)rows, (int)cols, inv_rows, vec, nll_max, \
+                                                         strict)
     switch (chunks_for(cols)) {
     case 1: TF_CE_LAUNCH(1); break;
     case 2: TF_CE_LAUNCH(2); break;
@@ -317,6 +326,63 @@ tf_status launch_ce(tf_ctx* ctx, const float* logits, const int64_t* targets, co
     }
 #undef TF_CE_LAUNCH
     return tfh::check_launch("ce_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// Row argmax with the reference's rule (examples/train_mlp.cpp:95-100): scan
+// the row in order, take column c when x[c] > the running maximum, which
+// starts at -1e30 with prediction 0.  The result is the first column holding
+// the row's largest value when that value exceeds -1e30, else 0 (NaN never
+// wins a comparison).  One wave per row: each lane scans its columns in
+// increasing order under the same strict rule from (-1e30, none), and lanes
+// combine by larger value, then smaller column; a row no lane took gets 0.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ x, int64_t* __restrict__ pred,
+                                                     int rows, int cols, int vec) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float* row = x + (int64_t)r * cols;
+    constexpr int kNone = 0x7fffffff;
+    float best = -1e30f;
+    int idx = kNone;
+    for (int c = 0; 256 * c < cols; ++c) {
+        float v[1][4];
+        load_row<1, true>(row + 256 * c, cols - 256 * c, lane, vec != 0, v, -INFINITY);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {   // the lane's columns of this chunk, in increasing order
+            if (v[0][q] > best) {
+                best = v[0][q];
+                idx = col_of(c, lane, q, vec != 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ob = __shfl_xor(best, off, tfd::kWave);
+        const int oi = __shfl_xor(idx, off, tfd::kWave);
+        if (ob > best || (ob == best && oi < idx)) {
+            best = ob;
+            idx = oi;
+        }
+    }
+    if (lane == 0) pred[r] = idx == kNone ? 0 : idx;
+}
+
+// correct[0] = number of rows with pred[r] == labels[r] (one block, fixed order).
+__global__ __launch_bounds__(256) void count_equal_kernel(const int64_t* __restrict__ pred,
+                                                          const int64_t* __restrict__ labels, int rows,
+                                                          int64_t* __restrict__ correct) {
+    __shared__ int part[256];
+    int n = 0;
+    for (int r = threadIdx.x; r < rows; r += 256) n += pred[r] == labels[r] ? 1 : 0;
+    part[threadIdx.x] = n;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) part[threadIdx.x] += part[threadIdx.x + s];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) correct[0] = part[0];
 }
 
 tf_status check_rows(tf_ctx* ctx, int64_t rows, int64_t cols) {
@@ -331,7 +397,7 @@ tf_status check_rows(tf_ctx* ctx, int64_t rows, int64_t cols) {
 extern "C" {
 
 tf_status tf_ce_fwd(tf_ctx* ctx, const float* logits, const int64_t* targets, float* loss, float* lse,
-                    int64_t rows, int64_t cols) {
+                    int64_t rows, int64_t cols, int flags) {
     tf_status st = check_rows(ctx, rows, cols);
     if (st != TF_OK) return st;
     TF_REQUIRE(rows > 0 && cols > 0, "tf_ce_fwd: empty logits");
@@ -339,7 +405,8 @@ tf_status tf_ce_fwd(tf_ctx* ctx, const float* logits, const int64_t* targets, fl
     st = tfh::ensure_workspace(ctx, (size_t)rows * sizeof(float));
     if (st != TF_OK) return st;
     float* nll = reinterpret_cast<float*>(ctx->ws);
-    st = launch_ce<0>(ctx, logits, targets, nullptr, nullptr, lse, nll, nullptr, rows, cols);
+    TF_REQUIRE((flags & ~TF_CE_MODULE) == 0, "tf_ce_fwd: unknown flags");
+    st = launch_ce<0>(ctx, logits, targets, nullptr, nullptr, lse, nll, nullptr, rows, cols, flags);
     if (st != TF_OK) return st;
     mean_kernel<<<1, 256, 0, ctx->stream>>>(nll, (int)rows, (float)(1.0 / (double)rows), loss);
     return tfh::check_launch("mean_kernel");
@@ -355,7 +422,7 @@ tf_status tf_ce_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets, co
 }
 
 tf_status tf_ce_fwd_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets, float* loss, float* dlogits,
-                        int64_t rows, int64_t cols) {
+                        int64_t rows, int64_t cols, int flags) {
     tf_status st = check_rows(ctx, rows, cols);
     if (st != TF_OK) return st;
     TF_REQUIRE(rows > 0 && cols > 0, "tf_ce_fwd_bwd: empty logits");
@@ -363,10 +430,29 @@ tf_status tf_ce_fwd_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets
     st = tfh::ensure_workspace(ctx, (size_t)rows * sizeof(float));
     if (st != TF_OK) return st;
     float* nll = reinterpret_cast<float*>(ctx->ws);
-    st = launch_ce<2>(ctx, logits, targets, nullptr, nullptr, nullptr, nll, dlogits, rows, cols);
+    TF_REQUIRE((flags & ~TF_CE_MODULE) == 0, "tf_ce_fwd_bwd: unknown flags");
+    st = launch_ce<2>(ctx, logits, targets, nullptr, nullptr, nullptr, nll, dlogits, rows, cols, flags);
     if (st != TF_OK) return st;
     mean_kernel<<<1, 256, 0, ctx->stream>>>(nll, (int)rows, (float)(1.0 / (double)rows), loss);
     return tfh::check_launch("mean_kernel");
+}
+
+tf_status tf_argmax_rows(tf_ctx* ctx, const float* x, int64_t* pred, const int64_t* labels, int64_t* correct,
+                         int64_t rows, int64_t cols) {
+    tf_status st = check_rows(ctx, rows, cols);
+    if (st != TF_OK) return st;
+    TF_REQUIRE((labels == nullptr) == (correct == nullptr), "tf_argmax_rows: labels and correct go together");
+    if (rows == 0) {
+        if (correct) return tf_hip_zero(ctx, correct, sizeof(int64_t));
+        return TF_OK;
+    }
+    TF_REQUIRE(x && pred && (cols > 0), "tf_argmax_rows: null pointer or no columns");
+    dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+    argmax_kernel<<<grid, 256, 0, ctx->stream>>>(x, pred, (int)rows, (int)cols, row_vec_ok(x, cols));
+    st = tfh::check_launch("argmax_kernel");
+    if (st != TF_OK || correct == nullptr) return st;
+    count_equal_kernel<<<1, 256, 0, ctx->stream>>>(pred, labels, (int)rows, correct);
+    return tfh::check_launch("count_equal_kernel");
 }
 
 #define TF_ROW_LAUNCH(KERNEL, KIND, ...)                                          \

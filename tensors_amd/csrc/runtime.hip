@@ -11,6 +11,7 @@
 // of that class on the same stream, so steady-state steps make no pool calls
 // either (a hipFreeAsync + hipMallocFromPoolAsync pair took 30-70 us of host
 // time per block here, which made small training steps host-bound).
+#include "alloc_policy.hpp"
 #include "common.hpp"
 
 #include <mutex>
@@ -55,6 +56,27 @@ tf_status release_cached(tf_ctx* ctx) {
     ctx->cached.clear();
     ctx->cached_bytes = 0;
     return TF_OK;
+}
+
+// Out-of-memory release: hands the cached blocks and the workspace back to
+// the pool (stream-ordered, then waits for the stream so the pool can reuse
+// them) and reports whether anything was freed.  Caller holds ctx->cache_mu.
+bool release_for_retry(tf_ctx* ctx) {
+    const bool any = ctx->cached_bytes > 0 || ctx->ws != nullptr;
+    if (!any) return false;
+    if (release_cached(ctx) != TF_OK) return false;
+    if (ctx->ws) {
+        if (hipFreeAsync(ctx->ws, ctx->stream) != hipSuccess) return false;
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+    }
+    return hipStreamSynchronize(ctx->stream) == hipSuccess;
+}
+
+tfh::AllocOutcome outcome_of(hipError_t e) {
+    if (e == hipSuccess) return tfh::AllocOutcome::Ok;
+    (void)hipGetLastError();
+    return e == hipErrorOutOfMemory ? tfh::AllocOutcome::OutOfMemory : tfh::AllocOutcome::Failed;
 }
 
 // Launch-timing records (tf_hip_timing_*), process-wide.
@@ -113,23 +135,15 @@ tf_status ensure_workspace(tf_ctx* ctx, size_t bytes) {
         ctx->ws = nullptr;
         ctx->ws_bytes = 0;
     }
-    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-    hipError_t e = hipMallocFromPoolAsync(&ctx->ws, want, ctx->pool, ctx->stream);
-    if (e == hipErrorOutOfMemory) {
-        // The block cache may hold the memory: hand it back and retry once.
-        (void)hipGetLastError();
-        std::lock_guard<std::mutex> lock(ctx->cache_mu);
-        if (ctx->cached_bytes > 0) {
-            tf_status st = release_cached(ctx);
-            if (st != TF_OK) return st;
-            TF_HIP_CHECK(hipStreamSynchronize(ctx->stream));
-            e = hipMallocFromPoolAsync(&ctx->ws, want, ctx->pool, ctx->stream);
-        }
-    }
-    if (e != hipSuccess) {
-        ctx->ws = nullptr;
-        return hip_error(e, "ensure_workspace: hipMallocFromPoolAsync");
-    }
+    const size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+    hipError_t e = hipSuccess;
+    void* p = nullptr;
+    std::lock_guard<std::mutex> lock(ctx->cache_mu);
+    const AllocOutcome r = allocate_with_retry(
+        [&] { return outcome_of(e = hipMallocFromPoolAsync(&p, want, ctx->pool, ctx->stream)); },
+        [&] { return release_for_retry(ctx); });
+    if (r != AllocOutcome::Ok) return hip_error(e, "ensure_workspace: hipMallocFromPoolAsync");
+    ctx->ws = p;
     ctx->ws_bytes = want;
     return TF_OK;
 }
@@ -232,15 +246,11 @@ tf_status tf_hip_alloc(tf_ctx* ctx, size_t bytes, void** out) {
         ctx->live.emplace(*out, cls);
         return TF_OK;
     }
-    hipError_t e = hipMallocFromPoolAsync(out, cls, ctx->pool, ctx->stream);
-    if (e == hipErrorOutOfMemory && ctx->cached_bytes > 0) {
-        (void)hipGetLastError();
-        tf_status st = release_cached(ctx);
-        if (st != TF_OK) return st;
-        TF_HIP_CHECK(hipStreamSynchronize(ctx->stream));
-        e = hipMallocFromPoolAsync(out, cls, ctx->pool, ctx->stream);
-    }
-    if (e != hipSuccess) {
+    hipError_t e = hipSuccess;
+    const tfh::AllocOutcome r = tfh::allocate_with_retry(
+        [&] { return outcome_of(e = hipMallocFromPoolAsync(out, cls, ctx->pool, ctx->stream)); },
+        [&] { return release_for_retry(ctx); });
+    if (r != tfh::AllocOutcome::Ok) {
         *out = nullptr;
         return tfh::hip_error(e, "tf_hip_alloc: hipMallocFromPoolAsync");
     }

@@ -62,6 +62,23 @@ def relu(x, y):
     return y
 
 
+def leaky_relu(x, y, alpha):
+    call("tf_leaky_relu_fwd", _ctx(x), x.ptr, y.ptr, _same(x, y), float(alpha), x.tf_dtype)
+    return y
+
+
+def argmax_rows(x, pred, labels=None, correct=None):
+    """pred[r] = argmax of row r (int64), the reference's first-max rule;
+    with labels and correct, also correct[0] = number of matches."""
+    if len(x.shape) != 2 or pred.size != x.shape[0]:
+        raise ValueError("argmax_rows: x must be 2-D and pred hold one entry per row")
+    if (labels is None) != (correct is None) or (labels is not None and labels.size != x.shape[0]):
+        raise ValueError("argmax_rows: labels (one per row) and correct go together")
+    call("tf_argmax_rows", _ctx(x), x.ptr, pred.ptr, labels.ptr if labels is not None else None,
+         correct.ptr if correct is not None else None, x.shape[0], x.shape[1])
+    return pred
+
+
 def sigmoid(x, y):
     call("tf_sigmoid_fwd", _ctx(x), x.ptr, y.ptr, _same(x, y), x.tf_dtype)
     return y
@@ -94,13 +111,14 @@ def _check_targets(logits, targets):
         raise ValueError("targets must be int64 with one entry per row")
 
 
-def ce_fwd(logits, targets, loss, lse=None):
+def ce_fwd(logits, targets, loss, lse=None, flags=_lib.TF_CE_CHAIN):
+    """loss[0] = mean cross-entropy; flags TF_CE_* (0: the train_mlp chain)."""
     rows, cols = _rows_cols(logits)
     _check_targets(logits, targets)
     if lse is not None and lse.size != rows:
         raise ValueError("lse must have one entry per row")
     call("tf_ce_fwd", _ctx(logits), logits.ptr, targets.ptr, loss.ptr, lse.ptr if lse is not None else None,
-         rows, cols)
+         rows, cols, flags)
     return loss
 
 
@@ -113,11 +131,11 @@ def ce_bwd(logits, targets, dlogits, lse=None, grad_loss=None):
     return dlogits
 
 
-def ce_fwd_bwd(logits, targets, loss, dlogits):
+def ce_fwd_bwd(logits, targets, loss, dlogits, flags=_lib.TF_CE_CHAIN):
     rows, cols = _rows_cols(logits)
     _check_targets(logits, targets)
     _same(logits, dlogits)
-    call("tf_ce_fwd_bwd", _ctx(logits), logits.ptr, targets.ptr, loss.ptr, dlogits.ptr, rows, cols)
+    call("tf_ce_fwd_bwd", _ctx(logits), logits.ptr, targets.ptr, loss.ptr, dlogits.ptr, rows, cols, flags)
     return loss, dlogits
 
 
@@ -265,5 +283,5 @@ def col2im(col, dx, kH, kW, stride=(1, 1), pad=(0, 0), dil=(1, 1)):
     if col.size != N * Cc * kH * kW * oh * ow:
         raise ValueError("col2im: col has the wrong size")
     call("tf_col2im", _ctx(col), col.ptr, dx.ptr, N, Cc, H, W, kH, kW, stride[0], stride[1], pad[0], pad[1],
-         dil[0], dil[1], col.tf_dtype)
+         dil[0], dil[1], oh, ow, col.tf_dtype)
     return dx

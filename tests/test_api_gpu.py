@@ -114,3 +114,25 @@ def test_c5_bf16_mlp_tracks_fp32(ctx):
     l16, _, _ = api.mlp_train(dims, xs, ys, steps=steps, lr=0.01, mu=0.9, on_gpu=True, bf16=True)
     assert np.all(np.isfinite(l16))
     assert_close(l16, l32, 2e-2, "bf16 vs fp32 losses", atol=1e-2)
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c5"])
+def test_pool_use_is_flat_across_steps(ctx, cfg):
+    """Storage is released when its last reference goes (the reference never
+    frees, tensor/Storage.hpp:27): the device pool's bytes in use after each
+    step stop growing after the first steps (C1: steps 10 and 100 equal; C5
+    at full size: steps 4 and 12 equal)."""
+    if cfg == "c1":
+        dims, steps, early = C1, 100, 9
+        xs, ys = _c1_inputs(100)
+        kw = dict(lr=0.1, mu=0.9, reference_compat=True)
+    else:
+        dims, steps, early = [4096, 8192, 8192, 4096, 1000], 12, 3
+        xs = np.random.default_rng(5500).standard_normal((1, 4096, 4096), dtype=np.float32)
+        ys = np.random.default_rng(5501).integers(0, 1000, (1, 4096)).astype(np.int64)
+        kw = dict(lr=0.01, mu=0.9, bf16=True)
+    trace = np.zeros(steps, np.uint64)
+    losses, _, _ = api.mlp_train(dims, xs, ys, steps=steps, on_gpu=True, pool_trace=trace, **kw)
+    assert np.all(np.isfinite(losses))
+    assert trace[early] > 0
+    assert np.all(trace[early:] == trace[early]), f"pool bytes in use grow: {trace.tolist()}"

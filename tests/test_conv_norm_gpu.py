@@ -185,3 +185,14 @@ def test_gemm_row_bias_relu_splitk(ctx):
                 bias=ctx.array(bias))
     want = np.maximum(a.astype(np.float64) @ b.astype(np.float64) + bias[:, None], 0)
     assert_close(c.numpy(), want, RTOL32, "row bias relu split-K")
+
+
+def test_col2im_checks_out_extent(ctx):
+    """tf_col2im takes launch_col2im's outH/outW (cuda/kernels/col2im.cuh:22-29)
+    and rejects values that disagree with the geometry."""
+    from tensors_amd._lib import TFError, call, TF_F32
+    col = ctx.zeros((1, 9, 16))
+    dx = ctx.empty((1, 1, 4, 4))
+    call("tf_col2im", ctx.handle, col.ptr, dx.ptr, 1, 1, 4, 4, 3, 3, 1, 1, 1, 1, 1, 1, 4, 4, TF_F32)
+    with pytest.raises(TFError, match="outH"):
+        call("tf_col2im", ctx.handle, col.ptr, dx.ptr, 1, 1, 4, 4, 3, 3, 1, 1, 1, 1, 1, 1, 4, 3, TF_F32)

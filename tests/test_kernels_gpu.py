@@ -606,6 +606,35 @@ def test_ce_upstream_scale_and_bad_labels(ctx):
     assert_close(loss.numpy(), [loss_ref], RTOL32, "loss with skipped labels")
 
 
+def test_ce_module_flags_clamp_and_nan(ctx):
+    """TF_CE_MODULE gives nn::CrossEntropyLoss's loss (probability clamped at
+    1e-9, oracle.ce_module pinned to the reference); a bad target makes the
+    loss NaN instead of a plausible value; the gradient is unchanged."""
+    from tensors_amd import _lib
+    ops = _ops()
+    R, Cc = 64, 10
+    logits = synth.normal(133, (R, Cc), std=3.0)
+    labels = synth.uniform_int(134, (R,), Cc)
+    logits[5] = np.array([0, 0, 0, 0, 0, 0, 0, 0, 0, 40], np.float32)
+    labels[5] = 0
+    dl, dt = ctx.array(logits), ctx.array(labels)
+    loss, d = ctx.empty((1,)), ctx.empty((R, Cc))
+    ops.ce_fwd(dl, dt, loss, flags=_lib.TF_CE_MODULE)
+    assert_close(loss.numpy(), [oracle.ce_module(logits, labels)], RTOL32, "module loss with clamp")
+    ops.ce_fwd(dl, dt, loss)                       # the chain: no clamp (row 5 contributes 40)
+    assert float(loss.numpy()[0]) > oracle.ce_module(logits, labels) + 15.0 / R
+    ops.ce_fwd_bwd(dl, dt, loss, d, flags=_lib.TF_CE_MODULE)
+    assert_close(loss.numpy(), [oracle.ce_module(logits, labels)], RTOL32, "fused module loss")
+    _, d_ref = oracle.ce_chain(logits, labels)
+    assert_close(d.numpy(), d_ref, RTOL32, "gradient unchanged by the flags")
+    labels[9] = Cc
+    dt = ctx.array(labels)
+    ops.ce_fwd(dl, dt, loss, flags=_lib.TF_CE_MODULE)
+    assert np.isnan(loss.numpy()[0])
+    ops.ce_fwd(dl, dt, loss, flags=_lib.TF_CE_CHAIN)
+    assert np.isfinite(loss.numpy()[0])
+
+
 @pytest.mark.parametrize("R,Cc", [(64, 10), (256, 1024), (3, 777), (2, 5000)])
 def test_softmax_family(ctx, R, Cc):
     ops = _ops()

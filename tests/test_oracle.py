@@ -478,6 +478,26 @@ def _conv64(x, w, b, s, p):
 def test_argmax_first_max_wins():
     x = np.array([[1, 3, 3, 2], [5, 5, 5, 5], [-1, -2, -0.5, -0.5]], np.float32)
     assert list(oracle.argmax_rows(x)) == [1, 0, 2]
+    # examples/train_mlp.cpp:95-100 starts from -1e30 with prediction 0 and
+    # compares with '>': values at or below -1e30 and NaN never win; -0.0
+    # and +0.0 tie (the first stays).
+    nan = np.float32(np.nan)
+    y = np.array([[-1e30, -3e30, -1e30, -np.inf], [nan, nan, 2, nan], [nan, nan, nan, nan],
+                  [-0.0, 0.0, -0.0, -1], [0.0, -0.0, 0, -1], [-2e30, -1e29, -1e30, -1e29]], np.float32)
+    assert list(oracle.argmax_rows(y)) == [0, 2, 0, 0, 0, 1]
+
+
+@needs_ref
+def test_leaky_relu_live_bits_and_known_answers():
+    x = np.concatenate([synth.normal(800, (999,)), np.array([0.0, -0.0, 1e-45, -1e-45, 3e38, -3e38],
+                                                             np.float32)])
+    for alpha in (0.01, 0.2, 1.5, 0.0):
+        y = np.empty_like(x)
+        oracle.ref_call("ref_leaky_relu_fwd", x, y, x.size, alpha)
+        assert_bitexact(oracle.leaky_relu(x, alpha), y, f"leaky_relu alpha={alpha}")
+    got = oracle.leaky_relu(np.array([-2, -0.5, 0, 0.5], np.float32), 0.1)
+    assert_bitexact(got, np.array([np.float32(0.1) * np.float32(-2), np.float32(0.1) * np.float32(-0.5), 0, 0.5],
+                                  np.float32), "known")
 
 
 # ---------------------------------------------------------------------------
@@ -581,3 +601,39 @@ def test_mixed_step_rounding_changes_results_by_bf16_amounts():
     l16 = oracle.mlp_step_mixed(*args()[:2], *args()[2:], x, y, 0.1, 0.9, rounding=True)
     l32 = oracle.mlp_step_mixed(*args()[:2], *args()[2:], x, y, 0.1, 0.9, rounding=False)
     assert 0 < abs(l16 - l32) < 2e-2 * abs(l32)
+
+
+@needs_ref
+def test_sum_dim_live_bits_and_float64():
+    x = synth.normal(810, (37, 53))
+    for dim, (o, r, i) in ((0, (1, 37, 53)), (1, (37, 53, 1))):
+        out = np.empty(53 if dim == 0 else 37, np.float32)
+        oracle.ref_call("ref_sum", x, out, 37, 53, dim)
+        assert_bitexact(oracle.sum_dim(x, o, r, i).reshape(-1), out, f"sum dim {dim}")
+    y = synth.normal(811, (5, 7, 9))
+    assert_close(oracle.sum_dim(y, 5, 7, 9), y.astype(np.float64).sum(1), 1e-6, "3-D middle dim")
+
+
+@needs_ref
+def test_ce_module_live_bits_and_clamp():
+    """nn::CrossEntropyLoss::forward: the compiled reference's loss equals the
+    oracle's bit for bit, including rows whose target probability is below
+    the 1e-9 clamp; a bad target raises in both."""
+    logits = synth.normal(820, (64, 10), std=3.0)
+    labels = synth.uniform_int(821, (64,), 10)
+    logits[5] = np.array([0, 0, 0, 0, 0, 0, 0, 0, 0, 40], np.float32)   # p(t=0) ~ 4e-18 < 1e-9
+    labels[5] = 0
+    out = np.zeros(1, np.float32)
+    oracle.ref_call("ref_ce_module", logits, labels, 64, 10, out)
+    assert oracle.ce_module(logits, labels) == float(out[0])
+    # the clamped row contributes -log(1e-9) = 20.72
+    mask = np.ones(64, bool)
+    mask[5] = False
+    rest = oracle.ce_module(logits[mask], labels[mask])
+    assert abs(float(out[0]) * 64 - (rest * 63 + 20.7232658)) < 1e-3
+    bad = labels.copy()
+    bad[3] = 10
+    with pytest.raises(IndexError):
+        oracle.ce_module(logits, bad)
+    with pytest.raises(RuntimeError):
+        oracle.ref_call("ref_ce_module", logits, bad, 64, 10, out)
