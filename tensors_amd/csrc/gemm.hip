@@ -1423,6 +1423,149 @@ void gemm_bf16_dl8_kernel(GemmParams p) {
     big_epilogue<64>(p, acc, m0, n0, split, batch, reinterpret_cast<float*>(sb) + (wave & 1) * 4096);
 }
 
+// Eight waves in two groups of four, one wave of each group per SIMD, with
+// their phases offset by half a block ("ping-pong"): while one group runs
+// a block's 16 MFMAs from registers, the other issues its share of a later
+// block's direct loads and reads the next block's fragments from LDS, then
+// they swap, so each SIMD's MFMA pipe is fed by one of its two waves while
+// the other waits (for LDS reads, for loads, at the barrier).  Same tile,
+// wave layout, LDS ring (five 32-deep blocks), loads, fragments and
+// epilogue as gemm_bf16_dl8_kernel.
+//
+// Every wave runs the same loop: for block t, M(t) (issue its share of
+// block t+4 into block t-1's buffer when t >= 1, read block t's fragments),
+// barrier, C(t) (16 MFMAs), barrier.  Group 1 passes one extra barrier before
+// the loop and group 0 one after it, so when group 0 is in M(t) group 1 is
+// in C(t-1), and when group 0 is in C(t) group 1 is in M(t).  Every barrier
+// waits (in each wave) for all of the wave's loads but its newest three
+// blocks and for its LDS reads.  Hazards: block t is read in M(t) by group 0
+// (phase 2t) and group 1 (phase 2t+1); a wave's share of block t is waited
+// for before the barrier that opens phase 2t (it was issued three or more
+// blocks earlier); block t-1's buffer is refilled in M(t), from phase 2t
+// on, after both groups have read it (phases 2t-2 and 2t-1).
+template <bool A_KMAJ, bool B_KMAJ, bool KTAIL = false>
+__global__ __launch_bounds__(2 * kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_bf16_pp_kernel(GemmParams p) {
+    __shared__ u32x4 s0[2 * kDlVec], s1[2 * kDlVec], s2[2 * kDlVec], s3[2 * kDlVec], s4[2 * kDlVec];
+
+    int tm, tn;
+    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int split = blockIdx.y;
+    const int batch = blockIdx.z;
+    const int m0 = tm * kBigTile, n0 = tn * kBigTile;
+    const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A) + (int64_t)batch * p.stride_a;
+    const uint16_t* B = reinterpret_cast<const uint16_t*>(p.B) + (int64_t)batch * p.stride_b;
+    const int kb64_elem = KTAIL ? (p.K + 63) / 64 : p.K / 64;
+    const int kb64_total = kb64_elem * p.reduce_batch;
+    const int kb64_beg = split * p.kb_per_split;
+    const int nk = 2 * max(0, min(kb64_total, kb64_beg + p.kb_per_split) - kb64_beg);
+    const int kb_beg = 2 * kb64_beg;
+    const int kpb = 2 * kb64_elem;
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int half = lane >> 5;
+    const bool g1 = __builtin_amdgcn_readfirstlane(wave >> 2) != 0;  // wave-uniform
+    v16f acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+
+    if (nk > 0) {
+        DlOperand<A_KMAJ> oa;
+        DlOperand<B_KMAJ, 2> ob;
+        oa.init((wave >> 2) * 128);
+        ob.init((wave & 3) * 64);
+        uint32_t voff_a[kDl8Loads], voff_b[kDl8Loads];
+        dl_offsets<A_KMAJ, kDl8Loads>(p.lda, voff_a);
+        dl_offsets<B_KMAJ, kDl8Loads>(p.ldb, voff_b);
+        BigFrags8 f[2];
+        auto buf_a = [&](auto Bc) TF_LAMBDA_INLINE -> u32x4* {
+            constexpr int b = decltype(Bc)::value;
+            if constexpr (b == 0) return s0;
+            else if constexpr (b == 1) return s1;
+            else if constexpr (b == 2) return s2;
+            else if constexpr (b == 3) return s3;
+            else return s4;
+        };
+        auto buf_b = [&](auto Bc) TF_LAMBDA_INLINE -> u32x4* { return buf_a(Bc) + kDlVec; };
+        KWalk walk;
+        walk.init(A, B, 2 * p.stride_a, 2 * p.stride_b, kb_beg, nk, kpb);
+        const uint32_t ta0 = 2u * (A_KMAJ ? (uint32_t)m0 * (uint32_t)p.lda : (uint32_t)m0);
+        const uint32_t tb0 = 2u * (B_KMAJ ? (uint32_t)n0 * (uint32_t)p.ldb : (uint32_t)n0);
+        const uint32_t a_kstep = 2u * kDlK * (A_KMAJ ? 1u : (uint32_t)p.lda);
+        const uint32_t b_kstep = 2u * kDlK * (B_KMAJ ? 1u : (uint32_t)p.ldb);
+        const uint32_t wave_lds = dl_wave_offset<kDl8Loads>();
+        int kl_a[kDl8Loads], kl_b[kDl8Loads];
+        if constexpr (KTAIL) {
+            dl_klane<A_KMAJ, kDl8Loads>(kl_a);
+            dl_klane<B_KMAJ, kDl8Loads>(kl_b);
+        }
+        auto issue_next = [&](u32x4* la, u32x4* lb) TF_LAMBDA_INLINE {
+            const uint32_t so_a = ta0 + (uint32_t)walk.kin * a_kstep, so_b = tb0 + (uint32_t)walk.kin * b_kstep;
+            if constexpr (KTAIL) {
+                const int rem = p.K - walk.kin * kDlK;
+                uint32_t va[kDl8Loads], vb[kDl8Loads];
+#pragma unroll
+                for (int i = 0; i < kDl8Loads; ++i) {
+                    va[i] = kl_a[i] < rem ? voff_a[i] : kDlOob;
+                    vb[i] = kl_b[i] < rem ? voff_b[i] : kDlOob;
+                }
+                dl_issue<kDl8Loads>(dl_rsrc(walk.a_base, p.a_bytes), so_a, va, lds_addr(la) + wave_lds);
+                dl_issue<kDl8Loads>(dl_rsrc(walk.b_base, p.b_bytes), so_b, vb, lds_addr(lb) + wave_lds);
+            } else {
+                dl_issue<kDl8Loads>(dl_rsrc(walk.a_base, p.a_bytes), so_a, voff_a, lds_addr(la) + wave_lds);
+                dl_issue<kDl8Loads>(dl_rsrc(walk.b_base, p.b_bytes), so_b, voff_b, lds_addr(lb) + wave_lds);
+            }
+            walk.advance();
+        };
+        // Both k steps of a block: A0, B0, B1, A1..A3 per step.
+        auto read_block = [&](const u32x4* la, const u32x4* lb) TF_LAMBDA_INLINE {
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                f[s].a[0] = oa.frag(la, 0, s, half);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) f[s].b[j] = ob.frag(lb, j, s, half);
+#pragma unroll
+                for (int i = 1; i < 4; ++i) f[s].a[i] = oa.frag(la, i, s, half);
+            }
+        };
+        constexpr int kAhead = 3 * 2 * kDl8Loads;  // loads of the newest three blocks
+        // Prologue: blocks 0 .. 4 (clamped) into buffers 0 .. 4.
+        static_for<kDlBufs>([&](auto Bc) TF_LAMBDA_INLINE { issue_next(buf_a(Bc), buf_b(Bc)); });
+        dl_barrier<(kDlBufs - 1) * 2 * kDl8Loads>();  // block 0 has landed
+        if (g1) dl_barrier<kAhead>();                 // group 1 starts half a block later
+        int t = 0;
+        bool stop = false;
+        while (!stop) {
+            static_for<kDlBufs>([&](auto Bc) TF_LAMBDA_INLINE {
+                constexpr int bp = (decltype(Bc)::value + kDlBufs - 1) % kDlBufs;
+                if (stop) return;
+                // M(t)
+                if (t >= 1) issue_next(buf_a(std::integral_constant<int, bp>{}), buf_b(std::integral_constant<int, bp>{}));
+                read_block(buf_a(Bc), buf_b(Bc));
+                __builtin_amdgcn_sched_barrier(0);
+                // Group 1's share of block t+1 is read by group 0 right after
+                // this barrier; group 0's is not needed until the next one.
+                if (g1) dl_barrier<kAhead>();
+                else dl_barrier<kAhead + 2 * kDl8Loads>();
+                // C(t)
+                big_mfma8(f[0], acc);
+                big_mfma8(f[1], acc);
+                __builtin_amdgcn_sched_barrier(0);
+                dl_barrier<kAhead>();
+                ++t;
+                if (t >= nk) stop = true;
+            });
+        }
+        if (!g1) dl_barrier<kAhead>();  // matches group 1's extra barrier
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // drain the clamped loads before the epilogue
+    }
+    __syncthreads();
+    u32x4* sb = (wave >> 1) == 0 ? s0 : (wave >> 1) == 1 ? s1 : (wave >> 1) == 2 ? s2 : s3;
+    big_epilogue<64>(p, acc, m0, n0, split, batch, reinterpret_cast<float*>(sb) + (wave & 1) * 4096);
+}
+
 // Edge-tile kernel (or every tile when the direct path does not apply):
 // register-staged, bounds-checked 64-deep blocks over the tiles edge_coords
 // assigns.
@@ -2200,16 +2343,28 @@ KernelFn pick_bf16_big(bool a_kmaj, bool b_kmaj) {
     return gemm_bf16_big_kernel<false, false>;
 }
 
-// Interior bf16 tiles run on the eight-wave form (3.5-5 % faster than four
-// waves on the C5 shapes with random data); building with
-// -DTF_BF16_DL8=0 selects the four-wave kernel.
-#ifndef TF_BF16_DL8
-#define TF_BF16_DL8 1
+// Interior bf16 tiles run on the eight-wave ping-pong kernel (2-3 % faster
+// than the eight-wave kernel on the C5 backward GEMMs, which itself was
+// 3.5-5 % faster than four waves).  Building with -DTF_BF16_KERNEL=1 selects
+// the eight-wave kernel, 0 the four-wave one.
+#ifndef TF_BF16_KERNEL
+#define TF_BF16_KERNEL 2
 #endif
-constexpr bool kBf16Dl8 = TF_BF16_DL8 != 0;
-constexpr int kBf16DlThreads = kBf16Dl8 ? 2 * kThreads : kThreads;
+constexpr int kBf16Kernel = TF_BF16_KERNEL;
+constexpr int kBf16DlThreads = kBf16Kernel >= 1 ? 2 * kThreads : kThreads;
 KernelFn pick_bf16_dl(bool a_kmaj, bool b_kmaj, bool ktail) {
-    if constexpr (kBf16Dl8) {
+    if constexpr (kBf16Kernel == 2) {
+        if (ktail) {
+            if (a_kmaj && b_kmaj) return gemm_bf16_pp_kernel<true, true, true>;
+            if (a_kmaj && !b_kmaj) return gemm_bf16_pp_kernel<true, false, true>;
+            if (!a_kmaj && b_kmaj) return gemm_bf16_pp_kernel<false, true, true>;
+            return gemm_bf16_pp_kernel<false, false, true>;
+        }
+        if (a_kmaj && b_kmaj) return gemm_bf16_pp_kernel<true, true, false>;
+        if (a_kmaj && !b_kmaj) return gemm_bf16_pp_kernel<true, false, false>;
+        if (!a_kmaj && b_kmaj) return gemm_bf16_pp_kernel<false, true, false>;
+        return gemm_bf16_pp_kernel<false, false, false>;
+    } else if constexpr (kBf16Kernel == 1) {
         if (ktail) {
             if (a_kmaj && b_kmaj) return gemm_bf16_dl8_kernel<true, true, true>;
             if (a_kmaj && !b_kmaj) return gemm_bf16_dl8_kernel<true, false, true>;
@@ -2220,11 +2375,12 @@ KernelFn pick_bf16_dl(bool a_kmaj, bool b_kmaj, bool ktail) {
         if (a_kmaj && !b_kmaj) return gemm_bf16_dl8_kernel<true, false>;
         if (!a_kmaj && b_kmaj) return gemm_bf16_dl8_kernel<false, true>;
         return gemm_bf16_dl8_kernel<false, false>;
+    } else {
+        if (a_kmaj && b_kmaj) return gemm_bf16_dl_kernel<true, true>;
+        if (a_kmaj && !b_kmaj) return gemm_bf16_dl_kernel<true, false>;
+        if (!a_kmaj && b_kmaj) return gemm_bf16_dl_kernel<false, true>;
+        return gemm_bf16_dl_kernel<false, false>;
     }
-    if (a_kmaj && b_kmaj) return gemm_bf16_dl_kernel<true, true>;
-    if (a_kmaj && !b_kmaj) return gemm_bf16_dl_kernel<true, false>;
-    if (!a_kmaj && b_kmaj) return gemm_bf16_dl_kernel<false, true>;
-    return gemm_bf16_dl_kernel<false, false>;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -2350,7 +2506,7 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
         const int64_t ext_a = trans_a ? (K - 1) * lda + M : (M - 1) * lda + K;
         const int64_t ext_b = trans_b ? (N - 1) * ldb + K : (K - 1) * ldb + N;
         const int64_t lim = (int64_t)0x7fffffff;  // descriptor extent is passed as int
-        const int64_t k_unit = kBf16Dl8 ? 8 : 64;   // the four-wave kernel has no K tail
+        const int64_t k_unit = kBf16Kernel >= 1 ? 8 : 64;   // the four-wave kernel has no K tail
         const bool direct = K > 0 && K % k_unit == 0 && p.vec_a && p.vec_b && ext_a * esz <= lim && ext_b * esz <= lim;
         p.a_bytes = direct ? (uint32_t)(ext_a * esz) : 0u;
         p.b_bytes = direct ? (uint32_t)(ext_b * esz) : 0u;
