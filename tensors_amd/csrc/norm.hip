@@ -13,9 +13,9 @@
 //
 // Rows of up to 2048 columns: one fused pass (one wave per row, the row held
 // in registers; each wave also accumulates its rows' dgamma/dbeta column
-// partials, combined per block in LDS and then across blocks by the shared
-// fixed-order reduction tfh::partial_rows_sum).  Wider rows: a streaming row kernel for dx and a
-// column kernel for dgamma/dbeta.
+// partials, combined per block in LDS and then across blocks by a
+// fixed-order column-strip reduction).  Wider rows: a streaming row kernel
+// for dx and a column kernel for dgamma/dbeta.
 #include "common.hpp"
 
 #include <algorithm>
@@ -149,8 +149,6 @@ __global__ __launch_bounds__(256) void ln_fwd_stream_kernel(const float* __restr
 // Fused backward for cols <= 256 * NC.  Block b (WAVES waves) handles rows
 // [b * rpb, (b+1) * rpb); each wave takes every WAVES-th of them.  Column
 // partial sums of dy * xhat and dy go to part[b][0][:] and part[b][1][:].
-// Eight waves per block halve the partials (8 bytes per column per block)
-// against four while keeping one row per wave at 1024 rows.
 // ---------------------------------------------------------------------------
 template <int NC, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void ln_bwd_fused_kernel(const float* __restrict__ dy,
@@ -228,6 +226,50 @@ __global__ __launch_bounds__(WAVES * 64) void ln_bwd_fused_kernel(const float* _
 #pragma unroll
             for (int w = 1; w < WAVES; ++w) t += red[w][h][slot];
             pg[h * cols + j] = t;
+        }
+    }
+}
+
+// Column sums of the row pass's partials part[K][W] (W = 2 * cols: the
+// dgamma columns, then the dbeta columns) in one launch of 32-column
+// strips.  Block s owns columns 32s .. 32s + 31 of every partial row: thread
+// t adds 16-byte vectors at columns 32s + 4(t % 8) of rows k = t / 8,
+// k + 32, ... (a row segment is one whole 128-byte line; the block's loads
+// are all in flight together), then the 32 row groups are combined through
+// LDS in a fixed order, so the result is deterministic.  (Strips of 16 and
+// 64 columns were measured slower at 1024 x 1024.)
+__global__ __launch_bounds__(256) void ln_part_strip_kernel(const float* __restrict__ part, float* __restrict__ dgamma,
+                                                            float* __restrict__ dbeta, int K, int W, int cols,
+                                                            int vec) {
+    constexpr int kQuads = 8, kGroups = 32;
+    __shared__ float red[kGroups][4 * kQuads + 1];
+    const int q = threadIdx.x % kQuads, kg = threadIdx.x / kQuads;
+    const int j = blockIdx.x * 4 * kQuads + 4 * q;
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (vec && j + 4 <= W) {
+#pragma unroll 8
+        for (int k = kg; k < K; k += kGroups) {
+            const float4 v = *reinterpret_cast<const float4*>(part + (int64_t)k * W + j);
+            a[0] += v.x; a[1] += v.y; a[2] += v.z; a[3] += v.w;
+        }
+    } else {
+        for (int k = kg; k < K; k += kGroups)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (j + e < W) a[e] += part[(int64_t)k * W + j + e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[kg][4 * q + e] = a[e];
+    __syncthreads();
+    if (threadIdx.x < 4 * kQuads) {
+        const int c = threadIdx.x, jj = blockIdx.x * 4 * kQuads + c;
+        float t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t[i] = (red[4 * i][c] + red[4 * i + 1][c]) + (red[4 * i + 2][c] + red[4 * i + 3][c]);
+        const float v = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+        if (jj < W) {
+            if (jj < cols) dgamma[jj] = v;
+            else dbeta[jj - cols] = v;
         }
     }
 }
@@ -356,31 +398,35 @@ tf_status tf_layernorm_bwd(tf_ctx* ctx, const float* dy, const float* x, const f
         return tf_hip_fill_f32(ctx, dbeta, 0.0f, cols);
     }
     const int nc = chunks_for(cols);
+    const bool vec = row_vec(x, cols) && row_vec(dy, cols) && row_vec(dx, cols);
     if (nc > 0) {
-        // 128 .. 256 blocks of 8 waves (4 for rows over 1024 columns, whose
-        // registers need the whole file), >= 1 row per wave.
-        const int waves = nc <= 4 ? 8 : 4;
-        const int64_t target = std::min<int64_t>(256, std::max<int64_t>(128, rows / (4 * waves)));
-        int64_t rpb = std::max<int64_t>(waves, (rows + target - 1) / target);
-        int64_t nblocks = (rows + rpb - 1) / rpb;
+        // Blocks of 4 waves, >= 1 row per wave, >= 256 blocks when the rows
+        // allow (1024 rows: 256 blocks of one row per wave, every CU busy;
+        // blocks of 8 waves left half of them idle).
+        constexpr int waves = 4;
+        const int64_t rpb = std::max<int64_t>(waves, (rows + 255) / 256);
+        const int64_t nblocks = (rows + rpb - 1) / rpb;
         tf_status st = tfh::ensure_workspace(ctx, (size_t)nblocks * 2 * cols * sizeof(float));
         if (st != TF_OK) return st;
         float* part = reinterpret_cast<float*>(ctx->ws);
-        const int vec = row_vec(x, cols) && row_vec(dy, cols) && row_vec(dx, cols);
         const dim3 grid((unsigned)nblocks);
-#define TF_LN_BWD(NC, W) ln_bwd_fused_kernel<NC, W><<<grid, W * 64, 0, ctx->stream>>>(dy, x, gamma, mean, rstd, dx, \
-                                                     part, (int)rows, (int)cols, (int)rpb, vec)
+#define TF_LN_BWD(NC) ln_bwd_fused_kernel<NC, waves><<<grid, waves * 64, 0, ctx->stream>>>(dy, x, gamma, mean, rstd, \
+                                                     dx, part, (int)rows, (int)cols, (int)rpb, vec)
         switch (nc) {
-        case 1: TF_LN_BWD(1, 8); break;
-        case 2: TF_LN_BWD(2, 8); break;
-        case 4: TF_LN_BWD(4, 8); break;
-        default: TF_LN_BWD(kMaxCached, 4); break;
+        case 1: TF_LN_BWD(1); break;
+        case 2: TF_LN_BWD(2); break;
+        case 4: TF_LN_BWD(4); break;
+        default: TF_LN_BWD(kMaxCached); break;
         }
 #undef TF_LN_BWD
         st = tfh::check_launch("ln_bwd_fused_kernel");
         if (st != TF_OK) return st;
-        // part is [nblocks][dgamma cols | dbeta cols]: one [K][2 cols] reduction.
-        return tfh::partial_rows_sum(ctx, part, dgamma, dbeta, nblocks, 2 * cols, cols);
+        // part is [nblocks][dgamma cols | dbeta cols]: column sums of a
+        // [nblocks][2 cols] matrix, split into the two outputs.
+        const int64_t W = 2 * cols;
+        ln_part_strip_kernel<<<(unsigned)((W + 31) / 32), 256, 0, ctx->stream>>>(part, dgamma, dbeta, (int)nblocks,
+                                                                               (int)W, (int)cols, W % 4 == 0);
+        return tfh::check_launch("ln_part_strip_kernel");
     }
     ln_bwd_dx_stream_kernel<<<row_grid(rows), 256, 0, ctx->stream>>>(dy, x, gamma, mean, rstd, dx, (int)rows, (int)cols);
     tf_status st = tfh::check_launch("ln_bwd_dx_stream_kernel");

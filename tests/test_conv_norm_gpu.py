@@ -18,11 +18,15 @@ def _ops():
     return ops
 
 
-# Backward paths: rows cached in registers with column partials (up to 2048
-# columns, incl. partly filled row chunks: 520, 264, 1536, 1001, 1) and
-# streamed wide rows (3000).
+# Backward paths: one launch with per-block column strips (16-byte rows of
+# up to 2048 columns: 1024, 64 x 1000 with a partly filled last strip,
+# 2048 x 1024 with two rows per wave, 96 x 256 and 1024 x 4 with strips past
+# the last column, 256 x 2048, grids of 8k blocks and not); rows cached in
+# registers with column partials (odd widths, few rows: 1001, 1, 520, 264,
+# 40 x 2048); streamed wide rows (3000).
 @pytest.mark.parametrize("R,Cc", [(1024, 1024), (64, 128), (7, 3000), (33, 1001), (1, 1), (300, 2048), (4096, 1024),
-                                  (2, 520), (5, 264), (1000, 1536)])
+                                  (2, 520), (5, 264), (1000, 1536), (64, 1000), (2048, 1024), (96, 256), (1024, 4),
+                                  (40, 2048), (256, 2048), (12, 1024)])
 def test_layernorm_fwd_bwd(ctx, R, Cc):
     ops = _ops()
     x = synth.normal(201 + Cc, (R, Cc))
