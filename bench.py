@@ -123,11 +123,20 @@ def _rotating_bench(ctx, n_sets, launch, reps=60):
     return e0.elapsed_ms(e1) / reps
 
 
-def bench_c3():
+def _bw_entry(label: str, ms: float) -> dict:
+    from tensors_amd.profiling import BW_KERNELS
+    algo = BW_KERNELS[label][1]
+    return {"us": round(ms * 1e3, 2), "bytes": algo, "gbps": round(algo / ms / 1e6, 1),
+            "frac_hbm": round(algo / ms / 1e6 / PEAK_HBM_GBPS, 3)}
+
+
+def bench_c3(more: bool = True, reps: int = 60):
     """Config 3 bandwidth kernels: fused LogSoftmax+NLL backward [4096 x 1024],
-    ReLU backward [4096 x 1024], LayerNorm backward [1024 x 1024]."""
+    ReLU backward [4096 x 1024], LayerNorm backward [1024 x 1024]; with
+    `more`, the other backward kernels of the path at C3b's shape."""
     import tensors_amd as ta
     from tensors_amd import ops, synth
+    from tensors_amd.profiling import LN_OP_BYTES
 
     ctx = ta.Context(0)
     out = {}
@@ -140,29 +149,26 @@ def bench_c3():
     for i in range(sets):
         ops.ce_fwd(logits[i], tg, loss, lse[i])
     dl = [ctx.empty((R, Cc)) for _ in range(sets)]
-    ms = _rotating_bench(ctx, sets, lambda i: ops.ce_bwd(logits[i], tg, dl[i], lse=lse[i]))
-    algo = R * Cc * 4 * 2 + R * 8
-    out["c3a_logsoftmax_nll_bwd"] = {"us": round(ms * 1e3, 2), "bytes": algo, "gbps": round(algo / ms / 1e6, 1),
-                                     "frac_hbm": round(algo / ms / 1e6 / PEAK_HBM_GBPS, 3)}
-    ms = _rotating_bench(ctx, sets, lambda i: ops.ce_fwd_bwd(logits[i], tg, loss, dl[i]))
-    out["c3a_ce_fused_fwd_bwd"] = {"us": round(ms * 1e3, 2), "bytes": algo, "gbps": round(algo / ms / 1e6, 1)}
+    ms = _rotating_bench(ctx, sets, lambda i: ops.ce_bwd(logits[i], tg, dl[i], lse=lse[i]), reps)
+    out["c3a_logsoftmax_nll_bwd"] = _bw_entry("ce_bwd_c3a", ms)
+    ms = _rotating_bench(ctx, sets, lambda i: ops.ce_fwd_bwd(logits[i], tg, loss, dl[i]), reps)
+    out["c3a_ce_fused_fwd_bwd"] = _bw_entry("ce_fused_fwd_bwd_c3a", ms)
     del logits, dl, lse
     sets = 6
     xs = [ctx.array(synth.normal(synth.seed(3, 2) + i, (R, Cc))) for i in range(sets)]
     dys = [ctx.array(synth.normal(synth.seed(3, 3) + i, (R, Cc))) for i in range(sets)]
     dxs = [ctx.empty((R, Cc)) for _ in range(sets)]
-    ms = _rotating_bench(ctx, sets, lambda i: ops.relu_bwd(dys[i], xs[i], dxs[i]))
-    algo = R * Cc * 4 * 3
-    out["c3b_relu_bwd"] = {"us": round(ms * 1e3, 2), "bytes": algo, "gbps": round(algo / ms / 1e6, 1),
-                           "frac_hbm": round(algo / ms / 1e6 / PEAK_HBM_GBPS, 3)}
+    ms = _rotating_bench(ctx, sets, lambda i: ops.relu_bwd(dys[i], xs[i], dxs[i]), reps)
+    out["c3b_relu_bwd"] = _bw_entry("relu_bwd_c3b", ms)
     # The other backward kernels of the path at the same shape (two reads and
     # one write of 16 MB each); the values do not affect their speed.
+    algo = R * Cc * 4 * 3
     for name, fn in (("sigmoid_bwd", lambda i: ops.sigmoid_bwd(dys[i], xs[i], dxs[i])),
                      ("tanh_bwd", lambda i: ops.tanh_bwd(dys[i], xs[i], dxs[i])),
                      ("softmax_bwd", lambda i: ops.softmax_bwd(xs[i], dys[i], dxs[i])),
                      ("mul", lambda i: ops.mul(dys[i], xs[i], dxs[i])),
-                     ("add", lambda i: ops.add(dys[i], xs[i], dxs[i]))):
-        ms = _rotating_bench(ctx, sets, fn)
+                     ("add", lambda i: ops.add(dys[i], xs[i], dxs[i]))) if more else ():
+        ms = _rotating_bench(ctx, sets, fn, reps)
         out[f"c3_more_{name}"] = {"us": round(ms * 1e3, 2), "bytes": algo, "gbps": round(algo / ms / 1e6, 1),
                                   "frac_hbm": round(algo / ms / 1e6 / PEAK_HBM_GBPS, 3)}
     del xs, dys, dxs
@@ -179,12 +185,93 @@ def bench_c3():
         ops.layernorm_fwd(xs[i], g, beta, ys, means[i], rstds[i])
     dxs = [ctx.empty((R, Cc)) for _ in range(sets)]
     dg, db = ctx.empty((Cc,)), ctx.empty((Cc,))
-    ms = _rotating_bench(ctx, sets, lambda i: ops.layernorm_bwd(dys[i], xs[i], g, means[i], rstds[i], dxs[i], dg, db))
-    algo = R * Cc * 4 * 3 + Cc * 4 * 3 + R * 8
-    out["c3c_layernorm_bwd"] = {"us": round(ms * 1e3, 2), "bytes": algo, "gbps": round(algo / ms / 1e6, 1),
-                                "frac_hbm": round(algo / ms / 1e6 / PEAK_HBM_GBPS, 3)}
+    ms = _rotating_bench(ctx, sets, lambda i: ops.layernorm_bwd(dys[i], xs[i], g, means[i], rstds[i], dxs[i], dg, db),
+                         reps)
+    out["c3c_layernorm_bwd"] = {"us": round(ms * 1e3, 2), "bytes": LN_OP_BYTES,
+                                "gbps": round(LN_OP_BYTES / ms / 1e6, 1),
+                                "frac_hbm": round(LN_OP_BYTES / ms / 1e6 / PEAK_HBM_GBPS, 3)}
     ctx.close()
     return out
+
+
+def bench_bandwidth_rotated(reps: int = 60):
+    """The other bandwidth kernels of the path at their configurations'
+    shapes, each launch on a buffer set not touched since the cache last held
+    it (sets together > 256 MB): C2's bias column sum and SGD-momentum step
+    (W and b in one launch), C5's SGD step over its 138 M parameters with the
+    bf16 copies, C4 conv2's im2col and col2im (N 128, C 32, 32 x 32, k 3,
+    stride 2, pad 1)."""
+    import tensors_amd as ta
+    from tensors_amd import ops, synth
+    from tensors_amd.profiling import CONV2
+
+    ctx = ta.Context(0)
+    out = {}
+    sets = 20                                         # 20 x 16 MB
+    dys = [ctx.array(synth.normal(synth.seed(6, 0) + i, (N2, N2))) for i in range(sets)]
+    db = ctx.empty((N2,))
+    out["colsum_c2"] = _bw_entry("colsum_c2", _rotating_bench(ctx, sets, lambda i: ops.colsum(dys[i], db), reps))
+    del dys
+    sets = 6                                          # 6 x 3 x 16 MB
+    Ws = [ctx.array(synth.normal(synth.seed(6, 1) + i, (N2, N2))) for i in range(sets)]
+    bs = [ctx.zeros((N2,)) for _ in range(sets)]
+    dWs = [ctx.array(synth.normal(synth.seed(6, 2) + i, (N2, N2), std=1e-3)) for i in range(sets)]
+    dbs = [ctx.zeros((N2,)) for _ in range(sets)]
+    vWs, vbs = [ctx.zeros((N2, N2)) for _ in range(sets)], [ctx.zeros((N2,)) for _ in range(sets)]
+    out["sgd_c2"] = _bw_entry("sgd_c2", _rotating_bench(
+        ctx, sets, lambda i: ops.sgd_momentum_multi([Ws[i], bs[i]], [dWs[i], dbs[i]], [vWs[i], vbs[i]], 1e-3, 0.9),
+        reps))
+    del Ws, bs, dWs, dbs, vWs, vbs
+    # C5: one set of 1.9 GB, far past the cache.
+    shapes = [s for i in range(4) for s in ((C5_DIMS[i + 1], C5_DIMS[i]), (C5_DIMS[i + 1],))]
+    ps = [ctx.zeros(s) for s in shapes]
+    gs = [ctx.zeros(s) for s in shapes]
+    vs = [ctx.zeros(s) for s in shapes]
+    sh = [ctx.empty(s, ta.BF16) for s in shapes]
+    out["sgd_c5"] = _bw_entry("sgd_c5", _rotating_bench(
+        ctx, 1, lambda i: ops.sgd_momentum_multi(ps, gs, vs, 1e-2, 0.9, sh), max(3, reps // 6)))
+    del ps, gs, vs, sh
+    N, C, H, W, k, oh = CONV2
+    sets = 6                                          # 6 x (16.8 + 37.7) MB
+    xs = [ctx.array(synth.normal(synth.seed(6, 3) + i, (N, C, H, W))) for i in range(sets)]
+    cols = [ctx.empty((N, C * k * k, oh * oh)) for _ in range(sets)]
+    out["im2col_conv2_c4"] = _bw_entry("im2col_conv2_c4", _rotating_bench(
+        ctx, sets, lambda i: ops.im2col(xs[i], cols[i], k, k, (2, 2), (1, 1)), reps))
+    out["col2im_conv2_c4"] = _bw_entry("col2im_conv2_c4", _rotating_bench(
+        ctx, sets, lambda i: ops.col2im(cols[i], xs[i], k, k, (2, 2), (1, 1)), reps))
+    ctx.close()
+    return out
+
+
+HBM_PROBE_MB = (4, 16, 64, 256, 512)
+HBM_PROBE_KINDS = ("copy (1R+1W)", "2R+1W", "3R+2W (SGD mix)", "read only (1R)")
+
+
+def hbm_ceiling() -> dict:
+    """Streaming rate of plain copy / 2R+1W / 3R+2W / read-only kernels (the
+    elementwise kernels' loop and grid, libtf_hbm_probe.so) over arrays of 4
+    to 512 MB, buffers rotated past the 256 MB cache, cached and
+    non-temporal."""
+    import ctypes as C
+    lib = C.CDLL(str(ROOT / "tensors_amd" / "lib" / "libtf_hbm_probe.so"))
+    lib.tf_hbm_probe.argtypes = [C.c_int, C.c_int, C.c_int64, C.c_int, C.POINTER(C.c_double)]
+    lib.tf_hbm_probe.restype = C.c_int
+    lib.tf_hbm_probe_bytes.argtypes = [C.c_int, C.c_int64]
+    lib.tf_hbm_probe_bytes.restype = C.c_int64
+    rows = []
+    for kind, kname in enumerate(HBM_PROBE_KINDS):
+        for nt in (0, 1):
+            for mb in HBM_PROBE_MB:
+                us = C.c_double()
+                rc = lib.tf_hbm_probe(kind, nt, mb << 20, max(10, 2048 // mb), C.byref(us))
+                if rc != 0:
+                    raise RuntimeError(f"tf_hbm_probe({kind}, {nt}, {mb} MB) failed: {rc}")
+                moved = lib.tf_hbm_probe_bytes(kind, mb << 20)
+                rows.append({"mix": kname, "nt": bool(nt), "mb_per_array": mb, "us": round(us.value, 2),
+                             "bytes": moved, "gbps": round(moved / us.value / 1e3, 1)})
+                print(f"hbm ceiling: {kname} nt={nt} {mb} MB: {us.value:.2f} us, "
+                      f"{moved / us.value / 1e3:.0f} GB/s", flush=True)
+    return {"rows": rows}
 
 
 def bench_api_steps():
@@ -461,6 +548,27 @@ def probe_c5(steps: int = 3) -> None:
     print(f"probe: {steps} x the C5 step's GEMMs, 3 calibration launches", flush=True)
 
 
+def probe_bw() -> None:
+    """Launches for rocprofv3 runs: every bandwidth kernel of the path at its
+    configuration's shape (bench_c3 without the extra kernels, then
+    bench_bandwidth_rotated), 20 timed launches each over rotated buffers,
+    then the calibration launches.  Prints the event timings (us per launch,
+    keyed by the labels of tensors_amd.profiling.BW_KERNELS) as one JSON
+    line; run unprofiled, they are the figures a --kernel-trace run of the
+    same command is set beside."""
+    c3 = bench_c3(more=False, reps=20)
+    out = {"ce_bwd_c3a": c3["c3a_logsoftmax_nll_bwd"]["us"],
+           "ce_fused_fwd_bwd_c3a": c3["c3a_ce_fused_fwd_bwd"]["us"],
+           "relu_bwd_c3b": c3["c3b_relu_bwd"]["us"],
+           "layernorm_bwd_op_c3c": c3["c3c_layernorm_bwd"]["us"]}
+    out.update({k: v["us"] for k, v in bench_bandwidth_rotated(reps=20).items()})
+    import tensors_amd as ta
+    ctx = ta.Context(0)
+    _probe_calibration(ctx)
+    ctx.close()
+    print(json.dumps({"bw_events_us": out}), flush=True)
+
+
 def c2_report(steps: int, warmup: int) -> dict:
     ms_step, mean, per = bench_c2(steps, warmup)
     bwd_ms = 0.5 * (mean["bwd_gemm_dx"] + mean["bwd_gemm_dw"])
@@ -502,10 +610,16 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--only-headline", action="store_true", help="skip the other configurations' measurements")
-    ap.add_argument("--probe", choices=["c2", "c5"], help="launch a config's kernels for a profiler, then exit")
+    ap.add_argument("--probe", choices=["c2", "c5", "bw"],
+                    help="launch a config's kernels (bw: the bandwidth kernels) for a profiler, then exit")
+    ap.add_argument("--hbm-ceiling", action="store_true",
+                    help="run the HBM streaming-ceiling microbenchmark, print its JSON line, then exit")
     args = ap.parse_args(argv)
     if args.probe:
-        (probe_c2 if args.probe == "c2" else probe_c5)()
+        {"c2": probe_c2, "c5": probe_c5, "bw": probe_bw}[args.probe]()
+        return 0
+    if args.hbm_ceiling:
+        print(json.dumps({"hbm_ceiling": hbm_ceiling()}), flush=True)
         return 0
 
     if args.gpus != 1:
@@ -553,7 +667,8 @@ def main(argv=None):
         "losses_finite": c5["losses_finite"],
     }
     if not args.only_headline:
-        line["other_configs"] = {"c2": c2_report(100, 50), "c3": bench_c3(), **bench_api_steps()}
+        line["other_configs"] = {"c2": c2_report(100, 50), "c3": bench_c3(),
+                                 "bandwidth_rotated": bench_bandwidth_rotated(), **bench_api_steps()}
     if rank == 0 and not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_c5()
         if "other_configs" in line:

@@ -10,7 +10,10 @@ import os
 from pathlib import Path
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
-HIP_LIB_PATH = LIB_DIR / "libtf_hip.so"
+# TF_HIP_LIBRARY names another build of the same library (a kernel-variant
+# build made by ``python -m tensors_amd.build --variant``, for A/B
+# measurements); the default is the in-tree build.
+HIP_LIB_PATH = Path(os.environ["TF_HIP_LIBRARY"]) if os.environ.get("TF_HIP_LIBRARY") else LIB_DIR / "libtf_hip.so"
 
 TF_OK, TF_ERR_INVALID, TF_ERR_HIP, TF_ERR_UNSUPPORTED, TF_ERR_OOM = range(5)
 TF_F32, TF_F16, TF_BF16, TF_I32, TF_I64, TF_BOOL = range(6)

@@ -2,6 +2,9 @@
 
 * ``tensors_amd/lib/libtf_hip.so`` — the HIP kernels and the C ABI declared in
   ``include/tf_hip.h``, compiled for gfx950 only with ``hipcc``.
+* ``tensors_amd/lib/libtf_hbm_probe.so`` — the HBM streaming-ceiling
+  microbenchmark (``csrc/probe/hbm_ceiling.hip``), used by ``bench.py
+  --hbm-ceiling``.
 * ``tensors_amd/lib/libtensorforge.so`` — the C++20 tensorforge API
   (Tensor / autograd Engine / nn / optim) that dispatches device tensors to
   libtf_hip.so; compiled with ``g++`` (no HIP headers involved).
@@ -53,18 +56,24 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build step failed: {cmd[0]} ... {cmd[-1]}")
 
 
-def build_hip(jobs: int = 8) -> Path:
-    BUILD.mkdir(exist_ok=True)
+def build_hip(jobs: int = 8, defines: tuple[str, ...] = (), out: Path | None = None,
+              build_dir: Path = BUILD) -> Path:
+    build_dir.mkdir(parents=True, exist_ok=True)
     LIB.mkdir(exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip"))
-    objs = [BUILD / (s.stem + ".hip.o") for s in srcs]
+    objs = [build_dir / (s.stem + ".hip.o") for s in srcs]
+    dflags = [f"-D{d}" for d in defines]
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        futs = [ex.submit(_run, [HIPCC, *HIP_FLAGS, "-c", str(s), "-o", str(o)]) for s, o in zip(srcs, objs)]
+        futs = [ex.submit(_run, [HIPCC, *HIP_FLAGS, *dflags, "-c", str(s), "-o", str(o)]) for s, o in zip(srcs, objs)]
         for f in futs:
             f.result()
-    out = LIB / "libtf_hip.so"
-    tmp = LIB / "libtf_hip.so.tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    out = out or LIB / "libtf_hip.so"
+    out.parent.mkdir(parents=True, exist_ok=True)
+    tmp = out.with_name(out.name + ".tmp")
+    # Every build is named libtf_hip.so to the loader, so a variant loaded
+    # first (TF_HIP_LIBRARY) also serves libtensorforge.so's dependency.
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-soname,libtf_hip.so", "-o", str(tmp),
+          *map(str, objs)])
     os.replace(tmp, out)
     return out
 
@@ -88,11 +97,41 @@ def build_cpp(jobs: int = 8) -> Path | None:
     return out
 
 
+def build_probe() -> Path:
+    """libtf_hbm_probe.so: the HBM streaming-ceiling microbenchmark
+    (csrc/probe/), a measuring instrument kept out of libtf_hip.so."""
+    LIB.mkdir(exist_ok=True)
+    out = LIB / "libtf_hbm_probe.so"
+    tmp = LIB / "libtf_hbm_probe.so.tmp"
+    _run([HIPCC, *HIP_FLAGS, "-shared", "-o", str(tmp), str(CSRC / "probe" / "hbm_ceiling.hip")])
+    os.replace(tmp, out)
+    return out
+
+
 def build(jobs: int = 8) -> None:
-    build_hip(jobs)
+    with cf.ThreadPoolExecutor(max_workers=2) as ex:
+        probe = ex.submit(build_probe)
+        build_hip(jobs)
+        probe.result()
     build_cpp(jobs)
 
 
+def build_variant(define: str) -> Path:
+    """A kernel-variant build of libtf_hip.so with one extra -D (e.g.
+    TF_BF16_KERNEL=1), at lib/variants/libtf_hip_<NAME>_<VALUE>.so; load it
+    with TF_HIP_LIBRARY=<that path>."""
+    tag = define.replace("=", "_").lower()
+    return build_hip(defines=(define,), out=LIB / "variants" / f"libtf_hip_{tag}.so",
+                     build_dir=BUILD / f"variant_{tag}")
+
+
 if __name__ == "__main__":
-    build()
-    print("built:", *sorted(p.name for p in LIB.glob("*.so")))
+    import argparse
+    ap = argparse.ArgumentParser(prog="python -m tensors_amd.build")
+    ap.add_argument("--variant", help="build only a kernel-variant libtf_hip.so with this -D (NAME=VALUE)")
+    a = ap.parse_args()
+    if a.variant:
+        print("built:", build_variant(a.variant))
+    else:
+        build()
+        print("built:", *sorted(p.name for p in LIB.glob("*.so")))

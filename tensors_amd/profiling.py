@@ -4,8 +4,9 @@
     python -m tensors_amd.profiling stats <dir>/run_kernel_stats.csv --title "..." --cmd "..."
 
     # per-launch HBM traffic from two --pmc runs (FETCH_SIZE, then WRITE_SIZE)
-    # of ``bench.py --probe c2`` (or ``--probe c5`` with ``--config c5``),
-    # calibrated against the probe's copy kernel
+    # of ``bench.py --probe c2`` (or ``--probe c5`` with ``--config c5``, or
+    # ``--probe bw`` with ``--config bw``: the bandwidth kernels),
+    # calibrated against the probe's tf_add kernel
     python -m tensors_amd.profiling traffic --fetch <dir>/run_counter_collection.csv \
         --write <dir>/run_counter_collection.csv --json profiles/<name>.json --cmd "..."
 
@@ -30,7 +31,65 @@ C2_KERNELS = {
     "gemm_f32_bwd_dx_c2": ("gemm_f32_dl_kernel<true, false>", 4 * 3 * N2 * N2),
     "gemm_f32_bwd_dw_c2": ("gemm_f32_dl_kernel<false, false>", 4 * 3 * N2 * N2),
 }
-CAL_NAME = "binary_kernel"
+CAL_NAME = "binary_kernel<float, AddOp>"
+
+C5_DIMS = [4096, 8192, 8192, 4096, 1000]
+C5_B = 4096
+C5_PARAMS = sum(C5_DIMS[i + 1] * C5_DIMS[i] + C5_DIMS[i + 1] for i in range(4))   # 138,286,056
+
+# The path's bandwidth kernels at their configurations' shapes (launched by
+# ``bench.py --probe bw``): label -> (kernel-name substring, algorithmic
+# bytes per launch).  Algorithmic bytes count each operand once: what a
+# launch must read and write, not what its caches re-fetch.
+R3, C3 = 4096, 1024                  # C3a / C3b: [4096 x 1024] fp32
+L3 = 1024                            # C3c: LayerNorm [1024 x 1024]
+LN_ROW_BLOCKS = 256                  # row blocks at 1024 rows; each writes 2 x 1024 partial sums
+CONV2 = (128, 32, 32, 32, 3, 16)     # C4 conv2: N, C, H, W, k, output side (stride 2, pad 1)
+_conv_x = CONV2[0] * CONV2[1] * CONV2[2] * CONV2[3] * 4
+_conv_col = CONV2[0] * CONV2[1] * CONV2[4] ** 2 * CONV2[5] ** 2 * 4
+BW_KERNELS = {
+    # logits read, dlogits written, int64 targets and the saved logsumexp read
+    "ce_bwd_c3a": ("ce_kernel<4, 1>", 2 * R3 * C3 * 4 + R3 * 8 + R3 * 4),
+    # one pass: logits and targets read, dlogits and the per-row nll written
+    "ce_fused_fwd_bwd_c3a": ("ce_kernel<4, 2>", 2 * R3 * C3 * 4 + R3 * 8 + R3 * 4),
+    "relu_bwd_c3b": ("binary_kernel<float, ReluBwdOp>", 3 * R3 * C3 * 4),
+    # dy, x read, dx written; gamma, mean, rstd read; the block partials written
+    "layernorm_bwd_rows_c3c": ("ln_bwd_fused_kernel<4, 4>",
+                               3 * L3 * L3 * 4 + 3 * L3 * 4 + LN_ROW_BLOCKS * 2 * L3 * 4),
+    # the partials read, dgamma and dbeta written
+    "layernorm_bwd_partials_c3c": ("ln_part_strip_kernel", LN_ROW_BLOCKS * 2 * L3 * 4 + 2 * L3 * 4),
+    "colsum_c2": ("colsum_strip_kernel<float, 8>", N2 * N2 * 4 + N2 * 4),
+    # p, g, v read; p, v written (W and b in one launch)
+    "sgd_c2": ("sgd_multi_kernel<false>", 20 * (N2 * N2 + N2)),
+    # as above plus the bf16 copy of every parameter
+    "sgd_c5": ("sgd_multi_kernel<true>", 22 * C5_PARAMS),
+    "im2col_conv2_c4": ("im2col_plane_kernel<float>", _conv_x + _conv_col),
+    "col2im_conv2_c4": ("col2im_plane_kernel<float>", _conv_col + _conv_x),
+}
+# The streaming-ceiling row (bench.py --hbm-ceiling: mix, non-temporal,
+# MB per array) each kernel is read against: the mix of its reads and writes
+# at the nearest array size.
+BW_CEILING = {
+    "ce_bwd_c3a": ("copy (1R+1W)", True, 16),
+    "ce_fused_fwd_bwd_c3a": ("copy (1R+1W)", True, 16),
+    "relu_bwd_c3b": ("2R+1W", True, 16),
+    "layernorm_bwd_rows_c3c": ("2R+1W", True, 4),
+    "layernorm_bwd_partials_c3c": ("read only (1R)", True, 4),
+    "colsum_c2": ("read only (1R)", True, 16),
+    "sgd_c2": ("3R+2W (SGD mix)", False, 16),
+    "sgd_c5": ("3R+2W (SGD mix)", True, 512),
+    "im2col_conv2_c4": ("copy (1R+1W)", True, 16),
+    "col2im_conv2_c4": ("copy (1R+1W)", True, 16),
+}
+# The LayerNorm backward op as a whole (C3c): dy, x, dx, gamma, dgamma,
+# dbeta, mean, rstd -- the block partials are not part of it.
+LN_OP_BYTES = 3 * L3 * L3 * 4 + 3 * L3 * 4 + 2 * L3 * 4
+
+
+def _kname(name: str) -> str:
+    """Kernel name as the stats tables print it (no anonymous-namespace
+    qualifiers), which the label tables' substrings are written against."""
+    return name.replace("(anonymous namespace)::", "")
 
 
 def per_dispatch(path: str | Path, counter: str) -> dict[str, list[float]]:
@@ -42,7 +101,7 @@ def per_dispatch(path: str | Path, counter: str) -> dict[str, list[float]]:
             if r["Counter_Name"] != counter:
                 continue
             sums[(r["Dispatch_Id"], r["Counter_Name"])] += float(r["Counter_Value"])
-            names[r["Dispatch_Id"]] = r["Kernel_Name"]
+            names[r["Dispatch_Id"]] = _kname(r["Kernel_Name"])
     out: dict[str, list[float]] = defaultdict(list)
     for (disp, _), v in sums.items():
         out[names[disp]].append(v)
@@ -56,7 +115,10 @@ def _match(table: dict[str, list[float]], sub: str) -> list[float]:
     return vals
 
 
-def traffic(fetch_csv, write_csv, cal_n: int) -> dict:
+def traffic(fetch_csv, write_csv, cal_n: int, kernels: dict | None = None) -> dict:
+    """Calibrated HBM bytes per launch of each kernel in `kernels` (label ->
+    (name substring, algorithmic bytes)); C2's GEMMs by default."""
+    kernels = C2_KERNELS if kernels is None else kernels
     fetch = per_dispatch(fetch_csv, "FETCH_SIZE")
     write = per_dispatch(write_csv, "WRITE_SIZE")
     cal_read, cal_write = 2 * 4 * cal_n, 4 * cal_n
@@ -67,15 +129,22 @@ def traffic(fetch_csv, write_csv, cal_n: int) -> dict:
                            "known_write_bytes": cal_write, "measured_fetch_bytes": round(cal_f),
                            "measured_write_bytes": round(cal_w), "fetch_scale": round(f_scale, 4),
                            "write_scale": round(w_scale, 4)}}
-    for label, (sub, algo) in C2_KERNELS.items():
+    for label, (sub, algo) in kernels.items():
         fv, wv = _match(fetch, sub), _match(write, sub)
         fb = sum(fv) / len(fv) * 1024.0 * f_scale
         wb = sum(wv) / len(wv) * 1024.0 * w_scale
         res[label] = {"kernel": sub, "fetch_bytes": round(fb), "write_bytes": round(wb),
                       "traffic_bytes": round(fb + wb), "algorithmic_bytes": algo,
                       "traffic_over_algorithmic": round((fb + wb) / algo, 3), "dispatches": len(fv)}
-    bwd = [res["gemm_f32_bwd_dx_c2"], res["gemm_f32_bwd_dw_c2"]]
-    res["gemm_f32_bwd_c2"] = round(sum(r["traffic_bytes"] for r in bwd) / 2)  # bench.py roofline.traffic
+    if kernels is C2_KERNELS:
+        bwd = [res["gemm_f32_bwd_dx_c2"], res["gemm_f32_bwd_dw_c2"]]
+        res["gemm_f32_bwd_c2"] = round(sum(r["traffic_bytes"] for r in bwd) / 2)  # bench.py roofline.traffic
+    if "layernorm_bwd_rows_c3c" in res and "layernorm_bwd_partials_c3c" in res:
+        ln = [res["layernorm_bwd_rows_c3c"], res["layernorm_bwd_partials_c3c"]]
+        tb = sum(r["traffic_bytes"] for r in ln)
+        res["layernorm_bwd_op_c3c"] = {"kernels": "rows + partials", "traffic_bytes": tb,
+                                       "algorithmic_bytes": LN_OP_BYTES,
+                                       "traffic_over_algorithmic": round(tb / LN_OP_BYTES, 3)}
     return res
 
 
@@ -83,10 +152,6 @@ def traffic(fetch_csv, write_csv, cal_n: int) -> dict:
 # (kind, M, N, K, output bytes per element): forward L1..L4, then per layer
 # from the last: dW, dX (no dX for layer 1).  A split-K reduction dispatch
 # belongs to the GEMM launched right before it.
-C5_DIMS = [4096, 8192, 8192, 4096, 1000]
-C5_B = 4096
-
-
 def c5_gemm_order() -> list[tuple[str, int, int, int, int]]:
     d, B = C5_DIMS, C5_B
     seq = [("fwd", B, d[i + 1], d[i], 2) for i in range(4)]
@@ -108,7 +173,7 @@ def _ordered(path: str | Path, counter: str) -> list[tuple[str, float]]:
                 continue
             d = int(r["Dispatch_Id"])
             sums[d] += float(r["Counter_Value"])
-            names[d] = r["Kernel_Name"]
+            names[d] = _kname(r["Kernel_Name"])
     return [(names[d], sums[d]) for d in sorted(sums)]
 
 
@@ -160,6 +225,59 @@ def traffic_c5(fetch_csv, write_csv, cal_n: int) -> dict:
     n_bwd = sum(r["launches_per_step"] for r in bwd)
     res["gemm_bf16_bwd_c5"] = round(sum(r["traffic_bytes_per_step"] for r in bwd) / n_bwd)  # bench roofline.traffic
     return res
+
+
+def _gemm_positions(rows: list[tuple[str, float]]) -> list[list[float]]:
+    """Values of the GEMM dispatches of ``bench.py --probe c5`` grouped by
+    position in c5_gemm_order (one entry per step)."""
+    order = c5_gemm_order()
+    vals = [v for n, v in rows if "gemm_" in n]
+    if len(vals) % len(order):
+        raise SystemExit(f"{len(vals)} GEMM dispatches is not a whole number of C5 steps")
+    return [[vals[i] for i in range(pos, len(vals), len(order))] for pos in range(len(order))]
+
+
+def _trace_ordered(trace_csv: str | Path) -> list[tuple[str, float]]:
+    rows = []
+    with open(trace_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), _kname(r["Kernel_Name"]),
+                         (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    rows.sort()
+    return [(n, d) for _, n, d in rows]
+
+
+def mfma_table(runs: list[tuple[str, str, str]]) -> str:
+    """Per C5 GEMM shape: MFMA busy (the derived counter MfmaUtil: MFMA busy
+    cycles over GPU-active cycles x SIMDs) and kernel duration, for each run
+    (label, counter CSV of --pmc MfmaUtil, kernel_trace.csv), both of
+    ``bench.py --probe c5``."""
+    cols = []
+    for label, pmc, trace in runs:
+        util = _gemm_positions(_ordered(pmc, "MfmaUtil"))
+        dur = _gemm_positions(_trace_ordered(trace))
+        names = [n for n, _ in _trace_ordered(trace) if "gemm_" in n][:len(c5_gemm_order())]
+        cols.append((label, util, dur, names))
+    head = "| GEMM | M x N x K | " + " | ".join(
+        f"{lab}: kernel | {lab}: MFMA busy | {lab}: us | {lab}: TF/s" for lab, *_ in cols) + " |"
+    lines = [head, "|---|---|" + "---|---:|---:|---:|" * len(cols)]
+    tot = [[0.0, 0.0, 0.0] for _ in cols]        # bwd: flop, us, busy x us
+    for pos, (kind, M, N, K, _) in enumerate(c5_gemm_order()):
+        cells = []
+        for ci, (lab, util, dur, names) in enumerate(cols):
+            u = sum(util[pos]) / len(util[pos])
+            d = sum(dur[pos]) / len(dur[pos])
+            flop = 2.0 * M * N * K
+            k = names[pos].split("(")[0].replace("void ", "")
+            cells.append(f"`{k}` | {u:.1f} % | {d:.1f} | {flop / d / 1e6:.0f}")
+            if kind != "fwd":
+                tot[ci][0] += flop
+                tot[ci][1] += d
+                tot[ci][2] += u * d
+        lines.append(f"| {kind} | {M} x {N} x {K} | " + " | ".join(cells) + " |")
+    cells = [f"backward | {t[2] / t[1]:.1f} % (time-weighted) | {t[1]:.1f} | {t[0] / t[1] / 1e6:.0f}" for t in tot]
+    lines.append("| all dW + dX | | " + " | ".join(cells) + " |")
+    return "\n".join(lines)
 
 
 def c5_api_order() -> list[tuple[str, int, int, int]]:
@@ -268,6 +386,63 @@ def phase_table(trace_csv: str | Path, phases: list[tuple[str, int]], match: lis
     return "\n".join(lines)
 
 
+def _json_line(path: str | Path, key: str) -> dict:
+    for ln in Path(path).read_text().splitlines():
+        if ln.startswith("{") and f'"{key}"' in ln:
+            return json.loads(ln)[key]
+    raise SystemExit(f"no JSON line with {key!r} in {path}")
+
+
+def ceiling_table(ceiling_log: str | Path) -> str:
+    rows = _json_line(ceiling_log, "hbm_ceiling")["rows"]
+    sizes = sorted({r["mb_per_array"] for r in rows})
+    lines = ["| mix | loads/stores | " + " | ".join(f"{m} MB/array" for m in sizes) + " |",
+             "|---|---|" + "---:|" * len(sizes)]
+    for mix in dict.fromkeys(r["mix"] for r in rows):
+        for nt in (False, True):
+            cells = []
+            for m in sizes:
+                r = next((r for r in rows if r["mix"] == mix and r["nt"] == nt and r["mb_per_array"] == m), None)
+                cells.append(f"{r['gbps'] / 1e3:.2f} TB/s ({r['us']:.1f} us)" if r else "")
+            lines.append(f"| {mix} | {'non-temporal' if nt else 'cached'} | " + " | ".join(cells) + " |")
+    return "\n".join(lines)
+
+
+def bw_table(stats_csv: str | Path, traffic_json: str | Path, events_log: str | Path,
+             ceiling_log: str | Path) -> str:
+    """One row per bandwidth kernel: event-timed and rocprof durations,
+    algorithmic bytes and rate, the matching streaming ceiling, and the
+    counters' HBM bytes."""
+    stats = {_kname(r["Name"]): r for r in csv.DictReader(open(stats_csv, newline=""))}
+    traffic_res = json.loads(Path(traffic_json).read_text())
+    events = _json_line(events_log, "bw_events_us")
+    ceil = _json_line(ceiling_log, "hbm_ceiling")["rows"]
+    lines = ["| kernel | config shape | event us | rocprof avg us | algorithmic MB | GB/s (event) | of 8 TB/s | "
+             "ceiling (mix, us) | of ceiling | FETCH+WRITE MB | traffic / algorithmic |",
+             "|---|---|---:|---:|---:|---:|---:|---|---:|---:|---:|"]
+    for label, (sub, algo) in BW_KERNELS.items():
+        st = [r for n, r in stats.items() if sub in n]
+        avg = sum(float(r["TotalDurationNs"]) for r in st) / max(1, sum(int(r["Calls"]) for r in st)) / 1e3
+        ev = events.get(label)
+        t = traffic_res.get(label, {})
+        mix, nt, mb = BW_CEILING[label]
+        c = next((r for r in ceil if r["mix"] == mix and r["nt"] == nt and r["mb_per_array"] == mb), None)
+        us = ev if ev is not None else avg
+        gbps = algo / us / 1e3
+        cell_c = f"{mix}{' nt' if nt else ''} {mb} MB: {c['gbps'] / 1e3:.2f} TB/s" if c else "-"
+        of_c = f"{gbps / c['gbps']:.0%}" if c else "-"
+        lines.append(f"| `{sub}` | {label} | {ev if ev is not None else '-'} | {avg:.2f} | {algo / 1e6:.2f} | "
+                     f"{gbps:.0f} | {gbps / 8000:.0%} | {cell_c} | {of_c} | "
+                     f"{t.get('traffic_bytes', 0) / 1e6:.2f} | {t.get('traffic_over_algorithmic', '-')} |")
+    op = traffic_res.get("layernorm_bwd_op_c3c")
+    if op and "layernorm_bwd_op_c3c" in events:
+        us = events["layernorm_bwd_op_c3c"]
+        lines.append(f"| rows + partials | layernorm_bwd_op_c3c | {us} | - | {op['algorithmic_bytes'] / 1e6:.2f} | "
+                     f"{op['algorithmic_bytes'] / us / 1e3:.0f} | {op['algorithmic_bytes'] / us / 8e6:.0%} | - | - | "
+                     f"{op['traffic_bytes'] / 1e6:.2f} | {op['traffic_over_algorithmic']} |")
+    return "\n".join(lines)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(prog="python -m tensors_amd.profiling")
     sub = ap.add_subparsers(dest="action", required=True)
@@ -286,10 +461,49 @@ def main(argv=None) -> int:
     t.add_argument("--fetch", required=True)
     t.add_argument("--write", required=True)
     t.add_argument("--cal-n", type=int, default=1 << 26)
-    t.add_argument("--config", choices=["c2", "c5"], default="c2")
+    t.add_argument("--config", choices=["c2", "c5", "bw"], default="c2")
     t.add_argument("--json", required=True)
     t.add_argument("--cmd", required=True, nargs="+", help="the two rocprofv3 commands")
+    b = sub.add_parser("bw-summary", help="markdown table of the bandwidth kernels (bench.py --probe bw)")
+    b.add_argument("--stats", required=True, help="kernel_stats.csv of a --kernel-trace --stats run of --probe bw")
+    b.add_argument("--traffic", required=True, help="the traffic JSON (--config bw)")
+    b.add_argument("--events", required=True, help="log of an unprofiled --probe bw run")
+    b.add_argument("--ceiling", required=True, help="log of bench.py --hbm-ceiling")
+    b.add_argument("--cmd", required=True, nargs="+", help="the commands that produced the inputs")
+    b.add_argument("--out", required=True)
+    c = sub.add_parser("ceiling-summary", help="markdown table of bench.py --hbm-ceiling")
+    c.add_argument("--ceiling", required=True)
+    c.add_argument("--stats", help="kernel_stats.csv of a --kernel-trace run of the same command")
+    c.add_argument("--cmd", required=True, nargs="+")
+    c.add_argument("--out", required=True)
+    m = sub.add_parser("mfma-summary", help="MFMA busy per config-5 GEMM shape (bench.py --probe c5)")
+    m.add_argument("--run", nargs=3, action="append", required=True, metavar=("LABEL", "PMC_CSV", "TRACE_CSV"))
+    m.add_argument("--cmd", required=True, nargs="+")
+    m.add_argument("--out", required=True)
     a = ap.parse_args(argv)
+    if a.action == "mfma-summary":
+        cmds = "\n".join(a.cmd)
+        text = (f"# MFMA busy per config-5 GEMM shape (bf16 in, fp32 accumulate; 3 steps of GEMMs, averaged)\n\n"
+                f"Commands (repo root):\n\n```\n{cmds}\n```\n\n{mfma_table(a.run)}\n")
+        Path(a.out).write_text(text)
+        sys.stdout.write(text)
+        return 0
+    if a.action == "bw-summary":
+        cmds = "\n".join(a.cmd)
+        text = (f"# Bandwidth kernels of the path at their configurations' shapes\n\nCommands (repo root):\n\n"
+                f"```\n{cmds}\n```\n\n{bw_table(a.stats, a.traffic, a.events, a.ceiling)}\n")
+        Path(a.out).write_text(text)
+        sys.stdout.write(text)
+        return 0
+    if a.action == "ceiling-summary":
+        cmds = "\n".join(a.cmd)
+        text = (f"# HBM streaming ceilings (one MI355X)\n\nCommands (repo root):\n\n```\n{cmds}\n```\n\n"
+                f"Event-timed, buffers rotated past the 256 MB last-level cache:\n\n{ceiling_table(a.ceiling)}\n")
+        if a.stats:
+            text += f"\nKernel trace of the same command:\n\n{stats_table(a.stats)}\n"
+        Path(a.out).write_text(text)
+        sys.stdout.write(text)
+        return 0
     if a.action == "stats":
         text = f"# {a.title}\n\nCommand (repo root):\n\n```\n{a.cmd}\n```\n\n{stats_table(a.csv)}\n"
         if a.trace and a.phases:
@@ -309,7 +523,10 @@ def main(argv=None) -> int:
         else:
             sys.stdout.write(text)
     else:
-        res = (traffic if a.config == "c2" else traffic_c5)(a.fetch, a.write, a.cal_n)
+        if a.config == "c5":
+            res = traffic_c5(a.fetch, a.write, a.cal_n)
+        else:
+            res = traffic(a.fetch, a.write, a.cal_n, BW_KERNELS if a.config == "bw" else None)
         res["commands"] = a.cmd
         Path(a.json).write_text(json.dumps(res, indent=2) + "\n")
         print(json.dumps(res, indent=2))

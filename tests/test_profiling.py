@@ -111,3 +111,104 @@ def test_traffic_c5_attributes_split_reductions_to_their_gemm(tmp_path):
     assert res["gemm_bf16_bwd_c5"] == round((dx["traffic_bytes_per_step"] + dw["traffic_bytes_per_step"]) / 7)
     # algorithmic bytes of the L2 dW (8192 x 8192 x 4096, bf16 in, fp32 out) are part of dW's total
     assert dw["algorithmic_bytes_per_step"] >= 2 * (8192 * 4096 * 2) + 4 * 8192 * 8192
+
+
+def test_bandwidth_traffic_matches_qualified_names_and_sums_the_layernorm_op(tmp_path):
+    # rocprofv3's counter CSV names kernels with their anonymous-namespace
+    # qualifiers; the label table's substrings are written without them.
+    n = 1 << 20
+    fetch, write = [], []
+    kernels = [("void (anonymous namespace)::binary_kernel<float, (anonymous namespace)::AddOp>(float const*)",
+                2 * 4 * n / 1024 / 2, 4 * n / 1024)]
+    for label, (sub, algo) in profiling.BW_KERNELS.items():
+        # every kernel's raw reading is exactly its algorithmic bytes once the
+        # fetch scale of 2 is applied (reads = all but the 1/4 that is written)
+        kernels.append((f"void (anonymous namespace)::{sub}(float const*)", algo * 0.75 / 1024 / 2,
+                        algo * 0.25 / 1024))
+    for d, (name, f_kib, w_kib) in enumerate(kernels, 1):
+        fetch.append({"Dispatch_Id": d, "Kernel_Name": name, "Counter_Name": "FETCH_SIZE", "Counter_Value": f_kib})
+        write.append({"Dispatch_Id": d, "Kernel_Name": name, "Counter_Name": "WRITE_SIZE", "Counter_Value": w_kib})
+    fp, wp = tmp_path / "f.csv", tmp_path / "w.csv"
+    _write_counters(fp, fetch)
+    _write_counters(wp, write)
+    res = profiling.traffic(fp, wp, n, profiling.BW_KERNELS)
+    for label, (_, algo) in profiling.BW_KERNELS.items():
+        assert abs(res[label]["traffic_over_algorithmic"] - 1.0) < 1e-3, label
+    assert "gemm_f32_bwd_c2" not in res
+    op = res["layernorm_bwd_op_c3c"]
+    assert op["algorithmic_bytes"] == profiling.LN_OP_BYTES == 12603392
+    rows, parts = res["layernorm_bwd_rows_c3c"], res["layernorm_bwd_partials_c3c"]
+    assert op["traffic_bytes"] == rows["traffic_bytes"] + parts["traffic_bytes"]
+    # the block partials' round trip is what the op moves beyond its operands
+    assert abs(op["traffic_bytes"] - op["algorithmic_bytes"] - 2 * profiling.LN_ROW_BLOCKS * 2 * 1024 * 4) < 64
+
+
+def test_ceiling_and_bandwidth_tables(tmp_path):
+    ceil = {"hbm_ceiling": {"rows": [
+        {"mix": m, "nt": nt, "mb_per_array": mb, "us": 10.0, "bytes": 40_000_000, "gbps": 4000.0}
+        for m in ("copy (1R+1W)", "2R+1W", "3R+2W (SGD mix)", "read only (1R)")
+        for nt in (False, True) for mb in (4, 16, 512)]}}
+    clog = tmp_path / "hbm.log"
+    clog.write_text("hbm ceiling: progress line\n" + json.dumps(ceil) + "\n")
+    table = profiling.ceiling_table(clog)
+    assert table.count("\n") == 1 + 8 and "4.00 TB/s (10.0 us)" in table
+    events = {label: 20.0 for label in profiling.BW_KERNELS}
+    events["layernorm_bwd_op_c3c"] = 10.0
+    elog = tmp_path / "ev.log"
+    elog.write_text(json.dumps({"bw_events_us": events}) + "\n")
+    stats = tmp_path / "s.csv"
+    with open(stats, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Name", "Calls", "TotalDurationNs"])
+        w.writeheader()
+        for label, (sub, _) in profiling.BW_KERNELS.items():
+            w.writerow({"Name": f"void (anonymous namespace)::{sub}(int)", "Calls": 4, "TotalDurationNs": 80000})
+    tj = tmp_path / "t.json"
+    tj.write_text(json.dumps({"layernorm_bwd_op_c3c": {"traffic_bytes": 17_000_000, "algorithmic_bytes": 12603392,
+                                                        "traffic_over_algorithmic": 1.349}}))
+    bw = profiling.bw_table(stats, tj, elog, clog)
+    lines = bw.splitlines()
+    assert len(lines) == 2 + len(profiling.BW_KERNELS) + 1
+    relu = next(ln for ln in lines if "relu_bwd_c3b" in ln)
+    # 50,331,648 B in 20 us = 2517 GB/s; 20 us rocprof average
+    assert "| 20.0 | 20.00 | 50.33 | 2517 |" in relu
+    assert "layernorm_bwd_op_c3c | 10.0 |" in lines[-1]
+
+
+def test_mfma_table_groups_dispatches_by_c5_position(tmp_path):
+    order = profiling.c5_gemm_order()
+    steps = 2
+    pmc, trace = [], []
+    t = 0
+    d = 0
+    for s in range(steps):
+        for pos, (kind, M, N, K, _) in enumerate(order):
+            d += 1
+            name = f"void (anonymous namespace)::gemm_bf16_pp_kernel<{kind}>(GemmParams)"
+            pmc.append({"Dispatch_Id": d, "Kernel_Name": name, "Counter_Name": "MfmaUtil",
+                        "Counter_Value": 50.0 + pos + 10 * s})
+            dur = 1000 * (pos + 1)              # ns
+            trace.append({"Kernel_Name": name, "Start_Timestamp": t, "End_Timestamp": t + dur})
+            t += dur + 100
+            if kind != "fwd":                   # a split-K reduction between GEMMs is skipped
+                d += 1
+                pmc.append({"Dispatch_Id": d, "Kernel_Name": "splitk_reduce_kernel(GemmParams, int)",
+                            "Counter_Name": "MfmaUtil", "Counter_Value": 0.0})
+                trace.append({"Kernel_Name": "splitk_reduce_kernel(GemmParams, int)", "Start_Timestamp": t,
+                              "End_Timestamp": t + 50})
+                t += 150
+    pp, tp = tmp_path / "p.csv", tmp_path / "t.csv"
+    _write_counters(pp, pmc)
+    with open(tp, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        trace.reverse()                         # rows out of time order are sorted
+        for r in trace:
+            w.writerow(r)
+    table = profiling.mfma_table([("pp", str(pp), str(tp))])
+    lines = table.splitlines()
+    assert len(lines) == 2 + len(order) + 1
+    first = lines[2]
+    # position 0: MfmaUtil 50 and 60 over the two steps -> 55 %, 1 us each
+    assert "| 55.0 % | 1.0 |" in first
+    M, N, K = order[0][1:4]
+    assert f"{M} x {N} x {K}" in first
