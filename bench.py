@@ -284,6 +284,11 @@ def bench_api_steps():
     _, _, ms = api.mlp_train([784, 256, 128, 10], xs, ys, steps=100, warmup=10, lr=0.1, mu=0.9, on_gpu=True,
                              reference_compat=True)
     out["c1_mlp_step_ms"] = round(ms, 4)
+    # The same loop with its step captured once in a HIP graph and replayed
+    # (batch selection and loss recording on the device).
+    _, _, ms = api.mlp_train([784, 256, 128, 10], xs, ys, steps=100, warmup=10, lr=0.1, mu=0.9, on_gpu=True,
+                             reference_compat=True, graph=1)
+    out["c1_mlp_step_ms_graph"] = round(ms, 4)
     xs = synth.normal(synth.seed(4, 0), (1, 128, 3, 32, 32))
     ys = synth.uniform_int(synth.seed(4, 1), (1, 128), 10)
     _, ms = api.cnn_train(xs, ys, steps=23, warmup=3, lr=0.01, mu=0.9, on_gpu=True)

@@ -127,6 +127,45 @@ tf_status tf_hip_event_record(tf_ctx* ctx, void* event);
 tf_status tf_hip_event_elapsed(void* start, void* end, float* ms);
 tf_status tf_hip_event_destroy(void* event);
 
+/* HIP-graph capture (no counterpart in the reference, which launches every
+ * kernel of a step from the host, examples/train_mlp.cpp:141-199).  For
+ * callers whose step is launch-bound: capture it once, then replay it with
+ * one tf_graph_launch per step.
+ *   tf_graph_begin  starts capturing the context's stream: every library call
+ *                   on the context until tf_graph_end is recorded, not run.
+ *                   While capturing, tf_hip_alloc serves only from blocks
+ *                   freed earlier in the capture or from the block cache (a
+ *                   miss is TF_ERR_INVALID: run the step once eagerly first,
+ *                   which fills the cache), the workspace may not grow, and
+ *                   tf_hip_sync, tf_hip_set_stream, tf_hip_trim and copies
+ *                   other than TF_COPY_D2D are errors.
+ *   tf_graph_end    ends the capture and instantiates the graph; after a
+ *                   failed call during capture it returns that error and no
+ *                   graph.  Blocks freed during capture belong to the graph
+ *                   until tf_graph_destroy (so no other allocation receives a
+ *                   replay's temporaries); blocks allocated during capture
+ *                   and still live must stay live while the graph is replayed.
+ *   tf_graph_launch enqueues one replay on the context's stream (the context
+ *                   must be the capturing one, its workspace unmoved).
+ *   tf_graph_destroy returns the graph's blocks to the context's cache;
+ *                   destroy graphs before tf_hip_shutdown of their context.
+ * Captured work contains no hipMemsetAsync (fills are kernels). */
+typedef struct tf_graph tf_graph;
+tf_status tf_graph_begin(tf_ctx* ctx);
+tf_status tf_graph_end(tf_ctx* ctx, tf_graph** out);
+tf_status tf_graph_launch(tf_ctx* ctx, tf_graph* graph);
+tf_status tf_graph_destroy(tf_graph* graph);
+/* Device-side step selection for a replayed step (no counterpart in the
+ * reference).  tf_gather_indexed: dst[0:bytes) = table[*counter % n][0:bytes),
+ * where table holds n device addresses (as uint64), each of a buffer of at
+ * least `bytes` bytes.  tf_record_step: ring[*counter] = *src when
+ * 0 <= *counter < ring_len, then *counter += 1.  Both read the counter on
+ * the device, so a captured step picks a new batch and records its loss on
+ * every replay. */
+tf_status tf_gather_indexed(tf_ctx* ctx, void* dst, const uint64_t* table, int64_t n, const int64_t* counter,
+                            int64_t bytes);
+tf_status tf_record_step(tf_ctx* ctx, const float* src, float* ring, int64_t ring_len, int64_t* counter);
+
 /* Launch timing, for measurement (no counterpart in the reference, whose
  * benchmarks time from outside).  tf_hip_timing_start creates `max_records`
  * event pairs and starts recording: from then on every GEMM call

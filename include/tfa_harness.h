@@ -36,11 +36,18 @@ const char* tfa_last_error(void);
  *                      host launch work included, device drained at both ends.
  *   pool_used          NULL or out [steps]: the device pool's bytes in use after each
  *                      step (the device drained first; GPU only, and then the steps
- *                      are not timed). */
+ *                      are not timed).
+ *   graph              0: every step launched from the host.  1: the warmup steps
+ *                      (>= 1) run eagerly, one step is captured in a HIP graph
+ *                      (tf_graph_*) and the remaining steps are replays of it, each
+ *                      picking its batch and recording its loss on the device.
+ *                      2: as 1, with the host waiting for every replay and reading
+ *                      its loss before the next (checked replays; not a timing mode).
+ *                      GPU only, without pool_used. */
 int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t steps, int64_t warmup,
                   int64_t n_batches, const float* xs, const int64_t* ys, float lr, float mu, int32_t on_gpu,
                   int32_t reference_compat, int32_t bf16, const float* init_weights, float* losses,
-                  float* final_weights, double* ms_per_step, uint64_t* pool_used);
+                  float* final_weights, double* ms_per_step, uint64_t* pool_used, int32_t graph);
 
 /* CNN training (the config-4 network): Conv2dModule(3,32,3,1,1) - ReLU -
  * Conv2dModule(32,64,3,2,1) - ReLU - flatten - Linear(64*(H/2)*(W/2), 10) -

@@ -96,6 +96,12 @@ SIGNATURES: dict[str, list] = {
     "tf_sgd_momentum": [_p, _p, _p, _p, _p, _i64, _f, _f],
     "tf_sgd_momentum_multi": [_p, _i, _p, _p, _p, _p, _p, _f, _f],
     "tf_cast_f32_bf16": [_p, _p, _p, _i64],
+    "tf_graph_begin": [_p],
+    "tf_graph_end": [_p, _p],
+    "tf_graph_launch": [_p, _p],
+    "tf_graph_destroy": [_p],
+    "tf_gather_indexed": [_p, _p, _p, _i64, _p, _i64],
+    "tf_record_step": [_p, _p, _p, _i64, _p],
     "tf_cast_bf16_f32": [_p, _p, _p, _i64],
 }
 

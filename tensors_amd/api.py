@@ -28,7 +28,7 @@ def _load() -> C.CDLL:
     lib.tfa_selftest.argtypes = [C.c_char_p, C.c_int32]
     lib.tfa_selftest.restype = C.c_int
     p, i64, i32, f = C.c_void_p, C.c_int64, C.c_int32, C.c_float
-    lib.tfa_mlp_train.argtypes = [p, i32, i64, i64, i64, i64, p, p, f, f, i32, i32, i32, p, p, p, p, p]
+    lib.tfa_mlp_train.argtypes = [p, i32, i64, i64, i64, i64, p, p, f, f, i32, i32, i32, p, p, p, p, p, i32]
     lib.tfa_mlp_train.restype = C.c_int
     lib.tfa_cnn_train.argtypes = [i64, i64, i64, i64, i64, i64, p, p, f, f, i32, p, p, p, p]
     lib.tfa_cnn_train.restype = C.c_int
@@ -56,10 +56,12 @@ def selftest(name: str, on_gpu: bool) -> None:
 
 
 def mlp_train(dims, xs, ys, *, steps, lr, mu, on_gpu, reference_compat=False, bf16=False, init_weights=None,
-              warmup=0, want_weights=False, pool_trace=None):
+              warmup=0, want_weights=False, pool_trace=None, graph=0):
     """Returns (losses[steps], final_weights or None, ms_per_step).  With
     pool_trace a uint64 array [steps], it receives the device pool's bytes in
-    use after each step (GPU only)."""
+    use after each step (GPU only).  graph=1 replays a HIP graph of one step
+    after the warmup steps (warmup >= 1, GPU only); graph=2 also waits for and
+    reads every replay's loss before the next."""
     dims_a = np.ascontiguousarray(dims, dtype=np.int32)
     xs = np.ascontiguousarray(xs, dtype=np.float32)
     ys = np.ascontiguousarray(ys, dtype=np.int64)
@@ -76,7 +78,7 @@ def mlp_train(dims, xs, ys, *, steps, lr, mu, on_gpu, reference_compat=False, bf
         assert pool_trace.dtype == np.uint64 and pool_trace.size == steps and pool_trace.flags["C_CONTIGUOUS"]
     _check(lib.tfa_mlp_train(_ptr(dims_a), len(dims_a), batch, steps, warmup, n_batches, _ptr(xs), _ptr(ys), lr, mu,
                              int(on_gpu), int(reference_compat), int(bf16), _ptr(iw), _ptr(losses), _ptr(fw),
-                             C.byref(ms), _ptr(pool_trace)))
+                             C.byref(ms), _ptr(pool_trace), int(graph)))
     return losses, fw, ms.value
 
 

@@ -556,12 +556,15 @@ int tfa_selftest(const char* name, int32_t on_gpu) {
 int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t steps, int64_t warmup, int64_t n_batches,
                   const float* xs, const int64_t* ys, float lr, float mu, int32_t on_gpu, int32_t reference_compat,
                   int32_t bf16, const float* init_weights, float* losses, float* final_weights, double* ms_per_step,
-                  uint64_t* pool_used) {
+                  uint64_t* pool_used, int32_t graph) {
     return guarded([&] {
         if (ndims < 2 || batch <= 0 || steps < 0 || n_batches <= 0 || warmup < 0 || warmup > steps)
             throw std::invalid_argument("tfa_mlp_train: bad sizes");
         if (bf16 && !on_gpu) throw std::invalid_argument("tfa_mlp_train: bf16 needs the GPU");
         if (pool_used && !on_gpu) throw std::invalid_argument("tfa_mlp_train: pool_used needs the GPU");
+        if (graph < 0 || graph > 2) throw std::invalid_argument("tfa_mlp_train: graph must be 0, 1 or 2");
+        if (graph && (!on_gpu || pool_used || warmup < 1))
+            throw std::invalid_argument("tfa_mlp_train: graph needs the GPU, warmup >= 1 and no pool_used");
         CompatScope scope(reference_compat != 0);
         const Device d = dev_of(on_gpu);
         std::vector<std::shared_ptr<nn::Linear>> layers;
@@ -605,16 +608,75 @@ int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t ste
                 hip::pool_stats(0, nullptr, &pool_used[s]);
             }
         };
-        for (int64_t s = 0; s < warmup; ++s) run_step(s);
-        sync_if_gpu(on_gpu);
-        auto t0 = std::chrono::steady_clock::now();
-        for (int64_t s = warmup; s < steps; ++s) run_step(s);
-        sync_if_gpu(on_gpu);
-        auto t1 = std::chrono::steady_clock::now();
-        if (ms_per_step)
-            *ms_per_step = steps > warmup ? std::chrono::duration<double, std::milli>(t1 - t0).count() / double(steps - warmup) : 0.0;
-        if (losses)
-            for (int64_t s = 0; s < steps; ++s) losses[s] = to_host(loss_t[static_cast<size_t>(s)])[0];
+        if (!graph) {
+            for (int64_t s = 0; s < warmup; ++s) run_step(s);
+            sync_if_gpu(on_gpu);
+            auto t0 = std::chrono::steady_clock::now();
+            for (int64_t s = warmup; s < steps; ++s) run_step(s);
+            sync_if_gpu(on_gpu);
+            auto t1 = std::chrono::steady_clock::now();
+            if (ms_per_step)
+                *ms_per_step = steps > warmup ? std::chrono::duration<double, std::milli>(t1 - t0).count() / double(steps - warmup) : 0.0;
+            if (losses)
+                for (int64_t s = 0; s < steps; ++s) losses[s] = to_host(loss_t[static_cast<size_t>(s)])[0];
+        } else {
+            // One HIP graph per step: the step reads its batch through a
+            // device table indexed by a device step counter and records its
+            // loss in a device ring (which advances the counter), so a replay
+            // needs no host work but its launch.  The warmup steps run the
+            // same step eagerly, which also fills the block cache that the
+            // capture allocates from.
+            std::vector<int64_t> xt, yt;
+            for (int64_t i = 0; i < n_batches; ++i) {
+                xt.push_back(static_cast<int64_t>(reinterpret_cast<uintptr_t>(xb[i].data())));
+                yt.push_back(static_cast<int64_t>(reinterpret_cast<uintptr_t>(yb[i].data())));
+            }
+            const Tensor xtab = host_i64(xt.data(), Shape{n_batches}).to(d);
+            const Tensor ytab = host_i64(yt.data(), Shape{n_batches}).to(d);
+            const int64_t zero = 0;
+            Tensor counter = host_i64(&zero, Shape{1}).to(d);
+            Tensor ring = Tensor::empty(Shape{steps}, Dtype::Float32, d);
+            Tensor xs_dev = Tensor::empty(Shape{batch, dims[0]}, Dtype::Float32, d);
+            Tensor ys_dev = Tensor::empty(Shape{batch}, Dtype::Int64, d);
+            auto graph_step = [&] {
+                hip::gather_indexed(xs_dev.data(), static_cast<const uint64_t*>(xtab.data()), n_batches,
+                                    static_cast<const int64_t*>(counter.data()), batch * dims[0] * 4);
+                hip::gather_indexed(ys_dev.data(), static_cast<const uint64_t*>(ytab.data()), n_batches,
+                                    static_cast<const int64_t*>(counter.data()), batch * 8);
+                Tensor h = xs_dev;
+                for (size_t l = 0; l < layers.size(); ++l)
+                    h = l + 1 < layers.size() ? layers[l]->forward_relu(h) : layers[l]->forward(h);
+                Tensor loss = ce.forward(h, ys_dev);
+                loss.backward();
+                opt.step();
+                hip::record_step(static_cast<const float*>(loss.data()), static_cast<float*>(ring.data()), steps,
+                                 static_cast<int64_t*>(counter.data()));
+            };
+            for (int64_t s = 0; s < warmup; ++s) graph_step();
+            sync_if_gpu(on_gpu);
+            hip::CapturedGraph g = hip::capture(graph_step);
+            std::vector<float> seen;
+            auto t0 = std::chrono::steady_clock::now();
+            for (int64_t s = warmup; s < steps; ++s) {
+                g.launch();
+                if (graph == 2) {
+                    // Checked replay: the host waits for each replay and reads
+                    // its loss (eager work and a synchronisation between
+                    // replays), then the ring is compared with these reads.
+                    seen.push_back(to_host(ring)[static_cast<size_t>(s)]);
+                }
+            }
+            sync_if_gpu(on_gpu);
+            auto t1 = std::chrono::steady_clock::now();
+            if (ms_per_step)
+                *ms_per_step = steps > warmup ? std::chrono::duration<double, std::milli>(t1 - t0).count() / double(steps - warmup) : 0.0;
+            const std::vector<float> ring_h = to_host(ring);
+            for (size_t i = 0; i < seen.size(); ++i)
+                if (std::memcmp(&seen[i], &ring_h[static_cast<size_t>(warmup) + i], sizeof(float)) != 0)
+                    throw std::runtime_error("tfa_mlp_train: a replay's loss changed after later replays");
+            if (losses)
+                for (int64_t s = 0; s < steps; ++s) losses[s] = ring_h[static_cast<size_t>(s)];
+        }
         if (final_weights) {
             size_t o = 0;
             for (auto& fc : layers)

@@ -126,6 +126,50 @@ void pool_stats(int device, uint64_t* reserved, uint64_t* used) {
 
 void set_stream(void* stream, int device) { check(tf_hip_set_stream(context(device), stream), "hip::set_stream"); }
 
+CapturedGraph::~CapturedGraph() {
+    if (g_) (void)tf_graph_destroy(g_);
+}
+
+CapturedGraph& CapturedGraph::operator=(CapturedGraph&& o) noexcept {
+    if (this != &o) {
+        if (g_) (void)tf_graph_destroy(g_);
+        g_ = o.g_;
+        device_ = o.device_;
+        o.g_ = nullptr;
+    }
+    return *this;
+}
+
+void CapturedGraph::launch() const {
+    if (g_ == nullptr) throw std::logic_error("hip::CapturedGraph::launch: empty graph");
+    check(tf_graph_launch(context(device_), g_), "hip::CapturedGraph::launch");
+}
+
+CapturedGraph capture(const std::function<void()>& record, int device) {
+    tf_ctx* ctx = context(device);
+    check(tf_graph_begin(ctx), "hip::capture");
+    try {
+        record();
+    } catch (...) {
+        // End the capture (its graph, if any, is dropped) and report the
+        // failing call's own error.
+        tf_graph* g = nullptr;
+        if (tf_graph_end(ctx, &g) == TF_OK && g) (void)tf_graph_destroy(g);
+        throw;
+    }
+    tf_graph* g = nullptr;
+    check(tf_graph_end(ctx, &g), "hip::capture");
+    return CapturedGraph(g, device);
+}
+
+void gather_indexed(void* dst, const uint64_t* table, int64_t n, const int64_t* counter, int64_t bytes, int device) {
+    check(tf_gather_indexed(context(device), dst, table, n, counter, bytes), "hip::gather_indexed");
+}
+
+void record_step(const float* src, float* ring, int64_t ring_len, int64_t* counter, int device) {
+    check(tf_record_step(context(device), src, ring, ring_len, counter), "hip::record_step");
+}
+
 Storage allocate(size_t size_bytes, Device device, Dtype dtype) {
     require(device.type == DeviceType::CUDA, "hip::allocate: not a GPU device");
     void* p = nullptr;

@@ -13,12 +13,14 @@
 #include "tensor/CPUStorageAllocator.hpp"
 #include "tensor/Tensor.hpp"
 
+#include <functional>
 #include <vector>
 
 #include <cstddef>
 #include <cstdint>
 
 struct tf_ctx;
+struct tf_graph;
 
 namespace tensorforge::hip {
 
@@ -36,6 +38,35 @@ void register_backend();
 void synchronize(int device = 0);
 // Launch on a caller-owned hipStream_t from now on (nullptr: the context's own).
 void set_stream(void* stream, int device = 0);
+
+// ---- HIP graphs (tf_graph_*) ----------------------------------------------
+// The device work that `record` enqueues on `device`, captured once and
+// replayed with one launch.  Under capture the block cache serves every
+// allocation (run the same work eagerly once first), and nothing may wait for
+// the device or copy from / to the host.  Tensors created during the capture
+// that outlive it must stay alive while the graph is replayed.
+class CapturedGraph {
+public:
+    CapturedGraph() = default;
+    CapturedGraph(tf_graph* g, int device) : g_(g), device_(device) {}
+    ~CapturedGraph();
+    CapturedGraph(const CapturedGraph&) = delete;
+    CapturedGraph& operator=(const CapturedGraph&) = delete;
+    CapturedGraph(CapturedGraph&& o) noexcept : g_(o.g_), device_(o.device_) { o.g_ = nullptr; }
+    CapturedGraph& operator=(CapturedGraph&& o) noexcept;
+    // Enqueues one replay on the device's stream.
+    void launch() const;
+
+private:
+    tf_graph* g_ = nullptr;
+    int device_ = 0;
+};
+CapturedGraph capture(const std::function<void()>& record, int device = 0);
+// dst[0:bytes) = table[*counter % n][0:bytes) on the device (tf_gather_indexed).
+void gather_indexed(void* dst, const uint64_t* table, int64_t n, const int64_t* counter, int64_t bytes,
+                    int device = 0);
+// ring[*counter] = *src, then ++*counter, on the device (tf_record_step).
+void record_step(const float* src, float* ring, int64_t ring_len, int64_t* counter, int device = 0);
 
 // ---- memory --------------------------------------------------------------
 Storage allocate(size_t size_bytes, Device device, Dtype dtype);

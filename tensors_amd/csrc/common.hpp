@@ -33,6 +33,14 @@ struct tf_ctx {
     std::unordered_map<size_t, std::vector<void*>> cached;  // size class -> free blocks
     std::unordered_map<void*, size_t> live;                  // block -> size class
     size_t cached_bytes = 0;
+    // HIP-graph capture of the stream (tf_graph_begin .. tf_graph_end).
+    // While capturing, allocations come from capture_free (blocks freed
+    // earlier in the same capture) or the block cache, never from the pool;
+    // frees go to capture_free, whose blocks the graph keeps until it is
+    // destroyed, so a replay's temporaries are never handed to other work.
+    bool capturing = false;
+    bool capture_failed = false;  // a call failed while capturing
+    std::unordered_map<size_t, std::vector<void*>> capture_free;
 };
 
 namespace tfh {

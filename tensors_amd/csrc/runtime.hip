@@ -105,7 +105,7 @@ TimedLaunch::TimedLaunch(tf_ctx* ctx, int64_t M, int64_t N, int64_t K, int64_t b
     : ctx_(ctx) {
     TimingState& t = timing();
     std::lock_guard<std::mutex> lock(t.mu);
-    if (!t.on || ctx == nullptr || t.used >= t.records.size()) return;
+    if (!t.on || ctx == nullptr || ctx->capturing || t.used >= t.records.size()) return;
     slot_ = (int)t.used++;
     t.records[slot_] = TimingRecord{{M, N, K, batch}, {trans_a, trans_b, in_dtype, out_dtype}};
     (void)hipEventRecord(t.events[2 * slot_], ctx->stream);
@@ -130,6 +130,11 @@ tf_status hip_error(hipError_t e, const char* what) {
 
 tf_status ensure_workspace(tf_ctx* ctx, size_t bytes) {
     if (ctx->ws_bytes >= bytes) return TF_OK;
+    if (ctx->capturing) {
+        ctx->capture_failed = true;
+        return set_error(TF_ERR_INVALID, "ensure_workspace: the workspace would grow while a graph is being captured "
+                                         "(run the captured work once eagerly first)");
+    }
     if (ctx->ws) {
         TF_HIP_CHECK(hipFreeAsync(ctx->ws, ctx->stream));
         ctx->ws = nullptr;
@@ -194,6 +199,16 @@ tf_status tf_hip_init(int device, tf_ctx** out) {
 
 tf_status tf_hip_shutdown(tf_ctx* ctx) {
     if (ctx == nullptr) return TF_OK;
+    if (ctx->capturing) {
+        // An unfinished capture: end it, drop the graph, keep its blocks.
+        hipGraph_t g = nullptr;
+        if (hipStreamEndCapture(ctx->stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+        (void)hipGetLastError();
+        ctx->capturing = false;
+        for (auto& kv : ctx->capture_free)
+            for (void* p : kv.second) ctx->cached[kv.first].push_back(p);
+        ctx->capture_free.clear();
+    }
     if (ctx->own_stream) {
         // Cached blocks go back to the pool once the current stream's work is done.
         if (ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->stream);
@@ -216,6 +231,7 @@ tf_status tf_hip_stream(tf_ctx* ctx, void** stream) {
 
 tf_status tf_hip_set_stream(tf_ctx* ctx, void* stream) {
     TF_CTX_CHECK(ctx);
+    TF_REQUIRE(!ctx->capturing, "tf_hip_set_stream: a graph is being captured on this context");
     // Workspace frees are stream-ordered on the stream that last used them:
     // order the switch so the workspace is never used on two streams at once.
     hipStream_t next = stream ? (hipStream_t)stream : ctx->own_stream;
@@ -226,6 +242,10 @@ tf_status tf_hip_set_stream(tf_ctx* ctx, void* stream) {
 
 tf_status tf_hip_sync(tf_ctx* ctx) {
     TF_CTX_CHECK(ctx);
+    if (ctx->capturing) {
+        ctx->capture_failed = true;
+        return tfh::set_error(TF_ERR_INVALID, "tf_hip_sync: a graph is being captured on this context");
+    }
     TF_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     return TF_OK;
 }
@@ -235,6 +255,17 @@ tf_status tf_hip_alloc(tf_ctx* ctx, size_t bytes, void** out) {
     TF_REQUIRE(out != nullptr, "tf_hip_alloc: null out");
     const size_t cls = size_class(bytes == 0 ? 1 : bytes);
     std::lock_guard<std::mutex> lock(ctx->cache_mu);
+    if (ctx->capturing) {
+        // Blocks freed earlier in this capture first (stream order inside the
+        // graph makes their reuse safe), then the cache; never the pool.
+        auto cf = ctx->capture_free.find(cls);
+        if (cf != ctx->capture_free.end() && !cf->second.empty()) {
+            *out = cf->second.back();
+            cf->second.pop_back();
+            ctx->live.emplace(*out, cls);
+            return TF_OK;
+        }
+    }
     auto it = ctx->cached.find(cls);
     if (it != ctx->cached.end() && !it->second.empty()) {
         // Last freed first (the block likeliest to still be in the caches).
@@ -245,6 +276,13 @@ tf_status tf_hip_alloc(tf_ctx* ctx, size_t bytes, void** out) {
         ctx->cached_bytes -= cls;
         ctx->live.emplace(*out, cls);
         return TF_OK;
+    }
+    if (ctx->capturing) {
+        *out = nullptr;
+        ctx->capture_failed = true;
+        return tfh::set_error(TF_ERR_INVALID, "tf_hip_alloc: no cached block of " + std::to_string(cls) +
+                                                  " bytes while a graph is being captured (run the captured work "
+                                                  "once eagerly first, so the block cache holds its blocks)");
     }
     hipError_t e = hipSuccess;
     const tfh::AllocOutcome r = tfh::allocate_with_retry(
@@ -264,14 +302,19 @@ tf_status tf_hip_free(tf_ctx* ctx, void* ptr) {
     std::lock_guard<std::mutex> lock(ctx->cache_mu);
     auto it = ctx->live.find(ptr);
     TF_REQUIRE(it != ctx->live.end(), "tf_hip_free: pointer not allocated by this context (or freed twice)");
-    ctx->cached[it->second].push_back(ptr);
-    ctx->cached_bytes += it->second;
+    if (ctx->capturing) {
+        ctx->capture_free[it->second].push_back(ptr);
+    } else {
+        ctx->cached[it->second].push_back(ptr);
+        ctx->cached_bytes += it->second;
+    }
     ctx->live.erase(it);
     return TF_OK;
 }
 
 tf_status tf_hip_trim(tf_ctx* ctx, size_t keep_bytes) {
     TF_CTX_CHECK(ctx);
+    TF_REQUIRE(!ctx->capturing, "tf_hip_trim: a graph is being captured on this context");
     {
         std::lock_guard<std::mutex> lock(ctx->cache_mu);
         tf_status st = release_cached(ctx);
@@ -303,6 +346,12 @@ tf_status tf_hip_memcpy(tf_ctx* ctx, void* dst, const void* src, size_t bytes, i
     case TF_COPY_D2H: k = hipMemcpyDeviceToHost; break;
     case TF_COPY_D2D: k = hipMemcpyDeviceToDevice; break;
     default: return tfh::set_error(TF_ERR_INVALID, "tf_hip_memcpy: bad copy kind");
+    }
+    if (ctx->capturing && kind != TF_COPY_D2D) {
+        // A host buffer would be read or written at replay time, long after
+        // the caller has reused it.
+        ctx->capture_failed = true;
+        return tfh::set_error(TF_ERR_INVALID, "tf_hip_memcpy: only device-to-device copies can be captured");
     }
     TF_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, k, ctx->stream));
     if (kind == TF_COPY_D2H || kind == TF_COPY_H2H || kind == TF_COPY_H2D) {

@@ -51,6 +51,45 @@ def test_c1_loss_trajectory_matches_reference(ctx):
     assert_close(got, want, 1e-3, "weights after 100 steps")
 
 
+@pytest.mark.parametrize("graph", [1, 2])
+def test_c1_graph_replay_matches_eager_and_reference(ctx, graph):
+    """The config-1 loop with its step captured in a HIP graph after 10 eager
+    steps: the 90 replays reproduce the eager loop bit for bit (same kernels,
+    same order, same buffers' contents) and so follow the reference's
+    trajectory within 1e-3.  graph=2 waits for every replay and reads its
+    loss before launching the next (eager work and synchronisations between
+    replays; the harness also checks that no later replay changed an earlier
+    replay's recorded loss)."""
+    xs, ys = _c1_inputs(100)
+    kw = dict(steps=100, warmup=10, lr=0.1, mu=0.9, on_gpu=True, reference_compat=True, want_weights=True)
+    eager, fw_e, _ = api.mlp_train(C1, xs, ys, **kw)
+    print(f"graph mode {graph}", flush=True)
+    replay, fw_g, _ = api.mlp_train(C1, xs, ys, graph=graph, **kw)
+    assert np.array_equal(replay.view(np.uint32), eager.view(np.uint32)), \
+        f"first differing step {int(np.argmax(replay != eager))}"
+    assert np.array_equal(fw_g.view(np.uint32), fw_e.view(np.uint32))
+    err = np.max(np.abs(replay.astype(np.float64) - FIX["c1_losses_100"]))
+    assert err <= 1e-3, f"max |loss - reference| = {err}"
+
+
+def test_c1_graph_replay_with_fewer_batches_than_steps(ctx):
+    """Batch selection on the device wraps around the batch table (step s
+    uses batch s % n_batches), as the eager loop does."""
+    xs, ys = _c1_inputs(7)
+    kw = dict(steps=30, warmup=3, lr=0.1, mu=0.9, on_gpu=True, reference_compat=True)
+    eager, _, _ = api.mlp_train(C1, xs, ys, **kw)
+    replay, _, _ = api.mlp_train(C1, xs, ys, graph=1, **kw)
+    assert np.array_equal(replay.view(np.uint32), eager.view(np.uint32))
+
+
+def test_c1_graph_mode_rejects_bad_arguments(ctx):
+    xs, ys = _c1_inputs(2)
+    with pytest.raises(api.HarnessError):
+        api.mlp_train(C1, xs, ys, steps=4, warmup=0, lr=0.1, mu=0.9, on_gpu=True, graph=1)
+    with pytest.raises(api.HarnessError):
+        api.mlp_train(C1, xs, ys, steps=4, warmup=1, lr=0.1, mu=0.9, on_gpu=False, graph=1)
+
+
 def test_c1_first_step_update_matches_reference(ctx):
     """The first SGD update (= -lr * gradient) of every weight matches the
     reference's within rtol 1e-4 (atol 1e-4 * rms of the update)."""
