@@ -36,6 +36,9 @@ public:
     virtual std::vector<Tensor> apply(std::vector<Tensor>&& grads) = 0;
     // Drop saved tensors once the node has run (keep_graph == false).
     virtual void release_saved() {}
+    // True when apply() takes an undefined gradient as "all ones", so that
+    // Tensor::backward() on this node's output can skip filling the seed.
+    virtual bool accepts_unit_seed() const { return false; }
 };
 
 }  // namespace tensorforge

@@ -45,9 +45,12 @@ Tensor Tensor::grad() const { return autograd_meta_ ? autograd_meta_->grad_ : Te
 void Tensor::backward() {
     if (!autograd_meta_ || !autograd_meta_->grad_fn_)
         throw std::runtime_error("backward() called on tensor without grad_fn");
-    // Seed dL/dL = 1 (a fill kernel for GPU tensors).
+    // Seed dL/dL = 1 (a fill kernel for GPU tensors), or an undefined tensor
+    // meaning ones for a node that takes it so.
     Shape s = numel() == 0 ? Shape{1} : shape();
-    Tensor seed = dtype() == Dtype::Float32 ? ones(s, Dtype::Float32, device()) : Tensor::empty(s, dtype(), device());
+    Tensor seed;
+    if (!autograd_meta_->grad_fn_->accepts_unit_seed())
+        seed = dtype() == Dtype::Float32 ? ones(s, Dtype::Float32, device()) : Tensor::empty(s, dtype(), device());
     Engine engine;
     engine.execute(autograd_meta_->grad_fn_, seed, false);
 }

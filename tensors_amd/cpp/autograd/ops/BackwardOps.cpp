@@ -346,6 +346,14 @@ std::vector<Tensor> LinearBackward::apply(std::vector<Tensor>&& grads) {
 }
 
 std::vector<Tensor> CrossEntropyBackward::apply(std::vector<Tensor>&& grads) {
+    if (precomputed_) {
+        // dlogits for g = 1; an undefined gradient is the unit seed.
+        const Tensor& dl = stats_.unpack();
+        if (!grads[0].storage()) return {dl};
+        Tensor d = raw::empty_like(dl);
+        hip::scale_by(dl, grads[0], d);
+        return {std::move(d)};
+    }
     const Tensor& logits = logits_.unpack();
     const Tensor& targets = targets_.unpack();
     const Tensor& stats = stats_.unpack();

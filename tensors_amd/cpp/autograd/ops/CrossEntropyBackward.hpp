@@ -16,11 +16,19 @@ public:
     // lse: saved row log-sum-exp (GPU) or softmax probabilities (CPU).
     CrossEntropyBackward(const Tensor& logits, const Tensor& targets, const Tensor& row_stats)
         : logits_(logits), targets_(targets), stats_(row_stats) {}
+    // GPU, fused with the forward: dlogits for an upstream gradient of 1,
+    // computed in the forward's pass over the logits.
+    struct Precomputed {};
+    CrossEntropyBackward(Precomputed, const Tensor& dlogits)
+        : logits_(Tensor()), targets_(Tensor()), stats_(dlogits), precomputed_(true) {}
     std::vector<Tensor> apply(std::vector<Tensor>&& grads) override;
     void release_saved() override { logits_.reset(); targets_.reset(); stats_.reset(); }
+    // The precomputed dlogits are the answer for a unit seed as they are.
+    bool accepts_unit_seed() const override { return precomputed_; }
 
 private:
     SavedTensor logits_, targets_, stats_;
+    bool precomputed_ = false;
 };
 
 }  // namespace tensorforge

@@ -346,6 +346,29 @@ void cross_entropy_backward(const Tensor& logits, const Tensor& targets, const T
           "hip::cross_entropy_backward");
 }
 
+void cross_entropy_forward_backward(const Tensor& logits, const Tensor& targets, Tensor& loss, Tensor& dlogits,
+                                    int flags) {
+    require_gpu(logits, "hip::cross_entropy_forward_backward"); require_gpu(targets, "hip::cross_entropy_forward_backward");
+    require_gpu(loss, "hip::cross_entropy_forward_backward");
+    check_same(logits, dlogits, "hip::cross_entropy_forward_backward");
+    int64_t r, c; rows_cols(logits, r, c, "hip::cross_entropy_forward_backward");
+    require(targets.dtype() == Dtype::Int64 && targets.numel() == r, "hip::cross_entropy_forward_backward: targets");
+    require(loss.dtype() == Dtype::Float32 && loss.numel() >= 1, "hip::cross_entropy_forward_backward: loss");
+    check(tf_ce_fwd_bwd(ctx_of(logits), static_cast<const float*>(logits.data()),
+                        static_cast<const int64_t*>(targets.data()), static_cast<float*>(loss.data()),
+                        static_cast<float*>(dlogits.data()), r, c, flags),
+          "hip::cross_entropy_forward_backward");
+}
+
+void scale_by(const Tensor& x, const Tensor& s, Tensor& out) {
+    require_gpu(x, "hip::scale_by"); require_gpu(s, "hip::scale_by");
+    check_same(x, out, "hip::scale_by");
+    require(s.dtype() == Dtype::Float32 && s.numel() >= 1, "hip::scale_by: the scale must be Float32");
+    check(tf_scale_by(ctx_of(x), x.data(), static_cast<const float*>(s.data()), out.data(), x.numel(),
+                      static_cast<int>(x.dtype())),
+          "hip::scale_by");
+}
+
 void layernorm_forward(const Tensor& x, const Tensor& gamma, const Tensor& beta, Tensor& y, Tensor& mean,
                        Tensor& rstd, float eps) {
     require_gpu(x, "hip::layer_norm"); check_same(x, y, "hip::layer_norm");

@@ -106,6 +106,11 @@ void log_softmax_backward(const Tensor& y, const Tensor& dy, Tensor& dx);
 void cross_entropy_forward(const Tensor& logits, const Tensor& targets, Tensor& loss, Tensor* lse, int flags);
 void cross_entropy_backward(const Tensor& logits, const Tensor& targets, const Tensor* lse, const Tensor* grad_loss,
                             Tensor& dlogits);
+// Loss and dlogits = (softmax - onehot) / N in one pass (tf_ce_fwd_bwd).
+void cross_entropy_forward_backward(const Tensor& logits, const Tensor& targets, Tensor& loss, Tensor& dlogits,
+                                    int flags);
+// out = x * s[0] for a device scalar s (tf_scale_by).
+void scale_by(const Tensor& x, const Tensor& s, Tensor& out);
 void layernorm_forward(const Tensor& x, const Tensor& gamma, const Tensor& beta, Tensor& y, Tensor& mean,
                        Tensor& rstd, float eps);
 void layernorm_backward(const Tensor& dy, const Tensor& x, const Tensor& gamma, const Tensor& mean, const Tensor& rstd,

@@ -27,10 +27,18 @@ Tensor CrossEntropyLoss::forward(Tensor logits, Tensor targets) {
         // the probability clamped at 1e-9, and a target outside [0, C) makes
         // the loss NaN instead of throwing (a host check would need a
         // device->host copy per step); such a row gets a zero gradient.
+        // With a gradient to come, dlogits (for an upstream gradient of 1)
+        // are computed in the same pass over the logits as the loss, and the
+        // loss mean in the same kernel; the backward node returns them, or
+        // scales them by a non-unit upstream gradient.
         Tensor lf = logits.dtype() == Dtype::Float32 ? logits : logits.to(Dtype::Float32);
-        Tensor lse = Tensor::empty(Shape{N}, Dtype::Float32, logits.device());
-        hip::cross_entropy_forward(lf, targets, loss, &lse, TF_CE_MODULE);
-        if (logits.requires_grad()) node = std::make_shared<CrossEntropyBackward>(lf, targets, lse);
+        if (logits.requires_grad()) {
+            Tensor dl = Tensor::empty(lf.shape(), Dtype::Float32, logits.device());
+            hip::cross_entropy_forward_backward(lf, targets, loss, dl, TF_CE_MODULE);
+            node = std::make_shared<CrossEntropyBackward>(CrossEntropyBackward::Precomputed{}, dl);
+        } else {
+            hip::cross_entropy_forward(lf, targets, loss, nullptr, TF_CE_MODULE);
+        }
     } else {
         // softmax -> gather -> clamp(1e-9) -> -log -> mean, as
         // reference nn/CrossEntropyLoss.cpp:36-62.

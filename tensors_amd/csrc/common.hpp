@@ -41,6 +41,11 @@ struct tf_ctx {
     bool capturing = false;
     bool capture_failed = false;  // a call failed while capturing
     std::unordered_map<size_t, std::vector<void*>> capture_free;
+    // Arrival counters of the kernels whose last block to finish does a
+    // final step (tfh::kTicket*): zero between launches (that block resets
+    // its counter), so captured graphs replay them unchanged.  Launches on
+    // one context are stream-ordered, so one counter per kernel suffices.
+    unsigned* tickets = nullptr;
 };
 
 namespace tfh {
@@ -57,6 +62,13 @@ tf_status partial_rows_sum(tf_ctx* ctx, const float* part, float* out_lo, float*
                            int64_t split);
 
 inline bool bad_ctx(tf_ctx* ctx) { return ctx == nullptr || ctx->stream == nullptr; }
+
+// Slots of tf_ctx::tickets: the CE kernel's, then one per output tile of
+// the small fp32 GEMM (at most kTicketGemmTiles tiles).
+constexpr int kTicketCE = 0;
+constexpr int kTicketGemm = 64;
+constexpr int kTicketGemmTiles = 4096;
+constexpr int kTickets = kTicketGemm + kTicketGemmTiles;
 
 // Launch timing (tf_hip_timing_*): a GEMM entry point constructs one of
 // these around its launches; while recording is on it records an event on

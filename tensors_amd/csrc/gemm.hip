@@ -2192,6 +2192,168 @@ __global__ __launch_bounds__(kF32DlThreads) void gemm_f32_dl_kernel(GemmParams p
         store_wave<2, !A_KMAJ, !B_KMAJ>(p, acc, m0 + wm * 64, n0 + wn * 64, (int64_t)batch * p.stride_c, split, g);
 }
 
+// Small fp32 products (C1's layers, C4's fully connected layer): one block
+// per 32 x 32 output tile and K chunk, so even a 64 x 256 x 784 product runs
+// on ~200 blocks whose loads are all issued at once.  A block walks `cps`
+// chunks of 64 k (the next chunk's loads in flight while the current one is
+// summed from LDS) with plain FMAs: thread t owns column t % 32 and rows
+// 4 (t / 32) .. +3 of the tile.  With more than one chunk group per tile,
+// each block writes its partial tile and counts itself in on the tile's
+// arrival counter; the block that arrives last adds the partials in chunk
+// order (deterministic) and applies the epilogue, then resets the counter.
+// The tile kernels above need a chain of load round trips per k block and a
+// separate split-K reduction; at these sizes that latency, not arithmetic,
+// set their 10-17 us per product.
+constexpr int kSmT = 32;    // tile side
+constexpr int kSmKC = 64;   // k per chunk
+template <bool A_KMAJ, bool B_KMAJ>
+__global__ __launch_bounds__(256) void gemm_f32_small_kernel(GemmParams p, int nchunks, int cps,
+                                                             unsigned* __restrict__ tickets) {
+    __shared__ float As[kSmKC][kSmT];   // As[k][m]
+    __shared__ float Bs[kSmKC][kSmT];   // Bs[k][n]
+    __shared__ int last;
+    const int tile = blockIdx.x / nchunks, chunk = blockIdx.x - tile * nchunks;
+    const int tm = tile / p.tiles_n, tn = tile - tm * p.tiles_n;
+    const int m0 = tm * kSmT, n0 = tn * kSmT;
+    const float* A = reinterpret_cast<const float*>(p.A);
+    const float* B = reinterpret_cast<const float*>(p.B);
+    const int t = threadIdx.x, col = t & 31, rg = t >> 5;
+
+    // Loads of one 64-deep chunk: 512 float4 of A and 512 of B, two of each
+    // per thread.  Element (m, k) of A is A[m*lda + k] (K-major) or
+    // A[k*lda + m]; (k, n) of B is B[n*ldb + k] (K-major) or B[k*ldb + n].
+    // A quad runs along the operand's contiguous dimension; out-of-range
+    // elements read as zero.
+    auto load_quad = [&](const float* X, int64_t ld, int mn0, int MN, bool kmaj, bool vec, int k0, int q) -> float4 {
+        int mn, k;
+        if (kmaj) { mn = q >> 4; k = k0 + 4 * (q & 15); }    // 32 rows x 16 quads along k
+        else { k = k0 + (q >> 3); mn = 4 * (q & 7); }       // 64 k rows x 8 quads along m/n
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (kmaj) {
+            const int row = mn0 + mn;
+            if (row < MN) {
+                const float* src = X + (int64_t)row * ld + k;
+                if (vec && k + 4 <= p.K) {
+                    const float4 w = *reinterpret_cast<const float4*>(src);
+                    v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) if (k + e < p.K) v[e] = src[e];
+                }
+            }
+        } else {
+            if (k < p.K) {
+                const int c0 = mn0 + mn;
+                const float* src = X + (int64_t)k * ld + c0;
+                if (vec && c0 + 4 <= MN) {
+                    const float4 w = *reinterpret_cast<const float4*>(src);
+                    v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) if (c0 + e < MN) v[e] = src[e];
+                }
+            }
+        }
+        return make_float4(v[0], v[1], v[2], v[3]);
+    };
+    auto store_quad = [&](float (*S)[kSmT], bool kmaj, int q, const float4& w) {
+        if (kmaj) {
+            const int mn = q >> 4, k = 4 * (q & 15);
+            S[k][mn] = w.x; S[k + 1][mn] = w.y; S[k + 2][mn] = w.z; S[k + 3][mn] = w.w;
+        } else {
+            const int k = q >> 3, mn = 4 * (q & 7);
+            *reinterpret_cast<float4*>(&S[k][mn]) = w;
+        }
+    };
+
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int kc_first = chunk * cps;
+    const int kc_end = min(kc_first + cps, (p.K + kSmKC - 1) / kSmKC);
+    float4 ra[2], rb[2];
+    auto fetch = [&](int kc) {
+        const int k0 = kc * kSmKC;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            ra[j] = load_quad(A, p.lda, m0, p.M, A_KMAJ, p.vec_a, k0, t + 256 * j);
+            rb[j] = load_quad(B, p.ldb, n0, p.N, B_KMAJ, p.vec_b, k0, t + 256 * j);
+        }
+    };
+    if (kc_first < kc_end) fetch(kc_first);
+    for (int kc = kc_first; kc < kc_end; ++kc) {
+        __syncthreads();   // the previous chunk's reads are done
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            store_quad(As, A_KMAJ, t + 256 * j, ra[j]);
+            store_quad(Bs, B_KMAJ, t + 256 * j, rb[j]);
+        }
+        __syncthreads();
+        if (kc + 1 < kc_end) fetch(kc + 1);
+        const int kn = min(kSmKC, p.K - kc * kSmKC);
+        for (int k = 0; k < kn; ++k) {
+            const float4 a = *reinterpret_cast<const float4*>(&As[k][4 * rg]);
+            const float b = Bs[k][col];
+            acc[0] = fmaf(a.x, b, acc[0]);
+            acc[1] = fmaf(a.y, b, acc[1]);
+            acc[2] = fmaf(a.z, b, acc[2]);
+            acc[3] = fmaf(a.w, b, acc[3]);
+        }
+    }
+
+    if (nchunks > 1) {
+        // Partials and counter go through agent-scope (cross-XCD coherent)
+        // relaxed atomics, which need no cache maintenance; a block's stores
+        // have completed (vmcnt 0 in every thread, then the barrier) before
+        // it counts itself in.  A device-scope fence here instead writes
+        // back and invalidates the XCD's L2 in every block: 208 blocks of a
+        // 64 x 256 x 784 product took 35 us that way.
+        float* part = p.partial + ((int64_t)tile * nchunks + chunk) * (kSmT * kSmT);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __hip_atomic_store(part + (4 * rg + i) * kSmT + col, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        __syncthreads();
+        if (t == 0)
+            last = __hip_atomic_fetch_add(tickets + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   (unsigned)(nchunks - 1);
+        __syncthreads();
+        if (!last) return;
+        const float* base = p.partial + (int64_t)tile * nchunks * (kSmT * kSmT);
+        auto ld = [&](int c, int i) {
+            return __hip_atomic_load(base + (int64_t)c * (kSmT * kSmT) + (4 * rg + i) * kSmT + col, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        };
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = 0.0f;
+        int c = 0;
+        for (; c + 4 <= nchunks; c += 4) {
+            float v[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[u][i] = ld(c + u, i);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i] += v[u][i];
+        }
+        for (; c < nchunks; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += ld(c, i);
+        if (t == 0) __hip_atomic_store(tickets + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU || p.epi == TF_EPI_ROW_BIAS_RELU;
+    const bool has_bias = p.epi != TF_EPI_NONE && p.epi != TF_EPI_RELU;
+    const int n = n0 + col;
+    if (n >= p.N) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 4 * rg + i;
+        if (m >= p.M) break;
+        const float bv = has_bias ? (p.row_bias ? p.bias[m] : p.bias[n]) : 0.0f;
+        emit(p, (int64_t)m * p.ldc + n, acc[i], bv, relu);
+    }
+}
+
 // Split-K reduction: C = epi(alpha * sum_s partial[s] + beta * C), summing the
 // splits in ascending order (deterministic).  Grid (ceil(N / 1024), M): a
 // block covers 1024 columns of one row, 4 per thread, with 16-byte loads of
@@ -2494,6 +2656,39 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     p.pair_c = (reinterpret_cast<uintptr_t>(C) & 7) == 0 && (ldc % 2 == 0) && (p.stride_c % 2 == 0);
     const uintptr_t c_vec_bytes = out_dtype == TF_BF16 ? 8 : 16;
     p.vec_c4 = (reinterpret_cast<uintptr_t>(C) & (c_vec_bytes - 1)) == 0 && (ldc % 4 == 0) && (p.stride_c % 4 == 0);
+    // Small fp32 products: 32 x 32 tiles with K over many blocks (see
+    // gemm_f32_small_kernel).
+    const int64_t sm_tiles = ((M + kSmT - 1) / kSmT) * ((N + kSmT - 1) / kSmT);
+    if (in_dtype == TF_F32 && batch == 1 && K > 0 && K <= 2048 && (double)M * (double)N * (double)K <= 134217728.0 &&
+        sm_tiles <= tfh::kTicketGemmTiles) {
+        p.tiles_m = (int)((M + kSmT - 1) / kSmT);
+        p.tiles_n = (int)((N + kSmT - 1) / kSmT);
+        const int64_t nkc = (K + kSmKC - 1) / kSmKC;
+        // Enough chunk groups for ~256 blocks, at most 32 per tile (the
+        // last block adds them up), each of >= 1 chunk.
+        int64_t groups = std::min<int64_t>({nkc, 32, std::max<int64_t>(1, (ncu + sm_tiles - 1) / sm_tiles)});
+        const int cps = (int)((nkc + groups - 1) / groups);
+        groups = (nkc + cps - 1) / cps;
+        if (groups > 1) {
+            const size_t need = (size_t)sm_tiles * (size_t)groups * kSmT * kSmT * sizeof(float);
+            if (noalloc) {
+                if (need > kNoAllocScratchBytes) return tfh::set_error(TF_ERR_INVALID, "tf_gemm_noalloc: partials too large");
+                tf_status st = scratch_address(ctx->device, &p.partial);
+                if (st != TF_OK) return st;
+            } else {
+                tf_status st = tfh::ensure_workspace(ctx, need);
+                if (st != TF_OK) return st;
+                p.partial = reinterpret_cast<float*>(ctx->ws);
+            }
+        }
+        const dim3 grid((unsigned)(sm_tiles * groups));
+        unsigned* tickets = ctx->tickets + tfh::kTicketGemm;
+        if (a_kmaj && b_kmaj) gemm_f32_small_kernel<true, true><<<grid, 256, 0, ctx->stream>>>(p, (int)groups, cps, tickets);
+        else if (a_kmaj) gemm_f32_small_kernel<true, false><<<grid, 256, 0, ctx->stream>>>(p, (int)groups, cps, tickets);
+        else if (b_kmaj) gemm_f32_small_kernel<false, true><<<grid, 256, 0, ctx->stream>>>(p, (int)groups, cps, tickets);
+        else gemm_f32_small_kernel<false, false><<<grid, 256, 0, ctx->stream>>>(p, (int)groups, cps, tickets);
+        return tfh::check_launch("gemm_f32_small_kernel");
+    }
     if (in_dtype == TF_F32 && !trans_a && !trans_b && !reduce_batch && K <= 32 && M <= 64 && N >= 256) {
         const dim3 grid((unsigned)((N + 255) / 256), (unsigned)batch);
         gemm_f32_smallk_kernel<<<grid, 256, 0, ctx->stream>>>(p);

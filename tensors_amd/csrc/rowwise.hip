@@ -14,6 +14,8 @@
 namespace {
 
 constexpr int kRowsPerBlock = 4;
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt not waited for) on gfx950.
+constexpr int kWaitVm0 = 0x0F70;
 constexpr int kMaxCached = 8;  // 2048 columns cached in registers
 
 __device__ __forceinline__ int col_of(int c, int lane, int q, bool vec) {
@@ -101,16 +103,32 @@ __device__ __forceinline__ void stream_stats(const float* __restrict__ row, int 
 // the probability at 1e-9, nn/CrossEntropyLoss.cpp:54-55; +inf: no cap).
 // dlogits = scale * (exp(x - lse) - onehot), scale = g / rows.
 // ---------------------------------------------------------------------------
+// loss[0] = (sum_r nll[r]) * inv_rows by one block of 256 threads in a fixed
+// order: thread i adds nll[i], nll[i + 256], ... in turn, then a wave
+// butterfly, then the four waves' sums as (w0 + w1) + (w2 + w3).
+// The nll values are read with agent-scope atomic loads (coherent across
+// XCDs, written by other blocks with agent-scope atomic stores).
+__device__ __forceinline__ void block_mean(const float* __restrict__ nll, int rows, float inv_rows,
+                                           float* __restrict__ loss) {
+    __shared__ float part[4];
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < rows; i += 256)
+        s += __hip_atomic_load(nll + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s = tfd::wave_sum(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) loss[0] = ((part[0] + part[1]) + (part[2] + part[3])) * inv_rows;
+}
+
+// One row of ce_kernel, by one wave.
 template <int NC, int MODE>
-__global__ __launch_bounds__(256) void ce_kernel(const float* __restrict__ logits, const int64_t* __restrict__ targets,
-                                                 const float* __restrict__ lse_in, const float* __restrict__ grad_loss,
-                                                 float* __restrict__ lse_out, float* __restrict__ nll,
-                                                 float* __restrict__ dlogits, int rows, int cols, float inv_rows,
-                                                 int vec, float nll_max, int strict) {
+__device__ __forceinline__ void ce_row(const float* __restrict__ logits, const int64_t* __restrict__ targets,
+                                       const float* __restrict__ lse_in, const float* __restrict__ grad_loss,
+                                       float* __restrict__ lse_out, float* __restrict__ nll,
+                                       float* __restrict__ dlogits, int r, int cols, float inv_rows, int vec,
+                                       float nll_max, int strict) {
     constexpr int NCC = NC > 0 ? NC : 1;
     const int lane = threadIdx.x & 63;
-    const int r = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-    if (r >= rows) return;
     const float* x = logits + (int64_t)r * cols;
     const int64_t t = targets[r];
     const bool t_ok = t >= 0 && t < cols;
@@ -146,7 +164,8 @@ __global__ __launch_bounds__(256) void ce_kernel(const float* __restrict__ logit
         if (lane == 0) {
             if (lse_out) lse_out[r] = lse;
             float nl = t_ok ? lse - x[t] : (strict ? __builtin_nanf("") : 0.0f);
-            nll[r] = nl > nll_max ? nll_max : nl;   // NaN stays NaN
+            // NaN stays NaN; an agent-scope store, read by another block
+            __hip_atomic_store(nll + r, nl > nll_max ? nll_max : nl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     if (MODE != 0) {
@@ -179,16 +198,35 @@ __global__ __launch_bounds__(256) void ce_kernel(const float* __restrict__ logit
     }
 }
 
-// loss[0] = (sum_r nll[r]) * inv_rows, one block, fixed reduction order.
-__global__ __launch_bounds__(256) void mean_kernel(const float* __restrict__ nll, int rows, float inv_rows,
-                                                   float* __restrict__ loss) {
-    __shared__ float part[4];
-    float s = 0.0f;
-    for (int i = threadIdx.x; i < rows; i += 256) s += nll[i];
-    s = tfd::wave_sum(s);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
-    __syncthreads();
-    if (threadIdx.x == 0) loss[0] = ((part[0] + part[1]) + (part[2] + part[3])) * inv_rows;
+// With `ticket` (MODE 0 and 2): every block counts itself in once its rows'
+// nll are written, and the block that arrives last computes the mean loss
+// with block_mean and resets the counter for the next launch.  nll and the
+// counter go through agent-scope relaxed atomics (coherent across XCDs, no
+// cache maintenance); a block's stores have completed (vmcnt 0 in every
+// thread, then the barrier) before it counts itself in.  (A device-scope
+// fence instead writes back and invalidates the XCD's L2 in every block.)
+template <int NC, int MODE>
+__global__ __launch_bounds__(256) void ce_kernel(const float* __restrict__ logits, const int64_t* __restrict__ targets,
+                                                 const float* __restrict__ lse_in, const float* __restrict__ grad_loss,
+                                                 float* __restrict__ lse_out, float* __restrict__ nll,
+                                                 float* __restrict__ dlogits, int rows, int cols, float inv_rows,
+                                                 int vec, float nll_max, int strict, float* __restrict__ loss,
+                                                 unsigned* __restrict__ ticket) {
+    const int r = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (r < rows) ce_row<NC, MODE>(logits, targets, lse_in, grad_loss, lse_out, nll, dlogits, r, cols, inv_rows,
+                                   vec, nll_max, strict);
+    if (MODE != 1 && ticket != nullptr) {
+        __shared__ int last;
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+        __syncthreads();
+        if (last) {
+            block_mean(nll, rows, inv_rows, loss);
+            if (threadIdx.x == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -303,10 +341,24 @@ int chunks_for(int64_t cols) {
     return 0;
 }
 
+// The mean loss by a separate one-block launch: for grids over
+// kTicketMaxBlocks blocks, whose arrivals on one counter (one atomic per
+// block, serialised) would cost more than the launch (1024 blocks: ~10 us).
+constexpr int kTicketMaxBlocks = 64;
+__global__ __launch_bounds__(256) void mean_kernel(const float* __restrict__ nll, int rows, float inv_rows,
+                                                   float* __restrict__ loss) {
+    block_mean(nll, rows, inv_rows, loss);
+}
+
 template <int MODE>
 tf_status launch_ce(tf_ctx* ctx, const float* logits, const int64_t* targets, const float* lse_in,
                     const float* grad_loss, float* lse_out, float* nll, float* dlogits, int64_t rows, int64_t cols,
-                    int flags = 0) {
+                    int flags = 0, float* loss = nullptr) {
+    // With `loss`: the mean loss too, by the kernel's last block when the
+    // grid is small, else by mean_kernel after it.
+    const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    const bool in_kernel = loss != nullptr && blocks <= kTicketMaxBlocks;
+    unsigned* ticket = in_kernel ? ctx->tickets + tfh::kTicketCE : nullptr;
     // -log(1e-9f) with the host's logf, as the module computes it.
     const float nll_max = (flags & TF_CE_CLAMP) ? -std::log(1e-9f) : INFINITY;
     const int strict = (flags & TF_CE_STRICT) ? 1 : 0;
@@ -316,7 +368,7 @@ tf_status launch_ce(tf_ctx* ctx, const float* logits, const int64_t* targets, co
 #define TF_CE_LAUNCH(NC)                                                                              \
     ce_kernel<NC, MODE><<<grid, 256, 0, ctx->stream>>>(logits, targets, lse_in, grad_loss, lse_out, nll, \
                                                          dlogits, (int)rows, (int)cols, inv_rows, vec, nll_max, \
-                                                         strict)
+                                                         strict, loss, ticket)
     switch (chunks_for(cols)) {
     case 1: TF_CE_LAUNCH(1); break;
     case 2: TF_CE_LAUNCH(2); break;
@@ -325,7 +377,10 @@ tf_status launch_ce(tf_ctx* ctx, const float* logits, const int64_t* targets, co
     default: TF_CE_LAUNCH(0); break;
     }
 #undef TF_CE_LAUNCH
-    return tfh::check_launch("ce_kernel");
+    tf_status st = tfh::check_launch("ce_kernel");
+    if (st != TF_OK || loss == nullptr || in_kernel) return st;
+    mean_kernel<<<1, 256, 0, ctx->stream>>>(nll, (int)rows, inv_rows, loss);
+    return tfh::check_launch("mean_kernel");
 }
 
 // ---------------------------------------------------------------------------
@@ -406,10 +461,7 @@ tf_status tf_ce_fwd(tf_ctx* ctx, const float* logits, const int64_t* targets, fl
     if (st != TF_OK) return st;
     float* nll = reinterpret_cast<float*>(ctx->ws);
     TF_REQUIRE((flags & ~TF_CE_MODULE) == 0, "tf_ce_fwd: unknown flags");
-    st = launch_ce<0>(ctx, logits, targets, nullptr, nullptr, lse, nll, nullptr, rows, cols, flags);
-    if (st != TF_OK) return st;
-    mean_kernel<<<1, 256, 0, ctx->stream>>>(nll, (int)rows, (float)(1.0 / (double)rows), loss);
-    return tfh::check_launch("mean_kernel");
+    return launch_ce<0>(ctx, logits, targets, nullptr, nullptr, lse, nll, nullptr, rows, cols, flags, loss);
 }
 
 tf_status tf_ce_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets, const float* lse,
@@ -431,10 +483,7 @@ tf_status tf_ce_fwd_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets
     if (st != TF_OK) return st;
     float* nll = reinterpret_cast<float*>(ctx->ws);
     TF_REQUIRE((flags & ~TF_CE_MODULE) == 0, "tf_ce_fwd_bwd: unknown flags");
-    st = launch_ce<2>(ctx, logits, targets, nullptr, nullptr, nullptr, nll, dlogits, rows, cols, flags);
-    if (st != TF_OK) return st;
-    mean_kernel<<<1, 256, 0, ctx->stream>>>(nll, (int)rows, (float)(1.0 / (double)rows), loss);
-    return tfh::check_launch("mean_kernel");
+    return launch_ce<2>(ctx, logits, targets, nullptr, nullptr, nullptr, nll, dlogits, rows, cols, flags, loss);
 }
 
 tf_status tf_argmax_rows(tf_ctx* ctx, const float* x, int64_t* pred, const int64_t* labels, int64_t* correct,

@@ -193,6 +193,11 @@ tf_status tf_hip_init(int device, tf_ctx** out) {
     TF_HIP_CHECK(hipDeviceGetDefaultMemPool(&ctx->pool, device));
     uint64_t threshold = UINT64_MAX;  // keep freed blocks cached
     TF_HIP_CHECK(hipMemPoolSetAttribute(ctx->pool, hipMemPoolAttrReleaseThreshold, &threshold));
+    TF_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&ctx->tickets), tfh::kTickets * sizeof(unsigned)));
+    zero_bytes_kernel<<<1, 256, 0, ctx->stream>>>(reinterpret_cast<uint8_t*>(ctx->tickets),
+                                                  tfh::kTickets * sizeof(unsigned));
+    TF_HIP_CHECK(hipGetLastError());
+    TF_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     *out = ctx;
     return TF_OK;
 }
@@ -218,6 +223,7 @@ tf_status tf_hip_shutdown(tf_ctx* ctx) {
         (void)hipStreamSynchronize(ctx->own_stream);
         (void)hipStreamDestroy(ctx->own_stream);
     }
+    if (ctx->tickets) (void)hipFree(ctx->tickets);
     delete ctx;
     return TF_OK;
 }

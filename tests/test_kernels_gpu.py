@@ -163,6 +163,32 @@ def test_gemm_epilogues(ctx):
     assert_close(got, np.broadcast_to(bias, (M, N)), RTOL32, "K=0")
 
 
+@pytest.mark.parametrize("ta,tb", [(False, True), (True, False), (False, False)])
+@pytest.mark.parametrize("M,N,K", [(33, 65, 2048), (31, 1, 1000), (128, 1024, 1024), (64, 256, 784), (5, 7, 129)])
+def test_gemm_small_path_repeatable(ctx, ta, tb, M, N, K):
+    """Products of the small fp32 path (32 x 32 tiles, K over up to 32 chunk
+    groups whose partials the tile's last-arriving block adds in chunk
+    order): within fp32 tolerance of float64, and bit-identical across calls
+    interleaved with another product that reuses the tiles' arrival counters
+    (each tile's counter must be back at zero after every call)."""
+    ops = _ops()
+    seed = synth.seed(2, 9) + M + N + K
+    a = synth.normal(seed, (K, M) if ta else (M, K))
+    b = synth.normal(seed + 1, (N, K) if tb else (K, N))
+    o = synth.normal(seed + 2, (48, 700))
+    da, db, dc = ctx.array(a), ctx.array(b), ctx.empty((M, N))
+    do, dw, dz = ctx.array(o), ctx.array(synth.normal(seed + 3, (700, 96))), ctx.empty((48, 96))
+    outs = []
+    for _ in range(3):
+        ops.gemm(da, db, dc, trans_a=ta, trans_b=tb)
+        outs.append(dc.numpy())
+        ops.gemm(do, dw, dz)
+    assert_close(outs[0], _gemm_truth(a, b, ta, tb), RTOL32, f"small gemm {M}x{N}x{K}")
+    for r in (1, 2):
+        assert_bitexact(outs[r], outs[0], f"call {r} vs call 0")
+    assert_close(dz.numpy(), _gemm_truth(o, synth.normal(seed + 3, (700, 96)), False, False), RTOL32, "other")
+
+
 def test_gemm_splitk_with_epilogue(ctx):
     a = synth.normal(41, (64, 8192))
     b = synth.normal(42, (8192, 64))
