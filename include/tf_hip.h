@@ -350,6 +350,28 @@ tf_status tf_col2im(tf_ctx* ctx, const void* col, void* dx, int64_t N, int64_t C
                     int64_t pad_w, int64_t dilation_h, int64_t dilation_w, int64_t outH, int64_t outW,
                     int dtype);
 
+/* Conv2d forward without a col buffer (implicit GEMM; replaces
+ * nn/Conv2d.cpp:101-139's launch_im2col + per-image launch_gemm_tiled_16x16 +
+ * launch_bias_add): y[N][Cout][outH][outW] = conv(x[N][C][H][W],
+ * w[Cout][C][kH][kW]) + bias[co] (bias may be NULL), then max(., 0) when
+ * relu != 0.  Float32.  TF_ERR_UNSUPPORTED when Cout x C*kH*kW filter rows
+ * and the input rows of 128 output pixels (all channels, padded width) do not
+ * fit the 160 KB of LDS; the caller then uses tf_im2col + tf_gemm_ex. */
+tf_status tf_conv2d_fwd(tf_ctx* ctx, const float* x, const float* w, const float* bias, float* y, int64_t N,
+                        int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t stride_h,
+                        int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dilation_h, int64_t dilation_w,
+                        int relu);
+/* Conv2d weight gradient without a col buffer (implicit GEMM; replaces
+ * nn/Conv2d.cpp:140-260's launch_im2col + per-sample GEMM + host
+ * accumulation): dw[Cout][C][kH][kW] = sum over images and output pixels of
+ * dy[n][co][p] * col[n][k][p], col gathered from x.  Float32; per-block
+ * partials are summed in a fixed order (deterministic).  TF_ERR_UNSUPPORTED
+ * when the dy tile, tap tables and input patch do not fit the LDS. */
+tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, float* dw, int64_t N, int64_t C,
+                               int64_t H, int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t stride_h,
+                               int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dilation_h,
+                               int64_t dilation_w);
+
 /* ---------------------------------------------------------------------------
  * Layout kernels over contiguous data viewed as [outer][reduce][inner].
  * ------------------------------------------------------------------------- */

@@ -387,8 +387,18 @@ std::vector<Tensor> Conv2dBackward::apply(std::vector<Tensor>&& grads) {
         const int dev = dy.device().index;
         if (wants(*this, 1)) {
             dw = Tensor::empty(w.shape(), Dtype::Float32, dy.device());
-            hip::gemm_ex(dev, false, true, g_.Cout, KK, P, dy.data(), P, g_.Cout * P, saved.data(), P, KK * P,
-                         dw.data(), KK, 0, g_.N, true, dy.dtype(), Dtype::Float32, TF_EPI_NONE, nullptr);
+            // With the input saved (implicit forward): the implicit weight
+            // gradient, else col is formed here for the GEMM.
+            if (!saved_input_ || !hip::conv2d_backward_weight_implicit(saved, dy, dw, g_.sh, g_.sw, g_.ph, g_.pw,
+                                                                      g_.dh, g_.dw)) {
+                Tensor col = saved;
+                if (saved_input_) {
+                    col = Tensor::empty(Shape{g_.N, KK, P}, Dtype::Float32, dy.device());
+                    hip::im2col(saved, col, g_.kH, g_.kW, g_.sh, g_.sw, g_.ph, g_.pw, g_.dh, g_.dw);
+                }
+                hip::gemm_ex(dev, false, true, g_.Cout, KK, P, dy.data(), P, g_.Cout * P, col.data(), P, KK * P,
+                             dw.data(), KK, 0, g_.N, true, dy.dtype(), Dtype::Float32, TF_EPI_NONE, nullptr);
+            }
         }
         if (has_bias_ && wants(*this, 2)) {
             db = Tensor::empty(Shape{g_.Cout}, Dtype::Float32, dy.device());

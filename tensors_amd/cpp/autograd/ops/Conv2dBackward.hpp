@@ -3,7 +3,9 @@
 //   dW = sum_n dY[n] col[n]^T     one batch-reduced MFMA GEMM
 //   dcol[n] = W^T dY[n]           one batched GEMM, then dX = col2im(dcol)
 //   db = sum_{n,h,w} dY           deterministic channel reduction
-// col = im2col(x) is saved from the forward.  Outputs follow
+// The forward saves col = im2col(x) when it built one (im2col + GEMM), or x
+// when it ran the implicit-GEMM kernel (no col buffer); then the backward
+// forms col for dW itself.  Outputs follow
 // next_edges_ = {x, W, b}; an empty edge skips that gradient (e.g. dX of the
 // network input).
 #pragma once
@@ -22,10 +24,10 @@ struct ConvGeometry {
 
 class Conv2dBackward : public Node {
 public:
-    // GPU: `x_or_col` is the im2col matrix [N, Cin*kH*kW, outH*outW];
-    // CPU: the input itself.
-    Conv2dBackward(const Tensor& x_or_col, const Tensor& weight, bool has_bias, ConvGeometry g)
-        : saved_(x_or_col), w_(weight), has_bias_(has_bias), g_(g) {}
+    // GPU: `x_or_col` is the im2col matrix [N, Cin*kH*kW, outH*outW], or the
+    // input when `saved_input` (implicit forward); CPU: the input itself.
+    Conv2dBackward(const Tensor& x_or_col, const Tensor& weight, bool has_bias, ConvGeometry g, bool saved_input = false)
+        : saved_(x_or_col), w_(weight), has_bias_(has_bias), g_(g), saved_input_(saved_input) {}
     std::vector<Tensor> apply(std::vector<Tensor>&& grads) override;
     void release_saved() override { saved_.reset(); w_.reset(); }
 
@@ -33,6 +35,7 @@ private:
     SavedTensor saved_, w_;
     bool has_bias_;
     ConvGeometry g_;
+    bool saved_input_ = false;
 };
 
 }  // namespace tensorforge

@@ -428,6 +428,37 @@ void colsum(const Tensor& dy, Tensor& db) {
     check(tf_colsum(ctx_of(dy), static_cast<const float*>(dy.data()), static_cast<float*>(db.data()), r, c), "hip::colsum");
 }
 
+bool conv2d_forward_implicit(const Tensor& x, const Tensor& w, const Tensor* bias, Tensor& y, int64_t sh, int64_t sw,
+                             int64_t ph, int64_t pw, int64_t dh, int64_t dw, bool relu) {
+    require_gpu(x, "hip::conv2d_forward"); require_gpu(w, "hip::conv2d_forward"); require_gpu(y, "hip::conv2d_forward");
+    require(x.dtype() == Dtype::Float32 && w.dtype() == Dtype::Float32 && y.dtype() == Dtype::Float32,
+            "hip::conv2d_forward: Float32 only");
+    const auto& xs = x.shape();
+    const auto& ws = w.shape();
+    const int st = tf_conv2d_fwd(ctx_of(x), static_cast<const float*>(x.data()), static_cast<const float*>(w.data()),
+                                 bias ? static_cast<const float*>(bias->data()) : nullptr, static_cast<float*>(y.data()),
+                                 xs[0], xs[1], xs[2], xs[3], ws[0], ws[2], ws[3], sh, sw, ph, pw, dh, dw, relu ? 1 : 0);
+    if (st == TF_ERR_UNSUPPORTED) return false;
+    check(st, "hip::conv2d_forward");
+    return true;
+}
+
+bool conv2d_backward_weight_implicit(const Tensor& x, const Tensor& dy, Tensor& dw, int64_t sh, int64_t sw, int64_t ph,
+                                     int64_t pw, int64_t dh, int64_t dwl) {
+    require_gpu(x, "hip::conv2d_backward_weight"); require_gpu(dy, "hip::conv2d_backward_weight");
+    require_gpu(dw, "hip::conv2d_backward_weight");
+    require(x.dtype() == Dtype::Float32 && dy.dtype() == Dtype::Float32 && dw.dtype() == Dtype::Float32,
+            "hip::conv2d_backward_weight: Float32 only");
+    const auto& xs = x.shape();
+    const auto& ws = dw.shape();
+    const int st = tf_conv2d_bwd_weight(ctx_of(x), static_cast<const float*>(x.data()),
+                                        static_cast<const float*>(dy.data()), static_cast<float*>(dw.data()), xs[0],
+                                        xs[1], xs[2], xs[3], ws[0], ws[2], ws[3], sh, sw, ph, pw, dh, dwl);
+    if (st == TF_ERR_UNSUPPORTED) return false;
+    check(st, "hip::conv2d_backward_weight");
+    return true;
+}
+
 void chansum_nchw(const Tensor& dy, Tensor& db) {
     require_gpu(dy, "hip::chansum");
     require(dy.shape().ndim() == 4, "hip::chansum: NCHW");

@@ -122,6 +122,14 @@ void expand_dim(const Tensor& up, Tensor& out, int64_t outer, int64_t reduce, in
 void transpose2d(const Tensor& x, Tensor& out, int64_t batch, int64_t rows, int64_t cols);
 void colsum(const Tensor& dy, Tensor& db);
 void chansum_nchw(const Tensor& dy, Tensor& db);
+// Implicit-GEMM convolution forward (tf_conv2d_fwd): false when the shape
+// does not fit the kernel's LDS (nothing was launched), else y is written.
+bool conv2d_forward_implicit(const Tensor& x, const Tensor& w, const Tensor* bias, Tensor& y, int64_t sh, int64_t sw,
+                             int64_t ph, int64_t pw, int64_t dh, int64_t dw, bool relu);
+// Implicit-GEMM weight gradient (tf_conv2d_bwd_weight): false when the shape
+// does not fit the kernel's LDS (nothing was launched), else dw is written.
+bool conv2d_backward_weight_implicit(const Tensor& x, const Tensor& dy, Tensor& dw, int64_t sh, int64_t sw, int64_t ph,
+                                     int64_t pw, int64_t dh, int64_t dwl);
 
 // ---- conv index maps -----------------------------------------------------
 void im2col(const Tensor& x, Tensor& col, int64_t kH, int64_t kW, int64_t sh, int64_t sw, int64_t ph, int64_t pw,

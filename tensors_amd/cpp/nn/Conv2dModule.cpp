@@ -38,7 +38,13 @@ Tensor conv2d_forward(const Tensor& x, const Tensor& w, const Tensor* bias, int6
 
     Tensor y = Tensor::empty(Shape{g.N, g.Cout, g.outH, g.outW}, Dtype::Float32, x.device());
     Tensor saved = x;
-    if (x.device().type == DeviceType::CUDA) {
+    bool saved_input = false;
+    if (x.device().type == DeviceType::CUDA &&
+        hip::conv2d_forward_implicit(x, w, bias, y, sh, sw, ph, pw, dh, dw, relu)) {
+        // Implicit GEMM: no col buffer; the backward forms col from x if it
+        // needs dW.
+        saved_input = true;
+    } else if (x.device().type == DeviceType::CUDA) {
         Tensor col = Tensor::empty(Shape{g.N, KK, P}, Dtype::Float32, x.device());
         hip::im2col(x, col, g.kH, g.kW, sh, sw, ph, pw, dh, dw);
         hip::gemm_ex(x.device().index, false, false, g.Cout, P, KK, w.data(), KK, 0, col.data(), P, KK * P, y.data(), P,
@@ -72,7 +78,7 @@ Tensor conv2d_forward(const Tensor& x, const Tensor& w, const Tensor* bias, int6
                     }
     }
     if (x.requires_grad() || w.requires_grad() || (bias && bias->requires_grad())) {
-        auto node = std::make_shared<Conv2dBackward>(saved, w, bias != nullptr, g);
+        auto node = std::make_shared<Conv2dBackward>(saved, w, bias != nullptr, g, saved_input);
         std::vector<Edge> edges = {wiring::accumulator_edge(x), wiring::accumulator_edge(w),
                                    bias ? wiring::accumulator_edge(*bias) : Edge(nullptr, 0)};
         if (relu) {

@@ -56,6 +56,9 @@ tf_status hip_error(hipError_t e, const char* what);
 
 // Make sure ctx->ws holds at least `bytes`; returns TF_OK or an error.
 tf_status ensure_workspace(tf_ctx* ctx, size_t bytes);
+// out[m][n] (row stride ldc) = sum over s < splits of part[s][m][n] in a
+// fixed order (16 split groups, each ascending, combined in a tree).
+tf_status sum_partials(tf_ctx* ctx, const float* part, int64_t splits, int64_t M, int64_t N, float* out, int64_t ldc);
 // out[j] = sum_k part[k * W + j] (fixed order) for j < W; columns j < split
 // go to out_lo[j], the rest to out_hi[j - split].  Launched on ctx->stream.
 tf_status partial_rows_sum(tf_ctx* ctx, const float* part, float* out_lo, float* out_hi, int64_t K, int64_t W,

@@ -199,6 +199,309 @@ __global__ __launch_bounds__(256) void col2im_plane_kernel(const T* __restrict__
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Implicit-GEMM convolution forward (fp32, NCHW, MFMA): y[n][co][p] =
+// epi(sum_k w[co][k] * col[n][k][p]) with col gathered from x on the fly, so
+// no col buffer is written (nn/Conv2d.cpp:101-139 materialises it with
+// launch_im2col, cuda/kernels/im2col.cu:57-99, then multiplies per image).
+//
+// Block (8 waves, two per SIMD) = MT output channels x NP consecutive output
+// pixels of one image, NP = 128 (MT = 64) or 256 (MT = 32), so each wave
+// owns one 32 x 32 sub-tile.  The block stages in LDS, once:
+//   * the MT x K filter rows, split by k parity: wk[row][h][j] = w[row][2j+h]
+//     (row stride KH2 + 4 words), so lane half h reads four consecutive k
+//     steps' operands with one 16-byte read;
+//   * the tap table, split the same way: koff[h][j] = patch offset of tap
+//     k = 2j + h = (ci, kh, kw), i.e. (ci PH + kh dh) PW + kw dw;
+//   * the input patch its pixels read: every channel, input rows ih_lo ..
+//     ih_lo + PH - 1 of its output rows, each padded to PW = W + 2 pw
+//     columns with zeros.
+// Pixel (oh, ow) then reads tap k at koff + ((oh - oh_lo) sh) PW + ow sw:
+// per four k steps one filter read, one tap read and four patch reads feed
+// four v_mfma_f32_32x32x2f32 (lane half h supplies k = 2j + h of both
+// operands).  K is padded to a multiple of 8 with zero filter columns (their
+// taps read a valid offset).  Staged loads are issued 16 at a time into
+// registers before their LDS stores.  Epilogue: + bias[co], ReLU.
+// ---------------------------------------------------------------------------
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+constexpr int kIgThreads = 512;
+template <int MT>
+constexpr int ig_pixels() { return MT == 64 ? 128 : 256; }
+
+template <int MT>
+__global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const float* __restrict__ x,
+                                                                       const float* __restrict__ w,
+                                                                       const float* __restrict__ bias,
+                                                                       float* __restrict__ y, ConvGeom g, int Cout,
+                                                                       int K, int Kp, int PH, int PW,
+                                                                       int tiles_per_image, int relu) {
+    extern __shared__ float smem[];
+    constexpr int NP = ig_pixels<MT>();
+    constexpr int MSUB = MT / 32;
+    const int KH2 = Kp / 2;                     // k steps per half
+    const int RS = 2 * (KH2 + 4);               // filter row stride (words)
+    float* wk = smem;                           // [MT][2][KH2 + 4]
+    int* koff = reinterpret_cast<int*>(wk + MT * RS);   // [2][KH2]
+    float* patch = reinterpret_cast<float*>(koff + Kp); // [C][PH][PW]
+    const int P = (int)(g.outH * g.outW), outW = (int)g.outW;
+    const int n = blockIdx.x / tiles_per_image, pt = blockIdx.x - n * tiles_per_image;
+    const int p0 = pt * NP, p_end = min(p0 + NP, P);
+    const int co0 = blockIdx.y * MT;
+    const int oh_lo = p0 / outW;
+    const int ih_lo = oh_lo * (int)g.sh - (int)g.ph;
+    const int C = (int)g.C, H = (int)g.H, W = (int)g.W, kHW = (int)(g.kH * g.kW), kW = (int)g.kW;
+    const int t = threadIdx.x;
+
+    constexpr int kStage = 16;
+    for (int base = t; base < MT * Kp; base += kIgThreads * kStage) {
+        float v[kStage];
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int i = base + kIgThreads * u;
+            const int r = i / Kp, k = i - r * Kp;
+            v[u] = (i < MT * Kp && co0 + r < Cout && k < K) ? w[(int64_t)(co0 + r) * K + k] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int i = base + kIgThreads * u;
+            if (i < MT * Kp) {
+                const int r = i / Kp, k = i - r * Kp;
+                wk[r * RS + (k & 1) * (KH2 + 4) + (k >> 1)] = v[u];
+            }
+        }
+    }
+    for (int k = t; k < Kp; k += kIgThreads) {
+        const int kc = min(k, K - 1);
+        const int ci = kc / kHW, rem = kc - ci * kHW, kh = rem / kW, kw = rem - kh * kW;
+        koff[(k & 1) * KH2 + (k >> 1)] = (ci * PH + kh * (int)g.dh) * PW + kw * (int)g.dw;
+    }
+    const float* xn = x + (int64_t)n * C * H * W;
+    const int plane = PH * PW;
+    for (int base = t; base < C * plane; base += kIgThreads * kStage) {
+        float v[kStage];
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int i = base + kIgThreads * u;
+            const int ci = i / plane, rr = (i - ci * plane) / PW, cc = i - ci * plane - rr * PW;
+            const int ih = ih_lo + rr, iw = cc - (int)g.pw;
+            v[u] = (i < C * plane && ih >= 0 && ih < H && iw >= 0 && iw < W) ? xn[((int64_t)ci * H + ih) * W + iw]
+                                                                              : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int i = base + kIgThreads * u;
+            if (i < C * plane) patch[i] = v[u];
+        }
+    }
+    __syncthreads();
+
+    const int wave = t >> 6, lane = t & 63, l32 = lane & 31, half = lane >> 5;
+    const int m_sub = wave % MSUB, n_sub = wave / MSUB;
+    const int pp = p0 + n_sub * 32 + l32;
+    int pix_off;
+    {
+        const int q = pp < p_end ? pp : p0;
+        const int oh = q / outW, ow = q - oh * outW;
+        pix_off = (oh - oh_lo) * (int)g.sh * PW + ow * (int)g.sw;
+    }
+    v16f acc = v16f{};
+    const float* wrow = wk + (m_sub * 32 + l32) * RS + half * (KH2 + 4);
+    const int* krow = koff + half * KH2;
+    const float* pbase = patch + pix_off;
+    // KH2 is a multiple of 4 (Kp a multiple of 8).
+    for (int j = 0; j < KH2; j += 4) {
+        const v4f a = *reinterpret_cast<const v4f*>(wrow + j);
+        const v4i ko = *reinterpret_cast<const v4i*>(krow + j);
+        const float b0 = pbase[ko.x], b1 = pbase[ko.y], b2 = pbase[ko.z], b3 = pbase[ko.w];
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b1, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b2, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b3, acc, 0, 0, 0);
+    }
+
+    if (pp >= p_end) return;
+    float* yn = y + (int64_t)n * Cout * P;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int co = co0 + m_sub * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (co >= Cout) continue;
+        float v = acc[r] + (bias ? bias[co] : 0.0f);
+        if (relu) v = fmaxf(v, 0.0f);
+        yn[(int64_t)co * P + pp] = v;
+    }
+}
+
+// LDS layout of conv_fwd_implicit_kernel, or 0 when it does not fit.
+size_t implicit_lds_bytes(const ConvGeom& g, int MT, int K, int& Kp, int& PH, int& PW) {
+    Kp = (K + 7) / 8 * 8;
+    const int np = MT == 64 ? ig_pixels<64>() : ig_pixels<32>();
+    const int64_t rows_max = (np - 1) / g.outW + 2;               // output rows a pixel run can touch
+    const int64_t ph_rows = std::min<int64_t>(rows_max, g.outH) - 1;
+    PH = (int)(ph_rows * g.sh + (g.kH - 1) * g.dh + 1);
+    PW = (int)(g.W + 2 * g.pw);
+    const int64_t floats = (int64_t)MT * 2 * (Kp / 2 + 4) + Kp + g.C * (int64_t)PH * PW;
+    const int64_t bytes = floats * 4;
+    return bytes <= 160 * 1024 ? (size_t)bytes : 0;
+}
+
+// ---------------------------------------------------------------------------
+// Implicit-GEMM convolution weight gradient (fp32, NCHW, MFMA):
+//   dw[co][k] = sum_n sum_p dy[n][co][p] * col[n][k][p]
+// with col gathered from x on the fly (nn/Conv2d.cpp:140-260 builds col with
+// launch_im2col and multiplies per image).  Blocks tile the pixels as the
+// forward does (MT channels x NP pixels of one image, 8 waves); each block
+// stages dy's MT x NP tile (split by pixel parity, like the forward's
+// filter rows), the pixel-offset table poff[h][j] of pixel 2j + h, the tap
+// table koff[k] and the input patch, then computes its MT x K partial with
+// v_mfma_f32_32x32x2f32 over its pixels (lane half h supplies pixel 2j + h
+// of both operands: dy[co][p] and patch[koff[k] + poff[p]]).  Work items are
+// (32 x 32 output tile, pixel slice): with fewer tiles than waves, each
+// tile's pixels are split over several waves and their sums combined in LDS
+// in slice order.  The block writes its partial to part[block][co][k]; the
+// partials are then summed in a fixed order (tfh::sum_partials).  Pixels
+// past the image's end carry dy = 0.
+// ---------------------------------------------------------------------------
+template <int MT>
+__global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(const float* __restrict__ x,
+                                                                              const float* __restrict__ dy,
+                                                                              float* __restrict__ part, ConvGeom g,
+                                                                              int Cout, int K, int Kc, int PH, int PW,
+                                                                              int tiles_per_image, int slices) {
+    extern __shared__ float smem[];
+    constexpr int NP = ig_pixels<MT>();
+    constexpr int NH = NP / 2;
+    constexpr int RS = 2 * (NH + 4);
+    float* dyt = smem;                                     // [MT][2][NH + 4]
+    int* poff = reinterpret_cast<int*>(dyt + MT * RS);      // [2][NH]
+    int* koff = poff + NP;                                  // [Kc]
+    float* patch = reinterpret_cast<float*>(koff + Kc);    // [C][PH][PW]
+    const int P = (int)(g.outH * g.outW), outW = (int)g.outW;
+    const int n = blockIdx.x / tiles_per_image, pt = blockIdx.x - n * tiles_per_image;
+    const int p0 = pt * NP, p_end = min(p0 + NP, P);
+    const int co0 = blockIdx.y * MT;
+    const int oh_lo = p0 / outW;
+    const int ih_lo = oh_lo * (int)g.sh - (int)g.ph;
+    const int C = (int)g.C, H = (int)g.H, W = (int)g.W, kHW = (int)(g.kH * g.kW), kW = (int)g.kW;
+    const int t = threadIdx.x;
+    const int plane = PH * PW;
+    float* red = patch + C * plane;                         // [8][16][64] when slices > 1
+
+    constexpr int kStage = 16;
+    const float* dyn = dy + (int64_t)n * Cout * P;
+    for (int base = t; base < MT * NP; base += kIgThreads * kStage) {
+        float v[kStage];
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int i = base + kIgThreads * u;
+            const int r = i / NP, q = i - r * NP;
+            v[u] = (i < MT * NP && co0 + r < Cout && p0 + q < p_end) ? dyn[(int64_t)(co0 + r) * P + p0 + q] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int i = base + kIgThreads * u;
+            if (i < MT * NP) {
+                const int r = i / NP, q = i - r * NP;
+                dyt[r * RS + (q & 1) * (NH + 4) + (q >> 1)] = v[u];
+            }
+        }
+    }
+    for (int q = t; q < NP; q += kIgThreads) {
+        const int pp = p0 + q < p_end ? p0 + q : p0;
+        const int oh = pp / outW, ow = pp - oh * outW;
+        poff[(q & 1) * NH + (q >> 1)] = (oh - oh_lo) * (int)g.sh * PW + ow * (int)g.sw;
+    }
+    for (int k = t; k < Kc; k += kIgThreads) {
+        const int kc = min(k, K - 1);
+        const int ci = kc / kHW, rem = kc - ci * kHW, kh = rem / kW, kw = rem - kh * kW;
+        koff[k] = (ci * PH + kh * (int)g.dh) * PW + kw * (int)g.dw;
+    }
+    const float* xn = x + (int64_t)n * C * H * W;
+    for (int base = t; base < C * plane; base += kIgThreads * kStage) {
+        float v[kStage];
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int i = base + kIgThreads * u;
+            const int ci = i / plane, rr = (i - ci * plane) / PW, cc = i - ci * plane - rr * PW;
+            const int ih = ih_lo + rr, iw = cc - (int)g.pw;
+            v[u] = (i < C * plane && ih >= 0 && ih < H && iw >= 0 && iw < W) ? xn[((int64_t)ci * H + ih) * W + iw]
+                                                                              : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int i = base + kIgThreads * u;
+            if (i < C * plane) patch[i] = v[u];
+        }
+    }
+    __syncthreads();
+
+    const int wave = t >> 6, lane = t & 63, l32 = lane & 31, half = lane >> 5;
+    const int TM = MT / 32, TK = Kc / 32, T = TM * TK;
+    const int steps = NH / slices;                          // pixel pairs per slice (a multiple of 4)
+    float* outp = part + (int64_t)blockIdx.x * Cout * K;
+    for (int item = wave; item < T * slices; item += kIgThreads / 64) {
+        const int tile = item / slices, sl = item - tile * slices;
+        const int tr = tile / TK, tc = tile - tr * TK;
+        const float* arow = dyt + (tr * 32 + l32) * RS + half * (NH + 4) + sl * steps;
+        const int* prow = poff + half * NH + sl * steps;
+        const float* pb = patch + koff[tc * 32 + l32];
+        v16f acc = v16f{};
+        for (int j = 0; j < steps; j += 4) {
+            const v4f a = *reinterpret_cast<const v4f*>(arow + j);
+            const v4i po = *reinterpret_cast<const v4i*>(prow + j);
+            const float b0 = pb[po.x], b1 = pb[po.y], b2 = pb[po.z], b3 = pb[po.w];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b0, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b1, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b2, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b3, acc, 0, 0, 0);
+        }
+        if (slices == 1) {
+            const int k = tc * 32 + l32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int co = co0 + tr * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (co < Cout && k < K) outp[(int64_t)co * K + k] = acc[r];
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) red[(item * 16 + r) * 64 + lane] = acc[r];
+        }
+    }
+    if (slices > 1) {
+        __syncthreads();
+        // Combine each tile's slices in slice order: one wave per tile.
+        for (int tile = wave; tile < T; tile += kIgThreads / 64) {
+            const int tr = tile / TK, tc = tile - tr * TK, k = tc * 32 + l32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float v = red[((tile * slices) * 16 + r) * 64 + lane];
+                for (int sl = 1; sl < slices; ++sl) v += red[((tile * slices + sl) * 16 + r) * 64 + lane];
+                const int co = co0 + tr * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (co < Cout && k < K) outp[(int64_t)co * K + k] = v;
+            }
+        }
+    }
+}
+
+// LDS layout of conv_bwd_weight_implicit_kernel, or 0 when it does not fit.
+size_t implicit_dw_lds_bytes(const ConvGeom& g, int MT, int K, int& Kc, int& PH, int& PW, int& slices) {
+    Kc = (K + 31) / 32 * 32;
+    const int np = MT == 64 ? ig_pixels<64>() : ig_pixels<32>();
+    const int64_t rows_max = (np - 1) / g.outW + 2;
+    const int64_t ph_rows = std::min<int64_t>(rows_max, g.outH) - 1;
+    PH = (int)(ph_rows * g.sh + (g.kH - 1) * g.dh + 1);
+    PW = (int)(g.W + 2 * g.pw);
+    const int tiles = (MT / 32) * (Kc / 32);
+    slices = 1;
+    while (tiles * slices * 2 <= kIgThreads / 64 && (np / 2) / (slices * 2) >= 4) slices *= 2;
+    const int64_t floats = (int64_t)MT * 2 * (np / 2 + 4) + np + Kc + g.C * (int64_t)PH * PW +
+                           (slices > 1 ? (int64_t)tiles * slices * 16 * 64 : 0);
+    const int64_t bytes = floats * 4;
+    return bytes <= 160 * 1024 ? (size_t)bytes : 0;
+}
+
 // The plane forms' 32-bit index arithmetic stays in range: every input
 // coordinate they form lies within +-2^24.
 bool plane_indices_fit(const ConvGeom& g) {
@@ -289,6 +592,105 @@ tf_status tf_col2im(tf_ctx* ctx, const void* col, void* dx, int64_t N, int64_t C
         return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_col2im: dtype must be Float32 or BFloat16");
     }
     return tfh::check_launch("col2im_kernel");
+}
+
+tf_status tf_conv2d_fwd(tf_ctx* ctx, const float* x, const float* w, const float* bias, float* y, int64_t N,
+                        int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t sh, int64_t sw,
+                        int64_t ph, int64_t pw, int64_t dh, int64_t dw, int relu) {
+    TF_CTX_CHECK(ctx);
+    ConvGeom g;
+    tf_status st = make_geom(g, N, C, H, W, kH, kW, sh, sw, ph, pw, dh, dw);
+    if (st != TF_OK) return st;
+    TF_REQUIRE(Cout > 0 && C > 0, "tf_conv2d_fwd: empty channel count");
+    if (N == 0) return TF_OK;
+    TF_REQUIRE(x && w && y, "tf_conv2d_fwd: null pointer");
+    const int64_t K = C * kH * kW;
+    TF_REQUIRE(K < (1 << 20) && N * C * H * W < (1LL << 31) && N * Cout * g.outH * g.outW < (1LL << 31) &&
+                   Cout < (1 << 20),
+               "tf_conv2d_fwd: extent beyond this kernel's 32-bit indexing");
+    const int MT = Cout <= 32 ? 32 : 64;
+    int Kp, PH, PW;
+    const size_t lds = implicit_lds_bytes(g, MT, (int)K, Kp, PH, PW);
+    if (lds == 0)
+        return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_conv2d_fwd: filter rows and input patch exceed the 160 KB of LDS "
+                                                  "(use tf_im2col + tf_gemm_ex)");
+    const int64_t P = g.outH * g.outW;
+    const int np = MT == 64 ? ig_pixels<64>() : ig_pixels<32>();
+    const int tpi = (int)((P + np - 1) / np);
+    TF_REQUIRE(N * tpi < (1LL << 31), "tf_conv2d_fwd: too many blocks");
+    const dim3 grid((unsigned)(N * tpi), (unsigned)((Cout + MT - 1) / MT));
+    // Dynamic LDS above 64 KB needs the attribute; set once per kernel to the
+    // whole 160 KB, before any launch (and any graph capture) uses it.
+    static const bool lds_ok = [] {
+        const int all = 160 * 1024;
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(conv_fwd_implicit_kernel<32>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, all) == hipSuccess &&
+               hipFuncSetAttribute(reinterpret_cast<const void*>(conv_fwd_implicit_kernel<64>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, all) == hipSuccess;
+    }();
+    if (!lds_ok) {
+        (void)hipGetLastError();
+        return tfh::set_error(TF_ERR_HIP, "tf_conv2d_fwd: hipFuncSetAttribute (dynamic LDS) failed");
+    }
+    if (MT == 32) {
+        conv_fwd_implicit_kernel<32><<<grid, kIgThreads, lds, ctx->stream>>>(x, w, bias, y, g, (int)Cout, (int)K, Kp, PH, PW,
+                                                                      tpi, relu);
+    } else {
+        conv_fwd_implicit_kernel<64><<<grid, kIgThreads, lds, ctx->stream>>>(x, w, bias, y, g, (int)Cout, (int)K, Kp, PH, PW,
+                                                                      tpi, relu);
+    }
+    return tfh::check_launch("conv_fwd_implicit_kernel");
+}
+
+tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, float* dw, int64_t N, int64_t C,
+                               int64_t H, int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t sh, int64_t sw,
+                               int64_t ph, int64_t pw, int64_t dh, int64_t dw_) {
+    TF_CTX_CHECK(ctx);
+    ConvGeom g;
+    tf_status st = make_geom(g, N, C, H, W, kH, kW, sh, sw, ph, pw, dh, dw_);
+    if (st != TF_OK) return st;
+    TF_REQUIRE(Cout > 0 && C > 0, "tf_conv2d_bwd_weight: empty channel count");
+    TF_REQUIRE(x && dy && dw, "tf_conv2d_bwd_weight: null pointer");
+    const int64_t K = C * kH * kW;
+    TF_REQUIRE(K < (1 << 20) && N * C * H * W < (1LL << 31) && N * Cout * g.outH * g.outW < (1LL << 31) &&
+                   Cout < (1 << 20),
+               "tf_conv2d_bwd_weight: extent beyond this kernel's 32-bit indexing");
+    if (N == 0) return tf_hip_fill_f32(ctx, dw, 0.0f, Cout * K);
+    const int MT = Cout <= 32 ? 32 : 64;
+    int Kc, PH, PW, slices;
+    const size_t lds = implicit_dw_lds_bytes(g, MT, (int)K, Kc, PH, PW, slices);
+    if (lds == 0)
+        return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_conv2d_bwd_weight: dy tile, tap tables and input patch exceed the "
+                                                  "160 KB of LDS (use tf_im2col + tf_gemm_ex)");
+    const int64_t P = g.outH * g.outW;
+    const int np = MT == 64 ? ig_pixels<64>() : ig_pixels<32>();
+    const int tpi = (int)((P + np - 1) / np);
+    const int64_t blocks = N * tpi;
+    TF_REQUIRE(blocks < (1LL << 31), "tf_conv2d_bwd_weight: too many blocks");
+    st = tfh::ensure_workspace(ctx, (size_t)blocks * Cout * K * sizeof(float));
+    if (st != TF_OK) return st;
+    float* part = reinterpret_cast<float*>(ctx->ws);
+    static const bool lds_ok = [] {
+        const int all = 160 * 1024;
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(conv_bwd_weight_implicit_kernel<32>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, all) == hipSuccess &&
+               hipFuncSetAttribute(reinterpret_cast<const void*>(conv_bwd_weight_implicit_kernel<64>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, all) == hipSuccess;
+    }();
+    if (!lds_ok) {
+        (void)hipGetLastError();
+        return tfh::set_error(TF_ERR_HIP, "tf_conv2d_bwd_weight: hipFuncSetAttribute (dynamic LDS) failed");
+    }
+    const dim3 grid((unsigned)blocks, (unsigned)((Cout + MT - 1) / MT));
+    if (MT == 32)
+        conv_bwd_weight_implicit_kernel<32><<<grid, kIgThreads, lds, ctx->stream>>>(x, dy, part, g, (int)Cout, (int)K,
+                                                                                   Kc, PH, PW, tpi, slices);
+    else
+        conv_bwd_weight_implicit_kernel<64><<<grid, kIgThreads, lds, ctx->stream>>>(x, dy, part, g, (int)Cout, (int)K,
+                                                                                   Kc, PH, PW, tpi, slices);
+    st = tfh::check_launch("conv_bwd_weight_implicit_kernel");
+    if (st != TF_OK) return st;
+    return tfh::sum_partials(ctx, part, blocks, Cout, K, dw, K);
 }
 
 }  // extern "C"

@@ -2429,6 +2429,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_wide_kernel(GemmParams p, i
 
 using KernelFn = void (*)(GemmParams);
 
+
 // fp32 GEMM with a short K (<= 32) and few rows (<= 64), A K-major and B
 // MN-major: a convolution over few input channels (W [Cout x Cin*k*k] times
 // each image's im2col block).  An MFMA tile would be mostly padding and one
@@ -2830,6 +2831,24 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
 }
 
 }  // namespace
+
+namespace tfh {
+
+tf_status sum_partials(tf_ctx* ctx, const float* part, int64_t splits, int64_t M, int64_t N, float* out, int64_t ldc) {
+    if (M == 0 || N == 0) return TF_OK;
+    GemmParams p{};
+    p.partial = const_cast<float*>(part);
+    p.C = out;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.ldc = ldc;
+    p.alpha = 1.0f;
+    p.epi = TF_EPI_NONE;
+    splitk_reduce_wide_kernel<<<(unsigned)((M * N + 15) / 16), 256, 0, ctx->stream>>>(p, (int)splits);
+    return check_launch("splitk_reduce_wide_kernel");
+}
+
+}  // namespace tfh
 
 extern "C" {
 

@@ -277,6 +277,39 @@ def im2col(x, col, kH, kW, stride=(1, 1), pad=(0, 0), dil=(1, 1)):
     return col
 
 
+def conv2d_fwd(x, w, y, bias=None, stride=(1, 1), pad=(0, 0), dil=(1, 1), relu=False):
+    """y = conv(x, w) (+ bias, ReLU) by the implicit-GEMM kernel (no col
+    buffer); TFError with TF_ERR_UNSUPPORTED when the shape does not fit it."""
+    N, Cc, H, W = x.shape
+    Cout, Cw, kH, kW = w.shape
+    if Cw != Cc:
+        raise ValueError("conv2d_fwd: weight and input channel counts differ")
+    oh, ow = conv_out(H, kH, stride[0], pad[0], dil[0]), conv_out(W, kW, stride[1], pad[1], dil[1])
+    if tuple(y.shape) != (N, Cout, oh, ow):
+        raise ValueError("conv2d_fwd: y has the wrong shape")
+    if bias is not None and bias.size != Cout:
+        raise ValueError("conv2d_fwd: bias must have one entry per output channel")
+    call("tf_conv2d_fwd", _ctx(x), x.ptr, w.ptr, bias.ptr if bias is not None else None, y.ptr, N, Cc, H, W, Cout,
+         kH, kW, stride[0], stride[1], pad[0], pad[1], dil[0], dil[1], int(relu))
+    return y
+
+
+def conv2d_bwd_weight(x, dy, dw, stride=(1, 1), pad=(0, 0), dil=(1, 1)):
+    """dw = sum over images and pixels of dy (x) col(x), by the implicit-GEMM
+    kernel (no col buffer); TFError with TF_ERR_UNSUPPORTED when the shape
+    does not fit it."""
+    N, Cc, H, W = x.shape
+    Cout, Cw, kH, kW = dw.shape
+    if Cw != Cc:
+        raise ValueError("conv2d_bwd_weight: dw and input channel counts differ")
+    oh, ow = conv_out(H, kH, stride[0], pad[0], dil[0]), conv_out(W, kW, stride[1], pad[1], dil[1])
+    if tuple(dy.shape) != (N, Cout, oh, ow):
+        raise ValueError("conv2d_bwd_weight: dy has the wrong shape")
+    call("tf_conv2d_bwd_weight", _ctx(x), x.ptr, dy.ptr, dw.ptr, N, Cc, H, W, Cout, kH, kW, stride[0], stride[1],
+         pad[0], pad[1], dil[0], dil[1])
+    return dw
+
+
 def col2im(col, dx, kH, kW, stride=(1, 1), pad=(0, 0), dil=(1, 1)):
     N, Cc, H, W = dx.shape
     oh, ow = conv_out(H, kH, stride[0], pad[0], dil[0]), conv_out(W, kW, stride[1], pad[1], dil[1])

@@ -205,10 +205,11 @@ def _col2im64(col, shape, k, s, p):
     return dxp[:, :, p:p + H, p:p + W]
 
 
-def _cnn_step64(params, x, y):
+def _cnn_step64(params, x, y, keep=None):
     """Loss and gradients of the config-4 network in float64: the same math
     as the reference's conv loop (nn/conv2d_backward_test.cpp:50-106), the
-    Linear backward and the CE chain, summed exactly enough to judge fp32."""
+    Linear backward and the CE chain, summed exactly enough to judge fp32.
+    With `keep` a dict, the intermediates go into it."""
     w1, b1, w2, b2, wf, bf = [p.astype(np.float64) for p in params]
     B = x.shape[0]
     col1, oh1, ow1 = _im2col64(x, 3, 1, 1)
@@ -226,14 +227,50 @@ def _cnn_step64(params, x, y):
     g[np.arange(B), y] -= 1
     g /= B
     dwf, dbf = g.T @ f, g.sum(0)
-    dz2 = (g @ wf).reshape(z2.shape) * (z2 > 0)
+    dh2 = (g @ wf).reshape(z2.shape)
+    dz2 = dh2 * (z2 > 0)
     dw2 = np.einsum("nop,nkp->ok", dz2, col2).reshape(w2.shape)
     db2 = dz2.sum((0, 2))
     dh1 = _col2im64(np.einsum("ok,nop->nkp", w2.reshape(64, -1), dz2), h1.shape, 3, 2, 1)
     dz1 = dh1.reshape(z1.shape) * (z1 > 0)
     dw1 = np.einsum("nop,nkp->ok", dz1, col1).reshape(w1.shape)
     db1 = dz1.sum((0, 2))
+    if keep is not None:
+        keep.update(col1=col1, z1=z1, col2=col2, z2=z2, dh2=dh2, dh1=dh1.reshape(z1.shape), w2=w2, h1_shape=h1.shape)
     return loss, [dw1, db1, dw2, db2, dwf, dbf]
+
+
+def _relu_tie_envelope(k, delta_rel=1e-4):
+    """Bound on how far an fp32 step's conv gradients may sit from the
+    float64 ones because a ReLU mask differs where the pre-activation is
+    within delta_rel * rms of zero (a tie: 2 M conv2 pre-activations here,
+    the smallest |z| ~ 5e-9, far below fp32's rounding of a 288-term sum).
+    Flipping the mask at (n, c, p) moves dz by dh there: db by |dh|, dW row
+    c by |dh| |col[n, :, p]|, and, for conv2, conv1's upstream gradient by
+    |dh| |W2[c, :]| at that column's taps (then through conv1's mask into
+    its dW and db).  Returns per-element bounds for [dw1, db1, dw2, db2]."""
+    col1, z1, col2, z2, dh2, dh1, w2 = (k[n] for n in ("col1", "z1", "col2", "z2", "dh2", "dh1", "w2"))
+    env_dw1 = np.zeros((32, col1.shape[1]))
+    env_db1 = np.zeros(32)
+    env_dw2 = np.zeros((64, col2.shape[1]))
+    env_db2 = np.zeros(64)
+    t2 = np.argwhere(np.abs(z2) < delta_rel * np.sqrt(np.mean(z2 ** 2)))
+    spread = np.zeros_like(col2)                  # |change of dcol2| from conv2's ties
+    for n, c, p_ in t2:
+        a = abs(dh2[n, c, p_])
+        env_db2[c] += a
+        env_dw2[c] += a * np.abs(col2[n, :, p_])
+        spread[n, :, p_] += a * np.abs(w2.reshape(64, -1)[c])
+    if len(t2):
+        d1 = _col2im64(spread, k["h1_shape"], 3, 2, 1).reshape(z1.shape) * (z1 > 0)
+        env_dw1 += np.einsum("nop,nkp->ok", d1, np.abs(col1))
+        env_db1 += d1.sum((0, 2))
+    t1 = np.argwhere(np.abs(z1) < delta_rel * np.sqrt(np.mean(z1 ** 2)))
+    for n, c, p_ in t1:
+        a = abs(dh1[n, c, p_])
+        env_db1[c] += a
+        env_dw1[c] += a * np.abs(col1[n, :, p_])
+    return [env_dw1, env_db1, env_dw2, env_db2], len(t1), len(t2)
 
 
 def test_c4_full_batch_step_vs_float64(ctx):
@@ -246,7 +283,12 @@ def test_c4_full_batch_step_vs_float64(ctx):
     loop's own sequential fp32 sums (131,072 terms per conv1 weight, 32,768
     per conv2 weight) are themselves off float64 by up to 0.2 % (conv1) and
     0.9 % (conv2) of the gradient's rms here, far above rtol 1e-4, so the
-    gradients are judged against float64, as every other fp32 reduction."""
+    gradients are judged against float64, as every other fp32 reduction.
+    The conv gradients get, on top of rtol 1e-4, the bound that ReLU ties
+    allow (_relu_tie_envelope): an fp32 forward may put a pre-activation
+    within ~1e-6 of zero on the other side from float64 (one such flip moves
+    a conv2 bias gradient by ~1e-3 of its rms), whichever kernel computes
+    the convolution."""
     B, H = 128, 32
     xs = synth.normal(synth.seed(4, 0), (1, B, 3, H, H))
     ys = synth.uniform_int(synth.seed(4, 1), (1, B), 10)
@@ -259,12 +301,21 @@ def test_c4_full_batch_step_vs_float64(ctx):
     ps = [p.copy() for p in params]
     ref = oracle.cnn_step(ps, [np.zeros_like(p) for p in ps], xs[0], ys[0], 1.0, 0.0)
     assert abs(float(losses[0]) - ref) <= RTOL32 * max(1.0, abs(ref)), (float(losses[0]), ref)
-    loss64, grads = _cnn_step64(params, xs[0], ys[0])
+    keep = {}
+    loss64, grads = _cnn_step64(params, xs[0], ys[0], keep)
     assert abs(float(losses[0]) - loss64) <= RTOL32 * max(1.0, abs(loss64))
+    env, n_t1, n_t2 = _relu_tie_envelope(keep)
+    assert n_t1 + n_t2 < 2000, (n_t1, n_t2)       # ties are rare: the envelope stays tight
     off = 0
     names = ["conv1.w", "conv1.b", "conv2.w", "conv2.b", "fc.w", "fc.b"]
-    for name, p0, g64 in zip(names, params, grads):
+    for i, (name, p0, g64) in enumerate(zip(names, params, grads)):
         n = p0.size
         got = p0.ravel().astype(np.float64) - fp[off:off + n]
         off += n
-        assert_close(got, g64.ravel(), RTOL32, f"{name} gradient")
+        truth = g64.ravel()
+        atol = RTOL32 * np.sqrt(np.mean(truth ** 2))
+        slack = env[i].ravel() if i < 4 else 0.0
+        err = np.abs(got - truth)
+        bad = err > atol + RTOL32 * np.abs(truth) + slack
+        assert not bad.any(), (f"{name} gradient: {int(bad.sum())}/{n} outside rtol 1e-4 + ReLU-tie bound; worst "
+                               f"err {float(err.max()):.3g}, rms {float(np.sqrt(np.mean(truth ** 2))):.3g}")

@@ -177,6 +177,86 @@ def test_conv2d_forward_row_bias(ctx, relu):
     assert_close(y.numpy(), np.maximum(want, 0) if relu else want, RTOL32, "conv fwd")
 
 
+IMPLICIT_CASES = [
+    # N, C, H, W, Cout, k, stride, pad, dil
+    (128, 3, 32, 32, 32, 3, 1, 1, 1),      # C4 conv1
+    (128, 32, 32, 32, 64, 3, 2, 1, 1),     # C4 conv2
+    (3, 5, 13, 17, 40, 3, 2, 0, 1),        # odd extents, partial pixel tiles and channel block
+    (2, 4, 12, 11, 70, 3, 1, 2, 2),        # dilation 2, two channel blocks (64 + 6)
+    (2, 6, 19, 23, 8, 5, 3, 2, 1),         # 5 x 5, stride 3
+    (4, 7, 9, 9, 3, 1, 1, 0, 1),           # 1 x 1, odd K
+    (1, 2, 40, 200, 33, 3, 1, 1, 1),       # output rows wider than a pixel tile
+]
+
+
+def _conv_truth(x, w, b, s, p, d, relu):
+    """float64 from the bit-exact im2col restatement: y[n] = W @ col[n]."""
+    N = x.shape[0]
+    Cout, _, kH, kW = w.shape
+    col = oracle.im2col(x, kH, kW, s, s, p, p, d, d).astype(np.float64)
+    y = np.einsum("ok,nkp->nop", w.reshape(Cout, -1).astype(np.float64), col)
+    if b is not None:
+        y += b.astype(np.float64)[None, :, None]
+    if relu:
+        y = np.maximum(y, 0.0)
+    H, W = x.shape[2:]
+    oh, ow = (H + 2 * p - d * (kH - 1) - 1) // s + 1, (W + 2 * p - d * (kW - 1) - 1) // s + 1
+    return y.reshape(N, Cout, oh, ow)
+
+
+@pytest.mark.parametrize("case", IMPLICIT_CASES)
+@pytest.mark.parametrize("bias_relu", [(True, True), (False, False)])
+def test_conv2d_fwd_implicit_vs_float64(ctx, case, bias_relu):
+    """tf_conv2d_fwd (implicit GEMM: filter rows and input patch in LDS, no
+    col buffer) against float64 on the bit-exact im2col restatement."""
+    ops = _ops()
+    N, C, H, W, Cout, k, s, p, d = case
+    use_bias, relu = bias_relu
+    x = synth.normal(251 + N + C, (N, C, H, W))
+    w = synth.normal(252 + Cout, (Cout, C, k, k), std=0.2)
+    b = synth.normal(253, (Cout,)) if use_bias else None
+    oh, ow = ops.conv_out(H, k, s, p, d), ops.conv_out(W, k, s, p, d)
+    y = ctx.empty((N, Cout, oh, ow))
+    ops.conv2d_fwd(ctx.array(x), ctx.array(w), y, ctx.array(b) if b is not None else None, (s, s), (p, p), (d, d),
+                   relu)
+    assert_close(y.numpy(), _conv_truth(x, w, b, s, p, d, relu), RTOL32, f"implicit conv {case}")
+
+
+@pytest.mark.parametrize("case", IMPLICIT_CASES)
+def test_conv2d_bwd_weight_implicit_vs_float64(ctx, case):
+    """tf_conv2d_bwd_weight (implicit GEMM over each block's pixels, then a
+    fixed-order sum of the per-block partials) against float64 on the
+    bit-exact im2col restatement; and bit-identical on a second call."""
+    ops = _ops()
+    N, C, H, W, Cout, k, s, p, d = case
+    x = synth.normal(261 + N + C, (N, C, H, W))
+    oh, ow = ops.conv_out(H, k, s, p, d), ops.conv_out(W, k, s, p, d)
+    gy = synth.normal(262 + Cout, (N, Cout, oh, ow))
+    col = oracle.im2col(x, k, k, s, s, p, p, d, d).astype(np.float64)
+    want = np.einsum("nop,nkp->ok", gy.astype(np.float64).reshape(N, Cout, -1), col).reshape(Cout, C, k, k)
+    dxx, dgy = ctx.array(x), ctx.array(gy)
+    gw = ctx.empty((Cout, C, k, k))
+    ops.conv2d_bwd_weight(dxx, dgy, gw, (s, s), (p, p), (d, d))
+    first = gw.numpy()
+    assert_close(first, want, RTOL32, f"implicit dW {case}")
+    ops.conv2d_bwd_weight(dxx, dgy, gw, (s, s), (p, p), (d, d))
+    assert_bitexact(gw.numpy(), first, "second call")
+
+
+def test_conv2d_fwd_implicit_reports_unsupported(ctx):
+    """Filter rows plus input patch over 160 KB of LDS: TF_ERR_UNSUPPORTED,
+    nothing written (the API then takes im2col + GEMM)."""
+    from tensors_amd._lib import TF_ERR_UNSUPPORTED, TFError
+    ops = _ops()
+    x = ctx.zeros((1, 64, 70, 70))
+    w = ctx.zeros((64, 64, 3, 3))
+    y = ctx.array(np.full((1, 64, 70, 70), 7.0, np.float32))
+    with pytest.raises(TFError) as e:
+        ops.conv2d_fwd(x, w, y, None, (1, 1), (1, 1))
+    assert e.value.status == TF_ERR_UNSUPPORTED
+    assert np.all(y.numpy() == 7.0)
+
+
 def test_gemm_row_bias_relu_splitk(ctx):
     from tensors_amd._lib import TF_EPI_ROW_BIAS_RELU
     ops = _ops()
