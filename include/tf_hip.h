@@ -372,6 +372,13 @@ tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, flo
                                int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dilation_h,
                                int64_t dilation_w);
 
+/* Byte -> float decode of the file loaders (data/MnistLoader.cpp:43-80 and
+ * data/CifarLoader.cpp:40-75 normalise each pixel on the host):
+ * dst[i] = table[(i / plane) % channels][src[i]] for i < n, table being
+ * channels x 256 floats (1 to 4 channels) on the device. */
+tf_status tf_decode_u8(tf_ctx* ctx, const uint8_t* src, float* dst, int64_t n, int64_t plane, int channels,
+                       const float* table);
+
 /* ---------------------------------------------------------------------------
  * Layout kernels over contiguous data viewed as [outer][reduce][inner].
  * ------------------------------------------------------------------------- */

@@ -4,6 +4,8 @@
 // Every self-test runs on CPU tensors or on GPU 0.
 #include "tfa_harness.h"
 
+#include "data/CifarLoader.hpp"
+#include "data/MnistLoader.hpp"
 #include "autograd/AccumulateGrad.hpp"
 #include "autograd/AutogradMeta.hpp"
 #include "autograd/Engine.hpp"
@@ -21,6 +23,9 @@
 #include "tensor/shape_ops.hpp"
 
 #include <chrono>
+#include <unistd.h>
+#include <fstream>
+#include <filesystem>
 #include <cmath>
 #include <cstring>
 #include <functional>
@@ -500,9 +505,69 @@ void t_sum_broadcast(Device d) {
     check_vec(x.grad(), {1, 1, 1, 5, 5, 5}, "dx");
 }
 
+// The file loaders on synthetic files (3 MNIST images and labels, 4 CIFAR
+// records in two batches): shapes, the reference's normalisation of known
+// bytes, and -- on the GPU -- the device decode bit for bit equal to the
+// host decode.
+void t_data_loaders(Device d) {
+    namespace fs = std::filesystem;
+    const fs::path dir = fs::temp_directory_path() / ("tfa_data_" + std::to_string(::getpid()));
+    fs::create_directories(dir);
+    auto put = [&](const char* name, const std::vector<uint8_t>& bytes) {
+        std::ofstream(dir / name, std::ios::binary).write(reinterpret_cast<const char*>(bytes.data()),
+                                                          static_cast<std::streamsize>(bytes.size()));
+    };
+    auto be = [](std::vector<uint8_t>& v, uint32_t x) {
+        for (int s = 24; s >= 0; s -= 8) v.push_back(static_cast<uint8_t>(x >> s));
+    };
+    std::vector<uint8_t> img, lab;
+    be(img, 0x803); be(img, 3); be(img, 28); be(img, 28);
+    for (int i = 0; i < 3 * 784; ++i) img.push_back(static_cast<uint8_t>((i * 37 + 11) & 255));
+    be(lab, 0x801); be(lab, 3);
+    for (uint8_t v : {7, 0, 9}) lab.push_back(v);
+    for (const char* f : {"train-images-idx3-ubyte", "t10k-images-idx3-ubyte"}) put(f, img);
+    for (const char* f : {"train-labels-idx1-ubyte", "t10k-labels-idx1-ubyte"}) put(f, lab);
+    std::vector<uint8_t> rec;
+    for (int r = 0; r < 2; ++r) {
+        rec.push_back(static_cast<uint8_t>(3 + r));
+        for (int i = 0; i < 3072; ++i) rec.push_back(static_cast<uint8_t>((i * 13 + 7 * r) & 255));
+    }
+    for (const char* f : {"data_batch_1.bin", "data_batch_2.bin", "data_batch_3.bin", "data_batch_4.bin",
+                          "data_batch_5.bin", "test_batch.bin"})
+        put(f, rec);
+    auto [mx, my] = data::load_mnist_train(dir.string());
+    TFA_CHECK(mx.shape() == (Shape{3, 1, 28, 28}) && my.shape() == (Shape{3}));
+    const float* px = static_cast<const float*>(mx.data());
+    for (int i : {0, 1, 783, 2351}) {
+        const float want = (static_cast<float>((i * 37 + 11) & 255) * (1.0f / 255.0f) - 0.1307f) * (1.0f / 0.3081f);
+        TFA_CHECK(px[i] == want);
+    }
+    TFA_CHECK(static_cast<const int64_t*>(my.data())[2] == 9);
+    auto [cx, cy] = data::load_cifar10_train(dir.string());
+    TFA_CHECK(cx.shape() == (Shape{10, 3, 32, 32}) && cy.shape() == (Shape{10}));
+    const float* pc = static_cast<const float*>(cx.data());
+    const float want_g = (static_cast<float>((1024 * 13 + 5 * 0) & 255) * (1.0f / 255.0f) - 0.4822f) / 0.2435f;
+    TFA_CHECK(pc[1024] == want_g && static_cast<const int64_t*>(cy.data())[1] == 4);
+    if (d.type == DeviceType::CUDA) {
+        auto [gx, gy] = data::load_mnist_test(dir.string(), d);
+        auto [hx, hy] = data::load_cifar10_test(dir.string(), d);
+        auto bits_equal = [](const Tensor& dev, const Tensor& host) {
+            Tensor back = dev.to(Device::cpu());
+            return back.numel() == host.numel() &&
+                   std::memcmp(back.data(), host.data(), static_cast<size_t>(host.numel()) * dtype_size(host.dtype())) == 0;
+        };
+        auto [tx, ty] = data::load_mnist_test(dir.string());
+        auto [ux, uy] = data::load_cifar10_test(dir.string());
+        TFA_CHECK(gx.device() == d && bits_equal(gx, tx) && bits_equal(gy, ty));
+        TFA_CHECK(hx.device() == d && bits_equal(hx, ux) && bits_equal(hy, uy));
+    }
+    fs::remove_all(dir);
+}
+
 const std::map<std::string, std::function<void(Device)>>& registry() {
     static const std::map<std::string, std::function<void(Device)>> r = {
         {"engine_fan_in", t_engine_fan_in},
+        {"data_loaders", t_data_loaders},
         {"engine_deep_chain", t_engine_deep_chain},
         {"chain_add_mul_sum", t_chain_add_mul_sum},
         {"transpose_grad", t_transpose_grad},

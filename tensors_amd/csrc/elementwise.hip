@@ -509,3 +509,48 @@ tf_status tf_cast_bf16_f32(tf_ctx* ctx, const void* x, float* y, int64_t n) {
 }
 
 }  // extern "C"
+
+namespace {
+
+// dst[i] = table[(i / plane) % channels][src[i]]: the file loaders' byte ->
+// float decode (data/Decode.cpp) through a per-channel table of 256 values
+// held in LDS; four bytes per thread per step when plane % 4 == 0 (a quad
+// then stays in one channel).
+__global__ __launch_bounds__(256) void decode_u8_kernel(const uint8_t* __restrict__ src, float* __restrict__ dst,
+                                                        int64_t n, int64_t plane, int channels,
+                                                        const float* __restrict__ table, int quads) {
+    __shared__ float tab[4 * 256];
+    for (int i = threadIdx.x; i < channels * 256; i += 256) tab[i] = table[i];
+    __syncthreads();
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    if (quads) {
+        for (int64_t q = tid; q < n / 4; q += stride) {
+            const uchar4 b = reinterpret_cast<const uchar4*>(src)[q];
+            const float* t = tab + 256 * (int)(((4 * q) / plane) % channels);
+            reinterpret_cast<float4*>(dst)[q] = make_float4(t[b.x], t[b.y], t[b.z], t[b.w]);
+        }
+    } else {
+        for (int64_t i = tid; i < n; i += stride) dst[i] = tab[256 * (int)((i / plane) % channels) + src[i]];
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+tf_status tf_decode_u8(tf_ctx* ctx, const uint8_t* src, float* dst, int64_t n, int64_t plane, int channels,
+                       const float* table) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(n >= 0 && plane > 0 && channels >= 1 && channels <= 4, "tf_decode_u8: bad sizes (1 to 4 channels)");
+    if (n == 0) return TF_OK;
+    TF_REQUIRE(src && dst && table, "tf_decode_u8: null pointer");
+    const int quads = (plane % 4 == 0 && n % 4 == 0 && (reinterpret_cast<uintptr_t>(src) & 3) == 0 &&
+                       (reinterpret_cast<uintptr_t>(dst) & 15) == 0) ? 1 : 0;
+    decode_u8_kernel<<<tfd::grid_for(n, quads ? 16 : 4), 256, 0, ctx->stream>>>(src, dst, n, plane, channels, table,
+                                                                                quads);
+    return tfh::check_launch("decode_u8_kernel");
+}
+
+}  // extern "C"
+

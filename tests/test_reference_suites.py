@@ -7,12 +7,13 @@ reference's own headers and linked with the reference's objects and
 libtf_hip.so (oracle/_ref/route_b_check).
 
 CPU only; skipped where /root/reference is absent (the GPU box).  The suites
-are every ``*_test.cpp`` under the reference's tensor/, autograd/, nn/ and
-tests/ except those that include the CUDA toolkit's ``cuda_runtime.h``
-(tensor/tensor_to_test.cpp, nn/conv2d_forward_test.cpp,
-nn/conv2d_backward_test.cpp: they drive CUDA directly).  The reference's
-cuda/ suites test its CUDA kernels and data/ its file loaders, neither of
-which this build provides.
+are every ``*_test.cpp`` under the reference's tensor/, autograd/, nn/,
+data/ and tests/ except those that include the CUDA toolkit's
+``cuda_runtime.h`` (tensor/tensor_to_test.cpp, nn/conv2d_forward_test.cpp,
+nn/conv2d_backward_test.cpp: they drive CUDA directly); the reference's
+cuda/ suites test its CUDA kernels, which this build replaces.  The
+reference's two example programs (examples/train_mlp.cpp, train_cnn.cpp)
+are also built unchanged and run on small synthetic MNIST / CIFAR-10 files.
 """
 from __future__ import annotations
 
@@ -21,6 +22,7 @@ import os
 import subprocess
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -36,7 +38,7 @@ def _suites() -> list[Path]:
     if not (REF / "third_party" / "doctest" / "doctest.h").exists():
         return []
     out = []
-    for top in ("tensor", "autograd", "nn", "tests"):
+    for top in ("tensor", "autograd", "nn", "data", "tests"):
         for f in sorted((REF / top).rglob("*_test.cpp")):
             if "cuda_runtime.h" not in f.read_text(errors="replace"):
                 out.append(f)
@@ -136,3 +138,59 @@ def test_route_b_registrar_builds_against_the_reference_and_registers():
     for slot in ("register_cuda_add", "register_cuda_mul", "register_cuda_relu", "register_cuda_sigmoid",
                  "register_cuda_tanh", "register_cuda_leaky_relu", "register_allocator", "register_cuda_copy"):
         assert f"{slot}(" in reg, f"the registrar does not call {slot}"
+
+
+def _write_mnist(d, n_train, n_test, seed):
+    """Learnable synthetic MNIST: each image is its class's fixed random
+    prototype plus noise, so the example's 95 % test-accuracy exit check
+    (examples/train_mlp.cpp) can pass."""
+    rng = np.random.default_rng(seed)
+    proto = rng.integers(0, 256, (10, 784))
+    for split, n in (("train", n_train), ("t10k", n_test)):
+        y = rng.integers(0, 10, n)
+        x = np.clip(proto[y] + rng.integers(-24, 25, (n, 784)), 0, 255).astype(np.uint8)
+        hdr = np.array([0x803, n, 28, 28], ">u4").tobytes()
+        (d / f"{split}-images-idx3-ubyte").write_bytes(hdr + x.tobytes())
+        (d / f"{split}-labels-idx1-ubyte").write_bytes(np.array([0x801, n], ">u4").tobytes() +
+                                                       y.astype(np.uint8).tobytes())
+
+
+def _write_cifar(d, per_batch, seed):
+    rng = np.random.default_rng(seed)
+    for f in [f"data_batch_{i}.bin" for i in range(1, 6)] + ["test_batch.bin"]:
+        recs = rng.integers(0, 256, (per_batch, 3073), dtype=np.uint8)
+        recs[:, 0] = rng.integers(0, 10, per_batch)
+        (d / f).write_bytes(recs.tobytes())
+
+
+@pytest.mark.parametrize("example,env,writer", [
+    ("train_mlp", "TENSORFORGE_MNIST_DIR", lambda d: _write_mnist(d, 256, 64, 5)),
+    ("train_cnn", "TENSORFORGE_CIFAR_DIR", lambda d: _write_cifar(d, 16, 6)),
+])
+def test_reference_example_builds_and_runs(tmp_path, doctest_include, example, env, writer):
+    """examples/<example>.cpp compiled unchanged against tensors_amd/cpp and
+    libtensorforge.so, run on CPU tensors (as written) over small synthetic
+    files in the on-disk formats.  train_mlp must train to its own 95 %
+    test-accuracy exit check.  train_cnn loads the files and then stops, as
+    it does against the reference itself: with padding 0 (the reference's
+    Conv2dModule default, nn/Conv2dModule.hpp:17-19) its 32 x 32 inputs reach
+    the flatten as [bs, 32, 14, 14], which it reshapes to [bs, 32 * 7 * 7]
+    (examples/train_cnn.cpp:65-68, 96), and reshape throws
+    std::invalid_argument on the element count (tensor/shape_ops.cpp)."""
+    if not (LIB / "libtensorforge.so").exists():
+        pytest.fail("libtensorforge.so is not built")
+    src = REF / "examples" / f"{example}.cpp"
+    exe = tmp_path / example
+    r = _run(["g++", "-std=c++20", "-O2", f"-I{CPP}", str(src), f"-L{LIB}", "-ltensorforge", f"-Wl,-rpath,{LIB}",
+              "-o", str(exe)])
+    assert r.returncode == 0, r.stderr[-3000:]
+    data = tmp_path / "data"
+    data.mkdir()
+    writer(data)
+    r = _run([str(exe)], timeout=600, env={**os.environ, env: str(data)})
+    if example == "train_mlp":
+        assert r.returncode == 0, (r.stdout[-2000:], r.stderr[-2000:])
+        assert "final_test_acc=" in r.stdout
+    else:
+        assert "[train_cnn] train=80 test=16" in r.stdout, r.stdout[-2000:]
+        assert r.returncode != 0 and "invalid_argument" in r.stderr and "reshape" in r.stderr, r.stderr[-2000:]
