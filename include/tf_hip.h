@@ -371,6 +371,17 @@ tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, flo
                                int64_t H, int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t stride_h,
                                int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dilation_h,
                                int64_t dilation_w);
+/* Conv2d data gradient without the dcol buffer or col2im (implicit GEMM over
+ * the stride's sub-pixel phases; replaces nn/Conv2d.cpp:178-204's per-image
+ * launch_gemm_tiled_16x16 of W^T x dy into col_grad + launch_col2im):
+ * dx[N][C][H][W] = sum over co and the taps reaching each input pixel of
+ * w[co][c][ki][kj] * dy[n][co][oh][ow].  Float32, deterministic (a fixed
+ * order per geometry), every dx element written (zeros where no tap reaches).
+ * TF_ERR_UNSUPPORTED when the filter columns and the dy patch of one phase
+ * tile do not fit the LDS; the caller then uses tf_gemm_ex + tf_col2im. */
+tf_status tf_conv2d_bwd_data(tf_ctx* ctx, const float* dy, const float* w, float* dx, int64_t N, int64_t C, int64_t H,
+                             int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t stride_h, int64_t stride_w,
+                             int64_t pad_h, int64_t pad_w, int64_t dilation_h, int64_t dilation_w);
 
 /* Byte -> float decode of the file loaders (data/MnistLoader.cpp:43-80 and
  * data/CifarLoader.cpp:40-75 normalise each pixel on the host):

@@ -405,11 +405,16 @@ std::vector<Tensor> Conv2dBackward::apply(std::vector<Tensor>&& grads) {
             hip::chansum_nchw(dy, db);
         }
         if (wants(*this, 0)) {
-            Tensor dcol = Tensor::empty(Shape{g_.N, KK, P}, dy.dtype(), dy.device());
-            hip::gemm_ex(dev, true, false, KK, P, g_.Cout, w.data(), KK, 0, dy.data(), P, g_.Cout * P, dcol.data(), P,
-                         KK * P, g_.N, false, dy.dtype(), dy.dtype(), TF_EPI_NONE, nullptr);
             dx = Tensor::empty(Shape{g_.N, g_.Cin, g_.H, g_.W}, dy.dtype(), dy.device());
-            hip::col2im(dcol, dx, g_.kH, g_.kW, g_.sh, g_.sw, g_.ph, g_.pw, g_.dh, g_.dw);
+            // The implicit data gradient (no dcol buffer, no col2im) when the
+            // shape fits it, else dcol = W^T dy per image and col2im.
+            if (dy.dtype() != Dtype::Float32 || w.dtype() != Dtype::Float32 ||
+                !hip::conv2d_backward_data_implicit(dy, w, dx, g_.sh, g_.sw, g_.ph, g_.pw, g_.dh, g_.dw)) {
+                Tensor dcol = Tensor::empty(Shape{g_.N, KK, P}, dy.dtype(), dy.device());
+                hip::gemm_ex(dev, true, false, KK, P, g_.Cout, w.data(), KK, 0, dy.data(), P, g_.Cout * P, dcol.data(),
+                             P, KK * P, g_.N, false, dy.dtype(), dy.dtype(), TF_EPI_NONE, nullptr);
+                hip::col2im(dcol, dx, g_.kH, g_.kW, g_.sh, g_.sw, g_.ph, g_.pw, g_.dh, g_.dw);
+            }
         }
         return {std::move(dx), std::move(dw), std::move(db)};
     }

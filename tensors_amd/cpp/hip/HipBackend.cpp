@@ -459,6 +459,22 @@ bool conv2d_backward_weight_implicit(const Tensor& x, const Tensor& dy, Tensor& 
     return true;
 }
 
+bool conv2d_backward_data_implicit(const Tensor& dy, const Tensor& w, Tensor& dx, int64_t sh, int64_t sw, int64_t ph,
+                                   int64_t pw, int64_t dh, int64_t dwl) {
+    require_gpu(dy, "hip::conv2d_backward_data"); require_gpu(w, "hip::conv2d_backward_data");
+    require_gpu(dx, "hip::conv2d_backward_data");
+    require(dy.dtype() == Dtype::Float32 && w.dtype() == Dtype::Float32 && dx.dtype() == Dtype::Float32,
+            "hip::conv2d_backward_data: Float32 only");
+    const auto& xs = dx.shape();
+    const auto& ws = w.shape();
+    const int st = tf_conv2d_bwd_data(ctx_of(dy), static_cast<const float*>(dy.data()),
+                                      static_cast<const float*>(w.data()), static_cast<float*>(dx.data()), xs[0], xs[1],
+                                      xs[2], xs[3], ws[0], ws[2], ws[3], sh, sw, ph, pw, dh, dwl);
+    if (st == TF_ERR_UNSUPPORTED) return false;
+    check(st, "hip::conv2d_backward_data");
+    return true;
+}
+
 void chansum_nchw(const Tensor& dy, Tensor& db) {
     require_gpu(dy, "hip::chansum");
     require(dy.shape().ndim() == 4, "hip::chansum: NCHW");

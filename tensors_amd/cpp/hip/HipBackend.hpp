@@ -131,6 +131,11 @@ bool conv2d_forward_implicit(const Tensor& x, const Tensor& w, const Tensor* bia
 bool conv2d_backward_weight_implicit(const Tensor& x, const Tensor& dy, Tensor& dw, int64_t sh, int64_t sw, int64_t ph,
                                      int64_t pw, int64_t dh, int64_t dwl);
 
+// Implicit-GEMM data gradient (tf_conv2d_bwd_data): false when the shape does
+// not fit the kernel's LDS (nothing was launched), else dx is written.
+bool conv2d_backward_data_implicit(const Tensor& dy, const Tensor& w, Tensor& dx, int64_t sh, int64_t sw, int64_t ph,
+                                   int64_t pw, int64_t dh, int64_t dwl);
+
 // ---- conv index maps -----------------------------------------------------
 void im2col(const Tensor& x, Tensor& col, int64_t kH, int64_t kW, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
             int64_t dh, int64_t dw);

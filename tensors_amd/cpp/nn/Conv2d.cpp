@@ -45,18 +45,27 @@ Conv2dGrad Conv2d::backward(Tensor grad_output, Tensor input) {
     const int dev = input.device().index;
     const Tensor& w = weight().data_;
 
-    Tensor col = Tensor::empty(Shape{N, KK, P}, Dtype::Float32, input.device());
-    hip::im2col(input, col, kernel_h_, kernel_w_, stride_h_, stride_w_, pad_h_, pad_w_, dilation_h_, dilation_w_);
+    // Implicit-GEMM weight and data gradients (no col / dcol buffers) when
+    // the shape fits their LDS layouts; else the im2col / col2im forms.
     Conv2dGrad g;
     g.grad_weight = Tensor::empty(w.shape(), Dtype::Float32, input.device());
-    hip::gemm_ex(dev, false, true, out_channels_, KK, P, grad_output.data(), P, out_channels_ * P, col.data(), P, KK * P,
-                 g.grad_weight.data(), KK, 0, N, true, Dtype::Float32, Dtype::Float32, TF_EPI_NONE, nullptr);
-    Tensor dcol = Tensor::empty(Shape{N, KK, P}, Dtype::Float32, input.device());
-    hip::gemm_ex(dev, true, false, KK, P, out_channels_, w.data(), KK, 0, grad_output.data(), P, out_channels_ * P,
-                 dcol.data(), P, KK * P, N, false, Dtype::Float32, Dtype::Float32, TF_EPI_NONE, nullptr);
+    if (!hip::conv2d_backward_weight_implicit(input, grad_output, g.grad_weight, stride_h_, stride_w_, pad_h_, pad_w_,
+                                              dilation_h_, dilation_w_)) {
+        Tensor col = Tensor::empty(Shape{N, KK, P}, Dtype::Float32, input.device());
+        hip::im2col(input, col, kernel_h_, kernel_w_, stride_h_, stride_w_, pad_h_, pad_w_, dilation_h_, dilation_w_);
+        hip::gemm_ex(dev, false, true, out_channels_, KK, P, grad_output.data(), P, out_channels_ * P, col.data(), P,
+                     KK * P, g.grad_weight.data(), KK, 0, N, true, Dtype::Float32, Dtype::Float32, TF_EPI_NONE, nullptr);
+    }
     g.grad_input = Tensor::empty(input.shape(), Dtype::Float32, input.device());
-    hip::col2im(dcol, g.grad_input, kernel_h_, kernel_w_, stride_h_, stride_w_, pad_h_, pad_w_, dilation_h_,
-                dilation_w_);
+    if (!hip::conv2d_backward_data_implicit(grad_output, w, g.grad_input, stride_h_, stride_w_, pad_h_, pad_w_,
+                                            dilation_h_, dilation_w_)) {
+        Tensor dcol = Tensor::empty(Shape{N, KK, P}, Dtype::Float32, input.device());
+        hip::gemm_ex(dev, true, false, KK, P, out_channels_, w.data(), KK, 0, grad_output.data(), P,
+                     out_channels_ * P, dcol.data(), P, KK * P, N, false, Dtype::Float32, Dtype::Float32, TF_EPI_NONE,
+                     nullptr);
+        hip::col2im(dcol, g.grad_input, kernel_h_, kernel_w_, stride_h_, stride_w_, pad_h_, pad_w_, dilation_h_,
+                    dilation_w_);
+    }
     g.grad_bias = zeros(Shape{out_channels_}, Dtype::Float32, input.device());
     if (bias_enabled_) hip::chansum_nchw(grad_output, g.grad_bias);
     return g;

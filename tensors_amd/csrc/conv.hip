@@ -209,20 +209,23 @@ __global__ __launch_bounds__(256) void col2im_plane_kernel(const T* __restrict__
 // Block (8 waves, two per SIMD) = MT output channels x NP consecutive output
 // pixels of one image, NP = 128 (MT = 64) or 256 (MT = 32), so each wave
 // owns one 32 x 32 sub-tile.  The block stages in LDS, once:
-//   * the MT x K filter rows, split by k parity: wk[row][h][j] = w[row][2j+h]
-//     (row stride KH2 + 4 words), so lane half h reads four consecutive k
-//     steps' operands with one 16-byte read;
-//   * the tap table, split the same way: koff[h][j] = patch offset of tap
-//     k = 2j + h = (ci, kh, kw), i.e. (ci PH + kh dh) PW + kw dw;
+//   * the MT x K filter rows, wk[row][k] (row stride Kp + 4 words, Kp = K
+//     rounded up to 8, zero past K), copied with 16-byte loads and stores
+//     when K % 4 == 0;
+//   * the tap table koff[k] = patch offset of tap k = (ci, kh, kw), i.e.
+//     (ci PH + kh dh) PWs + kw dw;
 //   * the input patch its pixels read: every channel, input rows ih_lo ..
-//     ih_lo + PH - 1 of its output rows, each padded to PW = W + 2 pw
-//     columns with zeros.
-// Pixel (oh, ow) then reads tap k at koff + ((oh - oh_lo) sh) PW + ow sw:
-// per four k steps one filter read, one tap read and four patch reads feed
-// four v_mfma_f32_32x32x2f32 (lane half h supplies k = 2j + h of both
-// operands).  K is padded to a multiple of 8 with zero filter columns (their
-// taps read a valid offset).  Staged loads are issued 16 at a time into
-// registers before their LDS stores.  Epilogue: + bias[co], ReLU.
+//     ih_lo + PH - 1 of its output rows, each stored as PWs = 4 m columns
+//     (column c holds iw = c - L, L = pw rounded up to 4, zeros outside the
+//     image), so a row's interior is copied with 16-byte loads and stores
+//     when W % 4 == 0.
+// Pixel (oh, ow) then reads tap k at koff[k] + (oh - oh_lo) sh PWs + ow sw +
+// L - pw.  Lane half h supplies k in [h Kp/2, (h + 1) Kp/2) of both operands:
+// per four k steps one 16-byte filter read, one 16-byte tap read and four
+// patch reads feed four v_mfma_f32_32x32x2f32; the reads of the next four
+// steps are issued before the current four MFMAs (taps two steps ahead), so
+// the LDS latency is not on the MFMA chain.  Padded k steps carry zero
+// filter values and a valid tap.  Epilogue: + bias[co], ReLU.
 // ---------------------------------------------------------------------------
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -231,21 +234,155 @@ constexpr int kIgThreads = 512;
 template <int MT>
 constexpr int ig_pixels() { return MT == 64 ? 128 : 256; }
 
+// x / d and x % d for 0 <= x < 2^22, 0 < d, by a float reciprocal and one
+// correction step (the rounded product is within one of the quotient): about
+// ten instructions instead of a signed division's expansion, in the staging
+// loops that split every LDS element's index.
+struct FastDiv {
+    int d;
+    float rcp;
+};
+__device__ __forceinline__ FastDiv fast_div(int d) { return FastDiv{d, 1.0f / (float)d}; }
+__device__ __forceinline__ int divmod(int x, const FastDiv& f, int& r) {
+    int q = (int)((float)x * f.rcp);
+    r = x - __mul24(q, f.d);
+    if (r < 0) {
+        --q;
+        r += f.d;
+    } else if (r >= f.d) {
+        ++q;
+        r -= f.d;
+    }
+    return q;
+}
+
+constexpr int kStage4 = 8;  // 16-byte staging loads in flight per thread
+
+// rows x cols floats from src (row stride ld, rows < nrows valid, columns
+// < cols valid, zero elsewhere) into dst[r][0 .. 4 spr) with row stride
+// dst_ld; 16-byte global loads when vec (cols and ld multiples of 4, src
+// 16-byte aligned).  rows * spr < 2^22.
+__device__ __forceinline__ void stage_rows(const float* __restrict__ src, int ld, int nrows, int cols, float* dst,
+                                           int dst_ld, int rows, int spr, bool vec) {
+    const int total = rows * spr;
+    const FastDiv fspr = fast_div(spr);
+    for (int base = threadIdx.x; base < total; base += kIgThreads * kStage4) {
+        v4f v[kStage4];
+#pragma unroll
+        for (int u = 0; u < kStage4; ++u) {
+            const int i = base + kIgThreads * u;
+            int sl;
+            const int r = divmod(i, fspr, sl);
+            const int c = 4 * sl;
+            v4f val = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (i < total && r < nrows) {
+                const float* sp = src + r * ld + c;
+                if (vec) {
+                    if (c < cols) val = *reinterpret_cast<const v4f*>(sp);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (c + e < cols) val[e] = sp[e];
+                }
+            }
+            v[u] = val;
+        }
+#pragma unroll
+        for (int u = 0; u < kStage4; ++u) {
+            const int i = base + kIgThreads * u;
+            if (i < total) {
+                int sl;
+                const int r = divmod(i, fspr, sl);
+                *reinterpret_cast<v4f*>(dst + r * dst_ld + 4 * sl) = v[u];
+            }
+        }
+    }
+}
+
+// patch[ci][rr][c] = x[ci][ih_lo + rr][c - L] (zero outside the image) for
+// ci < C, rr < PH, c < PWs; xn is the image's first element.  16-byte loads
+// when vec (W % 4 == 0 and xn 16-byte aligned; L is a multiple of 4, so slots
+// never straddle the image edge).
+__device__ __forceinline__ void stage_patch(const float* __restrict__ xn, float* patch, int C, int H, int W, int PH,
+                                            int PWs, int L, int ih_lo, bool vec) {
+    const int spr = PWs / 4;
+    const int total = C * PH * spr;
+    const FastDiv fspr = fast_div(spr), fPH = fast_div(PH);
+    for (int base = threadIdx.x; base < total; base += kIgThreads * kStage4) {
+        v4f v[kStage4];
+#pragma unroll
+        for (int u = 0; u < kStage4; ++u) {
+            const int i = base + kIgThreads * u;
+            int sl, rr;
+            const int row = divmod(i, fspr, sl);
+            const int ci = divmod(row, fPH, rr);
+            const int ih = ih_lo + rr, iw = 4 * sl - L;
+            v4f val = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (i < total && ih >= 0 && ih < H) {
+                const float* sp = xn + (ci * H + ih) * W + iw;
+                if (vec) {
+                    if (iw >= 0 && iw < W) val = *reinterpret_cast<const v4f*>(sp);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (iw + e >= 0 && iw + e < W) val[e] = sp[e];
+                }
+            }
+            v[u] = val;
+        }
+#pragma unroll
+        for (int u = 0; u < kStage4; ++u) {
+            const int i = base + kIgThreads * u;
+            if (i < total) *reinterpret_cast<v4f*>(patch + 4 * i) = v[u];
+        }
+    }
+}
+
+// acc += A (32 rows of wrow, k along the row) x B (32 pixels: pbase[koff[k]])
+// over KH2 k steps per lane half (KH2 a multiple of 4, >= 4), with the next
+// four steps' reads in flight during the current four MFMAs.
+__device__ __forceinline__ v16f mfma_gather_loop(const float* wrow, const int* krow, const float* pbase, int KH2) {
+    v16f acc = v16f{};
+    v4f a = *reinterpret_cast<const v4f*>(wrow);
+    v4i kn = *reinterpret_cast<const v4i*>(krow);
+    float b0 = pbase[kn.x], b1 = pbase[kn.y], b2 = pbase[kn.z], b3 = pbase[kn.w];
+    kn = *reinterpret_cast<const v4i*>(krow + min(4, KH2 - 4));
+    for (int j = 0; j < KH2; j += 4) {
+        const v4i kn2 = *reinterpret_cast<const v4i*>(krow + min(j + 8, KH2 - 4));
+        const v4f an = *reinterpret_cast<const v4f*>(wrow + min(j + 4, KH2 - 4));
+        const float c0 = pbase[kn.x], c1 = pbase[kn.y], c2 = pbase[kn.z], c3 = pbase[kn.w];
+        // Keep the reads above the MFMAs (otherwise they are sunk to their use
+        // in the next step and each step waits for its own reads).
+        __builtin_amdgcn_sched_barrier(0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b1, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b2, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b3, acc, 0, 0, 0);
+        a = an;
+        b0 = c0;
+        b1 = c1;
+        b2 = c2;
+        b3 = c3;
+        kn = kn2;
+    }
+    return acc;
+}
+
 template <int MT>
 __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const float* __restrict__ x,
                                                                        const float* __restrict__ w,
                                                                        const float* __restrict__ bias,
                                                                        float* __restrict__ y, ConvGeom g, int Cout,
-                                                                       int K, int Kp, int PH, int PW,
-                                                                       int tiles_per_image, int relu) {
+                                                                       int K, int Kp, int PH, int PWs, int L,
+                                                                       int tiles_per_image, int relu, int vec) {
     extern __shared__ float smem[];
     constexpr int NP = ig_pixels<MT>();
     constexpr int MSUB = MT / 32;
-    const int KH2 = Kp / 2;                     // k steps per half
-    const int RS = 2 * (KH2 + 4);               // filter row stride (words)
-    float* wk = smem;                           // [MT][2][KH2 + 4]
-    int* koff = reinterpret_cast<int*>(wk + MT * RS);   // [2][KH2]
-    float* patch = reinterpret_cast<float*>(koff + Kp); // [C][PH][PW]
+    const int KH2 = Kp / 2;
+    const int RS = Kp + 4;                      // filter row stride (words): RS / 4 odd, no bank conflicts
+    float* wk = smem;                           // [MT][RS]
+    int* koff = reinterpret_cast<int*>(wk + MT * RS);   // [Kp]
+    float* patch = reinterpret_cast<float*>(koff + Kp); // [C][PH][PWs]
     const int P = (int)(g.outH * g.outW), outW = (int)g.outW;
     const int n = blockIdx.x / tiles_per_image, pt = blockIdx.x - n * tiles_per_image;
     const int p0 = pt * NP, p_end = min(p0 + NP, P);
@@ -255,47 +392,13 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
     const int C = (int)g.C, H = (int)g.H, W = (int)g.W, kHW = (int)(g.kH * g.kW), kW = (int)g.kW;
     const int t = threadIdx.x;
 
-    constexpr int kStage = 16;
-    for (int base = t; base < MT * Kp; base += kIgThreads * kStage) {
-        float v[kStage];
-#pragma unroll
-        for (int u = 0; u < kStage; ++u) {
-            const int i = base + kIgThreads * u;
-            const int r = i / Kp, k = i - r * Kp;
-            v[u] = (i < MT * Kp && co0 + r < Cout && k < K) ? w[(int64_t)(co0 + r) * K + k] : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < kStage; ++u) {
-            const int i = base + kIgThreads * u;
-            if (i < MT * Kp) {
-                const int r = i / Kp, k = i - r * Kp;
-                wk[r * RS + (k & 1) * (KH2 + 4) + (k >> 1)] = v[u];
-            }
-        }
-    }
+    stage_rows(w + (int64_t)co0 * K, K, min(MT, Cout - co0), K, wk, RS, MT, Kp / 4, (vec & 2) != 0);
     for (int k = t; k < Kp; k += kIgThreads) {
         const int kc = min(k, K - 1);
         const int ci = kc / kHW, rem = kc - ci * kHW, kh = rem / kW, kw = rem - kh * kW;
-        koff[(k & 1) * KH2 + (k >> 1)] = (ci * PH + kh * (int)g.dh) * PW + kw * (int)g.dw;
+        koff[k] = (ci * PH + kh * (int)g.dh) * PWs + kw * (int)g.dw;
     }
-    const float* xn = x + (int64_t)n * C * H * W;
-    const int plane = PH * PW;
-    for (int base = t; base < C * plane; base += kIgThreads * kStage) {
-        float v[kStage];
-#pragma unroll
-        for (int u = 0; u < kStage; ++u) {
-            const int i = base + kIgThreads * u;
-            const int ci = i / plane, rr = (i - ci * plane) / PW, cc = i - ci * plane - rr * PW;
-            const int ih = ih_lo + rr, iw = cc - (int)g.pw;
-            v[u] = (i < C * plane && ih >= 0 && ih < H && iw >= 0 && iw < W) ? xn[((int64_t)ci * H + ih) * W + iw]
-                                                                              : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < kStage; ++u) {
-            const int i = base + kIgThreads * u;
-            if (i < C * plane) patch[i] = v[u];
-        }
-    }
+    stage_patch(x + (int64_t)n * C * H * W, patch, C, H, W, PH, PWs, L, ih_lo, (vec & 1) != 0);
     __syncthreads();
 
     const int wave = t >> 6, lane = t & 63, l32 = lane & 31, half = lane >> 5;
@@ -305,22 +408,10 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
     {
         const int q = pp < p_end ? pp : p0;
         const int oh = q / outW, ow = q - oh * outW;
-        pix_off = (oh - oh_lo) * (int)g.sh * PW + ow * (int)g.sw;
+        pix_off = (oh - oh_lo) * (int)g.sh * PWs + ow * (int)g.sw + L - (int)g.pw;
     }
-    v16f acc = v16f{};
-    const float* wrow = wk + (m_sub * 32 + l32) * RS + half * (KH2 + 4);
-    const int* krow = koff + half * KH2;
-    const float* pbase = patch + pix_off;
-    // KH2 is a multiple of 4 (Kp a multiple of 8).
-    for (int j = 0; j < KH2; j += 4) {
-        const v4f a = *reinterpret_cast<const v4f*>(wrow + j);
-        const v4i ko = *reinterpret_cast<const v4i*>(krow + j);
-        const float b0 = pbase[ko.x], b1 = pbase[ko.y], b2 = pbase[ko.z], b3 = pbase[ko.w];
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b1, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b2, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b3, acc, 0, 0, 0);
-    }
+    const v16f acc = mfma_gather_loop(wk + (m_sub * 32 + l32) * RS + half * KH2, koff + half * KH2, patch + pix_off,
+                                      KH2);
 
     if (pp >= p_end) return;
     float* yn = y + (int64_t)n * Cout * P;
@@ -334,17 +425,41 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
     }
 }
 
-// LDS layout of conv_fwd_implicit_kernel, or 0 when it does not fit.
-size_t implicit_lds_bytes(const ConvGeom& g, int MT, int K, int& Kp, int& PH, int& PW) {
+// Patch columns of the forward and weight-gradient kernels: column c holds
+// iw = c - L, L = pw (rounded up to 4 for the aligned layout, whose image
+// columns start on 16-byte boundaries), PWs = one past the last column a tap
+// reads, rounded up to 4.
+void patch_cols(const ConvGeom& g, bool aligned, int& L, int& PWs) {
+    L = (int)(aligned ? (g.pw + 3) / 4 * 4 : g.pw);
+    PWs = (int)((L + (g.outW - 1) * g.sw + (g.kW - 1) * g.dw - g.pw + 1 + 3) / 4 * 4);
+}
+
+// Most rows that a run of np consecutive pixels (starting at multiples of np)
+// of a rows x cols grid spans.
+int64_t rows_spanned(int64_t rows, int64_t cols, int64_t np) {
+    const int64_t total = rows * cols;
+    int64_t most = 0;
+    // A run's start column p0 mod cols repeats after cols / gcd(np, cols) runs.
+    for (int64_t k = 0; k < cols && k * np < total; ++k) {
+        const int64_t p0 = k * np;
+        most = std::max(most, (std::min(p0 + np, total) - 1) / cols - p0 / cols + 1);
+    }
+    return most;
+}
+
+// LDS layout of conv_fwd_implicit_kernel (the aligned patch layout when it
+// fits, else the tight one), or 0 when neither fits.
+size_t implicit_lds_bytes(const ConvGeom& g, int MT, int K, int& Kp, int& PH, int& PWs, int& L, bool& aligned) {
     Kp = (K + 7) / 8 * 8;
     const int np = MT == 64 ? ig_pixels<64>() : ig_pixels<32>();
-    const int64_t rows_max = (np - 1) / g.outW + 2;               // output rows a pixel run can touch
-    const int64_t ph_rows = std::min<int64_t>(rows_max, g.outH) - 1;
-    PH = (int)(ph_rows * g.sh + (g.kH - 1) * g.dh + 1);
-    PW = (int)(g.W + 2 * g.pw);
-    const int64_t floats = (int64_t)MT * 2 * (Kp / 2 + 4) + Kp + g.C * (int64_t)PH * PW;
-    const int64_t bytes = floats * 4;
-    return bytes <= 160 * 1024 ? (size_t)bytes : 0;
+    PH = (int)((rows_spanned(g.outH, g.outW, np) - 1) * g.sh + (g.kH - 1) * g.dh + 1);
+    for (int a = 1; a >= 0; --a) {
+        aligned = a != 0;
+        patch_cols(g, aligned, L, PWs);
+        const int64_t bytes = ((int64_t)MT * (Kp + 4) + Kp + g.C * (int64_t)PH * PWs) * 4;
+        if (bytes <= 160 * 1024) return (size_t)bytes;
+    }
+    return 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -353,31 +468,33 @@ size_t implicit_lds_bytes(const ConvGeom& g, int MT, int K, int& Kp, int& PH, in
 // with col gathered from x on the fly (nn/Conv2d.cpp:140-260 builds col with
 // launch_im2col and multiplies per image).  Blocks tile the pixels as the
 // forward does (MT channels x NP pixels of one image, 8 waves); each block
-// stages dy's MT x NP tile (split by pixel parity, like the forward's
-// filter rows), the pixel-offset table poff[h][j] of pixel 2j + h, the tap
-// table koff[k] and the input patch, then computes its MT x K partial with
-// v_mfma_f32_32x32x2f32 over its pixels (lane half h supplies pixel 2j + h
-// of both operands: dy[co][p] and patch[koff[k] + poff[p]]).  Work items are
-// (32 x 32 output tile, pixel slice): with fewer tiles than waves, each
-// tile's pixels are split over several waves and their sums combined in LDS
-// in slice order.  The block writes its partial to part[block][co][k]; the
-// partials are then summed in a fixed order (tfh::sum_partials).  Pixels
-// past the image's end carry dy = 0.
+// stages dy's MT x NP tile (dyt[co][p], row stride NP + 4 words), the
+// pixel-offset table poff[p], the tap table koff[k] and the input patch (the
+// forward's layout), then computes its MT x K partial with
+// v_mfma_f32_32x32x2f32 over its pixels (lane half h supplies the pixels of
+// its half of each slice for both operands: dy[co][p] and
+// patch[koff[k] + poff[p]]).  Work items are (32 x 32 output tile, pixel
+// slice): with fewer tiles than waves, each tile's pixels are split over
+// several waves and their sums combined in LDS in slice order.  The block
+// writes its partial to part[block][co][k]; the partials are then summed in
+// a fixed order (tfh::sum_partials).  Pixels past the image's end carry
+// dy = 0.
 // ---------------------------------------------------------------------------
 template <int MT>
 __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(const float* __restrict__ x,
                                                                               const float* __restrict__ dy,
                                                                               float* __restrict__ part, ConvGeom g,
-                                                                              int Cout, int K, int Kc, int PH, int PW,
-                                                                              int tiles_per_image, int slices) {
+                                                                              int Cout, int K, int Kc, int PH, int PWs,
+                                                                              int L, int tiles_per_image, int slices,
+                                                                              int vec) {
     extern __shared__ float smem[];
     constexpr int NP = ig_pixels<MT>();
     constexpr int NH = NP / 2;
-    constexpr int RS = 2 * (NH + 4);
-    float* dyt = smem;                                     // [MT][2][NH + 4]
-    int* poff = reinterpret_cast<int*>(dyt + MT * RS);      // [2][NH]
+    constexpr int RS = NP + 4;                             // RS / 4 odd: no bank conflicts
+    float* dyt = smem;                                     // [MT][RS]
+    int* poff = reinterpret_cast<int*>(dyt + MT * RS);      // [NP]
     int* koff = poff + NP;                                  // [Kc]
-    float* patch = reinterpret_cast<float*>(koff + Kc);    // [C][PH][PW]
+    float* patch = reinterpret_cast<float*>(koff + Kc);    // [C][PH][PWs]
     const int P = (int)(g.outH * g.outW), outW = (int)g.outW;
     const int n = blockIdx.x / tiles_per_image, pt = blockIdx.x - n * tiles_per_image;
     const int p0 = pt * NP, p_end = min(p0 + NP, P);
@@ -386,77 +503,34 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
     const int ih_lo = oh_lo * (int)g.sh - (int)g.ph;
     const int C = (int)g.C, H = (int)g.H, W = (int)g.W, kHW = (int)(g.kH * g.kW), kW = (int)g.kW;
     const int t = threadIdx.x;
-    const int plane = PH * PW;
+    const int plane = PH * PWs;
     float* red = patch + C * plane;                         // [8][16][64] when slices > 1
 
-    constexpr int kStage = 16;
-    const float* dyn = dy + (int64_t)n * Cout * P;
-    for (int base = t; base < MT * NP; base += kIgThreads * kStage) {
-        float v[kStage];
-#pragma unroll
-        for (int u = 0; u < kStage; ++u) {
-            const int i = base + kIgThreads * u;
-            const int r = i / NP, q = i - r * NP;
-            v[u] = (i < MT * NP && co0 + r < Cout && p0 + q < p_end) ? dyn[(int64_t)(co0 + r) * P + p0 + q] : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < kStage; ++u) {
-            const int i = base + kIgThreads * u;
-            if (i < MT * NP) {
-                const int r = i / NP, q = i - r * NP;
-                dyt[r * RS + (q & 1) * (NH + 4) + (q >> 1)] = v[u];
-            }
-        }
-    }
+    stage_rows(dy + ((int64_t)n * Cout + co0) * P + p0, P, min(MT, Cout - co0), p_end - p0, dyt, RS, MT, NP / 4,
+               (vec & 2) != 0);
     for (int q = t; q < NP; q += kIgThreads) {
         const int pp = p0 + q < p_end ? p0 + q : p0;
         const int oh = pp / outW, ow = pp - oh * outW;
-        poff[(q & 1) * NH + (q >> 1)] = (oh - oh_lo) * (int)g.sh * PW + ow * (int)g.sw;
+        poff[q] = (oh - oh_lo) * (int)g.sh * PWs + ow * (int)g.sw + L - (int)g.pw;
     }
     for (int k = t; k < Kc; k += kIgThreads) {
         const int kc = min(k, K - 1);
         const int ci = kc / kHW, rem = kc - ci * kHW, kh = rem / kW, kw = rem - kh * kW;
-        koff[k] = (ci * PH + kh * (int)g.dh) * PW + kw * (int)g.dw;
+        koff[k] = (ci * PH + kh * (int)g.dh) * PWs + kw * (int)g.dw;
     }
-    const float* xn = x + (int64_t)n * C * H * W;
-    for (int base = t; base < C * plane; base += kIgThreads * kStage) {
-        float v[kStage];
-#pragma unroll
-        for (int u = 0; u < kStage; ++u) {
-            const int i = base + kIgThreads * u;
-            const int ci = i / plane, rr = (i - ci * plane) / PW, cc = i - ci * plane - rr * PW;
-            const int ih = ih_lo + rr, iw = cc - (int)g.pw;
-            v[u] = (i < C * plane && ih >= 0 && ih < H && iw >= 0 && iw < W) ? xn[((int64_t)ci * H + ih) * W + iw]
-                                                                              : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < kStage; ++u) {
-            const int i = base + kIgThreads * u;
-            if (i < C * plane) patch[i] = v[u];
-        }
-    }
+    stage_patch(x + (int64_t)n * C * H * W, patch, C, H, W, PH, PWs, L, ih_lo, (vec & 1) != 0);
     __syncthreads();
 
     const int wave = t >> 6, lane = t & 63, l32 = lane & 31, half = lane >> 5;
     const int TM = MT / 32, TK = Kc / 32, T = TM * TK;
-    const int steps = NH / slices;                          // pixel pairs per slice (a multiple of 4)
+    const int steps = NH / slices;                          // pixels per slice and lane half (a multiple of 4)
     float* outp = part + (int64_t)blockIdx.x * Cout * K;
     for (int item = wave; item < T * slices; item += kIgThreads / 64) {
         const int tile = item / slices, sl = item - tile * slices;
         const int tr = tile / TK, tc = tile - tr * TK;
-        const float* arow = dyt + (tr * 32 + l32) * RS + half * (NH + 4) + sl * steps;
-        const int* prow = poff + half * NH + sl * steps;
-        const float* pb = patch + koff[tc * 32 + l32];
-        v16f acc = v16f{};
-        for (int j = 0; j < steps; j += 4) {
-            const v4f a = *reinterpret_cast<const v4f*>(arow + j);
-            const v4i po = *reinterpret_cast<const v4i*>(prow + j);
-            const float b0 = pb[po.x], b1 = pb[po.y], b2 = pb[po.z], b3 = pb[po.w];
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b0, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b1, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b2, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b3, acc, 0, 0, 0);
-        }
+        const int q0 = half * NH + sl * steps;
+        const v16f acc = mfma_gather_loop(dyt + (tr * 32 + l32) * RS + q0, poff + q0, patch + koff[tc * 32 + l32],
+                                          steps);
         if (slices == 1) {
             const int k = tc * 32 + l32;
 #pragma unroll
@@ -486,20 +560,233 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
 }
 
 // LDS layout of conv_bwd_weight_implicit_kernel, or 0 when it does not fit.
-size_t implicit_dw_lds_bytes(const ConvGeom& g, int MT, int K, int& Kc, int& PH, int& PW, int& slices) {
+size_t implicit_dw_lds_bytes(const ConvGeom& g, int MT, int K, int& Kc, int& PH, int& PWs, int& L, int& slices,
+                             bool& aligned) {
     Kc = (K + 31) / 32 * 32;
     const int np = MT == 64 ? ig_pixels<64>() : ig_pixels<32>();
-    const int64_t rows_max = (np - 1) / g.outW + 2;
-    const int64_t ph_rows = std::min<int64_t>(rows_max, g.outH) - 1;
-    PH = (int)(ph_rows * g.sh + (g.kH - 1) * g.dh + 1);
-    PW = (int)(g.W + 2 * g.pw);
+    PH = (int)((rows_spanned(g.outH, g.outW, np) - 1) * g.sh + (g.kH - 1) * g.dh + 1);
     const int tiles = (MT / 32) * (Kc / 32);
     slices = 1;
     while (tiles * slices * 2 <= kIgThreads / 64 && (np / 2) / (slices * 2) >= 4) slices *= 2;
-    const int64_t floats = (int64_t)MT * 2 * (np / 2 + 4) + np + Kc + g.C * (int64_t)PH * PW +
-                           (slices > 1 ? (int64_t)tiles * slices * 16 * 64 : 0);
-    const int64_t bytes = floats * 4;
-    return bytes <= 160 * 1024 ? (size_t)bytes : 0;
+    for (int a = 1; a >= 0; --a) {
+        aligned = a != 0;
+        patch_cols(g, aligned, L, PWs);
+        const int64_t floats = (int64_t)MT * (np + 4) + np + Kc + g.C * (int64_t)PH * PWs +
+                               (slices > 1 ? (int64_t)tiles * slices * 16 * 64 : 0);
+        if (floats * 4 <= 160 * 1024) return (size_t)(floats * 4);
+    }
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Implicit-GEMM convolution data gradient (fp32, NCHW, MFMA):
+//   dx[n][c][ih][iw] = sum_co sum_{ki,kj} w[co][c][ki][kj] dy[n][co][oh][ow],
+//   oh = (ih + ph - ki dh) / sh, ow = (iw + pw - kj dw) / sw (whole, in range)
+// with neither the dcol buffer nor col2im (nn/Conv2d.cpp:178-204 forms
+// dcol = W^T dy per image, then launch_col2im, cuda/kernels/col2im.cu:50-80).
+//
+// Sub-pixel phases: the taps that reach input row ih depend only on
+// (ih + ph) mod sh.  Phase (i0, j0), i0 < sh, j0 < sw, holds the pixels
+// ih = i0 + sh a, iw = j0 + sw b; its row taps are the ki with
+// ki dh = i0 + ph (mod sh), and each reaches oh = a + e(ki) with the whole
+// number e(ki) = (i0 + ph - ki dh) / sh (columns likewise, f(kj)).  Within a
+// phase the data gradient is therefore a stride-1 correlation of dy, an
+// implicit GEMM with M = C (rows c), N = the phase's pixels, and
+// K = Cout x row taps x column taps, k = (co, ti, tj):
+//   A[c][k] = w[co][c][ki(ti)][kj(tj)],  B[k][(a, b)] = dy[co][a + e][b + f].
+// A block (8 waves, two per SIMD) takes MT input channels x NP consecutive
+// pixels of one phase of one image and lays out LDS as the forward kernel
+// does: the MT filter rows split by k parity, the tap offset table split the
+// same way, and the dy patch [Cout][PH][PW] its pixels read (dy rows
+// a_lo + e_min .. , columns f_min .. , zero outside dy).  A phase without
+// taps (possible for sh > kH dh, or dilations sharing a residue) has K = 0
+// and stores zeros.  The sum for one dx element runs over k in (co, ti, tj)
+// order, fixed per geometry: deterministic.
+// ---------------------------------------------------------------------------
+struct PhaseTaps {
+    int n;         // taps of this phase along the axis
+    int e_min;     // smallest offset e(k) over them
+    int span;      // e_max - e_min (0 without taps)
+};
+
+// Taps of phase r0 (< s) along one axis: k in [0, kk) with k d = r0 + p (mod s),
+// e(k) = (r0 + p - k d) / s.
+__host__ __device__ inline PhaseTaps phase_taps(int r0, int p, int kk, int s, int d) {
+    PhaseTaps t{0, 0, 0};
+    int e_max = 0;
+    for (int k = 0; k < kk; ++k) {
+        const int num = r0 + p - k * d;
+        if (((num % s) + s) % s != 0) continue;
+        const int e = num / s;
+        if (t.n == 0 || e < t.e_min) t.e_min = e;
+        if (t.n == 0 || e > e_max) e_max = e;
+        ++t.n;
+    }
+    t.span = t.n ? e_max - t.e_min : 0;
+    return t;
+}
+
+// The ti-th tap (in increasing k) of phase r0 along one axis; ti < its count.
+__device__ inline int phase_tap(int r0, int p, int kk, int s, int d, int ti) {
+    for (int k = 0; k < kk; ++k) {
+        const int num = r0 + p - k * d;
+        if (((num % s) + s) % s != 0) continue;
+        if (ti-- == 0) return k;
+    }
+    return 0;
+}
+
+template <int MT>
+__global__ __launch_bounds__(kIgThreads) void conv_bwd_data_implicit_kernel(const float* __restrict__ dy,
+                                                                            const float* __restrict__ w,
+                                                                            float* __restrict__ dx, ConvGeom g,
+                                                                            int Cout, int PH, int PWs, int L,
+                                                                            int tiles_per_phase, int vec) {
+    extern __shared__ float smem[];
+    constexpr int NP = ig_pixels<MT>();
+    constexpr int MSUB = MT / 32;
+    const int sh = (int)g.sh, sw = (int)g.sw;
+    const int phases = sh * sw;
+    // Block b runs on XCD b % 8 and the phases carry different numbers of
+    // taps, so consecutive groups of 8 blocks take consecutive phases: each
+    // XCD's share cycles through all of them.  Block (q = b / 8, x = b % 8):
+    // phase q % phases, image tile r = (q / phases) 8 + x = n tiles + pt.
+    const int q8 = blockIdx.x >> 3;
+    const int phase = q8 % phases;
+    const int r = (q8 / phases) * 8 + (blockIdx.x & 7);
+    if (r >= (int)g.N * tiles_per_phase) return;         // uniform per block
+    const int n = r / tiles_per_phase, pt = r - n * tiles_per_phase;
+    const int i0 = phase / sw, j0 = phase - i0 * sw;
+    const int H = (int)g.H, W = (int)g.W;
+    const int Ha = i0 < H ? (H - i0 + sh - 1) / sh : 0;
+    const int Wb = j0 < W ? (W - j0 + sw - 1) / sw : 0;
+    const int Pph = Ha * Wb;
+    const int p0 = pt * NP;
+    if (p0 >= Pph) return;                               // uniform per block
+    const int p_end = min(p0 + NP, Pph);
+    const int kH = (int)g.kH, kW = (int)g.kW, dh = (int)g.dh, dwl = (int)g.dw;
+    const int ph = (int)g.ph, pw = (int)g.pw;
+    const PhaseTaps th = phase_taps(i0, ph, kH, sh, dh), tw = phase_taps(j0, pw, kW, sw, dwl);
+    const int taps = th.n * tw.n;
+    const int K = Cout * taps;
+    const int Kp = max(8, (K + 7) / 8 * 8);
+    const int KH2 = Kp / 2;
+    const int RS = Kp + 4;                               // RS / 4 odd: no bank conflicts
+    const int C = (int)g.C, outH = (int)g.outH, outW = (int)g.outW;
+    const int c0 = blockIdx.y * MT;
+    const int a_lo = p0 / Wb;
+    const int kHW = kH * kW;
+    float* wk = smem;                                    // [MT][RS]
+    int* koff = reinterpret_cast<int*>(wk + MT * RS);    // [Kp]
+    int* tap_w = koff + Kp;                              // [kH kW]: ki kW + kj of tap tt
+    int* tap_p = tap_w + kHW;                            // [kH kW]: its dy patch offset
+    float* patch = smem + (((MT * RS + Kp + 2 * kHW) + 3) & ~3);  // [Cout][PH][PWs]
+    const int t = threadIdx.x;
+
+    // Tap tt = (ti, tj) of this phase: its filter position and patch offset
+    // (patch row e - e_min, column b + f + L for pixel column b).
+    for (int tt = t; tt < taps; tt += kIgThreads) {
+        const int ti = tt / tw.n, tj = tt - ti * tw.n;
+        const int ki = phase_tap(i0, ph, kH, sh, dh, ti), kj = phase_tap(j0, pw, kW, sw, dwl, tj);
+        tap_w[tt] = ki * kW + kj;
+        tap_p[tt] = ((i0 + ph - ki * dh) / sh - th.e_min) * PWs + (j0 + pw - kj * dwl) / sw + L;
+    }
+    __syncthreads();
+
+    constexpr int kStage = 16;
+    const FastDiv ftaps = fast_div(max(taps, 1));
+    // Filter columns: i = k MT + r (r fastest: consecutive lanes read
+    // consecutive input channels, kH kW floats apart).
+    for (int base = t; base < MT * Kp; base += kIgThreads * kStage) {
+        float v[kStage];
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int i = base + kIgThreads * u;
+            const int r = i & (MT - 1), k = i / MT;
+            float val = 0.0f;
+            if (i < MT * Kp && c0 + r < C && k < K) {
+                int tt;
+                const int co = divmod(k, ftaps, tt);
+                val = w[((int64_t)co * C + c0 + r) * kHW + tap_w[tt]];
+            }
+            v[u] = val;
+        }
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int i = base + kIgThreads * u;
+            if (i < MT * Kp) wk[(i & (MT - 1)) * RS + i / MT] = v[u];
+        }
+    }
+    for (int k = t; k < Kp; k += kIgThreads) {
+        int tt = 0, co = 0;
+        if (K > 0) co = divmod(min(k, K - 1), ftaps, tt);
+        koff[k] = K > 0 ? co * PH * PWs + tap_p[tt] : 0;
+    }
+    if (K > 0)
+        stage_patch(dy + (int64_t)n * Cout * outH * outW, patch, Cout, outH, outW, PH, PWs, L, a_lo + th.e_min,
+                    vec != 0);
+    __syncthreads();
+
+    const int wave = t >> 6, lane = t & 63, l32 = lane & 31, half = lane >> 5;
+    const int m_sub = wave % MSUB, n_sub = wave / MSUB;
+    const int pp = p0 + n_sub * 32 + l32;
+    int pix_off;
+    {
+        const int q = pp < p_end ? pp : p0;
+        const int a = q / Wb, bb = q - a * Wb;
+        pix_off = (a - a_lo) * PWs + bb;
+    }
+    const v16f acc = K > 0 ? mfma_gather_loop(wk + (m_sub * 32 + l32) * RS + half * KH2, koff + half * KH2,
+                                              patch + pix_off, KH2)
+                           : v16f{};
+
+    if (pp >= p_end) return;
+    const int a = pp / Wb, bb = pp - a * Wb;
+    float* dxn = dx + (int64_t)n * C * H * W + (int64_t)(i0 + sh * a) * W + (j0 + sw * bb);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int c = c0 + m_sub * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (c < C) dxn[(int64_t)c * H * W] = acc[r];
+    }
+}
+
+// LDS layout of conv_bwd_data_implicit_kernel (the largest phase), or 0 when
+// it does not fit; tpp = pixel tiles of the largest phase.  Patch columns:
+// column c holds dy column c - L, L = the most negative column offset of
+// any phase's taps (rounded up to 4 for the aligned layout when that fits).
+size_t implicit_dx_lds_bytes(const ConvGeom& g, int MT, int Cout, int& PH, int& PWs, int& L, int& tpp,
+                             bool& aligned) {
+    const int np = MT == 64 ? ig_pixels<64>() : ig_pixels<32>();
+    PH = 1;
+    tpp = 1;
+    int64_t kmax = 0, neg = 0, right = 1;
+    for (int i0 = 0; i0 < g.sh; ++i0) {
+        const PhaseTaps th = phase_taps(i0, (int)g.ph, (int)g.kH, (int)g.sh, (int)g.dh);
+        const int64_t Ha = i0 < g.H ? (g.H - i0 + g.sh - 1) / g.sh : 0;
+        for (int j0 = 0; j0 < g.sw; ++j0) {
+            const PhaseTaps tw = phase_taps(j0, (int)g.pw, (int)g.kW, (int)g.sw, (int)g.dw);
+            const int64_t Wb = j0 < g.W ? (g.W - j0 + g.sw - 1) / g.sw : 0;
+            if (Ha == 0 || Wb == 0) continue;
+            tpp = std::max<int>(tpp, (int)((Ha * Wb + np - 1) / np));
+            const int64_t rows = rows_spanned(Ha, Wb, np);                  // phase rows a tile touches
+            PH = std::max<int>(PH, (int)(rows + th.span));
+            kmax = std::max<int64_t>(kmax, (int64_t)Cout * th.n * tw.n);
+            if (tw.n) {
+                neg = std::max<int64_t>(neg, -(int64_t)tw.e_min);
+                right = std::max<int64_t>(right, Wb + tw.e_min + tw.span);   // columns b + f < this
+            }
+        }
+    }
+    const int64_t kp = std::max<int64_t>(8, (kmax + 7) / 8 * 8);
+    const int64_t head = ((int64_t)MT * (kp + 4) + kp + 2 * g.kH * g.kW + 3) / 4 * 4;
+    for (int a = 1; a >= 0; --a) {
+        aligned = a != 0;
+        L = (int)(aligned ? (neg + 3) / 4 * 4 : neg);
+        PWs = (int)((L + right + 3) / 4 * 4);
+        const int64_t bytes = (head + (int64_t)Cout * PH * PWs) * 4;
+        if (bytes <= 160 * 1024) return (size_t)bytes;
+    }
+    return 0;
 }
 
 // The plane forms' 32-bit index arithmetic stays in range: every input
@@ -509,6 +796,8 @@ bool plane_indices_fit(const ConvGeom& g) {
     return (g.outH - 1) * g.sh + (g.kH - 1) * g.dh < lim && (g.outW - 1) * g.sw + (g.kW - 1) * g.dw < lim &&
            g.ph < lim && g.pw < lim && g.H < lim && g.W < lim;
 }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 tf_status make_geom(ConvGeom& g, int64_t N, int64_t C, int64_t H, int64_t W, int64_t kH, int64_t kW, int64_t sh,
                     int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw) {
@@ -609,8 +898,9 @@ tf_status tf_conv2d_fwd(tf_ctx* ctx, const float* x, const float* w, const float
                    Cout < (1 << 20),
                "tf_conv2d_fwd: extent beyond this kernel's 32-bit indexing");
     const int MT = Cout <= 32 ? 32 : 64;
-    int Kp, PH, PW;
-    const size_t lds = implicit_lds_bytes(g, MT, (int)K, Kp, PH, PW);
+    int Kp, PH, PWs, L;
+    bool aligned;
+    const size_t lds = implicit_lds_bytes(g, MT, (int)K, Kp, PH, PWs, L, aligned);
     if (lds == 0)
         return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_conv2d_fwd: filter rows and input patch exceed the 160 KB of LDS "
                                                   "(use tf_im2col + tf_gemm_ex)");
@@ -618,6 +908,8 @@ tf_status tf_conv2d_fwd(tf_ctx* ctx, const float* x, const float* w, const float
     const int np = MT == 64 ? ig_pixels<64>() : ig_pixels<32>();
     const int tpi = (int)((P + np - 1) / np);
     TF_REQUIRE(N * tpi < (1LL << 31), "tf_conv2d_fwd: too many blocks");
+    // 16-byte staging loads: bit 0 input rows, bit 1 filter rows.
+    const int vec = (aligned && W % 4 == 0 && aligned16(x) ? 1 : 0) | (K % 4 == 0 && aligned16(w) ? 2 : 0);
     const dim3 grid((unsigned)(N * tpi), (unsigned)((Cout + MT - 1) / MT));
     // Dynamic LDS above 64 KB needs the attribute; set once per kernel to the
     // whole 160 KB, before any launch (and any graph capture) uses it.
@@ -633,11 +925,11 @@ tf_status tf_conv2d_fwd(tf_ctx* ctx, const float* x, const float* w, const float
         return tfh::set_error(TF_ERR_HIP, "tf_conv2d_fwd: hipFuncSetAttribute (dynamic LDS) failed");
     }
     if (MT == 32) {
-        conv_fwd_implicit_kernel<32><<<grid, kIgThreads, lds, ctx->stream>>>(x, w, bias, y, g, (int)Cout, (int)K, Kp, PH, PW,
-                                                                      tpi, relu);
+        conv_fwd_implicit_kernel<32><<<grid, kIgThreads, lds, ctx->stream>>>(x, w, bias, y, g, (int)Cout, (int)K, Kp, PH,
+                                                                             PWs, L, tpi, relu, vec);
     } else {
-        conv_fwd_implicit_kernel<64><<<grid, kIgThreads, lds, ctx->stream>>>(x, w, bias, y, g, (int)Cout, (int)K, Kp, PH, PW,
-                                                                      tpi, relu);
+        conv_fwd_implicit_kernel<64><<<grid, kIgThreads, lds, ctx->stream>>>(x, w, bias, y, g, (int)Cout, (int)K, Kp, PH,
+                                                                             PWs, L, tpi, relu, vec);
     }
     return tfh::check_launch("conv_fwd_implicit_kernel");
 }
@@ -657,8 +949,9 @@ tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, flo
                "tf_conv2d_bwd_weight: extent beyond this kernel's 32-bit indexing");
     if (N == 0) return tf_hip_fill_f32(ctx, dw, 0.0f, Cout * K);
     const int MT = Cout <= 32 ? 32 : 64;
-    int Kc, PH, PW, slices;
-    const size_t lds = implicit_dw_lds_bytes(g, MT, (int)K, Kc, PH, PW, slices);
+    int Kc, PH, PWs, L, slices;
+    bool aligned;
+    const size_t lds = implicit_dw_lds_bytes(g, MT, (int)K, Kc, PH, PWs, L, slices, aligned);
     if (lds == 0)
         return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_conv2d_bwd_weight: dy tile, tap tables and input patch exceed the "
                                                   "160 KB of LDS (use tf_im2col + tf_gemm_ex)");
@@ -667,6 +960,8 @@ tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, flo
     const int tpi = (int)((P + np - 1) / np);
     const int64_t blocks = N * tpi;
     TF_REQUIRE(blocks < (1LL << 31), "tf_conv2d_bwd_weight: too many blocks");
+    // 16-byte staging loads: bit 0 input rows, bit 1 dy rows.
+    const int vec = (aligned && W % 4 == 0 && aligned16(x) ? 1 : 0) | (P % 4 == 0 && aligned16(dy) ? 2 : 0);
     st = tfh::ensure_workspace(ctx, (size_t)blocks * Cout * K * sizeof(float));
     if (st != TF_OK) return st;
     float* part = reinterpret_cast<float*>(ctx->ws);
@@ -684,13 +979,58 @@ tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, flo
     const dim3 grid((unsigned)blocks, (unsigned)((Cout + MT - 1) / MT));
     if (MT == 32)
         conv_bwd_weight_implicit_kernel<32><<<grid, kIgThreads, lds, ctx->stream>>>(x, dy, part, g, (int)Cout, (int)K,
-                                                                                   Kc, PH, PW, tpi, slices);
+                                                                                   Kc, PH, PWs, L, tpi, slices, vec);
     else
         conv_bwd_weight_implicit_kernel<64><<<grid, kIgThreads, lds, ctx->stream>>>(x, dy, part, g, (int)Cout, (int)K,
-                                                                                   Kc, PH, PW, tpi, slices);
+                                                                                   Kc, PH, PWs, L, tpi, slices, vec);
     st = tfh::check_launch("conv_bwd_weight_implicit_kernel");
     if (st != TF_OK) return st;
     return tfh::sum_partials(ctx, part, blocks, Cout, K, dw, K);
+}
+
+tf_status tf_conv2d_bwd_data(tf_ctx* ctx, const float* dy, const float* w, float* dx, int64_t N, int64_t C, int64_t H,
+                             int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t sh, int64_t sw, int64_t ph,
+                             int64_t pw, int64_t dh, int64_t dw_) {
+    TF_CTX_CHECK(ctx);
+    ConvGeom g;
+    tf_status st = make_geom(g, N, C, H, W, kH, kW, sh, sw, ph, pw, dh, dw_);
+    if (st != TF_OK) return st;
+    TF_REQUIRE(Cout > 0 && C > 0, "tf_conv2d_bwd_data: empty channel count");
+    if (N == 0) return TF_OK;
+    TF_REQUIRE(dy && w && dx, "tf_conv2d_bwd_data: null pointer");
+    TF_REQUIRE(Cout * kH * kW < (1 << 20) && N * C * H * W < (1LL << 31) && N * Cout * g.outH * g.outW < (1LL << 31) &&
+                   C * kH * kW < (1 << 20) && sh * sw <= 4096 && kH <= 4096 && kW <= 4096,
+               "tf_conv2d_bwd_data: extent beyond this kernel's 32-bit indexing");
+    const int MT = C <= 32 ? 32 : 64;
+    int PH, PWs, L, tpp;
+    bool aligned;
+    const size_t lds = implicit_dx_lds_bytes(g, MT, (int)Cout, PH, PWs, L, tpp, aligned);
+    if (lds == 0)
+        return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_conv2d_bwd_data: filter columns and dy patch exceed the 160 KB "
+                                                  "of LDS (use tf_gemm_ex + tf_col2im)");
+    const int64_t blocks = (N * tpp + 7) / 8 * 8 * sh * sw;  // see the kernel's block order
+    TF_REQUIRE(blocks < (1LL << 31), "tf_conv2d_bwd_data: too many blocks");
+    // 16-byte loads of dy rows.
+    const int vec = aligned && g.outW % 4 == 0 && aligned16(dy) ? 1 : 0;
+    static const bool lds_ok = [] {
+        const int all = 160 * 1024;
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(conv_bwd_data_implicit_kernel<32>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, all) == hipSuccess &&
+               hipFuncSetAttribute(reinterpret_cast<const void*>(conv_bwd_data_implicit_kernel<64>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, all) == hipSuccess;
+    }();
+    if (!lds_ok) {
+        (void)hipGetLastError();
+        return tfh::set_error(TF_ERR_HIP, "tf_conv2d_bwd_data: hipFuncSetAttribute (dynamic LDS) failed");
+    }
+    const dim3 grid((unsigned)blocks, (unsigned)((C + MT - 1) / MT));
+    if (MT == 32)
+        conv_bwd_data_implicit_kernel<32><<<grid, kIgThreads, lds, ctx->stream>>>(dy, w, dx, g, (int)Cout, PH, PWs, L, tpp,
+                                                                                 vec);
+    else
+        conv_bwd_data_implicit_kernel<64><<<grid, kIgThreads, lds, ctx->stream>>>(dy, w, dx, g, (int)Cout, PH, PWs, L, tpp,
+                                                                                 vec);
+    return tfh::check_launch("conv_bwd_data_implicit_kernel");
 }
 
 }  // extern "C"

@@ -310,6 +310,22 @@ def conv2d_bwd_weight(x, dy, dw, stride=(1, 1), pad=(0, 0), dil=(1, 1)):
     return dw
 
 
+def conv2d_bwd_data(dy, w, dx, stride=(1, 1), pad=(0, 0), dil=(1, 1)):
+    """dx = the data gradient of conv(x, w) for upstream dy, by the implicit-GEMM
+    kernel over the stride's sub-pixel phases (no dcol buffer, no col2im);
+    TFError with TF_ERR_UNSUPPORTED when the shape does not fit it."""
+    N, Cc, H, W = dx.shape
+    Cout, Cw, kH, kW = w.shape
+    if Cw != Cc:
+        raise ValueError("conv2d_bwd_data: weight and dx channel counts differ")
+    oh, ow = conv_out(H, kH, stride[0], pad[0], dil[0]), conv_out(W, kW, stride[1], pad[1], dil[1])
+    if tuple(dy.shape) != (N, Cout, oh, ow):
+        raise ValueError("conv2d_bwd_data: dy has the wrong shape")
+    call("tf_conv2d_bwd_data", _ctx(dy), dy.ptr, w.ptr, dx.ptr, N, Cc, H, W, Cout, kH, kW, stride[0], stride[1],
+         pad[0], pad[1], dil[0], dil[1])
+    return dx
+
+
 def col2im(col, dx, kH, kW, stride=(1, 1), pad=(0, 0), dil=(1, 1)):
     N, Cc, H, W = dx.shape
     oh, ow = conv_out(H, kH, stride[0], pad[0], dil[0]), conv_out(W, kW, stride[1], pad[1], dil[1])

@@ -243,6 +243,67 @@ def test_conv2d_bwd_weight_implicit_vs_float64(ctx, case):
     assert_bitexact(gw.numpy(), first, "second call")
 
 
+DX_EXTRA_CASES = [
+    # N, C, H, W, Cout, k, stride, pad, dil: phases that no tap reaches
+    (2, 3, 9, 10, 5, 1, 2, 0, 1),          # 1 x 1, stride 2: odd rows / columns get nothing
+    (2, 4, 11, 12, 6, 3, 2, 1, 2),         # dilation 2 = stride: every tap in one residue class
+    (1, 3, 10, 10, 4, 2, 3, 0, 1),         # stride 3 > kernel 2, trailing row beyond the last window
+    (3, 70, 8, 8, 16, 3, 1, 1, 1),         # 64 + 6 input channels: two channel blocks
+    (1, 2, 40, 200, 8, 3, 1, 1, 1),        # rows wider than a pixel tile (the dy patch holds Cout channels)
+]
+# The forward cases whose dy patch (Cout channels) fits the LDS.
+DX_CASES = [c for c in IMPLICIT_CASES if c[3] <= 64] + DX_EXTRA_CASES
+
+
+def _dx_truth(gy, w, x_shape, s, p, d):
+    """float64 adjoint of the bit-exact im2col map: dcol[n] = W^T dy[n], then
+    each col element adds into the input pixel im2col copied it from (found by
+    running im2col on the pixel index + 1; 0 marks padding)."""
+    N, C, H, W = x_shape
+    Cout, _, kH, kW = w.shape
+    src = (np.arange(N * C * H * W, dtype=np.float64) + 1).reshape(x_shape).astype(np.float32)
+    assert src.size < (1 << 24)                       # exact in float32
+    idx = oracle.im2col(src, kH, kW, s, s, p, p, d, d).astype(np.int64)
+    dcol = np.einsum("ok,nop->nkp", w.reshape(Cout, -1).astype(np.float64),
+                     gy.astype(np.float64).reshape(N, Cout, -1))
+    keep = idx > 0
+    return np.bincount(idx[keep] - 1, weights=dcol[keep], minlength=N * C * H * W).reshape(x_shape)
+
+
+@pytest.mark.parametrize("case", DX_CASES)
+def test_conv2d_bwd_data_implicit_vs_float64(ctx, case):
+    """tf_conv2d_bwd_data (implicit GEMM per sub-pixel phase, no dcol buffer,
+    no col2im) against the float64 adjoint of the bit-exact im2col map; every
+    dx element is written (dx starts as 7.0); bit-identical on a second call."""
+    ops = _ops()
+    N, C, H, W, Cout, k, s, p, d = case
+    oh, ow = ops.conv_out(H, k, s, p, d), ops.conv_out(W, k, s, p, d)
+    w = synth.normal(271 + Cout, (Cout, C, k, k), std=0.2)
+    gy = synth.normal(272 + N + C, (N, Cout, oh, ow))
+    want = _dx_truth(gy, w, (N, C, H, W), s, p, d)
+    dw_, dgy = ctx.array(w), ctx.array(gy)
+    dx = ctx.array(np.full((N, C, H, W), 7.0, np.float32))
+    ops.conv2d_bwd_data(dgy, dw_, dx, (s, s), (p, p), (d, d))
+    first = dx.numpy()
+    assert_close(first, want, RTOL32, f"implicit dX {case}")
+    ops.conv2d_bwd_data(dgy, dw_, dx, (s, s), (p, p), (d, d))
+    assert_bitexact(dx.numpy(), first, "second call")
+
+
+def test_conv2d_bwd_data_implicit_reports_unsupported(ctx):
+    """Filter columns plus dy patch over 160 KB of LDS: TF_ERR_UNSUPPORTED,
+    nothing written (the API then takes the dcol GEMM + col2im)."""
+    from tensors_amd._lib import TF_ERR_UNSUPPORTED, TFError
+    ops = _ops()
+    dy = ctx.zeros((1, 256, 40, 40))
+    w = ctx.zeros((256, 64, 3, 3))
+    dx = ctx.array(np.full((1, 64, 40, 40), 7.0, np.float32))
+    with pytest.raises(TFError) as e:
+        ops.conv2d_bwd_data(dy, w, dx, (1, 1), (1, 1))
+    assert e.value.status == TF_ERR_UNSUPPORTED
+    assert np.all(dx.numpy() == 7.0)
+
+
 def test_conv2d_fwd_implicit_reports_unsupported(ctx):
     """Filter rows plus input patch over 160 KB of LDS: TF_ERR_UNSUPPORTED,
     nothing written (the API then takes im2col + GEMM)."""
