@@ -364,10 +364,13 @@ tf_status tf_conv2d_fwd(tf_ctx* ctx, const float* x, const float* w, const float
 /* Conv2d weight gradient without a col buffer (implicit GEMM; replaces
  * nn/Conv2d.cpp:140-260's launch_im2col + per-sample GEMM + host
  * accumulation): dw[Cout][C][kH][kW] = sum over images and output pixels of
- * dy[n][co][p] * col[n][k][p], col gathered from x.  Float32; per-block
- * partials are summed in a fixed order (deterministic).  TF_ERR_UNSUPPORTED
- * when the dy tile, tap tables and input patch do not fit the LDS. */
-tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, float* dw, int64_t N, int64_t C,
+ * dy[n][co][p] * col[n][k][p], col gathered from x; and, when db is not
+ * NULL, the bias gradient db[co] = sum over images and pixels of dy[n][co][p]
+ * (launch_reduce_sum_axis_nchw, cuda/kernels/reduce_sum_axis.cu:53-120) from
+ * the same dy tiles.  Float32; per-block partials are summed in a fixed
+ * order (deterministic).  TF_ERR_UNSUPPORTED when the dy tile, tap tables
+ * and input patch do not fit the LDS. */
+tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, float* dw, float* db, int64_t N, int64_t C,
                                int64_t H, int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t stride_h,
                                int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dilation_h,
                                int64_t dilation_w);

@@ -385,12 +385,18 @@ std::vector<Tensor> Conv2dBackward::apply(std::vector<Tensor>&& grads) {
     Tensor dx, dw, db;
     if (gpu(dy)) {
         const int dev = dy.device().index;
+        const bool want_db = has_bias_ && wants(*this, 2);
+        bool implicit_dw = false;
         if (wants(*this, 1)) {
             dw = Tensor::empty(w.shape(), Dtype::Float32, dy.device());
+            if (want_db) db = Tensor::empty(Shape{g_.Cout}, Dtype::Float32, dy.device());
             // With the input saved (implicit forward): the implicit weight
-            // gradient, else col is formed here for the GEMM.
-            if (!saved_input_ || !hip::conv2d_backward_weight_implicit(saved, dy, dw, g_.sh, g_.sw, g_.ph, g_.pw,
-                                                                      g_.dh, g_.dw)) {
+            // gradient, which also forms the bias gradient from its dy tiles;
+            // else col is formed here for the GEMM.
+            implicit_dw = saved_input_ && dy.dtype() == Dtype::Float32 &&
+                          hip::conv2d_backward_weight_implicit(saved, dy, dw, want_db ? &db : nullptr, g_.sh, g_.sw,
+                                                               g_.ph, g_.pw, g_.dh, g_.dw);
+            if (!implicit_dw) {
                 Tensor col = saved;
                 if (saved_input_) {
                     col = Tensor::empty(Shape{g_.N, KK, P}, Dtype::Float32, dy.device());
@@ -400,7 +406,7 @@ std::vector<Tensor> Conv2dBackward::apply(std::vector<Tensor>&& grads) {
                              dw.data(), KK, 0, g_.N, true, dy.dtype(), Dtype::Float32, TF_EPI_NONE, nullptr);
             }
         }
-        if (has_bias_ && wants(*this, 2)) {
+        if (want_db && !implicit_dw) {
             db = Tensor::empty(Shape{g_.Cout}, Dtype::Float32, dy.device());
             hip::chansum_nchw(dy, db);
         }

@@ -443,17 +443,22 @@ bool conv2d_forward_implicit(const Tensor& x, const Tensor& w, const Tensor* bia
     return true;
 }
 
-bool conv2d_backward_weight_implicit(const Tensor& x, const Tensor& dy, Tensor& dw, int64_t sh, int64_t sw, int64_t ph,
-                                     int64_t pw, int64_t dh, int64_t dwl) {
+bool conv2d_backward_weight_implicit(const Tensor& x, const Tensor& dy, Tensor& dw, Tensor* db, int64_t sh, int64_t sw,
+                                     int64_t ph, int64_t pw, int64_t dh, int64_t dwl) {
     require_gpu(x, "hip::conv2d_backward_weight"); require_gpu(dy, "hip::conv2d_backward_weight");
     require_gpu(dw, "hip::conv2d_backward_weight");
     require(x.dtype() == Dtype::Float32 && dy.dtype() == Dtype::Float32 && dw.dtype() == Dtype::Float32,
             "hip::conv2d_backward_weight: Float32 only");
     const auto& xs = x.shape();
     const auto& ws = dw.shape();
+    if (db) {
+        require_gpu(*db, "hip::conv2d_backward_weight");
+        require(db->dtype() == Dtype::Float32 && db->numel() == ws[0], "hip::conv2d_backward_weight: db size");
+    }
     const int st = tf_conv2d_bwd_weight(ctx_of(x), static_cast<const float*>(x.data()),
-                                        static_cast<const float*>(dy.data()), static_cast<float*>(dw.data()), xs[0],
-                                        xs[1], xs[2], xs[3], ws[0], ws[2], ws[3], sh, sw, ph, pw, dh, dwl);
+                                        static_cast<const float*>(dy.data()), static_cast<float*>(dw.data()),
+                                        db ? static_cast<float*>(db->data()) : nullptr, xs[0], xs[1], xs[2], xs[3], ws[0],
+                                        ws[2], ws[3], sh, sw, ph, pw, dh, dwl);
     if (st == TF_ERR_UNSUPPORTED) return false;
     check(st, "hip::conv2d_backward_weight");
     return true;

@@ -127,9 +127,10 @@ void chansum_nchw(const Tensor& dy, Tensor& db);
 bool conv2d_forward_implicit(const Tensor& x, const Tensor& w, const Tensor* bias, Tensor& y, int64_t sh, int64_t sw,
                              int64_t ph, int64_t pw, int64_t dh, int64_t dw, bool relu);
 // Implicit-GEMM weight gradient (tf_conv2d_bwd_weight): false when the shape
-// does not fit the kernel's LDS (nothing was launched), else dw is written.
-bool conv2d_backward_weight_implicit(const Tensor& x, const Tensor& dy, Tensor& dw, int64_t sh, int64_t sw, int64_t ph,
-                                     int64_t pw, int64_t dh, int64_t dwl);
+// does not fit the kernel's LDS (nothing was launched), else dw is written,
+// and db (the bias gradient) too when it is not nullptr.
+bool conv2d_backward_weight_implicit(const Tensor& x, const Tensor& dy, Tensor& dw, Tensor* db, int64_t sh, int64_t sw,
+                                     int64_t ph, int64_t pw, int64_t dh, int64_t dwl);
 
 // Implicit-GEMM data gradient (tf_conv2d_bwd_data): false when the shape does
 // not fit the kernel's LDS (nothing was launched), else dx is written.

@@ -49,8 +49,12 @@ Conv2dGrad Conv2d::backward(Tensor grad_output, Tensor input) {
     // the shape fits their LDS layouts; else the im2col / col2im forms.
     Conv2dGrad g;
     g.grad_weight = Tensor::empty(w.shape(), Dtype::Float32, input.device());
-    if (!hip::conv2d_backward_weight_implicit(input, grad_output, g.grad_weight, stride_h_, stride_w_, pad_h_, pad_w_,
-                                              dilation_h_, dilation_w_)) {
+    g.grad_bias = bias_enabled_ ? Tensor::empty(Shape{out_channels_}, Dtype::Float32, input.device())
+                                : zeros(Shape{out_channels_}, Dtype::Float32, input.device());
+    const bool db_done = hip::conv2d_backward_weight_implicit(input, grad_output, g.grad_weight,
+                                                              bias_enabled_ ? &g.grad_bias : nullptr, stride_h_,
+                                                              stride_w_, pad_h_, pad_w_, dilation_h_, dilation_w_);
+    if (!db_done) {
         Tensor col = Tensor::empty(Shape{N, KK, P}, Dtype::Float32, input.device());
         hip::im2col(input, col, kernel_h_, kernel_w_, stride_h_, stride_w_, pad_h_, pad_w_, dilation_h_, dilation_w_);
         hip::gemm_ex(dev, false, true, out_channels_, KK, P, grad_output.data(), P, out_channels_ * P, col.data(), P,
@@ -66,8 +70,7 @@ Conv2dGrad Conv2d::backward(Tensor grad_output, Tensor input) {
         hip::col2im(dcol, g.grad_input, kernel_h_, kernel_w_, stride_h_, stride_w_, pad_h_, pad_w_, dilation_h_,
                     dilation_w_);
     }
-    g.grad_bias = zeros(Shape{out_channels_}, Dtype::Float32, input.device());
-    if (bias_enabled_) hip::chansum_nchw(grad_output, g.grad_bias);
+    if (bias_enabled_ && !db_done) hip::chansum_nchw(grad_output, g.grad_bias);
     return g;
 }
 

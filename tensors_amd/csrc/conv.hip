@@ -486,7 +486,7 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
                                                                               float* __restrict__ part, ConvGeom g,
                                                                               int Cout, int K, int Kc, int PH, int PWs,
                                                                               int L, int tiles_per_image, int slices,
-                                                                              int vec) {
+                                                                              int vec, int with_db) {
     extern __shared__ float smem[];
     constexpr int NP = ig_pixels<MT>();
     constexpr int NH = NP / 2;
@@ -524,7 +524,20 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
     const int wave = t >> 6, lane = t & 63, l32 = lane & 31, half = lane >> 5;
     const int TM = MT / 32, TK = Kc / 32, T = TM * TK;
     const int steps = NH / slices;                          // pixels per slice and lane half (a multiple of 4)
-    float* outp = part + (int64_t)blockIdx.x * Cout * K;
+    const int KD = K + with_db;                             // partial row: dw[co][0 .. K) then db[co]
+    float* outp = part + (int64_t)blockIdx.x * Cout * KD;
+    if (with_db) {
+        // db partial: the block's dy row sums (pixels past the image hold 0),
+        // lane pairs then a butterfly in a fixed order.
+        for (int r = wave; r < MT; r += kIgThreads / 64) {
+            const float* row = dyt + r * RS;
+            float v = 0.0f;
+            for (int q = lane; q < NP; q += 64) v += row[q];
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+            if (lane == 0 && co0 + r < Cout) outp[(int64_t)(co0 + r) * KD + K] = v;
+        }
+    }
     for (int item = wave; item < T * slices; item += kIgThreads / 64) {
         const int tile = item / slices, sl = item - tile * slices;
         const int tr = tile / TK, tc = tile - tr * TK;
@@ -536,7 +549,7 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int co = co0 + tr * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                if (co < Cout && k < K) outp[(int64_t)co * K + k] = acc[r];
+                if (co < Cout && k < K) outp[(int64_t)co * KD + k] = acc[r];
             }
         } else {
 #pragma unroll
@@ -553,10 +566,39 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
                 float v = red[((tile * slices) * 16 + r) * 64 + lane];
                 for (int sl = 1; sl < slices; ++sl) v += red[((tile * slices + sl) * 16 + r) * 64 + lane];
                 const int co = co0 + tr * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                if (co < Cout && k < K) outp[(int64_t)co * K + k] = v;
+                if (co < Cout && k < K) outp[(int64_t)co * KD + k] = v;
             }
         }
     }
+}
+
+// dw[co][k] (k < K) and db[co] (k == K when KD = K + 1) = the sum over the
+// weight-gradient blocks b of part[b][co][k].  A workgroup owns 16
+// consecutive partial elements x 16 block groups; each thread adds blocks
+// g, g + 16, ... in ascending order (loads in flight together) and the 16
+// group sums are combined in a fixed tree order: deterministic.
+__global__ __launch_bounds__(256) void conv_partial_sum_kernel(const float* __restrict__ part, int blocks,
+                                                               int64_t plane, int K, int KD, float* __restrict__ dw,
+                                                               float* __restrict__ db) {
+    __shared__ float red[16][17];
+    const int el = threadIdx.x & 15, g = threadIdx.x >> 4;
+    const int64_t i = (int64_t)blockIdx.x * 16 + el;
+    float s = 0.0f;
+    if (i < plane) {
+#pragma unroll 8
+        for (int b = g; b < blocks; b += 16) s += part[(int64_t)b * plane + i];
+    }
+    red[g][el] = s;
+    __syncthreads();
+    if (threadIdx.x >= 16 || i >= plane) return;
+    float t[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) t[q] = red[2 * q][el] + red[2 * q + 1][el];
+    const float sum = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+    const int64_t co = i / KD;
+    const int k = (int)(i - co * KD);
+    if (k < K) dw[co * K + k] = sum;
+    else db[co] = sum;
 }
 
 // LDS layout of conv_bwd_weight_implicit_kernel, or 0 when it does not fit.
@@ -934,9 +976,9 @@ tf_status tf_conv2d_fwd(tf_ctx* ctx, const float* x, const float* w, const float
     return tfh::check_launch("conv_fwd_implicit_kernel");
 }
 
-tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, float* dw, int64_t N, int64_t C,
-                               int64_t H, int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t sh, int64_t sw,
-                               int64_t ph, int64_t pw, int64_t dh, int64_t dw_) {
+tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, float* dw, float* db, int64_t N,
+                               int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t sh,
+                               int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw_) {
     TF_CTX_CHECK(ctx);
     ConvGeom g;
     tf_status st = make_geom(g, N, C, H, W, kH, kW, sh, sw, ph, pw, dh, dw_);
@@ -947,7 +989,10 @@ tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, flo
     TF_REQUIRE(K < (1 << 20) && N * C * H * W < (1LL << 31) && N * Cout * g.outH * g.outW < (1LL << 31) &&
                    Cout < (1 << 20),
                "tf_conv2d_bwd_weight: extent beyond this kernel's 32-bit indexing");
-    if (N == 0) return tf_hip_fill_f32(ctx, dw, 0.0f, Cout * K);
+    if (N == 0) {
+        st = tf_hip_fill_f32(ctx, dw, 0.0f, Cout * K);
+        return st == TF_OK && db ? tf_hip_fill_f32(ctx, db, 0.0f, Cout) : st;
+    }
     const int MT = Cout <= 32 ? 32 : 64;
     int Kc, PH, PWs, L, slices;
     bool aligned;
@@ -962,7 +1007,9 @@ tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, flo
     TF_REQUIRE(blocks < (1LL << 31), "tf_conv2d_bwd_weight: too many blocks");
     // 16-byte staging loads: bit 0 input rows, bit 1 dy rows.
     const int vec = (aligned && W % 4 == 0 && aligned16(x) ? 1 : 0) | (P % 4 == 0 && aligned16(dy) ? 2 : 0);
-    st = tfh::ensure_workspace(ctx, (size_t)blocks * Cout * K * sizeof(float));
+    const int with_db = db ? 1 : 0;
+    const int64_t KD = K + with_db;
+    st = tfh::ensure_workspace(ctx, (size_t)blocks * Cout * KD * sizeof(float));
     if (st != TF_OK) return st;
     float* part = reinterpret_cast<float*>(ctx->ws);
     static const bool lds_ok = [] {
@@ -979,13 +1026,18 @@ tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, flo
     const dim3 grid((unsigned)blocks, (unsigned)((Cout + MT - 1) / MT));
     if (MT == 32)
         conv_bwd_weight_implicit_kernel<32><<<grid, kIgThreads, lds, ctx->stream>>>(x, dy, part, g, (int)Cout, (int)K,
-                                                                                   Kc, PH, PWs, L, tpi, slices, vec);
+                                                                                   Kc, PH, PWs, L, tpi, slices, vec,
+                                                                                   with_db);
     else
         conv_bwd_weight_implicit_kernel<64><<<grid, kIgThreads, lds, ctx->stream>>>(x, dy, part, g, (int)Cout, (int)K,
-                                                                                   Kc, PH, PWs, L, tpi, slices, vec);
+                                                                                   Kc, PH, PWs, L, tpi, slices, vec,
+                                                                                   with_db);
     st = tfh::check_launch("conv_bwd_weight_implicit_kernel");
     if (st != TF_OK) return st;
-    return tfh::sum_partials(ctx, part, blocks, Cout, K, dw, K);
+    const int64_t plane = Cout * KD;
+    conv_partial_sum_kernel<<<(unsigned)((plane + 15) / 16), 256, 0, ctx->stream>>>(part, (int)blocks, plane, (int)K,
+                                                                                  (int)KD, dw, db);
+    return tfh::check_launch("conv_partial_sum_kernel");
 }
 
 tf_status tf_conv2d_bwd_data(tf_ctx* ctx, const float* dy, const float* w, float* dx, int64_t N, int64_t C, int64_t H,

@@ -294,8 +294,9 @@ def conv2d_fwd(x, w, y, bias=None, stride=(1, 1), pad=(0, 0), dil=(1, 1), relu=F
     return y
 
 
-def conv2d_bwd_weight(x, dy, dw, stride=(1, 1), pad=(0, 0), dil=(1, 1)):
-    """dw = sum over images and pixels of dy (x) col(x), by the implicit-GEMM
+def conv2d_bwd_weight(x, dy, dw, stride=(1, 1), pad=(0, 0), dil=(1, 1), db=None):
+    """dw = sum over images and pixels of dy (x) col(x), and (db given) the
+    bias gradient db = sum of dy over images and pixels, by the implicit-GEMM
     kernel (no col buffer); TFError with TF_ERR_UNSUPPORTED when the shape
     does not fit it."""
     N, Cc, H, W = x.shape
@@ -305,7 +306,10 @@ def conv2d_bwd_weight(x, dy, dw, stride=(1, 1), pad=(0, 0), dil=(1, 1)):
     oh, ow = conv_out(H, kH, stride[0], pad[0], dil[0]), conv_out(W, kW, stride[1], pad[1], dil[1])
     if tuple(dy.shape) != (N, Cout, oh, ow):
         raise ValueError("conv2d_bwd_weight: dy has the wrong shape")
-    call("tf_conv2d_bwd_weight", _ctx(x), x.ptr, dy.ptr, dw.ptr, N, Cc, H, W, Cout, kH, kW, stride[0], stride[1],
+    if db is not None and db.size != Cout:
+        raise ValueError("conv2d_bwd_weight: db must have one entry per output channel")
+    call("tf_conv2d_bwd_weight", _ctx(x), x.ptr, dy.ptr, dw.ptr, db.ptr if db is not None else None, N, Cc, H, W,
+         Cout, kH, kW, stride[0], stride[1],
          pad[0], pad[1], dil[0], dil[1])
     return dw
 

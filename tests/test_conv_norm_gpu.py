@@ -226,7 +226,8 @@ def test_conv2d_fwd_implicit_vs_float64(ctx, case, bias_relu):
 def test_conv2d_bwd_weight_implicit_vs_float64(ctx, case):
     """tf_conv2d_bwd_weight (implicit GEMM over each block's pixels, then a
     fixed-order sum of the per-block partials) against float64 on the
-    bit-exact im2col restatement; and bit-identical on a second call."""
+    bit-exact im2col restatement, with and without the bias gradient it forms
+    from the same dy tiles; bit-identical on a second call."""
     ops = _ops()
     N, C, H, W, Cout, k, s, p, d = case
     x = synth.normal(261 + N + C, (N, C, H, W))
@@ -239,8 +240,10 @@ def test_conv2d_bwd_weight_implicit_vs_float64(ctx, case):
     ops.conv2d_bwd_weight(dxx, dgy, gw, (s, s), (p, p), (d, d))
     first = gw.numpy()
     assert_close(first, want, RTOL32, f"implicit dW {case}")
-    ops.conv2d_bwd_weight(dxx, dgy, gw, (s, s), (p, p), (d, d))
-    assert_bitexact(gw.numpy(), first, "second call")
+    gb = ctx.array(np.full((Cout,), 7.0, np.float32))
+    ops.conv2d_bwd_weight(dxx, dgy, gw, (s, s), (p, p), (d, d), db=gb)
+    assert_bitexact(gw.numpy(), first, "second call, with db")
+    assert_close(gb.numpy(), gy.astype(np.float64).sum(axis=(0, 2, 3)), RTOL32, f"implicit db {case}")
 
 
 DX_EXTRA_CASES = [
