@@ -792,6 +792,188 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_data_implicit_kernel(cons
     }
 }
 
+// ---------------------------------------------------------------------------
+// Data gradient for convolutions with at most 256 output pixels per image
+// (strided layers): per image, the column gradient of a group of CG input
+// channels, dcol[m][p] = sum_co w[co][c0 + m / kk][m % kk] dy[n][co][p]
+// (m < CG kk, kk = kH kW), is formed on MFMA straight into LDS, and the
+// block then gathers it into dx (col2im from LDS).  nn/Conv2d.cpp:178-204
+// writes dcol for the whole batch to memory and launch_col2im reads it back.
+//
+// Block (8 waves) = one image x one channel group.  The K loop runs over co
+// in chunks of KC: LDS holds A[m][k] = w[k0 + k][c0 + m/kk][m%kk] (row stride
+// KC + 4) and B[k][p] = dy[n][k0 + k][p] (row stride 272, columns >= P zero);
+// wave w owns pixels 32 w .. 32 w + 31 (two 16-column tiles) and all R row
+// tiles of 16 (M = CG kk <= 16 R; tiles past M read rows that are never
+// stored, within the LDS allocation), with v_mfma_f32_16x16x4f32: per four
+// co, the R A reads and two B reads are issued together, then the 2 R
+// MFMAs.  Both strides keep the reads free of bank conflicts.  After the K
+// loop the accumulators go to LDS as D[m][p] (row stride 260, conflict-free
+// for the stores), and each thread sums, for its dx elements, the taps
+// reaching them in (ki, kj) order, as col2im does, from two small tables
+// built at the start: per input row the D offsets ki kW RD + oh outW of its
+// row taps, per input column the offsets kj RD + ow of its column taps.
+// ---------------------------------------------------------------------------
+constexpr int kDlxRB = 256 + 16;     // B row stride (words)
+constexpr int kDlxRD = 256 + 4;      // D row stride (words)
+
+// kDlxR row tiles of 16 (M <= 16 kDlxR), kDlxKC co per K chunk: <9, 64> (one
+// block per CU) or <5, 32> (two blocks per CU, whose phases then overlap).
+template <int kDlxR, int kDlxKC>
+__global__ __launch_bounds__(kIgThreads) void conv_bwd_data_lds_kernel(const float* __restrict__ dy,
+                                                                       const float* __restrict__ w,
+                                                                       float* __restrict__ dx, ConvGeom g, int Cout,
+                                                                       int CG, int RT, int tab_off, int vec,
+                                                                       int cols4) {
+    extern __shared__ float smem[];
+    const int C = (int)g.C, H = (int)g.H, W = (int)g.W, outW = (int)g.outW, outH = (int)g.outH;
+    const int P = outH * outW, kH = (int)g.kH, kW = (int)g.kW, kk = kH * kW;
+    const int groups = (C + CG - 1) / CG;
+    const int n = blockIdx.x / groups, c0 = (blockIdx.x - n * groups) * CG;
+    const int CGv = min(CG, C - c0), Mv = CGv * kk, Mp = RT * 16;
+    constexpr int RA = kDlxKC + 4;
+    float* As = smem;                                     // [Mp][RA]
+    float* Bs = smem + Mp * RA;                           // [KC][kDlxRB]
+    // Tap tables (after the larger of the two phases' layouts):
+    int* rcnt = reinterpret_cast<int*>(smem + tab_off);   // [H]
+    int* roff = rcnt + H;                                 // [H][kH]
+    int* ccnt = roff + H * kH;                            // [W]
+    int* coff = ccnt + W;                                 // [W][kW]
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, l16 = lane & 15, q = lane >> 4;
+    {
+        const int sh = (int)g.sh, sw = (int)g.sw, dh = (int)g.dh, dwl = (int)g.dw, ph = (int)g.ph, pw = (int)g.pw;
+        for (int ih = t; ih < H; ih += kIgThreads) {
+            int c = 0;
+            for (int ki = 0; ki < kH; ++ki) {
+                const int hh = ih + ph - ki * dh;
+                if (hh >= 0 && hh % sh == 0 && hh / sh < outH) roff[ih * kH + c++] = ki * kW * kDlxRD + (hh / sh) * outW;
+            }
+            rcnt[ih] = c;
+        }
+        for (int iw = t; iw < W; iw += kIgThreads) {
+            int c = 0;
+            for (int kj = 0; kj < kW; ++kj) {
+                const int ww = iw + pw - kj * dwl;
+                if (ww >= 0 && ww % sw == 0 && ww / sw < outW) coff[iw * kW + c++] = kj * kDlxRD + ww / sw;
+            }
+            ccnt[iw] = c;
+        }
+    }
+    v4f acc[kDlxR][2];
+#pragma unroll
+    for (int r = 0; r < kDlxR; ++r) acc[r][0] = acc[r][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const float* dyn = dy + (int64_t)n * Cout * P;
+    for (int k0 = 0; k0 < Cout; k0 += kDlxKC) {
+        const int kc = min(kDlxKC, Cout - k0), kcp = (kc + 3) & ~3;
+        // A: i = k Mp + m, consecutive m read consecutive filter elements.
+        const FastDiv fMp = fast_div(Mp);
+        for (int i = t; i < kcp * Mp; i += kIgThreads) {
+            int m;
+            const int k = divmod(i, fMp, m);
+            As[m * RA + k] = (k < kc && m < Mv) ? w[((int64_t)(k0 + k) * C + c0) * kk + m] : 0.0f;
+        }
+        stage_rows(dyn + (int64_t)k0 * P, P, kc, P, Bs, kDlxRB, kcp, kDlxRB / 4 - 4, vec != 0);
+        __syncthreads();
+        for (int s = 0; s < kcp; s += 4) {
+            const float* brow = Bs + (s + q) * kDlxRB + wave * 32 + l16;
+            const float b0 = brow[0], b1 = brow[16];
+            float a[kDlxR];
+#pragma unroll
+            for (int r = 0; r < kDlxR; ++r) a[r] = As[(r * 16 + l16) * RA + s + q];
+#pragma unroll
+            for (int r = 0; r < kDlxR; ++r) {
+                acc[r][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], b0, acc[r][0], 0, 0, 0);
+                acc[r][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], b1, acc[r][1], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+    // D[m][p]: lane holds rows 16 r + 4 q + i, column 32 wave + 16 ct + l16.
+    float* Ds = smem;
+#pragma unroll
+    for (int r = 0; r < kDlxR; ++r) {
+        if (r < RT) {
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (r * 16 + 4 * q + i < Mv) Ds[(r * 16 + 4 * q + i) * kDlxRD + wave * 32 + ct * 16 + l16] = acc[r][ct][i];
+        }
+    }
+    __syncthreads();
+    // col2im from LDS: dx[c0 + cl][ih][iw] = sum over its row taps (ki order)
+    // and column taps (kj order) of D[cl kk + ki kW + kj][oh outW + ow].
+    const int HW = H * W;
+    float* dxn = dx + ((int64_t)n * C + c0) * HW;
+    if (cols4) {
+        // Lane <-> input column (so a thread's column taps, at most four, sit
+        // in registers and the stores are coalesced); rpp rows per pass.
+        const int rpp = kIgThreads / W, slot = t / W, iw = t - slot * W;
+        if (slot < rpp) {
+            const int nc = ccnt[iw];
+            int cof[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) cof[b] = b < nc ? coff[iw * kW + b] : 0;
+            const int dcl = rpp / H, dih = rpp - dcl * H;
+            int cl = slot / H, ih = slot - cl * H;
+            for (int r = slot; r < CGv * H; r += rpp) {
+                const float* dc = Ds + cl * kk * kDlxRD;
+                const int nr = rcnt[ih];
+                float sum = 0.0f;
+                for (int a = 0; a < nr; ++a) {
+                    const float* drow = dc + roff[ih * kH + a];
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        if (b < nc) sum += drow[cof[b]];
+                }
+                dxn[cl * HW + ih * W + iw] = sum;
+                ih += dih;
+                cl += dcl;
+                if (ih >= H) {
+                    ih -= H;
+                    ++cl;
+                }
+            }
+        }
+        return;
+    }
+    const FastDiv fHW = fast_div(HW), fW = fast_div(W);
+    for (int e = t; e < CGv * HW; e += kIgThreads) {
+        int rem, iw;
+        const int cl = divmod(e, fHW, rem);
+        const int ih = divmod(rem, fW, iw);
+        const float* dc = Ds + cl * kk * kDlxRD;
+        const int nr = rcnt[ih], nc = ccnt[iw];
+        float sum = 0.0f;
+        for (int a = 0; a < nr; ++a) {
+            const float* drow = dc + roff[ih * kH + a];
+            for (int b = 0; b < nc; ++b) sum += drow[coff[iw * kW + b]];
+        }
+        dxn[e] = sum;
+    }
+}
+
+// LDS bytes, channel group and tap-table offset (words) of
+// conv_bwd_data_lds_kernel<R, KC>, or 0 when the shape is not its kind (more
+// than 256 output pixels, or no channel group whose D tile fits `limit`).
+size_t dx_lds_bytes(const ConvGeom& g, int R, int KC, int64_t limit, int& CG, int& RT, int& tab_off) {
+    const int64_t P = g.outH * g.outW, kk = g.kH * g.kW;
+    if (P > 256 || kk > 16 * R) return 0;
+    CG = (int)std::min<int64_t>(g.C, 16 * R / kk);
+    RT = (int)((CG * kk + 15) / 16);
+    if ((int64_t)CG * g.H * g.W >= (1 << 22)) return 0;
+    // Phase 1 reads A rows up to 16 R - 1 (tiles past RT are computed and
+    // dropped): As plus Bs must cover them.  Phase 2 stores the CG kk rows.
+    const int64_t phase1 = std::max<int64_t>((int64_t)RT * 16 * (KC + 4) + (int64_t)KC * kDlxRB,
+                                             (int64_t)16 * R * (KC + 4));
+    const int64_t phase2 = (int64_t)CG * kk * kDlxRD;
+    tab_off = (int)std::max(phase1, phase2);
+    const int64_t tables = g.H * (1 + g.kH) + g.W * (1 + g.kW);
+    const int64_t bytes = (tab_off + tables) * 4;
+    return bytes <= limit ? (size_t)bytes : 0;
+}
+
 // LDS layout of conv_bwd_data_implicit_kernel (the largest phase), or 0 when
 // it does not fit; tpp = pixel tiles of the largest phase.  Patch columns:
 // column c holds dy column c - L, L = the most negative column offset of
@@ -1053,6 +1235,49 @@ tf_status tf_conv2d_bwd_data(tf_ctx* ctx, const float* dy, const float* w, float
     TF_REQUIRE(Cout * kH * kW < (1 << 20) && N * C * H * W < (1LL << 31) && N * Cout * g.outH * g.outW < (1LL << 31) &&
                    C * kH * kW < (1 << 20) && sh * sw <= 4096 && kH <= 4096 && kW <= 4096,
                "tf_conv2d_bwd_data: extent beyond this kernel's 32-bit indexing");
+    static const bool lds_ok = [] {
+        const int all = 160 * 1024;
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(conv_bwd_data_implicit_kernel<32>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, all) == hipSuccess &&
+               hipFuncSetAttribute(reinterpret_cast<const void*>(conv_bwd_data_implicit_kernel<64>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, all) == hipSuccess &&
+               hipFuncSetAttribute(reinterpret_cast<const void*>(conv_bwd_data_lds_kernel<5, 32>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, all) == hipSuccess &&
+               hipFuncSetAttribute(reinterpret_cast<const void*>(conv_bwd_data_lds_kernel<9, 64>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, all) == hipSuccess;
+    }();
+    if (!lds_ok) {
+        (void)hipGetLastError();
+        return tfh::set_error(TF_ERR_HIP, "tf_conv2d_bwd_data: hipFuncSetAttribute (dynamic LDS) failed");
+    }
+    // Strided layers with few output pixels and enough (image, channel group)
+    // blocks to fill the GPU: dcol per image in LDS, then col2im from LDS;
+    // two blocks per CU (small channel groups) when that layout fits.
+    if (sh > 1 || sw > 1) {
+        int CG, RT, tab_off;
+        bool two = true;
+        size_t lds_b = dx_lds_bytes(g, 5, 32, 80 * 1024, CG, RT, tab_off);
+        if (lds_b == 0 || N * ((C + CG - 1) / CG) < 256) {
+            two = false;
+            lds_b = dx_lds_bytes(g, 9, 64, 160 * 1024, CG, RT, tab_off);
+        }
+        const int64_t nblk = lds_b ? N * ((C + CG - 1) / CG) : 0;
+        if (nblk >= 128 && nblk < (1LL << 31)) {
+            const int64_t P = g.outH * g.outW;
+            const int vec = P % 4 == 0 && aligned16(dy) ? 1 : 0;
+            // Column-per-lane col2im: at most four column taps per input column.
+            int most = 0;
+            for (int j0 = 0; j0 < sw; ++j0) most = std::max(most, phase_taps(j0, (int)pw, (int)kW, (int)sw, (int)dw_).n);
+            const int cols4 = W <= kIgThreads && most <= 4 ? 1 : 0;
+            if (two)
+                conv_bwd_data_lds_kernel<5, 32><<<(unsigned)nblk, kIgThreads, lds_b, ctx->stream>>>(
+                    dy, w, dx, g, (int)Cout, CG, RT, tab_off, vec, cols4);
+            else
+                conv_bwd_data_lds_kernel<9, 64><<<(unsigned)nblk, kIgThreads, lds_b, ctx->stream>>>(
+                    dy, w, dx, g, (int)Cout, CG, RT, tab_off, vec, cols4);
+            return tfh::check_launch("conv_bwd_data_lds_kernel");
+        }
+    }
     const int MT = C <= 32 ? 32 : 64;
     int PH, PWs, L, tpp;
     bool aligned;
@@ -1064,17 +1289,6 @@ tf_status tf_conv2d_bwd_data(tf_ctx* ctx, const float* dy, const float* w, float
     TF_REQUIRE(blocks < (1LL << 31), "tf_conv2d_bwd_data: too many blocks");
     // 16-byte loads of dy rows.
     const int vec = aligned && g.outW % 4 == 0 && aligned16(dy) ? 1 : 0;
-    static const bool lds_ok = [] {
-        const int all = 160 * 1024;
-        return hipFuncSetAttribute(reinterpret_cast<const void*>(conv_bwd_data_implicit_kernel<32>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, all) == hipSuccess &&
-               hipFuncSetAttribute(reinterpret_cast<const void*>(conv_bwd_data_implicit_kernel<64>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, all) == hipSuccess;
-    }();
-    if (!lds_ok) {
-        (void)hipGetLastError();
-        return tfh::set_error(TF_ERR_HIP, "tf_conv2d_bwd_data: hipFuncSetAttribute (dynamic LDS) failed");
-    }
     const dim3 grid((unsigned)blocks, (unsigned)((C + MT - 1) / MT));
     if (MT == 32)
         conv_bwd_data_implicit_kernel<32><<<grid, kIgThreads, lds, ctx->stream>>>(dy, w, dx, g, (int)Cout, PH, PWs, L, tpp,

@@ -253,6 +253,10 @@ DX_EXTRA_CASES = [
     (1, 3, 10, 10, 4, 2, 3, 0, 1),         # stride 3 > kernel 2, trailing row beyond the last window
     (3, 70, 8, 8, 16, 3, 1, 1, 1),         # 64 + 6 input channels: two channel blocks
     (1, 2, 40, 200, 8, 3, 1, 1, 1),        # rows wider than a pixel tile (the dy patch holds Cout channels)
+    # strided, >= 128 (image, channel group) blocks: dcol per image in LDS, col2im from LDS
+    (160, 5, 13, 17, 12, 5, 3, 2, 1),      # 5 x 5, stride 3: 5 channels x 25 taps = 125 dcol rows, 56 pixels
+    (128, 3, 9, 10, 5, 1, 2, 0, 1),        # 1 x 1, stride 2: odd rows / columns get nothing
+    (64, 40, 12, 11, 70, 3, 2, 2, 2),      # dilation 2, 40 channels in groups of 16, 70 co (two K chunks)
 ]
 # The forward cases whose dy patch (Cout channels) fits the LDS.
 DX_CASES = [c for c in IMPLICIT_CASES if c[3] <= 64] + DX_EXTRA_CASES
@@ -275,9 +279,11 @@ def _dx_truth(gy, w, x_shape, s, p, d):
 
 @pytest.mark.parametrize("case", DX_CASES)
 def test_conv2d_bwd_data_implicit_vs_float64(ctx, case):
-    """tf_conv2d_bwd_data (implicit GEMM per sub-pixel phase, no dcol buffer,
-    no col2im) against the float64 adjoint of the bit-exact im2col map; every
-    dx element is written (dx starts as 7.0); bit-identical on a second call."""
+    """tf_conv2d_bwd_data (implicit GEMM per sub-pixel phase, or for strided
+    layers with enough blocks the column gradient per image in LDS gathered
+    from there; no dcol buffer in memory, no col2im launch) against the
+    float64 adjoint of the bit-exact im2col map; every dx element is written
+    (dx starts as 7.0); bit-identical on a second call."""
     ops = _ops()
     N, C, H, W, Cout, k, s, p, d = case
     oh, ow = ops.conv_out(H, k, s, p, d), ops.conv_out(W, k, s, p, d)
