@@ -574,6 +574,42 @@ def probe_bw() -> None:
     print(json.dumps({"bw_events_us": out}), flush=True)
 
 
+def probe_c4() -> None:
+    """Launches for rocprofv3 runs of config 4: 13 API training steps (3
+    warmup), then its five implicit-GEMM convolution launches at their C4
+    shapes (N 128; conv1 3 -> 32, 32 x 32, stride 1; conv2 32 -> 64, stride 2;
+    both 3 x 3, pad 1), 40 event-timed launches each over 4 buffer sets.
+    Prints the step time and the per-launch event timings (us) as one JSON
+    line."""
+    import tensors_amd as ta
+    from tensors_amd import api, ops, synth
+    xs = synth.normal(synth.seed(4, 0), (1, 128, 3, 32, 32))
+    ys = synth.uniform_int(synth.seed(4, 1), (1, 128), 10)
+    _, step_ms = api.cnn_train(xs, ys, steps=13, warmup=3, lr=0.01, mu=0.9, on_gpu=True)
+    ctx = ta.Context(0)
+    B, S = 128, 4
+    x1 = [ctx.array(synth.normal(synth.seed(7, i), (B, 3, 32, 32))) for i in range(S)]
+    h1 = [ctx.array(synth.normal(synth.seed(7, 10 + i), (B, 32, 32, 32))) for i in range(S)]
+    w1, b1 = ctx.array(synth.normal(synth.seed(7, 20), (32, 3, 3, 3), std=0.2)), ctx.zeros((32,))
+    w2, b2 = ctx.array(synth.normal(synth.seed(7, 21), (64, 32, 3, 3), std=0.06)), ctx.zeros((64,))
+    y1 = [ctx.empty((B, 32, 32, 32)) for _ in range(S)]
+    y2 = [ctx.empty((B, 64, 16, 16)) for _ in range(S)]
+    dy1 = [ctx.array(synth.normal(synth.seed(7, 30 + i), (B, 32, 32, 32))) for i in range(S)]
+    dy2 = [ctx.array(synth.normal(synth.seed(7, 40 + i), (B, 64, 16, 16))) for i in range(S)]
+    dh1 = [ctx.empty((B, 32, 32, 32)) for _ in range(S)]
+    gw1, gw2, gb1, gb2 = ctx.empty((32, 3, 3, 3)), ctx.empty((64, 32, 3, 3)), ctx.empty((32,)), ctx.empty((64,))
+    cases = {
+        "conv1_fwd": lambda i: ops.conv2d_fwd(x1[i], w1, y1[i], b1, (1, 1), (1, 1), (1, 1), True),
+        "conv2_fwd": lambda i: ops.conv2d_fwd(h1[i], w2, y2[i], b2, (2, 2), (1, 1), (1, 1), True),
+        "conv1_dw_db": lambda i: ops.conv2d_bwd_weight(x1[i], dy1[i], gw1, (1, 1), (1, 1), db=gb1),
+        "conv2_dw_db": lambda i: ops.conv2d_bwd_weight(h1[i], dy2[i], gw2, (2, 2), (1, 1), db=gb2),
+        "conv2_dx": lambda i: ops.conv2d_bwd_data(dy2[i], w2, dh1[i], (2, 2), (1, 1)),
+    }
+    out = {name: round(_rotating_bench(ctx, S, f, 40) * 1e3, 2) for name, f in cases.items()}
+    ctx.close()
+    print(json.dumps({"c4_step_ms": round(step_ms, 4), "conv_events_us": out}), flush=True)
+
+
 def c2_report(steps: int, warmup: int) -> dict:
     ms_step, mean, per = bench_c2(steps, warmup)
     bwd_ms = 0.5 * (mean["bwd_gemm_dx"] + mean["bwd_gemm_dw"])
@@ -615,13 +651,13 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--only-headline", action="store_true", help="skip the other configurations' measurements")
-    ap.add_argument("--probe", choices=["c2", "c5", "bw"],
+    ap.add_argument("--probe", choices=["c2", "c4", "c5", "bw"],
                     help="launch a config's kernels (bw: the bandwidth kernels) for a profiler, then exit")
     ap.add_argument("--hbm-ceiling", action="store_true",
                     help="run the HBM streaming-ceiling microbenchmark, print its JSON line, then exit")
     args = ap.parse_args(argv)
     if args.probe:
-        {"c2": probe_c2, "c5": probe_c5, "bw": probe_bw}[args.probe]()
+        {"c2": probe_c2, "c4": probe_c4, "c5": probe_c5, "bw": probe_bw}[args.probe]()
         return 0
     if args.hbm_ceiling:
         print(json.dumps({"hbm_ceiling": hbm_ceiling()}), flush=True)

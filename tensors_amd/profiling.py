@@ -457,6 +457,7 @@ def main(argv=None) -> int:
     s.add_argument("--c5-gemms", help="the run's kernel_trace.csv: add the per-GEMM table of the config-5 step")
     s.add_argument("--bench-log", help="file holding the bench's JSON line (event timings for that table)")
     s.add_argument("--tail-steps", type=int, default=7, help="steps of the bench's event-timed pass")
+    s.add_argument("--events-log", help="log of an unprofiled run of the same command: its JSON line is appended")
     t = sub.add_parser("traffic")
     t.add_argument("--fetch", required=True)
     t.add_argument("--write", required=True)
@@ -518,6 +519,11 @@ def main(argv=None) -> int:
                         line = json.loads(ln)
             text += ("\nConfig-5 GEMMs (dispatches of the C++ API step in launch order; split-K reductions "
                      "counted with their GEMM):\n\n" + c5_gemm_table(a.c5_gemms, line, a.tail_steps) + "\n")
+        if a.events_log:
+            ev = [ln for ln in Path(a.events_log).read_text().splitlines() if ln.startswith("{")]
+            if ev:
+                body = json.dumps(json.loads(ev[-1]), indent=1)
+                text += f"\nEvent timings of an unprofiled run of the same command:\n\n```json\n{body}\n```\n"
         if a.out:
             Path(a.out).write_text(text)
         else:
