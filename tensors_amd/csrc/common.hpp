@@ -67,11 +67,14 @@ tf_status partial_rows_sum(tf_ctx* ctx, const float* part, float* out_lo, float*
 inline bool bad_ctx(tf_ctx* ctx) { return ctx == nullptr || ctx->stream == nullptr; }
 
 // Slots of tf_ctx::tickets: the CE kernel's, then one per output tile of
-// the small fp32 GEMM (at most kTicketGemmTiles tiles).
+// the small fp32 GEMM (at most kTicketGemmTiles tiles), then one per
+// 32-column strip of the one-launch colsum.
 constexpr int kTicketCE = 0;
 constexpr int kTicketGemm = 64;
 constexpr int kTicketGemmTiles = 4096;
-constexpr int kTickets = kTicketGemm + kTicketGemmTiles;
+constexpr int kTicketColsum = kTicketGemm + kTicketGemmTiles;
+constexpr int kTicketColsumStrips = 4096;
+constexpr int kTickets = kTicketColsum + kTicketColsumStrips;
 
 // Launch timing (tf_hip_timing_*): a GEMM entry point constructs one of
 // these around its launches; while recording is on it records an event on

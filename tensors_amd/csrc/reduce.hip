@@ -1,8 +1,9 @@
 // Bias-gradient reductions, deterministic (no atomics, fixed summation order):
 //   colsum : db[c] = sum_r dy[r, c]           (Linear bias grad; fp32 or bf16 dy)
 //   chansum: db[c] = sum_{n,p} dy[n, c, p]    (Conv2d bias grad, NCHW)
-// Wide colsums (>= 2048 columns) run as one launch of column strips.  The
-// others are two-stage: stage 1 writes per-chunk partial sums to the context
+// Colsums over a multiple of 32 columns run as one launch of (strip, chunk)
+// blocks whose last arrival per strip adds the chunks.  The others are
+// two-stage: stage 1 writes per-chunk partial sums to the context
 // workspace, stage 2 (tfh::partial_rows_sum, also used by the LayerNorm
 // backward) adds them in a fixed order.  The reference's conv kernel
 // lets every block overwrite out[c] with its own partial
@@ -68,61 +69,109 @@ __global__ __launch_bounds__(256) void colsum_stage1(const T* __restrict__ dy, f
     }
 }
 
-// Single-launch colsum for wide matrices: block b owns a strip of W
-// consecutive columns and sums every row of it (no partials, no second
-// launch).  A lane takes 4 columns (one 16- or 8-byte load per row), W / 4
-// lanes cover a row of the strip, and the block's 256 / (W / 4) row groups
-// take rows g, g + groups, ... in ascending order, sixteen loads in flight.
-// The row groups are then added in a fixed order: a butterfly across the
-// lanes of a wave that hold the same columns, then the four waves in order
-// through LDS.  Strips are assigned XCD by XCD: workgroups are dispatched
-// round-robin over the 8 XCDs (block b on XCD b % 8), so strip
-// (b % 8) * (strips / 8) + b / 8 gives each XCD a contiguous column range,
-// and the strips that share a cache line share an L2.
-template <typename T, int W>
-__global__ __launch_bounds__(256) void colsum_strip_kernel(const T* __restrict__ dy, float* __restrict__ db, int rows,
-                                                           int cols, int strips) {
-    constexpr int LPR = W / 4;      // lanes per row of the strip
-    constexpr int RG = 256 / LPR;   // row groups
-    constexpr int U = 16;           // loads in flight per lane
-    __shared__ float4 red[4][LPR];
-    const int b = blockIdx.x;
-    const int strip = (b % 8) * (strips / 8) + b / 8;
-    const int cg = threadIdx.x % LPR, rg = threadIdx.x / LPR;
-    const int c0 = strip * W + 4 * cg;
+// One-launch colsum over (strip, chunk) blocks: block (s, c) sums rows
+// [c rpc, (c + 1) rpc) of the 32-column strip s (a 128-byte line per fp32
+// row): 8 lanes per row, 4 columns per lane, 32 row groups taking rows
+// g, g + 32, ... in ascending order with sixteen loads in flight, then a
+// butterfly across the lanes of a wave that hold the same columns and the
+// four waves in order through LDS.  The block stores its 32 sums to
+// part[s][c] and counts itself in on the strip's arrival counter; the block
+// that arrives last adds the strip's chunks in order 0, 1, ... into db and
+// resets the counter.  Partials and counter use agent-scope relaxed atomics
+// (coherent across the XCDs' L2s without cache maintenance), and a block's
+// stores have completed (vmcnt 0 in every thread, then the barrier) before it
+// counts itself in.  Strips are spread XCD by XCD (see the kernel).  Every
+// strip's counter sees only `chunks` arrivals, so
+// strips finish independently.  fp32 and bf16 inputs of one shape share the
+// grid and the order, so their sums are equal for equal values.
+constexpr int kTileCols = 32;
+constexpr int kTileU = 16;
+#ifndef TF_COLSUM_BLOCKS
+#define TF_COLSUM_BLOCKS 256
+#endif
+constexpr int kTileBlocks = TF_COLSUM_BLOCKS;   // (strip, chunk) blocks aimed for
+constexpr int kWaitVm0 = 0x0F70;   // s_waitcnt vmcnt(0), other counters free
+
+template <typename T>
+__global__ __launch_bounds__(256) void colsum_tile_kernel(const T* __restrict__ dy, float* __restrict__ db,
+                                                          float* __restrict__ part, unsigned* __restrict__ tickets,
+                                                          int rows, int cols, int rpc, int chunks) {
+    __shared__ float4 red[4][8];
+    __shared__ bool last;
+    // Workgroups go to the 8 XCDs round-robin (block x of a row of the grid
+    // on XCD x % 8 when the row length is a multiple of 8): each XCD takes a
+    // contiguous range of strips, so strips sharing a cache line (bf16: two
+    // 64-byte strips per 128-byte line) share an L2.
+    const int strips = gridDim.x;
+    const int strip = strips % 8 == 0 ? (blockIdx.x % 8) * (strips / 8) + blockIdx.x / 8 : blockIdx.x;
+    const int chunk = blockIdx.y;
+    const int cg = threadIdx.x & 7, rg = threadIdx.x >> 3;
+    const int c0 = strip * kTileCols + 4 * cg;
+    const int r0 = chunk * rpc, r1 = min(rows, r0 + rpc);
     const T* base = dy + c0;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    int r = rg;
-    for (; r + (U - 1) * RG < rows; r += U * RG) {
-        float4 v[U];
+    int r = r0 + rg;
+    for (; r + (kTileU - 1) * 32 < r1; r += kTileU * 32) {
+        float4 v[kTileU];
 #pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = vec4_f32(base + (int64_t)(r + u * RG) * cols);
+        for (int u = 0; u < kTileU; ++u) v[u] = vec4_f32(base + (int64_t)(r + 32 * u) * cols);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
+        for (int u = 0; u < kTileU; ++u) {
             acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
         }
     }
-    for (; r < rows; r += RG) {
+    for (; r < r1; r += 32) {
         const float4 v = vec4_f32(base + (int64_t)r * cols);
         acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
     }
 #pragma unroll
-    for (int off = LPR; off < 64; off <<= 1) {
+    for (int off = 8; off < 64; off <<= 1) {
         acc.x += __shfl_xor(acc.x, off, 64);
         acc.y += __shfl_xor(acc.y, off, 64);
         acc.z += __shfl_xor(acc.z, off, 64);
         acc.w += __shfl_xor(acc.w, off, 64);
     }
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (lane < LPR) red[wave][lane] = acc;
+    if (lane < 8) red[wave][lane] = acc;
     __syncthreads();
-    if (threadIdx.x < LPR) {
+    float* mine = part + ((int64_t)strip * chunks + chunk) * kTileCols;
+    if (threadIdx.x < 8) {
         const float4 a = red[0][cg], b1 = red[1][cg], c = red[2][cg], d = red[3][cg];
-        db[c0 + 0] = (a.x + b1.x) + (c.x + d.x);
-        db[c0 + 1] = (a.y + b1.y) + (c.y + d.y);
-        db[c0 + 2] = (a.z + b1.z) + (c.z + d.z);
-        db[c0 + 3] = (a.w + b1.w) + (c.w + d.w);
+        const float s[4] = {(a.x + b1.x) + (c.x + d.x), (a.y + b1.y) + (c.y + d.y), (a.z + b1.z) + (c.z + d.z),
+                            (a.w + b1.w) + (c.w + d.w)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // One chunk: the block's sums are the result.
+            if (chunks == 1) db[c0 + e] = s[e];
+            else __hip_atomic_store(mine + 4 * cg + e, s[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
+    if (chunks == 1) return;
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(tickets + strip, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (unsigned)(chunks - 1);
+    __syncthreads();
+    if (!last) return;
+    if (threadIdx.x < kTileCols) {
+        // The chunks' loads eight at a time in flight, added in chunk order.
+        const float* sp = part + (int64_t)strip * chunks * kTileCols + threadIdx.x;
+        float v = 0.0f;
+        int k = 0;
+        for (; k + 8 <= chunks; k += 8) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                t[u] = __hip_atomic_load(sp + (int64_t)(k + u) * kTileCols, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += t[u];
+        }
+        for (; k < chunks; ++k)
+            v += __hip_atomic_load(sp + (int64_t)k * kTileCols, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        db[strip * kTileCols + threadIdx.x] = v;
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(tickets + strip, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Stage 2 of every two-stage reduction here (colsum, chansum, LayerNorm
@@ -204,21 +253,19 @@ tf_status colsum_impl(tf_ctx* ctx, const T* dy, float* db, int64_t rows, int64_t
     TF_REQUIRE(db != nullptr && (rows == 0 || dy != nullptr), "tf_colsum: null pointer");
     if (rows == 0) return tf_hip_fill_f32(ctx, db, 0.0f, cols);
     const int vec = (reinterpret_cast<uintptr_t>(dy) & (4 * sizeof(T) - 1)) == 0 && cols % 4 == 0;
-    // Wide matrices: one launch of column strips (about one per CU), W = 8,
-    // 16 or 32 columns each.  The strip width depends only on cols, so an
-    // fp32 and a bf16 input of the same shape are summed in the same order.
-    if (vec && cols >= 2048) {
-        int w = 8;
-        while (w < 32 && cols / w > 256) w *= 2;
-        const int nstrips = (int)(cols / w);
-        if (cols % w == 0 && nstrips % 8 == 0) {
-            switch (w) {
-            case 8: colsum_strip_kernel<T, 8><<<nstrips, 256, 0, ctx->stream>>>(dy, db, (int)rows, (int)cols, nstrips); break;
-            case 16: colsum_strip_kernel<T, 16><<<nstrips, 256, 0, ctx->stream>>>(dy, db, (int)rows, (int)cols, nstrips); break;
-            default: colsum_strip_kernel<T, 32><<<nstrips, 256, 0, ctx->stream>>>(dy, db, (int)rows, (int)cols, nstrips); break;
-            }
-            return tfh::check_launch("colsum_strip_kernel");
-        }
+    // Widths in 32-column strips: one launch of (strip, chunk) blocks, about
+    // kTileBlocks of them, with the last block of each strip adding its chunks.
+    const int64_t tstrips = cols / kTileCols;
+    if (vec && cols % kTileCols == 0 && tstrips <= tfh::kTicketColsumStrips) {
+        int64_t chunks = std::max<int64_t>(1, std::min<int64_t>((kTileBlocks + tstrips - 1) / tstrips, (rows + 31) / 32));
+        const int rpc = (int)((rows + chunks - 1) / chunks);
+        chunks = (rows + rpc - 1) / rpc;
+        tf_status st = tfh::ensure_workspace(ctx, (size_t)tstrips * chunks * kTileCols * sizeof(float));
+        if (st != TF_OK) return st;
+        colsum_tile_kernel<T><<<dim3((unsigned)tstrips, (unsigned)chunks), 256, 0, ctx->stream>>>(
+            dy, db, reinterpret_cast<float*>(ctx->ws), ctx->tickets + tfh::kTicketColsum, (int)rows, (int)cols, rpc,
+            (int)chunks);
+        return tfh::check_launch("colsum_tile_kernel");
     }
     const int strips = (int)((cols + kColsPerBlock - 1) / kColsPerBlock);
     // Aim for ~512 stage-1 blocks (two per CU) with at least 16 rows each.

@@ -58,7 +58,8 @@ BW_KERNELS = {
                                3 * L3 * L3 * 4 + 3 * L3 * 4 + LN_ROW_BLOCKS * 2 * L3 * 4),
     # the partials read, dgamma and dbeta written
     "layernorm_bwd_partials_c3c": ("ln_part_strip_kernel", LN_ROW_BLOCKS * 2 * L3 * 4 + 2 * L3 * 4),
-    "colsum_c2": ("colsum_strip_kernel<float, 8>", N2 * N2 * 4 + N2 * 4),
+    # dy read, db written; the (strip, chunk) partials written and read back
+    "colsum_c2": ("colsum_tile_kernel<float>", N2 * N2 * 4 + N2 * 4),
     # p, g, v read; p, v written (W and b in one launch)
     "sgd_c2": ("sgd_multi_kernel<false>", 20 * (N2 * N2 + N2)),
     # as above plus the bf16 copy of every parameter

@@ -693,12 +693,12 @@ def test_softmax_bwd_uniform_is_zero(ctx):
 # ---------------------------------------------------------------------------
 # reductions
 # ---------------------------------------------------------------------------
-# (2048, 2048), (4096, 8192), (7, 4096), (3001, 16384): the one-launch strip
-# kernel (8, 32, 16, 32 columns per strip; row counts that do and do not fill
-# its 8-row batches); (100, 2056): wide, but 2056 columns do not split into
-# 16-column strips, so two-stage.
+# Multiples of 32 columns take the one-launch tile kernel: (2048, 2048),
+# (4096, 8192), (7, 4096), (3001, 16384), (64, 256), (33, 64) (a short last
+# chunk), (5000, 96) (157 chunks added by each strip's last block); the
+# others ((17, 19), (1, 5), (4096, 10), (3, 1001), (100, 2056)) are two-stage.
 @pytest.mark.parametrize("R,Cc", [(2048, 2048), (64, 256), (17, 19), (1, 5), (4096, 10), (3, 1001), (4096, 8192),
-                                  (7, 4096), (3001, 16384), (100, 2056)])
+                                  (7, 4096), (3001, 16384), (100, 2056), (33, 64), (5000, 96)])
 def test_colsum(ctx, R, Cc):
     ops = _ops()
     dy = synth.normal(151 + R, (R, Cc))
@@ -709,7 +709,7 @@ def test_colsum(ctx, R, Cc):
 
 
 @pytest.mark.parametrize("R,Cc", [(2048, 2048), (4096, 8192), (17, 19), (1, 5), (3, 1001), (64, 258), (7, 4096),
-                                  (3001, 16384)])
+                                  (3001, 16384), (5000, 96)])
 def test_colsum_bf16(ctx, R, Cc):
     # bf16 dy summed in fp32: bit-exact against the fp32 colsum of the widened
     # tensor (same order; widening is exact), and within fp32 tolerance of
