@@ -257,6 +257,7 @@ DX_EXTRA_CASES = [
     (160, 5, 13, 17, 12, 5, 3, 2, 1),      # 5 x 5, stride 3: 5 channels x 25 taps = 125 dcol rows, 56 pixels
     (128, 3, 9, 10, 5, 1, 2, 0, 1),        # 1 x 1, stride 2: odd rows / columns get nothing
     (64, 40, 12, 11, 70, 3, 2, 2, 2),      # dilation 2, 40 channels in groups of 16, 70 co (two K chunks)
+    (128, 2, 20, 21, 6, 9, 2, 4, 1),       # 9 x 9, stride 2: five column taps, the per-element col2im loop
 ]
 # The forward cases whose dy patch (Cout channels) fits the LDS.
 DX_CASES = [c for c in IMPLICIT_CASES if c[3] <= 64] + DX_EXTRA_CASES
@@ -297,6 +298,48 @@ def test_conv2d_bwd_data_implicit_vs_float64(ctx, case):
     assert_close(first, want, RTOL32, f"implicit dX {case}")
     ops.conv2d_bwd_data(dgy, dw_, dx, (s, s), (p, p), (d, d))
     assert_bitexact(dx.numpy(), first, "second call")
+
+
+class _Offset:
+    """A view of a device array starting one float in (4-byte aligned, not
+    16-byte aligned), with `shape` elements."""
+
+    def __init__(self, base, shape):
+        self.base = base                   # keeps the allocation alive
+        self.ctx, self.shape, self.dtype = base.ctx, tuple(shape), base.dtype
+        self.size = int(np.prod(self.shape))
+        self.ptr = base.ptr + 4
+
+
+@pytest.mark.parametrize("case", [(128, 32, 32, 32, 64, 3, 2, 1, 1), (3, 5, 13, 16, 40, 3, 1, 1, 1)])
+def test_conv2d_implicit_unaligned_operands_match_aligned(ctx, case):
+    """Operands that are not 16-byte aligned take the scalar staging loads of
+    the implicit kernels (forward, weight + bias gradient, both data-gradient
+    forms); the results equal the aligned calls bit for bit (same values,
+    same summation order)."""
+    ops = _ops()
+    N, C, H, W, Cout, k, s, p, d = case
+    oh, ow = ops.conv_out(H, k, s, p, d), ops.conv_out(W, k, s, p, d)
+    x = synth.normal(281, (N, C, H, W))
+    w = synth.normal(282, (Cout, C, k, k), std=0.2)
+    gy = synth.normal(283, (N, Cout, oh, ow))
+    pad = np.zeros(1, np.float32)
+
+    def both(a):
+        return ctx.array(a), _Offset(ctx.array(np.concatenate([pad, a.ravel()])), a.shape)
+
+    (xa, xu), (wa, wu), (ga, gu) = both(x), both(w), both(gy)
+    outs = []
+    for xx, ww, gg in ((xa, wa, ga), (xu, wu, gu)):
+        y = ctx.empty((N, Cout, oh, ow))
+        ops.conv2d_fwd(xx, ww, y, None, (s, s), (p, p), (d, d), False)
+        gw, gb = ctx.empty((Cout, C, k, k)), ctx.empty((Cout,))
+        ops.conv2d_bwd_weight(xx, gg, gw, (s, s), (p, p), (d, d), db=gb)
+        gx = ctx.empty((N, C, H, W))
+        ops.conv2d_bwd_data(gg, ww, gx, (s, s), (p, p), (d, d))
+        outs.append([t.numpy() for t in (y, gw, gb, gx)])
+    for name, a, b in zip(("y", "dw", "db", "dx"), outs[0], outs[1]):
+        assert_bitexact(b, a, f"unaligned {name} {case}")
 
 
 def test_conv2d_bwd_data_implicit_reports_unsupported(ctx):
