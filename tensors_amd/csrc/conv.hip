@@ -258,84 +258,134 @@ __device__ __forceinline__ int divmod(int x, const FastDiv& f, int& r) {
 
 constexpr int kStage4 = 8;  // 16-byte staging loads in flight per thread
 
+// Staging sources: slot i of a source is 16 bytes (4 floats) bound for LDS
+// word offset dst(i) (a multiple of 4), read by load(i, dst) with zeros
+// outside the operand.
+
+// rows x (slots s0 .. s0 + ns) of a row-major matrix: slot i is row i / ns,
+// columns 4 (s0 + i % ns) .. + 3 of src (row stride ld; rows < nrows and
+// columns < cols valid); 16-byte global loads when vec (cols and ld
+// multiples of 4, src 16-byte aligned).  LDS row stride dst_ld.
+struct RowSlots {
+    const float* src;
+    int ld, nrows, cols, dst_ld, s0, ns;
+    bool vec;
+    FastDiv fns;
+    __device__ __forceinline__ RowSlots(const float* src_, int ld_, int nrows_, int cols_, int dst_ld_, int s0_,
+                                        int ns_, bool vec_)
+        : src(src_), ld(ld_), nrows(nrows_), cols(cols_), dst_ld(dst_ld_), s0(s0_), ns(ns_), vec(vec_),
+          fns(fast_div(ns_)) {}
+    __device__ __forceinline__ v4f load(int i, int& dst) const {
+        int sl;
+        const int r = divmod(i, fns, sl);
+        const int c = 4 * (s0 + sl);
+        dst = r * dst_ld + c;
+        v4f val = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (r < nrows) {
+            const float* sp = src + r * ld + c;
+            if (vec) {
+                if (c < cols) val = *reinterpret_cast<const v4f*>(sp);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (c + e < cols) val[e] = sp[e];
+            }
+        }
+        return val;
+    }
+};
+
+// The zero-padded input patch: slot i (counted from slot g0) of
+// patch[ci][rr][c] = x[ci][ih_lo + rr][c - L] (zero outside the image), ci <
+// C, rr < PH, c < PWs, 4 floats per slot; xn is the image's first element.
+// 16-byte loads when vec (W % 4 == 0 and xn 16-byte aligned; L is a
+// multiple of 4, so slots never straddle the image edge).
+struct PatchSlots {
+    const float* xn;
+    int H, W, PH, L, ih_lo, g0;
+    bool vec;
+    FastDiv fspr, fPH;
+    __device__ __forceinline__ PatchSlots(const float* xn_, int H_, int W_, int PH_, int PWs, int L_, int ih_lo_,
+                                          int g0_, bool vec_)
+        : xn(xn_), H(H_), W(W_), PH(PH_), L(L_), ih_lo(ih_lo_), g0(g0_), vec(vec_), fspr(fast_div(PWs / 4)),
+          fPH(fast_div(PH_)) {}
+    __device__ __forceinline__ v4f load(int i, int& dst) const {
+        const int gi = g0 + i;
+        dst = 4 * gi;
+        int sl, rr;
+        const int row = divmod(gi, fspr, sl);
+        const int ci = divmod(row, fPH, rr);
+        const int ih = ih_lo + rr, iw = 4 * sl - L;
+        v4f val = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (ih >= 0 && ih < H) {
+            const float* sp = xn + (ci * H + ih) * W + iw;
+            if (vec) {
+                if (iw >= 0 && iw < W) val = *reinterpret_cast<const v4f*>(sp);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (iw + e >= 0 && iw + e < W) val[e] = sp[e];
+            }
+        }
+        return val;
+    }
+};
+
+// Slots [first, n) of `src` into LDS at `lds`, by the whole block, kStage4
+// loads in flight per thread before their stores.
+template <class Src>
+__device__ __forceinline__ void stage_slots(const Src& src, float* lds, int first, int n) {
+    for (int base = first + threadIdx.x; base < n; base += kIgThreads * kStage4) {
+        v4f v[kStage4];
+        int d[kStage4];
+#pragma unroll
+        for (int u = 0; u < kStage4; ++u) {
+            const int i = base + kIgThreads * u;
+            v[u] = i < n ? src.load(i, d[u]) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < kStage4; ++u) {
+            const int i = base + kIgThreads * u;
+            if (i < n) *reinterpret_cast<v4f*>(lds + d[u]) = v[u];
+        }
+    }
+}
+
+// The first R * kIgThreads slots of a source held in registers: load() issues
+// them, store() (after other work) writes them to LDS; the remaining slots
+// go through stage_slots(src, lds, R * kIgThreads, n).
+template <int R>
+struct Ahead {
+    v4f v[R];
+    int d[R];
+    template <class Src>
+    __device__ __forceinline__ void load(const Src& src, int n) {
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+            const int i = threadIdx.x + kIgThreads * u;
+            v[u] = i < n ? src.load(i, d[u]) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    __device__ __forceinline__ void store(float* lds, int n) const {
+#pragma unroll
+        for (int u = 0; u < R; ++u)
+            if ((int)threadIdx.x + kIgThreads * u < n) *reinterpret_cast<v4f*>(lds + d[u]) = v[u];
+    }
+};
+
 // rows x cols floats from src (row stride ld, rows < nrows valid, columns
 // < cols valid, zero elsewhere) into dst[r][0 .. 4 spr) with row stride
 // dst_ld; 16-byte global loads when vec (cols and ld multiples of 4, src
 // 16-byte aligned).  rows * spr < 2^22.
 __device__ __forceinline__ void stage_rows(const float* __restrict__ src, int ld, int nrows, int cols, float* dst,
                                            int dst_ld, int rows, int spr, bool vec) {
-    const int total = rows * spr;
-    const FastDiv fspr = fast_div(spr);
-    for (int base = threadIdx.x; base < total; base += kIgThreads * kStage4) {
-        v4f v[kStage4];
-#pragma unroll
-        for (int u = 0; u < kStage4; ++u) {
-            const int i = base + kIgThreads * u;
-            int sl;
-            const int r = divmod(i, fspr, sl);
-            const int c = 4 * sl;
-            v4f val = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-            if (i < total && r < nrows) {
-                const float* sp = src + r * ld + c;
-                if (vec) {
-                    if (c < cols) val = *reinterpret_cast<const v4f*>(sp);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (c + e < cols) val[e] = sp[e];
-                }
-            }
-            v[u] = val;
-        }
-#pragma unroll
-        for (int u = 0; u < kStage4; ++u) {
-            const int i = base + kIgThreads * u;
-            if (i < total) {
-                int sl;
-                const int r = divmod(i, fspr, sl);
-                *reinterpret_cast<v4f*>(dst + r * dst_ld + 4 * sl) = v[u];
-            }
-        }
-    }
+    stage_slots(RowSlots(src, ld, nrows, cols, dst_ld, 0, spr, vec), dst, 0, rows * spr);
 }
 
-// patch[ci][rr][c] = x[ci][ih_lo + rr][c - L] (zero outside the image) for
-// ci < C, rr < PH, c < PWs; xn is the image's first element.  16-byte loads
-// when vec (W % 4 == 0 and xn 16-byte aligned; L is a multiple of 4, so slots
-// never straddle the image edge).
+// The whole patch (C channels) into LDS; see PatchSlots.
 __device__ __forceinline__ void stage_patch(const float* __restrict__ xn, float* patch, int C, int H, int W, int PH,
                                             int PWs, int L, int ih_lo, bool vec) {
-    const int spr = PWs / 4;
-    const int total = C * PH * spr;
-    const FastDiv fspr = fast_div(spr), fPH = fast_div(PH);
-    for (int base = threadIdx.x; base < total; base += kIgThreads * kStage4) {
-        v4f v[kStage4];
-#pragma unroll
-        for (int u = 0; u < kStage4; ++u) {
-            const int i = base + kIgThreads * u;
-            int sl, rr;
-            const int row = divmod(i, fspr, sl);
-            const int ci = divmod(row, fPH, rr);
-            const int ih = ih_lo + rr, iw = 4 * sl - L;
-            v4f val = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-            if (i < total && ih >= 0 && ih < H) {
-                const float* sp = xn + (ci * H + ih) * W + iw;
-                if (vec) {
-                    if (iw >= 0 && iw < W) val = *reinterpret_cast<const v4f*>(sp);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (iw + e >= 0 && iw + e < W) val[e] = sp[e];
-                }
-            }
-            v[u] = val;
-        }
-#pragma unroll
-        for (int u = 0; u < kStage4; ++u) {
-            const int i = base + kIgThreads * u;
-            if (i < total) *reinterpret_cast<v4f*>(patch + 4 * i) = v[u];
-        }
-    }
+    stage_slots(PatchSlots(xn, H, W, PH, PWs, L, ih_lo, 0, vec), patch, 0, C * PH * (PWs / 4));
 }
 
 // acc += A (32 rows of wrow, k along the row) x B (32 pixels: pbase[koff[k]])
@@ -368,6 +418,35 @@ __device__ __forceinline__ v16f mfma_gather_loop(const float* wrow, const int* k
     return acc;
 }
 
+// acc += the k steps j0 .. j1 - 1 of 8 k each, lane half h taking k =
+// 8 j + 4 h .. 8 j + 4 h + 3 (wrow and krow already offset by 4 h), with the
+// next step's reads in flight during the current four MFMAs as above.
+__device__ __forceinline__ v16f mfma_gather_steps(v16f acc, const float* wrow, const int* krow, const float* pbase,
+                                                  int j0, int j1) {
+    if (j0 >= j1) return acc;
+    v4f a = *reinterpret_cast<const v4f*>(wrow + 8 * j0);
+    v4i kn = *reinterpret_cast<const v4i*>(krow + 8 * j0);
+    float b0 = pbase[kn.x], b1 = pbase[kn.y], b2 = pbase[kn.z], b3 = pbase[kn.w];
+    kn = *reinterpret_cast<const v4i*>(krow + 8 * min(j0 + 1, j1 - 1));
+    for (int j = j0; j < j1; ++j) {
+        const v4i kn2 = *reinterpret_cast<const v4i*>(krow + 8 * min(j + 2, j1 - 1));
+        const v4f an = *reinterpret_cast<const v4f*>(wrow + 8 * min(j + 1, j1 - 1));
+        const float c0 = pbase[kn.x], c1 = pbase[kn.y], c2 = pbase[kn.z], c3 = pbase[kn.w];
+        __builtin_amdgcn_sched_barrier(0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b1, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b2, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b3, acc, 0, 0, 0);
+        a = an;
+        b0 = c0;
+        b1 = c1;
+        b2 = c2;
+        b3 = c3;
+        kn = kn2;
+    }
+    return acc;
+}
+
 template <int MT>
 __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const float* __restrict__ x,
                                                                        const float* __restrict__ w,
@@ -378,7 +457,6 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
     extern __shared__ float smem[];
     constexpr int NP = ig_pixels<MT>();
     constexpr int MSUB = MT / 32;
-    const int KH2 = Kp / 2;
     const int RS = Kp + 4;                      // filter row stride (words): RS / 4 odd, no bank conflicts
     float* wk = smem;                           // [MT][RS]
     int* koff = reinterpret_cast<int*>(wk + MT * RS);   // [Kp]
@@ -392,13 +470,33 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
     const int C = (int)g.C, H = (int)g.H, W = (int)g.W, kHW = (int)(g.kH * g.kW), kW = (int)g.kW;
     const int t = threadIdx.x;
 
-    stage_rows(w + (int64_t)co0 * K, K, min(MT, Cout - co0), K, wk, RS, MT, Kp / 4, (vec & 2) != 0);
+    // Two phases: the k steps whose taps lie in the first CA channels, then
+    // the rest.  Phase A's filter columns and channels are staged first;
+    // phase B's loads are issued into registers before phase A's MFMAs and
+    // stored to LDS after them, so their latency overlaps the arithmetic.
+    // (A loop over four such phases measured slower: each phase adds a
+    // barrier and a staging tail.)
+    const int KS = Kp / 8;                                  // k steps of 8
+    const int KA8 = C >= 2 ? max(1, min(KS, ((C + 1) / 2) * kHW / 8)) : KS;
+    const int CA = min(C, (8 * KA8 + kHW - 1) / kHW);       // channels phase A reads
+    const int spr = PWs / 4;
+    const RowSlots w_a(w + (int64_t)co0 * K, K, min(MT, Cout - co0), K, RS, 0, 2 * KA8, (vec & 2) != 0);
+    const RowSlots w_b(w + (int64_t)co0 * K, K, min(MT, Cout - co0), K, RS, 2 * KA8, Kp / 4 - 2 * KA8, (vec & 2) != 0);
+    const float* xn = x + (int64_t)n * C * H * W;
+    const PatchSlots p_a(xn, H, W, PH, PWs, L, ih_lo, 0, (vec & 1) != 0);
+    const PatchSlots p_b(xn, H, W, PH, PWs, L, ih_lo, CA * PH * spr, (vec & 1) != 0);
+    const int n_wb = MT * (Kp / 4 - 2 * KA8), n_pb = (C - CA) * PH * spr;
     for (int k = t; k < Kp; k += kIgThreads) {
         const int kc = min(k, K - 1);
         const int ci = kc / kHW, rem = kc - ci * kHW, kh = rem / kW, kw = rem - kh * kW;
         koff[k] = (ci * PH + kh * (int)g.dh) * PWs + kw * (int)g.dw;
     }
-    stage_patch(x + (int64_t)n * C * H * W, patch, C, H, W, PH, PWs, L, ih_lo, (vec & 1) != 0);
+    stage_slots(w_a, wk, 0, MT * 2 * KA8);
+    stage_slots(p_a, patch, 0, CA * PH * spr);
+    constexpr int kAhead = 6;
+    Ahead<kAhead> ahead_w, ahead_p;
+    ahead_w.load(w_b, n_wb);
+    ahead_p.load(p_b, n_pb);
     __syncthreads();
 
     const int wave = t >> 6, lane = t & 63, l32 = lane & 31, half = lane >> 5;
@@ -410,8 +508,17 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
         const int oh = q / outW, ow = q - oh * outW;
         pix_off = (oh - oh_lo) * (int)g.sh * PWs + ow * (int)g.sw + L - (int)g.pw;
     }
-    const v16f acc = mfma_gather_loop(wk + (m_sub * 32 + l32) * RS + half * KH2, koff + half * KH2, patch + pix_off,
-                                      KH2);
+    const float* wrow = wk + (m_sub * 32 + l32) * RS + 4 * half;
+    const int* krow = koff + 4 * half;
+    v16f acc = mfma_gather_steps(v16f{}, wrow, krow, patch + pix_off, 0, KA8);
+    if (KA8 < KS) {
+        ahead_w.store(wk, n_wb);
+        stage_slots(w_b, wk, kAhead * kIgThreads, n_wb);
+        ahead_p.store(patch, n_pb);
+        stage_slots(p_b, patch, kAhead * kIgThreads, n_pb);
+        __syncthreads();
+        acc = mfma_gather_steps(acc, wrow, krow, patch + pix_off, KA8, KS);
+    }
 
     if (pp >= p_end) return;
     float* yn = y + (int64_t)n * Cout * P;
