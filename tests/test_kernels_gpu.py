@@ -190,10 +190,12 @@ def test_gemm_small_path_repeatable(ctx, ta, tb, M, N, K):
 
 
 def test_gemm_splitk_with_epilogue(ctx):
+    # 64 x 320 over K = 8192: too large for the small path, few tiles, so
+    # split-K with the bias and ReLU applied by the reduction.
     a = synth.normal(41, (64, 8192))
-    b = synth.normal(42, (8192, 64))
-    bias = synth.normal(43, (64,))
-    got = _run_gemm(ctx, a, b, False, False, 64, 64, bias=bias, relu=True)
+    b = synth.normal(42, (8192, 320))
+    bias = synth.normal(43, (320,))
+    got = _run_gemm(ctx, a, b, False, False, 64, 320, bias=bias, relu=True)
     assert_close(got, _gemm_truth(a, b, False, False, bias=bias, relu=True), RTOL32, "split-K + bias/relu")
 
 
