@@ -31,14 +31,15 @@ __device__ __forceinline__ int col_of(int c, int lane, int q, bool vec) {
 
 // Whole rows held in registers, read and written once: non-temporal vector
 // accesses.
-template <int NC>
+template <int NC, bool NT = true>
 __device__ __forceinline__ void load_row(const float* __restrict__ row, int cols, int lane, bool vec,
                                          float (&v)[NC][4]) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         int base = 256 * c + 4 * lane;
         if (vec && base + 4 <= cols) {
-            float4 t = tfd::ld_nt(reinterpret_cast<const float4*>(row + base));
+            const float4 t = NT ? tfd::ld_nt(reinterpret_cast<const float4*>(row + base))
+                                : *reinterpret_cast<const float4*>(row + base);
             v[c][0] = t.x; v[c][1] = t.y; v[c][2] = t.z; v[c][3] = t.w;
         } else {
 #pragma unroll
@@ -230,6 +231,162 @@ __global__ __launch_bounds__(WAVES * 64) void ln_bwd_fused_kernel(const float* _
     }
 }
 
+// ---------------------------------------------------------------------------
+// One launch for rows of up to 2048 columns (16-byte rows, cols % 32 == 0).
+// dgamma / dbeta need only x, dy and the saved mean / rstd, not the row
+// pass, so they are computed beside it instead of after it: blocks
+// [0, row_blocks) compute dx (a wave per row, as ln_bwd_fused_kernel, without
+// column partials), and each block after them sums a 32-column strip over a
+// chunk of rpc rows: 8 lanes x 4 columns per row, 32 row groups taking rows
+// g, g + 32, ... in ascending order (four rows' loads in flight), a
+// butterfly across the lanes holding the same columns, the four waves in
+// order through LDS.  It stores its 2 x 32 sums with agent-scope stores
+// and counts in on the strip's counter; the strip's last block adds the
+// chunks in order (deterministic) and resets the counter.  Both kinds read
+// x and dy with plain loads, so the second reader mostly hits the caches.
+// ---------------------------------------------------------------------------
+constexpr int kLnStrip = 32;
+#ifndef TF_LN_COL_BLOCKS
+#define TF_LN_COL_BLOCKS 256
+#endif
+constexpr int kLnColBlocks = TF_LN_COL_BLOCKS;   // (strip, chunk) blocks aimed for
+constexpr int kWaitVm0 = 0x0F70;   // s_waitcnt vmcnt(0), other counters free
+
+template <int NC>
+__global__ __launch_bounds__(256) void ln_bwd_onepass_kernel(const float* __restrict__ dy, const float* __restrict__ x,
+                                                             const float* __restrict__ gamma,
+                                                             const float* __restrict__ mean,
+                                                             const float* __restrict__ rstd, float* __restrict__ dx,
+                                                             float* __restrict__ dgamma, float* __restrict__ dbeta,
+                                                             float* __restrict__ part, unsigned* __restrict__ tickets,
+                                                             int rows, int cols, int rows_per_block, int row_blocks,
+                                                             int strips, int rpc, int chunks) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if ((int)blockIdx.x < row_blocks) {
+        const int r0 = blockIdx.x * rows_per_block, r1 = min(rows, r0 + rows_per_block);
+        const float inv_c = 1.0f / (float)cols;
+        float gm[NC][4];
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int j = col_of(c, lane, q, true);
+                gm[c][q] = j < cols ? gamma[j] : 0.0f;
+            }
+        for (int r = r0 + wave; r < r1; r += 4) {
+            float xv[NC][4], gv[NC][4];
+            load_row<NC, false>(x + (int64_t)r * cols, cols, lane, true, xv);
+            load_row<NC, false>(dy + (int64_t)r * cols, cols, lane, true, gv);
+            const float m = mean[r], rs = rstd[r];
+            float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float xh = (xv[c][q] - m) * rs;
+                    const float g = gv[c][q] * gm[c][q];
+                    s1 += g;
+                    s2 += g * xh;
+                    xv[c][q] = xh;
+                }
+            s1 = tfd::wave_sum(s1) * inv_c;
+            s2 = tfd::wave_sum(s2) * inv_c;
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) xv[c][q] = rs * (gv[c][q] * gm[c][q] - s1 - xv[c][q] * s2);
+            store_row<NC>(dx + (int64_t)r * cols, cols, lane, true, xv);
+        }
+        return;
+    }
+    __shared__ float4 red[4][2][8];
+    __shared__ bool last;
+    const int tb = blockIdx.x - row_blocks;
+    const int strip = tb % strips, chunk = tb / strips;
+    const int cg = threadIdx.x & 7, rg = threadIdx.x >> 3;
+    const int c0 = strip * kLnStrip + 4 * cg;
+    const int r0 = chunk * rpc, r1 = min(rows, r0 + rpc);
+    float4 ag = make_float4(0.f, 0.f, 0.f, 0.f), ab = ag;
+    auto add_row = [&](const float4 xv, const float4 dv, float m, float rs) {
+        ag.x += dv.x * ((xv.x - m) * rs); ag.y += dv.y * ((xv.y - m) * rs);
+        ag.z += dv.z * ((xv.z - m) * rs); ag.w += dv.w * ((xv.w - m) * rs);
+        ab.x += dv.x; ab.y += dv.y; ab.z += dv.z; ab.w += dv.w;
+    };
+    int r = r0 + rg;
+    for (; r + 3 * 32 < r1; r += 4 * 32) {
+        float4 xv[4], dv[4];
+        float m[4], rs[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t off = (int64_t)(r + 32 * u) * cols + c0;
+            xv[u] = *reinterpret_cast<const float4*>(x + off);
+            dv[u] = *reinterpret_cast<const float4*>(dy + off);
+            m[u] = mean[r + 32 * u];
+            rs[u] = rstd[r + 32 * u];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) add_row(xv[u], dv[u], m[u], rs[u]);
+    }
+    for (; r < r1; r += 32) {
+        const int64_t off = (int64_t)r * cols + c0;
+        add_row(*reinterpret_cast<const float4*>(x + off), *reinterpret_cast<const float4*>(dy + off), mean[r],
+                rstd[r]);
+    }
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) {
+        ag.x += __shfl_xor(ag.x, off, 64); ag.y += __shfl_xor(ag.y, off, 64);
+        ag.z += __shfl_xor(ag.z, off, 64); ag.w += __shfl_xor(ag.w, off, 64);
+        ab.x += __shfl_xor(ab.x, off, 64); ab.y += __shfl_xor(ab.y, off, 64);
+        ab.z += __shfl_xor(ab.z, off, 64); ab.w += __shfl_xor(ab.w, off, 64);
+    }
+    if (lane < 8) {
+        red[wave][0][lane] = ag;
+        red[wave][1][lane] = ab;
+    }
+    __syncthreads();
+    float* mine = part + ((int64_t)strip * chunks + chunk) * 2 * kLnStrip;
+    if (threadIdx.x < 16) {
+        const int h = threadIdx.x >> 3, q = threadIdx.x & 7;
+        const float4 a = red[0][h][q], b1 = red[1][h][q], c = red[2][h][q], d = red[3][h][q];
+        const float v[4] = {(a.x + b1.x) + (c.x + d.x), (a.y + b1.y) + (c.y + d.y), (a.z + b1.z) + (c.z + d.z),
+                            (a.w + b1.w) + (c.w + d.w)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (chunks == 1) (h ? dbeta : dgamma)[strip * kLnStrip + 4 * q + e] = v[e];
+            else __hip_atomic_store(mine + h * kLnStrip + 4 * q + e, v[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (chunks == 1) return;
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(tickets + strip, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (unsigned)(chunks - 1);
+    __syncthreads();
+    if (!last) return;
+    if (threadIdx.x < 2 * kLnStrip) {
+        // The chunks' sums eight loads at a time in flight, added in order.
+        const float* sp = part + (int64_t)strip * chunks * 2 * kLnStrip + threadIdx.x;
+        float v = 0.0f;
+        int k = 0;
+        for (; k + 8 <= chunks; k += 8) {
+            float t8[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                t8[u] = __hip_atomic_load(sp + (int64_t)(k + u) * 2 * kLnStrip, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += t8[u];
+        }
+        for (; k < chunks; ++k)
+            v += __hip_atomic_load(sp + (int64_t)k * 2 * kLnStrip, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int j = strip * kLnStrip + (threadIdx.x & (kLnStrip - 1));
+        if (threadIdx.x < kLnStrip) dgamma[j] = v;
+        else dbeta[j] = v;
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(tickets + strip, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Column sums of the row pass's partials part[K][W] (W = 2 * cols: the
 // dgamma columns, then the dbeta columns) in one launch of 32-column
 // strips.  Block s owns columns 32s .. 32s + 31 of every partial row: thread
@@ -399,6 +556,36 @@ tf_status tf_layernorm_bwd(tf_ctx* ctx, const float* dy, const float* x, const f
     }
     const int nc = chunks_for(cols);
     const bool vec = row_vec(x, cols) && row_vec(dy, cols) && row_vec(dx, cols);
+    const int64_t tstrips = cols / kLnStrip;
+    if (nc > 0 && vec && cols % kLnStrip == 0 && tstrips <= tfh::kTicketColsumStrips) {
+        // One launch: row blocks (4 waves, >= 1 row per wave, >= 256 blocks
+        // when the rows allow) beside (strip, chunk) blocks for dgamma/dbeta,
+        // about 256 of those.  The strip counters are the column sum's
+        // (tfh::kTicketColsum): kernels on one stream run in order and each
+        // leaves its counters at zero.
+        constexpr int waves = 4;
+        const int64_t rpb = std::max<int64_t>(waves, (rows + 255) / 256);
+        const int64_t row_blocks = (rows + rpb - 1) / rpb;
+        int64_t chunks =
+            std::max<int64_t>(1, std::min<int64_t>((kLnColBlocks + tstrips - 1) / tstrips, (rows + 31) / 32));
+        const int rpc = (int)((rows + chunks - 1) / chunks);
+        chunks = (rows + rpc - 1) / rpc;
+        tf_status st = tfh::ensure_workspace(ctx, (size_t)tstrips * chunks * 2 * kLnStrip * sizeof(float));
+        if (st != TF_OK) return st;
+        float* part = reinterpret_cast<float*>(ctx->ws);
+        const dim3 grid((unsigned)(row_blocks + tstrips * chunks));
+#define TF_LN_ONE(NC) ln_bwd_onepass_kernel<NC><<<grid, 256, 0, ctx->stream>>>(dy, x, gamma, mean, rstd, dx, dgamma, \
+                          dbeta, part, ctx->tickets + tfh::kTicketColsum, (int)rows, (int)cols, (int)rpb, (int)row_blocks, \
+                          (int)tstrips, rpc, (int)chunks)
+        switch (nc) {
+        case 1: TF_LN_ONE(1); break;
+        case 2: TF_LN_ONE(2); break;
+        case 4: TF_LN_ONE(4); break;
+        default: TF_LN_ONE(kMaxCached); break;
+        }
+#undef TF_LN_ONE
+        return tfh::check_launch("ln_bwd_onepass_kernel");
+    }
     if (nc > 0) {
         // Blocks of 4 waves, >= 1 row per wave, >= 256 blocks when the rows
         // allow (1024 rows: 256 blocks of one row per wave, every CU busy;
