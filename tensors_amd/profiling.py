@@ -43,7 +43,6 @@ C5_PARAMS = sum(C5_DIMS[i + 1] * C5_DIMS[i] + C5_DIMS[i + 1] for i in range(4)) 
 # launch must read and write, not what its caches re-fetch.
 R3, C3 = 4096, 1024                  # C3a / C3b: [4096 x 1024] fp32
 L3 = 1024                            # C3c: LayerNorm [1024 x 1024]
-LN_ROW_BLOCKS = 256                  # row blocks at 1024 rows; each writes 2 x 1024 partial sums
 CONV2 = (128, 32, 32, 32, 3, 16)     # C4 conv2: N, C, H, W, k, output side (stride 2, pad 1)
 _conv_x = CONV2[0] * CONV2[1] * CONV2[2] * CONV2[3] * 4
 _conv_col = CONV2[0] * CONV2[1] * CONV2[4] ** 2 * CONV2[5] ** 2 * 4
@@ -53,11 +52,10 @@ BW_KERNELS = {
     # one pass: logits and targets read, dlogits and the per-row nll written
     "ce_fused_fwd_bwd_c3a": ("ce_kernel<4, 2>", 2 * R3 * C3 * 4 + R3 * 8 + R3 * 4),
     "relu_bwd_c3b": ("binary_kernel<float, ReluBwdOp>", 3 * R3 * C3 * 4),
-    # dy, x read, dx written; gamma, mean, rstd read; the block partials written
-    "layernorm_bwd_rows_c3c": ("ln_bwd_fused_kernel<4, 4>",
-                               3 * L3 * L3 * 4 + 3 * L3 * 4 + LN_ROW_BLOCKS * 2 * L3 * 4),
-    # the partials read, dgamma and dbeta written
-    "layernorm_bwd_partials_c3c": ("ln_part_strip_kernel", LN_ROW_BLOCKS * 2 * L3 * 4 + 2 * L3 * 4),
+    # the whole op in one launch: dy, x read, dx written; gamma, mean, rstd
+    # read; dgamma, dbeta written (the column blocks' read of x and dy and
+    # their partials are not part of it)
+    "layernorm_bwd_op_c3c": ("ln_bwd_onepass_kernel<4>", 3 * L3 * L3 * 4 + 3 * L3 * 4 + 2 * L3 * 4),
     # dy read, db written; the (strip, chunk) partials written and read back
     "colsum_c2": ("colsum_tile_kernel<float>", N2 * N2 * 4 + N2 * 4),
     # p, g, v read; p, v written (W and b in one launch)
@@ -74,8 +72,7 @@ BW_CEILING = {
     "ce_bwd_c3a": ("copy (1R+1W)", True, 16),
     "ce_fused_fwd_bwd_c3a": ("copy (1R+1W)", True, 16),
     "relu_bwd_c3b": ("2R+1W", True, 16),
-    "layernorm_bwd_rows_c3c": ("2R+1W", True, 4),
-    "layernorm_bwd_partials_c3c": ("read only (1R)", True, 4),
+    "layernorm_bwd_op_c3c": ("2R+1W", True, 4),
     "colsum_c2": ("read only (1R)", True, 16),
     "sgd_c2": ("3R+2W (SGD mix)", False, 16),
     "sgd_c5": ("3R+2W (SGD mix)", True, 512),
@@ -140,12 +137,6 @@ def traffic(fetch_csv, write_csv, cal_n: int, kernels: dict | None = None) -> di
     if kernels is C2_KERNELS:
         bwd = [res["gemm_f32_bwd_dx_c2"], res["gemm_f32_bwd_dw_c2"]]
         res["gemm_f32_bwd_c2"] = round(sum(r["traffic_bytes"] for r in bwd) / 2)  # bench.py roofline.traffic
-    if "layernorm_bwd_rows_c3c" in res and "layernorm_bwd_partials_c3c" in res:
-        ln = [res["layernorm_bwd_rows_c3c"], res["layernorm_bwd_partials_c3c"]]
-        tb = sum(r["traffic_bytes"] for r in ln)
-        res["layernorm_bwd_op_c3c"] = {"kernels": "rows + partials", "traffic_bytes": tb,
-                                       "algorithmic_bytes": LN_OP_BYTES,
-                                       "traffic_over_algorithmic": round(tb / LN_OP_BYTES, 3)}
     return res
 
 
@@ -435,12 +426,6 @@ def bw_table(stats_csv: str | Path, traffic_json: str | Path, events_log: str | 
         lines.append(f"| `{sub}` | {label} | {ev if ev is not None else '-'} | {avg:.2f} | {algo / 1e6:.2f} | "
                      f"{gbps:.0f} | {gbps / 8000:.0%} | {cell_c} | {of_c} | "
                      f"{t.get('traffic_bytes', 0) / 1e6:.2f} | {t.get('traffic_over_algorithmic', '-')} |")
-    op = traffic_res.get("layernorm_bwd_op_c3c")
-    if op and "layernorm_bwd_op_c3c" in events:
-        us = events["layernorm_bwd_op_c3c"]
-        lines.append(f"| rows + partials | layernorm_bwd_op_c3c | {us} | - | {op['algorithmic_bytes'] / 1e6:.2f} | "
-                     f"{op['algorithmic_bytes'] / us / 1e3:.0f} | {op['algorithmic_bytes'] / us / 8e6:.0%} | - | - | "
-                     f"{op['traffic_bytes'] / 1e6:.2f} | {op['traffic_over_algorithmic']} |")
     return "\n".join(lines)
 
 

@@ -113,7 +113,7 @@ def test_traffic_c5_attributes_split_reductions_to_their_gemm(tmp_path):
     assert dw["algorithmic_bytes_per_step"] >= 2 * (8192 * 4096 * 2) + 4 * 8192 * 8192
 
 
-def test_bandwidth_traffic_matches_qualified_names_and_sums_the_layernorm_op(tmp_path):
+def test_bandwidth_traffic_matches_qualified_names(tmp_path):
     # rocprofv3's counter CSV names kernels with their anonymous-namespace
     # qualifiers; the label table's substrings are written without them.
     n = 1 << 20
@@ -135,12 +135,10 @@ def test_bandwidth_traffic_matches_qualified_names_and_sums_the_layernorm_op(tmp
     for label, (_, algo) in profiling.BW_KERNELS.items():
         assert abs(res[label]["traffic_over_algorithmic"] - 1.0) < 1e-3, label
     assert "gemm_f32_bwd_c2" not in res
+    # the LayerNorm backward op is one launch; its algorithmic bytes are the
+    # op's operands and results
     op = res["layernorm_bwd_op_c3c"]
     assert op["algorithmic_bytes"] == profiling.LN_OP_BYTES == 12603392
-    rows, parts = res["layernorm_bwd_rows_c3c"], res["layernorm_bwd_partials_c3c"]
-    assert op["traffic_bytes"] == rows["traffic_bytes"] + parts["traffic_bytes"]
-    # the block partials' round trip is what the op moves beyond its operands
-    assert abs(op["traffic_bytes"] - op["algorithmic_bytes"] - 2 * profiling.LN_ROW_BLOCKS * 2 * 1024 * 4) < 64
 
 
 def test_ceiling_and_bandwidth_tables(tmp_path):
@@ -167,11 +165,11 @@ def test_ceiling_and_bandwidth_tables(tmp_path):
                                                         "traffic_over_algorithmic": 1.349}}))
     bw = profiling.bw_table(stats, tj, elog, clog)
     lines = bw.splitlines()
-    assert len(lines) == 2 + len(profiling.BW_KERNELS) + 1
+    assert len(lines) == 2 + len(profiling.BW_KERNELS)
     relu = next(ln for ln in lines if "relu_bwd_c3b" in ln)
     # 50,331,648 B in 20 us = 2517 GB/s; 20 us rocprof average
     assert "| 20.0 | 20.00 | 50.33 | 2517 |" in relu
-    assert "layernorm_bwd_op_c3c | 10.0 |" in lines[-1]
+    assert "layernorm_bwd_op_c3c | 10.0 |" in next(ln for ln in lines if "layernorm" in ln)
 
 
 def test_mfma_table_groups_dispatches_by_c5_position(tmp_path):
