@@ -11,11 +11,14 @@
 // Reference-compatible mode reproduces the stub exactly: dx = dy * gamma,
 // dgamma = dbeta = 0.
 //
-// Rows of up to 2048 columns: one fused pass (one wave per row, the row held
-// in registers; each wave also accumulates its rows' dgamma/dbeta column
-// partials, combined per block in LDS and then across blocks by a
-// fixed-order column-strip reduction).  Wider rows: a streaming row kernel
-// for dx and a column kernel for dgamma/dbeta.
+// Rows of up to 2048 columns whose width is a multiple of 32 (16-byte rows):
+// one launch, row blocks for dx beside (strip, chunk) blocks for
+// dgamma/dbeta (ln_bwd_onepass_kernel).  Other rows of up to 2048 columns:
+// one fused pass (one wave per row, the row held in registers; each wave
+// also accumulates its rows' dgamma/dbeta column partials, combined per block
+// in LDS and then across blocks by a fixed-order column-strip reduction).
+// Wider rows: a streaming row kernel for dx and a column kernel for
+// dgamma/dbeta.
 #include "common.hpp"
 
 #include <algorithm>
