@@ -265,8 +265,14 @@ __global__ __launch_bounds__(256) void ln_bwd_onepass_kernel(const float* __rest
                                                              int rows, int cols, int rows_per_block, int row_blocks,
                                                              int strips, int rpc, int chunks) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // Workgroups go to the 8 XCDs round-robin (block b to XCD b % 8).  When
+    // the counts allow, XCD x gets the row blocks of one contiguous eighth of
+    // the rows and the column blocks of the chunks inside that eighth, so a
+    // row's second reader finds it in the XCD's own L2.
+    const bool xcd_map = (row_blocks & 7) == 0 && (chunks & 7) == 0;
     if ((int)blockIdx.x < row_blocks) {
-        const int r0 = blockIdx.x * rows_per_block, r1 = min(rows, r0 + rows_per_block);
+        const int rb = xcd_map ? (blockIdx.x & 7) * (row_blocks >> 3) + (blockIdx.x >> 3) : (int)blockIdx.x;
+        const int r0 = rb * rows_per_block, r1 = min(rows, r0 + rows_per_block);
         const float inv_c = 1.0f / (float)cols;
         float gm[NC][4];
 #pragma unroll
@@ -305,7 +311,15 @@ __global__ __launch_bounds__(256) void ln_bwd_onepass_kernel(const float* __rest
     __shared__ float4 red[4][2][8];
     __shared__ bool last;
     const int tb = blockIdx.x - row_blocks;
-    const int strip = tb % strips, chunk = tb / strips;
+    int strip, chunk;
+    if (xcd_map) {
+        const int k = chunks >> 3, idx = tb >> 3;
+        chunk = (tb & 7) * k + idx % k;
+        strip = idx / k;
+    } else {
+        strip = tb % strips;
+        chunk = tb / strips;
+    }
     const int cg = threadIdx.x & 7, rg = threadIdx.x >> 3;
     const int c0 = strip * kLnStrip + 4 * cg;
     const int r0 = chunk * rpc, r1 = min(rows, r0 + rpc);
