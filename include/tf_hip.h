@@ -316,6 +316,15 @@ tf_status tf_colsum(tf_ctx* ctx, const float* dy, float* db, int64_t rows, int64
 /* The same for bf16 dy (bit patterns), summed in fp32; equal to tf_colsum of
  * the widened tensor (the bf16 compute path's bias grad, no cast pass). */
 tf_status tf_colsum_bf16(tf_ctx* ctx, const void* dy, float* db, int64_t rows, int64_t cols);
+/* dz = dy * (x > 0 ? 1 : 0) over a [rows x cols] matrix, then
+ * db[c] = sum_r dz[r, c]: the ReLU backward (autograd/ops/ReluBackward.hpp:22-32)
+ * of a ReLU that follows a Linear with bias, fused with that Linear's bias
+ * gradient (nn::Linear::forward_relu's backward).  dtype TF_F32 or TF_BF16
+ * (dy, x, dz); db is fp32.  dz is bit-identical to tf_relu_bwd and db to
+ * tf_colsum / tf_colsum_bf16 of that dz; one pass over dy and x where the
+ * column-strip launch applies, else those two calls. */
+tf_status tf_relu_bwd_colsum(tf_ctx* ctx, const void* dy, const void* x, void* dz, float* db, int64_t rows,
+                             int64_t cols, int dtype);
 /* db[c] = sum_{n,hw} dy[n, c, hw]  (replaces launch_reduce_sum_axis_nchw,
  * cuda/kernels/reduce_sum_axis.cu:53-120, which is wrong for H*W > 256) */
 tf_status tf_chansum_nchw(tf_ctx* ctx, const float* dy, float* db,

@@ -230,7 +230,22 @@ std::vector<Tensor> MatmulBackward::apply(std::vector<Tensor>&& grads) {
 }
 
 std::vector<Tensor> ReluBackward::apply(std::vector<Tensor>&& grads) {
-    return {raw::relu_backward(grads[0], input_.unpack())};
+    const Tensor& x = input_.unpack();
+    const Tensor& g = grads[0];
+    auto* linear = fuse_bias_grad_ && !next_edges_.empty()
+                       ? dynamic_cast<LinearBackward*>(next_edges_[0].function.get())
+                       : nullptr;
+    if (linear && gpu(g) && g.dtype() == x.dtype() && g.shape() == x.shape() && g.shape().ndim() >= 1 &&
+        g.stride() == Stride::compute_row_major(g.shape()) && linear->sums_bias_grad_of(g.dtype())) {
+        // The masked gradient's column sums are the Linear's bias gradient:
+        // both in one pass over g and x.
+        Tensor dz = raw::empty_like(g);
+        Tensor db = Tensor::empty(Shape{g.shape()[g.shape().ndim() - 1]}, Dtype::Float32, g.device());
+        hip::relu_backward_colsum(g, x, dz, db);
+        linear->set_bias_grad(std::move(db));
+        return {std::move(dz)};
+    }
+    return {raw::relu_backward(g, x)};
 }
 
 std::vector<Tensor> SigmoidBackward::apply(std::vector<Tensor>&& grads) {
@@ -341,8 +356,13 @@ std::vector<Tensor> LinearBackward::apply(std::vector<Tensor>&& grads) {
             dw = raw::gemm(dy, true, x, false);
         }
     }
-    if (has_bias_ && wants(*this, 2)) db = raw::colsum(dy);
+    if (has_bias_ && wants(*this, 2)) db = pending_db_.storage() ? std::move(pending_db_) : raw::colsum(dy);
+    pending_db_ = Tensor();
     return {std::move(dx), std::move(dw), std::move(db)};
+}
+
+bool LinearBackward::sums_bias_grad_of(Dtype dt) const {
+    return has_bias_ && wants(*this, 2) && x_.data_.storage() && x_.data_.dtype() == dt;
 }
 
 std::vector<Tensor> CrossEntropyBackward::apply(std::vector<Tensor>&& grads) {

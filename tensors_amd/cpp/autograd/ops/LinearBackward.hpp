@@ -19,12 +19,20 @@ public:
     LinearBackward(const Tensor& x, const Tensor& weight, bool has_bias, Dtype grad_dtype)
         : x_(x), w_(weight), has_bias_(has_bias), grad_dtype_(grad_dtype) {}
     std::vector<Tensor> apply(std::vector<Tensor>&& grads) override;
-    void release_saved() override { x_.reset(); w_.reset(); }
+    void release_saved() override { x_.reset(); w_.reset(); pending_db_ = Tensor(); }
+    // True when apply() will sum an upstream gradient of dtype `dt` into a
+    // bias gradient as it arrives (no cast first).
+    bool sums_bias_grad_of(Dtype dt) const;
+    // A bias gradient already computed from the upstream gradient this node
+    // is about to receive (by the ReluBackward in front of it); apply() uses
+    // it instead of summing the columns again.
+    void set_bias_grad(Tensor db) { pending_db_ = std::move(db); }
 
 private:
     SavedTensor x_, w_;
     bool has_bias_;
     Dtype grad_dtype_;
+    Tensor pending_db_;
 };
 
 }  // namespace tensorforge

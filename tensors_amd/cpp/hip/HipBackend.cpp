@@ -428,6 +428,18 @@ void colsum(const Tensor& dy, Tensor& db) {
     check(tf_colsum(ctx_of(dy), static_cast<const float*>(dy.data()), static_cast<float*>(db.data()), r, c), "hip::colsum");
 }
 
+void relu_backward_colsum(const Tensor& dy, const Tensor& x, Tensor& dz, Tensor& db) {
+    const char* what = "hip::relu_backward_colsum";
+    require_gpu(dy, what); require_gpu(x, what); require_gpu(dz, what); require_gpu(db, what);
+    check_same(dy, x, what); check_same(dy, dz, what);
+    require(dy.shape() == x.shape() && dy.shape() == dz.shape(), std::string(what) + ": shape mismatch");
+    require_contig(x, what); require_contig(dz, what);
+    int64_t r, c; rows_cols_any(dy, r, c, what);
+    require(db.numel() == c && db.dtype() == Dtype::Float32, std::string(what) + ": db size");
+    check(tf_relu_bwd_colsum(ctx_of(dy), dy.data(), x.data(), dz.data(), static_cast<float*>(db.data()), r, c,
+                             tf_code(dy.dtype())), what);
+}
+
 bool conv2d_forward_implicit(const Tensor& x, const Tensor& w, const Tensor* bias, Tensor& y, int64_t sh, int64_t sw,
                              int64_t ph, int64_t pw, int64_t dh, int64_t dw, bool relu) {
     require_gpu(x, "hip::conv2d_forward"); require_gpu(w, "hip::conv2d_forward"); require_gpu(y, "hip::conv2d_forward");

@@ -121,6 +121,9 @@ void sum_dim(const Tensor& x, Tensor& out, int64_t outer, int64_t reduce, int64_
 void expand_dim(const Tensor& up, Tensor& out, int64_t outer, int64_t reduce, int64_t inner);
 void transpose2d(const Tensor& x, Tensor& out, int64_t batch, int64_t rows, int64_t cols);
 void colsum(const Tensor& dy, Tensor& db);
+// dz = dy * (x > 0 ? 1 : 0) and db = the column sums of dz over the last
+// dimension, in one pass (tf_relu_bwd_colsum); dy, x, dz share shape and dtype.
+void relu_backward_colsum(const Tensor& dy, const Tensor& x, Tensor& dz, Tensor& db);
 void chansum_nchw(const Tensor& dy, Tensor& db);
 // Implicit-GEMM convolution forward (tf_conv2d_fwd): false when the shape
 // does not fit the kernel's LDS (nothing was launched), else y is written.

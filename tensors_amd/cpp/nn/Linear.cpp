@@ -98,7 +98,9 @@ Tensor Linear::forward_impl(Tensor x, bool relu) {
             // without the pre-activation tensor.  The ReLU node's mask is taken
             // from y (y > 0 exactly where the pre-activation is > 0).
             node->next_edges_ = std::move(edges);
-            wiring::attach(y, std::make_shared<ReluBackward>(y), {Edge(node, 0)});
+            auto relu_node = std::make_shared<ReluBackward>(y);
+            relu_node->fuse_bias_grad();
+            wiring::attach(y, relu_node, {Edge(node, 0)});
         } else {
             wiring::attach(y, node, std::move(edges));
         }

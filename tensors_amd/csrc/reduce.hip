@@ -174,6 +174,129 @@ __global__ __launch_bounds__(256) void colsum_tile_kernel(const T* __restrict__ 
     if (threadIdx.x == 0) __hip_atomic_store(tickets + strip, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ReLU backward fused with the column sum of its result
+// (tf_relu_bwd_colsum): dz = dy * (x > 0 ? 1 : 0) in fp32, rounded to T and
+// stored; db[c] = sum_r dz[r, c] over the stored values.  Streaming layout:
+// block (s, k) owns the 256-column strip s (a lane per 4 columns, so a wave
+// reads and writes 512 / 1024 contiguous bytes of a row) and the kRcRows
+// rows of chunk k, which its four waves take interleaved (r0 + w,
+// r0 + w + 4, ...), eight rows' loads in flight per wave.  The waves' sums
+// are added in order through LDS; with several chunks the block stores its
+// 256 sums with agent-scope stores and counts in on the strip's counter, and
+// the last block of the strip adds the chunks in order (deterministic) and
+// resets the counter, as in colsum_tile_kernel.  Measured at the C5 shapes
+// (bf16, buffers past the cache): 4096 x 8192 in 38 us against 51 us for
+// tf_relu_bwd + tf_colsum_bf16, 4096 x 4096 in 27 against 29; lanes of 16
+// bytes (8 bf16 columns) were slower at 4096 x 8192 (43-52 us).
+template <typename T> struct Raw4;   // four consecutive elements as loaded
+template <> struct Raw4<float> { using type = float4; };
+template <> struct Raw4<uint16_t> { using type = uint2; };
+__device__ __forceinline__ float4 ld_raw4(const float* p) { return tfd::ld_nt(reinterpret_cast<const float4*>(p)); }
+__device__ __forceinline__ uint2 ld_raw4(const uint16_t* p) { return tfd::ld_nt(reinterpret_cast<const uint2*>(p)); }
+__device__ __forceinline__ float4 widen4(const float4 v) { return v; }
+__device__ __forceinline__ float4 widen4(const uint2 u) {
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xffff0000u));
+}
+__device__ __forceinline__ float relu_mask(float x) { return x > 0.0f ? 1.0f : 0.0f; }
+// The rule of tf_relu_bwd on four elements; returns the stored values in fp32.
+__device__ __forceinline__ float4 relu_bwd4(const float4 g, const float4 x, float* dz) {
+    const float4 o = make_float4(g.x * relu_mask(x.x), g.y * relu_mask(x.y), g.z * relu_mask(x.z), g.w * relu_mask(x.w));
+    tfd::st_nt(reinterpret_cast<float4*>(dz), o);
+    return o;
+}
+__device__ __forceinline__ float4 relu_bwd4(const uint2 g16, const uint2 x16, uint16_t* dz) {
+    const float4 g = widen4(g16), x = widen4(x16);
+    const uint2 o = make_uint2(tfd::bf16x2_rne(g.x * relu_mask(x.x), g.y * relu_mask(x.y)),
+                               tfd::bf16x2_rne(g.z * relu_mask(x.z), g.w * relu_mask(x.w)));
+    tfd::st_nt(reinterpret_cast<uint2*>(dz), o);
+    return widen4(o);
+}
+
+constexpr int kRcCols = 256;   // columns per strip (64 lanes x 4)
+constexpr int kRcU = 8;        // rows in flight per wave
+constexpr int kRcRows = 128;   // rows per chunk (64 and 256 measured slower at the C5 shapes)
+constexpr int kRcMaxBlocks = 4096;
+
+template <typename T>
+__global__ __launch_bounds__(256) void relu_bwd_colsum_kernel(const T* __restrict__ dy, const T* __restrict__ x,
+                                                              T* __restrict__ dz, float* __restrict__ db,
+                                                              float* __restrict__ part, unsigned* __restrict__ tickets,
+                                                              int rows, int cols, int rpc, int chunks) {
+    using R4 = typename Raw4<T>::type;
+    __shared__ float4 red[4][64];
+    __shared__ bool last;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int strip = blockIdx.x, chunk = blockIdx.y;
+    const int c = strip * kRcCols + 4 * lane;
+    const bool on = c < cols;   // cols % 4 == 0: a lane's 4 columns are all in or all out
+    const int r0 = chunk * rpc, r1 = min(rows, r0 + rpc);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (on) {
+        int r = r0 + wave;
+        for (; r + 4 * (kRcU - 1) < r1; r += 4 * kRcU) {
+            R4 g[kRcU], m[kRcU];
+#pragma unroll
+            for (int u = 0; u < kRcU; ++u) {
+                const int64_t off = (int64_t)(r + 4 * u) * cols + c;
+                g[u] = ld_raw4(dy + off);
+                m[u] = ld_raw4(x + off);
+            }
+#pragma unroll
+            for (int u = 0; u < kRcU; ++u) {
+                const float4 f = relu_bwd4(g[u], m[u], dz + (int64_t)(r + 4 * u) * cols + c);
+                acc.x += f.x; acc.y += f.y; acc.z += f.z; acc.w += f.w;
+            }
+        }
+        for (; r < r1; r += 4) {
+            const int64_t off = (int64_t)r * cols + c;
+            const float4 f = relu_bwd4(ld_raw4(dy + off), ld_raw4(x + off), dz + off);
+            acc.x += f.x; acc.y += f.y; acc.z += f.z; acc.w += f.w;
+        }
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && on) {
+        const float4 a = red[0][lane], b1 = red[1][lane], c2 = red[2][lane], d = red[3][lane];
+        const float sum[4] = {(a.x + b1.x) + (c2.x + d.x), (a.y + b1.y) + (c2.y + d.y), (a.z + b1.z) + (c2.z + d.z),
+                              (a.w + b1.w) + (c2.w + d.w)};
+        float* mine = part + ((int64_t)strip * chunks + chunk) * kRcCols + 4 * lane;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (chunks == 1) db[c + e] = sum[e];
+            else __hip_atomic_store(mine + e, sum[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (chunks == 1) return;
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(tickets + strip, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (unsigned)(chunks - 1);
+    __syncthreads();
+    if (!last) return;
+    // A thread per column of the strip: the chunks' sums eight loads at a
+    // time in flight, added in chunk order.
+    const int col = strip * kRcCols + threadIdx.x;
+    if (col < cols) {
+        const float* sp = part + (int64_t)strip * chunks * kRcCols + threadIdx.x;
+        float v = 0.0f;
+        int k = 0;
+        for (; k + 8 <= chunks; k += 8) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                t[u] = __hip_atomic_load(sp + (int64_t)(k + u) * kRcCols, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += t[u];
+        }
+        for (; k < chunks; ++k)
+            v += __hip_atomic_load(sp + (int64_t)k * kRcCols, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        db[col] = v;
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(tickets + strip, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Stage 2 of every two-stage reduction here (colsum, chansum, LayerNorm
 // dgamma/dbeta): out[j] = sum_k part[k][j] over a [K][W] partial matrix, the
 // first `split` columns to out_lo, the rest to out_hi.  A block owns 16
@@ -284,9 +407,55 @@ tf_status colsum_impl(tf_ctx* ctx, const T* dy, float* db, int64_t rows, int64_t
     return tfh::partial_rows_sum(ctx, part, db, nullptr, chunks, cols, cols);
 }
 
+// dz = relu_bwd(dy, x) and db = colsum(dz): one launch of
+// relu_bwd_colsum_kernel where its layout applies, else tf_relu_bwd followed
+// by the colsum.
+template <typename T>
+tf_status relu_bwd_colsum_impl(tf_ctx* ctx, const T* dy, const T* x, T* dz, float* db, int64_t rows, int64_t cols,
+                               int dtype) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(rows >= 0 && cols >= 0 && rows < (1LL << 31) && cols < (1LL << 31), "tf_relu_bwd_colsum: bad extent");
+    if (cols == 0) return TF_OK;
+    TF_REQUIRE(db != nullptr && (rows == 0 || (dy && x && dz)), "tf_relu_bwd_colsum: null pointer");
+    if (rows == 0) return tf_hip_fill_f32(ctx, db, 0.0f, cols);
+    constexpr uintptr_t amask = 4 * sizeof(T) - 1;   // a lane's 4 elements in one access
+    const bool vec = ((reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(x) |
+                       reinterpret_cast<uintptr_t>(dz)) & amask) == 0 && cols % 4 == 0;
+    const int64_t strips = (cols + kRcCols - 1) / kRcCols;
+    if (vec && strips <= tfh::kTicketColsumStrips) {
+        // Chunks of kRcRows rows, fewer when that would exceed kRcMaxBlocks
+        // blocks.
+        int64_t chunks = std::max<int64_t>(1, std::min<int64_t>((rows + kRcRows - 1) / kRcRows,
+                                                                (kRcMaxBlocks + strips - 1) / strips));
+        const int rpc = (int)((rows + chunks - 1) / chunks);
+        chunks = (rows + rpc - 1) / rpc;
+        TF_REQUIRE(chunks <= 65535, "tf_relu_bwd_colsum: too many row chunks");
+        tf_status st = tfh::ensure_workspace(ctx, (size_t)strips * chunks * kRcCols * sizeof(float));
+        if (st != TF_OK) return st;
+        relu_bwd_colsum_kernel<T><<<dim3((unsigned)strips, (unsigned)chunks), 256, 0, ctx->stream>>>(
+            dy, x, dz, db, reinterpret_cast<float*>(ctx->ws), ctx->tickets + tfh::kTicketColsum, (int)rows, (int)cols,
+            rpc, (int)chunks);
+        return tfh::check_launch("relu_bwd_colsum_kernel");
+    }
+    tf_status st = tf_relu_bwd(ctx, dy, x, dz, rows * cols, dtype);
+    if (st != TF_OK) return st;
+    return colsum_impl(ctx, static_cast<const T*>(dz), db, rows, cols);
+}
+
 }  // namespace
 
 extern "C" {
+
+tf_status tf_relu_bwd_colsum(tf_ctx* ctx, const void* dy, const void* x, void* dz, float* db, int64_t rows,
+                             int64_t cols, int dtype) {
+    if (dtype == TF_F32)
+        return relu_bwd_colsum_impl(ctx, static_cast<const float*>(dy), static_cast<const float*>(x),
+                                    static_cast<float*>(dz), db, rows, cols, dtype);
+    if (dtype == TF_BF16)
+        return relu_bwd_colsum_impl(ctx, static_cast<const uint16_t*>(dy), static_cast<const uint16_t*>(x),
+                                    static_cast<uint16_t*>(dz), db, rows, cols, dtype);
+    return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_relu_bwd_colsum: dtype must be Float32 or BFloat16");
+}
 
 tf_status tf_colsum(tf_ctx* ctx, const float* dy, float* db, int64_t rows, int64_t cols) {
     return colsum_impl(ctx, dy, db, rows, cols);

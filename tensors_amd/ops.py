@@ -176,6 +176,18 @@ def colsum(dy, db):
     return db
 
 
+def relu_bwd_colsum(dy, x, dz, db):
+    """dz = relu_bwd(dy, x) and db = colsum(dz) in one call (tf_relu_bwd_colsum)."""
+    rows, cols = _rows_cols(dy)
+    _same(dy, x, dz)
+    if not dy.tf_dtype == x.tf_dtype == dz.tf_dtype:
+        raise ValueError("relu_bwd_colsum: dy, x and dz must share a dtype")
+    if db.size != cols:
+        raise ValueError("relu_bwd_colsum: db must have one entry per column")
+    call("tf_relu_bwd_colsum", _ctx(dy), dy.ptr, x.ptr, dz.ptr, db.ptr, rows, cols, dy.tf_dtype)
+    return dz, db
+
+
 def chansum_nchw(dy, db):
     if len(dy.shape) != 4:
         raise ValueError("chansum expects NCHW")

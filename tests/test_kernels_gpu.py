@@ -727,6 +727,58 @@ def test_colsum_bf16(ctx, R, Cc):
     assert_close(db16.numpy(), wide.astype(np.float64).sum(0), RTOL32, f"colsum_bf16 {R}x{Cc} vs float64")
 
 
+# tf_relu_bwd_colsum: one pass for widths that are multiples of 4
+# ((4096, 1024) over several row chunks, (64, 8192), (33, 64), (5000, 96),
+# (3, 1000) and (9, 1004) with a partial last 256-column strip), the two
+# separate kernels otherwise ((17, 19)).  dz must equal tf_relu_bwd bit for bit (and the
+# oracle's rule); db must be within fp32 tolerance of float64 and of the
+# colsum of that dz, and bit-identical on a second call.  Special values:
+# x = +-0 and NaN mask to 0, dy = +-inf under a zero mask gives NaN, dy = -0.
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("R,Cc", [(4096, 1024), (33, 64), (5000, 96), (64, 8192), (17, 19), (3, 1000), (9, 1004)])
+def test_relu_bwd_colsum(ctx, dtype, R, Cc):
+    import tensors_amd as ta_mod
+    ops = _ops()
+    x = synth.normal(181 + R, (R, Cc))
+    dy = synth.normal(182 + Cc, (R, Cc))
+    x[0, :6] = [0.0, -0.0, np.nan, 1e-30, -1e-30, 2.0]
+    dy[0, :6] = [np.inf, -np.inf, 3.0, -0.0, -0.0, -0.0]
+    if dtype == "bf16":
+        xb, dyb = ta_mod.f32_to_bf16_bits(x), ta_mod.f32_to_bf16_bits(dy)
+        dt = ta_mod.BF16
+        want_dz = ta_mod.f32_to_bf16_bits(oracle.relu_bwd(ta_mod.bf16_bits_to_f32(dyb), ta_mod.bf16_bits_to_f32(xb)))
+    else:
+        xb, dyb, dt = x, dy, np.float32
+        want_dz = oracle.relu_bwd(dy, x)
+    dy_d, x_d = ctx.array(dyb, dt), ctx.array(xb, dt)
+    dz, dz2 = ctx.empty((R, Cc), dt), ctx.empty((R, Cc), dt)
+    db, db2 = ctx.empty((Cc,)), ctx.empty((Cc,))
+    ops.relu_bwd_colsum(dy_d, x_d, dz, db)
+    ops.relu_bwd(dy_d, x_d, dz2)
+    ops.colsum(dz2, db2)
+    got = dz.numpy()
+    assert_bitexact(got, dz2.numpy(), f"relu_bwd_colsum dz {dtype} {R}x{Cc} vs tf_relu_bwd")
+    # inf * 0 is NaN on both sides, with the host's and the GPU's own default
+    # NaN bits: compare NaN positions as NaN, the rest bit for bit.
+    gw = ta_mod.bf16_bits_to_f32(got) if dtype == "bf16" else got
+    ww = ta_mod.bf16_bits_to_f32(want_dz) if dtype == "bf16" else want_dz
+    nan = np.isnan(ww)
+    assert np.array_equal(np.isnan(gw), nan) and nan[0, :2].all(), f"relu_bwd_colsum NaN positions {dtype}"
+    assert_bitexact(got[~nan], want_dz[~nan], f"relu_bwd_colsum dz {dtype} {R}x{Cc} vs oracle")
+    db1 = db.numpy()
+    ops.relu_bwd_colsum(dy_d, x_d, dz, db)
+    assert np.array_equal(db.numpy(), db1, equal_nan=True), f"relu_bwd_colsum db {dtype} {R}x{Cc} repeat"
+    assert np.array_equal(np.isnan(db1), np.isnan(db2.numpy())), f"relu_bwd_colsum db NaNs {dtype} {R}x{Cc}"
+    fin = ~np.isnan(db1)
+    assert_close(db1[fin], db2.numpy()[fin], RTOL32, f"relu_bwd_colsum db {dtype} {R}x{Cc} vs colsum")
+    wide = ta_mod.bf16_bits_to_f32(got) if dtype == "bf16" else got
+    # Row 0 holds the NaN of inf * 0: compare the other columns to float64.
+    truth = wide.astype(np.float64).sum(0)
+    ok = np.isfinite(truth)
+    assert np.isnan(db.numpy()[~ok]).all()
+    assert_close(db.numpy()[ok], truth[ok], RTOL32, f"relu_bwd_colsum db {dtype} {R}x{Cc} vs float64")
+
+
 def test_colsum_zero_rows(ctx):
     ops = _ops()
     db = ctx.array(np.full(7, 3.0, np.float32))
