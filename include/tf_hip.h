@@ -289,6 +289,13 @@ tf_status tf_ce_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets,
  * as tf_ce_fwd's (they change the loss only). */
 tf_status tf_ce_fwd_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets,
                         float* loss, float* dlogits, int64_t rows, int64_t cols, int flags);
+/* The same for bf16 logits (bit patterns): each value widened to fp32 in the
+ * kernel (exact), the loss in fp32, dlogits rounded to bf16 (nearest even).
+ * Equal to tf_ce_fwd_bwd on the widened logits followed by a cast of dlogits
+ * to bf16, in one pass: the cross entropy of a bf16 Linear's output
+ * (nn/CrossEntropyLoss.cpp:13-77 on the bf16 compute path). */
+tf_status tf_ce_fwd_bwd_bf16(tf_ctx* ctx, const void* logits, const int64_t* targets,
+                             float* loss, void* dlogits, int64_t rows, int64_t cols, int flags);
 /* pred[r] = first column of row r holding its largest value, with the
  * reference's scan (examples/train_mlp.cpp:95-100: running maximum from
  * -1e30, strict '>', prediction 0 when no value exceeds it).  With labels

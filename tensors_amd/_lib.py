@@ -88,6 +88,7 @@ SIGNATURES: dict[str, list] = {
     "tf_ce_fwd": [_p, _p, _p, _p, _p, _i64, _i64, _i],
     "tf_ce_bwd": [_p, _p, _p, _p, _p, _p, _i64, _i64],
     "tf_ce_fwd_bwd": [_p, _p, _p, _p, _p, _i64, _i64, _i],
+    "tf_ce_fwd_bwd_bf16": [_p, _p, _p, _p, _p, _i64, _i64, _i],
     "tf_log_softmax_fwd": [_p, _p, _p, _i64, _i64],
     "tf_softmax_fwd": [_p, _p, _p, _i64, _i64],
     "tf_argmax_rows": [_p, _p, _p, _p, _p, _i64, _i64],

@@ -370,8 +370,10 @@ std::vector<Tensor> CrossEntropyBackward::apply(std::vector<Tensor>&& grads) {
         // dlogits for g = 1; an undefined gradient is the unit seed.
         const Tensor& dl = stats_.unpack();
         if (!grads[0].storage()) return {dl};
-        Tensor d = raw::empty_like(dl);
-        hip::scale_by(dl, grads[0], d);
+        // A non-unit upstream gradient: g * dl in fp32 (bf16 dlogits widened).
+        Tensor df = dl.dtype() == Dtype::Float32 ? dl : dl.to(Dtype::Float32);
+        Tensor d = raw::empty_like(df);
+        hip::scale_by(df, grads[0], d);
         return {std::move(d)};
     }
     const Tensor& logits = logits_.unpack();

@@ -360,6 +360,21 @@ void cross_entropy_forward_backward(const Tensor& logits, const Tensor& targets,
           "hip::cross_entropy_forward_backward");
 }
 
+void cross_entropy_forward_backward_bf16(const Tensor& logits, const Tensor& targets, Tensor& loss, Tensor& dlogits,
+                                         int flags) {
+    const char* what = "hip::cross_entropy_forward_backward_bf16";
+    require_gpu(logits, what); require_gpu(targets, what); require_gpu(loss, what);
+    check_same(logits, dlogits, what);
+    require(logits.dtype() == Dtype::BFloat16, std::string(what) + ": BFloat16 logits");
+    int64_t r, c; rows_cols_any(logits, r, c, what);
+    require(logits.shape().ndim() == 2, std::string(what) + ": 2-D logits");
+    require(targets.dtype() == Dtype::Int64 && targets.numel() == r, std::string(what) + ": targets");
+    require(loss.dtype() == Dtype::Float32 && loss.numel() >= 1, std::string(what) + ": loss");
+    check(tf_ce_fwd_bwd_bf16(ctx_of(logits), logits.data(), static_cast<const int64_t*>(targets.data()),
+                             static_cast<float*>(loss.data()), dlogits.data(), r, c, flags),
+          what);
+}
+
 void scale_by(const Tensor& x, const Tensor& s, Tensor& out) {
     require_gpu(x, "hip::scale_by"); require_gpu(s, "hip::scale_by");
     check_same(x, out, "hip::scale_by");

@@ -109,6 +109,9 @@ void cross_entropy_backward(const Tensor& logits, const Tensor& targets, const T
 // Loss and dlogits = (softmax - onehot) / N in one pass (tf_ce_fwd_bwd).
 void cross_entropy_forward_backward(const Tensor& logits, const Tensor& targets, Tensor& loss, Tensor& dlogits,
                                     int flags);
+// The same for BFloat16 logits: dlogits in BFloat16 (tf_ce_fwd_bwd_bf16).
+void cross_entropy_forward_backward_bf16(const Tensor& logits, const Tensor& targets, Tensor& loss, Tensor& dlogits,
+                                         int flags);
 // out = x * s[0] for a device scalar s (tf_scale_by).
 void scale_by(const Tensor& x, const Tensor& s, Tensor& out);
 void layernorm_forward(const Tensor& x, const Tensor& gamma, const Tensor& beta, Tensor& y, Tensor& mean,

@@ -30,7 +30,16 @@ Tensor CrossEntropyLoss::forward(Tensor logits, Tensor targets) {
         // With a gradient to come, dlogits (for an upstream gradient of 1)
         // are computed in the same pass over the logits as the loss, and the
         // loss mean in the same kernel; the backward node returns them, or
-        // scales them by a non-unit upstream gradient.
+        // scales them by a non-unit upstream gradient.  BFloat16 logits (a
+        // bf16 Linear's output) are read as they are and their dlogits come
+        // out in BFloat16, the dtype that Linear's backward multiplies in.
+        if (logits.dtype() == Dtype::BFloat16 && logits.requires_grad()) {
+            Tensor dl = Tensor::empty(logits.shape(), Dtype::BFloat16, logits.device());
+            hip::cross_entropy_forward_backward_bf16(logits, targets, loss, dl, TF_CE_MODULE);
+            node = std::make_shared<CrossEntropyBackward>(CrossEntropyBackward::Precomputed{}, dl);
+            wiring::attach(loss, node, {wiring::accumulator_edge(logits)});
+            return loss;
+        }
         Tensor lf = logits.dtype() == Dtype::Float32 ? logits : logits.to(Dtype::Float32);
         if (logits.requires_grad()) {
             Tensor dl = Tensor::empty(lf.shape(), Dtype::Float32, logits.device());

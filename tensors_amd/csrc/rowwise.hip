@@ -66,15 +66,64 @@ __device__ __forceinline__ void store_row(float* __restrict__ row, int cols, int
     }
 }
 
+// bf16 rows (bit patterns, for the cross entropy of bf16 logits): the same
+// element mapping with 8-byte vectors, widened to fp32 on load (exact) and
+// rounded to nearest even on store (v_cvt_pk_bf16_f32, as every bf16 store).
+template <int NC, bool NT = false>
+__device__ __forceinline__ void load_row(const uint16_t* __restrict__ row, int cols, int lane, bool vec,
+                                         float (&v)[NC][4], float fill) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        int base = 256 * c + 4 * lane;
+        if (vec && base + 4 <= cols) {
+            const uint2* src = reinterpret_cast<const uint2*>(row + base);
+            const uint2 t = NT ? tfd::ld_nt(src) : *src;
+            v[c][0] = __uint_as_float(t.x << 16); v[c][1] = __uint_as_float(t.x & 0xffff0000u);
+            v[c][2] = __uint_as_float(t.y << 16); v[c][3] = __uint_as_float(t.y & 0xffff0000u);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                int j = col_of(c, lane, q, vec);
+                v[c][q] = j < cols ? tfd::bf16_to_f32(row[j]) : fill;
+            }
+        }
+    }
+}
+
+template <int NC, bool NT = false>
+__device__ __forceinline__ void store_row(uint16_t* __restrict__ row, int cols, int lane, bool vec,
+                                          const float (&v)[NC][4]) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        int base = 256 * c + 4 * lane;
+        if (vec && base + 4 <= cols) {
+            uint2* dst = reinterpret_cast<uint2*>(row + base);
+            const uint2 t = make_uint2(tfd::bf16x2_rne(v[c][0], v[c][1]), tfd::bf16x2_rne(v[c][2], v[c][3]));
+            if (NT) tfd::st_nt(dst, t);
+            else *dst = t;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                int j = col_of(c, lane, q, vec);
+                if (j < cols) row[j] = tfd::f32_to_bf16(v[c][q]);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ float elem_f32(const float* p, int64_t i) { return p[i]; }
+__device__ __forceinline__ float elem_f32(const uint16_t* p, int64_t i) { return tfd::bf16_to_f32(p[i]); }
+
 // Row statistics of a streamed (uncached) row: max and sum exp(x - max),
 // online over 256-column chunks.
-__device__ __forceinline__ void stream_stats(const float* __restrict__ row, int cols, int lane, bool vec,
+template <typename T>
+__device__ __forceinline__ void stream_stats(const T* __restrict__ row, int cols, int lane, bool vec,
                                              float& mx, float& sum) {
     float m = -INFINITY, s = 0.0f;
     for (int c = 0; 256 * c < cols; ++c) {
         float v[1][4];
         // load one chunk at offset 256c
-        const float* base = row + 256 * c;
+        const T* base = row + 256 * c;
         load_row<1>(base, cols - 256 * c, lane, vec, v, -INFINITY);
         float cm = fmaxf(fmaxf(v[0][0], v[0][1]), fmaxf(v[0][2], v[0][3]));
         float nm = fmaxf(m, cm);
@@ -121,15 +170,15 @@ __device__ __forceinline__ void block_mean(const float* __restrict__ nll, int ro
 }
 
 // One row of ce_kernel, by one wave.
-template <int NC, int MODE>
-__device__ __forceinline__ void ce_row(const float* __restrict__ logits, const int64_t* __restrict__ targets,
+template <typename T, int NC, int MODE>
+__device__ __forceinline__ void ce_row(const T* __restrict__ logits, const int64_t* __restrict__ targets,
                                        const float* __restrict__ lse_in, const float* __restrict__ grad_loss,
                                        float* __restrict__ lse_out, float* __restrict__ nll,
-                                       float* __restrict__ dlogits, int r, int cols, float inv_rows, int vec,
+                                       T* __restrict__ dlogits, int r, int cols, float inv_rows, int vec,
                                        float nll_max, int strict) {
     constexpr int NCC = NC > 0 ? NC : 1;
     const int lane = threadIdx.x & 63;
-    const float* x = logits + (int64_t)r * cols;
+    const T* x = logits + (int64_t)r * cols;
     const int64_t t = targets[r];
     const bool t_ok = t >= 0 && t < cols;
 
@@ -163,7 +212,7 @@ __device__ __forceinline__ void ce_row(const float* __restrict__ logits, const i
     if (MODE != 1) {
         if (lane == 0) {
             if (lse_out) lse_out[r] = lse;
-            float nl = t_ok ? lse - x[t] : (strict ? __builtin_nanf("") : 0.0f);
+            float nl = t_ok ? lse - elem_f32(x, t) : (strict ? __builtin_nanf("") : 0.0f);
             // NaN stays NaN; an agent-scope store, read by another block
             __hip_atomic_store(nll + r, nl > nll_max ? nll_max : nl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -171,7 +220,7 @@ __device__ __forceinline__ void ce_row(const float* __restrict__ logits, const i
     if (MODE != 0) {
         const float g = grad_loss ? grad_loss[0] : 1.0f;
         const float scale = t_ok ? g * inv_rows : 0.0f;
-        float* dx = dlogits + (int64_t)r * cols;
+        T* dx = dlogits + (int64_t)r * cols;
         if constexpr (NC > 0) {
 #pragma unroll
             for (int c = 0; c < NC; ++c)
@@ -205,15 +254,15 @@ __device__ __forceinline__ void ce_row(const float* __restrict__ logits, const i
 // cache maintenance); a block's stores have completed (vmcnt 0 in every
 // thread, then the barrier) before it counts itself in.  (A device-scope
 // fence instead writes back and invalidates the XCD's L2 in every block.)
-template <int NC, int MODE>
-__global__ __launch_bounds__(256) void ce_kernel(const float* __restrict__ logits, const int64_t* __restrict__ targets,
+template <typename T, int NC, int MODE>
+__global__ __launch_bounds__(256) void ce_kernel(const T* __restrict__ logits, const int64_t* __restrict__ targets,
                                                  const float* __restrict__ lse_in, const float* __restrict__ grad_loss,
                                                  float* __restrict__ lse_out, float* __restrict__ nll,
-                                                 float* __restrict__ dlogits, int rows, int cols, float inv_rows,
+                                                 T* __restrict__ dlogits, int rows, int cols, float inv_rows,
                                                  int vec, float nll_max, int strict, float* __restrict__ loss,
                                                  unsigned* __restrict__ ticket) {
     const int r = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-    if (r < rows) ce_row<NC, MODE>(logits, targets, lse_in, grad_loss, lse_out, nll, dlogits, r, cols, inv_rows,
+    if (r < rows) ce_row<T, NC, MODE>(logits, targets, lse_in, grad_loss, lse_out, nll, dlogits, r, cols, inv_rows,
                                    vec, nll_max, strict);
     if (MODE != 1 && ticket != nullptr) {
         __shared__ int last;
@@ -327,8 +376,12 @@ __global__ __launch_bounds__(256) void softmax_bwd_kernel(const float* __restric
     }
 }
 
-bool row_vec_ok(const void* p, int64_t cols) {
+// Four-element vectors of the row helpers: 16 bytes for fp32, 8 for bf16.
+bool row_vec_ok(const float* p, int64_t cols) {
     return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && (cols % 4) == 0;
+}
+bool row_vec_ok(const uint16_t* p, int64_t cols) {
+    return (reinterpret_cast<uintptr_t>(p) & 7) == 0 && (cols % 4) == 0;
 }
 
 // Number of register-cached 256-column chunks for a row width (0 = stream).
@@ -350,9 +403,12 @@ __global__ __launch_bounds__(256) void mean_kernel(const float* __restrict__ nll
     block_mean(nll, rows, inv_rows, loss);
 }
 
-template <int MODE>
-tf_status launch_ce(tf_ctx* ctx, const float* logits, const int64_t* targets, const float* lse_in,
-                    const float* grad_loss, float* lse_out, float* nll, float* dlogits, int64_t rows, int64_t cols,
+// T is deduced from the logits only (dlogits may be nullptr).
+template <typename T> struct Same { using type = T; };
+template <int MODE, typename T = float>
+tf_status launch_ce(tf_ctx* ctx, const T* logits, const int64_t* targets, const float* lse_in,
+                    const float* grad_loss, float* lse_out, float* nll, typename Same<T>::type* dlogits, int64_t rows,
+                    int64_t cols,
                     int flags = 0, float* loss = nullptr) {
     // With `loss`: the mean loss too, by the kernel's last block when the
     // grid is small, else by mean_kernel after it.
@@ -366,7 +422,7 @@ tf_status launch_ce(tf_ctx* ctx, const float* logits, const int64_t* targets, co
     const float inv_rows = (float)(1.0 / (double)rows);
     dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
 #define TF_CE_LAUNCH(NC)                                                                              \
-    ce_kernel<NC, MODE><<<grid, 256, 0, ctx->stream>>>(logits, targets, lse_in, grad_loss, lse_out, nll, \
+    ce_kernel<T, NC, MODE><<<grid, 256, 0, ctx->stream>>>(logits, targets, lse_in, grad_loss, lse_out, nll, \
                                                          dlogits, (int)rows, (int)cols, inv_rows, vec, nll_max, \
                                                          strict, loss, ticket)
     switch (chunks_for(cols)) {
@@ -484,6 +540,20 @@ tf_status tf_ce_fwd_bwd(tf_ctx* ctx, const float* logits, const int64_t* targets
     float* nll = reinterpret_cast<float*>(ctx->ws);
     TF_REQUIRE((flags & ~TF_CE_MODULE) == 0, "tf_ce_fwd_bwd: unknown flags");
     return launch_ce<2>(ctx, logits, targets, nullptr, nullptr, nullptr, nll, dlogits, rows, cols, flags, loss);
+}
+
+tf_status tf_ce_fwd_bwd_bf16(tf_ctx* ctx, const void* logits, const int64_t* targets, float* loss, void* dlogits,
+                             int64_t rows, int64_t cols, int flags) {
+    tf_status st = check_rows(ctx, rows, cols);
+    if (st != TF_OK) return st;
+    TF_REQUIRE(rows > 0 && cols > 0, "tf_ce_fwd_bwd_bf16: empty logits");
+    TF_REQUIRE(logits && targets && loss && dlogits, "tf_ce_fwd_bwd_bf16: null pointer");
+    st = tfh::ensure_workspace(ctx, (size_t)rows * sizeof(float));
+    if (st != TF_OK) return st;
+    float* nll = reinterpret_cast<float*>(ctx->ws);
+    TF_REQUIRE((flags & ~TF_CE_MODULE) == 0, "tf_ce_fwd_bwd_bf16: unknown flags");
+    return launch_ce<2>(ctx, static_cast<const uint16_t*>(logits), targets, nullptr, nullptr, nullptr, nll,
+                        static_cast<uint16_t*>(dlogits), rows, cols, flags, loss);
 }
 
 tf_status tf_argmax_rows(tf_ctx* ctx, const float* x, int64_t* pred, const int64_t* labels, int64_t* correct,

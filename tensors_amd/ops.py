@@ -139,6 +139,17 @@ def ce_fwd_bwd(logits, targets, loss, dlogits, flags=_lib.TF_CE_CHAIN):
     return loss, dlogits
 
 
+def ce_fwd_bwd_bf16(logits, targets, loss, dlogits, flags=_lib.TF_CE_CHAIN):
+    """tf_ce_fwd_bwd on bf16 logits (dlogits in bf16)."""
+    rows, cols = _rows_cols(logits)
+    _check_targets(logits, targets)
+    _same(logits, dlogits)
+    if logits.tf_dtype != _lib.TF_BF16 or dlogits.tf_dtype != _lib.TF_BF16:
+        raise ValueError("ce_fwd_bwd_bf16: logits and dlogits must be bf16")
+    call("tf_ce_fwd_bwd_bf16", _ctx(logits), logits.ptr, targets.ptr, loss.ptr, dlogits.ptr, rows, cols, flags)
+    return loss, dlogits
+
+
 def log_softmax(x, y):
     rows, cols = _rows_cols(x)
     _same(x, y)

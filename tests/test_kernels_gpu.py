@@ -617,6 +617,42 @@ def test_ce_fwd_bwd_vs_chain(ctx, R, Cc):
     assert_close(d.numpy(), d_ref, RTOL32, "fused dlogits")
 
 
+@pytest.mark.parametrize("R,Cc", CE_SHAPES + [(4096, 1004), (9, 1001)])
+def test_ce_fwd_bwd_bf16(ctx, R, Cc):
+    """tf_ce_fwd_bwd_bf16 equals tf_ce_fwd_bwd on the widened logits followed
+    by a round to bf16: bit for bit where both take the same element mapping
+    (widths that are multiples of 4: the loss, and dlogits after rounding),
+    within fp32 tolerance otherwise; and the oracle's chain within tolerance.
+    Module flags, with a bad target making the loss NaN."""
+    import tensors_amd as ta_mod
+    from tensors_amd import _lib
+    ops = _ops()
+    bits = ta_mod.f32_to_bf16_bits(synth.normal(141 + R, (R, Cc), std=3.0))
+    wide = ta_mod.bf16_bits_to_f32(bits)
+    labels = synth.uniform_int(142 + Cc, (R,), Cc)
+    dt = ctx.array(labels)
+    loss16, d16 = ctx.empty((1,)), ctx.empty((R, Cc), ta_mod.BF16)
+    loss32, d32 = ctx.empty((1,)), ctx.empty((R, Cc))
+    ops.ce_fwd_bwd_bf16(ctx.array(bits, ta_mod.BF16), dt, loss16, d16, flags=_lib.TF_CE_MODULE)
+    ops.ce_fwd_bwd(ctx.array(wide), dt, loss32, d32, flags=_lib.TF_CE_MODULE)
+    want = ta_mod.f32_to_bf16_bits(d32.numpy())
+    if Cc % 4 == 0:
+        assert_bitexact(loss16.numpy(), loss32.numpy(), f"ce bf16 loss {R}x{Cc}")
+        assert_bitexact(d16.numpy(), want, f"ce bf16 dlogits {R}x{Cc}")
+    else:
+        assert_close(loss16.numpy(), loss32.numpy(), RTOL32, f"ce bf16 loss {R}x{Cc}")
+        assert_close(ta_mod.bf16_bits_to_f32(d16.numpy()), ta_mod.bf16_bits_to_f32(want), RTOL16,
+                     f"ce bf16 dlogits {R}x{Cc}")
+    assert_close(loss16.numpy(), [oracle.ce_module(wide, labels)], RTOL32, "ce bf16 loss vs oracle")
+    _, d_ref = oracle.ce_chain(wide, labels)
+    assert_close(ta_mod.bf16_bits_to_f32(d16.numpy()), d_ref, RTOL16, "ce bf16 dlogits vs oracle")
+    if R > 1:
+        labels[R // 2] = Cc
+        ops.ce_fwd_bwd_bf16(ctx.array(bits, ta_mod.BF16), ctx.array(labels), loss16, d16, flags=_lib.TF_CE_MODULE)
+        assert np.isnan(loss16.numpy()[0])
+        assert np.all(d16.numpy()[R // 2] == 0)
+
+
 def test_ce_upstream_scale_and_bad_labels(ctx):
     ops = _ops()
     R, Cc = 16, 10
