@@ -1,7 +1,7 @@
 // Bias-gradient reductions, deterministic (no atomics, fixed summation order):
 //   colsum : db[c] = sum_r dy[r, c]           (Linear bias grad; fp32 or bf16 dy)
 //   chansum: db[c] = sum_{n,p} dy[n, c, p]    (Conv2d bias grad, NCHW)
-// Colsums over a multiple of 32 columns run as one launch of (strip, chunk)
+// Colsums over a multiple of 4 columns run as one launch of (strip, chunk)
 // blocks whose last arrival per strip adds the chunks.  The others are
 // two-stage: stage 1 writes per-chunk partial sums to the context
 // workspace, stage 2 (tfh::partial_rows_sum, also used by the LayerNorm
@@ -107,7 +107,9 @@ __global__ __launch_bounds__(256) void colsum_tile_kernel(const T* __restrict__ 
     const int chunk = blockIdx.y;
     const int cg = threadIdx.x & 7, rg = threadIdx.x >> 3;
     const int c0 = strip * kTileCols + 4 * cg;
-    const int r0 = chunk * rpc, r1 = min(rows, r0 + rpc);
+    // cols % 4 == 0: a lane's four columns are all inside or all past the
+    // last (ragged) strip's end.
+    const int r0 = chunk * rpc, r1 = c0 < cols ? min(rows, r0 + rpc) : r0;
     const T* base = dy + c0;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     int r = r0 + rg;
@@ -142,8 +144,11 @@ __global__ __launch_bounds__(256) void colsum_tile_kernel(const T* __restrict__ 
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             // One chunk: the block's sums are the result.
-            if (chunks == 1) db[c0 + e] = s[e];
-            else __hip_atomic_store(mine + 4 * cg + e, s[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (chunks == 1) {
+                if (c0 < cols) db[c0 + e] = s[e];
+            } else {
+                __hip_atomic_store(mine + 4 * cg + e, s[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
     if (chunks == 1) return;
@@ -154,7 +159,7 @@ __global__ __launch_bounds__(256) void colsum_tile_kernel(const T* __restrict__ 
                (unsigned)(chunks - 1);
     __syncthreads();
     if (!last) return;
-    if (threadIdx.x < kTileCols) {
+    if (threadIdx.x < kTileCols && strip * kTileCols + (int)threadIdx.x < cols) {
         // The chunks' loads eight at a time in flight, added in chunk order.
         const float* sp = part + (int64_t)strip * chunks * kTileCols + threadIdx.x;
         float v = 0.0f;
@@ -376,10 +381,11 @@ tf_status colsum_impl(tf_ctx* ctx, const T* dy, float* db, int64_t rows, int64_t
     TF_REQUIRE(db != nullptr && (rows == 0 || dy != nullptr), "tf_colsum: null pointer");
     if (rows == 0) return tf_hip_fill_f32(ctx, db, 0.0f, cols);
     const int vec = (reinterpret_cast<uintptr_t>(dy) & (4 * sizeof(T) - 1)) == 0 && cols % 4 == 0;
-    // Widths in 32-column strips: one launch of (strip, chunk) blocks, about
-    // kTileBlocks of them, with the last block of each strip adding its chunks.
-    const int64_t tstrips = cols / kTileCols;
-    if (vec && cols % kTileCols == 0 && tstrips <= tfh::kTicketColsumStrips) {
+    // 32-column strips (the last one ragged): one launch of (strip, chunk)
+    // blocks, about kTileBlocks of them, with the last block of each strip
+    // adding its chunks.  vec implies cols % 4 == 0.
+    const int64_t tstrips = (cols + kTileCols - 1) / kTileCols;
+    if (vec && tstrips <= tfh::kTicketColsumStrips) {
         int64_t chunks = std::max<int64_t>(1, std::min<int64_t>((kTileBlocks + tstrips - 1) / tstrips, (rows + 31) / 32));
         const int rpc = (int)((rows + chunks - 1) / chunks);
         chunks = (rows + rpc - 1) / rpc;

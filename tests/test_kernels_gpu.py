@@ -731,12 +731,13 @@ def test_softmax_bwd_uniform_is_zero(ctx):
 # ---------------------------------------------------------------------------
 # reductions
 # ---------------------------------------------------------------------------
-# Multiples of 32 columns take the one-launch tile kernel: (2048, 2048),
+# Multiples of 4 columns take the one-launch tile kernel: (2048, 2048),
 # (4096, 8192), (7, 4096), (3001, 16384), (64, 256), (33, 64) (a short last
-# chunk), (5000, 96) (157 chunks added by each strip's last block); the
-# others ((17, 19), (1, 5), (4096, 10), (3, 1001), (100, 2056)) are two-stage.
+# chunk), (5000, 96) (157 chunks added by each strip's last block), and with
+# a ragged last 32-column strip (100, 2056), (4096, 1000), (9, 4); the others
+# ((17, 19), (1, 5), (4096, 10), (3, 1001)) are two-stage.
 @pytest.mark.parametrize("R,Cc", [(2048, 2048), (64, 256), (17, 19), (1, 5), (4096, 10), (3, 1001), (4096, 8192),
-                                  (7, 4096), (3001, 16384), (100, 2056), (33, 64), (5000, 96)])
+                                  (7, 4096), (3001, 16384), (100, 2056), (33, 64), (5000, 96), (4096, 1000), (9, 4)])
 def test_colsum(ctx, R, Cc):
     ops = _ops()
     dy = synth.normal(151 + R, (R, Cc))
@@ -747,7 +748,7 @@ def test_colsum(ctx, R, Cc):
 
 
 @pytest.mark.parametrize("R,Cc", [(2048, 2048), (4096, 8192), (17, 19), (1, 5), (3, 1001), (64, 258), (7, 4096),
-                                  (3001, 16384), (5000, 96)])
+                                  (3001, 16384), (5000, 96), (4096, 1000), (100, 2056)])
 def test_colsum_bf16(ctx, R, Cc):
     # bf16 dy summed in fp32: bit-exact against the fp32 colsum of the widened
     # tensor (same order; widening is exact), and within fp32 tolerance of
