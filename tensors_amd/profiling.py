@@ -48,9 +48,9 @@ _conv_x = CONV2[0] * CONV2[1] * CONV2[2] * CONV2[3] * 4
 _conv_col = CONV2[0] * CONV2[1] * CONV2[4] ** 2 * CONV2[5] ** 2 * 4
 BW_KERNELS = {
     # logits read, dlogits written, int64 targets and the saved logsumexp read
-    "ce_bwd_c3a": ("ce_kernel<4, 1>", 2 * R3 * C3 * 4 + R3 * 8 + R3 * 4),
+    "ce_bwd_c3a": ("ce_kernel<float, 4, 1>", 2 * R3 * C3 * 4 + R3 * 8 + R3 * 4),
     # one pass: logits and targets read, dlogits and the per-row nll written
-    "ce_fused_fwd_bwd_c3a": ("ce_kernel<4, 2>", 2 * R3 * C3 * 4 + R3 * 8 + R3 * 4),
+    "ce_fused_fwd_bwd_c3a": ("ce_kernel<float, 4, 2>", 2 * R3 * C3 * 4 + R3 * 8 + R3 * 4),
     "relu_bwd_c3b": ("binary_kernel<float, ReluBwdOp>", 3 * R3 * C3 * 4),
     # the whole op in one launch: dy, x read, dx written; gamma, mean, rstd
     # read; dgamma, dbeta written (the column blocks' read of x and dy and
