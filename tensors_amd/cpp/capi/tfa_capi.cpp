@@ -451,6 +451,62 @@ void t_linear_relu_fused(Device d) {
     }
 }
 
+// Linear::forward_relu on a layer wide enough for the one-pass ReLU backward
+// + bias gradient (300 rows x 256 outputs, three row chunks), fp32 and (on
+// the GPU) bf16 compute: dX and dW equal those of forward() then relu(), db
+// within fp32 summation tolerance of it and of a double-precision sum of the
+// masked upstream gradient.
+void t_linear_relu_bias_wide(Device d) {
+    const int R = 300, I = 96, O = 256;
+    std::vector<float> xv(R * I), wv(O * I), bv(O), uv(R * O);
+    for (int i = 0; i < R * I; ++i) xv[i] = std::sin(0.37f * i);
+    for (int i = 0; i < O * I; ++i) wv[i] = 0.1f * std::cos(0.11f * i);
+    for (int i = 0; i < O; ++i) bv[i] = 0.5f * std::sin(1.3f * i);
+    for (int i = 0; i < R * O; ++i) uv[i] = std::cos(0.07f * i);
+    const bool gpu = d.type == DeviceType::CUDA;
+    for (int bf16 = 0; bf16 <= (gpu ? 1 : 0); ++bf16) {
+        std::vector<float> got[2][4];   // [fused?][y, dX, dW, db]
+        for (int fused = 0; fused < 2; ++fused) {
+            nn::Linear fc(I, O);
+            fc.to(d);
+            if (bf16) fc.set_compute_dtype(Dtype::BFloat16);
+            Tensor W = from_vals(wv, {O, I}, d), b = from_vals(bv, {O}, d);
+            for (auto& np : fc.named_parameters()) {
+                np.second->data_ = np.first == "weight" ? W : b;
+                np.second->data_.requires_grad(true);
+            }
+            Tensor x = from_vals(xv, {R, I}, d);
+            x.requires_grad(true);
+            Tensor y = fused ? fc.forward_relu(x) : fc.forward(x).relu();
+            Tensor up = from_vals(uv, {R, O}, d);
+            if (bf16) up = up.to(Dtype::BFloat16);
+            Engine().execute(y.autograd_meta()->grad_fn_, up, false);
+            got[fused][0] = to_host(y);
+            got[fused][1] = to_host(x.grad());
+            for (auto& np : fc.named_parameters())
+                got[fused][np.first == "weight" ? 2 : 3] = to_host(np.second->data_.grad());
+            TFA_CHECK(got[fused][2].size() == (size_t)O * I && got[fused][3].size() == (size_t)O);
+        }
+        const std::string tag = bf16 ? " (bf16)" : " (fp32)";
+        for (int k = 0; k < 3; ++k)
+            for (size_t i = 0; i < got[0][k].size(); ++i)
+                check_near(got[1][k][i], got[0][k][i], 1e-6f, "fused vs relu(forward)" + tag + " output " +
+                                                               std::to_string(k) + "[" + std::to_string(i) + "]");
+        for (int o = 0; o < O; ++o) {
+            // The masked upstream gradient as the backward sees it (bf16 up
+            // in bf16 compute), summed in double.
+            double s = 0.0;
+            for (int r = 0; r < R; ++r) {
+                float u = uv[r * O + o];
+                if (bf16) u = to_host(from_vals({u}, {1}, Device::cpu()).to(Dtype::BFloat16))[0];
+                if (got[0][0][r * O + o] > 0.0f) s += u;
+            }
+            check_near(got[1][3][o], got[0][3][o], 1e-5f, "db fused vs relu(forward)" + tag + "[" + std::to_string(o) + "]");
+            check_near(got[1][3][o], (float)s, 1e-4f, "db vs double sum" + tag + "[" + std::to_string(o) + "]");
+        }
+    }
+}
+
 // Conv2dModule::forward_relu on a 1x1 convolution (w = 2, b = 0).
 void t_conv_relu_fused(Device d) {
     Tensor x = from_vals({1, -2, 3, -4}, {1, 1, 2, 2}, d);
@@ -586,6 +642,7 @@ const std::map<std::string, std::function<void(Device)>>& registry() {
         {"conv2d_explicit_backward", t_conv2d_module_explicit_backward},
         {"linear_grads", t_linear_grads},
         {"linear_relu_fused", t_linear_relu_fused},
+        {"linear_relu_bias_wide", t_linear_relu_bias_wide},
         {"conv_relu_fused", t_conv_relu_fused},
         {"sgd_momentum_rule", t_sgd_momentum_rule},
         {"reshape_grad", t_reshape_grad},
