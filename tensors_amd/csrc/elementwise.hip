@@ -289,11 +289,16 @@ __device__ __forceinline__ float sgd1(float pv, float gv, float* vp, bool use_v,
 }
 
 // Several parameters in one launch (an optimiser's whole step).  Work units
-// of kSgdUnit consecutive elements of one tensor; unit u belongs to tensor t
+// of sgd_unit<NT>() consecutive elements of one tensor; unit u belongs to tensor t
 // with unit_start[t] <= u < unit_start[t + 1].  The element update is the
 // one of sgd_momentum_kernel (sgd4 / sgd1), so each tensor ends up exactly
 // as tf_sgd_momentum would leave it.
-constexpr int kSgdUnit = 2048;  // 256 threads x 2 float4
+// float4 per thread and stream, loaded together: 4 for updates that stream
+// past the last-level cache (C5's 138 M parameters: 551 -> 538 us), 2 for
+// small warm ones (C2: 16.1 us, against 16.9 with 4).  A work unit is 256
+// threads' worth.
+template <bool NT> constexpr int sgd_u() { return NT ? 4 : 2; }
+template <bool NT> constexpr int sgd_unit() { return 256 * 4 * sgd_u<NT>(); }
 struct SgdMultiArgs {
     float* p[TF_SGD_MULTI_MAX];
     const float* g[TF_SGD_MULTI_MAX];
@@ -313,8 +318,9 @@ __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdMultiArgs a, fl
     for (int64_t u = blockIdx.x; u < units; u += gridDim.x) {
         int t = 0;
         while (u >= a.unit_start[t + 1]) ++t;
-        const int64_t e0 = (u - a.unit_start[t]) * kSgdUnit;
-        const int64_t e1 = min(a.n[t], e0 + kSgdUnit);
+        constexpr int kU = sgd_u<NT>(), kUnit = sgd_unit<NT>();
+        const int64_t e0 = (u - a.unit_start[t]) * kUnit;
+        const int64_t e1 = min(a.n[t], e0 + kUnit);
         float* p = a.p[t];
         const float* g = a.g[t];
         float* v = a.v[t];
@@ -325,27 +331,26 @@ __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdMultiArgs a, fl
             const float4* G = reinterpret_cast<const float4*>(g);
             float4* V = reinterpret_cast<float4*>(v);
             const int64_t vend = e1 / 4;  // e0 is a multiple of 4
-            const int64_t i0 = e0 / 4 + threadIdx.x, i1 = i0 + 256;
-            const bool ok0 = i0 < vend, ok1 = i1 < vend;
-            float4 pp0, gg0, vv0 = make_float4(0.f, 0.f, 0.f, 0.f), pp1, gg1, vv1 = vv0;
-            if (ok0) {
-                pp0 = tfd::ld_v<NT>(P + i0);
-                gg0 = tfd::ld_v<NT>(G + i0);
-                if (use_v) vv0 = tfd::ld_v<NT>(V + i0);
+            const int64_t i0 = e0 / 4 + threadIdx.x;
+            float4 pp[kU], gg[kU], vv[kU];
+#pragma unroll
+            for (int k = 0; k < kU; ++k) {
+                vv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (i0 + 256 * k < vend) {
+                    pp[k] = tfd::ld_v<NT>(P + i0 + 256 * k);
+                    gg[k] = tfd::ld_v<NT>(G + i0 + 256 * k);
+                    if (use_v) vv[k] = tfd::ld_v<NT>(V + i0 + 256 * k);
+                }
             }
-            if (ok1) {
-                pp1 = tfd::ld_v<NT>(P + i1);
-                gg1 = tfd::ld_v<NT>(G + i1);
-                if (use_v) vv1 = tfd::ld_v<NT>(V + i1);
+#pragma unroll
+            for (int k = 0; k < kU; ++k) {
+                const int64_t i = i0 + 256 * k;
+                if (i >= vend) continue;
+                sgd4(pp[k], gg[k], vv[k], use_v, lr, mu);
+                tfd::st_v<NT>(P + i, pp[k]);
+                if (use_v) tfd::st_v<NT>(V + i, vv[k]);
+                if (s) tfd::st_v<NT>(reinterpret_cast<uint2*>(s) + i, bf16x4(pp[k]));
             }
-            auto finish = [&](int64_t i, float4& pp, const float4& gg, float4& vv) {
-                sgd4(pp, gg, vv, use_v, lr, mu);
-                tfd::st_v<NT>(P + i, pp);
-                if (use_v) tfd::st_v<NT>(V + i, vv);
-                if (s) tfd::st_v<NT>(reinterpret_cast<uint2*>(s) + i, bf16x4(pp));
-            };
-            if (ok0) finish(i0, pp0, gg0, vv0);
-            if (ok1) finish(i1, pp1, gg1, vv1);
             js = vend * 4;
         }
         for (int64_t j = js + threadIdx.x; j < e1; j += 256) {
@@ -477,15 +482,19 @@ tf_status tf_sgd_momentum_multi(tf_ctx* ctx, int count, float* const* p, const f
         a.n[m] = n[i];
         a.vec_ok[m] = aligned16<char>(p[i]) && aligned16<char>(g[i]) && (vi == nullptr || aligned16<char>(vi)) &&
                       (si == nullptr || (reinterpret_cast<uintptr_t>(si) & 7) == 0);
-        a.unit_start[m] = units;
-        units += (n[i] + kSgdUnit - 1) / kSgdUnit;
         bytes += n[i] * (12 + (mu != 0.0f ? 8 : 0) + (si ? 2 : 0));
         ++m;
     }
-    a.unit_start[m] = units;
     a.count = m;
+    const bool nt = bytes > tfd::kStreamMinBytes;
+    const int64_t unit = nt ? sgd_unit<true>() : sgd_unit<false>();
+    for (int i = 0; i < m; ++i) {
+        a.unit_start[i] = units;
+        units += (a.n[i] + unit - 1) / unit;
+    }
+    a.unit_start[m] = units;
     if (units == 0) return TF_OK;
-    auto kernel = bytes > tfd::kStreamMinBytes ? sgd_multi_kernel<true> : sgd_multi_kernel<false>;
+    auto kernel = nt ? sgd_multi_kernel<true> : sgd_multi_kernel<false>;
     kernel<<<(unsigned)std::min<int64_t>(units, 16384), 256, 0, ctx->stream>>>(a, lr, mu);
     return tfh::check_launch("sgd_multi_kernel");
 }
