@@ -161,8 +161,16 @@ __device__ __forceinline__ void block_mean(const float* __restrict__ nll, int ro
                                            float* __restrict__ loss) {
     __shared__ float part[4];
     float s = 0.0f;
-    for (int i = threadIdx.x; i < rows; i += 256)
-        s += __hip_atomic_load(nll + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int i = threadIdx.x;
+    // Sixteen loads in flight, then added in the same order as one at a time.
+    for (; i + 15 * 256 < rows; i += 16 * 256) {
+        float t[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) t[u] = __hip_atomic_load(nll + i + 256 * u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) s += t[u];
+    }
+    for (; i < rows; i += 256) s += __hip_atomic_load(nll + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s = tfd::wave_sum(s);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
     __syncthreads();
