@@ -2370,9 +2370,23 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
         const float* src = p.partial + (int64_t)row * p.N + col0;
         float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (vec) {
-            for (int k = 0; k < splits; ++k) {
-                const float4 v = *reinterpret_cast<const float4*>(src + k * plane);
-                s[0] += v.x; s[1] += v.y; s[2] += v.z; s[3] += v.w;
+            // Eight splits' loads in flight at a time, added in split order.
+            int k = 0;
+            for (; k + 8 <= splits; k += 8) {
+                float4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float4*>(src + (k + u) * plane);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) { s[0] += v[u].x; s[1] += v[u].y; s[2] += v[u].z; s[3] += v[u].w; }
+            }
+            if (k < splits) {
+                float4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (k + u < splits) v[u] = *reinterpret_cast<const float4*>(src + (k + u) * plane);
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (k + u < splits) { s[0] += v[u].x; s[1] += v[u].y; s[2] += v[u].z; s[3] += v[u].w; }
             }
         } else {
             for (int k = 0; k < splits; ++k)
