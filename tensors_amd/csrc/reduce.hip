@@ -2,8 +2,8 @@
 //   colsum : db[c] = sum_r dy[r, c]           (Linear bias grad; fp32 or bf16 dy)
 //   chansum: db[c] = sum_{n,p} dy[n, c, p]    (Conv2d bias grad, NCHW)
 // Colsums over a multiple of 4 columns run as one launch of (strip, chunk)
-// blocks whose last arrival per strip adds the chunks.  The others are
-// two-stage: stage 1 writes per-chunk partial sums to the context
+// blocks whose last arrival per strip adds the chunks; small ones as one
+// block.  The others are two-stage: stage 1 writes per-chunk partial sums to the context
 // workspace, stage 2 (tfh::partial_rows_sum, also used by the LayerNorm
 // backward) adds them in a fixed order.  The reference's conv kernel
 // lets every block overwrite out[c] with its own partial
@@ -302,6 +302,39 @@ __global__ __launch_bounds__(256) void relu_bwd_colsum_kernel(const T* __restric
     if (threadIdx.x == 0) __hip_atomic_store(tickets + strip, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Small colsums (cols <= 256, rows * cols <= kSmallColsum) in one block: the
+// 256 threads are cols columns x G = 256 / cols row groups; thread (c, g)
+// adds rows g, g + G, ... of column c in ascending order (eight loads in
+// flight), and thread c adds the G group sums in order.  One launch where
+// the two-stage path takes two (C4's 10-wide classifier bias).
+constexpr int64_t kSmallColsum = 1 << 16;
+template <typename T>
+__global__ __launch_bounds__(256) void colsum_small_kernel(const T* __restrict__ dy, float* __restrict__ db, int rows,
+                                                           int cols) {
+    __shared__ float red[256];
+    const int G = 256 / cols;
+    const int c = threadIdx.x % cols, g = threadIdx.x / cols;
+    float s = 0.0f;
+    if (g < G) {
+        int r = g;
+        for (; r + 7 * G < rows; r += 8 * G) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] = elem_f32(dy, (int64_t)(r + u * G) * cols + c);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += t[u];
+        }
+        for (; r < rows; r += G) s += elem_f32(dy, (int64_t)r * cols + c);
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+    if ((int)threadIdx.x < cols) {
+        float v = 0.0f;
+        for (int k = 0; k < G; ++k) v += red[k * cols + threadIdx.x];
+        db[threadIdx.x] = v;
+    }
+}
+
 // Stage 2 of every two-stage reduction here (colsum, chansum, LayerNorm
 // dgamma/dbeta): out[j] = sum_k part[k][j] over a [K][W] partial matrix, the
 // first `split` columns to out_lo, the rest to out_hi.  A block owns 16
@@ -395,6 +428,10 @@ tf_status colsum_impl(tf_ctx* ctx, const T* dy, float* db, int64_t rows, int64_t
             dy, db, reinterpret_cast<float*>(ctx->ws), ctx->tickets + tfh::kTicketColsum, (int)rows, (int)cols, rpc,
             (int)chunks);
         return tfh::check_launch("colsum_tile_kernel");
+    }
+    if (cols <= 256 && rows * cols <= kSmallColsum) {
+        colsum_small_kernel<T><<<1, 256, 0, ctx->stream>>>(dy, db, (int)rows, (int)cols);
+        return tfh::check_launch("colsum_small_kernel");
     }
     const int strips = (int)((cols + kColsPerBlock - 1) / kColsPerBlock);
     // Aim for ~512 stage-1 blocks (two per CU) with at least 16 rows each.

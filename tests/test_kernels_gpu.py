@@ -734,8 +734,8 @@ def test_softmax_bwd_uniform_is_zero(ctx):
 # Multiples of 4 columns take the one-launch tile kernel: (2048, 2048),
 # (4096, 8192), (7, 4096), (3001, 16384), (64, 256), (33, 64) (a short last
 # chunk), (5000, 96) (157 chunks added by each strip's last block), and with
-# a ragged last 32-column strip (100, 2056), (4096, 1000), (9, 4); the others
-# ((17, 19), (1, 5), (4096, 10), (3, 1001)) are two-stage.
+# a ragged last 32-column strip (100, 2056), (4096, 1000), (9, 4); small ones
+# ((17, 19), (1, 5), (4096, 10)) take one block, (3, 1001) the two stages.
 @pytest.mark.parametrize("R,Cc", [(2048, 2048), (64, 256), (17, 19), (1, 5), (4096, 10), (3, 1001), (4096, 8192),
                                   (7, 4096), (3001, 16384), (100, 2056), (33, 64), (5000, 96), (4096, 1000), (9, 4)])
 def test_colsum(ctx, R, Cc):
