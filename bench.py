@@ -200,7 +200,7 @@ def bench_bandwidth_rotated(reps: int = 60):
     it (sets together > 256 MB): C2's bias column sum and SGD-momentum step
     (W and b in one launch), C5's SGD step over its 138 M parameters with the
     bf16 copies, C4 conv2's im2col and col2im (N 128, C 32, 32 x 32, k 3,
-    stride 2, pad 1)."""
+    stride 2, pad 1), and C5's fused ReLU backward + bias gradient."""
     import tensors_amd as ta
     from tensors_amd import ops, synth
     from tensors_amd.profiling import CONV2
@@ -239,6 +239,17 @@ def bench_bandwidth_rotated(reps: int = 60):
         ctx, sets, lambda i: ops.im2col(xs[i], cols[i], k, k, (2, 2), (1, 1)), reps))
     out["col2im_conv2_c4"] = _bw_entry("col2im_conv2_c4", _rotating_bench(
         ctx, sets, lambda i: ops.col2im(cols[i], xs[i], k, k, (2, 2), (1, 1)), reps))
+    del xs, cols
+    # C5 layer 1's ReLU backward + the next Linear's bias gradient, bf16
+    # [4096 x 8192]; 4 x 3 x 64 MB.
+    R5, C5w = C5_BATCH, C5_DIMS[1]
+    sets = 4
+    gs = [ctx.array(ta.f32_to_bf16_bits(synth.normal(synth.seed(6, 4) + i, (R5, C5w))), ta.BF16) for i in range(sets)]
+    xs = [ctx.array(ta.f32_to_bf16_bits(synth.normal(synth.seed(6, 5) + i, (R5, C5w))), ta.BF16) for i in range(sets)]
+    dzs = [ctx.empty((R5, C5w), ta.BF16) for _ in range(sets)]
+    db5 = ctx.empty((C5w,))
+    out["relu_bwd_colsum_c5"] = _bw_entry("relu_bwd_colsum_c5", _rotating_bench(
+        ctx, sets, lambda i: ops.relu_bwd_colsum(gs[i], xs[i], dzs[i], db5), reps))
     ctx.close()
     return out
 

@@ -64,6 +64,9 @@ BW_KERNELS = {
     "sgd_c5": ("sgd_multi_kernel<true>", 22 * C5_PARAMS),
     "im2col_conv2_c4": ("im2col_plane_kernel<float>", _conv_x + _conv_col),
     "col2im_conv2_c4": ("col2im_plane_kernel<float>", _conv_col + _conv_x),
+    # C5 layer 1's ReLU backward with the next Linear's bias gradient
+    # (bf16 [4096 x 8192]): dy, x read, dz written, db (fp32) written
+    "relu_bwd_colsum_c5": ("relu_bwd_colsum_kernel<unsigned short>", 3 * C5_B * C5_DIMS[1] * 2 + C5_DIMS[1] * 4),
 }
 # The streaming-ceiling row (bench.py --hbm-ceiling: mix, non-temporal,
 # MB per array) each kernel is read against: the mix of its reads and writes
@@ -78,6 +81,7 @@ BW_CEILING = {
     "sgd_c5": ("3R+2W (SGD mix)", True, 512),
     "im2col_conv2_c4": ("copy (1R+1W)", True, 16),
     "col2im_conv2_c4": ("copy (1R+1W)", True, 16),
+    "relu_bwd_colsum_c5": ("2R+1W", True, 64),
 }
 # The LayerNorm backward op as a whole (C3c): dy, x, dx, gamma, dgamma,
 # dbeta, mean, rstd -- the block partials are not part of it.
