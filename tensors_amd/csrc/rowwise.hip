@@ -1,4 +1,5 @@
-// Row kernels: cross-entropy forward/backward (fused LogSoftmax+NLL),
+// Row kernels: cross-entropy forward/backward (fused LogSoftmax+NLL; the
+// fused form also for bf16 logits, widened on load and rounded on store),
 // log_softmax / softmax forward and backward.  One wave64 per row, 4 rows per
 // 256-thread block.  Rows of up to kMaxCached * 256 columns stay in registers
 // (one HBM read per pass); wider rows are streamed twice.
