@@ -2444,6 +2444,131 @@ __global__ __launch_bounds__(256) void splitk_reduce_wide_kernel(GemmParams p, i
 using KernelFn = void (*)(GemmParams);
 
 
+// Narrow outputs over a long reduction, fp32: C = epi(alpha * A B^T) with
+// A row-major [M x K] and B as [N x K] (trans_b), N <= 16 (a classifier
+// forward: C4's 128 x 10 x 16384).  Block (c, g) takes the rows 8g .. 8g+7
+// (a wave each) over the k chunk c of kSkC columns: the chunk of B (N x kSkC
+// floats) is staged in LDS once per block, each lane multiplies 4
+// consecutive k of its row, 256 apart, with all N rows of B, and a wave
+// butterfly adds the N dot products.  With several chunks each row's N sums
+// go to partials through agent-scope stores and the row group's last block
+// (arrival counter) adds them in chunk order (deterministic), then applies
+// alpha, the bias and ReLU.  C4's shape: 12.7 us, where the tiled kernel and
+// its split-K reduction took 12.9 + 4.4 us; what remains is the chain of
+// latencies (loads, partial stores, the counter, the last block's loads).
+constexpr int kSkN = 16, kSkC = 1024, kSkRows = 8;
+__global__ __launch_bounds__(512) void gemm_f32_skinny_kernel(GemmParams p, int chunks, unsigned* __restrict__ tickets) {
+    __shared__ float4 bs[kSkN][kSkC / 4];
+    __shared__ bool last;
+    const int N = p.N, K = p.K, M = p.M;
+    const int c = blockIdx.x, g = blockIdx.y;
+    const int k0 = c * kSkC;
+    const float* A = reinterpret_cast<const float*>(p.A);
+    const float* B = reinterpret_cast<const float*>(p.B);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int m = g * kSkRows + wave;
+    // This lane's A values first, so their latency overlaps the B staging.
+    float4 av[kSkC / 256];
+#pragma unroll
+    for (int j = 0; j < kSkC / 256; ++j) {
+        const int k = k0 + 4 * (lane + 64 * j);
+        const float* a = A + (int64_t)min(m, M - 1) * p.lda;
+        if (p.vec_a && k + 4 <= K) {
+            av[j] = *reinterpret_cast<const float4*>(a + k);
+        } else {
+            av[j].x = k + 0 < K ? a[k + 0] : 0.0f;
+            av[j].y = k + 1 < K ? a[k + 1] : 0.0f;
+            av[j].z = k + 2 < K ? a[k + 2] : 0.0f;
+            av[j].w = k + 3 < K ? a[k + 3] : 0.0f;
+        }
+    }
+    // The B chunk: all of this thread's loads in flight, then the LDS stores.
+    constexpr int kSkPer = kSkN * (kSkC / 4) / 512;
+    float4 bv[kSkPer];
+#pragma unroll
+    for (int r = 0; r < kSkPer; ++r) {
+        const int i = threadIdx.x + 512 * r;
+        const int n = i / (kSkC / 4), q = i % (kSkC / 4), k = k0 + 4 * q;
+        bv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (n < N) {
+            const float* src = B + (int64_t)n * p.ldb + k;
+            if (p.vec_b && k + 4 <= K) {
+                bv[r] = *reinterpret_cast<const float4*>(src);
+            } else {
+                bv[r].x = k + 0 < K ? src[0] : 0.0f;
+                bv[r].y = k + 1 < K ? src[1] : 0.0f;
+                bv[r].z = k + 2 < K ? src[2] : 0.0f;
+                bv[r].w = k + 3 < K ? src[3] : 0.0f;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kSkPer; ++r) {
+        const int i = threadIdx.x + 512 * r;
+        bs[i / (kSkC / 4)][i % (kSkC / 4)] = bv[r];
+    }
+    __syncthreads();
+    float acc[kSkN];
+#pragma unroll
+    for (int n = 0; n < kSkN; ++n) acc[n] = 0.0f;
+    if (m < M) {
+#pragma unroll
+        for (int j = 0; j < kSkC / 256; ++j)
+#pragma unroll
+            for (int n = 0; n < kSkN; ++n) {
+                if (n >= N) break;
+                const float4 b = bs[n][lane + 64 * j];
+                acc[n] += av[j].x * b.x + av[j].y * b.y + av[j].z * b.z + av[j].w * b.w;
+            }
+    }
+#pragma unroll
+    for (int n = 0; n < kSkN; ++n)
+        if (n < N) acc[n] = tfd::wave_sum(acc[n]);
+    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU || p.epi == TF_EPI_ROW_BIAS_RELU;
+    const bool has_bias = p.epi != TF_EPI_NONE && p.epi != TF_EPI_RELU;
+    auto finish = [&](int row, int n, float sum) {
+        float v = p.alpha * sum;
+        if (has_bias) v += p.row_bias ? p.bias[row] : p.bias[n];
+        if (relu) v = fmaxf(v, 0.0f);
+        reinterpret_cast<float*>(p.C)[(int64_t)row * p.ldc + n] = v;
+    };
+    // Lane n holds the row's n-th sum (every lane holds all of them after
+    // the butterfly; lane n keeps acc[n]).
+    float mine = 0.0f;
+#pragma unroll
+    for (int n = 0; n < kSkN; ++n)
+        if (lane == n) mine = acc[n];
+    if (chunks == 1) {
+        if (m < M && lane < N) finish(m, lane, mine);
+        return;
+    }
+    if (m < M && lane < N)
+        __hip_atomic_store(p.partial + ((int64_t)c * M + m) * N + lane, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the partials have landed
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(tickets + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (unsigned)(chunks - 1);
+    __syncthreads();
+    if (!last) return;
+    if (m < M && lane < N) {
+        const float* sp = p.partial + (int64_t)m * N + lane;
+        const int64_t step = (int64_t)M * N;
+        float v = 0.0f;
+        int k = 0;
+        for (; k + 8 <= chunks; k += 8) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] = __hip_atomic_load(sp + (k + u) * step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += t[u];
+        }
+        for (; k < chunks; ++k) v += __hip_atomic_load(sp + k * step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        finish(m, lane, v);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(tickets + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // fp32 GEMM with a short K (<= 32) and few rows (<= 64), A K-major and B
 // MN-major: a convolution over few input channels (W [Cout x Cin*k*k] times
 // each image's im2col block).  An MFMA tile would be mostly padding and one
@@ -2671,6 +2796,28 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     p.pair_c = (reinterpret_cast<uintptr_t>(C) & 7) == 0 && (ldc % 2 == 0) && (p.stride_c % 2 == 0);
     const uintptr_t c_vec_bytes = out_dtype == TF_BF16 ? 8 : 16;
     p.vec_c4 = (reinterpret_cast<uintptr_t>(C) & (c_vec_bytes - 1)) == 0 && (ldc % 4 == 0) && (p.stride_c % 4 == 0);
+    // Narrow fp32 outputs over a long K (see gemm_f32_skinny_kernel).
+    if (in_dtype == TF_F32 && out_dtype == TF_F32 && batch == 1 && !reduce_batch && a_kmaj && b_kmaj && N <= kSkN &&
+        K >= 2048 && beta == 0.0f && (M + kSkRows - 1) / kSkRows <= tfh::kTicketGemmTiles) {
+        const int64_t chunks = (K + kSkC - 1) / kSkC;
+        const int64_t groups = (M + kSkRows - 1) / kSkRows;
+        TF_REQUIRE(chunks < 65536 && groups < 65536, "tf_gemm: skinny grid too large");
+        if (chunks > 1) {
+            const size_t need = (size_t)chunks * (size_t)M * (size_t)N * sizeof(float);
+            if (noalloc) {
+                if (need > kNoAllocScratchBytes) return tfh::set_error(TF_ERR_INVALID, "tf_gemm_noalloc: partials too large");
+                tf_status st = scratch_address(ctx->device, &p.partial);
+                if (st != TF_OK) return st;
+            } else {
+                tf_status st = tfh::ensure_workspace(ctx, need);
+                if (st != TF_OK) return st;
+                p.partial = reinterpret_cast<float*>(ctx->ws);
+            }
+        }
+        gemm_f32_skinny_kernel<<<dim3((unsigned)chunks, (unsigned)groups), 512, 0, ctx->stream>>>(
+            p, (int)chunks, ctx->tickets + tfh::kTicketGemm);
+        return tfh::check_launch("gemm_f32_skinny_kernel");
+    }
     // Small fp32 products: 32 x 32 tiles with K over many blocks (see
     // gemm_f32_small_kernel).
     const int64_t sm_tiles = ((M + kSmT - 1) / kSmT) * ((N + kSmT - 1) / kSmT);

@@ -147,6 +147,29 @@ def test_gemm_splitk_long_k(ctx):
     assert_close(got, _gemm_truth(a, w, False, True), RTOL32, "split-K gemm")
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 10, 16384), (13, 1, 2051), (64, 16, 4096), (8, 7, 2048), (300, 3, 9001)])
+def test_gemm_narrow_output_long_k(ctx, M, N, K):
+    """Outputs of at most 16 columns over K >= 2048 (A row-major, B as
+    [N x K]): the narrow-output kernel, with a ragged last k chunk, a row
+    count off the 8-row groups, bias and bias + ReLU; bit-identical on a
+    second call (each row group's arrival counter back at zero)."""
+    ops = _ops()
+    seed = synth.seed(2, 11) + M + N + K
+    a = synth.normal(seed, (M, K))
+    w = synth.normal(seed + 1, (N, K))
+    bias = synth.normal(seed + 2, (N,))
+    da, dw, db = ctx.array(a), ctx.array(w), ctx.array(bias)
+    c = ctx.empty((M, N))
+    ops.gemm(da, dw, c, trans_b=True, bias=db)
+    first = c.numpy()
+    assert_close(first, _gemm_truth(a, w, False, True, bias=bias), RTOL32, f"narrow gemm {M}x{N}x{K}")
+    ops.gemm(da, dw, c, trans_b=True, bias=db)
+    assert_bitexact(c.numpy(), first, f"narrow gemm {M}x{N}x{K} repeat")
+    ops.gemm(da, dw, c, trans_b=True, bias=db, relu=True, alpha=0.5)
+    assert_close(c.numpy(), _gemm_truth(a, w, False, True, alpha=0.5, bias=bias, relu=True), RTOL32,
+                 f"narrow gemm {M}x{N}x{K} bias+relu")
+
+
 def test_gemm_epilogues(ctx):
     M, N, K = 96, 200, 150
     a = synth.normal(31, (M, K))
