@@ -170,6 +170,18 @@ def test_gemm_narrow_output_long_k(ctx, M, N, K):
                  f"narrow gemm {M}x{N}x{K} bias+relu")
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 16384, 10), (200, 300, 7), (64, 1024, 32), (256, 257, 1)])
+def test_gemm_short_k_wide_output(ctx, M, N, K):
+    """K <= 32 and at least 256 output columns (A and B row-major: a
+    classifier's data gradient), with a bias, against float64."""
+    seed = synth.seed(2, 12) + M + N + K
+    a = synth.normal(seed, (M, K))
+    b = synth.normal(seed + 1, (K, N))
+    bias = synth.normal(seed + 2, (N,))
+    got = _run_gemm(ctx, a, b, False, False, M, N, bias=bias)
+    assert_close(got, _gemm_truth(a, b, False, False, bias=bias), RTOL32, f"short-K gemm {M}x{N}x{K}")
+
+
 def test_gemm_epilogues(ctx):
     M, N, K = 96, 200, 150
     a = synth.normal(31, (M, K))
