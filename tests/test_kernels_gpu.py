@@ -140,7 +140,7 @@ def test_gemm_matches_reference_order_oracle(ctx):
 
 
 def test_gemm_splitk_long_k(ctx):
-    # C4's classifier: [128 x 16384] @ [16384 x 10] -> one tile, split over K.
+    # C4's classifier: [128 x 16384] @ [16384 x 10] (the narrow-output kernel's k chunks).
     a = synth.normal(21, (128, 16384))
     w = synth.normal(22, (10, 16384))
     got = _run_gemm(ctx, a, w, False, True, 128, 10)
