@@ -170,7 +170,8 @@ def test_gemm_narrow_output_long_k(ctx, M, N, K):
                  f"narrow gemm {M}x{N}x{K} bias+relu")
 
 
-@pytest.mark.parametrize("M,N,K", [(128, 16384, 10), (200, 300, 7), (64, 1024, 32), (256, 257, 1)])
+@pytest.mark.parametrize("M,N,K", [(128, 16384, 10), (200, 300, 7), (64, 1024, 32), (256, 257, 1), (77, 1027, 32),
+                                   (300, 2049, 5)])
 def test_gemm_short_k_wide_output(ctx, M, N, K):
     """K <= 32 and at least 256 output columns (A and B row-major: a
     classifier's data gradient), with a bias, against float64."""
