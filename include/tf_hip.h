@@ -143,8 +143,11 @@ tf_status tf_hip_event_destroy(void* event);
  *                   failed call during capture it returns that error and no
  *                   graph.  Blocks freed during capture belong to the graph
  *                   until tf_graph_destroy (so no other allocation receives a
- *                   replay's temporaries); blocks allocated during capture
- *                   and still live must stay live while the graph is replayed.
+ *                   replay's temporaries), and so do blocks allocated during
+ *                   capture that the caller frees while the graph exists:
+ *                   tf_hip_free hands them to the graph, not to the cache.
+ *                   Blocks allocated before the capture that the graph reads
+ *                   or writes must stay live while it is replayed.
  *   tf_graph_launch enqueues one replay on the context's stream (the context
  *                   must be the capturing one, its workspace unmoved).
  *   tf_graph_destroy returns the graph's blocks to the context's cache;

@@ -29,6 +29,7 @@ REF_SO = HERE / "_ref" / "libtfref.so"
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
 _i64 = C.c_int64
 _f = C.c_float
 
@@ -71,6 +72,8 @@ def _load_oracle() -> C.CDLL:
         "orc_conv2d_bwd": [_f32p, _f32p, C.c_int, _f32p, _f32p, _f32p, _f32p] + [_i64] * 13,
         "orc_argmax_rows": [_f32p, _i64p, _i64, _i64],
         "orc_sum_dim": [_f32p, _f32p, _i64, _i64, _i64],
+        "orc_f32_to_f16": [_f32p, _u16p, _i64],
+        "orc_f16_to_f32": [_u16p, _f32p, _i64],
     }
     lib.orc_ce_module.argtypes = [_f32p, _i64p, _i64, _i64, _f32p, _f32p]
     lib.orc_ce_module.restype = C.c_int
@@ -118,6 +121,23 @@ def linear_bwd(x, w, dy):
     dx = matmul(dy, w)
     dw = transpose2d(matmul(transpose2d(x), dy))
     return dx, dw
+
+
+def f32_to_f16_bits(x):
+    """IEEE binary16 bit patterns of float32 values, round to nearest even
+    (the reference's __float2half)."""
+    x = _f32(x)
+    h = np.empty(x.shape, np.uint16)
+    lib.orc_f32_to_f16(x.reshape(-1), h.reshape(-1), x.size)
+    return h
+
+
+def f16_bits_to_f32(h):
+    """float32 values of IEEE binary16 bit patterns (exact)."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    x = np.empty(h.shape, np.float32)
+    lib.orc_f16_to_f32(h.reshape(-1), x.reshape(-1), h.size)
+    return x
 
 
 def _unary(fn, x):

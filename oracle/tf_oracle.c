@@ -431,3 +431,67 @@ void orc_argmax_rows(const float* x, int64_t* out, int64_t R, int64_t C) {
         out[r] = pred;
     }
 }
+
+/* IEEE 754 binary16 <-> binary32.  The reference has no host function for
+ * this: its 16-bit device paths convert with __half2float (exact) and
+ * __float2half (round to nearest, ties to even), cuda/kernels/elementwise.cu
+ * :42-64, col2im.cu:44, im2col.cu:133-150.  Written from the format's
+ * definition (1 sign, 5 exponent bits biased by 15, 10 fraction bits;
+ * subnormals k * 2^-24).  A NaN stays a NaN (made quiet, top fraction bits
+ * kept); its payload is not part of any check. */
+static uint16_t f32_to_f16_rne(float f) {
+    uint32_t x;
+    memcpy(&x, &f, sizeof x);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t exp = (x >> 23) & 0xFFu;
+    const uint32_t man = x & 0x7FFFFFu;
+    if (exp == 0xFFu) return (uint16_t)(sign | 0x7C00u | (man ? (0x200u | (man >> 13)) : 0u));
+    if (exp == 0u) return (uint16_t)sign; /* f32 subnormal or zero: below half of the smallest f16 subnormal */
+    const int32_t e = (int32_t)exp - 127 + 15; /* biased f16 exponent */
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    uint32_t q, rem, half;
+    if (e >= 1) {
+        /* normal: keep 10 of the 23 fraction bits; a carry out of the
+         * fraction moves into the exponent (and to infinity at the top) */
+        q = ((uint32_t)e << 10) | (man >> 13);
+        rem = man & 0x1FFFu;
+        half = 0x1000u;
+    } else {
+        /* subnormal result: value = M * 2^(exp - 150) = k * 2^-24 with
+         * k = M >> (126 - exp), M the 24-bit significand */
+        const uint32_t M = man | 0x800000u;
+        const int s = 14 - e; /* 126 - exp, >= 14 */
+        if (s > 25) return (uint16_t)sign;
+        q = M >> s;
+        rem = M & ((1u << s) - 1u);
+        half = 1u << (s - 1);
+    }
+    if (rem > half || (rem == half && (q & 1u))) ++q;
+    return (uint16_t)(sign | q);
+}
+
+static float f16_to_f32(uint16_t h) {
+    const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    const uint32_t exp = ((uint32_t)h >> 10) & 0x1Fu;
+    const uint32_t man = (uint32_t)h & 0x3FFu;
+    uint32_t x;
+    if (exp == 0u) {
+        const float v = ldexpf((float)man, -24); /* exact: at most 10 significant bits */
+        memcpy(&x, &v, sizeof x);
+        x |= sign;
+    } else if (exp == 31u) {
+        x = sign | 0x7F800000u | (man << 13);
+    } else {
+        x = sign | ((exp - 15u + 127u) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &x, sizeof f);
+    return f;
+}
+
+void orc_f32_to_f16(const float* x, uint16_t* h, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) h[i] = f32_to_f16_rne(x[i]);
+}
+void orc_f16_to_f32(const uint16_t* h, float* x, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) x[i] = f16_to_f32(h[i]);
+}

@@ -370,10 +370,17 @@ std::vector<Tensor> CrossEntropyBackward::apply(std::vector<Tensor>&& grads) {
         // dlogits for g = 1; an undefined gradient is the unit seed.
         const Tensor& dl = stats_.unpack();
         if (!grads[0].storage()) return {dl};
-        // A non-unit upstream gradient: g * dl in fp32 (bf16 dlogits widened).
-        Tensor df = dl.dtype() == Dtype::Float32 ? dl : dl.to(Dtype::Float32);
-        Tensor d = raw::empty_like(df);
-        hip::scale_by(df, grads[0], d);
+        if (dl.dtype() == Dtype::Float32) {
+            // A non-unit upstream gradient: g * dl in fp32.
+            Tensor d = raw::empty_like(dl);
+            hip::scale_by(dl, grads[0], d);
+            return {std::move(d)};
+        }
+        // BFloat16 dlogits hold a rounding already: recompute
+        // g * (softmax - onehot) / N in fp32 from the widened logits.
+        const Tensor lf = logits_.unpack().to(Dtype::Float32);
+        Tensor d = raw::empty_like(lf);
+        hip::cross_entropy_backward(lf, targets_.unpack(), nullptr, &grads[0], d);
         return {std::move(d)};
     }
     const Tensor& logits = logits_.unpack();

@@ -17,10 +17,15 @@ public:
     CrossEntropyBackward(const Tensor& logits, const Tensor& targets, const Tensor& row_stats)
         : logits_(logits), targets_(targets), stats_(row_stats) {}
     // GPU, fused with the forward: dlogits for an upstream gradient of 1,
-    // computed in the forward's pass over the logits.
+    // computed in the forward's pass over the logits.  For BFloat16 logits
+    // the dlogits are BFloat16 and the node also keeps the logits and
+    // targets: a non-unit upstream gradient g then recomputes g * dlogits in
+    // fp32 from the logits, so they are rounded to bf16 once (by the
+    // consumer), not once before and once after the scaling.
     struct Precomputed {};
-    CrossEntropyBackward(Precomputed, const Tensor& dlogits)
-        : logits_(Tensor()), targets_(Tensor()), stats_(dlogits), precomputed_(true) {}
+    CrossEntropyBackward(Precomputed, const Tensor& dlogits, const Tensor& logits = Tensor(),
+                         const Tensor& targets = Tensor())
+        : logits_(logits), targets_(targets), stats_(dlogits), precomputed_(true) {}
     std::vector<Tensor> apply(std::vector<Tensor>&& grads) override;
     void release_saved() override { logits_.reset(); targets_.reset(); stats_.reset(); }
     // The precomputed dlogits are the answer for a unit seed as they are.

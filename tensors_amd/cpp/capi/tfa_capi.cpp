@@ -291,6 +291,109 @@ void t_cross_entropy_grad(Device d) {
     check_vec(logits.grad(), want, "dlogits", 1e-5f);
 }
 
+// nn::CrossEntropyLoss under a non-unit upstream gradient: (loss * 0.3)
+// and the sum of two losses (different targets) on the same logits, fp32
+// and (on the GPU) BFloat16 logits from a Linear.  logits.grad against
+// g * (softmax - onehot) / N in double (from the logits as stored), within
+// fp32 rounding: for bf16 logits this shows the scaled gradient is formed in
+// fp32 from the logits, not from dlogits already rounded to bf16.  W.grad
+// against double dlogits^T x, at the compute dtype's tolerance.  With a unit
+// seed the bf16 dlogits must be the double value rounded once (within half a
+// bf16 step).
+void t_cross_entropy_scaled_upstream(Device d) {
+    const int R = 37, I = 24, C = 13;
+    std::vector<float> xv(R * I), wv(C * I);
+    for (int i = 0; i < R * I; ++i) xv[i] = std::sin(0.31f * i + 0.2f);
+    for (int i = 0; i < C * I; ++i) wv[i] = 0.4f * std::cos(0.17f * i);
+    std::vector<int64_t> t1(R), t2(R);
+    for (int r = 0; r < R; ++r) {
+        t1[r] = (r * 7) % C;
+        t2[r] = (r * 5 + 3) % C;
+    }
+    const bool gpu = d.type == DeviceType::CUDA;
+    for (int bf16 = 0; bf16 <= (gpu ? 1 : 0); ++bf16) {
+        for (int mode = 0; mode < 3; ++mode) {   // 0: loss * 0.3, 1: loss1 + loss2, 2: loss (unit seed)
+            nn::Linear fc(I, C);
+            fc.to(d);
+            if (bf16) fc.set_compute_dtype(Dtype::BFloat16);
+            for (auto& np : fc.named_parameters()) {
+                np.second->data_ = np.first == "weight" ? from_vals(wv, {C, I}, d) : filled({C}, 0.0f, d);
+                np.second->data_.requires_grad(true);
+            }
+            Tensor x = from_vals(xv, {R, I}, d);
+            Tensor logits = fc.forward(x);
+            nn::CrossEntropyLoss ce;
+            Tensor l1 = ce.forward(logits, host_i64(t1.data(), {R}).to(d));
+            const float g = 0.3f;
+            if (mode == 0) (l1 * filled({1}, g, d)).backward();
+            else if (mode == 1) (l1 + ce.forward(logits, host_i64(t2.data(), {R}).to(d))).backward();
+            else l1.backward();
+            // Truth in double from the stored logits and inputs.
+            const std::vector<float> lg = to_host(logits);
+            const std::vector<float> xs = bf16 ? to_host(x.to(Dtype::BFloat16)) : xv;
+            std::vector<double> dl(R * C, 0.0);
+            for (int r = 0; r < R; ++r) {
+                double mx = lg[r * C];
+                for (int j = 1; j < C; ++j) mx = std::max(mx, (double)lg[r * C + j]);
+                double z = 0.0;
+                for (int j = 0; j < C; ++j) z += std::exp(lg[r * C + j] - mx);
+                for (int j = 0; j < C; ++j) {
+                    const double p = std::exp(lg[r * C + j] - mx) / z;
+                    if (mode == 0) dl[r * C + j] = g * (p - (j == t1[r])) / R;
+                    else if (mode == 1) dl[r * C + j] = (2 * p - (j == t1[r]) - (j == t2[r])) / R;
+                    else dl[r * C + j] = (p - (j == t1[r])) / R;
+                }
+            }
+            const std::string tag = std::string(bf16 ? " (bf16 logits" : " (fp32 logits") +
+                                    (mode == 0 ? ", loss * 0.3)" : mode == 1 ? ", loss1 + loss2)" : ", unit seed)");
+            const std::vector<float> gl = to_host(logits.grad());
+            TFA_CHECK(gl.size() == dl.size());
+            double rms = 0.0;
+            for (double v : dl) rms += v * v;
+            rms = std::sqrt(rms / dl.size());
+            for (size_t i = 0; i < dl.size(); ++i) {
+                double bound;
+                if (bf16 && mode == 2) {
+                    // bf16 dlogits: half a bf16 step of the value (2^(e-8)
+                    // for 2^e <= |v| < 2^(e+1)) plus fp32 noise.
+                    const double a = std::fabs(dl[i]);
+                    bound = (a > 0 ? std::ldexp(1.0, (int)std::floor(std::log2(a)) - 8) : 0.0) + 4e-6 * a + 1e-9;
+                } else {
+                    bound = 1e-5 * (std::fabs(dl[i]) + rms);
+                }
+                if (!(std::fabs(gl[i] - dl[i]) <= bound)) {
+                    std::ostringstream os;
+                    os << "dlogits" << tag << "[" << i << "]: got " << gl[i] << " want " << dl[i];
+                    throw std::runtime_error(os.str());
+                }
+            }
+            // W.grad = dlogits^T x (as the backward's GEMM sees dlogits: in
+            // the compute dtype).
+            std::vector<float> gw;
+            for (auto& np : fc.named_parameters())
+                if (np.first == "weight") gw = to_host(np.second->data_.grad());
+            TFA_CHECK(gw.size() == (size_t)C * I);
+            std::vector<double> tw(C * I, 0.0);
+            double wrms = 0.0;
+            for (int o = 0; o < C; ++o)
+                for (int k = 0; k < I; ++k) {
+                    double acc = 0.0;
+                    for (int r = 0; r < R; ++r) acc += dl[r * C + o] * xs[r * I + k];
+                    tw[o * I + k] = acc;
+                    wrms += acc * acc;
+                }
+            wrms = std::sqrt(wrms / tw.size());
+            const double rt = bf16 ? 2e-2 : 1e-4;
+            for (size_t i = 0; i < tw.size(); ++i)
+                if (!(std::fabs(gw[i] - tw[i]) <= rt * (std::fabs(tw[i]) + wrms))) {
+                    std::ostringstream os;
+                    os << "dW" << tag << "[" << i << "]: got " << gw[i] << " want " << tw[i];
+                    throw std::runtime_error(os.str());
+                }
+        }
+    }
+}
+
 // Sigmoid / tanh backward (wired here; the reference leaves them unwired).
 void t_sigmoid_tanh_grad(Device d) {
     Tensor x = from_vals({-1.5f, 0.0f, 0.7f}, {3}, d);
@@ -636,6 +739,7 @@ const std::map<std::string, std::function<void(Device)>>& registry() {
         {"saved_tensor_version", t_saved_tensor_version},
         {"cross_entropy_known", t_cross_entropy_known},
         {"cross_entropy_grad", t_cross_entropy_grad},
+        {"cross_entropy_scaled_upstream", t_cross_entropy_scaled_upstream},
         {"sigmoid_tanh_grad", t_sigmoid_tanh_grad},
         {"layernorm_grad", t_layernorm_grad},
         {"conv_1x1_golden", t_conv_1x1_golden},

@@ -36,7 +36,7 @@ Tensor CrossEntropyLoss::forward(Tensor logits, Tensor targets) {
         if (logits.dtype() == Dtype::BFloat16 && logits.requires_grad()) {
             Tensor dl = Tensor::empty(logits.shape(), Dtype::BFloat16, logits.device());
             hip::cross_entropy_forward_backward_bf16(logits, targets, loss, dl, TF_CE_MODULE);
-            node = std::make_shared<CrossEntropyBackward>(CrossEntropyBackward::Precomputed{}, dl);
+            node = std::make_shared<CrossEntropyBackward>(CrossEntropyBackward::Precomputed{}, dl, logits, targets);
             wiring::attach(loss, node, {wiring::accumulator_edge(logits)});
             return loss;
         }

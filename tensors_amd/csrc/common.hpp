@@ -14,6 +14,15 @@
 
 #include "tf_hip.h"
 
+// The kernels are written for gfx950 (CDNA4) only.  Beyond instruction
+// choice, the cross-block reductions (see tfd::wait_stores_landed below) rely on
+// how this GPU's memory system orders and completes agent-scope atomics, so
+// a device build for any other target is refused rather than left to run
+// with different guarantees.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "tensors_amd kernels target gfx950 only (build with --offload-arch=gfx950)"
+#endif
+
 struct tf_ctx {
     int device = 0;
     hipStream_t own_stream = nullptr;
@@ -41,6 +50,13 @@ struct tf_ctx {
     bool capturing = false;
     bool capture_failed = false;  // a call failed while capturing
     std::unordered_map<size_t, std::vector<void*>> capture_free;
+    // Blocks allocated during the current capture (the graph's kernels hold
+    // their addresses), and, after tf_graph_end, those of them still live,
+    // each mapped to its graph's list of held blocks: a tf_hip_free of such a
+    // block hands it to the graph instead of the cache, so no other work is
+    // given memory that later replays still write.
+    std::vector<void*> capture_allocs;
+    std::unordered_map<void*, std::vector<std::pair<void*, size_t>>*> graph_owned;
     // Arrival counters of the kernels whose last block to finish does a
     // final step (tfh::kTicket*): zero between launches (that block resets
     // its counter), so captured graphs replay them unchanged.  Launches on
@@ -124,6 +140,42 @@ namespace tfd {
 
 constexpr int kWave = 64;
 
+// s_waitcnt immediate (gfx9 encoding, which gfx950 keeps) waiting until at
+// most n vector memory operations of this wave are outstanding, leaving the
+// export and LDS counters unconstrained.
+constexpr int waitcnt_vm(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
+// ... and also for all outstanding LDS operations.
+constexpr int waitcnt_vm_lds(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0070; }
+
+// Cross-block reductions with a last-arriving block ("ticket" pattern):
+// every block stores its partial results with agent-scope relaxed atomic
+// stores, then counts itself in on a per-output counter with an agent-scope
+// relaxed fetch_add; the block that draws the last ticket reads all partials
+// with agent-scope relaxed atomic loads and writes the result.
+//
+// Why this is ordered on gfx950 without release/acquire cache maintenance:
+//  * agent-scope atomic stores and loads are issued with the system-coherent
+//    cache policy: a store is written through the issuing XCD's L2 to the
+//    memory-side coherence point and a load is not served from a (possibly
+//    stale) L2 line, so partials are visible to every XCD once they land;
+//  * the wave counter vmcnt counts stores as well as loads on this GPU, and
+//    a store leaves it only when the coherence point has acknowledged it, so
+//    s_waitcnt vmcnt(0) in every thread means every partial of the block has
+//    landed;
+//  * the workgroup barrier after that wait (with its workgroup-scope fences,
+//    which also keep the compiler from moving the atomic stores past it)
+//    makes thread 0's ticket fetch_add happen after all of the block's
+//    partials landed; the fetch_add is itself performed at the coherence
+//    point, so a block that sees count == blocks - 1 runs after every other
+//    block's partials landed, and its atomic loads see them.
+// The C++/HIP memory model by itself promises this only with a release on
+// the ticket and an acquire in the last block; on this GPU those lower to an
+// L2 write-back and invalidate per block (buffer_wbl2 / buffer_inv), which
+// made a one-launch column sum of 16 MB take 64 us instead of 7.4 us.  The
+// pattern is therefore tied to gfx950 (the #error above), and a GPU test
+// repeats each such kernel hundreds of times, comparing results bit for bit.
+__device__ __forceinline__ void wait_stores_landed() { __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); }
+
 // Butterfly sum over the 64 lanes of a wave; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -149,6 +201,17 @@ __device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {  // a in the 
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(cvt_f32x2{a, b}, cvt_bf16x2));
 }
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
+// f32 -> IEEE half, round to nearest even (v_cvt_f16_f32), from a value
+// that has been rounded to fp32 first.  The empty asm makes the fp32 value
+// opaque: otherwise the compiler folds the producing multiply or add into a
+// mixed-precision v_fma_mixlo_f16 (a * b + 0 straight to half), which rounds
+// once instead of twice and turns a -0 product into +0 (found by the GPU
+// test of the Float16 leaky ReLU on -0.0).
+__device__ __forceinline__ _Float16 f32_to_f16(float v) {
+    __asm__("" : "+v"(v));
+    return (_Float16)v;
+}
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return __uint_as_float(((uint32_t)h) << 16);

@@ -26,6 +26,8 @@ template <>
 __device__ __forceinline__ float ldf<float>(const float* p, int64_t i) { return p[i]; }
 template <>
 __device__ __forceinline__ float ldf<uint16_t>(const uint16_t* p, int64_t i) { return tfd::bf16_to_f32(p[i]); }
+template <>
+__device__ __forceinline__ float ldf<_Float16>(const _Float16* p, int64_t i) { return (float)p[i]; }
 
 template <typename T>
 __device__ __forceinline__ void stf(T* p, int64_t i, float v);
@@ -33,6 +35,10 @@ template <>
 __device__ __forceinline__ void stf<float>(float* p, int64_t i, float v) { p[i] = v; }
 template <>
 __device__ __forceinline__ void stf<uint16_t>(uint16_t* p, int64_t i, float v) { p[i] = tfd::f32_to_bf16(v); }
+// Half: round to nearest even (v_cvt_f16_f32), as __float2half in the
+// reference's typed col2im (cuda/kernels/col2im.cu:44).
+template <>
+__device__ __forceinline__ void stf<_Float16>(_Float16* p, int64_t i, float v) { p[i] = tfd::f32_to_f16(v); }
 
 template <typename T>
 __global__ void im2col_kernel(const T* __restrict__ x, T* __restrict__ col, ConvGeom g) {
@@ -1155,7 +1161,8 @@ tf_status tf_im2col(tf_ctx* ctx, const void* x, void* col, int64_t N, int64_t C,
     const int64_t total = N * C * kH * kW * g.outH * g.outW;
     if (total == 0) return TF_OK;
     TF_REQUIRE(x && col, "tf_im2col: null pointer");
-    TF_REQUIRE(dtype == TF_F32 || dtype == TF_BF16, "tf_im2col: dtype must be Float32 or BFloat16");
+    if (dtype != TF_F32 && dtype != TF_BF16 && dtype != TF_F16)
+        return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_im2col: dtype must be Float32, Float16 or BFloat16");
     const int64_t planes = N * C, sp = g.outH * g.outW, kk = kH * kW;
     if (H * W <= kPlaneLdsFloats && kk * sp <= (1LL << 30) && planes >= 256 && planes < (1LL << 31) &&
         plane_indices_fit(g)) {
@@ -1166,17 +1173,18 @@ tf_status tf_im2col(tf_ctx* ctx, const void* x, void* col, int64_t N, int64_t C,
         const size_t lds = (size_t)(H * W) * sizeof(float);
         if (dtype == TF_F32)
             im2col_plane_kernel<float><<<grid, 256, lds, ctx->stream>>>((const float*)x, (float*)col, g, rpb);
-        else
+        else if (dtype == TF_BF16)
             im2col_plane_kernel<uint16_t><<<grid, 256, lds, ctx->stream>>>((const uint16_t*)x, (uint16_t*)col, g, rpb);
+        else
+            im2col_plane_kernel<_Float16><<<grid, 256, lds, ctx->stream>>>((const _Float16*)x, (_Float16*)col, g, rpb);
         return tfh::check_launch("im2col_plane_kernel");
     }
-    if (dtype == TF_F32) {
+    if (dtype == TF_F32)
         im2col_kernel<float><<<tfd::grid_for(total, 4), 256, 0, ctx->stream>>>((const float*)x, (float*)col, g);
-    } else if (dtype == TF_BF16) {
+    else if (dtype == TF_BF16)
         im2col_kernel<uint16_t><<<tfd::grid_for(total, 4), 256, 0, ctx->stream>>>((const uint16_t*)x, (uint16_t*)col, g);
-    } else {
-        return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_im2col: dtype must be Float32 or BFloat16");
-    }
+    else
+        im2col_kernel<_Float16><<<tfd::grid_for(total, 4), 256, 0, ctx->stream>>>((const _Float16*)x, (_Float16*)col, g);
     return tfh::check_launch("im2col_kernel");
 }
 
@@ -1192,25 +1200,28 @@ tf_status tf_col2im(tf_ctx* ctx, const void* col, void* dx, int64_t N, int64_t C
     const int64_t total = N * C * H * W;
     if (total == 0) return TF_OK;
     TF_REQUIRE(col && dx, "tf_col2im: null pointer");
-    TF_REQUIRE(dtype == TF_F32 || dtype == TF_BF16, "tf_col2im: dtype must be Float32 or BFloat16");
+    if (dtype != TF_F32 && dtype != TF_BF16 && dtype != TF_F16)
+        return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_col2im: dtype must be Float32, Float16 or BFloat16");
     const int64_t planes = N * C, n_col = kH * kW * g.outH * g.outW;
     if (n_col <= kPlaneLdsFloats && H * W < (1LL << 30) && planes >= 256 && planes < (1LL << 31) &&
         plane_indices_fit(g)) {
         const size_t lds = (size_t)n_col * sizeof(float);
         if (dtype == TF_F32)
             col2im_plane_kernel<float><<<(unsigned)planes, 256, lds, ctx->stream>>>((const float*)col, (float*)dx, g);
-        else
+        else if (dtype == TF_BF16)
             col2im_plane_kernel<uint16_t><<<(unsigned)planes, 256, lds, ctx->stream>>>((const uint16_t*)col,
                                                                                      (uint16_t*)dx, g);
+        else
+            col2im_plane_kernel<_Float16><<<(unsigned)planes, 256, lds, ctx->stream>>>((const _Float16*)col,
+                                                                                     (_Float16*)dx, g);
         return tfh::check_launch("col2im_plane_kernel");
     }
-    if (dtype == TF_F32) {
+    if (dtype == TF_F32)
         col2im_kernel<float><<<tfd::grid_for(total, 2), 256, 0, ctx->stream>>>((const float*)col, (float*)dx, g);
-    } else if (dtype == TF_BF16) {
+    else if (dtype == TF_BF16)
         col2im_kernel<uint16_t><<<tfd::grid_for(total, 2), 256, 0, ctx->stream>>>((const uint16_t*)col, (uint16_t*)dx, g);
-    } else {
-        return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_col2im: dtype must be Float32 or BFloat16");
-    }
+    else
+        col2im_kernel<_Float16><<<tfd::grid_for(total, 2), 256, 0, ctx->stream>>>((const _Float16*)col, (_Float16*)dx, g);
     return tfh::check_launch("col2im_kernel");
 }
 

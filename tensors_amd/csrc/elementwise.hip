@@ -2,8 +2,9 @@
 // (ReLU / Sigmoid / Tanh), gradient accumulation (add), mul, scalar scale,
 // the fused SGD-momentum update and f32<->bf16 casts.
 //
-// Every kernel is a grid-stride loop over 16-byte vectors (4 x f32 or
-// 8 x bf16) with a scalar tail, 256 threads per block.  They are HBM-bound:
+// Every kernel is a grid-stride loop over 16-byte vectors (4 x f32, or
+// 8 x bf16 / f16) with a scalar tail, 256 threads per block; 16-bit types are
+// widened to f32 for the arithmetic and rounded once on the way out.  They are HBM-bound:
 // the algorithmic traffic per element is listed beside each one.  The
 // streaming kernels (activations, their backward, SGD) read and write their
 // vectors with non-temporal accesses (tfd::ld_nt / st_nt).
@@ -25,6 +26,13 @@ template <> struct Elem<float> {
 template <> struct Elem<uint16_t> {
     static __device__ __forceinline__ float ld(const uint16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
     static __device__ __forceinline__ void st(uint16_t* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+};
+// IEEE half: widened exactly (v_cvt_f32_f16), rounded to nearest even on
+// the way back (v_cvt_f16_f32 in the default round mode), as the
+// reference's __half2float / __float2half (cuda/kernels/elementwise.cu:42-64).
+template <> struct Elem<_Float16> {
+    static __device__ __forceinline__ float ld(const _Float16* p, int64_t i) { return (float)p[i]; }
+    static __device__ __forceinline__ void st(_Float16* p, int64_t i, float v) { p[i] = tfd::f32_to_f16(v); }
 };
 
 // Number of scalars in a 16-byte vector.
@@ -154,8 +162,11 @@ tf_status launch_binary(tf_ctx* ctx, const void* a, const void* b, void* out, in
     } else if (dtype == TF_BF16) {
         binary_kernel<uint16_t, Op><<<tfd::grid_for(n, 8 * kUnroll), 256, 0, ctx->stream>>>(
             (const uint16_t*)a, (const uint16_t*)b, (uint16_t*)out, n, op, vec_ok);
+    } else if (dtype == TF_F16) {
+        binary_kernel<_Float16, Op><<<tfd::grid_for(n, 8 * kUnroll), 256, 0, ctx->stream>>>(
+            (const _Float16*)a, (const _Float16*)b, (_Float16*)out, n, op, vec_ok);
     } else {
-        return tfh::set_error(TF_ERR_UNSUPPORTED, std::string(name) + ": dtype must be Float32 or BFloat16");
+        return tfh::set_error(TF_ERR_UNSUPPORTED, std::string(name) + ": dtype must be Float32, Float16 or BFloat16");
     }
     return tfh::check_launch(name);
 }
@@ -173,8 +184,11 @@ tf_status launch_unary(tf_ctx* ctx, const void* x, void* y, int64_t n, int dtype
     } else if (dtype == TF_BF16) {
         unary_kernel<uint16_t, Op><<<tfd::grid_for(n, 8 * kUnroll), 256, 0, ctx->stream>>>(
             (const uint16_t*)x, (uint16_t*)y, n, op, vec_ok);
+    } else if (dtype == TF_F16) {
+        unary_kernel<_Float16, Op><<<tfd::grid_for(n, 8 * kUnroll), 256, 0, ctx->stream>>>(
+            (const _Float16*)x, (_Float16*)y, n, op, vec_ok);
     } else {
-        return tfh::set_error(TF_ERR_UNSUPPORTED, std::string(name) + ": dtype must be Float32 or BFloat16");
+        return tfh::set_error(TF_ERR_UNSUPPORTED, std::string(name) + ": dtype must be Float32, Float16 or BFloat16");
     }
     return tfh::check_launch(name);
 }

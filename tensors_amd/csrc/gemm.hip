@@ -625,11 +625,8 @@ __device__ __forceinline__ uint32_t dl_wave_offset() {
 
 __device__ __forceinline__ int swz32(int row) { return (row >> 2) & 3; }
 
-// s_waitcnt immediate (gfx9 encoding) waiting for at most n outstanding
-// vector memory operations, leaving the other counters unconstrained.
-constexpr int waitcnt_vm(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
-// ... and for all outstanding LDS operations.
-constexpr int waitcnt_vm_lds(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0070; }
+using tfd::waitcnt_vm;
+using tfd::waitcnt_vm_lds;
 
 // Workgroup barrier for the direct-to-LDS pipeline: waits for this wave's
 // loads except the newest `outstanding` and for all of its LDS reads, then
@@ -2544,7 +2541,7 @@ __global__ __launch_bounds__(512) void gemm_f32_skinny_kernel(GemmParams p, int 
     }
     if (m < M && lane < N)
         __hip_atomic_store(p.partial + ((int64_t)c * M + m) * N + lane, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the partials have landed
+    tfd::wait_stores_landed();   // the partials have landed
     __syncthreads();
     if (threadIdx.x == 0)
         last = __hip_atomic_fetch_add(tickets + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -2729,6 +2726,24 @@ tf_status scratch_address(int device, float** out) {
     return TF_OK;
 }
 
+// Where a launch's cross-block partials go: the fixed scratch array for
+// tf_gemm_noalloc (rejected, with one message for every kernel path, when
+// they need more than it holds), else the context's pool-grown workspace.
+tf_status partials_buffer(tf_ctx* ctx, size_t need, bool noalloc, float** out) {
+    if (noalloc) {
+        if (need > kNoAllocScratchBytes)
+            return tfh::set_error(TF_ERR_INVALID,
+                                  "tf_gemm_noalloc: this shape's partial sums need " + std::to_string(need) +
+                                      " bytes, more than the fixed scratch of " +
+                                      std::to_string(kNoAllocScratchBytes) + " bytes (use tf_gemm)");
+        return scratch_address(ctx->device, out);
+    }
+    tf_status st = tfh::ensure_workspace(ctx, need);
+    if (st != TF_OK) return st;
+    *out = reinterpret_cast<float*>(ctx->ws);
+    return TF_OK;
+}
+
 // `noalloc`: split-K partials go to the fixed scratch array (no pool call).
 tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                     const void* A, int64_t lda, int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b,
@@ -2804,15 +2819,8 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
         TF_REQUIRE(chunks < 65536 && groups < 65536, "tf_gemm: skinny grid too large");
         if (chunks > 1) {
             const size_t need = (size_t)chunks * (size_t)M * (size_t)N * sizeof(float);
-            if (noalloc) {
-                if (need > kNoAllocScratchBytes) return tfh::set_error(TF_ERR_INVALID, "tf_gemm_noalloc: partials too large");
-                tf_status st = scratch_address(ctx->device, &p.partial);
-                if (st != TF_OK) return st;
-            } else {
-                tf_status st = tfh::ensure_workspace(ctx, need);
-                if (st != TF_OK) return st;
-                p.partial = reinterpret_cast<float*>(ctx->ws);
-            }
+            tf_status st = partials_buffer(ctx, need, noalloc, &p.partial);
+            if (st != TF_OK) return st;
         }
         gemm_f32_skinny_kernel<<<dim3((unsigned)chunks, (unsigned)groups), 512, 0, ctx->stream>>>(
             p, (int)chunks, ctx->tickets + tfh::kTicketGemm);
@@ -2833,15 +2841,8 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
         groups = (nkc + cps - 1) / cps;
         if (groups > 1) {
             const size_t need = (size_t)sm_tiles * (size_t)groups * kSmT * kSmT * sizeof(float);
-            if (noalloc) {
-                if (need > kNoAllocScratchBytes) return tfh::set_error(TF_ERR_INVALID, "tf_gemm_noalloc: partials too large");
-                tf_status st = scratch_address(ctx->device, &p.partial);
-                if (st != TF_OK) return st;
-            } else {
-                tf_status st = tfh::ensure_workspace(ctx, need);
-                if (st != TF_OK) return st;
-                p.partial = reinterpret_cast<float*>(ctx->ws);
-            }
+            tf_status st = partials_buffer(ctx, need, noalloc, &p.partial);
+            if (st != TF_OK) return st;
         }
         const dim3 grid((unsigned)(sm_tiles * groups));
         unsigned* tickets = ctx->tickets + tfh::kTicketGemm;
@@ -2920,20 +2921,9 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     }
 
     if (splits > 1) {
-        size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(float);
-        if (noalloc) {
-            if (need > kNoAllocScratchBytes)
-                return tfh::set_error(TF_ERR_INVALID,
-                                      "tf_gemm_noalloc: this shape's split-K partials need " + std::to_string(need) +
-                                          " bytes, more than the fixed scratch of " +
-                                          std::to_string(kNoAllocScratchBytes) + " bytes (use tf_gemm)");
-            tf_status st = scratch_address(ctx->device, &p.partial);
-            if (st != TF_OK) return st;
-        } else {
-            tf_status st = tfh::ensure_workspace(ctx, need);
-            if (st != TF_OK) return st;
-            p.partial = reinterpret_cast<float*>(ctx->ws);
-        }
+        const size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(float);
+        tf_status st = partials_buffer(ctx, need, noalloc, &p.partial);
+        if (st != TF_OK) return st;
     }
 
     tf_status st = TF_OK;

@@ -13,7 +13,8 @@
 // the workspace), frees go to a capture-local list that later allocations
 // of the same capture reuse, and synchronising calls or host copies are
 // errors.  The graph keeps the blocks freed during capture until it is
-// destroyed, so no other work is handed a replay's temporaries.
+// destroyed, and so are blocks allocated during capture that are freed while
+// the graph exists, so no other work is handed memory a replay writes.
 #include "common.hpp"
 
 #include <vector>
@@ -23,7 +24,9 @@ struct tf_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     void* ws = nullptr;                                // the context's workspace at capture
-    std::vector<std::pair<void*, size_t>> held;        // blocks freed during capture
+    // Blocks the graph keeps until it is destroyed: those freed during
+    // capture, and those allocated during capture and freed since.
+    std::vector<std::pair<void*, size_t>> held;
 };
 
 namespace {
@@ -74,6 +77,7 @@ tf_status tf_graph_begin(tf_ctx* ctx) {
     ctx->capturing = true;
     ctx->capture_failed = false;
     ctx->capture_free.clear();
+    ctx->capture_allocs.clear();
     return TF_OK;
 }
 
@@ -85,6 +89,7 @@ tf_status tf_graph_end(tf_ctx* ctx, tf_graph** out) {
     hipGraph_t graph = nullptr;
     const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
     std::vector<std::pair<void*, size_t>> held;
+    std::vector<void*> allocs;
     bool failed;
     {
         std::lock_guard<std::mutex> lock(ctx->cache_mu);
@@ -93,6 +98,7 @@ tf_status tf_graph_end(tf_ctx* ctx, tf_graph** out) {
         for (auto& kv : ctx->capture_free)
             for (void* p : kv.second) held.emplace_back(p, kv.first);
         ctx->capture_free.clear();
+        allocs.swap(ctx->capture_allocs);
         if (failed) {
             // Nothing was run: the blocks go back to the cache as they are.
             for (auto& b : held) {
@@ -127,6 +133,13 @@ tf_status tf_graph_end(tf_ctx* ctx, tf_graph** out) {
     g->exec = exec;
     g->ws = ctx->ws;
     g->held = std::move(held);
+    {
+        // Blocks allocated during capture and still live: a later free hands
+        // them to this graph (tf_hip_free) instead of the cache.
+        std::lock_guard<std::mutex> lock(ctx->cache_mu);
+        for (void* p : allocs)
+            if (ctx->live.count(p)) ctx->graph_owned[p] = &g->held;
+    }
     *out = g;
     return TF_OK;
 }
@@ -155,6 +168,9 @@ tf_status tf_graph_destroy(tf_graph* g) {
             ctx->cached[b.second].push_back(b.first);
             ctx->cached_bytes += b.second;
         }
+        // Its still-live blocks become ordinary ones again.
+        for (auto it = ctx->graph_owned.begin(); it != ctx->graph_owned.end();)
+            it = it->second == &g->held ? ctx->graph_owned.erase(it) : std::next(it);
     }
     delete g;
     if (e1 != hipSuccess) return tfh::hip_error(e1, "tf_graph_destroy: hipGraphExecDestroy");

@@ -253,7 +253,6 @@ constexpr int kLnStrip = 32;
 #define TF_LN_COL_BLOCKS 256
 #endif
 constexpr int kLnColBlocks = TF_LN_COL_BLOCKS;   // (strip, chunk) blocks aimed for
-constexpr int kWaitVm0 = 0x0F70;   // s_waitcnt vmcnt(0), other counters free
 
 template <int NC>
 __global__ __launch_bounds__(256) void ln_bwd_onepass_kernel(const float* __restrict__ dy, const float* __restrict__ x,
@@ -374,7 +373,7 @@ __global__ __launch_bounds__(256) void ln_bwd_onepass_kernel(const float* __rest
         }
     }
     if (chunks == 1) return;
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    tfd::wait_stores_landed();
     __syncthreads();
     if (threadIdx.x == 0)
         last = __hip_atomic_fetch_add(tickets + strip, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==

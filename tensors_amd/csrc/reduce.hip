@@ -90,7 +90,6 @@ constexpr int kTileU = 16;
 #define TF_COLSUM_BLOCKS 256
 #endif
 constexpr int kTileBlocks = TF_COLSUM_BLOCKS;   // (strip, chunk) blocks aimed for
-constexpr int kWaitVm0 = 0x0F70;   // s_waitcnt vmcnt(0), other counters free
 
 template <typename T>
 __global__ __launch_bounds__(256) void colsum_tile_kernel(const T* __restrict__ dy, float* __restrict__ db,
@@ -152,7 +151,7 @@ __global__ __launch_bounds__(256) void colsum_tile_kernel(const T* __restrict__ 
         }
     }
     if (chunks == 1) return;
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    tfd::wait_stores_landed();
     __syncthreads();
     if (threadIdx.x == 0)
         last = __hip_atomic_fetch_add(tickets + strip, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -273,7 +272,7 @@ __global__ __launch_bounds__(256) void relu_bwd_colsum_kernel(const T* __restric
         }
     }
     if (chunks == 1) return;
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    tfd::wait_stores_landed();
     __syncthreads();
     if (threadIdx.x == 0)
         last = __hip_atomic_fetch_add(tickets + strip, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==

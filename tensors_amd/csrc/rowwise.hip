@@ -15,8 +15,6 @@
 namespace {
 
 constexpr int kRowsPerBlock = 4;
-// s_waitcnt vmcnt(0) (expcnt and lgkmcnt not waited for) on gfx950.
-constexpr int kWaitVm0 = 0x0F70;
 constexpr int kMaxCached = 8;  // 2048 columns cached in registers
 
 __device__ __forceinline__ int col_of(int c, int lane, int q, bool vec) {
@@ -275,7 +273,7 @@ __global__ __launch_bounds__(256) void ce_kernel(const T* __restrict__ logits, c
                                    vec, nll_max, strict);
     if (MODE != 1 && ticket != nullptr) {
         __shared__ int last;
-        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        tfd::wait_stores_landed();
         __syncthreads();
         if (threadIdx.x == 0)
             last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;

@@ -213,6 +213,7 @@ tf_status tf_hip_shutdown(tf_ctx* ctx) {
         for (auto& kv : ctx->capture_free)
             for (void* p : kv.second) ctx->cached[kv.first].push_back(p);
         ctx->capture_free.clear();
+        ctx->capture_allocs.clear();
     }
     if (ctx->own_stream) {
         // Cached blocks go back to the pool once the current stream's work is done.
@@ -269,6 +270,7 @@ tf_status tf_hip_alloc(tf_ctx* ctx, size_t bytes, void** out) {
             *out = cf->second.back();
             cf->second.pop_back();
             ctx->live.emplace(*out, cls);
+            ctx->capture_allocs.push_back(*out);
             return TF_OK;
         }
     }
@@ -281,6 +283,7 @@ tf_status tf_hip_alloc(tf_ctx* ctx, size_t bytes, void** out) {
         it->second.pop_back();
         ctx->cached_bytes -= cls;
         ctx->live.emplace(*out, cls);
+        if (ctx->capturing) ctx->capture_allocs.push_back(*out);
         return TF_OK;
     }
     if (ctx->capturing) {
@@ -310,6 +313,11 @@ tf_status tf_hip_free(tf_ctx* ctx, void* ptr) {
     TF_REQUIRE(it != ctx->live.end(), "tf_hip_free: pointer not allocated by this context (or freed twice)");
     if (ctx->capturing) {
         ctx->capture_free[it->second].push_back(ptr);
+    } else if (auto g = ctx->graph_owned.find(ptr); g != ctx->graph_owned.end()) {
+        // Allocated while a graph was captured that still exists: its
+        // replays write this block, so the graph keeps it until destroyed.
+        g->second->emplace_back(ptr, it->second);
+        ctx->graph_owned.erase(g);
     } else {
         ctx->cached[it->second].push_back(ptr);
         ctx->cached_bytes += it->second;

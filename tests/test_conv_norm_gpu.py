@@ -99,6 +99,31 @@ def test_im2col_bitexact_and_col2im_adjoint(ctx, case):
     assert abs(lhs - rhs) <= 1e-4 * (abs(lhs) + 1.0)
 
 
+@pytest.mark.parametrize("case", [IM2COL_CASES[0], IM2COL_CASES[1], IM2COL_CASES[6], IM2COL_CASES[8],
+                                  IM2COL_CASES[12]])
+def test_im2col_col2im_float16(ctx, case):
+    # Float16, which the reference's im2col / col2im also take
+    # (cuda/kernels/im2col.cu:133-150, col2im.cu:163-185): im2col copies, so
+    # bit for bit; col2im sums the taps in fp32 in the element form's order
+    # and rounds once to f16 (to nearest even), so within one f16 step of the
+    # oracle's fp32 scatter rounded the same way.  Covers the plane forms,
+    # the element forms and the strided / dilated maps.
+    ops = _ops()
+    N, Cc, H, W, k, s, p, d = case
+    x16 = oracle.f32_to_f16_bits(synth.normal(231 + N * Cc, (N, Cc, H, W), std=3.0))
+    x = oracle.f16_bits_to_f32(x16)
+    col_ref = oracle.im2col(x, k, k, s, s, p, p, d, d)
+    col = ctx.empty(col_ref.shape, np.float16)
+    ops.im2col(ctx.array(x16.view(np.float16)), col, k, k, (s, s), (p, p), (d, d))
+    assert_bitexact(col.numpy().view(np.uint16), oracle.f32_to_f16_bits(col_ref), f"f16 im2col {case}")
+    c16 = oracle.f32_to_f16_bits(synth.normal(232 + N, col_ref.shape))
+    dx = ctx.empty(x.shape, np.float16)
+    ops.col2im(ctx.array(c16.view(np.float16)), dx, k, k, (s, s), (p, p), (d, d))
+    want = oracle.f16_bits_to_f32(oracle.f32_to_f16_bits(
+        oracle.col2im(oracle.f16_bits_to_f32(c16), x.shape, k, k, s, s, p, p, d, d)))
+    assert_close(dx.numpy().astype(np.float32), want, 2.0 ** -10, f"f16 col2im {case}")
+
+
 def _conv_bwd_gpu(ctx, x, w, gout, stride, pad, need_dx=True):
     """Conv2d backward from the C-ABI pieces, as the Conv2dModule backward node runs it."""
     from tensors_amd._lib import TF_EPI_NONE

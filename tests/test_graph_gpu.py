@@ -7,7 +7,8 @@ synchronisations between the replays, and every replay is checked bit for
 bit against the same calls run eagerly on the same inputs.  The capture's
 rules are checked from the host: a block-cache miss and a synchronising call
 during capture fail, the capture then yields no graph, and the context keeps
-working.
+working; a block allocated during capture and freed while its graph exists
+is not handed to other allocations.
 """
 from __future__ import annotations
 
@@ -102,3 +103,28 @@ def test_gather_and_record_in_a_replayed_graph(ctx):
         call("tf_graph_destroy", g)
     want = np.array([srcs[s % n].numpy()[0] for s in range(8)], np.float32)
     assert_bitexact(ring.numpy(), want, "recorded values")
+
+
+def test_block_allocated_during_capture_stays_with_its_graph(ctx):
+    # A size class no other test uses (2 MB steps above 1 MB: 38.1 MB -> 40 MB).
+    n = 10_000_000
+    x = ctx.array(synth.normal(1400, (n,)))
+    first = ctx.empty((n,))
+    first.free()                                   # the cache now holds one block of the class
+    call("tf_graph_begin", ctx.handle)
+    inside = ctx.empty((n,))                       # served from the cache during capture
+    ops.relu(x, inside)
+    g = _end(ctx)
+    try:
+        held = inside.ptr
+        inside.free()                              # freed while the graph exists
+        other = ctx.empty((n,))
+        assert other.ptr != held, "a block the graph writes was handed to another allocation"
+        call("tf_hip_fill_f32", ctx.handle, other.ptr, 5.0, n)
+        call("tf_graph_launch", ctx.handle, g)     # writes relu(x) into the held block
+        ctx.sync()
+        assert np.all(other.numpy() == 5.0), "a replay wrote into another allocation's memory"
+    finally:
+        call("tf_graph_destroy", g)
+    other.free()
+    ctx.sync()

@@ -627,6 +627,70 @@ def test_relu_bwd_bf16(ctx):
     assert_bitexact(d.numpy(), want, "relu_bwd bf16")
 
 
+# Float16 through the slots the reference's registry fills for Float16
+# (cuda/kernels/elementwise.cu:185-245: widen with __half2float, compute in
+# fp32, round with __float2half): the expected values are the oracle's fp32
+# loop on the widened inputs, rounded by the oracle's round-to-nearest-even.
+def _f16(x):
+    return oracle.f32_to_f16_bits(x)
+
+
+def _w16(h):
+    return oracle.f16_bits_to_f32(h)
+
+
+def _f16_inputs(seed, n, std=4.0):
+    h = _f16(synth.normal(seed, (n,), std=std))
+    if n >= 8:
+        h[:8] = [0x0000, 0x8000, 0x0001, 0x8001, 0x03FF, 0x7BFF, 0xFBFF, 0x3C00]   # +-0, subnormals, +-max, 1
+    return h
+
+
+@pytest.mark.parametrize("n", [1, 17, 4099, (1 << 20) + 5])
+def test_f16_add_mul_relu_leaky_bitexact(ctx, n):
+    ops = _ops()
+    a16, b16 = _f16_inputs(131, n), _f16_inputs(132, n)
+    if n >= 16:
+        b16[8:16] = [0x7BFF, 0x7BFF, 0x0001, 0x8001, 0x3C00, 0x3555, 0x7800, 0x0400]   # overflow, subnormal sums
+    a, b = _w16(a16), _w16(b16)
+    da, db = ctx.array(a16.view(np.float16)), ctx.array(b16.view(np.float16))
+    out = ctx.empty((n,), np.float16)
+    for name, fn, want in (("add", ops.add, oracle.add(a, b)), ("mul", ops.mul, a * b)):
+        fn(da, db, out)
+        assert_bitexact(out.numpy().view(np.uint16), _f16(want), f"f16 {name} n={n}")
+    ops.relu(da, out)
+    assert_bitexact(out.numpy().view(np.uint16), _f16(oracle.relu(a)), f"f16 relu n={n}")
+    ops.leaky_relu(da, out, 0.1)
+    assert_bitexact(out.numpy().view(np.uint16), _f16(oracle.leaky_relu(a, 0.1)), f"f16 leaky_relu n={n}")
+
+
+@pytest.mark.parametrize("n", [5, 4099, 1 << 20])
+def test_f16_sigmoid_tanh_and_backward(ctx, n):
+    # The device's expf / tanhf differ from the host's by a few fp32 ulp; after
+    # rounding to f16 that is at most one f16 step (2^-10 relative, 2^-24
+    # absolute near zero), so the bar is written in those units.
+    ops = _ops()
+    x16, dy16 = _f16_inputs(141, n), _f16_inputs(142, n, std=1.0)
+    x, dy = _w16(x16), _w16(dy16)
+    dx_, ddy = ctx.array(x16.view(np.float16)), ctx.array(dy16.view(np.float16))
+    out = ctx.empty((n,), np.float16)
+    rtol, atol = 2.0 ** -10, 2.0 ** -24
+    for name, fn, want in (("sigmoid", ops.sigmoid, oracle.sigmoid(x)), ("tanh", ops.tanh, oracle.tanh(x))):
+        fn(dx_, out)
+        assert_close(out.numpy().astype(np.float32), _w16(_f16(want)), rtol, f"f16 {name}", atol=atol)
+    # backward on f16 saved outputs: dy * y * (1 - y) and dy * (1 - y^2) may
+    # round differently in fp32 where the compiler fuses a multiply-add (as
+    # for fp32, where the bar is 1e-6), so within one f16 step; dy * [x > 0]
+    # is one exact selection, so bit for bit.
+    ys16, yt16 = _f16(oracle.sigmoid(x)), _f16(oracle.tanh(x))
+    for name, fn, y16, ref in (("sigmoid_bwd", ops.sigmoid_bwd, ys16, oracle.sigmoid_bwd),
+                               ("tanh_bwd", ops.tanh_bwd, yt16, oracle.tanh_bwd)):
+        fn(ddy, ctx.array(y16.view(np.float16)), out)
+        assert_close(out.numpy().astype(np.float32), _w16(_f16(ref(dy, _w16(y16)))), rtol, f"f16 {name}", atol=atol)
+    ops.relu_bwd(ddy, dx_, out)
+    assert_bitexact(out.numpy().view(np.uint16), _f16(oracle.relu_bwd(dy, x)), "f16 relu_bwd")
+
+
 # ---------------------------------------------------------------------------
 # cross entropy / softmax rows
 # ---------------------------------------------------------------------------

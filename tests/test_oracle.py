@@ -637,3 +637,76 @@ def test_ce_module_live_bits_and_clamp():
         oracle.ce_module(logits, bad)
     with pytest.raises(RuntimeError):
         oracle.ref_call("ref_ce_module", logits, bad, 64, 10, out)
+
+
+# ---------------------------------------------------------------------------
+# IEEE half conversions (the checker of the Float16 device paths)
+# ---------------------------------------------------------------------------
+def _f16_table():
+    """Every finite non-negative binary16 value as float64, from the format's
+    definition (not from any library): k * 2^-24 for subnormals,
+    2^(e-15) * (1 + m/1024) otherwise."""
+    h = np.arange(0x7C00, dtype=np.uint32)
+    e = (h >> 10).astype(np.int64)
+    m = (h & 0x3FF).astype(np.float64)
+    return np.where(e == 0, m * 2.0 ** -24, (1.0 + m / 1024.0) * np.exp2((e - 15).astype(np.float64)))
+
+
+def test_f16_to_f32_is_the_format_definition():
+    vals = _f16_table()
+    h = np.arange(0x7C00, dtype=np.uint16)
+    got = oracle.f16_bits_to_f32(h).astype(np.float64)
+    np.testing.assert_array_equal(got, vals)
+    np.testing.assert_array_equal(oracle.f16_bits_to_f32(h | 0x8000).astype(np.float64), -vals)
+    assert np.isposinf(oracle.f16_bits_to_f32(np.array([0x7C00], np.uint16)))[0]
+    assert np.isnan(oracle.f16_bits_to_f32(np.array([0x7E00, 0x7C01, 0xFE00], np.uint16))).all()
+    # numpy's own decode agrees for every pattern (NaNs as NaNs)
+    allh = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    a, b = oracle.f16_bits_to_f32(allh), allh.view(np.float16).astype(np.float32)
+    same = (a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))
+    assert same.all()
+
+
+def _nearest_even_by_brute_force(x):
+    """binary16 pattern of each float32 x by exhaustive nearest search over the
+    format's values (ties to the even pattern, overflow past the midpoint of
+    65504 and 2^16 to infinity); float64 holds every distance exactly."""
+    vals = np.append(_f16_table(), 65536.0)           # 65536: the pattern 0x7C00 (infinity)
+    ax = np.abs(x.astype(np.float64))
+    hi = np.clip(np.searchsorted(vals, ax, side="left"), 1, len(vals) - 1)
+    lo = hi - 1
+    dlo, dhi = ax - vals[lo], vals[hi] - ax
+    pick = np.where(dlo < dhi, lo, np.where(dhi < dlo, hi, np.where(lo % 2 == 0, lo, hi)))
+    pick = np.where(ax >= 65536.0, len(vals) - 1, pick)
+    return (pick.astype(np.uint32) | (np.signbit(x).astype(np.uint32) << 15)).astype(np.uint16)
+
+
+def test_f32_to_f16_rounds_to_nearest_even():
+    vals = _f16_table()
+    mids = (vals[:-1] + vals[1:]) / 2                  # every tie between neighbours
+    near = np.concatenate([mids, np.nextafter(mids.astype(np.float32), np.float32(np.inf)).astype(np.float64),
+                           np.nextafter(mids.astype(np.float32), np.float32(0)).astype(np.float64)])
+    rng = np.random.default_rng(0xF16)
+    rand = rng.standard_normal(200000) * np.exp2(rng.integers(-30, 18, 200000))
+    edges = np.array([0.0, 2.0 ** -25, 2.0 ** -25 * (1 + 2 ** -23), 2.0 ** -26, 2.0 ** -24 * 1.5, 65504.0,
+                      65519.99, 65520.0, 65535.0, 1e30, 1e-40])
+    x = np.concatenate([near, rand, edges]).astype(np.float32)
+    x = np.concatenate([x, -x])
+    # every tie is exactly representable in float32
+    assert np.array_equal(mids.astype(np.float32).astype(np.float64), mids)
+    got = oracle.f32_to_f16_bits(x)
+    assert_bitexact(got, _nearest_even_by_brute_force(x), "f32 -> f16 against brute force")
+    assert_bitexact(got, x.astype(np.float16).view(np.uint16), "f32 -> f16 against numpy")
+    assert (oracle.f32_to_f16_bits(np.array([np.inf, -np.inf], np.float32)) == [0x7C00, 0xFC00]).all()
+    assert np.isnan(oracle.f16_bits_to_f32(oracle.f32_to_f16_bits(np.array([np.nan], np.float32)))).all()
+
+
+def test_planted_f16_rounding_mistakes_are_caught():
+    # Truncation and ties-away-from-zero both disagree with the brute-force
+    # reference on the tie set, so the check above would catch either.
+    vals = _f16_table()
+    mids = ((vals[:-1] + vals[1:]) / 2).astype(np.float32)
+    want = _nearest_even_by_brute_force(mids)
+    trunc = np.searchsorted(vals, mids.astype(np.float64), side="right").astype(np.uint16) - 1
+    away = trunc + 1
+    assert (trunc != want).any() and (away != want).any()

@@ -1,8 +1,10 @@
 """tf_gemm_noalloc (the GEMM entry point that allocates nothing) against
 tf_gemm through the C ABI: the same kernels and split choices, so the outputs
 must be bit-identical.  Two calls in a row on the shared scratch array, the
-second smaller than the first, then a shape whose split-K partials exceed
-the fixed scratch, which must be rejected without touching the output."""
+second smaller than the first, products that use no partials at all, then
+shapes whose partials exceed the fixed scratch on the tiled split-K path and
+on the narrow-output path, which must be rejected without touching the
+output."""
 from __future__ import annotations
 
 import ctypes as C
@@ -50,11 +52,24 @@ def test_gemm_noalloc_matches_tf_gemm(ctx):
     wf = ctx.array(synth.normal(9103, (10, 16384), std=0.01))
     ref, got = _pair(ctx, x, wf, (128, 10), np.float32, False, True)
     assert_bitexact(got, ref, "fp32 128x10x16384 split-K")
-    # 3) a GEMM without split (no scratch involved) is unchanged too.
+    # 3) a small fp32 product (40 tiles of 32 x 32): its four K chunk groups
+    #    add their partials through the scratch too (gemm_f32_small_kernel).
     p = ctx.array(synth.normal(9104, (300, 200)))
     q = ctx.array(synth.normal(9105, (200, 100)))
     ref, got = _pair(ctx, p, q, (300, 100), np.float32, False, False, relu=True, bias=ctx.array(synth.normal(9106, (100,))))
     assert_bitexact(got, ref, "fp32 300x100x200")
+    # 4) products without any partials (one tile per CU or more, no split):
+    #    bf16 4096 x 4096 x 512 (256 tiles of 256 x 256) and config 2's
+    #    fp32 2048^3 (256 tiles of 128 x 128).
+    a = ctx.array(ta.f32_to_bf16_bits(rng.standard_normal((4096, 512), dtype=np.float32)), ta.BF16)
+    b = ctx.array(ta.f32_to_bf16_bits(rng.standard_normal((4096, 512), dtype=np.float32)), ta.BF16)
+    ref, got = _pair(ctx, a, b, (4096, 4096), np.float32, False, True)
+    assert_bitexact(got, ref, "bf16 4096x4096x512 (no split)")
+    del a, b
+    x2 = ctx.array(synth.normal(9107, (2048, 2048)))
+    w2 = ctx.array(synth.normal(9108, (2048, 2048)))
+    ref, got = _pair(ctx, x2, w2, (2048, 2048), np.float32, False, False)
+    assert_bitexact(got, ref, "fp32 2048^3 (no split)")
     ctx.sync()
 
 
@@ -71,4 +86,21 @@ def test_gemm_noalloc_rejects_partials_beyond_scratch(ctx):
     # tf_gemm takes the same shape (its workspace grows from the pool).
     _gemm(ctx, "tf_gemm", a, b, c, False, False)
     assert np.all(c.numpy() == 0.0)
+    ctx.sync()
+
+
+def test_gemm_noalloc_rejects_narrow_output_partials_beyond_scratch(ctx):
+    # The narrow-output fp32 path (<= 16 columns, K >= 2048): 32768 x 16 over
+    # K = 33792 is 33 chunks of 1024, whose partials need
+    # 33 * 32768 * 16 * 4 = 69.2 MB > 64 MiB.  Rejected before any launch, so
+    # the output keeps its contents; the operands are real allocations of
+    # the stated shapes all the same (A is 4.4 GB).
+    M, N, K = 32768, 16, 33792
+    a = ctx.zeros((M, K))
+    b = ctx.zeros((N, K))
+    c = ctx.array(np.full((M, N), 3.0, np.float32))
+    with pytest.raises(TFError, match="scratch"):
+        _gemm(ctx, "tf_gemm_noalloc", a, b, c, False, True)
+    assert np.all(c.numpy() == 3.0)
+    del a
     ctx.sync()
