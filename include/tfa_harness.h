@@ -49,6 +49,22 @@ int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t ste
                   int32_t reference_compat, int32_t bf16, const float* init_weights, float* losses,
                   float* final_weights, double* ms_per_step, uint64_t* pool_used, int32_t graph);
 
+/* One training step of tfa_mlp_train's MLP (biases on, zero at the start,
+ * as nn::Linear initialises them), keeping what the step stored, so that
+ * every GEMM and reduction of the step can be judged against float64 on the
+ * step's own operands.  x [batch][dims[0]] float32, y [batch] int64.
+ *   loss      out [1]
+ *   acts      out: the first layer's input as its GEMM read it (rounded to
+ *             bf16 in bf16 compute), then every layer's output (hidden
+ *             layers after their ReLU, then the logits): batch x dims[l] for
+ *             l = 0 .. ndims-1, concatenated, widened to float32 (exact)
+ *   grads     out: the gradient of every layer's output (Tensor::grad of the
+ *             intermediates, kept as in the reference), l = 1 .. ndims-1
+ *   final_weights, final_biases   NULL or out: parameters after the SGD step */
+int tfa_mlp_step_trace(const int32_t* dims, int32_t ndims, int64_t batch, const float* x, const int64_t* y, float lr,
+                       float mu, int32_t on_gpu, int32_t bf16, const float* init_weights, float* loss, float* acts,
+                       float* grads, float* final_weights, float* final_biases);
+
 /* CNN training (the config-4 network): Conv2dModule(3,32,3,1,1) - ReLU -
  * Conv2dModule(32,64,3,2,1) - ReLU - flatten - Linear(64*(H/2)*(W/2), 10) -
  * CrossEntropyLoss, optim::SGD.  xs [n_batches][batch][3][H][W]; init_params

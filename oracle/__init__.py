@@ -404,7 +404,7 @@ def _no_round(x):
     return np.ascontiguousarray(x, dtype=np.float32)
 
 
-def mlp_step_mixed(weights, biases, vels, bvels, x, labels, lr, mu, rounding=True):
+def mlp_step_mixed(weights, biases, vels, bvels, x, labels, lr, mu, rounding=True, trace=None):
     """One step of the mixed-precision MLP (config 5): bf16 operands and
     activations, float32 accumulation, float32 master weights.
 
@@ -426,7 +426,11 @@ def mlp_step_mixed(weights, biases, vels, bvels, x, labels, lr, mu, rounding=Tru
     leaves the float32 step (then equal to mlp_step up to summation order).
     Products run through numpy's float32 BLAS (float32 accumulation, in
     another order than the GPU).  weights/biases/vels/bvels are updated in
-    place (biases[l] may be None: no bias); returns the loss.
+    place (biases[l] may be None: no bias); returns the loss.  With `trace` a
+    dict, the step's stored tensors go into it: "w16" (working weights),
+    "acts" (the input and every layer's output), "dlogits", "dx" (each
+    layer's data gradient before the mask, layers 1 .. L-1), "dw" and "db"
+    (each layer's parameter gradients), all float32.
     """
     rnd = bf16_round if rounding else _no_round
     L = len(weights)
@@ -454,6 +458,8 @@ def mlp_step_mixed(weights, biases, vels, bvels, x, labels, lr, mu, rounding=Tru
     g[rows, labels] -= 1.0
     g /= N
     g = rnd(g.astype(np.float32))
+    if trace is not None:
+        trace.update(w16=w16, acts=acts, dlogits=g, dx=[None] * L, dw=[None] * L, db=[None] * L)
     f_lr, f_mu = np.float32(lr), np.float32(mu)
 
     def sgd(p, grad, v):
@@ -466,8 +472,12 @@ def mlp_step_mixed(weights, biases, vels, bvels, x, labels, lr, mu, rounding=Tru
     for li in range(L - 1, -1, -1):
         dw = (g.T @ acts[li]).astype(np.float32)
         db = g.astype(np.float64).sum(axis=0).astype(np.float32)
+        if trace is not None:
+            trace["dw"][li], trace["db"][li] = dw, db
         if li > 0:
             dh = rnd(g @ w16[li])
+            if trace is not None:
+                trace["dx"][li] = dh
             g = np.where(acts[li] > 0, dh, np.float32(0)).astype(np.float32)
         sgd(weights[li], dw, vels[li])
         if biases[li] is not None:

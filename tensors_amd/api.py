@@ -30,6 +30,8 @@ def _load() -> C.CDLL:
     p, i64, i32, f = C.c_void_p, C.c_int64, C.c_int32, C.c_float
     lib.tfa_mlp_train.argtypes = [p, i32, i64, i64, i64, i64, p, p, f, f, i32, i32, i32, p, p, p, p, p, i32]
     lib.tfa_mlp_train.restype = C.c_int
+    lib.tfa_mlp_step_trace.argtypes = [p, i32, i64, p, p, f, f, i32, i32, p, p, p, p, p, p]
+    lib.tfa_mlp_step_trace.restype = C.c_int
     lib.tfa_cnn_train.argtypes = [i64, i64, i64, i64, i64, i64, p, p, f, f, i32, p, p, p, p]
     lib.tfa_cnn_train.restype = C.c_int
     return lib
@@ -80,6 +82,41 @@ def mlp_train(dims, xs, ys, *, steps, lr, mu, on_gpu, reference_compat=False, bf
                              int(on_gpu), int(reference_compat), int(bf16), _ptr(iw), _ptr(losses), _ptr(fw),
                              C.byref(ms), _ptr(pool_trace), int(graph)))
     return losses, fw, ms.value
+
+
+def mlp_step_trace(dims, x, y, *, lr, mu, on_gpu, bf16=False, init_weights=None):
+    """One step of the MLP with biases (tfa_mlp_step_trace).  Returns
+    (loss, acts, grads, weights, biases): acts[l] is layer l's input as its
+    GEMM read it for l = 0 and layer l-1's output otherwise (l = 0 .. L),
+    grads[l - 1] the gradient of acts[l] (l = 1 .. L), weights / biases the
+    parameters after the SGD step; all float32 arrays."""
+    dims_a = np.ascontiguousarray(dims, dtype=np.int32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.ascontiguousarray(y, dtype=np.int64)
+    B = y.shape[0]
+    assert x.shape == (B, dims_a[0])
+    L = len(dims_a) - 1
+    acts = np.empty(B * int(dims_a.astype(np.int64).sum()), np.float32)
+    grads = np.empty(B * int(dims_a[1:].astype(np.int64).sum()), np.float32)
+    nw = int(sum(int(dims_a[i]) * int(dims_a[i + 1]) for i in range(L)))
+    fw, fb = np.empty(nw, np.float32), np.empty(int(dims_a[1:].astype(np.int64).sum()), np.float32)
+    iw = None if init_weights is None else np.ascontiguousarray(init_weights, dtype=np.float32)
+    loss = np.zeros(1, np.float32)
+    _check(lib.tfa_mlp_step_trace(_ptr(dims_a), len(dims_a), B, _ptr(x), _ptr(y), lr, mu, int(on_gpu), int(bf16),
+                                  _ptr(iw), _ptr(loss), _ptr(acts), _ptr(grads), _ptr(fw), _ptr(fb)))
+
+    def split(flat, rows_of, cols_of, n):
+        out, o = [], 0
+        for i in range(n):
+            k = rows_of(i) * cols_of(i)
+            out.append(flat[o:o + k].reshape(rows_of(i), cols_of(i)))
+            o += k
+        return out
+
+    d = [int(v) for v in dims_a]
+    return (float(loss[0]), split(acts, lambda i: B, lambda i: d[i], L + 1),
+            split(grads, lambda i: B, lambda i: d[i + 1], L),
+            split(fw, lambda i: d[i + 1], lambda i: d[i], L), split(fb, lambda i: d[i + 1], lambda i: 1, L))
 
 
 def cnn_train(xs, ys, *, steps, lr, mu, on_gpu, init_params=None, warmup=0, want_params=False):

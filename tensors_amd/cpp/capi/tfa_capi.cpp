@@ -916,6 +916,71 @@ int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t ste
     });
 }
 
+int tfa_mlp_step_trace(const int32_t* dims, int32_t ndims, int64_t batch, const float* x, const int64_t* y, float lr,
+                       float mu, int32_t on_gpu, int32_t bf16, const float* init_weights, float* loss, float* acts,
+                       float* grads, float* final_weights, float* final_biases) {
+    return guarded([&] {
+        if (ndims < 2 || batch <= 0) throw std::invalid_argument("tfa_mlp_step_trace: bad sizes");
+        if (bf16 && !on_gpu) throw std::invalid_argument("tfa_mlp_step_trace: bf16 needs the GPU");
+        CompatScope scope(false);
+        const Device d = dev_of(on_gpu);
+        std::vector<std::shared_ptr<nn::Linear>> layers;
+        size_t off = 0;
+        for (int32_t l = 0; l + 1 < ndims; ++l) {
+            auto fc = std::make_shared<nn::Linear>(dims[l], dims[l + 1]);
+            if (init_weights)
+                for (auto& np : fc->named_parameters())
+                    if (np.first == "weight")
+                        std::memcpy(np.second->data_.data(), init_weights + off, sizeof(float) * np.second->data_.numel());
+            off += static_cast<size_t>(dims[l]) * dims[l + 1];
+            fc->to(d);
+            if (bf16) fc->set_compute_dtype(Dtype::BFloat16);
+            layers.push_back(fc);
+        }
+        std::vector<Tensor*> params;
+        for (auto& fc : layers)
+            for (auto* p : fc->parameters()) params.push_back(&p->data_);
+        nn::optim::SGD opt(params, lr, mu);
+        nn::CrossEntropyLoss ce;
+        // The step of tfa_mlp_train, keeping every layer's output.
+        std::vector<Tensor> outs;
+        Tensor h = host_f32(x, Shape{batch, dims[0]}).to(d);
+        Tensor in = h;
+        for (size_t l = 0; l < layers.size(); ++l) {
+            h = l + 1 < layers.size() ? layers[l]->forward_relu(h) : layers[l]->forward(h);
+            outs.push_back(h);
+        }
+        Tensor lt = ce.forward(h, host_i64(y, Shape{batch}).to(d));
+        lt.backward();
+        opt.step();
+        *loss = to_host(lt)[0];
+        // The first layer's input as its GEMM read it (bf16 compute rounds it).
+        std::vector<float> a0 = to_host(bf16 ? in.to(Dtype::BFloat16) : in);
+        std::memcpy(acts, a0.data(), sizeof(float) * a0.size());
+        size_t ao = a0.size(), go = 0;
+        for (auto& t : outs) {
+            const std::vector<float> a = to_host(t), g = to_host(t.grad());
+            if (a.size() != g.size()) throw std::runtime_error("tfa_mlp_step_trace: a layer output has no gradient");
+            std::memcpy(acts + ao, a.data(), sizeof(float) * a.size());
+            std::memcpy(grads + go, g.data(), sizeof(float) * g.size());
+            ao += a.size();
+            go += g.size();
+        }
+        size_t wo = 0, bo = 0;
+        for (auto& fc : layers)
+            for (auto& np : fc->named_parameters()) {
+                const std::vector<float> v = to_host(np.second->data_);
+                if (np.first == "weight") {
+                    if (final_weights) std::memcpy(final_weights + wo, v.data(), sizeof(float) * v.size());
+                    wo += v.size();
+                } else {
+                    if (final_biases) std::memcpy(final_biases + bo, v.data(), sizeof(float) * v.size());
+                    bo += v.size();
+                }
+            }
+    });
+}
+
 int tfa_cnn_train(int64_t batch, int64_t H, int64_t W, int64_t steps, int64_t warmup, int64_t n_batches, const float* xs,
                   const int64_t* ys, float lr, float mu, int32_t on_gpu, const float* init_params, float* losses,
                   float* final_params, double* ms_per_step) {

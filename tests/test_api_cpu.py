@@ -69,3 +69,34 @@ def test_cpu_errors_are_reported():
     with pytest.raises(api.HarnessError, match="bf16"):
         api.mlp_train([784, 10], np.zeros((1, 2, 784), np.float32), np.zeros((1, 2), np.int64), steps=1, lr=0.1,
                       mu=0.0, on_gpu=False, bf16=True)
+
+
+def test_mlp_step_trace_on_cpu_matches_float64():
+    """tfa_mlp_step_trace on CPU tensors (fp32, reference loop order): the
+    stored outputs, gradients and updated parameters of one step of a small
+    MLP with biases against float64."""
+    dims, B = [20, 16, 12, 5], 9
+    rng = np.random.default_rng(77)
+    x = rng.standard_normal((B, dims[0])).astype(np.float32)
+    y = rng.integers(0, dims[-1], B).astype(np.int64)
+    w0 = [(rng.standard_normal((dims[i + 1], dims[i])) * 0.3).astype(np.float32) for i in range(3)]
+    loss, acts, grads, fw, fb = api.mlp_step_trace(dims, x, y, lr=1.0, mu=0.0, on_gpu=False,
+                                                   init_weights=np.concatenate([w.ravel() for w in w0]))
+    a = [x.astype(np.float64)]
+    for i in range(3):
+        z = a[-1] @ w0[i].T.astype(np.float64)
+        a.append(np.maximum(z, 0) if i < 2 else z)
+    for l in range(4):
+        np.testing.assert_allclose(acts[l], a[l], rtol=1e-5, atol=1e-6)
+    m = a[3].max(1, keepdims=True)
+    e = np.exp(a[3] - m)
+    p = e / e.sum(1, keepdims=True)
+    assert abs(loss - np.mean(-np.log(p[np.arange(B), y]))) < 1e-5
+    p[np.arange(B), y] -= 1
+    g = p / B
+    for l in range(3, 0, -1):
+        np.testing.assert_allclose(grads[l - 1], g, rtol=1e-4, atol=1e-7)
+        dz = g if l == 3 else g * (a[l] > 0)
+        np.testing.assert_allclose(w0[l - 1] - fw[l - 1], dz.T @ a[l - 1], rtol=1e-4, atol=1e-6)
+        np.testing.assert_allclose(-fb[l - 1].ravel(), dz.sum(0), rtol=1e-4, atol=1e-7)
+        g = dz @ w0[l - 1].astype(np.float64)

@@ -7,6 +7,11 @@ fp32 master weights, through the C++ API) is checked three ways:
     the GPU stores bf16), losses and weight updates within the bf16 bar;
   * the full 4096-8192-8192-4096-1000 step at batch 4096 against the same
     oracle run at full size (float32 BLAS on the host);
+  * the full step elementwise: every layer's output, weight gradient (on
+    sampled rows), whole bias gradient, data gradient and the logits'
+    gradient against float64 recomputed from the step's own stored bf16
+    operands (check_step_trace), so each GEMM and sum of the step is judged
+    at fp32 accuracy or one bf16 rounding, not by a norm;
   * every GEMM of the full step, at its exact shape, layout and epilogue,
     against float64 on sampled output rows.
 Config 4 (CNN, batch 128) runs a full-batch step against the reference-order
@@ -14,7 +19,9 @@ oracle step (the reference's own conv backward loop, restated).
 
 Bars: rtol 2e-2 for bf16 results, 1e-4 for fp32 results, atol = rtol * rms,
 elementwise wherever GPU and oracle see the same inputs (each GEMM, the
-losses).  A whole bf16 training step is judged per layer by the relative
+losses, the step trace, whose bf16 bar is one rounding).  Against the
+host-side oracle's own step, a whole bf16 training step is judged per layer
+by the relative
 Frobenius norm of the weight update (<= 2e-2): bf16 storage turns the
 different float32 summation orders of GPU and host into occasional
 one-ulp differences of logits and activations (0.4-0.8 %) and rare ReLU
@@ -128,6 +135,84 @@ def test_c5_full_size_step_matches_mixed_oracle(ctx):
         assert_rel_norm(g.astype(np.float64) - w0[i], w.astype(np.float64) - w0[i], RTOL16, f"layer {i} gradient")
 
 
+def check_step_trace(dims, B, bf16, seed):
+    """One step through the C++ API (tfa_mlp_step_trace: biases on, lr = 1,
+    mu = 0, so each parameter's change is its gradient), judged elementwise
+    against float64 computed from the step's own stored operands: each
+    layer's output on sampled rows, its weight gradient on sampled rows, its
+    whole bias gradient, the data gradient it passes down on sampled rows,
+    the logits' gradient and the loss.  Because the truth starts from the
+    same (bf16) operands the GPU multiplied, the GEMMs' and sums' own errors
+    are judged, not bf16 rounding chaos upstream:
+      * fp32 results (dW, db, and all of an fp32 step): rtol 1e-4,
+        atol = 1e-4 * rms;
+      * bf16 results (layer outputs, dX, dlogits): one rounding to bf16,
+        |err| <= 2^-8 |truth| (a bf16 step at most) + 1e-4 * rms."""
+    import tensors_amd as ta
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((B, dims[0]), dtype=np.float32)
+    y = rng.integers(0, dims[-1], B).astype(np.int64)
+    w0 = _mlp_init(dims, seed + 1)
+    init = np.concatenate([w.ravel() for w in w0])
+    loss, acts, grads, fw, fb = api.mlp_step_trace(dims, x, y, lr=1.0, mu=0.0, on_gpu=True, bf16=bf16,
+                                                   init_weights=init)
+    del init
+    L = len(dims) - 1
+    rnd = (lambda a: ta.bf16_bits_to_f32(ta.f32_to_bf16_bits(a))) if bf16 else (lambda a: a)
+
+    def close16(got, truth, what):
+        if not bf16:
+            assert_close(got, truth, RTOL32, what)
+            return
+        got, truth = np.asarray(got, np.float64), np.asarray(truth, np.float64)
+        atol = RTOL32 * np.sqrt(np.mean(truth ** 2))
+        bad = np.abs(got - truth) > 2.0 ** -8 * np.abs(truth) + atol
+        assert not bad.any(), f"{what}: {int(bad.sum())} of {bad.size} beyond one bf16 rounding"
+
+    if bf16:
+        np.testing.assert_array_equal(acts[0], rnd(x))           # the input as the first GEMM read it
+    else:
+        np.testing.assert_array_equal(acts[0], x)
+    # logits' gradient and the loss, from the stored logits
+    lg = acts[L].astype(np.float64)
+    m = lg.max(1, keepdims=True)
+    e = np.exp(lg - m)
+    lse = m[:, 0] + np.log(e.sum(1))
+    assert abs(loss - float(np.mean(lse - lg[np.arange(B), y]))) <= RTOL32 * abs(loss)
+    p_ = e / e.sum(1, keepdims=True)
+    p_[np.arange(B), y] -= 1.0
+    close16(grads[L - 1], p_ / B, "dlogits")
+    del lg, e, p_
+    for l in range(L, 0, -1):
+        i = l - 1
+        a_in = acts[i].astype(np.float64)
+        wq = rnd(w0[i]).astype(np.float64)                       # the weight as the GEMMs read it
+        dz = grads[l - 1] if l == L else np.where(acts[l] > 0, grads[l - 1], np.float32(0))
+        rows = np.unique(np.concatenate([[0, B - 1], _sample(B, 62, seed + 10 * l)]))
+        z = a_in[rows] @ wq.T
+        close16(acts[l][rows], np.maximum(z, 0.0) if l < L else z, f"layer {l} output, sampled rows")
+        orows = np.unique(np.concatenate([[0, dims[l] - 1], _sample(dims[l], 62, seed + 10 * l + 1)]))
+        dw = w0[i][orows].astype(np.float64) - fw[i][orows]
+        assert_close(dw, dz[:, orows].T.astype(np.float64) @ a_in, RTOL32, f"layer {l} dW, sampled rows")
+        assert_close(-fb[i].ravel(), dz.astype(np.float64).sum(0), RTOL32, f"layer {l} db")
+        if i >= 1:
+            close16(grads[i - 1][rows], dz[rows].astype(np.float64) @ wq, f"layer {l} dX, sampled rows")
+        del a_in, dz
+
+
+def test_c5_full_size_step_elementwise_vs_float64(ctx):
+    """Config 5's step at full size (4096-8192-8192-4096-1000, batch 4096,
+    bf16 compute, biases on): every GEMM output, weight and bias gradient of
+    the step elementwise against float64 of the step's own operands."""
+    check_step_trace(C5, 4096, True, 5300)
+
+
+def test_c2_like_fp32_step_elementwise_vs_float64(ctx):
+    """The same check on an fp32 step (one 2048 -> 2048 layer before a
+    2048 -> 10 output layer, batch 2048: config 2's Linear inside a step)."""
+    check_step_trace([2048, 2048, 10], 2048, False, 5310)
+
+
 # (M, N, K, trans_a, trans_b, out, epilogue) of every GEMM in the config-5
 # step: y = x W^T (+b, ReLU) in bf16, dX = dY W in bf16, dW = dY^T X in fp32.
 # Layer 1's dX is not computed (the input needs no gradient).
@@ -236,25 +321,55 @@ def _cnn_step64(params, x, y, keep=None):
     dw1 = np.einsum("nop,nkp->ok", dz1, col1).reshape(w1.shape)
     db1 = dz1.sum((0, 2))
     if keep is not None:
-        keep.update(col1=col1, z1=z1, col2=col2, z2=z2, dh2=dh2, dh1=dh1.reshape(z1.shape), w2=w2, h1_shape=h1.shape)
+        keep.update(col1=col1, z1=z1, col2=col2, z2=z2, dh2=dh2, dh1=dh1.reshape(z1.shape), w1=w1, b1=b1, w2=w2,
+                    b2=b2, h1_shape=h1.shape)
     return loss, [dw1, db1, dw2, db2, dwf, dbf]
 
 
-def _relu_tie_envelope(k, delta_rel=1e-4):
+U32 = 2.0 ** -24          # fp32 unit roundoff (round to nearest)
+
+
+def _gamma(n):
+    """gamma_n = n u / (1 - n u): the bound on the relative error of any fp32
+    evaluation of a sum of n + 1 terms (in any order and bracketing), relative
+    to the sum of the terms' magnitudes (Higham, Accuracy and Stability of
+    Numerical Algorithms, 2nd ed., section 3.1)."""
+    return n * U32 / (1.0 - n * U32)
+
+
+def _fp32_preactivation_bounds(k):
+    """Per pre-activation bound on |fp32 z - z| for any fp32 evaluation of the
+    two convolutions, from the error model above.  conv1: 27 products plus
+    the bias, e1 = gamma_28 (sum |w1| |x| + |b1|).  conv2 reads relu(z1)
+    computed in fp32, which is off by at most e1 at each tap (ReLU is
+    1-Lipschitz), and sums 288 products plus the bias:
+    e2 = gamma_289 (sum |w2| (|h1| + e1) + |b2|) + sum |w2| e1."""
+    w1a, w2a = np.abs(k["w1"].reshape(32, -1)), np.abs(k["w2"].reshape(64, -1))
+    e1 = _gamma(28) * (np.einsum("ok,nkp->nop", w1a, np.abs(k["col1"])) + np.abs(k["b1"])[None, :, None])
+    e1col, _, _ = _im2col64(e1.reshape(k["h1_shape"]), 3, 2, 1)
+    carried = np.einsum("ok,nkp->nop", w2a, e1col)
+    e2 = _gamma(289) * (np.einsum("ok,nkp->nop", w2a, np.abs(k["col2"]) + e1col)
+                        + np.abs(k["b2"])[None, :, None]) + carried
+    return e1, e2
+
+
+def _relu_tie_envelope(k):
     """Bound on how far an fp32 step's conv gradients may sit from the
-    float64 ones because a ReLU mask differs where the pre-activation is
-    within delta_rel * rms of zero (a tie: 2 M conv2 pre-activations here,
-    the smallest |z| ~ 5e-9, far below fp32's rounding of a 288-term sum).
-    Flipping the mask at (n, c, p) moves dz by dh there: db by |dh|, dW row
-    c by |dh| |col[n, :, p]|, and, for conv2, conv1's upstream gradient by
+    float64 ones because a ReLU mask differs: only where a pre-activation is
+    within its fp32 error bound of zero (_fp32_preactivation_bounds) can an
+    fp32 forward put it on the other side of zero from float64.  Flipping
+    the mask at (n, c, p) moves dz by dh there: db by |dh|, dW row c by
+    |dh| |col[n, :, p]|, and, for conv2, conv1's upstream gradient by
     |dh| |W2[c, :]| at that column's taps (then through conv1's mask into
-    its dW and db).  Returns per-element bounds for [dw1, db1, dw2, db2]."""
+    its dW and db).  Returns per-element bounds for [dw1, db1, dw2, db2] and
+    the numbers of such sites in conv1 and conv2."""
     col1, z1, col2, z2, dh2, dh1, w2 = (k[n] for n in ("col1", "z1", "col2", "z2", "dh2", "dh1", "w2"))
+    e1, e2 = _fp32_preactivation_bounds(k)
     env_dw1 = np.zeros((32, col1.shape[1]))
     env_db1 = np.zeros(32)
     env_dw2 = np.zeros((64, col2.shape[1]))
     env_db2 = np.zeros(64)
-    t2 = np.argwhere(np.abs(z2) < delta_rel * np.sqrt(np.mean(z2 ** 2)))
+    t2 = np.argwhere(np.abs(z2) <= e2)
     spread = np.zeros_like(col2)                  # |change of dcol2| from conv2's ties
     for n, c, p_ in t2:
         a = abs(dh2[n, c, p_])
@@ -265,7 +380,7 @@ def _relu_tie_envelope(k, delta_rel=1e-4):
         d1 = _col2im64(spread, k["h1_shape"], 3, 2, 1).reshape(z1.shape) * (z1 > 0)
         env_dw1 += np.einsum("nop,nkp->ok", d1, np.abs(col1))
         env_db1 += d1.sum((0, 2))
-    t1 = np.argwhere(np.abs(z1) < delta_rel * np.sqrt(np.mean(z1 ** 2)))
+    t1 = np.argwhere(np.abs(z1) <= e1)
     for n, c, p_ in t1:
         a = abs(dh1[n, c, p_])
         env_db1[c] += a
@@ -286,9 +401,10 @@ def test_c4_full_batch_step_vs_float64(ctx):
     gradients are judged against float64, as every other fp32 reduction.
     The conv gradients get, on top of rtol 1e-4, the bound that ReLU ties
     allow (_relu_tie_envelope): an fp32 forward may put a pre-activation
-    within ~1e-6 of zero on the other side from float64 (one such flip moves
-    a conv2 bias gradient by ~1e-3 of its rms), whichever kernel computes
-    the convolution."""
+    that lies within its fp32 error bound (gamma_K sum |w| |x|, per site) of
+    zero on the other side from float64 (one such flip moves a conv2 bias
+    gradient by ~1e-3 of its rms), whichever kernel computes the
+    convolution."""
     B, H = 128, 32
     xs = synth.normal(synth.seed(4, 0), (1, B, 3, H, H))
     ys = synth.uniform_int(synth.seed(4, 1), (1, B), 10)
@@ -305,7 +421,9 @@ def test_c4_full_batch_step_vs_float64(ctx):
     loss64, grads = _cnn_step64(params, xs[0], ys[0], keep)
     assert abs(float(losses[0]) - loss64) <= RTOL32 * max(1.0, abs(loss64))
     env, n_t1, n_t2 = _relu_tie_envelope(keep)
-    assert n_t1 + n_t2 < 2000, (n_t1, n_t2)       # ties are rare: the envelope stays tight
+    # sites within their fp32 bound of zero are rare among the 6.3 M
+    # pre-activations, so the envelope covers few gradient entries
+    assert n_t1 + n_t2 < 2000, (n_t1, n_t2)
     off = 0
     names = ["conv1.w", "conv1.b", "conv2.w", "conv2.b", "fc.w", "fc.b"]
     for i, (name, p0, g64) in enumerate(zip(names, params, grads)):

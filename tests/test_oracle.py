@@ -603,6 +603,86 @@ def test_mixed_step_rounding_changes_results_by_bf16_amounts():
     assert 0 < abs(l16 - l32) < 2e-2 * abs(l32)
 
 
+def _mixed_trace_problems(tr, bs, x, y):
+    """Where the stored tensors of a mixed step (oracle.mlp_step_mixed's
+    trace) break the rounding points of the bf16 compute path, judged from
+    the values alone against float64 recomputed from the trace's own inputs:
+    stored bf16 tensors (input, weights' working copies, layer outputs,
+    dlogits, data gradients) must be bf16 values within one rounding (half a
+    bf16 step) of their float64 value; fp32 gradients (dW, db) must be within
+    fp32 accumulation error of float64, which a bf16 rounding of them is not.
+    Returns a list of descriptions (empty: every point as specified)."""
+    probs = []
+    is16 = lambda a: np.array_equal(oracle.bf16_round(a), a)
+
+    def one_rounding(got, truth, what):
+        got, truth = np.asarray(got, np.float64), np.asarray(truth, np.float64)
+        if not is16(np.asarray(got, np.float32)):
+            probs.append(f"{what}: not bf16 values")
+        e = np.floor(np.log2(np.maximum(np.abs(truth), 1e-300)))
+        bound = np.exp2(e - 8) * (1 + 1e-3) + 1e-6 * np.sqrt(np.mean(truth ** 2))
+        if (np.abs(got - truth) > bound).any():
+            probs.append(f"{what}: beyond one bf16 rounding")
+
+    def fp32(got, truth, what):
+        truth = np.asarray(truth, np.float64)
+        if (np.abs(got - truth) > 1e-5 * (np.abs(truth) + np.sqrt(np.mean(truth ** 2)))).any():
+            probs.append(f"{what}: not within fp32 accumulation error")
+
+    acts, w16, L = tr["acts"], tr["w16"], len(tr["w16"])
+    one_rounding(acts[0], x, "input")
+    for i in range(L):
+        z = acts[i].astype(np.float64) @ w16[i].astype(np.float64).T + bs[i].astype(np.float64)
+        one_rounding(acts[i + 1], np.maximum(z, 0) if i + 1 < L else z, f"layer {i} output")
+    lg = acts[L].astype(np.float64)
+    e = np.exp(lg - lg.max(1, keepdims=True))
+    p = e / e.sum(1, keepdims=True)
+    p[np.arange(len(y)), y] -= 1
+    one_rounding(tr["dlogits"], p / len(y), "dlogits")
+    g = tr["dlogits"].astype(np.float64)
+    for i in range(L - 1, -1, -1):
+        fp32(tr["dw"][i], g.T @ acts[i].astype(np.float64), f"layer {i} dW")
+        fp32(tr["db"][i], g.sum(0), f"layer {i} db")
+        if i > 0:
+            one_rounding(tr["dx"][i], g @ w16[i].astype(np.float64), f"layer {i} dX")
+            g = np.where(acts[i] > 0, tr["dx"][i], 0.0).astype(np.float64)
+    return probs
+
+
+def test_mixed_step_rounding_points_are_pinned():
+    """The mixed oracle rounds to bf16 exactly where the GPU's bf16 step
+    stores bf16 tensors and nowhere else (the stored-tensor properties of
+    _mixed_trace_problems); planted mistakes in the oracle's output -- a
+    dropped rounding of the layer outputs or of dX, an extra rounding of dW,
+    db or of the pre-bias sum -- are each caught."""
+    dims = [64, 48, 40, 10]
+    ws, bs = _mixed_init(dims, 800, True)
+    bs = [b + np.float32(0.05) for b in bs]
+    x = synth.normal(801, (32, dims[0]))
+    y = synth.uniform_int(802, (32,), dims[-1])
+    tr = {}
+    oracle.mlp_step_mixed([w.copy() for w in ws], [b.copy() for b in bs], [np.zeros_like(w) for w in ws],
+                          [np.zeros_like(b) for b in bs], x, y, 0.1, 0.0, trace=tr)
+    assert _mixed_trace_problems(tr, bs, x, y) == []
+    rnd = oracle.bf16_round
+    planted = {
+        "dropped output rounding": dict(tr, acts=[tr["acts"][0]] + [
+            np.maximum(a.astype(np.float32) @ w.T + b, 0).astype(np.float32) if i + 1 < 3 else
+            (a.astype(np.float32) @ w.T + b).astype(np.float32)
+            for i, (a, w, b) in enumerate(zip(tr["acts"][:-1], tr["w16"], bs))]),
+        "dropped dX rounding": dict(tr, dx=[None] + [
+            (tr["dlogits"] if li == 2 else np.where(tr["acts"][li + 1] > 0, tr["dx"][li + 1], 0)).astype(np.float32)
+            @ tr["w16"][li] for li in (1, 2)]),
+        "rounded dW": dict(tr, dw=[rnd(d) for d in tr["dw"]]),
+        "rounded db": dict(tr, db=[rnd(d) for d in tr["db"]]),
+        "rounded pre-bias sum": dict(tr, acts=[tr["acts"][0]] + [
+            rnd(np.maximum(rnd(a @ w.T) + b, 0)) if i + 1 < 3 else rnd(rnd(a @ w.T) + b)
+            for i, (a, w, b) in enumerate(zip(tr["acts"][:-1], tr["w16"], bs))]),
+    }
+    for name, bad in planted.items():
+        assert _mixed_trace_problems(bad, bs, x, y), f"planted mistake not caught: {name}"
+
+
 @needs_ref
 def test_sum_dim_live_bits_and_float64():
     x = synth.normal(810, (37, 53))
