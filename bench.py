@@ -285,25 +285,104 @@ def hbm_ceiling() -> dict:
     return {"rows": rows}
 
 
-def bench_api_steps():
-    """Configs 1 and 4: whole training steps through the C++ API (host launch
-    work included)."""
+def bench_c1():
+    """Config 1: the MLP step through the C++ API (host launch work
+    included), eagerly and as a replayed HIP graph of the step."""
     from tensors_amd import api, synth
-    out = {}
     xs = synth.mnist_like(synth.seed(1, 0), (100, 64, 784))
     ys = synth.uniform_int(synth.seed(1, 1), (100, 64), 10)
     _, _, ms = api.mlp_train([784, 256, 128, 10], xs, ys, steps=100, warmup=10, lr=0.1, mu=0.9, on_gpu=True,
                              reference_compat=True)
-    out["c1_mlp_step_ms"] = round(ms, 4)
     # The same loop with its step captured once in a HIP graph and replayed
     # (batch selection and loss recording on the device).
-    _, _, ms = api.mlp_train([784, 256, 128, 10], xs, ys, steps=100, warmup=10, lr=0.1, mu=0.9, on_gpu=True,
-                             reference_compat=True, graph=1)
-    out["c1_mlp_step_ms_graph"] = round(ms, 4)
-    xs = synth.normal(synth.seed(4, 0), (1, 128, 3, 32, 32))
-    ys = synth.uniform_int(synth.seed(4, 1), (1, 128), 10)
-    _, ms = api.cnn_train(xs, ys, steps=23, warmup=3, lr=0.01, mu=0.9, on_gpu=True)
-    out["c4_cnn_step_ms"] = round(ms, 4)
+    _, _, ms_g = api.mlp_train([784, 256, 128, 10], xs, ys, steps=100, warmup=10, lr=0.1, mu=0.9, on_gpu=True,
+                               reference_compat=True, graph=1)
+    return {"workload": "C1 MLP 784-256-128-10 fp32, batch 64, Linear+ReLU, CE chain, SGD momentum (lr 0.1, "
+                        "mu 0.9), the reference's bias-free Linear; whole step through the C++ API",
+            "ms_per_step": round(ms, 4), "ms_per_step_graph": round(ms_g, 4),
+            "flop_per_step": C1_FLOP, "bound": "launch latency (16 dependent kernels of 2-10 us)"}
+
+
+# Config 4: the convolutions at batch 128 (N, Cin, H, Cout, stride); FLOP
+# and algorithmic bytes (each operand once) per launch.
+C4_B = 128
+C4_CONV1 = dict(cin=3, h=32, cout=32, stride=1, oh=32)
+C4_CONV2 = dict(cin=32, h=32, cout=64, stride=2, oh=16)
+
+
+def _conv_flop(c):
+    return 2 * C4_B * c["cout"] * c["oh"] ** 2 * c["cin"] * 9
+
+
+def _conv_bytes(c, kind):
+    x = C4_B * c["cin"] * c["h"] ** 2 * 4
+    y = C4_B * c["cout"] * c["oh"] ** 2 * 4
+    w = c["cout"] * c["cin"] * 9 * 4 + c["cout"] * 4
+    return x + y + w      # fwd: x, w, b in, y out; dW: x, dy in, dw, db out; dX: dy, w in, dx out
+
+
+C4_STEP_FLOP = 1476395008 + 2726297600     # fwd + bwd (conv1's data gradient is not needed)
+C1_FLOP = 30048256 + 34406400
+
+
+def bench_c4(reps: int = 40):
+    """Config 4: the CNN step through the C++ API, then its five convolution
+    launches at their batch-128 shapes (conv1 3 -> 32, 32 x 32, stride 1;
+    conv2 32 -> 64, stride 2; both 3 x 3, pad 1), `reps` event-timed
+    launches each over 4 buffer sets, each against its roofline: conv1
+    (27-deep products) against HBM, conv2 against fp32 MFMA."""
+    import tensors_amd as ta
+    from tensors_amd import api, ops, synth
+    xs = synth.normal(synth.seed(4, 0), (1, C4_B, 3, 32, 32))
+    ys = synth.uniform_int(synth.seed(4, 1), (1, C4_B), 10)
+    _, step_ms = api.cnn_train(xs, ys, steps=23, warmup=3, lr=0.01, mu=0.9, on_gpu=True)
+    events = _conv_events(reps)
+    kernels = {}
+    for name, us in events.items():
+        c = C4_CONV1 if name.startswith("conv1") else C4_CONV2
+        flop, nbytes = _conv_flop(c), _conv_bytes(c, name)
+        kernels[name] = {"us": us, "flop": flop, "tflops": round(flop / us / 1e6, 2),
+                         "frac_fp32": round(flop / us / 1e6 / PEAK_FP32_TFLOPS, 3), "bytes": nbytes,
+                         "gbps": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / PEAK_HBM_GBPS, 3),
+                         "bound": "hbm" if c is C4_CONV1 else "mfma"}
+    step_tf = C4_STEP_FLOP / (step_ms * 1e-3) / 1e12
+    return {"workload": "C4 CNN fp32, batch 128: Conv(3->32, 3x3, s1 p1)+ReLU, Conv(32->64, 3x3, s2 p1)+ReLU, "
+                        "flatten, Linear(16384->10), CE, SGD momentum (lr 0.01, mu 0.9); whole step through the "
+                        "C++ API",
+            "ms_per_step": round(step_ms, 4),
+            "roofline": {"bound": "mfma", "kernel": "whole step (4 convolution GEMMs + classifier), FLOP / step time",
+                         "achieved": round(step_tf, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(step_tf / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                         "algorithmic_flop_per_step": C4_STEP_FLOP},
+            "conv_kernels": kernels}
+
+
+def _conv_events(reps):
+    """Event-timed launches (us) of the five implicit convolution kernels at
+    their config-4 shapes, over 4 buffer sets."""
+    import tensors_amd as ta
+    from tensors_amd import ops, synth
+    ctx = ta.Context(0)
+    B, S = C4_B, 4
+    x1 = [ctx.array(synth.normal(synth.seed(7, i), (B, 3, 32, 32))) for i in range(S)]
+    h1 = [ctx.array(synth.normal(synth.seed(7, 10 + i), (B, 32, 32, 32))) for i in range(S)]
+    w1, b1 = ctx.array(synth.normal(synth.seed(7, 20), (32, 3, 3, 3), std=0.2)), ctx.zeros((32,))
+    w2, b2 = ctx.array(synth.normal(synth.seed(7, 21), (64, 32, 3, 3), std=0.06)), ctx.zeros((64,))
+    y1 = [ctx.empty((B, 32, 32, 32)) for _ in range(S)]
+    y2 = [ctx.empty((B, 64, 16, 16)) for _ in range(S)]
+    dy1 = [ctx.array(synth.normal(synth.seed(7, 30 + i), (B, 32, 32, 32))) for i in range(S)]
+    dy2 = [ctx.array(synth.normal(synth.seed(7, 40 + i), (B, 64, 16, 16))) for i in range(S)]
+    dh1 = [ctx.empty((B, 32, 32, 32)) for _ in range(S)]
+    gw1, gw2, gb1, gb2 = ctx.empty((32, 3, 3, 3)), ctx.empty((64, 32, 3, 3)), ctx.empty((32,)), ctx.empty((64,))
+    cases = {
+        "conv1_fwd": lambda i: ops.conv2d_fwd(x1[i], w1, y1[i], b1, (1, 1), (1, 1), (1, 1), True),
+        "conv2_fwd": lambda i: ops.conv2d_fwd(h1[i], w2, y2[i], b2, (2, 2), (1, 1), (1, 1), True),
+        "conv1_dw_db": lambda i: ops.conv2d_bwd_weight(x1[i], dy1[i], gw1, (1, 1), (1, 1), db=gb1),
+        "conv2_dw_db": lambda i: ops.conv2d_bwd_weight(h1[i], dy2[i], gw2, (2, 2), (1, 1), db=gb2),
+        "conv2_dx": lambda i: ops.conv2d_bwd_data(dy2[i], w2, dh1[i], (2, 2), (1, 1)),
+    }
+    out = {name: round(_rotating_bench(ctx, S, f, reps) * 1e3, 2) for name, f in cases.items()}
+    ctx.close()
     return out
 
 
@@ -481,6 +560,160 @@ def cpu_baseline_c2():
     }
 
 
+def _ref_seconds(name, *args):
+    """Mean seconds of one of oracle/_ref's timed runs (ref_time_*)."""
+    import ctypes as C
+    import oracle
+    sec = C.c_double(0.0)
+    oracle.ref_call(name, *args, C.byref(sec))
+    return sec.value
+
+
+def cpu_baseline_c1():
+    """The compiled reference's config-1 step: Linear(784,256)-ReLU-
+    Linear(256,128)-ReLU-Linear(128,10), the train_mlp cross-entropy chain,
+    loss.backward() and the manual momentum loop (examples/train_mlp.cpp:
+    54-76, 145-159), batch 64, through oracle/_ref's ref_mlp_train; 2 and 12
+    steps, the difference over 10 steps (the modules' construction cancels).
+    Without oracle/_ref: the C restatement of the same step."""
+    import oracle
+    from tensors_amd import synth
+    xs = synth.mnist_like(synth.seed(1, 0), (12, 64, 784))
+    ys = synth.uniform_int(synth.seed(1, 1), (12, 64), 10)
+    dims = np.array([784, 256, 128, 10], np.int32)
+    kind = "reference" if oracle.ref_available() else "port"
+    t = {}
+    for steps in (2, 12):
+        t0 = time.perf_counter()
+        if kind == "reference":
+            losses = np.empty(steps, np.float32)
+            oracle.ref_call("ref_mlp_train", xs, ys, steps, 64, 0.1, 0.9, losses, dims, 4, None)
+        else:
+            ws = [np.zeros((dims[i + 1], dims[i]), np.float32) + np.float32(0.01) for i in range(3)]
+            vs = [np.zeros_like(w) for w in ws]
+            for s_ in range(steps):
+                oracle.mlp_step(ws, vs, xs[s_], ys[s_], 0.1, 0.9)
+        t[steps] = time.perf_counter() - t0
+    model, ncpu = _host_info()
+    return {"value": round((t[12] - t[2]) / 10 * 1e3, 2), "unit": "ms/step", "cores": 1, "kind": kind,
+            "host": f"{model}, {ncpu} logical CPUs visible; the reference is single-threaded",
+            "sample": f"config-1 steps at batch 64: 12 steps {t[12]:.2f} s, 2 steps {t[2]:.2f} s; per step = "
+                      "the difference over 10 steps (fwd + loss.backward() + momentum loop)"}
+
+
+def cpu_baseline_c3():
+    """The compiled reference's backward nodes at config 3's shapes, each
+    timed alone (oracle/_ref ref_time_*, inputs and forward graphs built
+    outside the timed part): the whole train_mlp cross-entropy chain's
+    backward (loss.backward(), what the fused LogSoftmax+NLL kernel
+    replaces) and LogSoftmaxBackward::apply by itself at [4096 x 1024];
+    ReluBackward::apply at [4096 x 1024]; the LayerNorm backward through the
+    engine at [1024 x 1024] (the reference's stub, dX = dY * gamma), and the
+    true LayerNorm gradient's C restatement (oracle.layernorm_bwd), which
+    the GPU kernel computes.  Returns {c3 entry name: cpu_baseline}."""
+    import oracle
+    from tensors_amd import synth
+    model, ncpu = _host_info()
+    host = f"{model}, {ncpu} logical CPUs visible; the reference is single-threaded"
+    R, Cc = 4096, 1024
+    logits = synth.normal(synth.seed(3, 0), (R, Cc), std=3.0)
+    tg = synth.uniform_int(synth.seed(3, 1), (R,), Cc)
+    x = synth.normal(synth.seed(3, 2), (R, Cc))
+    dy = synth.normal(synth.seed(3, 3), (R, Cc))
+    L = 1024
+    lx, ldy = synth.normal(synth.seed(3, 4), (L, L)), synth.normal(synth.seed(3, 5), (L, L))
+    g, b = np.ones(L, np.float32), np.zeros(L, np.float32)
+    out = {}
+    if not oracle.ref_available():
+        return out
+    import ctypes as C
+    chain = _ref_seconds("ref_time_ce_chain_bwd", logits, tg, R, Cc, C.c_int32(3))
+    node = _ref_seconds("ref_time_log_softmax_bwd", logits, tg, R, Cc, C.c_int32(3))
+    out["c3a_logsoftmax_nll_bwd"] = {
+        "value": round(chain * 1e3, 2), "unit": "ms", "cores": 1, "kind": "reference", "host": host,
+        "sample": f"the cross-entropy chain's loss.backward() at [4096 x 1024], mean of 3 (LogSoftmaxBackward::apply "
+                  f"alone: {node * 1e3:.2f} ms)"}
+    relu = _ref_seconds("ref_time_relu_bwd", dy, x, R * Cc, C.c_int32(5))
+    out["c3b_relu_bwd"] = {"value": round(relu * 1e3, 2), "unit": "ms", "cores": 1, "kind": "reference",
+                           "host": host, "sample": "ReluBackward::apply at [4096 x 1024], mean of 5"}
+    stub = _ref_seconds("ref_time_layernorm_bwd", lx, g, b, ldy, L, L, 1e-5, C.c_int32(10))
+    _, mean, rstd = oracle.layernorm_fwd(lx, g, b)
+    t0 = time.perf_counter()
+    for _ in range(5):
+        oracle.layernorm_bwd(lx, ldy, g, mean, rstd)
+    true_ms = (time.perf_counter() - t0) / 5 * 1e3
+    out["c3c_layernorm_bwd"] = {
+        "value": round(stub * 1e3, 2), "unit": "ms", "cores": 1, "kind": "reference", "host": host,
+        "sample": f"the reference's LayerNorm backward (its stub, dX = dY * gamma) through the engine at "
+                  f"[1024 x 1024], mean of 10; the true gradient, which the GPU computes, in the C restatement: "
+                  f"{true_ms:.2f} ms"}
+    return out
+
+
+def cpu_baseline_c4():
+    """Config 4's step on the CPU, restated: the reference has no CPU
+    convolution backward.  The forward convolutions are the compiled
+    reference's Conv2dModule::forward (oracle/_ref ref_conv2d_fwd), the
+    backward convolutions the reference test's loop (nn/conv2d_backward_test
+    .cpp:50-106, restated in oracle.conv2d_bwd), the rest the restated
+    reference ops (oracle: ReLU, Linear, the CE chain, momentum SGD), all
+    single-threaded; batch 16 and 48 timed, extrapolated linearly to 128.
+    Labelled a port: its largest part, the backward loop, is the restated
+    one."""
+    import oracle
+    from tensors_amd import synth
+    ref = oracle.ref_available()
+    params = [synth.normal(synth.seed(4, 10 + i), s, std=sd) for i, (s, sd) in
+              enumerate(zip([(32, 3, 3, 3), (32,), (64, 32, 3, 3), (64,), (10, 16384), (10,)],
+                            [0.2, 0.1, 0.06, 0.1, 0.01, 0.1]))]
+    x_all = synth.normal(synth.seed(4, 0), (C4_B, 3, 32, 32))
+    y_all = synth.uniform_int(synth.seed(4, 1), (C4_B,), 10)
+
+    def conv_fwd(x, w, bb, stride):
+        if not ref:
+            return oracle.conv2d_fwd(x, w, bb, stride, 1)
+        N, Cin, H, _ = x.shape
+        Cout = w.shape[0]
+        oh = (H + 2 - 3) // stride + 1
+        yv = np.empty((N, Cout, oh, oh), np.float32)
+        oracle.ref_call("ref_conv2d_fwd", np.ascontiguousarray(x), w, bb, yv, N, Cin, H, H, Cout, 3, stride, 1)
+        return yv
+
+    t = {}
+    for B in (16, 48):
+        x, y = np.ascontiguousarray(x_all[:B]), y_all[:B].copy()
+        ps = [p.copy() for p in params]
+        vs = [np.zeros_like(p) for p in ps]
+        w1, b1, w2, b2, wf, bfc = ps
+        t0 = time.perf_counter()
+        z1 = conv_fwd(x, w1, b1, 1)
+        h1 = oracle.relu(z1)
+        z2 = conv_fwd(h1, w2, b2, 2)
+        h2 = oracle.relu(z2)
+        f = h2.reshape(B, -1)
+        logits = oracle.add(oracle.linear_fwd(f, wf), np.broadcast_to(bfc, (B, 10)))
+        _, gl = oracle.ce_chain(logits, y)
+        df, dwf = oracle.linear_bwd(f, wf, gl)
+        dbf = oracle.colsum(gl)
+        dz2 = oracle.relu_bwd(df.reshape(h2.shape), z2)
+        dh1, dw2, db2 = oracle.conv2d_bwd(h1, w2, dz2, (2, 2), (1, 1), (1, 1))
+        dz1 = oracle.relu_bwd(dh1, z1)
+        _, dw1, db1 = oracle.conv2d_bwd(x, w1, dz1, (1, 1), (1, 1), (1, 1))
+        for i, gr in enumerate((dw1, db1, dw2, db2, dwf, dbf)):
+            oracle.sgd_momentum(ps[i], gr, vs[i], 0.01, 0.9)
+        t[B] = time.perf_counter() - t0
+    slope = (t[48] - t[16]) / 32.0
+    fixed = max(t[16] - 16 * slope, 0.0)
+    model, ncpu = _host_info()
+    return {"value": round((fixed + slope * C4_B) * 1e3, 1), "unit": "ms/step", "cores": 1,
+            "kind": "port", "restated": True, "extrapolated": True,
+            "host": f"{model}, {ncpu} logical CPUs visible; single-threaded",
+            "sample": f"config-4 step at batch 16 and 48 ({t[16]:.2f} s, {t[48]:.2f} s), extrapolated linearly to "
+                      f"128; forward convolutions by {'the compiled reference' if ref else 'the C restatement of'} "
+                      f"Conv2dModule::forward, their "
+                      f"backward by the reference test's loop restated (the reference has no CPU conv backward)"}
+
+
 TRAFFIC_JSON = {"c2": ROOT / "profiles" / "gemm_f32_c2_traffic.json",
                 "c5": ROOT / "profiles" / "gemm_bf16_c5_traffic.json"}
 PROBE_CAL_N = 1 << 26      # calibration tf_add: reads 2 x 256 MB, writes 256 MB
@@ -588,35 +821,17 @@ def probe_bw() -> None:
 def probe_c4() -> None:
     """Launches for rocprofv3 runs of config 4: 13 API training steps (3
     warmup), then its five implicit-GEMM convolution launches at their C4
-    shapes (N 128; conv1 3 -> 32, 32 x 32, stride 1; conv2 32 -> 64, stride 2;
-    both 3 x 3, pad 1), 40 event-timed launches each over 4 buffer sets.
-    Prints the step time and the per-launch event timings (us) as one JSON
-    line."""
+    shapes, 40 event-timed launches each over 4 buffer sets (_conv_events),
+    then the calibration launches.  Prints the step time and the per-launch
+    event timings (us) as one JSON line."""
     import tensors_amd as ta
-    from tensors_amd import api, ops, synth
-    xs = synth.normal(synth.seed(4, 0), (1, 128, 3, 32, 32))
-    ys = synth.uniform_int(synth.seed(4, 1), (1, 128), 10)
+    from tensors_amd import api, synth
+    xs = synth.normal(synth.seed(4, 0), (1, C4_B, 3, 32, 32))
+    ys = synth.uniform_int(synth.seed(4, 1), (1, C4_B), 10)
     _, step_ms = api.cnn_train(xs, ys, steps=13, warmup=3, lr=0.01, mu=0.9, on_gpu=True)
+    out = _conv_events(40)
     ctx = ta.Context(0)
-    B, S = 128, 4
-    x1 = [ctx.array(synth.normal(synth.seed(7, i), (B, 3, 32, 32))) for i in range(S)]
-    h1 = [ctx.array(synth.normal(synth.seed(7, 10 + i), (B, 32, 32, 32))) for i in range(S)]
-    w1, b1 = ctx.array(synth.normal(synth.seed(7, 20), (32, 3, 3, 3), std=0.2)), ctx.zeros((32,))
-    w2, b2 = ctx.array(synth.normal(synth.seed(7, 21), (64, 32, 3, 3), std=0.06)), ctx.zeros((64,))
-    y1 = [ctx.empty((B, 32, 32, 32)) for _ in range(S)]
-    y2 = [ctx.empty((B, 64, 16, 16)) for _ in range(S)]
-    dy1 = [ctx.array(synth.normal(synth.seed(7, 30 + i), (B, 32, 32, 32))) for i in range(S)]
-    dy2 = [ctx.array(synth.normal(synth.seed(7, 40 + i), (B, 64, 16, 16))) for i in range(S)]
-    dh1 = [ctx.empty((B, 32, 32, 32)) for _ in range(S)]
-    gw1, gw2, gb1, gb2 = ctx.empty((32, 3, 3, 3)), ctx.empty((64, 32, 3, 3)), ctx.empty((32,)), ctx.empty((64,))
-    cases = {
-        "conv1_fwd": lambda i: ops.conv2d_fwd(x1[i], w1, y1[i], b1, (1, 1), (1, 1), (1, 1), True),
-        "conv2_fwd": lambda i: ops.conv2d_fwd(h1[i], w2, y2[i], b2, (2, 2), (1, 1), (1, 1), True),
-        "conv1_dw_db": lambda i: ops.conv2d_bwd_weight(x1[i], dy1[i], gw1, (1, 1), (1, 1), db=gb1),
-        "conv2_dw_db": lambda i: ops.conv2d_bwd_weight(h1[i], dy2[i], gw2, (2, 2), (1, 1), db=gb2),
-        "conv2_dx": lambda i: ops.conv2d_bwd_data(dy2[i], w2, dh1[i], (2, 2), (1, 1)),
-    }
-    out = {name: round(_rotating_bench(ctx, S, f, 40) * 1e3, 2) for name, f in cases.items()}
+    _probe_calibration(ctx)
     ctx.close()
     print(json.dumps({"c4_step_ms": round(step_ms, 4), "conv_events_us": out}), flush=True)
 
@@ -720,11 +935,17 @@ def main(argv=None):
     }
     if not args.only_headline:
         line["other_configs"] = {"c2": c2_report(100, 50), "c3": bench_c3(),
-                                 "bandwidth_rotated": bench_bandwidth_rotated(), **bench_api_steps()}
+                                 "bandwidth_rotated": bench_bandwidth_rotated(), "c1": bench_c1(),
+                                 "c4": bench_c4()}
     if rank == 0 and not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_c5()
         if "other_configs" in line:
-            line["other_configs"]["c2"]["cpu_baseline"] = cpu_baseline_c2()
+            oc = line["other_configs"]
+            oc["c2"]["cpu_baseline"] = cpu_baseline_c2()
+            oc["c1"]["cpu_baseline"] = cpu_baseline_c1()
+            for name, cb in cpu_baseline_c3().items():
+                oc["c3"][name]["cpu_baseline"] = cb
+            oc["c4"]["cpu_baseline"] = cpu_baseline_c4()
     if rank == 0:
         print(json.dumps(line), flush=True)
     return 0

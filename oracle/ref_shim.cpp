@@ -18,6 +18,7 @@
 #include "tensor/Tensor.hpp"
 #include "tensor/factory.hpp"
 
+#include <chrono>
 #include <cstdint>
 #include <cstring>
 #include <exception>
@@ -308,6 +309,95 @@ int ref_mlp_train(const float* xs, const int64_t* ys, int64_t steps, int64_t B, 
                 off += static_cast<size_t>(p->numel());
             }
         }
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Timed runs for bench.py's CPU baselines: each builds its inputs and graph
+// outside the timed part, runs the reference's operation `reps` times and
+// stores the mean wall seconds of the operation alone in *sec.
+// ---------------------------------------------------------------------------
+namespace {
+double seconds_since(std::chrono::steady_clock::time_point t0) {
+    return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+}
+}  // namespace
+
+// LogSoftmaxBackward::apply on y = log_softmax(logits) with the chain's
+// upstream gradient -onehot/N (autograd/ops/LogSoftmaxBackward.hpp:26-58).
+int ref_time_log_softmax_bwd(const float* logits, const int64_t* labels, int64_t R, int64_t C, int32_t reps,
+                             double* sec) {
+    return guarded([&] {
+        Tensor y = host_tensor(logits, Shape{R, C}).log_softmax(-1);
+        Tensor gy = zeros(Shape{R, C}, Dtype::Float32, Device::cpu());
+        float* gp = static_cast<float*>(gy.data());
+        for (int64_t r = 0; r < R; ++r)
+            if (labels[r] >= 0 && labels[r] < C) gp[r * C + labels[r]] = -1.0f / static_cast<float>(R);
+        double t = 0.0;
+        for (int32_t i = 0; i < reps; ++i) {
+            LogSoftmaxBackward node(y);
+            std::vector<Tensor> g{gy};
+            auto t0 = std::chrono::steady_clock::now();
+            Tensor gx = node.apply(std::move(g))[0];
+            t += seconds_since(t0);
+        }
+        *sec = t / reps;
+    });
+}
+
+// The whole backward of the train_mlp cross-entropy chain, loss.backward()
+// (examples/train_mlp.cpp:54-76); the forward chain is rebuilt untimed for
+// every repetition.
+int ref_time_ce_chain_bwd(const float* logits, const int64_t* labels, int64_t R, int64_t C, int32_t reps, double* sec) {
+    return guarded([&] {
+        Tensor lab = Tensor::empty(Shape{R}, Dtype::Int64, Device::cpu());
+        std::memcpy(lab.data(), labels, sizeof(int64_t) * R);
+        double t = 0.0;
+        for (int32_t i = 0; i < reps; ++i) {
+            Tensor tl = host_tensor(logits, Shape{R, C});
+            tl.requires_grad(true);
+            Tensor l = chain_cross_entropy(tl, lab);
+            auto t0 = std::chrono::steady_clock::now();
+            l.backward();
+            t += seconds_since(t0);
+        }
+        *sec = t / reps;
+    });
+}
+
+// ReluBackward::apply (autograd/ops/ReluBackward.hpp:22-32).
+int ref_time_relu_bwd(const float* dy, const float* x, int64_t n, int32_t reps, double* sec) {
+    return guarded([&] {
+        Tensor tx = host_tensor(x, Shape{n}), tdy = host_tensor(dy, Shape{n});
+        double t = 0.0;
+        for (int32_t i = 0; i < reps; ++i) {
+            ReluBackward node(tx);
+            std::vector<Tensor> g{tdy};
+            auto t0 = std::chrono::steady_clock::now();
+            Tensor dx = node.apply(std::move(g))[0];
+            t += seconds_since(t0);
+        }
+        *sec = t / reps;
+    });
+}
+
+// The backward of Tensor::layer_norm through the engine (its
+// LayerNormBackward stub, autograd/ops/LayerNormBackward.hpp:33-60); the
+// forward is rebuilt untimed for every repetition.
+int ref_time_layernorm_bwd(const float* x, const float* g, const float* b, const float* dy, int64_t R, int64_t C,
+                           float eps, int32_t reps, double* sec) {
+    return guarded([&] {
+        Tensor tg = host_tensor(g, Shape{C}), tb = host_tensor(b, Shape{C}), tdy = host_tensor(dy, Shape{R, C});
+        double t = 0.0;
+        for (int32_t i = 0; i < reps; ++i) {
+            Tensor tx = host_tensor(x, Shape{R, C});
+            tx.requires_grad(true);
+            Tensor y = tx.layer_norm(tg, tb, eps);
+            auto t0 = std::chrono::steady_clock::now();
+            run_backward(y, tdy);
+            t += seconds_since(t0);
+        }
+        *sec = t / reps;
     });
 }
 

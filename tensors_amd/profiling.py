@@ -68,6 +68,20 @@ BW_KERNELS = {
     # (bf16 [4096 x 8192]): dy, x read, dz written, db (fp32) written
     "relu_bwd_colsum_c5": ("relu_bwd_colsum_kernel<unsigned short>", 3 * C5_B * C5_DIMS[1] * 2 + C5_DIMS[1] * 4),
 }
+# Config 4's five implicit convolution launches (bench.py --probe c4):
+# label -> (kernel-name substring, algorithmic bytes per launch: each
+# operand read or written once).  conv1 (3 -> 32, 32 x 32, stride 1) and
+# conv2 (32 -> 64, stride 2), batch 128, 3 x 3, pad 1.
+_c4x1, _c4y1 = 128 * 3 * 32 * 32 * 4, 128 * 32 * 32 * 32 * 4
+_c4x2, _c4y2 = 128 * 32 * 32 * 32 * 4, 128 * 64 * 16 * 16 * 4
+_c4w1, _c4w2 = 32 * 27 * 4 + 32 * 4, 64 * 288 * 4 + 64 * 4
+C4_KERNELS = {
+    "conv1_fwd": ("conv_fwd_implicit_kernel<32>", _c4x1 + _c4y1 + _c4w1),
+    "conv2_fwd": ("conv_fwd_implicit_kernel<64>", _c4x2 + _c4y2 + _c4w2),
+    "conv1_dw_db": ("conv_bwd_weight_implicit_kernel<32>", _c4x1 + _c4y1 + _c4w1),
+    "conv2_dw_db": ("conv_bwd_weight_implicit_kernel<64>", _c4x2 + _c4y2 + _c4w2),
+    "conv2_dx": ("conv_bwd_data_lds_kernel", _c4x2 + _c4y2 + _c4w2),
+}
 # The streaming-ceiling row (bench.py --hbm-ceiling: mix, non-temporal,
 # MB per array) each kernel is read against: the mix of its reads and writes
 # at the nearest array size.
@@ -452,7 +466,7 @@ def main(argv=None) -> int:
     t.add_argument("--fetch", required=True)
     t.add_argument("--write", required=True)
     t.add_argument("--cal-n", type=int, default=1 << 26)
-    t.add_argument("--config", choices=["c2", "c5", "bw"], default="c2")
+    t.add_argument("--config", choices=["c2", "c4", "c5", "bw"], default="c2")
     t.add_argument("--json", required=True)
     t.add_argument("--cmd", required=True, nargs="+", help="the two rocprofv3 commands")
     b = sub.add_parser("bw-summary", help="markdown table of the bandwidth kernels (bench.py --probe bw)")
@@ -522,7 +536,8 @@ def main(argv=None) -> int:
         if a.config == "c5":
             res = traffic_c5(a.fetch, a.write, a.cal_n)
         else:
-            res = traffic(a.fetch, a.write, a.cal_n, BW_KERNELS if a.config == "bw" else None)
+            res = traffic(a.fetch, a.write, a.cal_n,
+                          {"bw": BW_KERNELS, "c4": C4_KERNELS}.get(a.config))
         res["commands"] = a.cmd
         Path(a.json).write_text(json.dumps(res, indent=2) + "\n")
         print(json.dumps(res, indent=2))
