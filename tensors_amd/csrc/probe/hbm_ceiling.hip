@@ -80,13 +80,53 @@ __global__ __launch_bounds__(256) void hbm_stream_kernel(const float4* __restric
     }
 }
 
+// A second, independent streaming form: persistent blocks (gridDim =
+// CUs x B), each owning one contiguous 1/gridDim of the arrays (split at
+// 256-vector granularity) and walking it with U 16-byte loads per input in
+// flight per thread before any arithmetic or store (U = 16 with one block
+// per CU, U = 8 with two).  It shares no loop shape with the elementwise
+// kernels, so a rate it reaches and they do not is a loss in those kernels.
+template <int NIN, int NOUT, bool NT, int U>
+__global__ __launch_bounds__(256) void hbm_persistent_kernel(const float4* __restrict__ a, const float4* __restrict__ b,
+                                                             const float4* __restrict__ c, float4* __restrict__ o0,
+                                                             float4* __restrict__ o1, int64_t nv) {
+    const int64_t groups = nv / 256;
+    const int64_t v0 = groups * blockIdx.x / gridDim.x * 256, v1 = groups * (blockIdx.x + 1) / gridDim.x * 256;
+    for (int64_t i = v0 + threadIdx.x; i < v1; i += (int64_t)U * 256) {
+        float4 va[U], vb[U], vc[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t j = i + u * 256 < v1 ? i + u * 256 : i;
+            va[u] = ld<NT>(a + j);
+            if constexpr (NIN > 1) vb[u] = ld<NT>(b + j);
+            if constexpr (NIN > 2) vc[u] = ld<NT>(c + j);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (i + u * 256 >= v1) break;
+            float4 r = va[u];
+            if constexpr (NIN > 1) r = add4(r, vb[u]);
+            if constexpr (NIN > 2) r = add4(r, vc[u]);
+            if constexpr (NOUT == 0) {
+                if (r.x + r.y + r.z + r.w == 1234.5f) o0[i + u * 256] = r;
+            } else {
+                st<NT>(o0 + i + u * 256, r);
+            }
+            if constexpr (NOUT > 1) st<NT>(o1 + i + u * 256, sub4(vb[u], vc[u]));
+        }
+    }
+}
+
 struct Mix {
     int nin, nout;
 };
 constexpr Mix kMixes[4] = {{1, 1}, {2, 1}, {3, 2}, {1, 0}};
 
+// form 0: the elementwise kernels' loop and grid; 1: the persistent form,
+// a block per CU (pgrid) with 16 loads per input in flight per thread; 2:
+// two blocks per CU with 8.
 template <int NIN, int NOUT>
-void launch_mix(bool nt, unsigned grid, float4** arr, int64_t nv, hipStream_t s) {
+void launch_mix(bool nt, int form, unsigned grid, unsigned pgrid, float4** arr, int64_t nv, hipStream_t s) {
     const float4* a = arr[0];
     const float4* b = NIN > 1 ? arr[1] : nullptr;
     const float4* c = NIN > 2 ? arr[2] : nullptr;
@@ -94,16 +134,24 @@ void launch_mix(bool nt, unsigned grid, float4** arr, int64_t nv, hipStream_t s)
     // for zero-filled data) would go to its input.
     float4* o0 = NOUT > 0 ? arr[NIN] : arr[0];
     float4* o1 = NOUT > 1 ? arr[NIN + 1] : nullptr;
-    if (nt) hbm_stream_kernel<NIN, NOUT, true><<<grid, 256, 0, s>>>(a, b, c, o0, o1, nv);
-    else hbm_stream_kernel<NIN, NOUT, false><<<grid, 256, 0, s>>>(a, b, c, o0, o1, nv);
+    if (form == 1) {
+        if (nt) hbm_persistent_kernel<NIN, NOUT, true, 16><<<pgrid, 256, 0, s>>>(a, b, c, o0, o1, nv);
+        else hbm_persistent_kernel<NIN, NOUT, false, 16><<<pgrid, 256, 0, s>>>(a, b, c, o0, o1, nv);
+    } else if (form == 2) {
+        if (nt) hbm_persistent_kernel<NIN, NOUT, true, 8><<<2 * pgrid, 256, 0, s>>>(a, b, c, o0, o1, nv);
+        else hbm_persistent_kernel<NIN, NOUT, false, 8><<<2 * pgrid, 256, 0, s>>>(a, b, c, o0, o1, nv);
+    } else {
+        if (nt) hbm_stream_kernel<NIN, NOUT, true><<<grid, 256, 0, s>>>(a, b, c, o0, o1, nv);
+        else hbm_stream_kernel<NIN, NOUT, false><<<grid, 256, 0, s>>>(a, b, c, o0, o1, nv);
+    }
 }
 
-void launch(int kind, bool nt, unsigned grid, float4** arr, int64_t nv, hipStream_t s) {
+void launch(int kind, bool nt, int form, unsigned grid, unsigned pgrid, float4** arr, int64_t nv, hipStream_t s) {
     switch (kind) {
-    case 0: launch_mix<1, 1>(nt, grid, arr, nv, s); break;
-    case 1: launch_mix<2, 1>(nt, grid, arr, nv, s); break;
-    case 2: launch_mix<3, 2>(nt, grid, arr, nv, s); break;
-    default: launch_mix<1, 0>(nt, grid, arr, nv, s); break;
+    case 0: launch_mix<1, 1>(nt, form, grid, pgrid, arr, nv, s); break;
+    case 1: launch_mix<2, 1>(nt, form, grid, pgrid, arr, nv, s); break;
+    case 2: launch_mix<3, 2>(nt, form, grid, pgrid, arr, nv, s); break;
+    default: launch_mix<1, 0>(nt, form, grid, pgrid, arr, nv, s); break;
     }
 }
 
@@ -113,20 +161,29 @@ extern "C" {
 
 // Average device time of one launch of mix `kind` (0 copy, 1 two reads + one
 // write, 2 three reads + two writes, 3 read only) over arrays of `bytes` bytes each
-// (rounded down to a multiple of 16 KiB), non-temporal when `nt` is set:
+// (rounded down to a multiple of 256 KiB), non-temporal when `nt` is set, in
+// streaming form `form` (0: the elementwise kernels' loop and grid, 1 / 2:
+// persistent blocks, one per CU with 16 loads per input in flight per
+// thread / two per CU with 8):
 // `reps` launches cycling over the buffer sets, timed with one event pair on
 // a stream of default priority after one untimed pass over every set.
 // Returns 0 on success, -1 for bad arguments, else the HIP error code.
-int tf_hbm_probe(int kind, int nt, int64_t bytes, int reps, double* us_per_launch) {
-    if (kind < 0 || kind > 3 || reps < 1 || us_per_launch == nullptr) return -1;
-    const int64_t nv = bytes / 16 / kChunk * kChunk;
+int tf_hbm_probe_form(int kind, int nt, int64_t bytes, int reps, int form, double* us_per_launch) {
+    if (kind < 0 || kind > 3 || reps < 1 || form < 0 || form > 2 || us_per_launch == nullptr) return -1;
+    const int64_t nv = bytes / 16 / (16 * kChunk) * (16 * kChunk);   // a whole number of form 2's steps too
     if (nv <= 0) return -1;
     const Mix m = kMixes[kind];
     const int per_set = m.nin + m.nout;
     const int64_t set_bytes = (int64_t)per_set * nv * 16;
     const int sets = (int)std::max<int64_t>(2, ((int64_t)1 << 30) / set_bytes + 1);
-    // One block per chunk up to 8192 blocks, as the elementwise kernels launch.
+    // One block per chunk up to 8192 blocks, as the elementwise kernels launch;
+    // the persistent forms: one or two blocks per CU.
     const unsigned grid = (unsigned)tfd::grid_for(nv, kUnroll);
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return -1;
+    const unsigned pgrid = (unsigned)cus;
 
     std::vector<float4*> bufs((size_t)sets * per_set, nullptr);
     hipStream_t s = nullptr;
@@ -153,10 +210,11 @@ int tf_hbm_probe(int kind, int nt, int64_t bytes, int reps, double* us_per_launc
     TF_PROBE_CHECK(hipStreamCreate(&s));
     TF_PROBE_CHECK(hipEventCreate(&e0));
     TF_PROBE_CHECK(hipEventCreate(&e1));
-    for (int i = 0; i < sets; ++i) launch(kind, nt != 0, grid, &bufs[(size_t)i * per_set], nv, s);
+    for (int i = 0; i < sets; ++i) launch(kind, nt != 0, form, grid, pgrid, &bufs[(size_t)i * per_set], nv, s);
     TF_PROBE_CHECK(hipGetLastError());
     TF_PROBE_CHECK(hipEventRecord(e0, s));
-    for (int r = 0; r < reps; ++r) launch(kind, nt != 0, grid, &bufs[(size_t)(r % sets) * per_set], nv, s);
+    for (int r = 0; r < reps; ++r)
+        launch(kind, nt != 0, form, grid, pgrid, &bufs[(size_t)(r % sets) * per_set], nv, s);
     TF_PROBE_CHECK(hipGetLastError());
     TF_PROBE_CHECK(hipEventRecord(e1, s));
     TF_PROBE_CHECK(hipEventSynchronize(e1));
@@ -168,11 +226,16 @@ int tf_hbm_probe(int kind, int nt, int64_t bytes, int reps, double* us_per_launc
     return 0;
 }
 
+// The elementwise kernels' form (form 0).
+int tf_hbm_probe(int kind, int nt, int64_t bytes, int reps, double* us_per_launch) {
+    return tf_hbm_probe_form(kind, nt, bytes, reps, 0, us_per_launch);
+}
+
 // Bytes one launch of `kind` moves for arrays of `bytes` bytes (after the
-// same rounding as tf_hbm_probe).
+// same rounding as tf_hbm_probe_form).
 int64_t tf_hbm_probe_bytes(int kind, int64_t bytes) {
     if (kind < 0 || kind > 3) return -1;
-    const int64_t nv = bytes / 16 / kChunk * kChunk;
+    const int64_t nv = bytes / 16 / (16 * kChunk) * (16 * kChunk);
     return (int64_t)(kMixes[kind].nin + kMixes[kind].nout) * nv * 16;
 }
 

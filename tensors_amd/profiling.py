@@ -413,8 +413,18 @@ def ceiling_table(ceiling_log: str | Path) -> str:
             cells = []
             for m in sizes:
                 r = next((r for r in rows if r["mix"] == mix and r["nt"] == nt and r["mb_per_array"] == m), None)
-                cells.append(f"{r['gbps'] / 1e3:.2f} TB/s ({r['us']:.1f} us)" if r else "")
+                if r is None:
+                    cells.append("")
+                    continue
+                cell = f"{r['gbps'] / 1e3:.2f} TB/s ({r['us']:.1f} us)"
+                if "gbps_by_form" in r:
+                    cell += " [" + " / ".join(f"{v / 1e3:.2f}" for v in r["gbps_by_form"].values()) + "]"
+                cells.append(cell)
             lines.append(f"| {mix} | {'non-temporal' if nt else 'cached'} | " + " | ".join(cells) + " |")
+    if rows and "gbps_by_form" in rows[0]:
+        lines.append("")
+        lines.append("Each cell: the best form's rate and time; in brackets the rate of every form, in the order "
+                     + ", ".join(rows[0]["gbps_by_form"]) + ".")
     return "\n".join(lines)
 
 

@@ -211,6 +211,9 @@ IMPLICIT_CASES = [
     (2, 6, 19, 23, 8, 5, 3, 2, 1),         # 5 x 5, stride 3
     (4, 7, 9, 9, 3, 1, 1, 0, 1),           # 1 x 1, odd K
     (1, 2, 40, 200, 33, 3, 1, 1, 1),       # output rows wider than a pixel tile
+    # few taps with stride, dilation and several 32-channel blocks
+    (5, 2, 15, 13, 20, 3, 2, 1, 2),        # K = 18, stride 2, dilation 2, a partial last pixel tile
+    (3, 1, 11, 9, 70, 5, 3, 2, 1),         # K = 25, stride 3, three channel blocks (32 + 32 + 6)
 ]
 
 
