@@ -893,9 +893,18 @@ def main(argv=None):
                     help="launch a config's kernels (bw: the bandwidth kernels) for a profiler, then exit")
     ap.add_argument("--hbm-ceiling", action="store_true",
                     help="run the HBM streaming-ceiling microbenchmark, print its JSON line, then exit")
+    ap.add_argument("--config", choices=["c1", "c2", "c3", "c4", "bw"],
+                    help="run only this entry of other_configs (as the full run measures it, without its CPU "
+                         "baseline), print it as one JSON line, then exit: the command a profiler wraps to "
+                         "reproduce that entry's figures")
     args = ap.parse_args(argv)
     if args.probe:
         {"c2": probe_c2, "c4": probe_c4, "c5": probe_c5, "bw": probe_bw}[args.probe]()
+        return 0
+    if args.config:
+        run = {"c1": bench_c1, "c2": lambda: c2_report(100, 50), "c3": bench_c3, "c4": bench_c4,
+               "bw": bench_bandwidth_rotated}[args.config]
+        print(json.dumps({"config": args.config, "report": run()}), flush=True)
         return 0
     if args.hbm_ceiling:
         print(json.dumps({"hbm_ceiling": hbm_ceiling()}), flush=True)

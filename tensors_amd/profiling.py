@@ -457,6 +457,53 @@ def bw_table(stats_csv: str | Path, traffic_json: str | Path, events_log: str | 
     return "\n".join(lines)
 
 
+def _stats_rows(stats_csv: str | Path) -> dict[str, tuple[int, float]]:
+    """kernel name -> (calls, average us) from a kernel_stats.csv."""
+    out = {}
+    with open(stats_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            out[_kname(r["Name"])] = (int(r["Calls"]), float(r["AverageNs"]) / 1e3)
+    return out
+
+
+C4_CONV_FLOP = {"conv1_fwd": 226492416, "conv2_fwd": 1207959552, "conv1_dw_db": 226492416,
+                "conv2_dw_db": 1207959552, "conv2_dx": 1207959552}
+
+
+def conv_table(stats_csv, traffic_json, mfma_csv, insts_csv, events_log) -> str:
+    """Config 4's five convolution kernels (bench.py --probe c4): trace
+    duration, event time, FLOP rate against fp32 MFMA, calibrated HBM bytes
+    against the algorithmic bytes, MFMA busy and instruction mix per MFMA."""
+    stats = _stats_rows(stats_csv)
+    tr = json.loads(Path(traffic_json).read_text())
+    ev = _json_line(events_log, "conv_events_us")
+    util = per_dispatch(mfma_csv, "MfmaUtil")
+    ins = {c: per_dispatch(insts_csv, c) for c in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS")}
+    avg = lambda v: sum(v) / len(v)
+    lines = ["| launch | kernel | trace avg us | event us | GFLOP | TF/s | of fp32 MFMA peak | HBM bytes (x algorithmic) "
+             "| GB/s | of 8 TB/s | MFMA busy | VALU / MFMA | LDS / MFMA |",
+             "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for label, (sub, algo) in C4_KERNELS.items():
+        name = next((n for n in stats if sub in n), None)
+        if name is None:
+            continue
+        calls, us = stats[name]
+        flop = C4_CONV_FLOP[label]
+        t = tr.get(label, {})
+        tb = t.get("traffic_bytes")
+        u = avg(_match(util, sub))
+        valu, mfma, lds = (avg(_match(ins[c], sub)) for c in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS"))
+        short = name.split("(")[0].replace("void ", "")
+        lines.append(f"| {label} | `{short}` | {us:.1f} | {ev.get(label, float('nan')):.1f} | {flop / 1e9:.3f} | "
+                     f"{flop / us / 1e6:.1f} | {flop / us / 1e6 / 157.3:.1%} | "
+                     f"{tb / 1e6:.1f} MB ({tb / algo:.2f}x) | {tb / us / 1e3:.0f} | {tb / us / 1e3 / 8000:.1%} | "
+                     f"{u:.1f} % | {(valu - mfma) / max(mfma, 1):.1f} | {lds / max(mfma, 1):.2f} |")
+    ps = next((n for n in stats if "conv_partial_sum_kernel" in n), None)
+    if ps:
+        lines.append(f"| weight-gradient partial sums | `conv_partial_sum_kernel` | {stats[ps][1]:.1f} | | | | | | | | | | |")
+    return "\n".join(lines)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(prog="python -m tensors_amd.profiling")
     sub = ap.add_subparsers(dest="action", required=True)
@@ -491,11 +538,31 @@ def main(argv=None) -> int:
     c.add_argument("--stats", help="kernel_stats.csv of a --kernel-trace run of the same command")
     c.add_argument("--cmd", required=True, nargs="+")
     c.add_argument("--out", required=True)
+    cs = sub.add_parser("conv-summary", help="config 4's convolution kernels (bench.py --probe c4)")
+    cs.add_argument("--stats", required=True, help="kernel_stats.csv of a --kernel-trace --stats run of --probe c4")
+    cs.add_argument("--traffic", required=True, help="the traffic JSON (--config c4)")
+    cs.add_argument("--mfma", required=True, help="counter CSV of a --pmc MfmaUtil run")
+    cs.add_argument("--insts", required=True, help="counter CSV of a --pmc SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS run")
+    cs.add_argument("--events", required=True, help="log of an unprofiled --probe c4 run")
+    cs.add_argument("--cmd", required=True, nargs="+")
+    cs.add_argument("--out", required=True)
     m = sub.add_parser("mfma-summary", help="MFMA busy per config-5 GEMM shape (bench.py --probe c5)")
     m.add_argument("--run", nargs=3, action="append", required=True, metavar=("LABEL", "PMC_CSV", "TRACE_CSV"))
     m.add_argument("--cmd", required=True, nargs="+")
     m.add_argument("--out", required=True)
     a = ap.parse_args(argv)
+    if a.action == "conv-summary":
+        cmds = "\n".join(a.cmd)
+        text = (f"# Config 4 (CNN, batch 128): the five convolution launches\n\nCommands (repo root):\n\n```\n{cmds}\n"
+                f"```\n\n{conv_table(a.stats, a.traffic, a.mfma, a.insts, a.events)}\n\nFLOP and algorithmic bytes per "
+                f"launch as in bench.py (each operand read or written once; conv1 is bound by HBM, conv2 by fp32 "
+                f"MFMA).  HBM bytes: FETCH_SIZE and WRITE_SIZE scaled by what they read for the probe's tf_add launches "
+                f"of known traffic.  "
+                f"VALU / MFMA: non-MFMA vector instructions per MFMA instruction (SQ_INSTS_VALU counts both).\n"
+                f"\nKernel trace of the same command:\n\n{stats_table(a.stats)}\n")
+        Path(a.out).write_text(text)
+        sys.stdout.write(text)
+        return 0
     if a.action == "mfma-summary":
         cmds = "\n".join(a.cmd)
         text = (f"# MFMA busy per config-5 GEMM shape (bf16 in, fp32 accumulate; 3 steps of GEMMs, averaged)\n\n"
