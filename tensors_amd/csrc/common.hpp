@@ -176,6 +176,37 @@ constexpr int waitcnt_vm_lds(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x00
 // repeats each such kernel hundreds of times, comparing results bit for bit.
 __device__ __forceinline__ void wait_stores_landed() { __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); }
 
+// Direct global -> LDS loads (buffer_load_dwordx4 ... lds).  One instruction
+// moves 16 bytes per active lane: lane l's bytes land at LDS byte M0 + 16 l,
+// so a wave fills one contiguous KB per instruction with no registers and no
+// LDS store instructions.  The loads count in vmcnt like any other load; the
+// caller waits for them (s_waitcnt vmcnt) before a barrier and the reads.
+// A lane offset at or past the descriptor's byte count reads zeros (raw
+// buffer range check), which is how padding is filled.
+typedef int buf_rsrc_t __attribute__((ext_vector_type(4)));
+constexpr uint32_t kBufOob = 0x80000000u;   // a lane offset past every descriptor's range
+// Descriptor for raw 16-byte loads of `bytes` bytes from `base` (gfx9-family
+// word 3: raw dword access).
+__device__ __forceinline__ buf_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return buf_rsrc_t{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), (int)bytes, 0x00020000};
+}
+// LDS byte address of a pointer into LDS.
+__device__ __forceinline__ uint32_t lds_byte_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)const_cast<void*>(p);
+}
+// One direct load: 16 bytes at byte offset voff of the descriptor's range
+// into LDS byte lds_chunk + 16 (lane).  lds_chunk is wave-uniform.  Inline
+// assembly so that the compiler's wait-count pass, which cannot track which
+// LDS bytes such a load writes, adds no waits of its own; M0 is written here
+// and used by nothing else in the kernels that call it.
+__device__ __forceinline__ void load16_to_lds(buf_rsrc_t rsrc, uint32_t voff, uint32_t lds_chunk) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_chunk), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
+
 // Butterfly sum over the 64 lanes of a wave; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -394,6 +394,47 @@ __device__ __forceinline__ void stage_patch(const float* __restrict__ xn, float*
     stage_slots(PatchSlots(xn, H, W, PH, PWs, L, ih_lo, 0, vec), patch, 0, C * PH * (PWs / 4));
 }
 
+// Direct-load staging: slots [0, n) of an LDS region at byte address lds0,
+// slot j's 16 bytes read from byte offset off(j) of `rsrc` (zeros for
+// tfd::kBufOob).  Wave w issues the 64-slot chunks w, w + 8, ...; every load
+// of the region is in flight at once.  The caller waits (vmcnt(0)) and
+// synchronises before reading.
+template <class Off>
+__device__ __forceinline__ void stage_direct(tfd::buf_rsrc_t rsrc, uint32_t lds0, int n, const Off& off) {
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+    for (int c = wave; c * 64 < n; c += kIgThreads / 64) {
+        const int j = c * 64 + lane;
+        if (j < n) tfd::load16_to_lds(rsrc, off(j), lds0 + (uint32_t)c * 1024u);
+    }
+}
+
+// Byte offset (from the image's first element) of patch slot j in the
+// aligned layout (PatchSlots), or tfd::kBufOob for a slot outside the image.
+struct PatchOff {
+    int H, W, PH, L, ih_lo;
+    FastDiv fspr, fPH;
+    __device__ __forceinline__ uint32_t operator()(int j) const {
+        int sl, rr;
+        const int row = divmod(j, fspr, sl);
+        const int ci = divmod(row, fPH, rr);
+        const int ih = ih_lo + rr, iw = 4 * sl - L;
+        return ih >= 0 && ih < H && iw >= 0 && iw < W ? 4u * (uint32_t)((ci * H + ih) * W + iw) : tfd::kBufOob;
+    }
+};
+
+// Byte offset of filter slot j of an LDS block [rows][RS words] (RS / 4
+// slots a row, the last of them padding) from `nrows` rows of K floats, or
+// tfd::kBufOob for padding and rows past nrows.
+struct RowOff {
+    int K, nrows;
+    FastDiv fspr;
+    __device__ __forceinline__ uint32_t operator()(int j) const {
+        int sl;
+        const int r = divmod(j, fspr, sl);
+        return r < nrows && 4 * sl < K ? 4u * (uint32_t)(r * K + 4 * sl) : tfd::kBufOob;
+    }
+};
+
 // acc += A (32 rows of wrow, k along the row) x B (32 pixels: pbase[koff[k]])
 // over KH2 k steps per lane half (KH2 a multiple of 4, >= 4), with the next
 // four steps' reads in flight during the current four MFMAs.
@@ -475,6 +516,46 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
     const int ih_lo = oh_lo * (int)g.sh - (int)g.ph;
     const int C = (int)g.C, H = (int)g.H, W = (int)g.W, kHW = (int)(g.kH * g.kW), kW = (int)g.kW;
     const int t = threadIdx.x;
+    const int wave = t >> 6, lane = t & 63, l32 = lane & 31, half = lane >> 5;
+    const int m_sub = wave % MSUB, n_sub = wave / MSUB;
+    const int pp = p0 + n_sub * 32 + l32;
+    int pix_off;
+    {
+        const int q = pp < p_end ? pp : p0;
+        const int oh = q / outW, ow = q - oh * outW;
+        pix_off = (oh - oh_lo) * (int)g.sh * PWs + ow * (int)g.sw + L - (int)g.pw;
+    }
+    const int KS = Kp / 8;                                  // k steps of 8
+    v16f acc;
+    if (vec & 4) {
+        // Direct loads (bit 2: aligned patch layout, 16-byte image rows):
+        // LDS = filter rows [MT][RS] | input patch | tap table, each of the
+        // first two regions rounded up to whole KB.  The patch and (when its
+        // rows are 16-byte loadable, bit 1) the filter go global -> LDS in one
+        // round trip; otherwise the filter is staged through registers while
+        // the patch loads are in flight.
+        float* wkd = smem;
+        float* patchd = smem + (MT * RS + 255) / 256 * 256;
+        int* koffd = reinterpret_cast<int*>(patchd + (C * PH * PWs + 255) / 256 * 256);
+        const float* xn = x + (int64_t)n * C * H * W;
+        const int nrows = min(MT, Cout - co0);
+        stage_direct(tfd::buf_rsrc(xn, (uint32_t)(C * H * W) * 4u), tfd::lds_byte_addr(patchd), C * PH * (PWs / 4),
+                     PatchOff{H, W, PH, L, ih_lo, fast_div(PWs / 4), fast_div(PH)});
+        if (vec & 2)
+            stage_direct(tfd::buf_rsrc(w + (int64_t)co0 * K, (uint32_t)(nrows * K) * 4u), tfd::lds_byte_addr(wkd),
+                         MT * (RS / 4), RowOff{K, nrows, fast_div(RS / 4)});
+        else
+            stage_slots(RowSlots(w + (int64_t)co0 * K, K, nrows, K, RS, 0, Kp / 4, false), wkd, 0, MT * (Kp / 4));
+        for (int k = t; k < Kp; k += kIgThreads) {
+            const int kc = min(k, K - 1);
+            const int ci = kc / kHW, rem = kc - ci * kHW, kh = rem / kW, kw = rem - kh * kW;
+            koffd[k] = (ci * PH + kh * (int)g.dh) * PWs + kw * (int)g.dw;
+        }
+        __builtin_amdgcn_s_waitcnt(tfd::waitcnt_vm(0));
+        __syncthreads();
+        acc = mfma_gather_steps(v16f{}, wkd + (m_sub * 32 + l32) * RS + 4 * half, koffd + 4 * half, patchd + pix_off,
+                                0, KS);
+    } else {
 
     // Two phases: the k steps whose taps lie in the first CA channels, then
     // the rest.  Phase A's filter columns and channels are staged first;
@@ -482,7 +563,6 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
     // stored to LDS after them, so their latency overlaps the arithmetic.
     // (A loop over four such phases measured slower: each phase adds a
     // barrier and a staging tail.)
-    const int KS = Kp / 8;                                  // k steps of 8
     const int KA8 = C >= 2 ? max(1, min(KS, ((C + 1) / 2) * kHW / 8)) : KS;
     const int CA = min(C, (8 * KA8 + kHW - 1) / kHW);       // channels phase A reads
     const int spr = PWs / 4;
@@ -505,18 +585,9 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
     ahead_p.load(p_b, n_pb);
     __syncthreads();
 
-    const int wave = t >> 6, lane = t & 63, l32 = lane & 31, half = lane >> 5;
-    const int m_sub = wave % MSUB, n_sub = wave / MSUB;
-    const int pp = p0 + n_sub * 32 + l32;
-    int pix_off;
-    {
-        const int q = pp < p_end ? pp : p0;
-        const int oh = q / outW, ow = q - oh * outW;
-        pix_off = (oh - oh_lo) * (int)g.sh * PWs + ow * (int)g.sw + L - (int)g.pw;
-    }
     const float* wrow = wk + (m_sub * 32 + l32) * RS + 4 * half;
     const int* krow = koff + 4 * half;
-    v16f acc = mfma_gather_steps(v16f{}, wrow, krow, patch + pix_off, 0, KA8);
+    acc = mfma_gather_steps(v16f{}, wrow, krow, patch + pix_off, 0, KA8);
     if (KA8 < KS) {
         ahead_w.store(wk, n_wb);
         stage_slots(w_b, wk, kAhead * kIgThreads, n_wb);
@@ -524,6 +595,7 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
         stage_slots(p_b, patch, kAhead * kIgThreads, n_pb);
         __syncthreads();
         acc = mfma_gather_steps(acc, wrow, krow, patch + pix_off, KA8, KS);
+    }
     }
 
     if (pp >= p_end) return;
@@ -1250,8 +1322,19 @@ tf_status tf_conv2d_fwd(tf_ctx* ctx, const float* x, const float* w, const float
     const int np = MT == 64 ? ig_pixels<64>() : ig_pixels<32>();
     const int tpi = (int)((P + np - 1) / np);
     TF_REQUIRE(N * tpi < (1LL << 31), "tf_conv2d_fwd: too many blocks");
-    // 16-byte staging loads: bit 0 input rows, bit 1 filter rows.
-    const int vec = (aligned && W % 4 == 0 && aligned16(x) ? 1 : 0) | (K % 4 == 0 && aligned16(w) ? 2 : 0);
+    // 16-byte staging loads: bit 0 input rows, bit 1 filter rows; bit 2: the
+    // direct-load layout (aligned 16-byte input rows, regions in whole KB),
+    // when it fits.
+    int vec = (aligned && W % 4 == 0 && aligned16(x) ? 1 : 0) | (K % 4 == 0 && aligned16(w) ? 2 : 0);
+    size_t lds_launch = lds;
+    if (vec & 1) {
+        const int64_t direct = ((MT * (int64_t)(Kp + 4) + 255) / 256 * 256 + (C * (int64_t)PH * PWs + 255) / 256 * 256 +
+                                Kp) * 4;
+        if (direct <= 160 * 1024) {
+            vec |= 4;
+            lds_launch = (size_t)direct;
+        }
+    }
     const dim3 grid((unsigned)(N * tpi), (unsigned)((Cout + MT - 1) / MT));
     // Dynamic LDS above 64 KB needs the attribute; set once per kernel to the
     // whole 160 KB, before any launch (and any graph capture) uses it.
@@ -1267,11 +1350,11 @@ tf_status tf_conv2d_fwd(tf_ctx* ctx, const float* x, const float* w, const float
         return tfh::set_error(TF_ERR_HIP, "tf_conv2d_fwd: hipFuncSetAttribute (dynamic LDS) failed");
     }
     if (MT == 32) {
-        conv_fwd_implicit_kernel<32><<<grid, kIgThreads, lds, ctx->stream>>>(x, w, bias, y, g, (int)Cout, (int)K, Kp, PH,
-                                                                             PWs, L, tpi, relu, vec);
+        conv_fwd_implicit_kernel<32><<<grid, kIgThreads, lds_launch, ctx->stream>>>(x, w, bias, y, g, (int)Cout, (int)K,
+                                                                                    Kp, PH, PWs, L, tpi, relu, vec);
     } else {
-        conv_fwd_implicit_kernel<64><<<grid, kIgThreads, lds, ctx->stream>>>(x, w, bias, y, g, (int)Cout, (int)K, Kp, PH,
-                                                                             PWs, L, tpi, relu, vec);
+        conv_fwd_implicit_kernel<64><<<grid, kIgThreads, lds_launch, ctx->stream>>>(x, w, bias, y, g, (int)Cout, (int)K,
+                                                                                    Kp, PH, PWs, L, tpi, relu, vec);
     }
     return tfh::check_launch("conv_fwd_implicit_kernel");
 }
