@@ -422,16 +422,17 @@ struct PatchOff {
     }
 };
 
-// Byte offset of filter slot j of an LDS block [rows][RS words] (RS / 4
-// slots a row, the last of them padding) from `nrows` rows of K floats, or
-// tfd::kBufOob for padding and rows past nrows.
+// Byte offset of slot j of an LDS block [rows][RS words] (RS / 4 slots a
+// row) holding columns c0 .. of `nrows` rows of a row-major matrix with row
+// stride ld floats: columns c0 + 4 sl .. + 3 of row r, or tfd::kBufOob for
+// columns at or past c0 + cols (padding) and rows past nrows.
 struct RowOff {
-    int K, nrows;
+    int ld, c0, cols, nrows;
     FastDiv fspr;
     __device__ __forceinline__ uint32_t operator()(int j) const {
         int sl;
         const int r = divmod(j, fspr, sl);
-        return r < nrows && 4 * sl < K ? 4u * (uint32_t)(r * K + 4 * sl) : tfd::kBufOob;
+        return r < nrows && 4 * sl < cols ? 4u * (uint32_t)(r * ld + c0 + 4 * sl) : tfd::kBufOob;
     }
 };
 
@@ -543,7 +544,7 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
                      PatchOff{H, W, PH, L, ih_lo, fast_div(PWs / 4), fast_div(PH)});
         if (vec & 2)
             stage_direct(tfd::buf_rsrc(w + (int64_t)co0 * K, (uint32_t)(nrows * K) * 4u), tfd::lds_byte_addr(wkd),
-                         MT * (RS / 4), RowOff{K, nrows, fast_div(RS / 4)});
+                         MT * (RS / 4), RowOff{K, 0, K, nrows, fast_div(RS / 4)});
         else
             stage_slots(RowSlots(w + (int64_t)co0 * K, K, nrows, K, RS, 0, Kp / 4, false), wkd, 0, MT * (Kp / 4));
         for (int k = t; k < Kp; k += kIgThreads) {
@@ -676,10 +677,6 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
     constexpr int NP = ig_pixels<MT>();
     constexpr int NH = NP / 2;
     constexpr int RS = NP + 4;                             // RS / 4 odd: no bank conflicts
-    float* dyt = smem;                                     // [MT][RS]
-    int* poff = reinterpret_cast<int*>(dyt + MT * RS);      // [NP]
-    int* koff = poff + NP;                                  // [Kc]
-    float* patch = reinterpret_cast<float*>(koff + Kc);    // [C][PH][PWs]
     const int P = (int)(g.outH * g.outW), outW = (int)g.outW;
     const int n = blockIdx.x / tiles_per_image, pt = blockIdx.x - n * tiles_per_image;
     const int p0 = pt * NP, p_end = min(p0 + NP, P);
@@ -689,10 +686,32 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
     const int C = (int)g.C, H = (int)g.H, W = (int)g.W, kHW = (int)(g.kH * g.kW), kW = (int)g.kW;
     const int t = threadIdx.x;
     const int plane = PH * PWs;
-    float* red = patch + C * plane;                         // [8][16][64] when slices > 1
-
-    stage_rows(dy + ((int64_t)n * Cout + co0) * P + p0, P, min(MT, Cout - co0), p_end - p0, dyt, RS, MT, NP / 4,
-               (vec & 2) != 0);
+    const int nrows = min(MT, Cout - co0);
+    float *dyt, *patch, *red;
+    int *poff, *koff;
+    if (vec & 4) {
+        // Direct loads (bit 2: 16-byte dy rows and the aligned patch layout):
+        // LDS = dy tile [MT][RS] | input patch (each rounded up to whole KB) |
+        // pixel and tap tables | slice sums.  Both regions go global -> LDS
+        // in one round trip while the tables are built.
+        dyt = smem;
+        patch = smem + (MT * RS + 255) / 256 * 256;
+        poff = reinterpret_cast<int*>(patch + (C * plane + 255) / 256 * 256);
+        koff = poff + NP;
+        red = reinterpret_cast<float*>(koff + Kc);
+        const float* xn = x + (int64_t)n * C * H * W;
+        stage_direct(tfd::buf_rsrc(xn, (uint32_t)(C * H * W) * 4u), tfd::lds_byte_addr(patch), C * PH * (PWs / 4),
+                     PatchOff{H, W, PH, L, ih_lo, fast_div(PWs / 4), fast_div(PH)});
+        stage_direct(tfd::buf_rsrc(dy + ((int64_t)n * Cout + co0) * P, (uint32_t)(nrows * P) * 4u),
+                     tfd::lds_byte_addr(dyt), MT * (RS / 4), RowOff{P, p0, p_end - p0, nrows, fast_div(RS / 4)});
+    } else {
+        dyt = smem;                                         // [MT][RS]
+        poff = reinterpret_cast<int*>(dyt + MT * RS);       // [NP]
+        koff = poff + NP;                                   // [Kc]
+        patch = reinterpret_cast<float*>(koff + Kc);        // [C][PH][PWs]
+        red = patch + C * plane;                            // [8][16][64] when slices > 1
+        stage_rows(dy + ((int64_t)n * Cout + co0) * P + p0, P, nrows, p_end - p0, dyt, RS, MT, NP / 4, (vec & 2) != 0);
+    }
     for (int q = t; q < NP; q += kIgThreads) {
         const int pp = p0 + q < p_end ? p0 + q : p0;
         const int oh = pp / outW, ow = pp - oh * outW;
@@ -703,7 +722,8 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
         const int ci = kc / kHW, rem = kc - ci * kHW, kh = rem / kW, kw = rem - kh * kW;
         koff[k] = (ci * PH + kh * (int)g.dh) * PWs + kw * (int)g.dw;
     }
-    stage_patch(x + (int64_t)n * C * H * W, patch, C, H, W, PH, PWs, L, ih_lo, (vec & 1) != 0);
+    if (vec & 4) __builtin_amdgcn_s_waitcnt(tfd::waitcnt_vm(0));
+    else stage_patch(x + (int64_t)n * C * H * W, patch, C, H, W, PH, PWs, L, ih_lo, (vec & 1) != 0);
     __syncthreads();
 
     const int wave = t >> 6, lane = t & 63, l32 = lane & 31, half = lane >> 5;
@@ -1388,8 +1408,19 @@ tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, flo
     const int tpi = (int)((P + np - 1) / np);
     const int64_t blocks = N * tpi;
     TF_REQUIRE(blocks < (1LL << 31), "tf_conv2d_bwd_weight: too many blocks");
-    // 16-byte staging loads: bit 0 input rows, bit 1 dy rows.
-    const int vec = (aligned && W % 4 == 0 && aligned16(x) ? 1 : 0) | (P % 4 == 0 && aligned16(dy) ? 2 : 0);
+    // 16-byte staging loads: bit 0 input rows, bit 1 dy rows; bit 2: the
+    // direct-load layout (both, regions in whole KB), when it fits.
+    int vec = (aligned && W % 4 == 0 && aligned16(x) ? 1 : 0) | (P % 4 == 0 && aligned16(dy) ? 2 : 0);
+    size_t lds_launch = lds;
+    if ((vec & 3) == 3) {
+        const int64_t tiles = (MT / 32) * (Kc / 32);
+        const int64_t direct = ((MT * (int64_t)(np + 4) + 255) / 256 * 256 + (C * (int64_t)PH * PWs + 255) / 256 * 256 +
+                                np + Kc + (slices > 1 ? tiles * slices * 16 * 64 : 0)) * 4;
+        if (direct <= 160 * 1024) {
+            vec |= 4;
+            lds_launch = (size_t)direct;
+        }
+    }
     const int with_db = db ? 1 : 0;
     const int64_t KD = K + with_db;
     st = tfh::ensure_workspace(ctx, (size_t)blocks * Cout * KD * sizeof(float));
@@ -1408,13 +1439,11 @@ tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, flo
     }
     const dim3 grid((unsigned)blocks, (unsigned)((Cout + MT - 1) / MT));
     if (MT == 32)
-        conv_bwd_weight_implicit_kernel<32><<<grid, kIgThreads, lds, ctx->stream>>>(x, dy, part, g, (int)Cout, (int)K,
-                                                                                   Kc, PH, PWs, L, tpi, slices, vec,
-                                                                                   with_db);
+        conv_bwd_weight_implicit_kernel<32><<<grid, kIgThreads, lds_launch, ctx->stream>>>(
+            x, dy, part, g, (int)Cout, (int)K, Kc, PH, PWs, L, tpi, slices, vec, with_db);
     else
-        conv_bwd_weight_implicit_kernel<64><<<grid, kIgThreads, lds, ctx->stream>>>(x, dy, part, g, (int)Cout, (int)K,
-                                                                                   Kc, PH, PWs, L, tpi, slices, vec,
-                                                                                   with_db);
+        conv_bwd_weight_implicit_kernel<64><<<grid, kIgThreads, lds_launch, ctx->stream>>>(
+            x, dy, part, g, (int)Cout, (int)K, Kc, PH, PWs, L, tpi, slices, vec, with_db);
     st = tfh::check_launch("conv_bwd_weight_implicit_kernel");
     if (st != TF_OK) return st;
     const int64_t plane = Cout * KD;
