@@ -1036,9 +1036,13 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_data_lds_kernel(const flo
     const int groups = (C + CG - 1) / CG;
     const int n = blockIdx.x / groups, c0 = (blockIdx.x - n * groups) * CG;
     const int CGv = min(CG, C - c0), Mv = CGv * kk, Mp = RT * 16;
-    constexpr int RA = kDlxKC + 4;
-    float* As = smem;                                     // [Mp][RA]
-    float* Bs = smem + Mp * RA;                           // [KC][kDlxRB]
+    // A is stored k-major, As[k][m] with row stride 16 R words (80 or 144, both
+    // 16 mod 64, so the four k rows of one MFMA operand read hit different
+    // banks): a k row is CG kk consecutive filter elements, which direct
+    // loads copy as they are.
+    constexpr int RAk = 16 * kDlxR;
+    float* As = smem;                                     // [KC][RAk]
+    float* Bs = smem + kDlxKC * RAk;                      // [KC][kDlxRB]
     // Tap tables (after the larger of the two phases' layouts):
     int* rcnt = reinterpret_cast<int*>(smem + tab_off);   // [H]
     int* roff = rcnt + H;                                 // [H][kH]
@@ -1071,21 +1075,34 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_data_lds_kernel(const flo
     const float* dyn = dy + (int64_t)n * Cout * P;
     for (int k0 = 0; k0 < Cout; k0 += kDlxKC) {
         const int kc = min(kDlxKC, Cout - k0), kcp = (kc + 3) & ~3;
-        // A: i = k Mp + m, consecutive m read consecutive filter elements.
-        const FastDiv fMp = fast_div(Mp);
-        for (int i = t; i < kcp * Mp; i += kIgThreads) {
-            int m;
-            const int k = divmod(i, fMp, m);
-            As[m * RA + k] = (k < kc && m < Mv) ? w[((int64_t)(k0 + k) * C + c0) * kk + m] : 0.0f;
+        // Bit 0 of vec: dy rows by direct loads (16-byte rows); bit 1: the
+        // filter rows too (C kk and CG kk multiples of 4, w 16-byte aligned).
+        // Rows kc .. kcp - 1 and columns past P read as zeros.
+        if (vec & 1)
+            stage_direct(tfd::buf_rsrc(dyn + (int64_t)k0 * P, (uint32_t)(kc * P) * 4u), tfd::lds_byte_addr(Bs),
+                         kcp * (kDlxRB / 4), RowOff{P, 0, P, kc, fast_div(kDlxRB / 4)});
+        else
+            stage_rows(dyn + (int64_t)k0 * P, P, kc, P, Bs, kDlxRB, kcp, kDlxRB / 4 - 4, false);
+        if (vec & 2) {
+            stage_direct(tfd::buf_rsrc(w + (int64_t)k0 * C * kk, (uint32_t)(kc * C * kk) * 4u), tfd::lds_byte_addr(As),
+                         kcp * (RAk / 4), RowOff{C * kk, c0 * kk, Mv, kc, fast_div(RAk / 4)});
+        } else {
+            // i = k Mp + m: consecutive m read consecutive filter elements.
+            const FastDiv fMp = fast_div(Mp);
+            for (int i = t; i < kcp * Mp; i += kIgThreads) {
+                int m;
+                const int k = divmod(i, fMp, m);
+                As[k * RAk + m] = (k < kc && m < Mv) ? w[((int64_t)(k0 + k) * C + c0) * kk + m] : 0.0f;
+            }
         }
-        stage_rows(dyn + (int64_t)k0 * P, P, kc, P, Bs, kDlxRB, kcp, kDlxRB / 4 - 4, vec != 0);
+        if (vec & 3) __builtin_amdgcn_s_waitcnt(tfd::waitcnt_vm(0));
         __syncthreads();
         for (int s = 0; s < kcp; s += 4) {
             const float* brow = Bs + (s + q) * kDlxRB + wave * 32 + l16;
             const float b0 = brow[0], b1 = brow[16];
             float a[kDlxR];
 #pragma unroll
-            for (int r = 0; r < kDlxR; ++r) a[r] = As[(r * 16 + l16) * RA + s + q];
+            for (int r = 0; r < kDlxR; ++r) a[r] = As[(s + q) * RAk + r * 16 + l16];
 #pragma unroll
             for (int r = 0; r < kDlxR; ++r) {
                 acc[r][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], b0, acc[r][0], 0, 0, 0);
@@ -1120,6 +1137,43 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_data_lds_kernel(const flo
             int cof[4];
 #pragma unroll
             for (int b = 0; b < 4; ++b) cof[b] = b < nc ? coff[iw * kW + b] : 0;
+            if (rpp <= H) {
+                // Rows ih = slot, slot + rpp, ...: a row's taps (at most four
+                // here) go to registers once and the channel group is walked
+                // under them, so an output's D reads are independent of each
+                // other and of the tables.  Same tap order as below.
+                for (int ih = slot; ih < H; ih += rpp) {
+                    const int nr = rcnt[ih];
+                    float* out = dxn + ih * W + iw;
+                    const float* dc = Ds;
+                    if (nr <= 4) {
+                        int ro[4];
+#pragma unroll
+                        for (int a = 0; a < 4; ++a) ro[a] = a < nr ? roff[ih * kH + a] : 0;
+                        for (int cl = 0; cl < CGv; ++cl, dc += kk * kDlxRD, out += HW) {
+                            float sum = 0.0f;
+#pragma unroll
+                            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                                for (int b = 0; b < 4; ++b)
+                                    if (a < nr && b < nc) sum += dc[ro[a] + cof[b]];
+                            *out = sum;
+                        }
+                    } else {
+                        for (int cl = 0; cl < CGv; ++cl, dc += kk * kDlxRD, out += HW) {
+                            float sum = 0.0f;
+                            for (int a = 0; a < nr; ++a) {
+                                const float* drow = dc + roff[ih * kH + a];
+#pragma unroll
+                                for (int b = 0; b < 4; ++b)
+                                    if (b < nc) sum += drow[cof[b]];
+                            }
+                            *out = sum;
+                        }
+                    }
+                }
+                return;
+            }
             const int dcl = rpp / H, dih = rpp - dcl * H;
             int cl = slot / H, ih = slot - cl * H;
             for (int r = slot; r < CGv * H; r += rpp) {
@@ -1168,10 +1222,10 @@ size_t dx_lds_bytes(const ConvGeom& g, int R, int KC, int64_t limit, int& CG, in
     CG = (int)std::min<int64_t>(g.C, 16 * R / kk);
     RT = (int)((CG * kk + 15) / 16);
     if ((int64_t)CG * g.H * g.W >= (1 << 22)) return 0;
-    // Phase 1 reads A rows up to 16 R - 1 (tiles past RT are computed and
-    // dropped): As plus Bs must cover them.  Phase 2 stores the CG kk rows.
-    const int64_t phase1 = std::max<int64_t>((int64_t)RT * 16 * (KC + 4) + (int64_t)KC * kDlxRB,
-                                             (int64_t)16 * R * (KC + 4));
+    // Phase 1: As [KC][16 R] (row tiles past RT read columns of it that
+    // are computed and dropped) and Bs [KC][kDlxRB].  Phase 2 stores the CG kk
+    // rows of D.
+    const int64_t phase1 = (int64_t)KC * 16 * R + (int64_t)KC * kDlxRB;
     const int64_t phase2 = (int64_t)CG * kk * kDlxRD;
     tab_off = (int)std::max(phase1, phase2);
     const int64_t tables = g.H * (1 + g.kH) + g.W * (1 + g.kW);
@@ -1494,7 +1548,9 @@ tf_status tf_conv2d_bwd_data(tf_ctx* ctx, const float* dy, const float* w, float
         const int64_t nblk = lds_b ? N * ((C + CG - 1) / CG) : 0;
         if (nblk >= 128 && nblk < (1LL << 31)) {
             const int64_t P = g.outH * g.outW;
-            const int vec = P % 4 == 0 && aligned16(dy) ? 1 : 0;
+            // Direct loads: bit 0 dy rows, bit 1 filter rows.
+            const int vec = (P % 4 == 0 && aligned16(dy) ? 1 : 0) |
+                            ((C * kH * kW) % 4 == 0 && (CG * kH * kW) % 4 == 0 && aligned16(w) ? 2 : 0);
             // Column-per-lane col2im: at most four column taps per input column.
             int most = 0;
             for (int j0 = 0; j0 < sw; ++j0) most = std::max(most, phase_taps(j0, (int)pw, (int)kW, (int)sw, (int)dw_).n);
