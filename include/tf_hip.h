@@ -335,6 +335,18 @@ tf_status tf_colsum_bf16(tf_ctx* ctx, const void* dy, float* db, int64_t rows, i
  * column-strip launch applies, else those two calls. */
 tf_status tf_relu_bwd_colsum(tf_ctx* ctx, const void* dy, const void* x, void* dz, float* db, int64_t rows,
                              int64_t cols, int dtype);
+/* The whole backward of a Linear layer with few outputs (fp32, N <= 16), in
+ * one launch: dx[r, k] = sum_n dy[r, n] w[n, k] (M x K), dw[n, k] =
+ * sum_r dy[r, n] x[r, k] (N x K), db[n] = sum_r dy[r, n].  Replaces, for such
+ * layers, the two products of MatmulBackward (autograd/ops/MatmulBackward.hpp:26-34)
+ * behind nn/Linear.cpp:60-63's x.matmul(W^T), the transpose of the weight
+ * gradient (autograd/ops/TransposeBackward.hpp) and the bias column sum.
+ * dx, dw or db may be NULL (not wanted).  Needs K % 4 == 0, M * N <= 16384,
+ * x, w, dx, dw 16-byte aligned; dy is [M x N] contiguous.  Each block owns 64
+ * columns of K for every row, so nothing is summed across blocks:
+ * deterministic, every output written once. */
+tf_status tf_linear_bwd_narrow(tf_ctx* ctx, const float* dy, const float* x, const float* w, float* dx, float* dw,
+                               float* db, int64_t M, int64_t N, int64_t K);
 /* db[c] = sum_{n,hw} dy[n, c, hw]  (replaces launch_reduce_sum_axis_nchw,
  * cuda/kernels/reduce_sum_axis.cu:53-120, which is wrong for H*W > 256) */
 tf_status tf_chansum_nchw(tf_ctx* ctx, const float* dy, float* db,

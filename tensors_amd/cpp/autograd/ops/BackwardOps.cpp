@@ -346,6 +346,15 @@ std::vector<Tensor> LinearBackward::apply(std::vector<Tensor>&& grads) {
         dy = c;
     }
     Tensor dx, dw, db;
+    // Few outputs (a classifier head): dX, dW and db in one launch.
+    const bool want_db = has_bias_ && wants(*this, 2) && !pending_db_.storage();
+    if (gpu(dy) && grad_dtype_ == Dtype::Float32 && (wants(*this, 0) || wants(*this, 1)) &&
+        hip::linear_backward_narrow(dy, x, w, wants(*this, 0) ? &dx : nullptr, wants(*this, 1) ? &dw : nullptr,
+                                    want_db ? &db : nullptr)) {
+        if (has_bias_ && wants(*this, 2) && !want_db) db = std::move(pending_db_);
+        pending_db_ = Tensor();
+        return {std::move(dx), std::move(dw), std::move(db)};
+    }
     if (wants(*this, 0)) dx = raw::gemm(dy, false, w, false);           // [B x in]
     if (wants(*this, 1)) {
         const int64_t out = w.shape()[0], in = w.shape()[1];

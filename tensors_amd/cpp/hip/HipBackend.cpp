@@ -455,6 +455,28 @@ void relu_backward_colsum(const Tensor& dy, const Tensor& x, Tensor& dz, Tensor&
                              tf_code(dy.dtype())), what);
 }
 
+bool linear_backward_narrow(const Tensor& dy, const Tensor& x, const Tensor& w, Tensor* dx, Tensor* dw, Tensor* db) {
+    const auto f32 = [](const Tensor& t) {
+        return t.device().type == DeviceType::CUDA && t.dtype() == Dtype::Float32 && t.shape().ndim() == 2 &&
+               t.stride() == Stride::compute_row_major(t.shape());
+    };
+    if (!f32(dy) || !f32(w) || (dw && !f32(x))) return false;
+    const int64_t M = dy.shape()[0], N = dy.shape()[1], K = w.shape()[1];
+    if (w.shape()[0] != N || N > 16 || K % 4 != 0 || M * N > 16384 || K < 1024) return false;
+    if (dw && (x.shape()[0] != M || x.shape()[1] != K)) return false;
+    const auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    if (!a16(w.data()) || (dw && !a16(x.data()))) return false;
+    if (dx) *dx = Tensor::empty(Shape{M, K}, Dtype::Float32, dy.device());
+    if (dw) *dw = Tensor::empty(Shape{N, K}, Dtype::Float32, dy.device());
+    if (db) *db = Tensor::empty(Shape{N}, Dtype::Float32, dy.device());
+    check(tf_linear_bwd_narrow(ctx_of(dy), static_cast<const float*>(dy.data()),
+                               dw ? static_cast<const float*>(x.data()) : nullptr, static_cast<const float*>(w.data()),
+                               dx ? static_cast<float*>(dx->data()) : nullptr, dw ? static_cast<float*>(dw->data()) : nullptr,
+                               db ? static_cast<float*>(db->data()) : nullptr, M, N, K),
+          "hip::linear_backward_narrow");
+    return true;
+}
+
 bool conv2d_forward_implicit(const Tensor& x, const Tensor& w, const Tensor* bias, Tensor& y, int64_t sh, int64_t sw,
                              int64_t ph, int64_t pw, int64_t dh, int64_t dw, bool relu) {
     require_gpu(x, "hip::conv2d_forward"); require_gpu(w, "hip::conv2d_forward"); require_gpu(y, "hip::conv2d_forward");

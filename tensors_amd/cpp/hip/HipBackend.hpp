@@ -127,6 +127,11 @@ void colsum(const Tensor& dy, Tensor& db);
 // dz = dy * (x > 0 ? 1 : 0) and db = the column sums of dz over the last
 // dimension, in one pass (tf_relu_bwd_colsum); dy, x, dz share shape and dtype.
 void relu_backward_colsum(const Tensor& dy, const Tensor& x, Tensor& dz, Tensor& db);
+// The backward of a Linear layer with at most 16 outputs in one launch
+// (tf_linear_bwd_narrow): dx = dy W, dw = dy^T x, db = column sums of dy,
+// each written when its pointer is given.  False (nothing launched) when
+// the shapes, dtypes or alignment do not fit that kernel.
+bool linear_backward_narrow(const Tensor& dy, const Tensor& x, const Tensor& w, Tensor* dx, Tensor* dw, Tensor* db);
 void chansum_nchw(const Tensor& dy, Tensor& db);
 // Implicit-GEMM convolution forward (tf_conv2d_fwd): false when the shape
 // does not fit the kernel's LDS (nothing was launched), else y is written.

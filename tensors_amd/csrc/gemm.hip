@@ -2981,6 +2981,112 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     return st;
 }
 
+
+// ---------------------------------------------------------------------------
+// Backward of a Linear layer with few outputs (N <= 16, fp32), in one launch:
+//   dX[r][k] = sum_n dY[r][n] W[n][k],  dW[n][k] = sum_r dY[r][n] X[r][k],
+//   db[n] = sum_r dY[r][n]
+// (nn/Linear.cpp's backward as LinearBackward forms it: two GEMMs and a
+// column sum).  Block b owns columns 64 b .. 64 b + 63 of K for every row, so
+// dW needs no sum across blocks: thread t takes the column quad t % 16 of
+// rows t / 16, t / 16 + 16, ... (eight rows' X loads in flight), adds its
+// rows in ascending order, and the 16 row groups are added in order through
+// LDS.  dY (M x N) and the block's 64 columns of W sit in LDS; each thread
+// forms dX for the same rows and columns from them.  Block 0 also sums db
+// (rows in order).  Deterministic; every output written once.
+// ---------------------------------------------------------------------------
+constexpr int kLnbCols = 64, kLnbMaxN = 16, kLnbRows = 8;
+__global__ __launch_bounds__(256) void linear_bwd_narrow_kernel(const float* __restrict__ dy,
+                                                                const float* __restrict__ x,
+                                                                const float* __restrict__ w, float* __restrict__ dx,
+                                                                float* __restrict__ dw, float* __restrict__ db, int M,
+                                                                int N, int K) {
+    extern __shared__ float lnb[];
+    float* dys = lnb;                                    // [M][N]
+    float* ws = dys + (M * N + 3) / 4 * 4;               // [N][64]
+    float* red = ws + N * kLnbCols;                      // [16][N][64]
+    const int t = threadIdx.x, cq = t & 15, rg = t >> 4;
+    const int k0 = blockIdx.x * kLnbCols, kq = k0 + 4 * cq;
+    const bool colok = kq < K;                           // K % 4 == 0: a quad is wholly in or out
+    // The first batch of this thread's X rows is loaded before dY and W are
+    // staged, so the two round trips overlap.
+    float4 xv[kLnbRows];
+    auto load_x = [&](int rb) {
+#pragma unroll
+        for (int u = 0; u < kLnbRows; ++u) {
+            const int r = rb + 16 * u;
+            xv[u] = dw && colok && r < M ? *reinterpret_cast<const float4*>(x + (int64_t)r * K + kq)
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    load_x(rg);
+    if ((M * N) % 4 == 0 && (reinterpret_cast<uintptr_t>(dy) & 15) == 0) {
+        for (int i = t; i < M * N / 4; i += 256)
+            reinterpret_cast<float4*>(dys)[i] = reinterpret_cast<const float4*>(dy)[i];
+    } else {
+        for (int i = t; i < M * N; i += 256) dys[i] = dy[i];
+    }
+    for (int i = t; i < N * 16; i += 256) {
+        const int n = i >> 4, q = i & 15, k = k0 + 4 * q;
+        *reinterpret_cast<float4*>(ws + n * kLnbCols + 4 * q) =
+            k < K ? *reinterpret_cast<const float4*>(w + (int64_t)n * K + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __syncthreads();
+    float4 wv[kLnbMaxN];
+#pragma unroll
+    for (int n = 0; n < kLnbMaxN; ++n)
+        wv[n] = n < N ? *reinterpret_cast<const float4*>(ws + n * kLnbCols + 4 * cq) : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 acc[kLnbMaxN];
+#pragma unroll
+    for (int n = 0; n < kLnbMaxN; ++n) acc[n] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int rb = rg; rb < M; rb += 16 * kLnbRows) {
+        if (rb != rg) load_x(rb);
+        // Predicates rather than early exits, so the loops unroll fully and
+        // the register arrays keep constant indices.
+#pragma unroll
+        for (int u = 0; u < kLnbRows; ++u) {
+            const int r = rb + 16 * u;
+            if (r < M) {
+                float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int n = 0; n < kLnbMaxN; ++n) {
+                    if (n < N) {
+                        const float d = dys[r * N + n];
+                        acc[n].x += d * xv[u].x; acc[n].y += d * xv[u].y;
+                        acc[n].z += d * xv[u].z; acc[n].w += d * xv[u].w;
+                        o.x += d * wv[n].x; o.y += d * wv[n].y; o.z += d * wv[n].z; o.w += d * wv[n].w;
+                    }
+                }
+                if (dx && colok) *reinterpret_cast<float4*>(dx + (int64_t)r * K + kq) = o;
+            }
+        }
+    }
+    if (dw) {
+#pragma unroll
+        for (int n = 0; n < kLnbMaxN; ++n)
+            if (n < N) *reinterpret_cast<float4*>(red + (rg * N + n) * kLnbCols + 4 * cq) = acc[n];
+        __syncthreads();
+        if (t < N * 16) {
+            const int n = t >> 4, q = t & 15, k = k0 + 4 * q;
+            float4 v = *reinterpret_cast<const float4*>(red + n * kLnbCols + 4 * q);
+            for (int g = 1; g < 16; ++g) {
+                const float4 a = *reinterpret_cast<const float4*>(red + (g * N + n) * kLnbCols + 4 * q);
+                v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
+            }
+            if (k < K) *reinterpret_cast<float4*>(dw + (int64_t)n * K + k) = v;
+        }
+    }
+    if (db && blockIdx.x == 0 && t < N) {
+        float v = 0.0f;
+        for (int r = 0; r < M; ++r) v += dys[r * N + t];
+        db[t] = v;
+    }
+}
+
+size_t linear_bwd_narrow_lds(int64_t M, int64_t N) {
+    return (size_t)(((M * N + 3) / 4 * 4) + N * kLnbCols + 16 * N * kLnbCols) * sizeof(float);
+}
+
 }  // namespace
 
 namespace tfh {
@@ -3035,6 +3141,33 @@ tf_status tf_gemm_ex(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N
     tfh::TimedLaunch timed(ctx, M, N, K, reduce_batch ? -batch : batch, trans_a, trans_b, in_dtype, out_dtype);
     return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
                      stride_c, batch, reduce_batch, in_dtype, out_dtype, epilogue, bias);
+}
+
+tf_status tf_linear_bwd_narrow(tf_ctx* ctx, const float* dy, const float* x, const float* w, float* dx, float* dw,
+                               float* db, int64_t M, int64_t N, int64_t K) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(M >= 0 && N >= 1 && N <= kLnbMaxN && K >= 0 && K % 4 == 0 && K < (1LL << 31) && M * K < (1LL << 40),
+               "tf_linear_bwd_narrow: needs 1 <= N <= 16 outputs and K % 4 == 0");
+    TF_REQUIRE(M * N <= 16384, "tf_linear_bwd_narrow: dY (M x N) must fit 64 KB of LDS");
+    if (M == 0 || K == 0) {
+        if (dw) { tf_status st = tf_hip_fill_f32(ctx, dw, 0.0f, N * K); if (st != TF_OK) return st; }
+        if (db) return tf_hip_fill_f32(ctx, db, 0.0f, N);
+        return TF_OK;
+    }
+    TF_REQUIRE(dy && w && (x || !dw), "tf_linear_bwd_narrow: null pointer");
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    TF_REQUIRE(a16(w) && (!x || a16(x)) && (!dx || a16(dx)) && (!dw || a16(dw)),
+               "tf_linear_bwd_narrow: x, w, dx and dw must be 16-byte aligned");
+    static const bool lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(linear_bwd_narrow_kernel),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    if (!lds_ok) {
+        (void)hipGetLastError();
+        return tfh::set_error(TF_ERR_HIP, "tf_linear_bwd_narrow: hipFuncSetAttribute (dynamic LDS) failed");
+    }
+    const unsigned blocks = (unsigned)((K + kLnbCols - 1) / kLnbCols);
+    linear_bwd_narrow_kernel<<<blocks, 256, linear_bwd_narrow_lds(M, N), ctx->stream>>>(dy, x, w, dx, dw, db, (int)M,
+                                                                                        (int)N, (int)K);
+    return tfh::check_launch("linear_bwd_narrow_kernel");
 }
 
 }  // extern "C"

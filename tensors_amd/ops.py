@@ -199,6 +199,22 @@ def relu_bwd_colsum(dy, x, dz, db):
     return dz, db
 
 
+def linear_bwd_narrow(dy, x, w, dx=None, dw=None, db=None):
+    """The backward of a Linear layer with at most 16 outputs in one launch
+    (tf_linear_bwd_narrow): dx = dy w, dw = dy^T x, db = column sums of dy;
+    each output is written when given.  dy [M, N], x [M, K], w [N, K], fp32."""
+    M, N = dy.shape
+    Nw, K = w.shape
+    if Nw != N or (dw is not None and tuple(x.shape) != (M, K)):
+        raise ValueError("linear_bwd_narrow: shape mismatch")
+    for t, shape in ((dx, (M, K)), (dw, (N, K)), (db, (N,))):
+        if t is not None and tuple(t.shape) != shape:
+            raise ValueError(f"linear_bwd_narrow: output shape {tuple(t.shape)} != {shape}")
+    ptr = lambda t: t.ptr if t is not None else None
+    call("tf_linear_bwd_narrow", _ctx(dy), dy.ptr, ptr(x), w.ptr, ptr(dx), ptr(dw), ptr(db), M, N, K)
+    return dx, dw, db
+
+
 def chansum_nchw(dy, db):
     if len(dy.shape) != 4:
         raise ValueError("chansum expects NCHW")
