@@ -2566,6 +2566,94 @@ __global__ __launch_bounds__(512) void gemm_f32_skinny_kernel(GemmParams p, int 
     if (threadIdx.x == 0) __hip_atomic_store(tickets + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Narrow fp32 outputs (N <= 16) over a long K on MFMA: 16 rows x 512 k per
+// block, v_mfma_f32_16x16x4f32 with A[i][k] = row i of A and B[k][j] = row j
+// of B (as [N x K]).  Lane (i = l % 16, q = l / 16) loads A[row i][k .. k+3]
+// and B[row i][k .. k+3] with k = base + 16 j + 4 q, and feeds element s to
+// the s-th of four MFMAs, so each k of the wave's 64 enters once and the
+// lanes' partial dot products are summed by the MFMA itself (no butterflies,
+// no staging).  The eight waves' 16 x 16 tiles are added in order through
+// LDS; with several k chunks each block stores its 16 x N partial and the
+// row group's last block adds the chunks in order (as gemm_f32_skinny_kernel,
+// which serves operands that are not 16-byte loadable).
+constexpr int kNmRows = 16, kNmKC = 512;
+__global__ __launch_bounds__(512) void gemm_f32_narrow_mfma_kernel(GemmParams p, int chunks,
+                                                                   unsigned* __restrict__ tickets) {
+    __shared__ float red[8][kNmRows][17];
+    __shared__ bool last;
+    const int M = p.M, N = p.N, K = p.K;
+    const int c = blockIdx.x, g = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
+    const int row = g * kNmRows + l16;
+    const int kw0 = c * kNmKC + wave * (kNmKC / 8);
+    const float* A = reinterpret_cast<const float*>(p.A) + (int64_t)min(row, M - 1) * p.lda;
+    const float* B = reinterpret_cast<const float*>(p.B) + (int64_t)min(l16, N - 1) * p.ldb;
+    float4 av[4], bv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = kw0 + 16 * j + 4 * q;   // K % 4 == 0: the quad is wholly in or out
+        av[j] = row < M && k < K ? *reinterpret_cast<const float4*>(A + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        bv[j] = l16 < N && k < K ? *reinterpret_cast<const float4*>(B + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].x, bv[j].x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].y, bv[j].y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].z, bv[j].z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].w, bv[j].w, acc, 0, 0, 0);
+    }
+    // acc[r] = D[4 q + r][l16]: row 4 q + r of the group, output column l16.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][4 * q + r][l16] = acc[r];
+    __syncthreads();
+    const int t = threadIdx.x, i = t >> 4, j = t & 15;   // threads 0 .. 255: (row i, column j)
+    const int orow = g * kNmRows + i;
+    const bool mine = t < kNmRows * 16 && orow < M && j < N;
+    float v = 0.0f;
+    if (mine) {
+#pragma unroll
+        for (int w = 0; w < 8; ++w) v += red[w][i][j];
+    }
+    const bool relu = p.epi == TF_EPI_BIAS_RELU || p.epi == TF_EPI_RELU || p.epi == TF_EPI_ROW_BIAS_RELU;
+    const bool has_bias = p.epi != TF_EPI_NONE && p.epi != TF_EPI_RELU;
+    auto finish = [&](float sum) {
+        float o = p.alpha * sum;
+        if (has_bias) o += p.row_bias ? p.bias[orow] : p.bias[j];
+        if (relu) o = fmaxf(o, 0.0f);
+        reinterpret_cast<float*>(p.C)[(int64_t)orow * p.ldc + j] = o;
+    };
+    if (chunks == 1) {
+        if (mine) finish(v);
+        return;
+    }
+    if (mine) __hip_atomic_store(p.partial + ((int64_t)c * M + orow) * N + j, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    tfd::wait_stores_landed();   // the partials have landed
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(tickets + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (unsigned)(chunks - 1);
+    __syncthreads();
+    if (!last) return;
+    if (mine) {
+        const float* sp = p.partial + (int64_t)orow * N + j;
+        const int64_t step = (int64_t)M * N;
+        float s = 0.0f;
+        int k = 0;
+        for (; k + 8 <= chunks; k += 8) {
+            float t8[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t8[u] = __hip_atomic_load(sp + (k + u) * step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += t8[u];
+        }
+        for (; k < chunks; ++k) s += __hip_atomic_load(sp + k * step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        finish(s);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(tickets + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+
 // fp32 GEMM with a short K (<= 32) and few rows (<= 64), A K-major and B
 // MN-major: a convolution over few input channels (W [Cout x Cin*k*k] times
 // each image's im2col block).  An MFMA tile would be mostly padding and one
@@ -2811,6 +2899,23 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     p.pair_c = (reinterpret_cast<uintptr_t>(C) & 7) == 0 && (ldc % 2 == 0) && (p.stride_c % 2 == 0);
     const uintptr_t c_vec_bytes = out_dtype == TF_BF16 ? 8 : 16;
     p.vec_c4 = (reinterpret_cast<uintptr_t>(C) & (c_vec_bytes - 1)) == 0 && (ldc % 4 == 0) && (p.stride_c % 4 == 0);
+    // Narrow fp32 outputs over a long K, 16-byte loadable operands: the MFMA
+    // form (gemm_f32_narrow_mfma_kernel).
+    if (in_dtype == TF_F32 && out_dtype == TF_F32 && batch == 1 && !reduce_batch && a_kmaj && b_kmaj && N <= 16 &&
+        K >= 2048 && K % 4 == 0 && p.vec_a && p.vec_b && beta == 0.0f &&
+        (M + kNmRows - 1) / kNmRows <= tfh::kTicketGemmTiles) {
+        const int64_t chunks = (K + kNmKC - 1) / kNmKC;
+        const int64_t groups = (M + kNmRows - 1) / kNmRows;
+        TF_REQUIRE(chunks < 65536 && groups < 65536, "tf_gemm: narrow grid too large");
+        if (chunks > 1) {
+            const size_t need = (size_t)chunks * (size_t)M * (size_t)N * sizeof(float);
+            tf_status st = partials_buffer(ctx, need, noalloc, &p.partial);
+            if (st != TF_OK) return st;
+        }
+        gemm_f32_narrow_mfma_kernel<<<dim3((unsigned)chunks, (unsigned)groups), 512, 0, ctx->stream>>>(
+            p, (int)chunks, ctx->tickets + tfh::kTicketGemm);
+        return tfh::check_launch("gemm_f32_narrow_mfma_kernel");
+    }
     // Narrow fp32 outputs over a long K (see gemm_f32_skinny_kernel).
     if (in_dtype == TF_F32 && out_dtype == TF_F32 && batch == 1 && !reduce_batch && a_kmaj && b_kmaj && N <= kSkN &&
         K >= 2048 && beta == 0.0f && (M + kSkRows - 1) / kSkRows <= tfh::kTicketGemmTiles) {

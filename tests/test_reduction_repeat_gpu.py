@@ -17,7 +17,7 @@ configuration shape that takes the ticket path:
 * ln_bwd_onepass_kernel: config 3c's LayerNorm backward (1024 x 1024);
 * gemm_f32_small_kernel: config 1's first layer forward (64 x 256 x 784,
   13 K chunk groups per tile);
-* gemm_f32_skinny_kernel: config 4's classifier forward (128 x 10 x 16384);
+* gemm_f32_narrow_mfma_kernel: config 4's classifier forward (128 x 10 x 16384);
 * ce_kernel's in-kernel loss mean: config 1's and config 4's cross entropy
   (64 x 10 and 128 x 10 logits: 16 and 32 blocks, a grid small enough for
   the last block to form the mean).
@@ -94,15 +94,15 @@ def test_layernorm_bwd_onepass_repeats_bit_for_bit(ctx):
     assert_close(dbt.numpy(), dy.astype(np.float64).sum(0), 1e-4, "dbeta vs float64")
 
 
-def test_small_and_skinny_gemm_repeat_bit_for_bit(ctx):
+def test_small_and_narrow_gemm_repeat_bit_for_bit(ctx):
     a, w = synth.normal(5108, (64, 784)), synth.normal(5109, (256, 784), std=0.05)
     da, dw, c = ctx.array(a), ctx.array(w), ctx.empty((64, 256))
     _repeat("gemm_f32_small C1 layer 1", lambda: ops.gemm(da, dw, c, trans_b=True), [c])
     assert_close(c.numpy(), a.astype(np.float64) @ w.astype(np.float64).T, 1e-4, "small GEMM vs float64")
     x, wf = synth.normal(5110, (128, 16384)), synth.normal(5111, (10, 16384), std=0.01)
     dxf, dwf, cf = ctx.array(x), ctx.array(wf), ctx.empty((128, 10))
-    _repeat("gemm_f32_skinny C4 classifier", lambda: ops.gemm(dxf, dwf, cf, trans_b=True), [cf])
-    assert_close(cf.numpy(), x.astype(np.float64) @ wf.astype(np.float64).T, 1e-4, "skinny GEMM vs float64")
+    _repeat("gemm_f32_narrow_mfma C4 classifier", lambda: ops.gemm(dxf, dwf, cf, trans_b=True), [cf])
+    assert_close(cf.numpy(), x.astype(np.float64) @ wf.astype(np.float64).T, 1e-4, "narrow GEMM vs float64")
 
 
 @pytest.mark.parametrize("R", [64, 128])

@@ -91,8 +91,8 @@ def test_gemm_noalloc_rejects_partials_beyond_scratch(ctx):
 
 def test_gemm_noalloc_rejects_narrow_output_partials_beyond_scratch(ctx):
     # The narrow-output fp32 path (<= 16 columns, K >= 2048): 32768 x 16 over
-    # K = 33792 is 33 chunks of 1024, whose partials need
-    # 33 * 32768 * 16 * 4 = 69.2 MB > 64 MiB.  Rejected before any launch, so
+    # K = 33792 is 66 chunks of 512 (the MFMA form), whose partials need
+    # 66 * 32768 * 16 * 4 = 138 MB > 64 MiB.  Rejected before any launch, so
     # the output keeps its contents; the operands are real allocations of
     # the stated shapes all the same (A is 4.4 GB).
     M, N, K = 32768, 16, 33792
