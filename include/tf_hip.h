@@ -416,6 +416,19 @@ tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, flo
 tf_status tf_conv2d_bwd_data(tf_ctx* ctx, const float* dy, const float* w, float* dx, int64_t N, int64_t C, int64_t H,
                              int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t stride_h, int64_t stride_w,
                              int64_t pad_h, int64_t pad_w, int64_t dilation_h, int64_t dilation_w);
+/* tf_conv2d_bwd_weight for a convolution followed by a ReLU (tf_conv2d_fwd
+ * with relu != 0), taking the gradient through the ReLU on the way: dy is
+ * the gradient of the ReLU's output y (same shape as dy), and dw, db are
+ * formed from dy * (y > 0 ? 1 : 0), the ReluBackward of
+ * autograd/ops/ReluBackward.hpp:22-32, applied to the kernel's staged dy
+ * tiles instead of in a pass of its own.  When dz is not NULL that masked
+ * gradient is also written there (the kernel's blocks cover dy once), for
+ * the data gradient that follows (tf_conv2d_bwd_data on dz).  Results equal
+ * tf_relu_bwd (dy, y) followed by tf_conv2d_bwd_weight, bit for bit. */
+tf_status tf_conv2d_bwd_weight_relu(tf_ctx* ctx, const float* x, const float* dy, const float* y, float* dz, float* dw,
+                                    float* db, int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t kH,
+                                    int64_t kW, int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                    int64_t dilation_h, int64_t dilation_w);
 
 /* Byte -> float decode of the file loaders (data/MnistLoader.cpp:43-80 and
  * data/CifarLoader.cpp:40-75 normalise each pixel on the host):

@@ -70,6 +70,7 @@ SIGNATURES: dict[str, list] = {
     "tf_conv2d_fwd": [_p, _p, _p, _p, _p] + [_i64] * 13 + [_i],
     "tf_conv2d_bwd_weight": [_p, _p, _p, _p, _p] + [_i64] * 13,
     "tf_conv2d_bwd_data": [_p, _p, _p, _p] + [_i64] * 13,
+    "tf_conv2d_bwd_weight_relu": [_p, _p, _p, _p, _p, _p, _p] + [_i64] * 13,
     "tf_decode_u8": [_p, _p, _p, _i64, _i64, _i, _p],
     "tf_col2im": [_p, _p, _p] + [_i64] * 14 + [_i],
     "tf_add": [_p, _p, _p, _p, _i64, _i],

@@ -418,23 +418,41 @@ std::vector<Tensor> CrossEntropyBackward::apply(std::vector<Tensor>&& grads) {
 std::vector<Tensor> Conv2dBackward::apply(std::vector<Tensor>&& grads) {
     const Tensor& saved = saved_.unpack();
     const Tensor& w = w_.unpack();
-    const Tensor& dy = grads[0];
+    // With a fused ReLU the incoming gradient is that of the ReLU's output y:
+    // the implicit weight gradient applies dy * (y > 0) to its staged tiles
+    // (and writes that masked gradient when dX is wanted); every other path
+    // uses masked(), ReluBackward's result formed once.
+    const Tensor* relu_y = relu_ ? &relu_y_.unpack() : nullptr;
+    Tensor dz;
+    auto masked = [&]() -> const Tensor& {
+        if (!relu_y) return grads[0];
+        if (!dz.storage()) dz = raw::relu_backward(grads[0], *relu_y);
+        return dz;
+    };
+    const Tensor& dy_in = grads[0];
     const int64_t P = g_.outH * g_.outW, KK = g_.Cin * g_.kH * g_.kW;
     Tensor dx, dw, db;
-    if (gpu(dy)) {
-        const int dev = dy.device().index;
+    if (gpu(dy_in)) {
+        const int dev = dy_in.device().index;
         const bool want_db = has_bias_ && wants(*this, 2);
         bool implicit_dw = false;
         if (wants(*this, 1)) {
-            dw = Tensor::empty(w.shape(), Dtype::Float32, dy.device());
-            if (want_db) db = Tensor::empty(Shape{g_.Cout}, Dtype::Float32, dy.device());
+            dw = Tensor::empty(w.shape(), Dtype::Float32, dy_in.device());
+            if (want_db) db = Tensor::empty(Shape{g_.Cout}, Dtype::Float32, dy_in.device());
             // With the input saved (implicit forward): the implicit weight
             // gradient, which also forms the bias gradient from its dy tiles;
             // else col is formed here for the GEMM.
-            implicit_dw = saved_input_ && dy.dtype() == Dtype::Float32 &&
-                          hip::conv2d_backward_weight_implicit(saved, dy, dw, want_db ? &db : nullptr, g_.sh, g_.sw,
-                                                               g_.ph, g_.pw, g_.dh, g_.dw);
+            // With the ReLU fused and dX wanted, the kernel also writes the
+            // masked gradient for the data gradient below.
+            Tensor dz_try;
+            if (relu_y && wants(*this, 0)) dz_try = raw::empty_like(dy_in);
+            implicit_dw = saved_input_ && dy_in.dtype() == Dtype::Float32 &&
+                          hip::conv2d_backward_weight_implicit(saved, dy_in, dw, want_db ? &db : nullptr, g_.sh, g_.sw,
+                                                               g_.ph, g_.pw, g_.dh, g_.dw, relu_y,
+                                                               dz_try.storage() ? &dz_try : nullptr);
+            if (implicit_dw && dz_try.storage()) dz = std::move(dz_try);
             if (!implicit_dw) {
+                const Tensor& dy = masked();
                 Tensor col = saved;
                 if (saved_input_) {
                     col = Tensor::empty(Shape{g_.N, KK, P}, Dtype::Float32, dy.device());
@@ -445,15 +463,16 @@ std::vector<Tensor> Conv2dBackward::apply(std::vector<Tensor>&& grads) {
             }
         }
         if (want_db && !implicit_dw) {
-            db = Tensor::empty(Shape{g_.Cout}, Dtype::Float32, dy.device());
-            hip::chansum_nchw(dy, db);
+            db = Tensor::empty(Shape{g_.Cout}, Dtype::Float32, dy_in.device());
+            hip::chansum_nchw(masked(), db);
         }
         if (wants(*this, 0)) {
-            dx = Tensor::empty(Shape{g_.N, g_.Cin, g_.H, g_.W}, dy.dtype(), dy.device());
+            dx = Tensor::empty(Shape{g_.N, g_.Cin, g_.H, g_.W}, dy_in.dtype(), dy_in.device());
             // The implicit data gradient (no dcol buffer, no col2im) when the
             // shape fits it, else dcol = W^T dy per image and col2im.
-            if (dy.dtype() != Dtype::Float32 || w.dtype() != Dtype::Float32 ||
-                !hip::conv2d_backward_data_implicit(dy, w, dx, g_.sh, g_.sw, g_.ph, g_.pw, g_.dh, g_.dw)) {
+            const bool f32 = dy_in.dtype() == Dtype::Float32 && w.dtype() == Dtype::Float32;
+            if (!f32 || !hip::conv2d_backward_data_implicit(masked(), w, dx, g_.sh, g_.sw, g_.ph, g_.pw, g_.dh, g_.dw)) {
+                const Tensor& dy = masked();
                 Tensor dcol = Tensor::empty(Shape{g_.N, KK, P}, dy.dtype(), dy.device());
                 hip::gemm_ex(dev, true, false, KK, P, g_.Cout, w.data(), KK, 0, dy.data(), P, g_.Cout * P, dcol.data(),
                              P, KK * P, g_.N, false, dy.dtype(), dy.dtype(), TF_EPI_NONE, nullptr);
@@ -463,6 +482,7 @@ std::vector<Tensor> Conv2dBackward::apply(std::vector<Tensor>&& grads) {
         return {std::move(dx), std::move(dw), std::move(db)};
     }
     // CPU: the reference's host loop (nn/conv2d_backward_test.cpp:50-106).
+    const Tensor& dy = masked();
     cpu_f32(dy, "conv2d backward");
     dx = zeros(Shape{g_.N, g_.Cin, g_.H, g_.W}, Dtype::Float32, Device::cpu());
     dw = zeros(w.shape(), Dtype::Float32, Device::cpu());

@@ -29,10 +29,19 @@ public:
     Conv2dBackward(const Tensor& x_or_col, const Tensor& weight, bool has_bias, ConvGeometry g, bool saved_input = false)
         : saved_(x_or_col), w_(weight), has_bias_(has_bias), g_(g), saved_input_(saved_input) {}
     std::vector<Tensor> apply(std::vector<Tensor>&& grads) override;
-    void release_saved() override { saved_.reset(); w_.reset(); }
+    void release_saved() override { saved_.reset(); w_.reset(); relu_y_.reset(); }
+    // The convolution is followed by a ReLU whose output y this node is then
+    // attached to (Conv2dModule::forward_relu): the incoming gradient is the
+    // ReLU output's, and dy * (y > 0), ReluBackward's result, is formed
+    // inside the gradient kernels where they take it, else explicitly.
+    void fuse_relu(const Tensor& y) {
+        relu_y_ = SavedTensor(y);
+        relu_ = true;
+    }
 
 private:
-    SavedTensor saved_, w_;
+    SavedTensor saved_, w_, relu_y_{Tensor()};
+    bool relu_ = false;
     bool has_bias_;
     ConvGeometry g_;
     bool saved_input_ = false;

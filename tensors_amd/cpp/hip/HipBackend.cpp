@@ -493,7 +493,8 @@ bool conv2d_forward_implicit(const Tensor& x, const Tensor& w, const Tensor* bia
 }
 
 bool conv2d_backward_weight_implicit(const Tensor& x, const Tensor& dy, Tensor& dw, Tensor* db, int64_t sh, int64_t sw,
-                                     int64_t ph, int64_t pw, int64_t dh, int64_t dwl) {
+                                     int64_t ph, int64_t pw, int64_t dh, int64_t dwl, const Tensor* relu_y,
+                                     Tensor* dz_out) {
     require_gpu(x, "hip::conv2d_backward_weight"); require_gpu(dy, "hip::conv2d_backward_weight");
     require_gpu(dw, "hip::conv2d_backward_weight");
     require(x.dtype() == Dtype::Float32 && dy.dtype() == Dtype::Float32 && dw.dtype() == Dtype::Float32,
@@ -504,10 +505,30 @@ bool conv2d_backward_weight_implicit(const Tensor& x, const Tensor& dy, Tensor& 
         require_gpu(*db, "hip::conv2d_backward_weight");
         require(db->dtype() == Dtype::Float32 && db->numel() == ws[0], "hip::conv2d_backward_weight: db size");
     }
-    const int st = tf_conv2d_bwd_weight(ctx_of(x), static_cast<const float*>(x.data()),
-                                        static_cast<const float*>(dy.data()), static_cast<float*>(dw.data()),
-                                        db ? static_cast<float*>(db->data()) : nullptr, xs[0], xs[1], xs[2], xs[3], ws[0],
-                                        ws[2], ws[3], sh, sw, ph, pw, dh, dwl);
+    float* dbp = db ? static_cast<float*>(db->data()) : nullptr;
+    int st;
+    if (relu_y) {
+        require_gpu(*relu_y, "hip::conv2d_backward_weight");
+        require(relu_y->dtype() == Dtype::Float32 && relu_y->shape() == dy.shape(),
+                "hip::conv2d_backward_weight: ReLU output must match dy");
+        require_contig(*relu_y, "hip::conv2d_backward_weight");
+        float* dzp = nullptr;
+        if (dz_out) {
+            require_gpu(*dz_out, "hip::conv2d_backward_weight");
+            require(dz_out->dtype() == Dtype::Float32 && dz_out->shape() == dy.shape(),
+                    "hip::conv2d_backward_weight: masked-gradient output must match dy");
+            require_contig(*dz_out, "hip::conv2d_backward_weight");
+            dzp = static_cast<float*>(dz_out->data());
+        }
+        st = tf_conv2d_bwd_weight_relu(ctx_of(x), static_cast<const float*>(x.data()),
+                                       static_cast<const float*>(dy.data()), static_cast<const float*>(relu_y->data()),
+                                       dzp, static_cast<float*>(dw.data()), dbp, xs[0], xs[1], xs[2], xs[3], ws[0],
+                                       ws[2], ws[3], sh, sw, ph, pw, dh, dwl);
+    } else {
+        st = tf_conv2d_bwd_weight(ctx_of(x), static_cast<const float*>(x.data()), static_cast<const float*>(dy.data()),
+                                  static_cast<float*>(dw.data()), dbp, xs[0], xs[1], xs[2], xs[3], ws[0], ws[2], ws[3],
+                                  sh, sw, ph, pw, dh, dwl);
+    }
     if (st == TF_ERR_UNSUPPORTED) return false;
     check(st, "hip::conv2d_backward_weight");
     return true;

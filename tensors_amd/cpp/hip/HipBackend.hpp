@@ -139,9 +139,13 @@ bool conv2d_forward_implicit(const Tensor& x, const Tensor& w, const Tensor* bia
                              int64_t ph, int64_t pw, int64_t dh, int64_t dw, bool relu);
 // Implicit-GEMM weight gradient (tf_conv2d_bwd_weight): false when the shape
 // does not fit the kernel's LDS (nothing was launched), else dw is written,
-// and db (the bias gradient) too when it is not nullptr.
+// and db (the bias gradient) too when it is not nullptr.  relu_y: dy is the
+// gradient of a ReLU's output relu_y; the gradient used is
+// dy * (relu_y > 0), which is also written to *dz_out when that is given
+// (tf_conv2d_bwd_weight_relu).
 bool conv2d_backward_weight_implicit(const Tensor& x, const Tensor& dy, Tensor& dw, Tensor* db, int64_t sh, int64_t sw,
-                                     int64_t ph, int64_t pw, int64_t dh, int64_t dwl);
+                                     int64_t ph, int64_t pw, int64_t dh, int64_t dwl, const Tensor* relu_y = nullptr,
+                                     Tensor* dz_out = nullptr);
 
 // Implicit-GEMM data gradient (tf_conv2d_bwd_data): false when the shape does
 // not fit the kernel's LDS (nothing was launched), else dx is written.

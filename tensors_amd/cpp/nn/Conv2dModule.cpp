@@ -1,7 +1,6 @@
 #include "nn/Conv2dModule.hpp"
 
 #include "autograd/Wiring.hpp"
-#include "autograd/ops/ReluBackward.hpp"
 #include "hip/HipBackend.hpp"
 #include "nn/ConvCommon.hpp"
 #include "tensor/factory.hpp"
@@ -81,14 +80,12 @@ Tensor conv2d_forward(const Tensor& x, const Tensor& w, const Tensor* bias, int6
         auto node = std::make_shared<Conv2dBackward>(saved, w, bias != nullptr, g, saved_input);
         std::vector<Edge> edges = {wiring::accumulator_edge(x), wiring::accumulator_edge(w),
                                    bias ? wiring::accumulator_edge(*bias) : Edge(nullptr, 0)};
-        if (relu) {
-            // The graph of the convolution then relu(), without the
-            // pre-activation tensor; the ReLU mask is y > 0.
-            node->next_edges_ = std::move(edges);
-            wiring::attach(y, std::make_shared<ReluBackward>(y), {Edge(node, 0)});
-        } else {
-            wiring::attach(y, node, std::move(edges));
-        }
+        // With relu: the gradient of the convolution then relu(), without the
+        // pre-activation tensor (the ReLU mask is y > 0), formed by the
+        // convolution's node itself (Conv2dBackward::fuse_relu), so the
+        // masked gradient needs no pass of its own.
+        if (relu) node->fuse_relu(y);
+        wiring::attach(y, node, std::move(edges));
     }
     return y;
 }

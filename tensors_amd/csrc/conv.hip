@@ -672,7 +672,9 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
                                                                               float* __restrict__ part, ConvGeom g,
                                                                               int Cout, int K, int Kc, int PH, int PWs,
                                                                               int L, int tiles_per_image, int slices,
-                                                                              int vec, int with_db) {
+                                                                              int vec, int with_db,
+                                                                              const float* __restrict__ relu_y,
+                                                                              float* __restrict__ dz_out) {
     extern __shared__ float smem[];
     constexpr int NP = ig_pixels<MT>();
     constexpr int NH = NP / 2;
@@ -722,9 +724,36 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
         const int ci = kc / kHW, rem = kc - ci * kHW, kh = rem / kW, kw = rem - kh * kW;
         koff[k] = (ci * PH + kh * (int)g.dh) * PWs + kw * (int)g.dw;
     }
+    // relu_y: the gradient is taken through a ReLU whose output is relu_y
+    // (same shape as dy): dy * (relu_y > 0 ? 1 : 0), as ReluBackward forms
+    // it, applied to the staged tile.  The mask values are loaded before
+    // the staging wait, so their latency overlaps it.
+    constexpr int kMaskPer = MT * NP / kIgThreads;
+    float mv[kMaskPer];
+    if (relu_y) {
+        const float* yb = relu_y + ((int64_t)n * Cout + co0) * P + p0;
+#pragma unroll
+        for (int u = 0; u < kMaskPer; ++u) {
+            const int i = t + kIgThreads * u, r = i / NP, pc = i - r * NP;
+            mv[u] = r < nrows && p0 + pc < p_end ? yb[(int64_t)r * P + pc] : 0.0f;
+        }
+    }
     if (vec & 4) __builtin_amdgcn_s_waitcnt(tfd::waitcnt_vm(0));
     else stage_patch(x + (int64_t)n * C * H * W, patch, C, H, W, PH, PWs, L, ih_lo, (vec & 1) != 0);
     __syncthreads();
+    if (relu_y) {
+        // dz_out: the masked gradient itself, for the data gradient that
+        // follows (these blocks cover every element of dy exactly once).
+        float* zb = dz_out ? dz_out + ((int64_t)n * Cout + co0) * P + p0 : nullptr;
+#pragma unroll
+        for (int u = 0; u < kMaskPer; ++u) {
+            const int i = t + kIgThreads * u, r = i / NP, pc = i - r * NP;
+            const float v = dyt[r * RS + pc] * (mv[u] > 0.0f ? 1.0f : 0.0f);
+            dyt[r * RS + pc] = v;
+            if (zb && r < nrows && p0 + pc < p_end) zb[(int64_t)r * P + pc] = v;
+        }
+        __syncthreads();
+    }
 
     const int wave = t >> 6, lane = t & 63, l32 = lane & 31, half = lane >> 5;
     const int TM = MT / 32, TK = Kc / 32, T = TM * TK;
@@ -1433,9 +1462,14 @@ tf_status tf_conv2d_fwd(tf_ctx* ctx, const float* x, const float* w, const float
     return tfh::check_launch("conv_fwd_implicit_kernel");
 }
 
-tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, float* dw, float* db, int64_t N,
-                               int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t sh,
-                               int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw_) {
+}  // extern "C"
+
+namespace {
+
+tf_status conv_bwd_weight_impl(tf_ctx* ctx, const float* x, const float* dy, const float* relu_y, float* dz,
+                               float* dw, float* db, int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout,
+                               int64_t kH, int64_t kW, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh,
+                               int64_t dw_) {
     TF_CTX_CHECK(ctx);
     ConvGeom g;
     tf_status st = make_geom(g, N, C, H, W, kH, kW, sh, sw, ph, pw, dh, dw_);
@@ -1494,10 +1528,10 @@ tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, flo
     const dim3 grid((unsigned)blocks, (unsigned)((Cout + MT - 1) / MT));
     if (MT == 32)
         conv_bwd_weight_implicit_kernel<32><<<grid, kIgThreads, lds_launch, ctx->stream>>>(
-            x, dy, part, g, (int)Cout, (int)K, Kc, PH, PWs, L, tpi, slices, vec, with_db);
+            x, dy, part, g, (int)Cout, (int)K, Kc, PH, PWs, L, tpi, slices, vec, with_db, relu_y, dz);
     else
         conv_bwd_weight_implicit_kernel<64><<<grid, kIgThreads, lds_launch, ctx->stream>>>(
-            x, dy, part, g, (int)Cout, (int)K, Kc, PH, PWs, L, tpi, slices, vec, with_db);
+            x, dy, part, g, (int)Cout, (int)K, Kc, PH, PWs, L, tpi, slices, vec, with_db, relu_y, dz);
     st = tfh::check_launch("conv_bwd_weight_implicit_kernel");
     if (st != TF_OK) return st;
     const int64_t plane = Cout * KD;
@@ -1506,9 +1540,9 @@ tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, flo
     return tfh::check_launch("conv_partial_sum_kernel");
 }
 
-tf_status tf_conv2d_bwd_data(tf_ctx* ctx, const float* dy, const float* w, float* dx, int64_t N, int64_t C, int64_t H,
-                             int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t sh, int64_t sw, int64_t ph,
-                             int64_t pw, int64_t dh, int64_t dw_) {
+tf_status conv_bwd_data_impl(tf_ctx* ctx, const float* dy, const float* w, float* dx, int64_t N, int64_t C,
+                             int64_t H, int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t sh, int64_t sw,
+                             int64_t ph, int64_t pw, int64_t dh, int64_t dw_) {
     TF_CTX_CHECK(ctx);
     ConvGeom g;
     tf_status st = make_geom(g, N, C, H, W, kH, kW, sh, sw, ph, pw, dh, dw_);
@@ -1583,6 +1617,31 @@ tf_status tf_conv2d_bwd_data(tf_ctx* ctx, const float* dy, const float* w, float
         conv_bwd_data_implicit_kernel<64><<<grid, kIgThreads, lds, ctx->stream>>>(dy, w, dx, g, (int)Cout, PH, PWs, L, tpp,
                                                                                  vec);
     return tfh::check_launch("conv_bwd_data_implicit_kernel");
+}
+
+}  // namespace
+
+extern "C" {
+
+tf_status tf_conv2d_bwd_weight(tf_ctx* ctx, const float* x, const float* dy, float* dw, float* db, int64_t N,
+                               int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t sh,
+                               int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw_) {
+    return conv_bwd_weight_impl(ctx, x, dy, nullptr, nullptr, dw, db, N, C, H, W, Cout, kH, kW, sh, sw, ph, pw, dh,
+                                dw_);
+}
+
+tf_status tf_conv2d_bwd_weight_relu(tf_ctx* ctx, const float* x, const float* dy, const float* y, float* dz, float* dw,
+                                    float* db, int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t kH,
+                                    int64_t kW, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh,
+                                    int64_t dw_) {
+    TF_REQUIRE(y, "tf_conv2d_bwd_weight_relu: null ReLU output");
+    return conv_bwd_weight_impl(ctx, x, dy, y, dz, dw, db, N, C, H, W, Cout, kH, kW, sh, sw, ph, pw, dh, dw_);
+}
+
+tf_status tf_conv2d_bwd_data(tf_ctx* ctx, const float* dy, const float* w, float* dx, int64_t N, int64_t C, int64_t H,
+                             int64_t W, int64_t Cout, int64_t kH, int64_t kW, int64_t sh, int64_t sw, int64_t ph,
+                             int64_t pw, int64_t dh, int64_t dw_) {
+    return conv_bwd_data_impl(ctx, dy, w, dx, N, C, H, W, Cout, kH, kW, sh, sw, ph, pw, dh, dw_);
 }
 
 }  // extern "C"

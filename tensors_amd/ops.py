@@ -333,11 +333,13 @@ def conv2d_fwd(x, w, y, bias=None, stride=(1, 1), pad=(0, 0), dil=(1, 1), relu=F
     return y
 
 
-def conv2d_bwd_weight(x, dy, dw, stride=(1, 1), pad=(0, 0), dil=(1, 1), db=None):
+def conv2d_bwd_weight(x, dy, dw, stride=(1, 1), pad=(0, 0), dil=(1, 1), db=None, relu_y=None, dz=None):
     """dw = sum over images and pixels of dy (x) col(x), and (db given) the
     bias gradient db = sum of dy over images and pixels, by the implicit-GEMM
     kernel (no col buffer); TFError with TF_ERR_UNSUPPORTED when the shape
-    does not fit it."""
+    does not fit it.  relu_y given: dy is the gradient of a ReLU's output
+    relu_y and dy * (relu_y > 0) is used, and written to dz when given
+    (tf_conv2d_bwd_weight_relu)."""
     N, Cc, H, W = x.shape
     Cout, Cw, kH, kW = dw.shape
     if Cw != Cc:
@@ -347,6 +349,15 @@ def conv2d_bwd_weight(x, dy, dw, stride=(1, 1), pad=(0, 0), dil=(1, 1), db=None)
         raise ValueError("conv2d_bwd_weight: dy has the wrong shape")
     if db is not None and db.size != Cout:
         raise ValueError("conv2d_bwd_weight: db must have one entry per output channel")
+    if relu_y is not None:
+        if tuple(relu_y.shape) != tuple(dy.shape):
+            raise ValueError("conv2d_bwd_weight: relu_y must have dy's shape")
+        if dz is not None and tuple(dz.shape) != tuple(dy.shape):
+            raise ValueError("conv2d_bwd_weight: dz must have dy's shape")
+        call("tf_conv2d_bwd_weight_relu", _ctx(x), x.ptr, dy.ptr, relu_y.ptr, dz.ptr if dz is not None else None,
+             dw.ptr, db.ptr if db is not None else None, N, Cc, H, W, Cout, kH, kW, stride[0], stride[1], pad[0],
+             pad[1], dil[0], dil[1])
+        return dw
     call("tf_conv2d_bwd_weight", _ctx(x), x.ptr, dy.ptr, dw.ptr, db.ptr if db is not None else None, N, Cc, H, W,
          Cout, kH, kW, stride[0], stride[1],
          pad[0], pad[1], dil[0], dil[1])

@@ -421,3 +421,43 @@ def test_col2im_checks_out_extent(ctx):
     call("tf_col2im", ctx.handle, col.ptr, dx.ptr, 1, 1, 4, 4, 3, 3, 1, 1, 1, 1, 1, 1, 4, 4, TF_F32)
     with pytest.raises(TFError, match="outH"):
         call("tf_col2im", ctx.handle, col.ptr, dx.ptr, 1, 1, 4, 4, 3, 3, 1, 1, 1, 1, 1, 1, 4, 3, TF_F32)
+
+
+
+RELU_CASES = [
+    (128, 3, 32, 32, 32, 3, 1, 1, 1),      # C4 conv1
+    (128, 32, 32, 32, 64, 3, 2, 1, 1),     # C4 conv2
+    (3, 5, 13, 17, 40, 3, 2, 0, 1),        # odd extents: partial pixel tiles and channel block
+    (2, 4, 12, 11, 70, 3, 1, 2, 2),        # two channel blocks (64 + 6), dilation 2
+    (5, 2, 15, 13, 20, 3, 2, 1, 2),        # slices of one tile over several waves
+]
+
+
+@pytest.mark.parametrize("case", RELU_CASES)
+def test_conv2d_bwd_weight_relu_equals_explicit_relu(ctx, case):
+    """tf_conv2d_bwd_weight_relu (the mask y > 0 of a following ReLU applied to
+    the staged dy tiles) equals tf_relu_bwd then tf_conv2d_bwd_weight, bit for
+    bit: dw, db, and the masked gradient it writes (every element once; the
+    buffer starts as 7.0).  y holds exact zeros (about half) and dy negative
+    values where y == 0 (ReluBackward's dy * 0 is -0 there)."""
+    ops = _ops()
+    N, C, H, W, Cout, k, s, p, d = case
+    oh, ow = ops.conv_out(H, k, s, p, d), ops.conv_out(W, k, s, p, d)
+    x = synth.normal(291, (N, C, H, W))
+    y = np.maximum(synth.normal(293, (N, Cout, oh, ow)), np.float32(0.0))
+    gy = synth.normal(294, (N, Cout, oh, ow))
+    dx_, dy_, gy_ = ctx.array(x), ctx.array(y), ctx.array(gy)
+    dz = ctx.empty((N, Cout, oh, ow))
+    ops.relu_bwd(gy_, dy_, dz)
+    want_w, want_b = ctx.empty((Cout, C, k, k)), ctx.empty((Cout,))
+    ops.conv2d_bwd_weight(dx_, dz, want_w, (s, s), (p, p), (d, d), db=want_b)
+    got_w, got_b = ctx.empty((Cout, C, k, k)), ctx.empty((Cout,))
+    got_z = ctx.array(np.full((N, Cout, oh, ow), 7.0, np.float32))
+    ops.conv2d_bwd_weight(dx_, gy_, got_w, (s, s), (p, p), (d, d), db=got_b, relu_y=dy_, dz=got_z)
+    assert_bitexact(got_w.numpy(), want_w.numpy(), f"dw with ReLU mask {case}")
+    assert_bitexact(got_b.numpy(), want_b.numpy(), f"db with ReLU mask {case}")
+    assert_bitexact(got_z.numpy(), dz.numpy(), f"masked gradient {case}")
+    # Without dz and without db: the same dw.
+    got_w2 = ctx.empty((Cout, C, k, k))
+    ops.conv2d_bwd_weight(dx_, gy_, got_w2, (s, s), (p, p), (d, d), relu_y=dy_)
+    assert_bitexact(got_w2.numpy(), want_w.numpy(), f"dw with ReLU mask, no db {case}")
