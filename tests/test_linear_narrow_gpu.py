@@ -28,6 +28,7 @@ CASES = [
     (64, 16, 2048),     # 16 outputs
     (300, 3, 1028),     # ragged last column block, 300 rows (three row batches)
     (1, 7, 1024),       # one row
+    (64, 10, 128),      # config 1's last layer (two column blocks)
 ]
 
 
