@@ -2899,10 +2899,10 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     p.pair_c = (reinterpret_cast<uintptr_t>(C) & 7) == 0 && (ldc % 2 == 0) && (p.stride_c % 2 == 0);
     const uintptr_t c_vec_bytes = out_dtype == TF_BF16 ? 8 : 16;
     p.vec_c4 = (reinterpret_cast<uintptr_t>(C) & (c_vec_bytes - 1)) == 0 && (ldc % 4 == 0) && (p.stride_c % 4 == 0);
-    // Narrow fp32 outputs over a long K, 16-byte loadable operands: the MFMA
-    // form (gemm_f32_narrow_mfma_kernel).
+    // Narrow fp32 outputs (K >= 64), 16-byte loadable operands: the MFMA form
+    // (gemm_f32_narrow_mfma_kernel; one k chunk, no partials, below 513).
     if (in_dtype == TF_F32 && out_dtype == TF_F32 && batch == 1 && !reduce_batch && a_kmaj && b_kmaj && N <= 16 &&
-        K >= 2048 && K % 4 == 0 && p.vec_a && p.vec_b && beta == 0.0f &&
+        K >= 64 && K % 4 == 0 && p.vec_a && p.vec_b && beta == 0.0f &&
         (M + kNmRows - 1) / kNmRows <= tfh::kTicketGemmTiles) {
         const int64_t chunks = (K + kNmKC - 1) / kNmKC;
         const int64_t groups = (M + kNmRows - 1) / kNmRows;

@@ -148,12 +148,13 @@ def test_gemm_splitk_long_k(ctx):
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 10, 16384), (13, 1, 2051), (64, 16, 4096), (8, 7, 2048), (300, 3, 9001),
-                                   (100, 10, 4100)])
+                                   (100, 10, 4100), (64, 10, 128)])
 def test_gemm_narrow_output_long_k(ctx, M, N, K):
     """Outputs of at most 16 columns over K >= 2048 (A row-major, B as
     [N x K]): the MFMA narrow-output kernel when K % 4 == 0 (128 x 10 x
-    16384, 64 x 16 x 4096, 8 x 7 x 2048, and 100 x 10 x 4100: a ragged last
-    512-deep chunk and a row count off the 16-row groups), the
+    16384, 64 x 16 x 4096, 8 x 7 x 2048, 100 x 10 x 4100: a ragged last
+    512-deep chunk and a row count off the 16-row groups, and config 1's last
+    layer 64 x 10 x 128: one chunk, no partials), the
     butterfly form otherwise (13 x 1 x 2051, 300 x 3 x 9001: ragged 1024-deep
     chunks, rows off its 8-row groups); bias and bias + ReLU; bit-identical on
     a second call (each row group's arrival counter back at zero)."""
