@@ -20,7 +20,8 @@ configuration shape that takes the ticket path:
 * gemm_f32_narrow_mfma_kernel: config 4's classifier forward (128 x 10 x 16384);
 * ce_kernel's in-kernel loss mean: config 1's and config 4's cross entropy
   (64 x 10 and 128 x 10 logits: 16 and 32 blocks, a grid small enough for
-  the last block to form the mean).
+  the last block to form the mean), and larger grids whose mean is a
+  separate one-block launch (4096 x 1024, 8000 and 8100 rows).
 
 A mismatch fails at the first repetition that differs (named in the
 message); the first result is also checked against float64.
@@ -105,13 +106,16 @@ def test_small_and_narrow_gemm_repeat_bit_for_bit(ctx):
     assert_close(cf.numpy(), x.astype(np.float64) @ wf.astype(np.float64).T, 1e-4, "narrow GEMM vs float64")
 
 
-@pytest.mark.parametrize("R", [64, 128])
-def test_ce_loss_mean_repeats_bit_for_bit(ctx, R):
-    logits = synth.normal(5112 + R, (R, 10), std=3.0)
-    labels = synth.uniform_int(5113 + R, (R,), 10)
+@pytest.mark.parametrize("R,Cc", [(64, 10), (128, 10), (4096, 1024), (8000, 16), (8100, 16)])
+def test_ce_loss_mean_repeats_bit_for_bit(ctx, R, Cc):
+    """The in-kernel mean up to 64 blocks (C1's and C4's 16 and 32 blocks);
+    the separate one-block mean launch after the kernel for larger grids
+    (C3a's 4096 x 1024: 1024 blocks; 8000 and 8100 rows)."""
+    logits = synth.normal(5112 + R, (R, Cc), std=3.0)
+    labels = synth.uniform_int(5113 + R, (R,), Cc)
     dl_, dt = ctx.array(logits), ctx.array(labels)
-    loss, dlog = ctx.empty((1,)), ctx.empty((R, 10))
-    _repeat(f"ce loss mean {R} x 10", lambda: ops.ce_fwd_bwd(dl_, dt, loss, dlog), [loss, dlog])
+    loss, dlog = ctx.empty((1,)), ctx.empty((R, Cc))
+    _repeat(f"ce loss mean {R} x {Cc}", lambda: ops.ce_fwd_bwd(dl_, dt, loss, dlog), [loss, dlog])
     lg = logits.astype(np.float64)
     lse = np.log(np.exp(lg - lg.max(1, keepdims=True)).sum(1)) + lg.max(1)
     want = float(np.mean(lse - lg[np.arange(R), labels]))
