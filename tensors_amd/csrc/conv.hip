@@ -527,6 +527,11 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
         pix_off = (oh - oh_lo) * (int)g.sh * PWs + ow * (int)g.sw + L - (int)g.pw;
     }
     const int KS = Kp / 8;                                  // k steps of 8
+    // The block's bias values, read from LDS by the epilogue: a global load
+    // in the store loop would make each store wait for the ones before it
+    // (loads and stores share one counter), which cost 2 us per launch.
+    __shared__ float bias_s[MT];
+    if (t < MT) bias_s[t] = bias && co0 + t < Cout ? bias[co0 + t] : 0.0f;
     v16f acc;
     if (vec & 4) {
         // Direct loads (bit 2: aligned patch layout, 16-byte image rows):
@@ -605,7 +610,7 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
     for (int r = 0; r < 16; ++r) {
         const int co = co0 + m_sub * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
         if (co >= Cout) continue;
-        float v = acc[r] + (bias ? bias[co] : 0.0f);
+        float v = acc[r] + bias_s[co - co0];
         if (relu) v = fmaxf(v, 0.0f);
         yn[(int64_t)co * P + pp] = v;
     }
@@ -633,6 +638,10 @@ int64_t rows_spanned(int64_t rows, int64_t cols, int64_t np) {
     return most;
 }
 
+// Dynamic LDS of conv_fwd_implicit_kernel: the 160 KB of a CU less its
+// static 256-byte bias table.
+constexpr int64_t kFwdDynLds = 160 * 1024 - 256;
+
 // LDS layout of conv_fwd_implicit_kernel (the aligned patch layout when it
 // fits, else the tight one), or 0 when neither fits.
 size_t implicit_lds_bytes(const ConvGeom& g, int MT, int K, int& Kp, int& PH, int& PWs, int& L, bool& aligned) {
@@ -643,7 +652,7 @@ size_t implicit_lds_bytes(const ConvGeom& g, int MT, int K, int& Kp, int& PH, in
         aligned = a != 0;
         patch_cols(g, aligned, L, PWs);
         const int64_t bytes = ((int64_t)MT * (Kp + 4) + Kp + g.C * (int64_t)PH * PWs) * 4;
-        if (bytes <= 160 * 1024) return (size_t)bytes;
+        if (bytes <= kFwdDynLds) return (size_t)bytes;
     }
     return 0;
 }
@@ -1433,7 +1442,7 @@ tf_status tf_conv2d_fwd(tf_ctx* ctx, const float* x, const float* w, const float
     if (vec & 1) {
         const int64_t direct = ((MT * (int64_t)(Kp + 4) + 255) / 256 * 256 + (C * (int64_t)PH * PWs + 255) / 256 * 256 +
                                 Kp) * 4;
-        if (direct <= 160 * 1024) {
+        if (direct <= kFwdDynLds) {
             vec |= 4;
             lds_launch = (size_t)direct;
         }
@@ -1442,7 +1451,7 @@ tf_status tf_conv2d_fwd(tf_ctx* ctx, const float* x, const float* w, const float
     // Dynamic LDS above 64 KB needs the attribute; set once per kernel to the
     // whole 160 KB, before any launch (and any graph capture) uses it.
     static const bool lds_ok = [] {
-        const int all = 160 * 1024;
+        const int all = (int)kFwdDynLds;
         return hipFuncSetAttribute(reinterpret_cast<const void*>(conv_fwd_implicit_kernel<32>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, all) == hipSuccess &&
                hipFuncSetAttribute(reinterpret_cast<const void*>(conv_fwd_implicit_kernel<64>),
