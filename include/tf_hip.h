@@ -335,6 +335,20 @@ tf_status tf_colsum_bf16(tf_ctx* ctx, const void* dy, float* db, int64_t rows, i
  * column-strip launch applies, else those two calls. */
 tf_status tf_relu_bwd_colsum(tf_ctx* ctx, const void* dy, const void* x, void* dz, float* db, int64_t rows,
                              int64_t cols, int dtype);
+/* C = (A * [mask > 0]) B in fp32, the ReLU backward folded into the load of a
+ * product's left operand: op(A)[m, k] is taken as op(A)[m, k] *
+ * (op(mask)[m, k] > 0 ? 1 : 0), mask laid out as A (same trans_a and lda).
+ * Replaces ReluBackward's mask product (autograd/ops/ReluBackward.hpp:22-32)
+ * in front of the two products of MatmulBackward
+ * (autograd/ops/MatmulBackward.hpp:26-34) when a bias-free Linear is followed
+ * by a ReLU: dX = (dY * [y > 0]) W and dW = (dY * [y > 0])^T X without the
+ * masked gradient in memory.  Bit-identical to tf_relu_bwd then tf_gemm.
+ * Only the small-product kernel takes the mask: K <= 2048 and M*N*K <= 2^27,
+ * else TF_ERR_UNSUPPORTED (the caller then masks and multiplies in two
+ * calls). */
+tf_status tf_gemm_relu_masked(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                              const float* A, int64_t lda, const float* mask, const float* B, int64_t ldb, float* C,
+                              int64_t ldc);
 /* The whole backward of a Linear layer with few outputs (fp32, N <= 16), in
  * one launch: dx[r, k] = sum_n dy[r, n] w[n, k] (M x K), dw[n, k] =
  * sum_r dy[r, n] x[r, k] (N x K), db[n] = sum_r dy[r, n].  Replaces, for such

@@ -346,17 +346,41 @@ std::vector<Tensor> LinearBackward::apply(std::vector<Tensor>&& grads) {
         dy = c;
     }
     Tensor dx, dw, db;
+    bool dx_done = false, dw_done = false;
+    if (relu_) {
+        // dz = dy * (y > 0) folded into the products' load of dy where the
+        // kernel takes it; whatever remains gets the explicit masked dz.
+        const Tensor& y = relu_y_.unpack();
+        if (gpu(dy) && dy.dtype() == Dtype::Float32 && grad_dtype_ == Dtype::Float32) {
+            if (wants(*this, 0)) {
+                Tensor t = Tensor::empty(Shape{dy.shape()[0], w.shape()[1]}, Dtype::Float32, dy.device());
+                if (hip::gemm_relu_masked(dy, false, y, w, false, t)) {
+                    dx = std::move(t);
+                    dx_done = true;
+                }
+            }
+            if (wants(*this, 1)) {
+                Tensor t = Tensor::empty(w.shape(), Dtype::Float32, dy.device());
+                if (hip::gemm_relu_masked(dy, true, y, x, false, t)) {
+                    dw = std::move(t);
+                    dw_done = true;
+                }
+            }
+        }
+        if ((wants(*this, 0) && !dx_done) || (wants(*this, 1) && !dw_done) || (has_bias_ && wants(*this, 2)))
+            dy = raw::relu_backward(dy, y);
+    }
     // Few outputs (a classifier head): dX, dW and db in one launch.
     const bool want_db = has_bias_ && wants(*this, 2) && !pending_db_.storage();
-    if (gpu(dy) && grad_dtype_ == Dtype::Float32 && (wants(*this, 0) || wants(*this, 1)) &&
+    if (!dx_done && !dw_done && gpu(dy) && grad_dtype_ == Dtype::Float32 && (wants(*this, 0) || wants(*this, 1)) &&
         hip::linear_backward_narrow(dy, x, w, wants(*this, 0) ? &dx : nullptr, wants(*this, 1) ? &dw : nullptr,
                                     want_db ? &db : nullptr)) {
         if (has_bias_ && wants(*this, 2) && !want_db) db = std::move(pending_db_);
         pending_db_ = Tensor();
         return {std::move(dx), std::move(dw), std::move(db)};
     }
-    if (wants(*this, 0)) dx = raw::gemm(dy, false, w, false);           // [B x in]
-    if (wants(*this, 1)) {
+    if (wants(*this, 0) && !dx_done) dx = raw::gemm(dy, false, w, false);   // [B x in]
+    if (wants(*this, 1) && !dw_done) {
         const int64_t out = w.shape()[0], in = w.shape()[1];
         if (gpu(dy)) {
             dw = Tensor::empty(Shape{out, in}, grad_dtype_, dy.device());

@@ -19,7 +19,15 @@ public:
     LinearBackward(const Tensor& x, const Tensor& weight, bool has_bias, Dtype grad_dtype)
         : x_(x), w_(weight), has_bias_(has_bias), grad_dtype_(grad_dtype) {}
     std::vector<Tensor> apply(std::vector<Tensor>&& grads) override;
-    void release_saved() override { x_.reset(); w_.reset(); pending_db_ = Tensor(); }
+    void release_saved() override { x_.reset(); w_.reset(); relu_y_.reset(); pending_db_ = Tensor(); }
+    // The layer is followed by a ReLU whose output y this node is then
+    // attached to (Linear::forward_relu without bias): the incoming gradient
+    // is the ReLU output's, and ReluBackward's dy * (y > 0) is applied by the
+    // products as they load dy, else formed explicitly first.
+    void fuse_relu(const Tensor& y) {
+        relu_y_ = SavedTensor(y);
+        relu_ = true;
+    }
     // True when apply() will sum an upstream gradient of dtype `dt` into a
     // bias gradient as it arrives (no cast first).
     bool sums_bias_grad_of(Dtype dt) const;
@@ -29,7 +37,8 @@ public:
     void set_bias_grad(Tensor db) { pending_db_ = std::move(db); }
 
 private:
-    SavedTensor x_, w_;
+    SavedTensor x_, w_, relu_y_{Tensor()};
+    bool relu_ = false;
     bool has_bias_;
     Dtype grad_dtype_;
     Tensor pending_db_;

@@ -610,6 +610,49 @@ void t_linear_relu_bias_wide(Device d) {
     }
 }
 
+// Linear::forward_relu on a bias-free fp32 layer, whose backward node takes
+// the ReLU itself (on the GPU its products apply the mask as they load dy):
+// y, dX and dW equal those of forward() then relu() bit for bit, with and
+// without dX wanted (a first layer), and the upstream gradient of y is left
+// unmasked.
+void t_linear_relu_nobias(Device d) {
+    const int R = 64, I = 96, O = 256;
+    std::vector<float> xv(R * I), wv(O * I), uv(R * O);
+    for (int i = 0; i < R * I; ++i) xv[i] = std::sin(0.37f * i);
+    for (int i = 0; i < O * I; ++i) wv[i] = 0.1f * std::cos(0.11f * i);
+    for (int i = 0; i < R * O; ++i) uv[i] = std::cos(0.07f * i);
+    for (int want_dx = 0; want_dx < 2; ++want_dx) {
+        std::vector<float> got[2][3];   // [fused?][y, dX, dW]
+        for (int fused = 0; fused < 2; ++fused) {
+            nn::Linear fc(I, O, false);
+            fc.to(d);
+            Tensor W = from_vals(wv, {O, I}, d);
+            for (auto& np : fc.named_parameters()) {
+                np.second->data_ = W;
+                np.second->data_.requires_grad(true);
+            }
+            Tensor x = from_vals(xv, {R, I}, d);
+            x.requires_grad(want_dx != 0);
+            Tensor y = fused ? fc.forward_relu(x) : fc.forward(x).relu();
+            Tensor up = from_vals(uv, {R, O}, d);
+            Engine().execute(y.autograd_meta()->grad_fn_, up, false);
+            got[fused][0] = to_host(y);
+            if (want_dx) got[fused][1] = to_host(x.grad());
+            else TFA_CHECK(!x.grad().storage());
+            got[fused][2] = to_host(fc.named_parameters().at(0).second->data_.grad());
+            TFA_CHECK(got[fused][2].size() == (size_t)O * I);
+            TFA_CHECK(to_host(up) == uv);
+        }
+        for (int k = 0; k < 3; ++k) {
+            TFA_CHECK(got[0][k].size() == got[1][k].size());
+            for (size_t i = 0; i < got[0][k].size(); ++i)
+                if (!(got[1][k][i] == got[0][k][i]))
+                    check_near(got[1][k][i], got[0][k][i], 0.0f, "bias-free fused vs relu(forward) output " +
+                                                                    std::to_string(k) + "[" + std::to_string(i) + "]");
+        }
+    }
+}
+
 // Conv2dModule::forward_relu on a 1x1 convolution (w = 2, b = 0).
 void t_conv_relu_fused(Device d) {
     Tensor x = from_vals({1, -2, 3, -4}, {1, 1, 2, 2}, d);
@@ -747,6 +790,7 @@ const std::map<std::string, std::function<void(Device)>>& registry() {
         {"linear_grads", t_linear_grads},
         {"linear_relu_fused", t_linear_relu_fused},
         {"linear_relu_bias_wide", t_linear_relu_bias_wide},
+        {"linear_relu_nobias", t_linear_relu_nobias},
         {"conv_relu_fused", t_conv_relu_fused},
         {"sgd_momentum_rule", t_sgd_momentum_rule},
         {"reshape_grad", t_reshape_grad},

@@ -269,6 +269,27 @@ void gemm(const Tensor& A, bool trans_a, const Tensor& B, bool trans_b, Tensor& 
           "hip::gemm");
 }
 
+bool gemm_relu_masked(const Tensor& A, bool trans_a, const Tensor& mask, const Tensor& B, bool trans_b, Tensor& C) {
+    const auto f32 = [](const Tensor& t) {
+        return t.device().type == DeviceType::CUDA && t.dtype() == Dtype::Float32 && t.shape().ndim() == 2 &&
+               t.stride() == Stride::compute_row_major(t.shape());
+    };
+    if (!f32(A) || !f32(mask) || !f32(B) || !f32(C) || mask.shape() != A.shape()) return false;
+    if (mask.device() != A.device() || B.device() != A.device() || C.device() != A.device()) return false;
+    const int64_t M = trans_a ? A.shape()[1] : A.shape()[0];
+    const int64_t K = trans_a ? A.shape()[0] : A.shape()[1];
+    const int64_t N = trans_b ? B.shape()[0] : B.shape()[1];
+    require((trans_b ? B.shape()[1] : B.shape()[0]) == K, "hip::gemm_relu_masked: inner dimensions differ");
+    require(C.shape()[0] == M && C.shape()[1] == N, "hip::gemm_relu_masked: output shape mismatch");
+    const int st = tf_gemm_relu_masked(ctx_of(A), trans_a, trans_b, M, N, K, static_cast<const float*>(A.data()),
+                                       A.shape()[1], static_cast<const float*>(mask.data()),
+                                       static_cast<const float*>(B.data()), B.shape()[1], static_cast<float*>(C.data()),
+                                       C.shape()[1]);
+    if (st == TF_ERR_UNSUPPORTED) return false;
+    check(st, "hip::gemm_relu_masked");
+    return true;
+}
+
 void gemm_ex(int device, bool trans_a, bool trans_b, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
              int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b, void* C, int64_t ldc, int64_t stride_c,
              int64_t batch, bool reduce_batch, Dtype in_dtype, Dtype out_dtype, int epilogue, const float* bias,

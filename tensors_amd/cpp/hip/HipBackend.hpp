@@ -91,6 +91,10 @@ void cast(const Tensor& x, Tensor& y);  // Float32 <-> BFloat16
 // op(X) = X^T when the flag is set.  bias: Float32 [N] or nullptr.
 void gemm(const Tensor& A, bool trans_a, const Tensor& B, bool trans_b, Tensor& C, float alpha = 1.0f,
           float beta = 0.0f, const Tensor* bias = nullptr, bool relu = false);
+// C = (A * [mask > 0]) op(B), Float32, mask shaped as A (tf_gemm_relu_masked):
+// a ReLU's backward folded into the product's left operand.  False (nothing
+// launched) when the product does not fit the kernel that takes the mask.
+bool gemm_relu_masked(const Tensor& A, bool trans_a, const Tensor& mask, const Tensor& B, bool trans_b, Tensor& C);
 // Raw tf_gemm_ex on device pointers (conv layers).
 void gemm_ex(int device, bool trans_a, bool trans_b, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
              int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b, void* C, int64_t ldc, int64_t stride_c,

@@ -93,7 +93,13 @@ Tensor Linear::forward_impl(Tensor x, bool relu) {
     if (node) {
         std::vector<Edge> edges = {wiring::accumulator_edge(x), wiring::accumulator_edge(W),
                                    b ? wiring::accumulator_edge(*b) : Edge(nullptr, 0)};
-        if (relu) {
+        if (relu && !b && x.device().type == DeviceType::CUDA && compute_dtype_ == Dtype::Float32) {
+            // Bias-free fp32: the Linear's node takes the ReLU's backward
+            // itself (its products apply the mask as they load dy), so the
+            // masked gradient is never written.
+            node->fuse_relu(y);
+            wiring::attach(y, node, std::move(edges));
+        } else if (relu) {
             // The graph of forward() then relu(): ReluBackward -> LinearBackward,
             // without the pre-activation tensor.  The ReLU node's mask is taken
             // from y (y > 0 exactly where the pre-activation is > 0).

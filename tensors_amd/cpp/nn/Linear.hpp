@@ -21,9 +21,11 @@ public:
 
     [[nodiscard]] Tensor forward(Tensor x) override;
     // relu(forward(x)) with the ReLU in the GEMM epilogue on the GPU (one
-    // launch, no pre-activation tensor).  Same values and the same backward
-    // graph (ReluBackward -> LinearBackward) as the two calls; no counterpart
-    // in the reference, which has only the separate modules.
+    // launch, no pre-activation tensor).  Same values and gradients as the
+    // two calls; the backward graph is ReluBackward -> LinearBackward, or,
+    // for a bias-free fp32 layer, one LinearBackward that applies the ReLU
+    // mask as its products load dy.  No counterpart in the reference, which
+    // has only the separate modules.
     [[nodiscard]] Tensor forward_relu(Tensor x);
 
     [[nodiscard]] int in_features() const noexcept { return in_features_; }

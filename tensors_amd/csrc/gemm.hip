@@ -90,6 +90,7 @@ struct GemmParams {
     int vec_c4;            // 4-element vector stores legal for C (16 bytes fp32, 8 bytes bf16)
     uint32_t a_bytes, b_bytes;  // byte extent of one batch element of A / B (buffer loads)
     int int_m, int_n;           // large-tile path: tile rows / columns covered by the direct kernel
+    const float* mask_a;        // small fp32 path: A(m, k) taken as A(m, k) * (mask(m, k) > 0), mask laid out as A
 };
 
 // Remap a linear workgroup id so that the ids one XCD receives (id % 8 == x)
@@ -2274,6 +2275,18 @@ __global__ __launch_bounds__(256) void gemm_f32_small_kernel(GemmParams p, int n
             ra[j] = load_quad(A, p.lda, m0, p.M, A_KMAJ, p.vec_a, k0, t + 256 * j);
             rb[j] = load_quad(B, p.ldb, n0, p.N, B_KMAJ, p.vec_b, k0, t + 256 * j);
         }
+        if (p.mask_a) {
+            // A ReLU's backward applied on the load: dy * (y > 0 ? 1 : 0),
+            // the same product as the separate pass, so bit-identical.
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float4 y = load_quad(p.mask_a, p.lda, m0, p.M, A_KMAJ, p.vec_a, k0, t + 256 * j);
+                ra[j].x *= y.x > 0.0f ? 1.0f : 0.0f;
+                ra[j].y *= y.y > 0.0f ? 1.0f : 0.0f;
+                ra[j].z *= y.z > 0.0f ? 1.0f : 0.0f;
+                ra[j].w *= y.w > 0.0f ? 1.0f : 0.0f;
+            }
+        }
     };
     if (kc_first < kc_end) fetch(kc_first);
     for (int kc = kc_first; kc < kc_end; ++kc) {
@@ -2836,7 +2849,8 @@ tf_status partials_buffer(tf_ctx* ctx, size_t need, bool noalloc, float** out) {
 tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                     const void* A, int64_t lda, int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b,
                     float beta, void* C, int64_t ldc, int64_t stride_c, int64_t batch, int reduce_batch,
-                    int in_dtype, int out_dtype, int epi, const float* bias, bool noalloc = false) {
+                    int in_dtype, int out_dtype, int epi, const float* bias, bool noalloc = false,
+                    const float* mask_a = nullptr) {
     TF_CTX_CHECK(ctx);
     TF_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "tf_gemm: negative extent");
     TF_REQUIRE(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31), "tf_gemm: extent exceeds 2^31");
@@ -2854,6 +2868,7 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     TF_REQUIRE(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N) && ldc >= N, "tf_gemm: leading dimension too small");
     TF_REQUIRE(batch < 65536, "tf_gemm: batch exceeds 65535");
     TF_REQUIRE(!reduce_batch || batch * ((K + 31) / 32) < (1LL << 31), "tf_gemm: reduced K too long");
+    TF_REQUIRE(!mask_a || (in_dtype == TF_F32 && batch == 1 && !reduce_batch), "tf_gemm: a mask needs one Float32 product");
 
     const bool a_kmaj = trans_a == 0;  // A[m*lda + k]
     const bool b_kmaj = trans_b != 0;  // B[n*ldb + k]
@@ -2896,12 +2911,14 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     p.reduce_batch = reduce_batch ? (int)batch : 1;
     p.vec_a = aligned16(A) && (lda % vec_elems == 0) && (stride_a % vec_elems == 0);
     p.vec_b = aligned16(B) && (ldb % vec_elems == 0) && (stride_b % vec_elems == 0);
+    p.mask_a = mask_a;
+    if (mask_a && !aligned16(mask_a)) p.vec_a = 0;
     p.pair_c = (reinterpret_cast<uintptr_t>(C) & 7) == 0 && (ldc % 2 == 0) && (p.stride_c % 2 == 0);
     const uintptr_t c_vec_bytes = out_dtype == TF_BF16 ? 8 : 16;
     p.vec_c4 = (reinterpret_cast<uintptr_t>(C) & (c_vec_bytes - 1)) == 0 && (ldc % 4 == 0) && (p.stride_c % 4 == 0);
     // Narrow fp32 outputs (K >= 64), 16-byte loadable operands: the MFMA form
     // (gemm_f32_narrow_mfma_kernel; one k chunk, no partials, below 513).
-    if (in_dtype == TF_F32 && out_dtype == TF_F32 && batch == 1 && !reduce_batch && a_kmaj && b_kmaj && N <= 16 &&
+    if (!mask_a && in_dtype == TF_F32 && out_dtype == TF_F32 && batch == 1 && !reduce_batch && a_kmaj && b_kmaj && N <= 16 &&
         K >= 64 && K % 4 == 0 && p.vec_a && p.vec_b && beta == 0.0f &&
         (M + kNmRows - 1) / kNmRows <= tfh::kTicketGemmTiles) {
         const int64_t chunks = (K + kNmKC - 1) / kNmKC;
@@ -2917,7 +2934,7 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
         return tfh::check_launch("gemm_f32_narrow_mfma_kernel");
     }
     // Narrow fp32 outputs over a long K (see gemm_f32_skinny_kernel).
-    if (in_dtype == TF_F32 && out_dtype == TF_F32 && batch == 1 && !reduce_batch && a_kmaj && b_kmaj && N <= kSkN &&
+    if (!mask_a && in_dtype == TF_F32 && out_dtype == TF_F32 && batch == 1 && !reduce_batch && a_kmaj && b_kmaj && N <= kSkN &&
         K >= 2048 && beta == 0.0f && (M + kSkRows - 1) / kSkRows <= tfh::kTicketGemmTiles) {
         const int64_t chunks = (K + kSkC - 1) / kSkC;
         const int64_t groups = (M + kSkRows - 1) / kSkRows;
@@ -2957,6 +2974,9 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
         else gemm_f32_small_kernel<false, false><<<grid, 256, 0, ctx->stream>>>(p, (int)groups, cps, tickets);
         return tfh::check_launch("gemm_f32_small_kernel");
     }
+    if (mask_a)
+        return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_gemm_relu_masked: the masked operand needs a Float32 product with "
+                                                  "K <= 2048 and M*N*K <= 2^27 (the small-product kernel)");
     if (in_dtype == TF_F32 && !trans_a && !trans_b && !reduce_batch && K <= 32 && M <= 64 && N >= 256) {
         const dim3 grid((unsigned)((N + 255) / 256), (unsigned)batch);
         gemm_f32_smallk_kernel<<<grid, 256, 0, ctx->stream>>>(p);
@@ -3246,6 +3266,15 @@ tf_status tf_gemm_ex(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N
     tfh::TimedLaunch timed(ctx, M, N, K, reduce_batch ? -batch : batch, trans_a, trans_b, in_dtype, out_dtype);
     return gemm_impl(ctx, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
                      stride_c, batch, reduce_batch, in_dtype, out_dtype, epilogue, bias);
+}
+
+tf_status tf_gemm_relu_masked(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                              const float* A, int64_t lda, const float* mask, const float* B, int64_t ldb, float* C,
+                              int64_t ldc) {
+    TF_REQUIRE(mask != nullptr || M == 0 || N == 0, "tf_gemm_relu_masked: null mask");
+    tfh::TimedLaunch timed(ctx, M, N, K, 1, trans_a, trans_b, TF_F32, TF_F32);
+    return gemm_impl(ctx, trans_a, trans_b, M, N, K, 1.0f, A, lda, 0, B, ldb, 0, 0.0f, C, ldc, 0, 1, 0, TF_F32,
+                     TF_F32, TF_EPI_NONE, nullptr, false, mask);
 }
 
 tf_status tf_linear_bwd_narrow(tf_ctx* ctx, const float* dy, const float* x, const float* w, float* dx, float* dw,

@@ -42,6 +42,20 @@ def gemm(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, trans_a=False, trans
     return c
 
 
+def gemm_relu_masked(a, mask, b, c, *, trans_a=False, trans_b=False):
+    """c = (a * (mask > 0)) as op(a), times op(b), fp32 (tf_gemm_relu_masked);
+    mask has a's shape and layout."""
+    if len(a.shape) != 2 or len(b.shape) != 2 or len(c.shape) != 2 or tuple(mask.shape) != tuple(a.shape):
+        raise ValueError("gemm_relu_masked expects 2-D arrays and a mask shaped as a")
+    M, K = (a.shape[1], a.shape[0]) if trans_a else a.shape
+    Kb, N = (b.shape[1], b.shape[0]) if trans_b else b.shape
+    if K != Kb or c.shape != (M, N):
+        raise ValueError(f"gemm_relu_masked shape mismatch: op(a) {M}x{K}, op(b) {Kb}x{N}, c {c.shape}")
+    call("tf_gemm_relu_masked", _ctx(a), int(trans_a), int(trans_b), M, N, K, a.ptr, a.shape[1], mask.ptr, b.ptr,
+         b.shape[1], c.ptr, c.shape[1])
+    return c
+
+
 def relu_bwd(dy, x, dx):
     call("tf_relu_bwd", _ctx(dy), dy.ptr, x.ptr, dx.ptr, _same(dy, x, dx), dy.tf_dtype)
     return dx

@@ -569,6 +569,50 @@ def test_c2_linear_full_size(ctx):
 # ---------------------------------------------------------------------------
 # elementwise backward
 # ---------------------------------------------------------------------------
+@pytest.mark.parametrize("ta,tb,M,N,K", [
+    (False, False, 64, 256, 128),    # config 1: second layer's dX = (dY * [y > 0]) W2
+    (True, False, 128, 256, 64),     # config 1: second layer's dW = (dY * [y > 0])^T X
+    (True, False, 256, 784, 64),     # config 1: first layer's dW
+    (False, True, 17, 19, 23), (True, True, 33, 65, 2048), (True, False, 5, 40, 129),
+])
+def test_gemm_relu_masked_equals_mask_then_gemm(ctx, ta, tb, M, N, K):
+    """tf_gemm_relu_masked (the ReLU backward applied as the small kernel
+    loads A) equals tf_relu_bwd followed by tf_gemm bit for bit: the masked
+    element is the same product dy * (y > 0 ? 1 : 0) and the GEMM the same
+    kernel.  The mask holds 0, -0 and +-1e-38 (strict > 0), and the product
+    is checked against float64 too."""
+    ops = _ops()
+    seed = synth.seed(2, 11) + M + N + K
+    shape_a = (K, M) if ta else (M, K)
+    a = synth.normal(seed, shape_a)
+    y = np.maximum(synth.normal(seed + 1, shape_a), 0.0).astype(np.float32)
+    y.flat[:4] = [0.0, -0.0, 1e-38, -1e-38]
+    b = synth.normal(seed + 2, (N, K) if tb else (K, N))
+    da, dy_, db = ctx.array(a), ctx.array(y), ctx.array(b)
+    got = ops.gemm_relu_masked(da, dy_, db, ctx.array(np.full((M, N), 7.0, np.float32)), trans_a=ta, trans_b=tb)
+    dz = ops.relu_bwd(da, dy_, ctx.empty(shape_a))
+    want = ops.gemm(dz, db, ctx.empty((M, N)), trans_a=ta, trans_b=tb)
+    assert_bitexact(got.numpy(), want.numpy(), f"masked gemm {M}x{N}x{K}")
+    assert_close(got.numpy(), _gemm_truth(oracle.relu_bwd(a, y), b, ta, tb), RTOL32, "masked gemm vs float64")
+    again = ops.gemm_relu_masked(da, dy_, db, ctx.empty((M, N)), trans_a=ta, trans_b=tb)
+    assert_bitexact(again.numpy(), got.numpy(), "second call")
+
+
+def test_gemm_relu_masked_outside_small_path(ctx):
+    """A product the small kernel does not take (K > 2048) is refused with
+    TF_ERR_UNSUPPORTED, and a narrow one (N <= 16, which plain tf_gemm sends
+    to another kernel) still takes the small kernel with the mask."""
+    ops = _ops()
+    a, y = ctx.array(np.ones((8, 4096), np.float32)), ctx.array(np.ones((8, 4096), np.float32))
+    with pytest.raises(Exception, match="small-product"):
+        ops.gemm_relu_masked(a, y, ctx.array(np.ones((4096, 40), np.float32)), ctx.empty((8, 40)))
+    a = synth.normal(901, (64, 256))
+    y = np.maximum(synth.normal(902, (64, 256)), 0.0).astype(np.float32)
+    b = synth.normal(903, (10, 256))
+    got = ops.gemm_relu_masked(ctx.array(a), ctx.array(y), ctx.array(b), ctx.empty((64, 10)), trans_b=True)
+    assert_close(got.numpy(), _gemm_truth(oracle.relu_bwd(a, y), b, False, True), RTOL32, "narrow masked")
+
+
 SIZES = [0, 1, 17, 1000, 4096 * 1024 + 3]
 
 
