@@ -816,32 +816,208 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
 }
 
 // dw[co][k] (k < K) and db[co] (k == K when KD = K + 1) = the sum over the
-// weight-gradient blocks b of part[b][co][k].  A workgroup owns 16
-// consecutive partial elements x 16 block groups; each thread adds blocks
-// g, g + 16, ... in ascending order (loads in flight together) and the 16
-// group sums are combined in a fixed tree order: deterministic.
+// weight-gradient blocks b of part[b][co][k].  A workgroup owns EL
+// consecutive partial elements x G = 256 / EL block groups; each thread adds
+// blocks g, g + G, ... in ascending order (16 loads in flight) and the G
+// group sums are combined in a fixed pairwise tree: deterministic.
+constexpr int kPsEl = 32;   // partial elements per workgroup (128-byte rows)
+template <int EL>
 __global__ __launch_bounds__(256) void conv_partial_sum_kernel(const float* __restrict__ part, int blocks,
                                                                int64_t plane, int K, int KD, float* __restrict__ dw,
                                                                float* __restrict__ db) {
-    __shared__ float red[16][17];
-    const int el = threadIdx.x & 15, g = threadIdx.x >> 4;
-    const int64_t i = (int64_t)blockIdx.x * 16 + el;
+    constexpr int G = 256 / EL;
+    __shared__ float red[G][EL + 1];
+    const int el = threadIdx.x % EL, g = threadIdx.x / EL;
+    const int64_t i = (int64_t)blockIdx.x * EL + el;
     float s = 0.0f;
     if (i < plane) {
-#pragma unroll 8
-        for (int b = g; b < blocks; b += 16) s += part[(int64_t)b * plane + i];
+        const float* src = part + i;
+        int b = g;
+        for (; b + 15 * G < blocks; b += 16 * G) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = src[(int64_t)(b + u * G) * plane];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) s += v[u];
+        }
+        for (; b < blocks; b += G) s += src[(int64_t)b * plane];
     }
     red[g][el] = s;
-    __syncthreads();
-    if (threadIdx.x >= 16 || i >= plane) return;
-    float t[8];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) t[q] = red[2 * q][el] + red[2 * q + 1][el];
-    const float sum = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+    for (int w = G / 2; w >= 1; w >>= 1) {
+        __syncthreads();
+        if (g < w) red[g][el] += red[g + w][el];
+    }
+    if (g != 0 || i >= plane) return;
+    const float sum = red[0][el];
     const int64_t co = i / KD;
     const int k = (int)(i - co * KD);
     if (k < K) dw[co * K + k] = sum;
     else db[co] = sum;
+}
+
+// ---------------------------------------------------------------------------
+// Streaming weight gradient for filters with few taps (K = C kH kW <= 31,
+// e.g. a first convolution over 3 input channels), where the implicit kernel
+// above waits on its staging round trips with little MFMA work to hide them.
+// A block takes kWsPixels consecutive pixels of one image and 32 output
+// channels.  The input patch those pixels read (a few KB) goes to LDS; dy
+// (and the ReLU output y) are read once, straight into registers, every
+// load of a thread issued before the patch is waited for (loads retire in
+// issue order, so the patch loads go first).  Lane (c = lane % 32,
+// h = lane / 32) of wave w holds dy[c][q .. q + 3] for the pixels
+// q = 8 j + 4 h of the wave's 8-pixel groups j and feeds them one pixel at a
+// time as the A operand of v_mfma_f32_32x32x2f32 (rows = output channels,
+// the two lane halves' pixels summed by the instruction), with B = the
+// patch value of tap k = lane % 32 at that pixel.  Column k = K carries
+// B = 1, so the same MFMAs form the bias gradient sum_p dy[c][p]; columns
+// past it carry 0.  The eight waves' 32 x 32 sums are added in wave order
+// through LDS and written as the block's partial (part[block][co][0 .. K],
+// db at K), which conv_partial_sum_kernel adds in a fixed order: the result
+// is deterministic and does not depend on the operands' alignment.
+// ---------------------------------------------------------------------------
+constexpr int kWsPixels = 512;                                // pixels per block
+constexpr int kWsGroups = kWsPixels / 8 / (kIgThreads / 64);  // 8-pixel groups per wave
+constexpr int kWsPatchSlots = 4;                              // 16-byte patch slots per thread
+constexpr int kWsMaxPatch = kWsPatchSlots * kIgThreads * 4;   // patch floats
+
+// Every load of the kernel below is unconditional (an address clamped into
+// the operand, then a select): a branch around a load makes the compiler
+// wait for all loads in flight where the paths join, which would put the
+// loads back in sequence.
+template <bool XVEC, bool DVEC, bool RELU>
+__global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_stream_kernel(
+    const float* __restrict__ x, const float* __restrict__ dy, const float* __restrict__ relu_y,
+    float* __restrict__ dz_out, float* __restrict__ part, ConvGeom g, int Cout, int K, int with_db, int PH, int PWs,
+    int L, int tiles_per_image) {
+    extern __shared__ float smem[];
+    const int C = (int)g.C, H = (int)g.H, W = (int)g.W, kHW = (int)(g.kH * g.kW), kW = (int)g.kW;
+    const int P = (int)(g.outH * g.outW), outW = (int)g.outW;
+    const int n = blockIdx.x / tiles_per_image, pt = blockIdx.x - n * tiles_per_image;
+    const int p0 = pt * kWsPixels, p_end = min(p0 + kWsPixels, P);
+    const int co0 = blockIdx.y * 32, nco = min(32, Cout - co0);
+    const int oh_lo = p0 / outW, ih_lo = oh_lo * (int)g.sh - (int)g.ph;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, l32 = lane & 31, half = lane >> 5;
+    const int spr = PWs / 4, nslots = C * PH * spr;
+    float* patch = smem;                                              // [C][PH][PWs]
+    int* poff = reinterpret_cast<int*>(smem + 4 * nslots);            // [kWsPixels]
+    float* red = reinterpret_cast<float*>(poff + kWsPixels);          // [8 waves][16][64]
+
+    // Patch slots (16 bytes each): patch[ci][rr][c] = x[ci][ih_lo + rr][c - L],
+    // zero outside the image.
+    const float* xn = x + (int64_t)n * C * H * W;
+    const FastDiv fspr = fast_div(spr), fPH = fast_div(PH);
+    v4f pv[kWsPatchSlots];
+#pragma unroll
+    for (int u = 0; u < kWsPatchSlots; ++u) {
+        const int i = min(t + kIgThreads * u, nslots - 1);
+        int sl, rr;
+        const int prow = divmod(i, fspr, sl);
+        const int ci = divmod(prow, fPH, rr);
+        const int ih = ih_lo + rr, iw = 4 * sl - L;
+        const bool row_ok = ih >= 0 && ih < H;
+        const int rbase = (ci * H + (row_ok ? ih : 0)) * W;
+        if (XVEC) {
+            const bool ok = row_ok && iw >= 0 && iw < W;
+            const v4f v = *reinterpret_cast<const v4f*>(xn + rbase + (ok ? iw : 0));
+            pv[u] = ok ? v : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool ok = row_ok && iw + e >= 0 && iw + e < W;
+                const float v = xn[rbase + (ok ? iw + e : 0)];
+                pv[u][e] = ok ? v : 0.0f;
+            }
+        }
+    }
+    // This lane's channel and pixels of dy (and y); zeros past the channels
+    // and pixels of the block.
+    const bool chan = l32 < nco;
+    const int64_t row = ((int64_t)n * Cout + co0 + (chan ? l32 : 0)) * P;
+    auto load4 = [&](const float* src, int p) -> v4f {
+        v4f v;
+        if (DVEC) {
+            const bool ok = chan && p < p_end;
+            v = *reinterpret_cast<const v4f*>(src + row + (ok ? p : p0));
+            if (!ok) v = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool ok = chan && p + e < p_end;
+                const float f = src[row + (ok ? p + e : p0)];
+                v[e] = ok ? f : 0.0f;
+            }
+        }
+        return v;
+    };
+    v4f gy[kWsGroups], gm[kWsGroups];
+#pragma unroll
+    for (int j = 0; j < kWsGroups; ++j) {
+        const int p = p0 + 8 * (wave * kWsGroups + j) + 4 * half;
+        gy[j] = load4(dy, p);
+        if (RELU) gm[j] = load4(relu_y, p);
+    }
+#pragma unroll
+    for (int u = 0; u < kWsPatchSlots; ++u) {
+        const int i = t + kIgThreads * u;
+        if (i < nslots) *reinterpret_cast<v4f*>(patch + 4 * i) = pv[u];
+    }
+    for (int q = t; q < kWsPixels; q += kIgThreads) {
+        const int pp = p0 + q < p_end ? p0 + q : p0;
+        const int oh = pp / outW, ow = pp - oh * outW;
+        poff[q] = (oh - oh_lo) * (int)g.sh * PWs + ow * (int)g.sw + L - (int)g.pw;
+    }
+    // Tap k = l32 of this lane; taps past K read a valid element and are
+    // replaced by bk (1 in the bias column, else 0).
+    const int kc = min(l32, K - 1);
+    const int ci = kc / kHW, rem = kc - ci * kHW, kh = rem / kW, kw = rem - kh * kW;
+    const int koff = (ci * PH + kh * (int)g.dh) * PWs + kw * (int)g.dw;
+    const bool tap = l32 < K;
+    const float bk = with_db && l32 == K ? 1.0f : 0.0f;
+    __syncthreads();
+
+    v16f acc = v16f{};
+#pragma unroll
+    for (int j = 0; j < kWsGroups; ++j) {
+        const int q = 8 * (wave * kWsGroups + j) + 4 * half;
+        const v4i po = *reinterpret_cast<const v4i*>(poff + q);
+        v4f d = gy[j];
+        if (RELU) {
+            // ReluBackward's dy * (y > 0 ? 1 : 0), and the masked gradient
+            // itself for a data gradient that follows (each element once).
+#pragma unroll
+            for (int e = 0; e < 4; ++e) d[e] *= gm[j][e] > 0.0f ? 1.0f : 0.0f;
+            if (dz_out && chan) {
+                const int p = p0 + q;
+                if (DVEC) {
+                    if (p < p_end) *reinterpret_cast<v4f*>(dz_out + row + p) = d;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (p + e < p_end) dz_out[row + p + e] = d[e];
+                }
+            }
+        }
+        const float r0 = patch[koff + po.x], r1 = patch[koff + po.y], r2 = patch[koff + po.z],
+                    r3 = patch[koff + po.w];
+        const float b0 = tap ? r0 : bk, b1 = tap ? r1 : bk, b2 = tap ? r2 : bk, b3 = tap ? r3 : bk;
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(d.x, b0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(d.y, b1, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(d.z, b2, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(d.w, b3, acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
+    __syncthreads();
+    const int KD = K + with_db;
+    float* outp = part + (int64_t)blockIdx.x * Cout * KD;
+    for (int e = t; e < 16 * 64; e += kIgThreads) {
+        const int r = e >> 6, ln = e & 63;
+        float v = red[r * 64 + ln];
+        for (int w = 1; w < kIgThreads / 64; ++w) v += red[(w * 16 + r) * 64 + ln];
+        const int co = co0 + 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3), k = ln & 31;
+        if (co < Cout && k < KD) outp[(int64_t)co * KD + k] = v;
+    }
 }
 
 // LDS layout of conv_bwd_weight_implicit_kernel, or 0 when it does not fit.
@@ -1493,6 +1669,50 @@ tf_status conv_bwd_weight_impl(tf_ctx* ctx, const float* x, const float* dy, con
         st = tf_hip_fill_f32(ctx, dw, 0.0f, Cout * K);
         return st == TF_OK && db ? tf_hip_fill_f32(ctx, db, 0.0f, Cout) : st;
     }
+    const int with_db = db ? 1 : 0;
+    const int64_t KD = K + with_db;
+    const int64_t plane = Cout * KD;
+    if (K <= 31) {
+        // Few filter taps: conv_bwd_weight_stream_kernel, when its patch fits.
+        const bool xal = g.W % 4 == 0 && aligned16(x);
+        int Ls, PWss;
+        patch_cols(g, xal, Ls, PWss);
+        const int PHs = (int)((rows_spanned(g.outH, g.outW, kWsPixels) - 1) * g.sh + (g.kH - 1) * g.dh + 1);
+        const int64_t pfl = C * (int64_t)PHs * PWss;
+        if (pfl <= kWsMaxPatch) {
+            const int64_t P = g.outH * g.outW;
+            const bool dvec = P % 4 == 0 && aligned16(dy) && (!relu_y || aligned16(relu_y)) && (!dz || aligned16(dz));
+            const int64_t tpi = (P + kWsPixels - 1) / kWsPixels;
+            const int64_t blocks = N * tpi;
+            TF_REQUIRE(blocks < (1LL << 31), "tf_conv2d_bwd_weight: too many blocks");
+            st = tfh::ensure_workspace(ctx, (size_t)blocks * Cout * KD * sizeof(float));
+            if (st != TF_OK) return st;
+            float* part = reinterpret_cast<float*>(ctx->ws);
+            // <= 32 + 2 + 32 KB: within the default dynamic LDS limit.
+            const size_t lds = (size_t)(pfl + kWsPixels + (kIgThreads / 64) * 16 * 64) * 4;
+            const dim3 grid((unsigned)blocks, (unsigned)((Cout + 31) / 32));
+            const int sel = (xal ? 4 : 0) | (dvec ? 2 : 0) | (relu_y ? 1 : 0);
+#define TF_WS_LAUNCH(XV, DV, RL)                                                                               \
+    conv_bwd_weight_stream_kernel<XV, DV, RL><<<grid, kIgThreads, lds, ctx->stream>>>(                      \
+        x, dy, relu_y, dz, part, g, (int)Cout, (int)K, with_db, PHs, PWss, Ls, (int)tpi)
+            switch (sel) {
+                case 0: TF_WS_LAUNCH(false, false, false); break;
+                case 1: TF_WS_LAUNCH(false, false, true); break;
+                case 2: TF_WS_LAUNCH(false, true, false); break;
+                case 3: TF_WS_LAUNCH(false, true, true); break;
+                case 4: TF_WS_LAUNCH(true, false, false); break;
+                case 5: TF_WS_LAUNCH(true, false, true); break;
+                case 6: TF_WS_LAUNCH(true, true, false); break;
+                default: TF_WS_LAUNCH(true, true, true); break;
+            }
+#undef TF_WS_LAUNCH
+            st = tfh::check_launch("conv_bwd_weight_stream_kernel");
+            if (st != TF_OK) return st;
+            conv_partial_sum_kernel<kPsEl><<<(unsigned)((plane + kPsEl - 1) / kPsEl), 256, 0, ctx->stream>>>(
+                part, (int)blocks, plane, (int)K, (int)KD, dw, db);
+            return tfh::check_launch("conv_partial_sum_kernel");
+        }
+    }
     const int MT = Cout <= 32 ? 32 : 64;
     int Kc, PH, PWs, L, slices;
     bool aligned;
@@ -1518,8 +1738,6 @@ tf_status conv_bwd_weight_impl(tf_ctx* ctx, const float* x, const float* dy, con
             lds_launch = (size_t)direct;
         }
     }
-    const int with_db = db ? 1 : 0;
-    const int64_t KD = K + with_db;
     st = tfh::ensure_workspace(ctx, (size_t)blocks * Cout * KD * sizeof(float));
     if (st != TF_OK) return st;
     float* part = reinterpret_cast<float*>(ctx->ws);
@@ -1543,9 +1761,8 @@ tf_status conv_bwd_weight_impl(tf_ctx* ctx, const float* x, const float* dy, con
             x, dy, part, g, (int)Cout, (int)K, Kc, PH, PWs, L, tpi, slices, vec, with_db, relu_y, dz);
     st = tfh::check_launch("conv_bwd_weight_implicit_kernel");
     if (st != TF_OK) return st;
-    const int64_t plane = Cout * KD;
-    conv_partial_sum_kernel<<<(unsigned)((plane + 15) / 16), 256, 0, ctx->stream>>>(part, (int)blocks, plane, (int)K,
-                                                                                  (int)KD, dw, db);
+    conv_partial_sum_kernel<kPsEl><<<(unsigned)((plane + kPsEl - 1) / kPsEl), 256, 0, ctx->stream>>>(
+        part, (int)blocks, plane, (int)K, (int)KD, dw, db);
     return tfh::check_launch("conv_partial_sum_kernel");
 }
 

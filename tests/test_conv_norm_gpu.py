@@ -340,11 +340,13 @@ class _Offset:
         self.ptr = base.ptr + 4
 
 
-@pytest.mark.parametrize("case", [(128, 32, 32, 32, 64, 3, 2, 1, 1), (3, 5, 13, 16, 40, 3, 1, 1, 1)])
+@pytest.mark.parametrize("case", [(128, 32, 32, 32, 64, 3, 2, 1, 1), (3, 5, 13, 16, 40, 3, 1, 1, 1),
+                                  (4, 3, 16, 20, 24, 3, 1, 1, 1), (2, 2, 9, 9, 40, 3, 1, 1, 1)])
 def test_conv2d_implicit_unaligned_operands_match_aligned(ctx, case):
     """Operands that are not 16-byte aligned take the scalar staging loads of
     the implicit kernels (forward, weight + bias gradient, both data-gradient
-    forms); the results equal the aligned calls bit for bit (same values,
+    forms) and the element-wise loads of the streaming weight gradient (the
+    last two shapes, K <= 31); the results equal the aligned calls bit for bit (same values,
     same summation order)."""
     ops = _ops()
     N, C, H, W, Cout, k, s, p, d = case
@@ -431,6 +433,7 @@ RELU_CASES = [
     (3, 5, 13, 17, 40, 3, 2, 0, 1),        # odd extents: partial pixel tiles and channel block
     (2, 4, 12, 11, 70, 3, 1, 2, 2),        # two channel blocks (64 + 6), dilation 2
     (5, 2, 15, 13, 20, 3, 2, 1, 2),        # slices of one tile over several waves
+    (3, 2, 9, 9, 40, 3, 1, 1, 1),          # 81 pixels (not a multiple of 4): element-wise dy, y and dz
 ]
 
 
