@@ -355,8 +355,8 @@ tf_status tf_gemm_relu_masked(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, 
  * layers, the two products of MatmulBackward (autograd/ops/MatmulBackward.hpp:26-34)
  * behind nn/Linear.cpp:60-63's x.matmul(W^T), the transpose of the weight
  * gradient (autograd/ops/TransposeBackward.hpp) and the bias column sum.
- * dx, dw or db may be NULL (not wanted).  Needs K % 4 == 0, M * N <= 16384,
- * x, w, dx, dw 16-byte aligned; dy is [M x N] contiguous.  Each block owns 64
+ * dx, dw or db may be NULL (not wanted).  Needs K % 4 == 0 and x, w, dx, dw
+ * 16-byte aligned; dy is [M x N] contiguous.  Each block owns 64
  * columns of K for every row, so nothing is summed across blocks:
  * deterministic, every output written once. */
 tf_status tf_linear_bwd_narrow(tf_ctx* ctx, const float* dy, const float* x, const float* w, float* dx, float* dw,

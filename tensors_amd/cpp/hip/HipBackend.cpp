@@ -483,7 +483,7 @@ bool linear_backward_narrow(const Tensor& dy, const Tensor& x, const Tensor& w, 
     };
     if (!f32(dy) || !f32(w) || (dw && !f32(x))) return false;
     const int64_t M = dy.shape()[0], N = dy.shape()[1], K = w.shape()[1];
-    if (w.shape()[0] != N || N > 16 || K % 4 != 0 || M * N > 16384 || K < 64) return false;
+    if (w.shape()[0] != N || N > 16 || K % 4 != 0 || K < 64) return false;
     if (dw && (x.shape()[0] != M || x.shape()[1] != K)) return false;
     const auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
     if (!a16(w.data()) || (dw && !a16(x.data()))) return false;

@@ -3114,81 +3114,107 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
 // (nn/Linear.cpp's backward as LinearBackward forms it: two GEMMs and a
 // column sum).  Block b owns columns 64 b .. 64 b + 63 of K for every row, so
 // dW needs no sum across blocks: thread t takes the column quad t % 16 of
-// rows t / 16, t / 16 + 16, ... (eight rows' X loads in flight), adds its
-// rows in ascending order, and the 16 row groups are added in order through
-// LDS.  dY (M x N) and the block's 64 columns of W sit in LDS; each thread
-// forms dX for the same rows and columns from them.  Block 0 also sums db
-// (rows in order).  Deterministic; every output written once.
+// rows t / 16, t / 16 + 16, ... (a batch of eight rows' X loads in flight),
+// adds its rows in ascending order, and the 16 row groups are added in order
+// through LDS.  dY goes through LDS a batch of 128 rows at a time (as laid
+// out in memory, read back as NP values a row, N rounded up to 4, zero past
+// N), and the block's 64 columns of W sit in registers, so the loops over n
+// have no branches and no load waits inside them.  All of a batch's loads
+// (dY, X, and W in the first batch) are in flight together.  Block 0 also
+// sums db (each row group's rows in order, then the 16 groups in order).
+// Deterministic; every output written once.
 // ---------------------------------------------------------------------------
-constexpr int kLnbCols = 64, kLnbMaxN = 16, kLnbRows = 8;
+constexpr int kLnbCols = 64, kLnbMaxN = 16, kLnbRows = 8, kLnbBatch = 16 * kLnbRows;
+template <int NP, bool DVEC>
 __global__ __launch_bounds__(256) void linear_bwd_narrow_kernel(const float* __restrict__ dy,
                                                                 const float* __restrict__ x,
                                                                 const float* __restrict__ w, float* __restrict__ dx,
                                                                 float* __restrict__ dw, float* __restrict__ db, int M,
                                                                 int N, int K) {
-    extern __shared__ float lnb[];
-    float* dys = lnb;                                    // [M][N]
-    float* ws = dys + (M * N + 3) / 4 * 4;               // [N][64]
-    float* red = ws + N * kLnbCols;                      // [16][N][64]
+    static_assert(NP % 4 == 0 && NP <= kLnbMaxN, "NP: N rounded up to 4, at most 16");
+    __shared__ float4 dys[kLnbBatch * kLnbMaxN / 4];    // one batch of dY rows, as in memory (N a row)
+    extern __shared__ float red[];                       // [16][N][64]
+    const float* dyf = reinterpret_cast<const float*>(dys);
     const int t = threadIdx.x, cq = t & 15, rg = t >> 4;
     const int k0 = blockIdx.x * kLnbCols, kq = k0 + 4 * cq;
     const bool colok = kq < K;                           // K % 4 == 0: a quad is wholly in or out
-    // The first batch of this thread's X rows is loaded before dY and W are
-    // staged, so the two round trips overlap.
-    float4 xv[kLnbRows];
-    auto load_x = [&](int rb) {
+    const int kc = colok ? kq : 0;
+    // X rows come from x when dW is wanted, else (values unused) from row 0
+    // of w, so the loads need no branch around them.
+    const float* xb = dw ? x : w;
+    const int64_t xld = dw ? K : 0;
+    float4 acc[NP];
 #pragma unroll
-        for (int u = 0; u < kLnbRows; ++u) {
-            const int r = rb + 16 * u;
-            xv[u] = dw && colok && r < M ? *reinterpret_cast<const float4*>(x + (int64_t)r * K + kq)
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
-    load_x(rg);
-    if ((M * N) % 4 == 0 && (reinterpret_cast<uintptr_t>(dy) & 15) == 0) {
-        for (int i = t; i < M * N / 4; i += 256)
-            reinterpret_cast<float4*>(dys)[i] = reinterpret_cast<const float4*>(dy)[i];
-    } else {
-        for (int i = t; i < M * N; i += 256) dys[i] = dy[i];
+    for (int n = 0; n < NP; ++n) acc[n] = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 wv[NP];
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+        const float4 v = *reinterpret_cast<const float4*>(w + (int64_t)min(n, N - 1) * K + kc);
+        wv[n] = n < N && colok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    for (int i = t; i < N * 16; i += 256) {
-        const int n = i >> 4, q = i & 15, k = k0 + 4 * q;
-        *reinterpret_cast<float4*>(ws + n * kLnbCols + 4 * q) =
-            k < K ? *reinterpret_cast<const float4*>(w + (int64_t)n * K + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    __syncthreads();
-    float4 wv[kLnbMaxN];
+    float dbv = 0.0f;
+    for (int rb0 = 0; rb0 < M; rb0 += kLnbBatch) {
+        // The batch's dY, then its X rows: in flight together with W's
+        // columns (clamped addresses, then a select); storing dY to LDS
+        // waits only for the loads issued before the X rows.
+        const int nfl = min(kLnbBatch, M - rb0) * N;     // the batch's dY floats
+        const float* dyb = dy + (int64_t)rb0 * N;
+        float4 dq[kLnbBatch * kLnbMaxN / 4 / 256];
 #pragma unroll
-    for (int n = 0; n < kLnbMaxN; ++n)
-        wv[n] = n < N ? *reinterpret_cast<const float4*>(ws + n * kLnbCols + 4 * cq) : make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 acc[kLnbMaxN];
+        for (int i = 0; i < kLnbBatch * kLnbMaxN / 4 / 256; ++i) {
+            const int j = t + 256 * i;
+            if (DVEC) {
+                const float4 v = *reinterpret_cast<const float4*>(dyb + 4 * min(j, nfl / 4 - 1));
+                dq[i] = 4 * j < nfl ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+            } else {
+                float e4[4];
 #pragma unroll
-    for (int n = 0; n < kLnbMaxN; ++n) acc[n] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int rb = rg; rb < M; rb += 16 * kLnbRows) {
-        if (rb != rg) load_x(rb);
-        // Predicates rather than early exits, so the loops unroll fully and
-        // the register arrays keep constant indices.
-#pragma unroll
-        for (int u = 0; u < kLnbRows; ++u) {
-            const int r = rb + 16 * u;
-            if (r < M) {
-                float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (int n = 0; n < kLnbMaxN; ++n) {
-                    if (n < N) {
-                        const float d = dys[r * N + n];
-                        acc[n].x += d * xv[u].x; acc[n].y += d * xv[u].y;
-                        acc[n].z += d * xv[u].z; acc[n].w += d * xv[u].w;
-                        o.x += d * wv[n].x; o.y += d * wv[n].y; o.z += d * wv[n].z; o.w += d * wv[n].w;
-                    }
+                for (int e = 0; e < 4; ++e) {
+                    const float v = dyb[min(4 * j + e, nfl - 1)];
+                    e4[e] = 4 * j + e < nfl ? v : 0.0f;
                 }
-                if (dx && colok) *reinterpret_cast<float4*>(dx + (int64_t)r * K + kq) = o;
+                dq[i] = make_float4(e4[0], e4[1], e4[2], e4[3]);
             }
+        }
+        float4 xv[kLnbRows];
+#pragma unroll
+        for (int u = 0; u < kLnbRows; ++u) {
+            const int r = rb0 + rg + 16 * u;
+            const float4 v = *reinterpret_cast<const float4*>(xb + (int64_t)min(r, M - 1) * xld + kc);
+            xv[u] = r < M && colok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (rb0 > 0) __syncthreads();                    // the previous batch's reads are done
+#pragma unroll
+        for (int i = 0; i < kLnbBatch * kLnbMaxN / 4 / 256; ++i) dys[t + 256 * i] = dq[i];
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < kLnbRows; ++u) {
+            const int rl = rg + 16 * u, r = rb0 + rl;
+            float d[NP];
+#pragma unroll
+            for (int n = 0; n < NP; ++n) {
+                const float v = dyf[rl * N + min(n, N - 1)];
+                d[n] = n < N ? v : 0.0f;
+            }
+            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int n = 0; n < NP; ++n) {
+                acc[n].x += d[n] * xv[u].x; acc[n].y += d[n] * xv[u].y;
+                acc[n].z += d[n] * xv[u].z; acc[n].w += d[n] * xv[u].w;
+                o.x += d[n] * wv[n].x; o.y += d[n] * wv[n].y; o.z += d[n] * wv[n].z; o.w += d[n] * wv[n].w;
+            }
+            if (dx && colok && r < M) *reinterpret_cast<float4*>(dx + (int64_t)r * K + kq) = o;
+        }
+        if (db && blockIdx.x == 0 && cq < N) {
+            // db: thread (column cq, row group rg) adds its rows of the batch.
+#pragma unroll
+            for (int u = 0; u < kLnbRows; ++u)
+                if (rb0 + rg + 16 * u < M) dbv += dyf[(rg + 16 * u) * N + cq];
         }
     }
     if (dw) {
 #pragma unroll
-        for (int n = 0; n < kLnbMaxN; ++n)
+        for (int n = 0; n < NP; ++n)
             if (n < N) *reinterpret_cast<float4*>(red + (rg * N + n) * kLnbCols + 4 * cq) = acc[n];
         __syncthreads();
         if (t < N * 16) {
@@ -3201,16 +3227,20 @@ __global__ __launch_bounds__(256) void linear_bwd_narrow_kernel(const float* __r
             if (k < K) *reinterpret_cast<float4*>(dw + (int64_t)n * K + k) = v;
         }
     }
-    if (db && blockIdx.x == 0 && t < N) {
-        float v = 0.0f;
-        for (int r = 0; r < M; ++r) v += dys[r * N + t];
-        db[t] = v;
+    if (db && blockIdx.x == 0) {
+        // The 16 row groups' db sums, added in group order.
+        __shared__ float dbs[16][kLnbMaxN];
+        if (cq < N) dbs[rg][cq] = dbv;
+        __syncthreads();
+        if (t < N) {
+            float v = dbs[0][t];
+            for (int g = 1; g < 16; ++g) v += dbs[g][t];
+            db[t] = v;
+        }
     }
 }
 
-size_t linear_bwd_narrow_lds(int64_t M, int64_t N) {
-    return (size_t)(((M * N + 3) / 4 * 4) + N * kLnbCols + 16 * N * kLnbCols) * sizeof(float);
-}
+size_t linear_bwd_narrow_lds(int64_t N) { return (size_t)(16 * N * kLnbCols) * sizeof(float); }
 
 }  // namespace
 
@@ -3282,7 +3312,6 @@ tf_status tf_linear_bwd_narrow(tf_ctx* ctx, const float* dy, const float* x, con
     TF_CTX_CHECK(ctx);
     TF_REQUIRE(M >= 0 && N >= 1 && N <= kLnbMaxN && K >= 0 && K % 4 == 0 && K < (1LL << 31) && M * K < (1LL << 40),
                "tf_linear_bwd_narrow: needs 1 <= N <= 16 outputs and K % 4 == 0");
-    TF_REQUIRE(M * N <= 16384, "tf_linear_bwd_narrow: dY (M x N) must fit 64 KB of LDS");
     if (M == 0 || K == 0) {
         if (dw) { tf_status st = tf_hip_fill_f32(ctx, dw, 0.0f, N * K); if (st != TF_OK) return st; }
         if (db) return tf_hip_fill_f32(ctx, db, 0.0f, N);
@@ -3292,15 +3321,44 @@ tf_status tf_linear_bwd_narrow(tf_ctx* ctx, const float* dy, const float* x, con
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     TF_REQUIRE(a16(w) && (!x || a16(x)) && (!dx || a16(dx)) && (!dw || a16(dw)),
                "tf_linear_bwd_narrow: x, w, dx and dw must be 16-byte aligned");
-    static const bool lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(linear_bwd_narrow_kernel),
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    static const bool lds_ok = [] {
+        const void* fns[] = {
+            reinterpret_cast<const void*>(linear_bwd_narrow_kernel<4, true>),
+            reinterpret_cast<const void*>(linear_bwd_narrow_kernel<8, true>),
+            reinterpret_cast<const void*>(linear_bwd_narrow_kernel<12, true>),
+            reinterpret_cast<const void*>(linear_bwd_narrow_kernel<16, true>),
+            reinterpret_cast<const void*>(linear_bwd_narrow_kernel<4, false>),
+            reinterpret_cast<const void*>(linear_bwd_narrow_kernel<8, false>),
+            reinterpret_cast<const void*>(linear_bwd_narrow_kernel<12, false>),
+            reinterpret_cast<const void*>(linear_bwd_narrow_kernel<16, false>)};
+        for (const void* f : fns)
+            if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)linear_bwd_narrow_lds(kLnbMaxN)) != hipSuccess)
+                return false;
+        return true;
+    }();
     if (!lds_ok) {
         (void)hipGetLastError();
         return tfh::set_error(TF_ERR_HIP, "tf_linear_bwd_narrow: hipFuncSetAttribute (dynamic LDS) failed");
     }
     const unsigned blocks = (unsigned)((K + kLnbCols - 1) / kLnbCols);
-    linear_bwd_narrow_kernel<<<blocks, 256, linear_bwd_narrow_lds(M, N), ctx->stream>>>(dy, x, w, dx, dw, db, (int)M,
-                                                                                        (int)N, (int)K);
+    const size_t lds = dw ? linear_bwd_narrow_lds(N) : 0;
+    const int np = (int)((N + 3) / 4 * 4);
+    const bool dvec = (M * N) % 4 == 0 && (reinterpret_cast<uintptr_t>(dy) & 15) == 0;
+#define TF_LNB_LAUNCH(NPV)                                                                                       \
+    do {                                                                                                         \
+        if (dvec)                                                                                                \
+            linear_bwd_narrow_kernel<NPV, true><<<blocks, 256, lds, ctx->stream>>>(dy, x, w, dx, dw, db, (int)M, \
+                                                                                   (int)N, (int)K);              \
+        else                                                                                                     \
+            linear_bwd_narrow_kernel<NPV, false><<<blocks, 256, lds, ctx->stream>>>(dy, x, w, dx, dw, db,        \
+                                                                                    (int)M, (int)N, (int)K);     \
+    } while (0)
+    if (np == 4) TF_LNB_LAUNCH(4);
+    else if (np == 8) TF_LNB_LAUNCH(8);
+    else if (np == 12) TF_LNB_LAUNCH(12);
+    else TF_LNB_LAUNCH(16);
+#undef TF_LNB_LAUNCH
     return tfh::check_launch("linear_bwd_narrow_kernel");
 }
 
