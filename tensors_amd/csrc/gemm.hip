@@ -2649,18 +2649,21 @@ __global__ __launch_bounds__(512) void gemm_f32_narrow_mfma_kernel(GemmParams p,
     __syncthreads();
     if (!last) return;
     if (mine) {
+        // The chunks' partials in chunk order, 32 loads in flight (clamped
+        // addresses; the ones past the last chunk are not added).
         const float* sp = p.partial + (int64_t)orow * N + j;
         const int64_t step = (int64_t)M * N;
         float s = 0.0f;
-        int k = 0;
-        for (; k + 8 <= chunks; k += 8) {
-            float t8[8];
+        for (int k = 0; k < chunks; k += 32) {
+            float t32[32];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) t8[u] = __hip_atomic_load(sp + (k + u) * step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int u = 0; u < 32; ++u)
+                t32[u] = __hip_atomic_load(sp + min(k + u, chunks - 1) * step, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-            for (int u = 0; u < 8; ++u) s += t8[u];
+            for (int u = 0; u < 32; ++u)
+                if (k + u < chunks) s += t32[u];
         }
-        for (; k < chunks; ++k) s += __hip_atomic_load(sp + k * step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         finish(s);
     }
     if (threadIdx.x == 0) __hip_atomic_store(tickets + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
