@@ -312,7 +312,7 @@ def bench_c1():
     return {"workload": "C1 MLP 784-256-128-10 fp32, batch 64, Linear+ReLU, CE chain, SGD momentum (lr 0.1, "
                         "mu 0.9), the reference's bias-free Linear; whole step through the C++ API",
             "ms_per_step": round(ms, 4), "ms_per_step_graph": round(ms_g, 4),
-            "flop_per_step": C1_FLOP, "bound": "launch latency (16 dependent kernels of 2-10 us)"}
+            "flop_per_step": C1_FLOP, "bound": "launch latency (11 dependent kernels of 4-9 us)"}
 
 
 # Config 4: the convolutions at batch 128 (N, Cin, H, Cout, stride); FLOP

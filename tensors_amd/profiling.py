@@ -78,7 +78,7 @@ _c4w1, _c4w2 = 32 * 27 * 4 + 32 * 4, 64 * 288 * 4 + 64 * 4
 C4_KERNELS = {
     "conv1_fwd": ("conv_fwd_implicit_kernel<32>", _c4x1 + _c4y1 + _c4w1),
     "conv2_fwd": ("conv_fwd_implicit_kernel<64>", _c4x2 + _c4y2 + _c4w2),
-    "conv1_dw_db": ("conv_bwd_weight_implicit_kernel<32>", _c4x1 + _c4y1 + _c4w1),
+    "conv1_dw_db": ("conv_bwd_weight_stream_kernel<true, true, false>", _c4x1 + _c4y1 + _c4w1),
     "conv2_dw_db": ("conv_bwd_weight_implicit_kernel<64>", _c4x2 + _c4y2 + _c4w2),
     "conv2_dx": ("conv_bwd_data_lds_kernel", _c4x2 + _c4y2 + _c4w2),
 }
