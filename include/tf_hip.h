@@ -349,6 +349,19 @@ tf_status tf_relu_bwd_colsum(tf_ctx* ctx, const void* dy, const void* x, void* d
 tf_status tf_gemm_relu_masked(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
                               const float* A, int64_t lda, const float* mask, const float* B, int64_t ldb, float* C,
                               int64_t ldc);
+/* Both weight-side products of a small bias-free Linear layer (y = x w^T,
+ * fp32) in one launch: dx = dz w (M x K) and dw = dz^T x (N x K), with
+ * dz = dy * (mask > 0 ? 1 : 0) when mask (shaped as dy) is given, else dy.
+ * dy and mask are [M x N], x and dx [M x K], w and dw [N x K], row-major.
+ * Replaces MatmulBackward's two products (autograd/ops/MatmulBackward.hpp:26-34)
+ * behind nn/Linear.cpp:60-63, and with a mask the ReluBackward before them
+ * (autograd/ops/ReluBackward.hpp:22-32).  Each block of the launch computes
+ * exactly what it computes in the product's own launch, so dx and dw are
+ * bit-identical to tf_gemm_relu_masked (tf_gemm without a mask) of each
+ * product.  TF_ERR_UNSUPPORTED when either product does not fit the
+ * small-product kernel (inner extent <= 2048, M*N*K <= 2^27). */
+tf_status tf_linear_bwd_small(tf_ctx* ctx, const float* dy, const float* mask, const float* x, const float* w,
+                              float* dx, float* dw, int64_t M, int64_t N, int64_t K);
 /* The whole backward of a Linear layer with few outputs (fp32, N <= 16), in
  * one launch: dx[r, k] = sum_n dy[r, n] w[n, k] (M x K), dw[n, k] =
  * sum_r dy[r, n] x[r, k] (N x K), db[n] = sum_r dy[r, n].  Replaces, for such

@@ -101,6 +101,7 @@ SIGNATURES: dict[str, list] = {
     "tf_relu_bwd_colsum": [_p, _p, _p, _p, _p, _i64, _i64, _i],
     "tf_linear_bwd_narrow": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64],
     "tf_gemm_relu_masked": [_p, _i, _i, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _p, _i64],
+    "tf_linear_bwd_small": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64],
     "tf_chansum_nchw": [_p, _p, _p, _i64, _i64, _i64],
     "tf_sgd_momentum": [_p, _p, _p, _p, _p, _i64, _f, _f],
     "tf_sgd_momentum_multi": [_p, _i, _p, _p, _p, _p, _p, _f, _f],

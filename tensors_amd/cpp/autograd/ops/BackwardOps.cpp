@@ -347,19 +347,27 @@ std::vector<Tensor> LinearBackward::apply(std::vector<Tensor>&& grads) {
     }
     Tensor dx, dw, db;
     bool dx_done = false, dw_done = false;
-    if (relu_) {
+    const bool gpu32 = gpu(dy) && dy.dtype() == Dtype::Float32 && grad_dtype_ == Dtype::Float32;
+    // Both products of a small layer in one launch (with the ReLU mask on
+    // dy's load when this node carries the ReLU); a head of at most 16
+    // outputs without ReLU takes the narrow kernel below instead, which also
+    // forms db.
+    if (gpu32 && wants(*this, 0) && wants(*this, 1) && (relu_ || w.shape()[0] > 16) &&
+        hip::linear_backward_small(dy, relu_ ? &relu_y_.unpack() : nullptr, x, w, dx, dw))
+        dx_done = dw_done = true;
+    if (relu_ && !(dx_done && dw_done && !(has_bias_ && wants(*this, 2)))) {
         // dz = dy * (y > 0) folded into the products' load of dy where the
         // kernel takes it; whatever remains gets the explicit masked dz.
         const Tensor& y = relu_y_.unpack();
-        if (gpu(dy) && dy.dtype() == Dtype::Float32 && grad_dtype_ == Dtype::Float32) {
-            if (wants(*this, 0)) {
+        if (gpu32) {
+            if (wants(*this, 0) && !dx_done) {
                 Tensor t = Tensor::empty(Shape{dy.shape()[0], w.shape()[1]}, Dtype::Float32, dy.device());
                 if (hip::gemm_relu_masked(dy, false, y, w, false, t)) {
                     dx = std::move(t);
                     dx_done = true;
                 }
             }
-            if (wants(*this, 1)) {
+            if (wants(*this, 1) && !dw_done) {
                 Tensor t = Tensor::empty(w.shape(), Dtype::Float32, dy.device());
                 if (hip::gemm_relu_masked(dy, true, y, x, false, t)) {
                     dw = std::move(t);

@@ -498,6 +498,29 @@ bool linear_backward_narrow(const Tensor& dy, const Tensor& x, const Tensor& w, 
     return true;
 }
 
+bool linear_backward_small(const Tensor& dy, const Tensor* mask, const Tensor& x, const Tensor& w, Tensor& dx,
+                           Tensor& dw) {
+    const auto f32 = [](const Tensor& t) {
+        return t.device().type == DeviceType::CUDA && t.dtype() == Dtype::Float32 && t.shape().ndim() == 2 &&
+               t.stride() == Stride::compute_row_major(t.shape());
+    };
+    if (!f32(dy) || !f32(x) || !f32(w) || (mask && (!f32(*mask) || mask->shape() != dy.shape()))) return false;
+    const int64_t M = dy.shape()[0], N = dy.shape()[1], K = w.shape()[1];
+    if (M == 0 || N == 0 || K == 0 || w.shape()[0] != N || x.shape()[0] != M || x.shape()[1] != K) return false;
+    if (x.device() != dy.device() || w.device() != dy.device() || (mask && mask->device() != dy.device())) return false;
+    Tensor tdx = Tensor::empty(Shape{M, K}, Dtype::Float32, dy.device());
+    Tensor tdw = Tensor::empty(Shape{N, K}, Dtype::Float32, dy.device());
+    const int st = tf_linear_bwd_small(ctx_of(dy), static_cast<const float*>(dy.data()),
+                                       mask ? static_cast<const float*>(mask->data()) : nullptr,
+                                       static_cast<const float*>(x.data()), static_cast<const float*>(w.data()),
+                                       static_cast<float*>(tdx.data()), static_cast<float*>(tdw.data()), M, N, K);
+    if (st == TF_ERR_UNSUPPORTED) return false;
+    check(st, "hip::linear_backward_small");
+    dx = std::move(tdx);
+    dw = std::move(tdw);
+    return true;
+}
+
 bool conv2d_forward_implicit(const Tensor& x, const Tensor& w, const Tensor* bias, Tensor& y, int64_t sh, int64_t sw,
                              int64_t ph, int64_t pw, int64_t dh, int64_t dw, bool relu) {
     require_gpu(x, "hip::conv2d_forward"); require_gpu(w, "hip::conv2d_forward"); require_gpu(y, "hip::conv2d_forward");

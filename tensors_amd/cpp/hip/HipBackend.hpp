@@ -136,6 +136,11 @@ void relu_backward_colsum(const Tensor& dy, const Tensor& x, Tensor& dz, Tensor&
 // each written when its pointer is given.  False (nothing launched) when
 // the shapes, dtypes or alignment do not fit that kernel.
 bool linear_backward_narrow(const Tensor& dy, const Tensor& x, const Tensor& w, Tensor* dx, Tensor* dw, Tensor* db);
+// dx = dz w and dw = dz^T x of a small Float32 Linear layer in one launch
+// (tf_linear_bwd_small), dz = dy * (mask > 0) when mask is given.  False
+// (nothing launched) when a product does not fit the small-product kernel.
+bool linear_backward_small(const Tensor& dy, const Tensor* mask, const Tensor& x, const Tensor& w, Tensor& dx,
+                           Tensor& dw);
 void chansum_nchw(const Tensor& dy, Tensor& db);
 // Implicit-GEMM convolution forward (tf_conv2d_fwd): false when the shape
 // does not fit the kernel's LDS (nothing was launched), else y is written.

@@ -2204,13 +2204,14 @@ __global__ __launch_bounds__(kF32DlThreads) void gemm_f32_dl_kernel(GemmParams p
 // set their 10-17 us per product.
 constexpr int kSmT = 32;    // tile side
 constexpr int kSmKC = 64;   // k per chunk
+// One block of a small product: block `bid` of its grid (tile, chunk group).
 template <bool A_KMAJ, bool B_KMAJ>
-__global__ __launch_bounds__(256) void gemm_f32_small_kernel(GemmParams p, int nchunks, int cps,
-                                                             unsigned* __restrict__ tickets) {
+__device__ __forceinline__ void small_gemm_block(const GemmParams& p, int bid, int nchunks, int cps,
+                                                 unsigned* __restrict__ tickets) {
     __shared__ float As[kSmKC][kSmT];   // As[k][m]
     __shared__ float Bs[kSmKC][kSmT];   // Bs[k][n]
     __shared__ int last;
-    const int tile = blockIdx.x / nchunks, chunk = blockIdx.x - tile * nchunks;
+    const int tile = bid / nchunks, chunk = bid - tile * nchunks;
     const int tm = tile / p.tiles_n, tn = tile - tm * p.tiles_n;
     const int m0 = tm * kSmT, n0 = tn * kSmT;
     const float* A = reinterpret_cast<const float*>(p.A);
@@ -2362,6 +2363,25 @@ __global__ __launch_bounds__(256) void gemm_f32_small_kernel(GemmParams p, int n
         const float bv = has_bias ? (p.row_bias ? p.bias[m] : p.bias[n]) : 0.0f;
         emit(p, (int64_t)m * p.ldc + n, acc[i], bv, relu);
     }
+}
+
+template <bool A_KMAJ, bool B_KMAJ>
+__global__ __launch_bounds__(256) void gemm_f32_small_kernel(GemmParams p, int nchunks, int cps,
+                                                             unsigned* __restrict__ tickets) {
+    small_gemm_block<A_KMAJ, B_KMAJ>(p, blockIdx.x, nchunks, cps, tickets);
+}
+
+// Two small products in one launch (a Linear layer's dX = dY W and
+// dW = dY^T X, which read the same dY): blocks [0, blocks1) are the first
+// product's grid, the rest the second's, each block exactly as in its own
+// launch (same tiles, chunk groups, order of sums), on separate arrival
+// counters and partial buffers.
+__global__ __launch_bounds__(256) void gemm_f32_small_pair_kernel(GemmParams p1, int nchunks1, int cps1,
+                                                                  unsigned* __restrict__ tickets1, int blocks1,
+                                                                  GemmParams p2, int nchunks2, int cps2,
+                                                                  unsigned* __restrict__ tickets2) {
+    if ((int)blockIdx.x < blocks1) small_gemm_block<true, false>(p1, blockIdx.x, nchunks1, cps1, tickets1);
+    else small_gemm_block<false, false>(p2, blockIdx.x - blocks1, nchunks2, cps2, tickets2);
 }
 
 // Split-K reduction: C = epi(alpha * sum_s partial[s] + beta * C), summing the
@@ -2848,6 +2868,21 @@ tf_status partials_buffer(tf_ctx* ctx, size_t need, bool noalloc, float** out) {
     return TF_OK;
 }
 
+// Grid of the small-product kernel for an M x N x K product: 32 x 32 tiles
+// and enough chunk groups for ~256 blocks, at most 32 per tile (the last
+// block adds them up), each of >= 1 chunk of 64 k.  False when the product
+// does not fit that kernel.
+bool small_grid(int64_t ncu, int64_t M, int64_t N, int64_t K, int64_t& tiles, int64_t& groups, int& cps) {
+    tiles = ((M + kSmT - 1) / kSmT) * ((N + kSmT - 1) / kSmT);
+    if (!(K > 0 && K <= 2048 && (double)M * (double)N * (double)K <= 134217728.0 && tiles <= tfh::kTicketGemmTiles))
+        return false;
+    const int64_t nkc = (K + kSmKC - 1) / kSmKC;
+    groups = std::min<int64_t>({nkc, 32, std::max<int64_t>(1, (ncu + tiles - 1) / tiles)});
+    cps = (int)((nkc + groups - 1) / groups);
+    groups = (nkc + cps - 1) / cps;
+    return true;
+}
+
 // `noalloc`: split-K partials go to the fixed scratch array (no pool call).
 tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                     const void* A, int64_t lda, int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b,
@@ -2953,17 +2988,11 @@ tf_status gemm_impl(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, int64_t N,
     }
     // Small fp32 products: 32 x 32 tiles with K over many blocks (see
     // gemm_f32_small_kernel).
-    const int64_t sm_tiles = ((M + kSmT - 1) / kSmT) * ((N + kSmT - 1) / kSmT);
-    if (in_dtype == TF_F32 && batch == 1 && K > 0 && K <= 2048 && (double)M * (double)N * (double)K <= 134217728.0 &&
-        sm_tiles <= tfh::kTicketGemmTiles) {
+    int64_t sm_tiles = 0, groups = 0;
+    int cps = 0;
+    if (in_dtype == TF_F32 && batch == 1 && small_grid(ncu, M, N, K, sm_tiles, groups, cps)) {
         p.tiles_m = (int)((M + kSmT - 1) / kSmT);
         p.tiles_n = (int)((N + kSmT - 1) / kSmT);
-        const int64_t nkc = (K + kSmKC - 1) / kSmKC;
-        // Enough chunk groups for ~256 blocks, at most 32 per tile (the
-        // last block adds them up), each of >= 1 chunk.
-        int64_t groups = std::min<int64_t>({nkc, 32, std::max<int64_t>(1, (ncu + sm_tiles - 1) / sm_tiles)});
-        const int cps = (int)((nkc + groups - 1) / groups);
-        groups = (nkc + cps - 1) / cps;
         if (groups > 1) {
             const size_t need = (size_t)sm_tiles * (size_t)groups * kSmT * kSmT * sizeof(float);
             tf_status st = partials_buffer(ctx, need, noalloc, &p.partial);
@@ -3308,6 +3337,50 @@ tf_status tf_gemm_relu_masked(tf_ctx* ctx, int trans_a, int trans_b, int64_t M, 
     tfh::TimedLaunch timed(ctx, M, N, K, 1, trans_a, trans_b, TF_F32, TF_F32);
     return gemm_impl(ctx, trans_a, trans_b, M, N, K, 1.0f, A, lda, 0, B, ldb, 0, 0.0f, C, ldc, 0, 1, 0, TF_F32,
                      TF_F32, TF_EPI_NONE, nullptr, false, mask);
+}
+
+tf_status tf_linear_bwd_small(tf_ctx* ctx, const float* dy, const float* mask, const float* x, const float* w,
+                              float* dx, float* dw, int64_t M, int64_t N, int64_t K) {
+    TF_CTX_CHECK(ctx);
+    TF_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31),
+               "tf_linear_bwd_small: extents must be positive");
+    TF_REQUIRE(dy && x && w && dx && dw, "tf_linear_bwd_small: null pointer");
+    // dX = dZ W: M x K over N (A = dZ K-major, B = W rows); dW = dZ^T X:
+    // N x K over M (A = dZ read transposed, B = X rows).
+    int64_t t1, g1, t2, g2;
+    int c1, c2;
+    if (!small_grid(ctx->num_cus, M, K, N, t1, g1, c1) || !small_grid(ctx->num_cus, N, K, M, t2, g2, c2) ||
+        t1 + t2 > tfh::kTicketGemmTiles)
+        return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_linear_bwd_small: a product does not fit the small-product kernel "
+                                                  "(K <= 2048 and M*N*K <= 2^27 for each)");
+    auto params = [&](const float* B, float* C, int64_t Mi, int64_t Ni, int64_t Ki) {
+        GemmParams q{};
+        q.A = dy; q.B = B; q.C = C;
+        q.lda = N; q.ldb = K; q.ldc = K;
+        q.M = (int)Mi; q.N = (int)Ni; q.K = (int)Ki;
+        q.tiles_m = (int)((Mi + kSmT - 1) / kSmT);
+        q.tiles_n = (int)((Ni + kSmT - 1) / kSmT);
+        q.reduce_batch = 1;
+        q.alpha = 1.0f; q.beta = 0.0f; q.epi = TF_EPI_NONE;
+        q.vec_a = aligned16(dy) && N % 4 == 0 && (!mask || aligned16(mask));
+        q.vec_b = aligned16(B) && K % 4 == 0;
+        q.mask_a = mask;
+        return q;
+    };
+    GemmParams p1 = params(w, dx, M, K, N), p2 = params(x, dw, N, K, M);
+    const size_t part1 = g1 > 1 ? (size_t)t1 * g1 * kSmT * kSmT * sizeof(float) : 0;
+    const size_t part2 = g2 > 1 ? (size_t)t2 * g2 * kSmT * kSmT * sizeof(float) : 0;
+    if (part1 + part2 > 0) {
+        tf_status st = tfh::ensure_workspace(ctx, part1 + part2);
+        if (st != TF_OK) return st;
+        p1.partial = reinterpret_cast<float*>(ctx->ws);
+        p2.partial = reinterpret_cast<float*>(reinterpret_cast<char*>(ctx->ws) + part1);
+    }
+    const int blocks1 = (int)(t1 * g1), blocks2 = (int)(t2 * g2);
+    unsigned* tickets = ctx->tickets + tfh::kTicketGemm;
+    gemm_f32_small_pair_kernel<<<(unsigned)(blocks1 + blocks2), 256, 0, ctx->stream>>>(
+        p1, (int)g1, c1, tickets, blocks1, p2, (int)g2, c2, tickets + t1);
+    return tfh::check_launch("gemm_f32_small_pair_kernel");
 }
 
 tf_status tf_linear_bwd_narrow(tf_ctx* ctx, const float* dy, const float* x, const float* w, float* dx, float* dw,

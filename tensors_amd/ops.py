@@ -213,6 +213,19 @@ def relu_bwd_colsum(dy, x, dz, db):
     return dz, db
 
 
+def linear_bwd_small(dy, x, w, dx, dw, mask=None):
+    """dx = dz w and dw = dz^T x in one launch (tf_linear_bwd_small), dz = dy
+    masked by mask > 0 when a mask is given.  dy [M, N], x [M, K], w [N, K]."""
+    M, N = dy.shape
+    K = w.shape[1]
+    if tuple(w.shape) != (N, K) or tuple(x.shape) != (M, K) or tuple(dx.shape) != (M, K) or \
+            tuple(dw.shape) != (N, K) or (mask is not None and tuple(mask.shape) != (M, N)):
+        raise ValueError("linear_bwd_small: shape mismatch")
+    call("tf_linear_bwd_small", _ctx(dy), dy.ptr, mask.ptr if mask is not None else None, x.ptr, w.ptr, dx.ptr,
+         dw.ptr, M, N, K)
+    return dx, dw
+
+
 def linear_bwd_narrow(dy, x, w, dx=None, dw=None, db=None):
     """The backward of a Linear layer with at most 16 outputs in one launch
     (tf_linear_bwd_narrow): dx = dy w, dw = dy^T x, db = column sums of dy;

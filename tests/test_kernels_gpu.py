@@ -598,6 +598,54 @@ def test_gemm_relu_masked_equals_mask_then_gemm(ctx, ta, tb, M, N, K):
     assert_bitexact(again.numpy(), got.numpy(), "second call")
 
 
+@pytest.mark.parametrize("M,N,K,masked", [
+    (64, 128, 256, True),      # config 1: the second layer's backward (dX 64 x 256, dW 128 x 256)
+    (64, 128, 256, False),
+    (50, 40, 70, True),        # ragged tiles in both products
+    (3, 300, 33, False),       # one row group; dW over a 3-deep batch
+])
+def test_linear_bwd_small_equals_two_products(ctx, M, N, K, masked):
+    """tf_linear_bwd_small (dX = dZ W and dW = dZ^T X in one launch, dZ = dY
+    masked by y > 0 or dY itself) equals the two products launched alone bit
+    for bit, twice in a row (the arrival counters are back at zero after each
+    call), and float64 within the fp32 tolerance."""
+    ops = _ops()
+    seed = synth.seed(2, 13) + M + N + K
+    dy = synth.normal(seed, (M, N))
+    y = np.maximum(synth.normal(seed + 1, (M, N)), 0.0).astype(np.float32)
+    x = synth.normal(seed + 2, (M, K))
+    w = synth.normal(seed + 3, (N, K), std=0.1)
+    d_dy, d_y, d_x, d_w = ctx.array(dy), ctx.array(y), ctx.array(x), ctx.array(w)
+    mask = d_y if masked else None
+    if masked:
+        want_dx = ops.gemm_relu_masked(d_dy, d_y, d_w, ctx.empty((M, K))).numpy()
+        want_dw = ops.gemm_relu_masked(d_dy, d_y, d_x, ctx.empty((N, K)), trans_a=True).numpy()
+    else:
+        want_dx = ops.gemm(d_dy, d_w, ctx.empty((M, K))).numpy()
+        want_dw = ops.gemm(d_dy, d_x, ctx.empty((N, K)), trans_a=True).numpy()
+    dz = oracle.relu_bwd(dy, y) if masked else dy
+    for call in range(2):
+        dx = ctx.array(np.full((M, K), 7.0, np.float32))
+        dw = ctx.array(np.full((N, K), 7.0, np.float32))
+        ops.linear_bwd_small(d_dy, d_x, d_w, dx, dw, mask=mask)
+        assert_bitexact(dx.numpy(), want_dx, f"dx call {call}")
+        assert_bitexact(dw.numpy(), want_dw, f"dw call {call}")
+    assert_close(want_dx, _gemm_truth(dz, w, False, False), RTOL32, "dx vs float64")
+    assert_close(want_dw, _gemm_truth(dz, x, True, False), RTOL32, "dw vs float64")
+
+
+def test_linear_bwd_small_rejects_large_products(ctx):
+    """A product whose inner extent exceeds the small kernel's 2048 is
+    refused with TF_ERR_UNSUPPORTED (the Linear backward then launches the
+    products separately)."""
+    from tensors_amd._lib import TF_ERR_UNSUPPORTED, TFError
+    ops = _ops()
+    dy, x, w = ctx.zeros((4, 3000)), ctx.zeros((4, 8)), ctx.zeros((3000, 8))
+    with pytest.raises(TFError) as e:
+        ops.linear_bwd_small(dy, x, w, ctx.empty((4, 8)), ctx.empty((3000, 8)))
+    assert e.value.status == TF_ERR_UNSUPPORTED
+
+
 def test_gemm_relu_masked_outside_small_path(ctx):
     """A product the small kernel does not take (K > 2048) is refused with
     TF_ERR_UNSUPPORTED, and a narrow one (N <= 16, which plain tf_gemm sends
