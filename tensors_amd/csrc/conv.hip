@@ -466,6 +466,44 @@ __device__ __forceinline__ v16f mfma_gather_loop(const float* wrow, const int* k
     return acc;
 }
 
+// Two tiles' mfma_gather_loop at once over the same pixels (the tap rows
+// krow shared): A rows wrow0 / wrow1 and patch bases pbase0 / pbase1.  The
+// two accumulators' MFMAs alternate, so each waits on its own chain only and
+// the matrix pipe has the other's to run meanwhile; each accumulator sees
+// the same MFMAs in the same order as in mfma_gather_loop.
+__device__ __forceinline__ void mfma_gather_loop2(const float* wrow0, const float* wrow1, const int* krow,
+                                                  const float* pbase0, const float* pbase1, int KH2, v16f& acc0,
+                                                  v16f& acc1) {
+    acc0 = v16f{};
+    acc1 = v16f{};
+    v4f a0 = *reinterpret_cast<const v4f*>(wrow0), a1 = *reinterpret_cast<const v4f*>(wrow1);
+    v4i kn = *reinterpret_cast<const v4i*>(krow);
+    float b0 = pbase0[kn.x], b1 = pbase0[kn.y], b2 = pbase0[kn.z], b3 = pbase0[kn.w];
+    float e0 = pbase1[kn.x], e1 = pbase1[kn.y], e2 = pbase1[kn.z], e3 = pbase1[kn.w];
+    kn = *reinterpret_cast<const v4i*>(krow + min(4, KH2 - 4));
+    for (int j = 0; j < KH2; j += 4) {
+        const v4i kn2 = *reinterpret_cast<const v4i*>(krow + min(j + 8, KH2 - 4));
+        const v4f an0 = *reinterpret_cast<const v4f*>(wrow0 + min(j + 4, KH2 - 4));
+        const v4f an1 = *reinterpret_cast<const v4f*>(wrow1 + min(j + 4, KH2 - 4));
+        const float c0 = pbase0[kn.x], c1 = pbase0[kn.y], c2 = pbase0[kn.z], c3 = pbase0[kn.w];
+        const float d0 = pbase1[kn.x], d1 = pbase1[kn.y], d2 = pbase1[kn.z], d3 = pbase1[kn.w];
+        __builtin_amdgcn_sched_barrier(0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.x, b0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.x, e0, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.y, b1, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.y, e1, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.z, b2, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.z, e2, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.w, b3, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.w, e3, acc1, 0, 0, 0);
+        a0 = an0;
+        a1 = an1;
+        b0 = c0; b1 = c1; b2 = c2; b3 = c3;
+        e0 = d0; e1 = d1; e2 = d2; e3 = d3;
+        kn = kn2;
+    }
+}
+
 // acc += the k steps j0 .. j1 - 1 of 8 k each, lane half h taking k =
 // 8 j + 4 h .. 8 j + 4 h + 3 (wrow and krow already offset by 4 h), with the
 // next step's reads in flight during the current four MFMAs as above.
@@ -781,7 +819,35 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
             if (lane == 0 && co0 + r < Cout) outp[(int64_t)(co0 + r) * KD + K] = v;
         }
     }
-    for (int item = wave; item < T * slices; item += kIgThreads / 64) {
+    auto store_tile = [&](int tile, const v16f& acc) {
+        const int tr = tile / TK, tc = tile - tr * TK, k = tc * 32 + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int co = co0 + tr * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (co < Cout && k < K) outp[(int64_t)co * KD + k] = acc[r];
+        }
+    };
+    if (slices == 1) {
+        // Tiles wave, wave + 8 as a pair (two MFMA chains), then the next
+        // pair: the same tiles per wave as one at a time.
+        const int q0 = half * NH;
+        for (int tile = wave; tile < T; tile += 2 * (kIgThreads / 64)) {
+            const int tile2 = tile + kIgThreads / 64;
+            const int tr = tile / TK, tc = tile - tr * TK;
+            if (tile2 < T) {
+                const int tr2 = tile2 / TK, tc2 = tile2 - tr2 * TK;
+                v16f acc0, acc1;
+                mfma_gather_loop2(dyt + (tr * 32 + l32) * RS + q0, dyt + (tr2 * 32 + l32) * RS + q0, poff + q0,
+                                  patch + koff[tc * 32 + l32], patch + koff[tc2 * 32 + l32], NH, acc0, acc1);
+                store_tile(tile, acc0);
+                store_tile(tile2, acc1);
+            } else {
+                store_tile(tile, mfma_gather_loop(dyt + (tr * 32 + l32) * RS + q0, poff + q0,
+                                                  patch + koff[tc * 32 + l32], NH));
+            }
+        }
+    }
+    for (int item = wave; slices > 1 && item < T * slices; item += kIgThreads / 64) {
         const int tile = item / slices, sl = item - tile * slices;
         const int tr = tile / TK, tc = tile - tr * TK;
         const int q0 = half * NH + sl * steps;
