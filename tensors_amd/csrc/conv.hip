@@ -533,6 +533,44 @@ __device__ __forceinline__ v16f mfma_gather_steps(v16f acc, const float* wrow, c
     return acc;
 }
 
+// mfma_gather_steps with the steps split over two accumulators by the
+// parity of j (even steps into acc0, odd into acc1), so consecutive steps'
+// MFMAs do not wait on each other; the caller adds acc0 + acc1.  Which
+// accumulator a step goes to depends only on j, so splitting a range
+// [j0, j1) into several calls gives the same sums.
+__device__ __forceinline__ void mfma_gather_steps2(v16f& acc0, v16f& acc1, const float* wrow, const int* krow,
+                                                   const float* pbase, int j0, int j1) {
+    if (j0 >= j1) return;
+    v4f a = *reinterpret_cast<const v4f*>(wrow + 8 * j0);
+    v4i kn = *reinterpret_cast<const v4i*>(krow + 8 * j0);
+    float b0 = pbase[kn.x], b1 = pbase[kn.y], b2 = pbase[kn.z], b3 = pbase[kn.w];
+    kn = *reinterpret_cast<const v4i*>(krow + 8 * min(j0 + 1, j1 - 1));
+    int j = j0;
+    auto step = [&](v16f& acc) __attribute__((always_inline)) {
+        const v4i kn2 = *reinterpret_cast<const v4i*>(krow + 8 * min(j + 2, j1 - 1));
+        const v4f an = *reinterpret_cast<const v4f*>(wrow + 8 * min(j + 1, j1 - 1));
+        const float c0 = pbase[kn.x], c1 = pbase[kn.y], c2 = pbase[kn.z], c3 = pbase[kn.w];
+        __builtin_amdgcn_sched_barrier(0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b1, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b2, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b3, acc, 0, 0, 0);
+        a = an;
+        b0 = c0;
+        b1 = c1;
+        b2 = c2;
+        b3 = c3;
+        kn = kn2;
+        ++j;
+    };
+    if (j & 1) step(acc1);
+    while (j + 1 < j1) {
+        step(acc0);
+        step(acc1);
+    }
+    if (j < j1) step(acc0);
+}
+
 template <int MT>
 __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const float* __restrict__ x,
                                                                        const float* __restrict__ w,
@@ -597,8 +635,16 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
         }
         __builtin_amdgcn_s_waitcnt(tfd::waitcnt_vm(0));
         __syncthreads();
-        acc = mfma_gather_steps(v16f{}, wkd + (m_sub * 32 + l32) * RS + 4 * half, koffd + 4 * half, patchd + pix_off,
-                                0, KS);
+        const float* wrow = wkd + (m_sub * 32 + l32) * RS + 4 * half;
+        if constexpr (MT == 64) {
+            // Two accumulators (a register cost that the 32-channel form,
+            // two blocks a CU, cannot pay).
+            v16f acc0 = v16f{}, acc1 = v16f{};
+            mfma_gather_steps2(acc0, acc1, wrow, koffd + 4 * half, patchd + pix_off, 0, KS);
+            acc = acc0 + acc1;
+        } else {
+            acc = mfma_gather_steps(v16f{}, wrow, koffd + 4 * half, patchd + pix_off, 0, KS);
+        }
     } else {
 
     // Two phases: the k steps whose taps lie in the first CA channels, then
@@ -631,15 +677,19 @@ __global__ __launch_bounds__(kIgThreads) void conv_fwd_implicit_kernel(const flo
 
     const float* wrow = wk + (m_sub * 32 + l32) * RS + 4 * half;
     const int* krow = koff + 4 * half;
-    acc = mfma_gather_steps(v16f{}, wrow, krow, patch + pix_off, 0, KA8);
+    v16f acc0 = v16f{}, acc1 = v16f{};
+    if constexpr (MT == 64) mfma_gather_steps2(acc0, acc1, wrow, krow, patch + pix_off, 0, KA8);
+    else acc0 = mfma_gather_steps(acc0, wrow, krow, patch + pix_off, 0, KA8);
     if (KA8 < KS) {
         ahead_w.store(wk, n_wb);
         stage_slots(w_b, wk, kAhead * kIgThreads, n_wb);
         ahead_p.store(patch, n_pb);
         stage_slots(p_b, patch, kAhead * kIgThreads, n_pb);
         __syncthreads();
-        acc = mfma_gather_steps(acc, wrow, krow, patch + pix_off, KA8, KS);
+        if constexpr (MT == 64) mfma_gather_steps2(acc0, acc1, wrow, krow, patch + pix_off, KA8, KS);
+        else acc0 = mfma_gather_steps(acc0, wrow, krow, patch + pix_off, KA8, KS);
     }
+    acc = MT == 64 ? acc0 + acc1 : acc0;
     }
 
     if (pp >= p_end) return;
