@@ -466,27 +466,32 @@ __device__ __forceinline__ v16f mfma_gather_loop(const float* wrow, const int* k
     return acc;
 }
 
-// Two tiles' mfma_gather_loop at once over the same pixels (the tap rows
-// krow shared): A rows wrow0 / wrow1 and patch bases pbase0 / pbase1.  The
-// two accumulators' MFMAs alternate, so each waits on its own chain only and
+// Two mfma_gather_loop chains at once: A rows wrow0 / wrow1, tap rows
+// krow0 / krow1 (the same rows when SAME_K: two tiles over the same
+// pixels, read once) and patch bases pbase0 / pbase1.  The two
+// accumulators' MFMAs alternate, so each waits on its own chain only and
 // the matrix pipe has the other's to run meanwhile; each accumulator sees
 // the same MFMAs in the same order as in mfma_gather_loop.
-__device__ __forceinline__ void mfma_gather_loop2(const float* wrow0, const float* wrow1, const int* krow,
-                                                  const float* pbase0, const float* pbase1, int KH2, v16f& acc0,
-                                                  v16f& acc1) {
+template <bool SAME_K>
+__device__ __forceinline__ void mfma_gather_loop2(const float* wrow0, const float* wrow1, const int* krow0,
+                                                  const int* krow1, const float* pbase0, const float* pbase1, int KH2,
+                                                  v16f& acc0, v16f& acc1) {
     acc0 = v16f{};
     acc1 = v16f{};
     v4f a0 = *reinterpret_cast<const v4f*>(wrow0), a1 = *reinterpret_cast<const v4f*>(wrow1);
-    v4i kn = *reinterpret_cast<const v4i*>(krow);
+    v4i kn = *reinterpret_cast<const v4i*>(krow0);
+    v4i km = SAME_K ? kn : *reinterpret_cast<const v4i*>(krow1);
     float b0 = pbase0[kn.x], b1 = pbase0[kn.y], b2 = pbase0[kn.z], b3 = pbase0[kn.w];
-    float e0 = pbase1[kn.x], e1 = pbase1[kn.y], e2 = pbase1[kn.z], e3 = pbase1[kn.w];
-    kn = *reinterpret_cast<const v4i*>(krow + min(4, KH2 - 4));
+    float e0 = pbase1[km.x], e1 = pbase1[km.y], e2 = pbase1[km.z], e3 = pbase1[km.w];
+    kn = *reinterpret_cast<const v4i*>(krow0 + min(4, KH2 - 4));
+    km = SAME_K ? kn : *reinterpret_cast<const v4i*>(krow1 + min(4, KH2 - 4));
     for (int j = 0; j < KH2; j += 4) {
-        const v4i kn2 = *reinterpret_cast<const v4i*>(krow + min(j + 8, KH2 - 4));
+        const v4i kn2 = *reinterpret_cast<const v4i*>(krow0 + min(j + 8, KH2 - 4));
+        const v4i km2 = SAME_K ? kn2 : *reinterpret_cast<const v4i*>(krow1 + min(j + 8, KH2 - 4));
         const v4f an0 = *reinterpret_cast<const v4f*>(wrow0 + min(j + 4, KH2 - 4));
         const v4f an1 = *reinterpret_cast<const v4f*>(wrow1 + min(j + 4, KH2 - 4));
         const float c0 = pbase0[kn.x], c1 = pbase0[kn.y], c2 = pbase0[kn.z], c3 = pbase0[kn.w];
-        const float d0 = pbase1[kn.x], d1 = pbase1[kn.y], d2 = pbase1[kn.z], d3 = pbase1[kn.w];
+        const float d0 = pbase1[km.x], d1 = pbase1[km.y], d2 = pbase1[km.z], d3 = pbase1[km.w];
         __builtin_amdgcn_sched_barrier(0);
         acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.x, b0, acc0, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.x, e0, acc1, 0, 0, 0);
@@ -501,6 +506,7 @@ __device__ __forceinline__ void mfma_gather_loop2(const float* wrow0, const floa
         b0 = c0; b1 = c1; b2 = c2; b3 = c3;
         e0 = d0; e1 = d1; e2 = d2; e3 = d3;
         kn = kn2;
+        km = km2;
     }
 }
 
@@ -887,13 +893,20 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_weight_implicit_kernel(co
             if (tile2 < T) {
                 const int tr2 = tile2 / TK, tc2 = tile2 - tr2 * TK;
                 v16f acc0, acc1;
-                mfma_gather_loop2(dyt + (tr * 32 + l32) * RS + q0, dyt + (tr2 * 32 + l32) * RS + q0, poff + q0,
-                                  patch + koff[tc * 32 + l32], patch + koff[tc2 * 32 + l32], NH, acc0, acc1);
+                mfma_gather_loop2<true>(dyt + (tr * 32 + l32) * RS + q0, dyt + (tr2 * 32 + l32) * RS + q0, poff + q0,
+                                        poff + q0, patch + koff[tc * 32 + l32], patch + koff[tc2 * 32 + l32], NH, acc0,
+                                        acc1);
                 store_tile(tile, acc0);
                 store_tile(tile2, acc1);
             } else {
-                store_tile(tile, mfma_gather_loop(dyt + (tr * 32 + l32) * RS + q0, poff + q0,
-                                                  patch + koff[tc * 32 + l32], NH));
+                // A tile without a partner: its pixels' two halves as the two
+                // chains, added at the end.
+                v16f acc0, acc1;
+                const float* wrow = dyt + (tr * 32 + l32) * RS + q0;
+                const float* pb = patch + koff[tc * 32 + l32];
+                mfma_gather_loop2<false>(wrow, wrow + NH / 2, poff + q0, poff + q0 + NH / 2, pb, pb, NH / 2, acc0,
+                                         acc1);
+                store_tile(tile, acc0 + acc1);
             }
         }
     }
