@@ -1365,6 +1365,152 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_data_implicit_kernel(cons
 constexpr int kDlxRB = 256 + 16;     // B row stride (words)
 constexpr int kDlxRD = 256 + 4;      // D row stride (words)
 
+// Tap tables of the col2im from LDS (NT threads build them): per input row
+// ih, rcnt[ih] taps with D offsets roff[ih kH + a] = ki kW RD + oh outW (ki
+// ascending); per input column iw, ccnt[iw] taps with offsets
+// coff[iw kW + b] = kj RD + ow (kj ascending).
+template <int NT>
+__device__ __forceinline__ void build_tap_tables(const ConvGeom& g, int* rcnt, int* roff, int* ccnt, int* coff,
+                                                 int t) {
+    const int H = (int)g.H, W = (int)g.W, kH = (int)g.kH, kW = (int)g.kW, outH = (int)g.outH, outW = (int)g.outW;
+    const int sh = (int)g.sh, sw = (int)g.sw, dh = (int)g.dh, dwl = (int)g.dw, ph = (int)g.ph, pw = (int)g.pw;
+    for (int ih = t; ih < H; ih += NT) {
+        int c = 0;
+        for (int ki = 0; ki < kH; ++ki) {
+            const int hh = ih + ph - ki * dh;
+            if (hh >= 0 && hh % sh == 0 && hh / sh < outH) roff[ih * kH + c++] = ki * kW * kDlxRD + (hh / sh) * outW;
+        }
+        rcnt[ih] = c;
+    }
+    for (int iw = t; iw < W; iw += NT) {
+        int c = 0;
+        for (int kj = 0; kj < kW; ++kj) {
+            const int ww = iw + pw - kj * dwl;
+            if (ww >= 0 && ww % sw == 0 && ww / sw < outW) coff[iw * kW + c++] = kj * kDlxRD + ww / sw;
+        }
+        ccnt[iw] = c;
+    }
+}
+
+// col2im from LDS with lane <-> input column, MT the most row taps and the
+// most column taps of any input pixel (2 for stride-2 3 x 3 layers): a
+// thread's column taps sit in registers, each output reads all MT x MT
+// candidates unconditionally (invalid ones at offset 0, a valid address)
+// and adds the valid ones in (ki, kj) order, so the LDS reads of an output
+// go out together instead of one branch and one wait per tap.  Adding +0.0
+// for an invalid tap leaves the sum's bits unchanged (a sum that starts at
+// +0.0 is never -0.0), so the result equals the tap-by-tap loop.
+template <int MT>
+__device__ __forceinline__ void col2im_cols(const float* Ds, float* __restrict__ dxn, const int* rcnt,
+                                            const int* roff, const int* ccnt, const int* coff, int CGv, int H,
+                                            int W, int kH, int kW, int rpp, int slot, int iw) {
+    const int HW = H * W, kk = kH * kW;
+    const int nc = ccnt[iw];
+    int cof[MT];
+#pragma unroll
+    for (int b = 0; b < MT; ++b) cof[b] = b < nc ? coff[iw * kW + b] : 0;
+    if (rpp <= H) {
+        // Rows ih = slot, slot + rpp, ...: a row's taps go to registers once
+        // and the channel group is walked under them.
+        for (int ih = slot; ih < H; ih += rpp) {
+            const int nr = rcnt[ih];
+            float* out = dxn + ih * W + iw;
+            const float* dc = Ds;
+            if (nr <= MT) {
+                int ro[MT];
+#pragma unroll
+                for (int a = 0; a < MT; ++a) ro[a] = a < nr ? roff[ih * kH + a] : 0;
+#pragma unroll(MT == 2 ? 2 : 1)
+                for (int cl = 0; cl < CGv; ++cl, dc += kk * kDlxRD, out += HW) {
+                    float v[MT][MT];
+#pragma unroll
+                    for (int a = 0; a < MT; ++a)
+#pragma unroll
+                        for (int b = 0; b < MT; ++b) v[a][b] = dc[ro[a] + cof[b]];
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int a = 0; a < MT; ++a)
+#pragma unroll
+                        for (int b = 0; b < MT; ++b) sum += a < nr && b < nc ? v[a][b] : 0.0f;
+                    *out = sum;
+                }
+            } else {
+                for (int cl = 0; cl < CGv; ++cl, dc += kk * kDlxRD, out += HW) {
+                    float sum = 0.0f;
+                    for (int a = 0; a < nr; ++a) {
+                        const float* drow = dc + roff[ih * kH + a];
+                        float v[MT];
+#pragma unroll
+                        for (int b = 0; b < MT; ++b) v[b] = drow[cof[b]];
+#pragma unroll
+                        for (int b = 0; b < MT; ++b) sum += b < nc ? v[b] : 0.0f;
+                    }
+                    *out = sum;
+                }
+            }
+        }
+        return;
+    }
+    const int dcl = rpp / H, dih = rpp - dcl * H;
+    int cl = slot / H, ih = slot - cl * H;
+    for (int r = slot; r < CGv * H; r += rpp) {
+        const float* dc = Ds + cl * kk * kDlxRD;
+        const int nr = rcnt[ih];
+        float sum = 0.0f;
+        for (int a = 0; a < nr; ++a) {
+            const float* drow = dc + roff[ih * kH + a];
+            float v[MT];
+#pragma unroll
+            for (int b = 0; b < MT; ++b) v[b] = drow[cof[b]];
+#pragma unroll
+            for (int b = 0; b < MT; ++b) sum += b < nc ? v[b] : 0.0f;
+        }
+        dxn[cl * HW + ih * W + iw] = sum;
+        ih += dih;
+        cl += dcl;
+        if (ih >= H) {
+            ih -= H;
+            ++cl;
+        }
+    }
+}
+
+// col2im from LDS, NT threads: dx[cl][ih][iw] (dxn = the group's first
+// channel) = sum over its row taps (ki order) and column taps (kj order) of
+// D[cl kk + ki kW + kj][oh outW + ow], D with row stride kDlxRD.  taps: 2
+// when W <= NT and no input pixel has more than two row or two column taps,
+// 4 when W <= NT and none more than four column taps, else 0 (a loop per
+// element).
+template <int NT>
+__device__ __forceinline__ void col2im_from_lds(const float* Ds, float* __restrict__ dxn, const int* rcnt,
+                                                const int* roff, const int* ccnt, const int* coff, int CGv, int H,
+                                                int W, int kH, int kW, int taps, int t) {
+    if (taps) {
+        const int rpp = NT / W, slot = t / W, iw = t - slot * W;
+        if (slot >= rpp) return;
+        if (taps == 2)
+            col2im_cols<2>(Ds, dxn, rcnt, roff, ccnt, coff, CGv, H, W, kH, kW, rpp, slot, iw);
+        else
+            col2im_cols<4>(Ds, dxn, rcnt, roff, ccnt, coff, CGv, H, W, kH, kW, rpp, slot, iw);
+        return;
+    }
+    const int HW = H * W, kk = kH * kW;
+    const FastDiv fHW = fast_div(HW), fW = fast_div(W);
+    for (int e = t; e < CGv * HW; e += NT) {
+        int rem, iw;
+        const int cl = divmod(e, fHW, rem);
+        const int ih = divmod(rem, fW, iw);
+        const float* dc = Ds + cl * kk * kDlxRD;
+        const int nr = rcnt[ih], nc = ccnt[iw];
+        float sum = 0.0f;
+        for (int a = 0; a < nr; ++a) {
+            const float* drow = dc + roff[ih * kH + a];
+            for (int b = 0; b < nc; ++b) sum += drow[coff[iw * kW + b]];
+        }
+        dxn[e] = sum;
+    }
+}
+
 // kDlxR row tiles of 16 (M <= 16 kDlxR), kDlxKC co per K chunk: <9, 64> (one
 // block per CU) or <5, 32> (two blocks per CU, whose phases then overlap).
 template <int kDlxR, int kDlxKC>
@@ -1372,12 +1518,21 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_data_lds_kernel(const flo
                                                                        const float* __restrict__ w,
                                                                        float* __restrict__ dx, ConvGeom g, int Cout,
                                                                        int CG, int RT, int tab_off, int vec,
-                                                                       int cols4) {
+                                                                       int taps) {
     extern __shared__ float smem[];
     const int C = (int)g.C, H = (int)g.H, W = (int)g.W, outW = (int)g.outW, outH = (int)g.outH;
     const int P = outH * outW, kH = (int)g.kH, kW = (int)g.kW, kk = kH * kW;
     const int groups = (C + CG - 1) / CG;
-    const int n = blockIdx.x / groups, c0 = (blockIdx.x - n * groups) * CG;
+    // Workgroups go to the 8 XCDs round-robin (block b to XCD b % 8): XCD x
+    // takes the x-th contiguous eighth of the (image, group) list, so the
+    // groups of one image, which all read that image's dy, run side by side
+    // on one XCD and share its L2.
+    int wi = (int)blockIdx.x;
+    {
+        const int nb = (int)gridDim.x, q8 = nb >> 3, r8 = nb & 7, x = wi & 7, s = wi >> 3;
+        wi = x < r8 ? x * (q8 + 1) + s : r8 * (q8 + 1) + (x - r8) * q8 + s;
+    }
+    const int n = wi / groups, c0 = (wi - n * groups) * CG;
     const int CGv = min(CG, C - c0), Mv = CGv * kk, Mp = RT * 16;
     // A is stored k-major, As[k][m] with row stride 16 R words (80 or 144, both
     // 16 mod 64, so the four k rows of one MFMA operand read hit different
@@ -1392,25 +1547,7 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_data_lds_kernel(const flo
     int* ccnt = roff + H * kH;                            // [W]
     int* coff = ccnt + W;                                 // [W][kW]
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, l16 = lane & 15, q = lane >> 4;
-    {
-        const int sh = (int)g.sh, sw = (int)g.sw, dh = (int)g.dh, dwl = (int)g.dw, ph = (int)g.ph, pw = (int)g.pw;
-        for (int ih = t; ih < H; ih += kIgThreads) {
-            int c = 0;
-            for (int ki = 0; ki < kH; ++ki) {
-                const int hh = ih + ph - ki * dh;
-                if (hh >= 0 && hh % sh == 0 && hh / sh < outH) roff[ih * kH + c++] = ki * kW * kDlxRD + (hh / sh) * outW;
-            }
-            rcnt[ih] = c;
-        }
-        for (int iw = t; iw < W; iw += kIgThreads) {
-            int c = 0;
-            for (int kj = 0; kj < kW; ++kj) {
-                const int ww = iw + pw - kj * dwl;
-                if (ww >= 0 && ww % sw == 0 && ww / sw < outW) coff[iw * kW + c++] = kj * kDlxRD + ww / sw;
-            }
-            ccnt[iw] = c;
-        }
-    }
+    build_tap_tables<kIgThreads>(g, rcnt, roff, ccnt, coff, t);
     v4f acc[kDlxR][2];
 #pragma unroll
     for (int r = 0; r < kDlxR; ++r) acc[r][0] = acc[r][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1467,93 +1604,8 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_data_lds_kernel(const flo
         }
     }
     __syncthreads();
-    // col2im from LDS: dx[c0 + cl][ih][iw] = sum over its row taps (ki order)
-    // and column taps (kj order) of D[cl kk + ki kW + kj][oh outW + ow].
-    const int HW = H * W;
-    float* dxn = dx + ((int64_t)n * C + c0) * HW;
-    if (cols4) {
-        // Lane <-> input column (so a thread's column taps, at most four, sit
-        // in registers and the stores are coalesced); rpp rows per pass.
-        const int rpp = kIgThreads / W, slot = t / W, iw = t - slot * W;
-        if (slot < rpp) {
-            const int nc = ccnt[iw];
-            int cof[4];
-#pragma unroll
-            for (int b = 0; b < 4; ++b) cof[b] = b < nc ? coff[iw * kW + b] : 0;
-            if (rpp <= H) {
-                // Rows ih = slot, slot + rpp, ...: a row's taps (at most four
-                // here) go to registers once and the channel group is walked
-                // under them, so an output's D reads are independent of each
-                // other and of the tables.  Same tap order as below.
-                for (int ih = slot; ih < H; ih += rpp) {
-                    const int nr = rcnt[ih];
-                    float* out = dxn + ih * W + iw;
-                    const float* dc = Ds;
-                    if (nr <= 4) {
-                        int ro[4];
-#pragma unroll
-                        for (int a = 0; a < 4; ++a) ro[a] = a < nr ? roff[ih * kH + a] : 0;
-                        for (int cl = 0; cl < CGv; ++cl, dc += kk * kDlxRD, out += HW) {
-                            float sum = 0.0f;
-#pragma unroll
-                            for (int a = 0; a < 4; ++a)
-#pragma unroll
-                                for (int b = 0; b < 4; ++b)
-                                    if (a < nr && b < nc) sum += dc[ro[a] + cof[b]];
-                            *out = sum;
-                        }
-                    } else {
-                        for (int cl = 0; cl < CGv; ++cl, dc += kk * kDlxRD, out += HW) {
-                            float sum = 0.0f;
-                            for (int a = 0; a < nr; ++a) {
-                                const float* drow = dc + roff[ih * kH + a];
-#pragma unroll
-                                for (int b = 0; b < 4; ++b)
-                                    if (b < nc) sum += drow[cof[b]];
-                            }
-                            *out = sum;
-                        }
-                    }
-                }
-                return;
-            }
-            const int dcl = rpp / H, dih = rpp - dcl * H;
-            int cl = slot / H, ih = slot - cl * H;
-            for (int r = slot; r < CGv * H; r += rpp) {
-                const float* dc = Ds + cl * kk * kDlxRD;
-                const int nr = rcnt[ih];
-                float sum = 0.0f;
-                for (int a = 0; a < nr; ++a) {
-                    const float* drow = dc + roff[ih * kH + a];
-#pragma unroll
-                    for (int b = 0; b < 4; ++b)
-                        if (b < nc) sum += drow[cof[b]];
-                }
-                dxn[cl * HW + ih * W + iw] = sum;
-                ih += dih;
-                cl += dcl;
-                if (ih >= H) {
-                    ih -= H;
-                    ++cl;
-                }
-            }
-        }
-        return;
-    }
-    const FastDiv fHW = fast_div(HW), fW = fast_div(W);
-    for (int e = t; e < CGv * HW; e += kIgThreads) {
-        int rem, iw;
-        const int cl = divmod(e, fHW, rem);
-        const int ih = divmod(rem, fW, iw);
-        const float* dc = Ds + cl * kk * kDlxRD;
-        const int nr = rcnt[ih], nc = ccnt[iw];
-        float sum = 0.0f;
-        for (int a = 0; a < nr; ++a) {
-            const float* drow = dc + roff[ih * kH + a];
-            for (int b = 0; b < nc; ++b) sum += drow[coff[iw * kW + b]];
-        }
-        dxn[e] = sum;
-    }
+    col2im_from_lds<kIgThreads>(Ds, dx + ((int64_t)n * C + c0) * H * W, rcnt, roff, ccnt, coff, CGv, H, W, kH, kW,
+                                taps, t);
 }
 
 // LDS bytes, channel group and tap-table offset (words) of
@@ -1928,6 +1980,12 @@ tf_status conv_bwd_data_impl(tf_ctx* ctx, const float* dy, const float* w, float
     // two blocks per CU (small channel groups) when that layout fits.
     if (sh > 1 || sw > 1) {
         int CG, RT, tab_off;
+        // Column-per-lane col2im: the most column and row taps of an input
+        // pixel.
+        int most = 0, most_r = 0;
+        for (int j0 = 0; j0 < sw; ++j0) most = std::max(most, phase_taps(j0, (int)pw, (int)kW, (int)sw, (int)dw_).n);
+        for (int i0 = 0; i0 < sh; ++i0) most_r = std::max(most_r, phase_taps(i0, (int)ph, (int)kH, (int)sh, (int)dh).n);
+        const auto taps_for = [&](int nt) { return W > nt ? 0 : most <= 2 && most_r <= 2 ? 2 : most <= 4 ? 4 : 0; };
         bool two = true;
         size_t lds_b = dx_lds_bytes(g, 5, 32, 80 * 1024, CG, RT, tab_off);
         if (lds_b == 0 || N * ((C + CG - 1) / CG) < 256) {
@@ -1940,16 +1998,13 @@ tf_status conv_bwd_data_impl(tf_ctx* ctx, const float* dy, const float* w, float
             // Direct loads: bit 0 dy rows, bit 1 filter rows.
             const int vec = (P % 4 == 0 && aligned16(dy) ? 1 : 0) |
                             ((C * kH * kW) % 4 == 0 && (CG * kH * kW) % 4 == 0 && aligned16(w) ? 2 : 0);
-            // Column-per-lane col2im: at most four column taps per input column.
-            int most = 0;
-            for (int j0 = 0; j0 < sw; ++j0) most = std::max(most, phase_taps(j0, (int)pw, (int)kW, (int)sw, (int)dw_).n);
-            const int cols4 = W <= kIgThreads && most <= 4 ? 1 : 0;
+            const int taps = taps_for(kIgThreads);
             if (two)
                 conv_bwd_data_lds_kernel<5, 32><<<(unsigned)nblk, kIgThreads, lds_b, ctx->stream>>>(
-                    dy, w, dx, g, (int)Cout, CG, RT, tab_off, vec, cols4);
+                    dy, w, dx, g, (int)Cout, CG, RT, tab_off, vec, taps);
             else
                 conv_bwd_data_lds_kernel<9, 64><<<(unsigned)nblk, kIgThreads, lds_b, ctx->stream>>>(
-                    dy, w, dx, g, (int)Cout, CG, RT, tab_off, vec, cols4);
+                    dy, w, dx, g, (int)Cout, CG, RT, tab_off, vec, taps);
             return tfh::check_launch("conv_bwd_data_lds_kernel");
         }
     }

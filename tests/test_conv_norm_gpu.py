@@ -287,6 +287,11 @@ DX_EXTRA_CASES = [
     (128, 3, 9, 10, 5, 1, 2, 0, 1),        # 1 x 1, stride 2: odd rows / columns get nothing
     (64, 40, 12, 11, 70, 3, 2, 2, 2),      # dilation 2, 40 channels in groups of 16, 70 co (two K chunks)
     (128, 2, 20, 21, 6, 9, 2, 4, 1),       # 9 x 9, stride 2: five column taps, the per-element col2im loop
+    # strided, two blocks per CU; col2im with at most 2 x 2 taps per pixel
+    # (stride-2 3 x 3) or at most 4 x 4 (5 x 5)
+    (128, 30, 24, 24, 40, 3, 2, 1, 1),     # 144 pixels, groups 8 + 8 + 8 + 6, filter by plain loads, 40 co
+    (130, 32, 16, 16, 24, 3, 2, 1, 1),     # 64 pixels, 24 co (a partly filled K chunk)
+    (256, 6, 16, 16, 16, 5, 2, 2, 1),      # 5 x 5: groups of 3 channels (75 dcol rows), up to 3 x 3 taps
 ]
 # The forward cases whose dy patch (Cout channels) fits the LDS.
 DX_CASES = [c for c in IMPLICIT_CASES if c[3] <= 64] + DX_EXTRA_CASES
