@@ -157,54 +157,84 @@ __global__ __launch_bounds__(256) void im2col_plane_kernel(const T* __restrict__
     }
 }
 
-template <typename T>
+// Tap tables of a col2im from LDS (NT threads build them), for column rows
+// (ki, kj) of RD words each: per input row ih, rcnt[ih] taps with offsets
+// roff[ih kH + a] = ki kW RD + oh outW (ki ascending); per input column iw,
+// ccnt[iw] taps with offsets coff[iw kW + b] = kj RD + ow (kj ascending).
+template <int NT>
+__device__ __forceinline__ void build_tap_tables(const ConvGeom& g, int RD, int* rcnt, int* roff, int* ccnt, int* coff,
+                                                 int t) {
+    const int H = (int)g.H, W = (int)g.W, kH = (int)g.kH, kW = (int)g.kW, outH = (int)g.outH, outW = (int)g.outW;
+    const int sh = (int)g.sh, sw = (int)g.sw, dh = (int)g.dh, dwl = (int)g.dw, ph = (int)g.ph, pw = (int)g.pw;
+    for (int ih = t; ih < H; ih += NT) {
+        int c = 0;
+        for (int ki = 0; ki < kH; ++ki) {
+            const int hh = ih + ph - ki * dh;
+            if (hh >= 0 && hh % sh == 0 && hh / sh < outH) roff[ih * kH + c++] = ki * kW * RD + (hh / sh) * outW;
+        }
+        rcnt[ih] = c;
+    }
+    for (int iw = t; iw < W; iw += NT) {
+        int c = 0;
+        for (int kj = 0; kj < kW; ++kj) {
+            const int ww = iw + pw - kj * dwl;
+            if (ww >= 0 && ww % sw == 0 && ww / sw < outW) coff[iw * kW + c++] = kj * RD + ww / sw;
+        }
+        ccnt[iw] = c;
+    }
+}
+
+// col2im of one (n, c) plane: its kH kW column rows staged in LDS, the tap
+// tables after them.  MT > 0: no input pixel has more than MT row taps or
+// MT column taps (2 for stride-2 3 x 3 layers, 3 for stride-1 ones), so a
+// pixel reads all MT x MT candidates unconditionally (invalid ones at offset
+// 0, a valid address) and adds the valid ones in (ki, kj) order: its LDS
+// reads go out together instead of one branch and one wait per tap, and the
+// sum equals the tap-by-tap one (adding +0.0 leaves it unchanged, and a sum
+// that starts at +0.0 is never -0.0).  MT = 0: the tap-by-tap loop.
+template <typename T, int MT>
 __global__ __launch_bounds__(256) void col2im_plane_kernel(const T* __restrict__ col, T* __restrict__ dx, ConvGeom g64) {
     extern __shared__ float cols[];
     const int H = (int)g64.H, W = (int)g64.W, kH = (int)g64.kH, kW = (int)g64.kW;
-    const int outH = (int)g64.outH, outW = (int)g64.outW, sh = (int)g64.sh, sw = (int)g64.sw;
-    const int ph = (int)g64.ph, pw = (int)g64.pw, dh = (int)g64.dh, dw = (int)g64.dw;
-    const int sp = outH * outW, n_col = kH * kW * sp, hw = H * W;
+    const int sp = (int)(g64.outH * g64.outW), n_col = kH * kW * sp, hw = H * W;
+    int* rcnt = reinterpret_cast<int*>(cols + n_col);   // [H]
+    int* roff = rcnt + H;                                // [H][kH]
+    int* ccnt = roff + H * kH;                           // [W]
+    int* coff = ccnt + W;                                // [W][kW]
+    build_tap_tables<256>(g64, sp, rcnt, roff, ccnt, coff, threadIdx.x);
     const int64_t nc = blockIdx.x;
-    const T* cp = col + nc * n_col;
-    stage_to_lds(cp, cols, n_col);
+    stage_to_lds(col + nc * n_col, cols, n_col);
     __syncthreads();
     T* dp = dx + nc * hw;
-    // Tap (ki, kj) reaches output row oh = (ih + ph - ki*dh) / sh when that
-    // is a whole number in [0, outH); the quotient and remainder are carried
-    // from tap to tap (one division per pixel and axis instead of per tap).
-    const int dqh = dh / sh, drh = dh - dqh * sh, dqw = dw / sw, drw = dw - dqw * sw;
+    constexpr int M = MT > 0 ? MT : 1;
     for (int p = threadIdx.x; p < hw; p += 256) {
         const int ih = p / W, iw = p - ih * W;
-        const int qw0 = (iw + pw) / sw, rw0 = (iw + pw) - qw0 * sw;
-        int qh = (ih + ph) / sh, rh = (ih + ph) - qh * sh;
+        const int nr = rcnt[ih], ncl = ccnt[iw];
         float acc = 0.0f;
-        for (int ki = 0; ki < kH; ++ki) {
-            if (qh < 0) break;  // hh < 0 here and for every later ki
-            if (rh == 0 && qh < outH) {
-                const float* crow = cols + ki * kW * sp + qh * outW;
-                int qw = qw0, rw = rw0;
-                for (int kj = 0; kj < kW; ++kj) {
-                    if (qw < 0) break;
-                    if (rw == 0 && qw < outW) acc += crow[kj * sp + qw];
-                    rw -= drw;
-                    qw -= dqw;
-                    if (rw < 0) {
-                        rw += sw;
-                        --qw;
-                    }
-                }
-            }
-            rh -= drh;
-            qh -= dqh;
-            if (rh < 0) {
-                rh += sh;
-                --qh;
+        if (MT > 0 && nr <= MT && ncl <= MT) {
+            int ro[M], co[M];
+#pragma unroll
+            for (int a = 0; a < M; ++a) ro[a] = a < nr ? roff[ih * kH + a] : 0;
+#pragma unroll
+            for (int b = 0; b < M; ++b) co[b] = b < ncl ? coff[iw * kW + b] : 0;
+            float v[M][M];
+#pragma unroll
+            for (int a = 0; a < M; ++a)
+#pragma unroll
+                for (int b = 0; b < M; ++b) v[a][b] = cols[ro[a] + co[b]];
+#pragma unroll
+            for (int a = 0; a < M; ++a)
+#pragma unroll
+                for (int b = 0; b < M; ++b) acc += a < nr && b < ncl ? v[a][b] : 0.0f;
+        } else {
+            for (int a = 0; a < nr; ++a) {
+                const float* crow = cols + roff[ih * kH + a];
+                for (int b = 0; b < ncl; ++b) acc += crow[coff[iw * kW + b]];
             }
         }
         stf(dp, p, acc);
     }
 }
-
 
 // ---------------------------------------------------------------------------
 // Implicit-GEMM convolution forward (fp32, NCHW, MFMA): y[n][co][p] =
@@ -1365,33 +1395,6 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_data_implicit_kernel(cons
 constexpr int kDlxRB = 256 + 16;     // B row stride (words)
 constexpr int kDlxRD = 256 + 4;      // D row stride (words)
 
-// Tap tables of the col2im from LDS (NT threads build them): per input row
-// ih, rcnt[ih] taps with D offsets roff[ih kH + a] = ki kW RD + oh outW (ki
-// ascending); per input column iw, ccnt[iw] taps with offsets
-// coff[iw kW + b] = kj RD + ow (kj ascending).
-template <int NT>
-__device__ __forceinline__ void build_tap_tables(const ConvGeom& g, int* rcnt, int* roff, int* ccnt, int* coff,
-                                                 int t) {
-    const int H = (int)g.H, W = (int)g.W, kH = (int)g.kH, kW = (int)g.kW, outH = (int)g.outH, outW = (int)g.outW;
-    const int sh = (int)g.sh, sw = (int)g.sw, dh = (int)g.dh, dwl = (int)g.dw, ph = (int)g.ph, pw = (int)g.pw;
-    for (int ih = t; ih < H; ih += NT) {
-        int c = 0;
-        for (int ki = 0; ki < kH; ++ki) {
-            const int hh = ih + ph - ki * dh;
-            if (hh >= 0 && hh % sh == 0 && hh / sh < outH) roff[ih * kH + c++] = ki * kW * kDlxRD + (hh / sh) * outW;
-        }
-        rcnt[ih] = c;
-    }
-    for (int iw = t; iw < W; iw += NT) {
-        int c = 0;
-        for (int kj = 0; kj < kW; ++kj) {
-            const int ww = iw + pw - kj * dwl;
-            if (ww >= 0 && ww % sw == 0 && ww / sw < outW) coff[iw * kW + c++] = kj * kDlxRD + ww / sw;
-        }
-        ccnt[iw] = c;
-    }
-}
-
 // col2im from LDS with lane <-> input column, MT the most row taps and the
 // most column taps of any input pixel (2 for stride-2 3 x 3 layers): a
 // thread's column taps sit in registers, each output reads all MT x MT
@@ -1547,7 +1550,7 @@ __global__ __launch_bounds__(kIgThreads) void conv_bwd_data_lds_kernel(const flo
     int* ccnt = roff + H * kH;                            // [W]
     int* coff = ccnt + W;                                 // [W][kW]
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, l16 = lane & 15, q = lane >> 4;
-    build_tap_tables<kIgThreads>(g, rcnt, roff, ccnt, coff, t);
+    build_tap_tables<kIgThreads>(g, kDlxRD, rcnt, roff, ccnt, coff, t);
     v4f acc[kDlxR][2];
 #pragma unroll
     for (int r = 0; r < kDlxR; ++r) acc[r][0] = acc[r][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1744,17 +1747,33 @@ tf_status tf_col2im(tf_ctx* ctx, const void* col, void* dx, int64_t N, int64_t C
     if (dtype != TF_F32 && dtype != TF_BF16 && dtype != TF_F16)
         return tfh::set_error(TF_ERR_UNSUPPORTED, "tf_col2im: dtype must be Float32, Float16 or BFloat16");
     const int64_t planes = N * C, n_col = kH * kW * g.outH * g.outW;
-    if (n_col <= kPlaneLdsFloats && H * W < (1LL << 30) && planes >= 256 && planes < (1LL << 31) &&
+    const int64_t tables = H * (1 + kH) + W * (1 + kW);
+    if (n_col + tables <= kPlaneLdsFloats && H * W < (1LL << 30) && planes >= 256 && planes < (1LL << 31) &&
         plane_indices_fit(g)) {
-        const size_t lds = (size_t)n_col * sizeof(float);
+        // The most row taps and column taps of any input pixel (an upper
+        // bound: taps by residue class, before the image edges).
+        int mt = 0;
+        for (int64_t i0 = 0; i0 < sh; ++i0) mt = std::max(mt, phase_taps((int)i0, (int)ph, (int)kH, (int)sh, (int)dh).n);
+        for (int64_t j0 = 0; j0 < sw; ++j0) mt = std::max(mt, phase_taps((int)j0, (int)pw, (int)kW, (int)sw, (int)dw).n);
+        const size_t lds = (size_t)(n_col + tables) * sizeof(float);
+#define TF_C2I_PLANE(T, MT)                                                                                   \
+    col2im_plane_kernel<T, MT><<<(unsigned)planes, 256, lds, ctx->stream>>>((const T*)col, (T*)dx, g)
+#define TF_C2I_PLANE_MT(T)                                                                                    \
+    do {                                                                                                      \
+        if (mt <= 1) TF_C2I_PLANE(T, 1);                                                                      \
+        else if (mt == 2) TF_C2I_PLANE(T, 2);                                                                 \
+        else if (mt == 3) TF_C2I_PLANE(T, 3);                                                                 \
+        else if (mt == 4) TF_C2I_PLANE(T, 4);                                                                 \
+        else TF_C2I_PLANE(T, 0);                                                                              \
+    } while (0)
         if (dtype == TF_F32)
-            col2im_plane_kernel<float><<<(unsigned)planes, 256, lds, ctx->stream>>>((const float*)col, (float*)dx, g);
+            TF_C2I_PLANE_MT(float);
         else if (dtype == TF_BF16)
-            col2im_plane_kernel<uint16_t><<<(unsigned)planes, 256, lds, ctx->stream>>>((const uint16_t*)col,
-                                                                                     (uint16_t*)dx, g);
+            TF_C2I_PLANE_MT(uint16_t);
         else
-            col2im_plane_kernel<_Float16><<<(unsigned)planes, 256, lds, ctx->stream>>>((const _Float16*)col,
-                                                                                     (_Float16*)dx, g);
+            TF_C2I_PLANE_MT(_Float16);
+#undef TF_C2I_PLANE_MT
+#undef TF_C2I_PLANE
         return tfh::check_launch("col2im_plane_kernel");
     }
     if (dtype == TF_F32)
