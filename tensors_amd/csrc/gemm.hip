@@ -3239,9 +3239,14 @@ __global__ __launch_bounds__(256) void linear_bwd_narrow_kernel(const float* __r
         }
         if (db && blockIdx.x == 0 && cq < N) {
             // db: thread (column cq, row group rg) adds its rows of the batch.
+            // Every row's read is issued and rows past M add +0.0 (no change
+            // to a sum that starts at +0.0), so the reads are in flight
+            // together instead of one branch and one wait per row.
+            float dr[kLnbRows];
 #pragma unroll
-            for (int u = 0; u < kLnbRows; ++u)
-                if (rb0 + rg + 16 * u < M) dbv += dyf[(rg + 16 * u) * N + cq];
+            for (int u = 0; u < kLnbRows; ++u) dr[u] = dyf[(rg + 16 * u) * N + cq];
+#pragma unroll
+            for (int u = 0; u < kLnbRows; ++u) dbv += rb0 + rg + 16 * u < M ? dr[u] : 0.0f;
         }
     }
     if (dw) {
