@@ -215,6 +215,7 @@ IMPLICIT_CASES = [
     (5, 2, 15, 13, 20, 3, 2, 1, 2),        # K = 18, stride 2, dilation 2, a partial last pixel tile
     (3, 1, 11, 9, 70, 5, 3, 2, 1),         # K = 25, stride 3, three channel blocks (32 + 32 + 6)
     (2, 39, 16, 16, 24, 3, 1, 1, 1),       # K = 351: 11 weight-gradient tiles, the last 3 split in 2 pixel slices
+    (2, 60, 8, 8, 20, 3, 1, 1, 1),         # K = 540: 17 weight-gradient tiles, the last one unpaired
 ]
 
 
