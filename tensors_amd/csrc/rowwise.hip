@@ -182,7 +182,7 @@ __device__ __forceinline__ void ce_row(const T* __restrict__ logits, const int64
                                        const float* __restrict__ lse_in, const float* __restrict__ grad_loss,
                                        float* __restrict__ lse_out, float* __restrict__ nll,
                                        T* __restrict__ dlogits, int r, int cols, float inv_rows, int vec,
-                                       float nll_max, int strict) {
+                                       float nll_max, int strict, bool nll_atomic) {
     constexpr int NCC = NC > 0 ? NC : 1;
     const int lane = threadIdx.x & 63;
     const T* x = logits + (int64_t)r * cols;
@@ -217,11 +217,27 @@ __device__ __forceinline__ void ce_row(const T* __restrict__ logits, const int64
     }
 
     if (MODE != 1) {
+        float xt = 0.0f;
+        if constexpr (NC > 0) {
+            // The target's logit from the row in registers (no dependent
+            // load): the lane holding column t adds it, every other term is
+            // +0.0, so the wave sum is that value (a -0.0 logit comes out as
+            // +0.0, which gives the same lse - x).
+            float h = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) h += col_of(c, lane, q, vec) == t ? v[c][q] : 0.0f;
+            xt = tfd::wave_sum(h);
+        }
         if (lane == 0) {
             if (lse_out) lse_out[r] = lse;
-            float nl = t_ok ? lse - elem_f32(x, t) : (strict ? __builtin_nanf("") : 0.0f);
-            // NaN stays NaN; an agent-scope store, read by another block
-            __hip_atomic_store(nll + r, nl > nll_max ? nll_max : nl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            float nl = t_ok ? lse - (NC > 0 ? xt : elem_f32(x, t)) : (strict ? __builtin_nanf("") : 0.0f);
+            nl = nl > nll_max ? nll_max : nl;   // NaN stays NaN
+            // With the in-kernel mean another block reads it: an agent-scope
+            // store; otherwise a later launch reads it.
+            if (nll_atomic) __hip_atomic_store(nll + r, nl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else nll[r] = nl;
         }
     }
     if (MODE != 0) {
@@ -270,7 +286,7 @@ __global__ __launch_bounds__(256) void ce_kernel(const T* __restrict__ logits, c
                                                  unsigned* __restrict__ ticket) {
     const int r = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     if (r < rows) ce_row<T, NC, MODE>(logits, targets, lse_in, grad_loss, lse_out, nll, dlogits, r, cols, inv_rows,
-                                   vec, nll_max, strict);
+                                   vec, nll_max, strict, ticket != nullptr);
     if (MODE != 1 && ticket != nullptr) {
         __shared__ int last;
         tfd::wait_stores_landed();
