@@ -872,7 +872,11 @@ int tfa_mlp_train(const int32_t* dims, int32_t ndims, int64_t batch, int64_t ste
             Tensor loss = ce.forward(h, yb[s % n_batches]);
             loss.backward();
             opt.step();
-            loss_t.push_back(loss);
+            // Keep the value only: the step's autograd graph (nodes, edges)
+            // is released with `loss` instead of living until the end.
+            Tensor kept = loss;
+            kept.autograd_meta().reset();
+            loss_t.push_back(kept);
             if (pool_used) {
                 hip::synchronize(0);
                 hip::pool_stats(0, nullptr, &pool_used[s]);
@@ -1074,7 +1078,11 @@ int tfa_cnn_train(int64_t batch, int64_t H, int64_t W, int64_t steps, int64_t wa
             Tensor loss = ce.forward(fc.forward(h), yb[s % n_batches]);
             loss.backward();
             opt.step();
-            loss_t.push_back(loss);
+            // Keep the value only: the step's autograd graph (nodes, edges)
+            // is released with `loss` instead of living until the end.
+            Tensor kept = loss;
+            kept.autograd_meta().reset();
+            loss_t.push_back(kept);
         };
         for (int64_t s = 0; s < warmup; ++s) run_step(s);
         sync_if_gpu(on_gpu);
