@@ -74,6 +74,12 @@ int tfa_cnn_train(int64_t batch, int64_t H, int64_t W, int64_t steps, int64_t wa
                   const float* xs, const int64_t* ys, float lr, float mu, int32_t on_gpu, const float* init_params,
                   float* losses, float* final_params, double* ms_per_step);
 
+/* Returns the GPU memory the harness's context holds unused (its block cache
+ * and the pool's free memory) to the driver, so that the next run starts
+ * from an empty pool as in a fresh process; 0 also when no GPU context
+ * exists yet. */
+int tfa_release_memory(void);
+
 /* Runs one of the C++ self-tests (`name`, see tfa_selftest_names) on the CPU
  * (on_gpu = 0) or on GPU 0 (on_gpu = 1). */
 int tfa_selftest(const char* name, int32_t on_gpu);

@@ -34,6 +34,8 @@ def _load() -> C.CDLL:
     lib.tfa_mlp_step_trace.restype = C.c_int
     lib.tfa_cnn_train.argtypes = [i64, i64, i64, i64, i64, i64, p, p, f, f, i32, p, p, p, p]
     lib.tfa_cnn_train.restype = C.c_int
+    lib.tfa_release_memory.argtypes = []
+    lib.tfa_release_memory.restype = C.c_int
     return lib
 
 
@@ -117,6 +119,12 @@ def mlp_step_trace(dims, x, y, *, lr, mu, on_gpu, bf16=False, init_weights=None)
     return (float(loss[0]), split(acts, lambda i: B, lambda i: d[i], L + 1),
             split(grads, lambda i: B, lambda i: d[i + 1], L),
             split(fw, lambda i: d[i + 1], lambda i: d[i], L), split(fb, lambda i: d[i + 1], lambda i: 1, L))
+
+
+def release_memory():
+    """Returns the GPU memory the harness holds unused (its block cache and
+    the memory pool's free memory) to the driver (tfa_release_memory)."""
+    _check(lib.tfa_release_memory())
 
 
 def cnn_train(xs, ys, *, steps, lr, mu, on_gpu, init_params=None, warmup=0, want_params=False):

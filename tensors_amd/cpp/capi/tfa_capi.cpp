@@ -1029,6 +1029,10 @@ int tfa_mlp_step_trace(const int32_t* dims, int32_t ndims, int64_t batch, const 
     });
 }
 
+int tfa_release_memory(void) {
+    return guarded([&] { hip::trim(0); });
+}
+
 int tfa_cnn_train(int64_t batch, int64_t H, int64_t W, int64_t steps, int64_t warmup, int64_t n_batches, const float* xs,
                   const int64_t* ys, float lr, float mu, int32_t on_gpu, const float* init_params, float* losses,
                   float* final_params, double* ms_per_step) {

@@ -120,6 +120,15 @@ void register_backend() {
 
 void synchronize(int device) { check(tf_hip_sync(context(device)), "hip::synchronize"); }
 
+void trim(int device) {
+    tf_ctx* c = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_ctx_mutex);
+        if (device >= 0 && device < kMaxDevices) c = g_ctx[device];
+    }
+    if (c) check(tf_hip_trim(c, 0), "hip::trim");
+}
+
 void pool_stats(int device, uint64_t* reserved, uint64_t* used) {
     check(tf_hip_pool_stats(context(device), reserved, used), "hip::pool_stats");
 }

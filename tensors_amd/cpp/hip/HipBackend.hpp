@@ -36,6 +36,9 @@ void check(int status, const char* what);
 void register_backend();
 // Blocks until the device's stream has drained.
 void synchronize(int device = 0);
+// Hands the device's cached blocks and the pool's unused memory back to the
+// driver (tf_hip_trim with nothing kept); a no-op before the context exists.
+void trim(int device = 0);
 // Launch on a caller-owned hipStream_t from now on (nullptr: the context's own).
 void set_stream(void* stream, int device = 0);
 

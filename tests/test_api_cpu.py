@@ -62,6 +62,11 @@ def test_cpu_training_tracks_oracle():
     assert_close(fw, np.concatenate([w.ravel() for w in ws]), 1e-4, "weights")
 
 
+def test_release_memory_without_gpu_context_is_a_no_op():
+    """tfa_release_memory before any GPU context exists (here: no GPU)."""
+    api.release_memory()
+
+
 def test_cpu_errors_are_reported():
     with pytest.raises(api.HarnessError):
         api.mlp_train([784, 10], np.zeros((1, 2, 784), np.float32), np.zeros((1, 2), np.int64), steps=1, lr=-1.0,

@@ -175,3 +175,23 @@ def test_pool_use_is_flat_across_steps(ctx, cfg):
     assert np.all(np.isfinite(losses))
     assert trace[early] > 0
     assert np.all(trace[early:] == trace[early]), f"pool bytes in use grow: {trace.tolist()}"
+
+
+def test_release_memory_returns_pool_memory(ctx):
+    """tfa_release_memory hands the harness's cached blocks and the pool's
+    free memory back to the driver: after a C1 run the device pool holds no
+    more than before (the pool is shared with this test's context, whose own
+    allocations stay), and training afterwards gives the same losses."""
+    xs, ys = _c1_inputs(20)
+    kw = dict(lr=0.1, mu=0.9, reference_compat=True)
+    before, _, _ = api.mlp_train(C1, xs, ys, steps=20, on_gpu=True, **kw)
+    ctx.sync()
+    reserved0, _ = ctx.pool_stats()
+    api.release_memory()
+    api.release_memory()                          # nothing left to release: still fine
+    ctx.sync()
+    reserved1, used1 = ctx.pool_stats()
+    assert used1 <= reserved1 <= reserved0, (reserved0, reserved1, used1)
+    after, _, _ = api.mlp_train(C1, xs, ys, steps=20, on_gpu=True, **kw)
+    assert np.array_equal(before, after)
+
