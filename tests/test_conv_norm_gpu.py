@@ -77,6 +77,8 @@ IM2COL_CASES = [
     (32, 8, 13, 11, 5, 3, 2, 1),        # stride 3, 5x5
     (16, 16, 64, 64, 5, 1, 2, 1),       # im2col in 25 row groups; col2im column chunk too big for LDS
     (2, 128, 130, 130, 3, 1, 1, 1),     # plane too big for LDS: element forms
+    (64, 4, 16, 16, 7, 2, 3, 1),        # 7x7 stride 2: col2im plane form with up to 4 x 4 taps per pixel
+    (64, 4, 12, 12, 9, 1, 4, 1),        # 9x9 stride 1: col2im plane form, 9 taps per axis (the per-tap loop)
 ]
 
 
