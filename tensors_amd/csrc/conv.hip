@@ -292,6 +292,45 @@ __device__ __forceinline__ int divmod(int x, const FastDiv& f, int& r) {
     return q;
 }
 
+// fp32 im2col, plane form, for output rows of whole quads (outW % 4 == 0)
+// and a 16-byte aligned col: work item w of the block's rows is col row
+// r0 + w / (sp / 4), output pixels 4 q .. 4 q + 3 of one output row, so a
+// wave stores 1 KB of one col row per instruction (im2col_plane_kernel: 256
+// bytes).  Every tap's LDS read is issued (at offset 0 outside the image)
+// and the value selected.  The same values as im2col_plane_kernel.
+__global__ __launch_bounds__(256) void im2col_plane4_kernel(const float* __restrict__ x, float* __restrict__ col,
+                                                            ConvGeom g64, int rows_per_block) {
+    extern __shared__ float plane[];
+    const int H = (int)g64.H, W = (int)g64.W, kW = (int)g64.kW, outW = (int)g64.outW;
+    const int sh = (int)g64.sh, sw = (int)g64.sw, dh = (int)g64.dh, dw = (int)g64.dw;
+    const int ph = (int)g64.ph, pw = (int)g64.pw;
+    const int kk = (int)(g64.kH * g64.kW), sp = (int)(g64.outH * g64.outW), hw = H * W;
+    const int64_t nc = blockIdx.x;
+    stage_to_lds(x + nc * hw, plane, hw);
+    __syncthreads();
+    const int r0 = blockIdx.y * rows_per_block, r1 = min(kk, r0 + rows_per_block);
+    const int q4 = sp >> 2, items = (r1 - r0) * q4;
+    const FastDiv fq = fast_div(q4), fw = fast_div(outW), fkw = fast_div(kW);
+    float4* cp4 = reinterpret_cast<float4*>(col + nc * kk * sp);
+    for (int w = threadIdx.x; w < items; w += 256) {
+        int qd, ow, kj;
+        const int r = r0 + divmod(w, fq, qd);
+        const int oh = divmod(4 * qd, fw, ow);
+        const int ki = divmod(r, fkw, kj);
+        const int ih = oh * sh - ph + ki * dh, iw0 = ow * sw - pw + kj * dw;
+        const bool row_in = (unsigned)ih < (unsigned)H;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int iw = iw0 + e * sw;
+            const bool in = row_in && (unsigned)iw < (unsigned)W;
+            const float t = plane[in ? ih * W + iw : 0];
+            v[e] = in ? t : 0.0f;
+        }
+        cp4[(int64_t)r * q4 + qd] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
 constexpr int kStage4 = 8;  // 16-byte staging loads in flight per thread
 
 // Staging sources: slot i of a source is 16 bytes (4 floats) bound for LDS
@@ -1715,7 +1754,9 @@ tf_status tf_im2col(tf_ctx* ctx, const void* x, void* col, int64_t N, int64_t C,
         const int rpb = (int)((kk + groups - 1) / groups);
         const dim3 grid((unsigned)planes, (unsigned)((kk + rpb - 1) / rpb));
         const size_t lds = (size_t)(H * W) * sizeof(float);
-        if (dtype == TF_F32)
+        if (dtype == TF_F32 && g.outW % 4 == 0 && aligned16(col))
+            im2col_plane4_kernel<<<grid, 256, lds, ctx->stream>>>((const float*)x, (float*)col, g, rpb);
+        else if (dtype == TF_F32)
             im2col_plane_kernel<float><<<grid, 256, lds, ctx->stream>>>((const float*)x, (float*)col, g, rpb);
         else if (dtype == TF_BF16)
             im2col_plane_kernel<uint16_t><<<grid, 256, lds, ctx->stream>>>((const uint16_t*)x, (uint16_t*)col, g, rpb);

@@ -62,7 +62,7 @@ BW_KERNELS = {
     "sgd_c2": ("sgd_multi_kernel<false>", 20 * (N2 * N2 + N2)),
     # as above plus the bf16 copy of every parameter
     "sgd_c5": ("sgd_multi_kernel<true>", 22 * C5_PARAMS),
-    "im2col_conv2_c4": ("im2col_plane_kernel<float>", _conv_x + _conv_col),
+    "im2col_conv2_c4": ("im2col_plane4_kernel", _conv_x + _conv_col),
     "col2im_conv2_c4": ("col2im_plane_kernel<float, 2>", _conv_col + _conv_x),
     # C5 layer 1's ReLU backward with the next Linear's bias gradient
     # (bf16 [4096 x 8192]): dy, x read, dz written, db (fp32) written
