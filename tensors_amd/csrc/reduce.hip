@@ -85,6 +85,8 @@ __global__ __launch_bounds__(256) void colsum_stage1(const T* __restrict__ dy, f
 // strips finish independently.  fp32 and bf16 inputs of one shape share the
 // grid and the order, so their sums are equal for equal values.
 constexpr int kTileCols = 32;
+constexpr int kTileLanes = kTileCols / 4;     // lanes per row segment (4 columns each)
+constexpr int kTileRG = 256 / kTileLanes;      // row groups per block
 constexpr int kTileU = 16;
 #ifndef TF_COLSUM_BLOCKS
 #define TF_COLSUM_BLOCKS 256
@@ -95,7 +97,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void colsum_tile_kernel(const T* __restrict__ dy, float* __restrict__ db,
                                                           float* __restrict__ part, unsigned* __restrict__ tickets,
                                                           int rows, int cols, int rpc, int chunks) {
-    __shared__ float4 red[4][8];
+    __shared__ float4 red[4][kTileLanes];
     __shared__ bool last;
     // Workgroups go to the 8 XCDs round-robin (block x of a row of the grid
     // on XCD x % 8 when the row length is a multiple of 8): each XCD takes a
@@ -104,7 +106,7 @@ __global__ __launch_bounds__(256) void colsum_tile_kernel(const T* __restrict__ 
     const int strips = gridDim.x;
     const int strip = strips % 8 == 0 ? (blockIdx.x % 8) * (strips / 8) + blockIdx.x / 8 : blockIdx.x;
     const int chunk = blockIdx.y;
-    const int cg = threadIdx.x & 7, rg = threadIdx.x >> 3;
+    const int cg = threadIdx.x % kTileLanes, rg = threadIdx.x / kTileLanes;
     const int c0 = strip * kTileCols + 4 * cg;
     // cols % 4 == 0: a lane's four columns are all inside or all past the
     // last (ragged) strip's end.
@@ -112,31 +114,31 @@ __global__ __launch_bounds__(256) void colsum_tile_kernel(const T* __restrict__ 
     const T* base = dy + c0;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     int r = r0 + rg;
-    for (; r + (kTileU - 1) * 32 < r1; r += kTileU * 32) {
+    for (; r + (kTileU - 1) * kTileRG < r1; r += kTileU * kTileRG) {
         float4 v[kTileU];
 #pragma unroll
-        for (int u = 0; u < kTileU; ++u) v[u] = vec4_f32(base + (int64_t)(r + 32 * u) * cols);
+        for (int u = 0; u < kTileU; ++u) v[u] = vec4_f32(base + (int64_t)(r + kTileRG * u) * cols);
 #pragma unroll
         for (int u = 0; u < kTileU; ++u) {
             acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
         }
     }
-    for (; r < r1; r += 32) {
+    for (; r < r1; r += kTileRG) {
         const float4 v = vec4_f32(base + (int64_t)r * cols);
         acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
     }
 #pragma unroll
-    for (int off = 8; off < 64; off <<= 1) {
+    for (int off = kTileLanes; off < 64; off <<= 1) {
         acc.x += __shfl_xor(acc.x, off, 64);
         acc.y += __shfl_xor(acc.y, off, 64);
         acc.z += __shfl_xor(acc.z, off, 64);
         acc.w += __shfl_xor(acc.w, off, 64);
     }
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (lane < 8) red[wave][lane] = acc;
+    if (lane < kTileLanes) red[wave][lane] = acc;
     __syncthreads();
     float* mine = part + ((int64_t)strip * chunks + chunk) * kTileCols;
-    if (threadIdx.x < 8) {
+    if (threadIdx.x < kTileLanes) {
         const float4 a = red[0][cg], b1 = red[1][cg], c = red[2][cg], d = red[3][cg];
         const float s[4] = {(a.x + b1.x) + (c.x + d.x), (a.y + b1.y) + (c.y + d.y), (a.z + b1.z) + (c.z + d.z),
                             (a.w + b1.w) + (c.w + d.w)};
@@ -418,7 +420,8 @@ tf_status colsum_impl(tf_ctx* ctx, const T* dy, float* db, int64_t rows, int64_t
     // adding its chunks.  vec implies cols % 4 == 0.
     const int64_t tstrips = (cols + kTileCols - 1) / kTileCols;
     if (vec && tstrips <= tfh::kTicketColsumStrips) {
-        int64_t chunks = std::max<int64_t>(1, std::min<int64_t>((kTileBlocks + tstrips - 1) / tstrips, (rows + 31) / 32));
+        int64_t chunks = std::max<int64_t>(1, std::min<int64_t>((kTileBlocks + tstrips - 1) / tstrips,
+                                                                (rows + kTileRG - 1) / kTileRG));
         const int rpc = (int)((rows + chunks - 1) / chunks);
         chunks = (rows + rpc - 1) / rpc;
         tf_status st = tfh::ensure_workspace(ctx, (size_t)tstrips * chunks * kTileCols * sizeof(float));
